@@ -1,0 +1,239 @@
+"""Throughput of the packed-weight linear hot path on one MI355X.
+
+Workload (the north-star shape): one SDXL-UNet
+GEGLU-input linear 1280 -> 5120 on batch 2 x 1024 tokens (M = 2048), bf16,
+winner optimizer flags (ratio-coherence gates, gf_consol = 50, no coh_pre),
+fused dequant-GEMM mode.  One step = forward (dequant-GEMM) + backward
+(dequant-GEMM dgrad, wgrad, v-hat EMA, packed update) + rebalance(), on
+synthetic x ~ N(0,1) and dy ~ N(0, 1e-3), random-init weights.
+
+Prints one JSON line.  value = dequant-matmul throughput of the whole step,
+6 M N K / step time (TFLOP/s).  roofline = the forward dequant-GEMM kernel
+against dense bf16 MFMA peak; roofline_update = the packed update kernel
+against HBM peak at 10 algorithmic B/param.  cpu_baseline = the same step on
+the host: torch fp32 GEMMs + the CPU oracle's v-hat / update / rebalance.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+N_OUT, K_IN, M_TOK = 5120, 1280, 2048
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBPS = 8000.0
+UPDATE_BYTES_PER_PARAM = 10      # int32 read + int32 write + bf16 grad read
+DECODE_BYTES_PER_PARAM = 6       # int32 read + bf16 write
+
+
+def _event_time_ms(fn, reps, torch):
+    s = torch.cuda.Event(enable_timing=True)
+    e = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        fn()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / reps
+
+
+def cpu_baseline(threads):
+    """One step of the same workload on the host cores: torch fp32 GEMMs and
+    the CPU oracle's v-hat EMA, packed update and rebalance."""
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    torch.set_num_threads(threads)
+    O.set_threads(threads)
+    rng = np.random.default_rng(0)
+    x = torch.from_numpy(rng.standard_normal((M_TOK, K_IN)).astype(np.float32))
+    dy = torch.from_numpy((rng.standard_normal((M_TOK, N_OUT)) * 1e-3).astype(np.float32))
+    W0 = (rng.standard_normal((N_OUT, K_IN)) * (2.0 / (N_OUT + K_IN)) ** 0.5).astype(np.float32)
+    pk, re, ce = O.load_weights(W0)
+    vr = np.zeros(N_OUT, np.float32)
+    vc = np.zeros(K_IN, np.float32)
+    P = O.UpdateParams(alpha=0.1, beta1=0.0, weight_decay=0.0, step_cap=10.0, v_scale=0.0,
+                       precond_p=0.5, gf_consol=50.0, drift_cancel_C=0.018036072144288578,
+                       alpha_v_fast=0.001, wd_sv=0.0, wd_sf=0.0, gf_trust_delta_sq=1.0,
+                       gate_gain=1.0, mantissa_bias=15)
+    flags = (O.MASS_PRESERVE | O.APPLY_CHASE | O.TRACK_REBALANCE | O.GF_TRUST_REGION
+             | O.GF_CONSOLIDATION | O.FIXED_COH | O.RATIO_COH)
+
+    def step(salt):
+        W = torch.from_numpy(O.bf16_bits_to_f32(O.materialize(pk, re, ce)).astype(np.float32))
+        y = x @ W.T
+        dx = dy @ W
+        gw = dy.T @ x
+        gb = O.f32_to_bf16_bits_array(gw.numpy())
+        svi = O.vhat_ema(gb, vr, vc, 0.999)
+        rm = np.zeros(N_OUT, np.int32)
+        cm = np.zeros(K_IN, np.int32)
+        S = O.UpdateScalars(lr=5e-4, eps=1e-10, chase_floor=0.9, leak_floor=0.999, v_bc=1.0,
+                            salt=salt, consolidate=1)
+        O.apply_adamw(pk, gb, None, re, ce, rm, cm, vr, vc, svi, None, P, S, flags)
+        O.rebalance(pk, re, ce, rm, cm, seed=salt)
+        return y, dx
+
+    step(1)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        step(2 + reps)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0 or reps >= 10:
+            break
+    sec = el / reps
+    return {"value": 6.0 * M_TOK * N_OUT * K_IN / sec / 1e12, "unit": "TFLOP/s", "cores": threads,
+            "kind": "port", "ms_per_step": sec * 1e3,
+            "sample": f"{reps} full steps of the 1280->5120 M=2048 workload: torch fp32 GEMMs "
+                      f"(fwd, dgrad, wgrad) + oracle v-hat, update, rebalance"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the packed path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    layer = ca.ConcordLinearPackedB(K_IN, N_OUT, bias=True, device=dev, lr=5e-4)
+    ca.set_ratio_coh(True)
+    ca.set_ratio_coh_floors(0.9, 0.999)
+    layer.disable_cohpre()
+    layer.gf_consol = 50.0
+    x = torch.randn(M_TOK, K_IN, device=dev).to(torch.bfloat16).requires_grad_(True)
+    dy = (torch.randn(M_TOK, N_OUT, device=dev) * 1e-3).to(torch.bfloat16)
+
+    def step():
+        x.grad = None
+        y = layer(x)
+        y.backward(dy)
+        layer.rebalance()
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+
+    mode = "eager"
+    run = step
+    if not args.no_graph:
+        try:
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for _ in range(2):
+                    step()
+            torch.cuda.current_stream().wait_stream(s)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step()
+            torch.cuda.synchronize()
+            run = g.replay
+            mode = "hipgraph"
+        except Exception as exc:  # capture unsupported: time eagerly
+            print(f"bench.py: graph capture failed ({exc}); timing eager steps", file=sys.stderr)
+            torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(args.steps):
+        run()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    flops_step = 6.0 * M_TOK * N_OUT * K_IN
+    value = flops_step / (ms_step * 1e-3) / 1e12
+
+    # per-kernel averages (HIP events on the stream the kernels run on)
+    xb = x.detach()
+    st = (layer.packed_w, layer.row_exp, layer.col_exp)
+    reps = 20
+    t_fwd = _event_time_ms(lambda: pb._gemm_fwd(xb, *st, 15, layer.bias, None), reps, torch)
+    t_dgrad = _event_time_ms(lambda: pb._gemm_dgrad(dy, *st, 15, None), reps, torch)
+    t_wgrad = _event_time_ms(lambda: pb._wgrad(dy, xb), reps, torch)
+    gw = pb._wgrad(dy, xb)
+    pk_copy = layer.packed_w.clone()
+    t_vhat = _event_time_ms(lambda: pb.vhat_ema(gw, layer.v_row, layer.v_col, layer._sum_v_inv),
+                            reps, torch)
+
+    def upd():
+        pb.apply_packed_adamw(pk_copy, gw, None, layer.row_exp, layer.col_exp, layer._row_max_buf,
+                              layer._col_max_buf, lr=layer._lr_buf, eps=layer._eps_buf, gf_consol=50.0,
+                              v_scale=0.0, mass_preserve=True, v_row=layer.v_row, v_col=layer.v_col,
+                              sum_v_inv=layer._sum_v_inv, gf_trust_delta_sq=1.0, coh_pre=None,
+                              salt_prebumped=True)
+    t_upd = _event_time_ms(upd, reps, torch)
+    wbuf = torch.empty((N_OUT, K_IN), dtype=torch.bfloat16, device=dev)
+    t_mat = _event_time_ms(lambda: pb.materialize_packed_bf16(layer.packed_w, layer.row_exp,
+                                                              layer.col_exp, wbuf), reps, torch)
+    t_reb = _event_time_ms(layer.rebalance, reps, torch)
+
+    gemm_flop = 2.0 * M_TOK * N_OUT * K_IN
+    fwd_tflops = gemm_flop / (t_fwd * 1e-3) / 1e12
+    params = N_OUT * K_IN
+    upd_gbps = UPDATE_BYTES_PER_PARAM * params / (t_upd * 1e-3) / 1e9
+
+    out = {
+        "metric": "dequant-matmul TFLOP/s (%MFMA peak) + packed-update GB/s (%HBM), SDXL linears",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "sdxl_linear_1280to5120_M2048_fwd_dgrad_wgrad_update_rebalance",
+                   "N": N_OUT, "K": K_IN, "M": M_TOK, "optimizer": "winner (ratio_coh, gf_consol=50)",
+                   "forward": "fused dequant-GEMM", "timing": mode},
+        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<FWD> (dequant-GEMM forward)",
+                     "achieved": round(fwd_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(fwd_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+        "roofline_update": {"bound": "hbm", "kernel": "apply_adamw_kernel<4>",
+                            "achieved": round(upd_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                            "frac": round(upd_gbps / PEAK_HBM_GBPS, 4), "traffic": None,
+                            "bytes_per_param": UPDATE_BYTES_PER_PARAM},
+        "kernel_us": {"dqgemm_fwd": round(t_fwd * 1e3, 2), "dqgemm_dgrad": round(t_dgrad * 1e3, 2),
+                      "wgrad": round(t_wgrad * 1e3, 2), "vhat_ema": round(t_vhat * 1e3, 2),
+                      "apply_adamw": round(t_upd * 1e3, 2), "materialize": round(t_mat * 1e3, 2),
+                      "rebalance_nofire": round(t_reb * 1e3, 2)},
+        "gemm_tflops": {"fwd": round(fwd_tflops, 1),
+                        "dgrad": round(gemm_flop / (t_dgrad * 1e-3) / 1e12, 1),
+                        "wgrad": round(gemm_flop / (t_wgrad * 1e-3) / 1e12, 1)},
+        "materialize_GBps": round(DECODE_BYTES_PER_PARAM * params / (t_mat * 1e-3) / 1e9, 1),
+        "wall_s_timed": round(wall, 3),
+    }
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        out["cpu_baseline"] = cpu_baseline(threads)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,67 @@
+"""Build libconcord_amd.so (the gfx950 HIP kernels + C ABI) in-tree.
+
+    python -m concord_amd.build        # or concord_amd.build.build()
+
+Every .hip file under concord_amd/csrc is compiled with hipcc for gfx950 and
+linked into concord_amd/_lib/libconcord_amd.so.  Flags:
+  -ffp-contract=off   the numerical contract forbids FMA contraction;
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                      no v_pk_*_f32 instructions in device code.
+"""
+import glob
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OUT_DIR = os.path.join(HERE, "_lib")
+LIB = os.path.join(OUT_DIR, "libconcord_amd.so")
+ARCH = os.environ.get("CONCORD_OFFLOAD_ARCH", "gfx950")
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CFLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+    "-I" + os.path.join(ROOT, "include"), "-I" + CSRC,
+]
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the device-only feature flag: drop that line
+    err = "\n".join(l for l in r.stderr.splitlines()
+                    if "packed-fp32-ops" not in l and "is not a recognized feature" not in l)
+    if r.returncode != 0:
+        raise RuntimeError(f"command failed: {' '.join(cmd)}\n{err}")
+    return err
+
+
+def build(verbose=False, jobs=8):
+    os.makedirs(OUT_DIR, exist_ok=True)
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    objs = [os.path.join(OUT_DIR, os.path.basename(s)[:-4] + ".o") for s in srcs]
+
+    def compile_one(so):
+        s, o = so
+        return _run([HIPCC] + CFLAGS + ["-c", s, "-o", o])
+
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        for msg in ex.map(compile_one, zip(srcs, objs)):
+            if verbose and msg.strip():
+                print(msg, file=sys.stderr)
+    tmp = LIB + ".tmp"
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp] + objs)
+    os.replace(tmp, LIB)
+    for o in objs:
+        os.remove(o)
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)

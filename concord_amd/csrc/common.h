@@ -1,0 +1,177 @@
+// common.h -- device helpers shared by the gfx950 kernels of the packed path.
+//
+// Numerical conventions (identical on every kernel):
+//  * binary32 +,-,*,/ and sqrt correctly rounded, no FMA contraction (the
+//    library is built with -ffp-contract=off; the __f*_rn intrinsics below
+//    make the intent explicit);
+//  * float -> int32 by v_cvt_i32_f32: truncate, saturate, NaN -> 0;
+//  * int32 arithmetic on the packed fields wraps modulo 2^32;
+//  * fp32 -> bf16 rounds to nearest even (v_cvt_pk_bf16_f32).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "concord_amd.h"
+
+#define CONCORD_DEV __device__ __forceinline__
+
+namespace concord {
+
+// ---- error reporting ----------------------------------------------------
+void set_error(const char* fmt, ...);
+int launch_status(const char* what);
+
+#define CONCORD_CHECK(cond, ...)      \
+  do {                                \
+    if (!(cond)) {                    \
+      ::concord::set_error(__VA_ARGS__); \
+      return CONCORD_EINVAL;          \
+    }                                 \
+  } while (0)
+
+// ---- integer helpers (wrap-around) -----------------------------------------
+CONCORD_DEV int32_t wadd(int32_t a, int32_t b) { return (int32_t)((uint32_t)a + (uint32_t)b); }
+CONCORD_DEV int32_t wsub(int32_t a, int32_t b) { return (int32_t)((uint32_t)a - (uint32_t)b); }
+CONCORD_DEV int32_t wshl(int32_t a, int s) { return (int32_t)((uint32_t)a << s); }
+CONCORD_DEV int32_t clampi(int32_t v, int32_t lo, int32_t hi) { return min(max(v, lo), hi); }
+
+// float -> int32 with the hardware's saturating semantics.
+CONCORD_DEV int32_t f2i(float f) {
+  int32_t r;
+  asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(f));
+  return r;
+}
+
+CONCORD_DEV float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// two floats -> packed bf16x2 (lo = a), round to nearest even.
+CONCORD_DEV uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  bf2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// ---- packed word --------------------------------------------------------------
+// concord/packed_b.py:143-147 (unpack) and 674-678 (pack)
+struct Fields {
+  int32_t sf, ss, vs;
+};
+CONCORD_DEV Fields unpack(int32_t w) {
+  Fields f;
+  f.sf = w >> 16;
+  f.ss = __builtin_amdgcn_sbfe(w, 8, 8);
+  f.vs = __builtin_amdgcn_sbfe(w, 0, 8);
+  return f;
+}
+CONCORD_DEV int32_t pack(int32_t sf, int32_t ss, int32_t vs) {
+  return (int32_t)(((uint32_t)sf << 16) | (((uint32_t)ss & 0xFFu) << 8) | ((uint32_t)vs & 0xFFu));
+}
+
+// ---- the SR hash: concord/packed_b.py:109-117 ------------------------------------
+CONCORD_DEV float hash_uniform(int32_t x, int32_t pos_salt) {
+  int32_t h = x ^ pos_salt;
+  h = h ^ wshl(h, 13);
+  h = h ^ (h >> 17);
+  h = h ^ wshl(h, 5);
+  h = h ^ (h >> 7);
+  return __fmul_rn((float)(h & 0xFFFFFF), 5.9604644775390625e-08f);
+}
+
+// int(floor(d) + (u < d - floor(d))), concord/packed_b.py:596-598
+CONCORD_DEV int32_t sr_tick(float d, float u) {
+  const float fl = floorf(d);
+  const float fr = __fsub_rn(d, fl);
+  return f2i(__fadd_rn(fl, u < fr ? 1.0f : 0.0f));
+}
+
+// ---- Philox4x32-10 as tl.rand (triton/language/random.py:13-44, 127-157) ------
+CONCORD_DEV float tl_rand(int32_t seed, int32_t offset) {
+  uint32_t c0 = (uint32_t)offset, c1 = 0, c2 = 0, c3 = 0;
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 31);  // sign-extended seed
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+    const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+    c0 = hi1 ^ c1 ^ k0;
+    c1 = lo1;
+    c2 = hi0 ^ c3 ^ k1;
+    c3 = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  int32_t x = (int32_t)c0;
+  if (x < 0) x = wsub(-1, x);
+  return __fmul_rn((float)x, 4.6566127342e-10f);
+}
+
+// ---- deterministic (x)^p for p outside {0, 0.5}; same op sequence as
+// oracle_pow_p (atanh-series log2, Taylor exp2) --------------------------------
+CONCORD_DEV float det_log2(float x) {
+  uint32_t u = __float_as_uint(x);
+  int32_t e = 0;
+  if ((u & 0x7F800000u) == 0) {
+    x = __fmul_rn(x, 8388608.0f);
+    u = __float_as_uint(x);
+    e = -23;
+  }
+  e += (int32_t)((u >> 23) & 0xFF) - 127;
+  float m = __uint_as_float((u & 0x007FFFFFu) | 0x3F800000u);
+  if (m > 1.41421356f) {
+    m = __fmul_rn(m, 0.5f);
+    e += 1;
+  }
+  const float t = __fdiv_rn(__fsub_rn(m, 1.0f), __fadd_rn(m, 1.0f));
+  const float t2 = __fmul_rn(t, t);
+  float s = 1.0f / 11.0f;
+  s = __fadd_rn(__fmul_rn(s, t2), 1.0f / 9.0f);
+  s = __fadd_rn(__fmul_rn(s, t2), 1.0f / 7.0f);
+  s = __fadd_rn(__fmul_rn(s, t2), 1.0f / 5.0f);
+  s = __fadd_rn(__fmul_rn(s, t2), 1.0f / 3.0f);
+  s = __fadd_rn(__fmul_rn(s, t2), 1.0f);
+  const float ln_m = __fmul_rn(__fmul_rn(2.0f, t), s);
+  return __fadd_rn((float)e, __fmul_rn(ln_m, 1.44269504f));
+}
+
+CONCORD_DEV float exp2i(int32_t e) {
+  e = min(max(e, -300), 300);
+  return ldexpf(1.0f, e);
+}
+
+CONCORD_DEV float det_exp2(float y) {
+  if (y != y) return y;
+  if (y >= 128.0f) return __builtin_inff();
+  if (y < -150.0f) return 0.0f;
+  const float n = floorf(__fadd_rn(y, 0.5f));
+  const float f = __fsub_rn(y, n);
+  const float z = __fmul_rn(f, 0.693147181f);
+  float p = 1.0f / 40320.0f;
+  p = __fadd_rn(__fmul_rn(p, z), 1.0f / 5040.0f);
+  p = __fadd_rn(__fmul_rn(p, z), 1.0f / 720.0f);
+  p = __fadd_rn(__fmul_rn(p, z), 1.0f / 120.0f);
+  p = __fadd_rn(__fmul_rn(p, z), 1.0f / 24.0f);
+  p = __fadd_rn(__fmul_rn(p, z), 1.0f / 6.0f);
+  p = __fadd_rn(__fmul_rn(p, z), 0.5f);
+  p = __fadd_rn(__fmul_rn(p, z), 1.0f);
+  p = __fadd_rn(__fmul_rn(p, z), 1.0f);
+  const int32_t ni = (int32_t)n;
+  const int32_t a = ni / 2, b = ni - a;
+  return __fmul_rn(__fmul_rn(p, exp2i(a)), exp2i(b));
+}
+
+CONCORD_DEV float pow_p(float x, float p) {
+  if (p == 0.5f) return __fsqrt_rn(x);
+  if (p == 0.0f) return 1.0f;
+  return det_exp2(__fmul_rn(p, det_log2(x)));
+}
+
+// ---- reductions ------------------------------------------------------------------
+CONCORD_DEV int32_t wave_max(int32_t v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace concord

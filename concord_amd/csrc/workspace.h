@@ -1,0 +1,34 @@
+// workspace.h -- layout of the caller-owned workspace.
+//
+// [0, 256)       counters: the v-hat "blocks done" counter and the rebalance
+//                "fired" flag; zero when the workspace is created and zero
+//                again after every call that uses them.
+// [256, total)   scratch shared by the entry points (they run in stream order):
+//                v-hat partials, rebalance decisions, bias-gradient partials.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+namespace concord {
+
+struct Workspace {
+  size_t vhat_counter, reb_fired, scratch, total;
+};
+
+inline Workspace workspace_layout(int64_t N, int64_t K, int64_t M) {
+  auto cd = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+  Workspace w;
+  w.vhat_counter = 0;
+  w.reb_fired = 64;
+  w.scratch = 256;
+  const size_t vhat = (size_t)(cd(K, 64) * N + cd(N, 32) * K) * sizeof(float);
+  const size_t reb = (size_t)(2 * (N + K)) * sizeof(int32_t);
+  const size_t bias = (size_t)(cd(M, 256) * (N > K ? N : K)) * sizeof(float);
+  size_t s = vhat;
+  if (reb > s) s = reb;
+  if (bias > s) s = bias;
+  w.total = w.scratch + ((s + 255) / 256) * 256;
+  return w;
+}
+
+}  // namespace concord

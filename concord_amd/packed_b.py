@@ -1,0 +1,875 @@
+"""ConcordLinearPackedB on MI355X: the packed-weight linear layer whose optimizer
+step runs inside its own backward.
+
+Drop-in for concord/packed_b.py (reference, file:line cited per function).
+Each weight is one int32 word -- s_fast int16 (bits 31..16), s_slow int8
+(15..8), v_slow int8 (7..0) -- on shared per-row/per-column int8 exponents:
+
+    W = (s_fast + 128 s_slow + 128 v_slow) * 2^(row_exp + col_exp - 15)
+
+All compute runs in libconcord_amd.so (hand-written gfx950 kernels, C ABI in
+include/concord_amd.h).  There is no CPU path: layers must live on a ROCm
+device and every compute call raises if the library is missing.
+
+Two forward/dgrad modes, both bit-identical in what they feed the MFMAs:
+  weight_cache=False (default)  fused dequant-GEMM: packed words are decoded
+                                into LDS tiles; no bf16 weight copy is kept.
+  weight_cache=True             the reference's dataflow: the update emits a
+                                bf16 weight_buf (materialize-merge) and the
+                                GEMMs read it.
+"""
+import ctypes
+import math
+
+import torch
+import torch.nn as nn
+
+from . import _lib as C
+
+MANTISSA_BIAS = 15
+INT8_MIN, INT8_MAX = -128, 127
+INT16_MIN, INT16_MAX = -32768, 32767
+S_SLOW_FACTOR = 128
+V_SLOW_FACTOR = 128
+
+
+def compute_drift_cancel_C(alpha, alpha_v_fast, alpha_v_slow=0.0, refit_period=1,
+                           mass_preserve=True):
+    """Drift-cancellation coefficient C* (concord/packed_b.py:52-102).
+
+    L = (1-alpha)/alpha, rho = alpha_v_fast + alpha_v_slow/T_r.  Mass-preserving
+    leak: C* = L*2rho/(1-2rho) (0.018036 at the defaults); legacy:
+    C* = L*rho/(1 - L*alpha_v_fast) (0.00908)."""
+    L = (1.0 - alpha) / max(alpha, 1e-12)
+    rho = alpha_v_fast + alpha_v_slow / max(refit_period, 1)
+    if mass_preserve:
+        rho2 = 2.0 * rho
+        return L * rho2 / (1.0 - rho2)
+    return L * rho / (1.0 - L * alpha_v_fast)
+
+
+# ---------------------------------------------------------------------------
+# Module-global switches (concord/packed_b.py:797-860; prototype additions
+# notebook/src/prototype_packed_b.py:325-353, 1016-1051)
+# ---------------------------------------------------------------------------
+_USE_FIXED_COH = True
+_GATE_GAIN = 1.0
+_COH_WEIGHTED_V = False
+_RATIO_COH = False
+_RATIO_CHASE_FLOOR = 0.9
+_RATIO_LEAK_FLOOR = 0.999
+_PROTO_SEMANTICS = False
+
+
+def set_fixed_coh(enabled):
+    global _USE_FIXED_COH
+    _USE_FIXED_COH = bool(enabled)
+
+
+def set_gate_gain(g):
+    global _GATE_GAIN
+    _GATE_GAIN = float(g)
+
+
+def set_coh_weighted_v(enabled):
+    """Experimental coh_pre-weighted v-hat accumulation (concord/packed_b.py:828-833).
+    Not implemented on this path; enabling it raises."""
+    global _COH_WEIGHTED_V
+    if enabled:
+        raise NotImplementedError(
+            "concord_amd: the coh_pre-weighted v-hat (experimental, default off) is not implemented")
+    _COH_WEIGHTED_V = False
+
+
+def set_ratio_coh(enabled):
+    global _RATIO_COH
+    _RATIO_COH = bool(enabled)
+
+
+def set_ratio_coh_floors(chase, leak):
+    """Per-step floors of the ratio-coherence gates.  The kernels read them from
+    per-device fp32[1] tensors, so a captured graph sees the update
+    (notebook/src/prototype_packed_b.py:1005-1013)."""
+    global _RATIO_CHASE_FLOOR, _RATIO_LEAK_FLOOR
+    _RATIO_CHASE_FLOOR = float(chase)
+    _RATIO_LEAK_FLOOR = float(leak)
+    for t in _CHASE_FLOOR_T.values():
+        t.fill_(_RATIO_CHASE_FLOOR)
+    for t in _LEAK_FLOOR_T.values():
+        t.fill_(_RATIO_LEAK_FLOOR)
+
+
+def set_prototype_semantics(enabled):
+    """Switch the update between concord/packed_b.py:422-703 (False, default) and
+    notebook/src/prototype_packed_b.py:454-778 (True): consolidate-gated
+    chase/leak/decay/weight-emit/watermarks, coherence-gated beta1
+    (+consf*beta1*coh*s_fast instead of -beta1*s_fast) and the v-hat
+    bias-correction factor.  Identical at beta1 = 0, consolidate = 1, v_bc = 1."""
+    global _PROTO_SEMANTICS
+    _PROTO_SEMANTICS = bool(enabled)
+
+
+# ---------------------------------------------------------------------------
+# Per-device device scalars (concord/packed_b.py:315-359; prototype 331-353,
+# 1016-1046)
+# ---------------------------------------------------------------------------
+def _dev_key(device):
+    d = torch.device(device)
+    if d.type == "cuda" and d.index is None:
+        d = torch.device("cuda", torch.cuda.current_device())
+    return str(d)
+
+
+_STEP_COUNTERS = {}
+_LR_SCALAR_CACHE = {}
+_EPS_SCALAR_CACHE = {}
+_CHASE_FLOOR_T = {}
+_LEAK_FLOOR_T = {}
+_CONSOLIDATE_FLAGS = {}
+_V_BC_BUFS = {}
+_REB_SEED_CACHE = {}
+_WORKSPACES = {}
+
+
+def _get_step_counter(device):
+    """The SR salt counter shared by every layer on a device, advanced once per
+    update (concord/packed_b.py:315-322, 910-911)."""
+    key = _dev_key(device)
+    if key not in _STEP_COUNTERS:
+        _STEP_COUNTERS[key] = torch.zeros(1, dtype=torch.int32, device=key)
+    return _STEP_COUNTERS[key]
+
+
+def _scalar_tensor(cache, value, device, dtype=torch.float32):
+    if isinstance(value, torch.Tensor):
+        return value
+    key = _dev_key(device)
+    buf = cache.get(key)
+    if buf is None:
+        buf = torch.zeros(1, dtype=dtype, device=key)
+        cache[key] = buf
+    buf.fill_(value)
+    return buf
+
+
+def _ensure_lr_tensor(lr, device):
+    return _scalar_tensor(_LR_SCALAR_CACHE, float(lr) if not isinstance(lr, torch.Tensor) else lr, device)
+
+
+def _ensure_eps_tensor(eps, device):
+    return _scalar_tensor(_EPS_SCALAR_CACHE, float(eps) if not isinstance(eps, torch.Tensor) else eps, device)
+
+
+def _ensure_floor_tensors(device):
+    key = _dev_key(device)
+    if key not in _CHASE_FLOOR_T:
+        _CHASE_FLOOR_T[key] = torch.full((1,), _RATIO_CHASE_FLOOR, dtype=torch.float32, device=key)
+        _LEAK_FLOOR_T[key] = torch.full((1,), _RATIO_LEAK_FLOOR, dtype=torch.float32, device=key)
+    return _CHASE_FLOOR_T[key], _LEAK_FLOOR_T[key]
+
+
+def _get_consolidate_flag(device):
+    key = _dev_key(device)
+    if key not in _CONSOLIDATE_FLAGS:
+        _CONSOLIDATE_FLAGS[key] = torch.ones(1, dtype=torch.int32, device=key)
+    return _CONSOLIDATE_FLAGS[key]
+
+
+def set_consolidate(device, consolidate):
+    """Gradient-accumulation gate (notebook/src/prototype_packed_b.py:348-353):
+    False for the first micro-steps of a cycle (tick-only), True for the last.
+    Turns on the prototype update semantics.  With weight_cache=False the
+    forward decodes the live words, so use weight_cache=True to keep the
+    forward weights frozen through a cycle as the prototype does."""
+    set_prototype_semantics(True)
+    _get_consolidate_flag(device).fill_(1 if consolidate else 0)
+
+
+def _v_bc_buf(device):
+    key = _dev_key(device)
+    if key not in _V_BC_BUFS:
+        _V_BC_BUFS[key] = torch.ones(1, dtype=torch.float32, device=key)
+    return _V_BC_BUFS[key]
+
+
+def set_v_bias_correction(factor):
+    """Fill the per-device v-hat bias-correction factor 1/(1-beta2^t)
+    (notebook/src/prototype_packed_b.py:1042-1046); turns on the prototype
+    update semantics."""
+    set_prototype_semantics(True)
+    for buf in _V_BC_BUFS.values():
+        buf.fill_(float(factor))
+
+
+def bias_correction_factor(step, beta2=0.999):
+    return 1.0 / (1.0 - beta2 ** (int(step) + 1))
+
+
+def _ensure_reb_seed_tensor(device):
+    key = _dev_key(device)
+    if key not in _REB_SEED_CACHE:
+        _REB_SEED_CACHE[key] = torch.zeros(1, dtype=torch.int32, device=key)
+    return _REB_SEED_CACHE[key]
+
+
+def _workspace(device, N, K):
+    """Zero-initialised per-device workspace, grown to the largest layer."""
+    key = _dev_key(device)
+    need = int(C.lib().concord_workspace_bytes(int(N), int(K), 0))
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=key)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+# ---------------------------------------------------------------------------
+# Rebalance statistics (concord/packed_b.py:1098-1111)
+# ---------------------------------------------------------------------------
+_REB_STATS = None
+
+
+def reset_reb_stats():
+    global _REB_STATS
+    _REB_STATS = dict(calls=0, tickup_dim=0, tickdown_dim=0, dim_total=0,
+                      clip_elems=0, elem_total=0)
+
+
+def get_reb_stats():
+    return _REB_STATS
+
+
+# ---------------------------------------------------------------------------
+# Launch wrappers (same names and argument meaning as the reference)
+# ---------------------------------------------------------------------------
+def _check_packed(packed_w, row_exp, col_exp):
+    C.require_device_tensor(packed_w, "packed_w")
+    if packed_w.dtype != torch.int32 or packed_w.dim() != 2 or packed_w.stride(1) != 1:
+        raise AssertionError("packed_w must be a row-major [N, K] int32 tensor")
+    N, K = packed_w.shape
+    if row_exp.dtype != torch.int8 or col_exp.dtype != torch.int8:
+        raise AssertionError("row_exp / col_exp must be int8")
+    if row_exp.numel() != N or col_exp.numel() != K:
+        raise AssertionError("row_exp / col_exp sizes do not match packed_w")
+    return N, K
+
+
+def materialize_packed_bf16(packed_w, row_exp, col_exp, out, mantissa_bias=15,
+                            consolidated=False):
+    """bf16 decode of the packed state into `out` (concord/packed_b.py:158-170;
+    consolidated=True drops s_fast as consolidated_weight does, 1632-1649)."""
+    N, K = _check_packed(packed_w, row_exp, col_exp)
+    assert out.dtype == torch.bfloat16 and tuple(out.shape) == (N, K) and out.stride(1) == 1
+    C.check(C.lib().concord_materialize(
+        C.ptr(packed_w), packed_w.stride(0), C.ptr(row_exp), C.ptr(col_exp), N, K,
+        int(mantissa_bias), int(bool(consolidated)), C.ptr(out), out.stride(0),
+        C.stream_of(packed_w.device)), "materialize_packed_bf16")
+    return out
+
+
+def apply_packed_sgd(packed_w, grad_W, weight_buf, row_exp, col_exp, row_max, col_max,
+                     lr, mantissa_bias=15, alpha=0.1, beta1=0.0, alpha_v_fast=0.001,
+                     mass_preserve=False, track_rebalance=True, salt_prebumped=False):
+    """SGD update (concord/packed_b.py:362-394); weight_buf may be None (no emit)."""
+    N, K = _check_packed(packed_w, row_exp, col_exp)
+    assert grad_W.dtype == torch.bfloat16 and tuple(grad_W.shape) == (N, K) and grad_W.stride(1) == 1
+    dev = packed_w.device
+    flags = (C.MASS_PRESERVE if mass_preserve else 0) | (C.TRACK_REBALANCE if track_rebalance else 0)
+    if weight_buf is not None:
+        assert weight_buf.dtype == torch.bfloat16 and tuple(weight_buf.shape) == (N, K)
+        flags |= C.EMIT_WEIGHT
+    if salt_prebumped:
+        flags |= C.SALT_PREBUMPED
+    lr_t = _ensure_lr_tensor(lr, dev)
+    C.check(C.lib().concord_apply_sgd(
+        C.ptr(packed_w), packed_w.stride(0), C.ptr(grad_W), grad_W.stride(0),
+        C.ptr(weight_buf), weight_buf.stride(0) if weight_buf is not None else K,
+        C.ptr(row_exp), C.ptr(col_exp), C.ptr(row_max), C.ptr(col_max), N, K, C.ptr(lr_t),
+        int(mantissa_bias), float(alpha), float(beta1), float(alpha_v_fast),
+        C.ptr(_get_step_counter(dev)), flags, C.stream_of(dev)), "apply_packed_sgd")
+
+
+def _adamw_flags(mass_preserve, apply_chase, track_rebalance, gf_trust_delta_sq, gf_consol,
+                 coh_pre, emit):
+    f = 0
+    if mass_preserve:
+        f |= C.MASS_PRESERVE
+    if apply_chase:
+        f |= C.APPLY_CHASE
+    if track_rebalance:
+        f |= C.TRACK_REBALANCE
+    if gf_trust_delta_sq > 0:
+        f |= C.GF_TRUST_REGION
+    if gf_consol > 0:
+        f |= C.GF_CONSOLIDATION
+    if coh_pre is not None:
+        f |= C.COHPRE
+    if _USE_FIXED_COH:
+        f |= C.FIXED_COH
+    if _RATIO_COH:
+        f |= C.RATIO_COH
+    if emit:
+        f |= C.EMIT_WEIGHT
+    if _PROTO_SEMANTICS:
+        f |= C.PROTO_CONSF
+    return f
+
+
+def apply_packed_adamw(packed_w, grad_W, weight_buf, row_exp, col_exp, row_max, col_max,
+                       lr, mantissa_bias=15, alpha=0.1, beta1=0.0, weight_decay=0.0, eps=1.0,
+                       step_cap=10.0, v_scale=1.0, precond_p=0.5, gf_consol=0.0,
+                       drift_cancel_C=None, alpha_v_fast=0.001, wd_sv=0.0, wd_sf=0.0,
+                       mass_preserve=False, apply_chase=True, track_rebalance=True,
+                       v_row=None, v_col=None, sum_v_inv=None, gf_trust_delta_sq=0.0,
+                       coh_pre=None, salt_prebumped=False, drive_muon=False):
+    """The packed optimizer update (concord/packed_b.py:863-951).  weight_buf may be
+    None (fused-forward mode: no bf16 emit).  drive_muon: grad_W carries the
+    Muon drive and the update uses it as the step (docs/MUON_IMPLEMENTATION.md:87-119)."""
+    if drift_cancel_C is None:
+        drift_cancel_C = compute_drift_cancel_C(alpha, alpha_v_fast, mass_preserve=mass_preserve)
+    N, K = _check_packed(packed_w, row_exp, col_exp)
+    assert grad_W.dtype == torch.bfloat16 and tuple(grad_W.shape) == (N, K) and grad_W.stride(1) == 1
+    dev = packed_w.device
+    use_vhat = gf_trust_delta_sq > 0 or gf_consol > 0 or coh_pre is not None or _RATIO_COH
+    if use_vhat:
+        assert v_row is not None and v_col is not None and sum_v_inv is not None, \
+            "gf_trust/gf_consol/coh_pre/ratio_coh require v_row, v_col, sum_v_inv"
+    flags = _adamw_flags(mass_preserve, apply_chase, track_rebalance, gf_trust_delta_sq,
+                         gf_consol, coh_pre, weight_buf is not None)
+    if salt_prebumped:
+        flags |= C.SALT_PREBUMPED
+    if drive_muon:
+        flags |= C.MUON
+    if weight_buf is not None:
+        assert weight_buf.dtype == torch.bfloat16 and tuple(weight_buf.shape) == (N, K)
+    if coh_pre is not None:
+        assert coh_pre.dtype == torch.float32 and tuple(coh_pre.shape) == (N, K)
+    lr_t = _ensure_lr_tensor(lr, dev)
+    eps_t = _ensure_eps_tensor(eps, dev)
+    cf, lf = _ensure_floor_tensors(dev)
+    P = C.UpdateParams(alpha=alpha, beta1=beta1, weight_decay=weight_decay, step_cap=step_cap,
+                       v_scale=v_scale, precond_p=precond_p, gf_consol=gf_consol,
+                       drift_cancel_C=drift_cancel_C, alpha_v_fast=alpha_v_fast, wd_sv=wd_sv,
+                       wd_sf=wd_sf, gf_trust_delta_sq=gf_trust_delta_sq, gate_gain=_GATE_GAIN,
+                       mantissa_bias=int(mantissa_bias))
+    S = C.DeviceScalars(lr_t.data_ptr(), eps_t.data_ptr(), cf.data_ptr(), lf.data_ptr(),
+                        _v_bc_buf(dev).data_ptr(), _get_step_counter(dev).data_ptr(),
+                        _get_consolidate_flag(dev).data_ptr())
+    C.check(C.lib().concord_apply_adamw(
+        C.ptr(packed_w), packed_w.stride(0), C.ptr(grad_W), grad_W.stride(0),
+        C.ptr(weight_buf), weight_buf.stride(0) if weight_buf is not None else K,
+        C.ptr(row_exp), C.ptr(col_exp), C.ptr(row_max), C.ptr(col_max),
+        C.ptr(v_row), C.ptr(v_col), C.ptr(sum_v_inv),
+        C.ptr(coh_pre), coh_pre.stride(0) if coh_pre is not None else K, N, K,
+        ctypes.byref(P), ctypes.byref(S), flags, C.stream_of(dev)), "apply_packed_adamw")
+
+
+def vhat_ema(grad_W, v_row, v_col, sum_v_inv, beta2=0.999, row_max=None, col_max=None,
+             salt_counter=None):
+    """v_row/v_col EMA of grad^2 and 1/sum(v_row) in place
+    (concord/packed_b.py:1288-1303); optionally zeroes the watermarks and
+    advances the salt counter for the update that follows."""
+    C.require_device_tensor(grad_W, "grad_W")
+    N, K = grad_W.shape
+    ws = _workspace(grad_W.device, N, K)
+    C.check(C.lib().concord_vhat_ema(
+        C.ptr(grad_W), grad_W.stride(0), N, K, float(beta2), C.ptr(v_row), C.ptr(v_col),
+        C.ptr(sum_v_inv), C.ptr(row_max), C.ptr(col_max), C.ptr(salt_counter), C.ptr(ws),
+        ws.numel(), C.stream_of(grad_W.device)), "vhat_ema")
+
+
+def _reb_stats_update(packed_w, row_exp, col_exp, row_max, col_max, MAX_M, EXP_MAX, EXP_MIN,
+                      allow_tickdown):
+    # diagnostic (concord/packed_b.py:1161-1179): host syncs, off by default
+    N, K = packed_w.shape
+    ss = (packed_w << 16) >> 24
+    vs = (packed_w << 24) >> 24
+    i8mag = torch.maximum(ss.abs(), vs.abs())
+    rmed = i8mag.median(dim=1).values.to(torch.int32)
+    cmed = i8mag.median(dim=0).values.to(torch.int32)
+    re, ce = row_exp.to(torch.int32), col_exp.to(torch.int32)
+    ru = (row_max > MAX_M) & (re < EXP_MAX)
+    cu = (col_max > MAX_M) & (ce < EXP_MAX)
+    if allow_tickdown:
+        rd = (row_max <= MAX_M) & (rmed <= 31) & (re > EXP_MIN)
+        cd = (col_max <= MAX_M) & (cmed <= 31) & (ce > EXP_MIN)
+    else:
+        rd, cd = torch.zeros_like(ru), torch.zeros_like(cu)
+    rt = ru.to(torch.int32) - rd.to(torch.int32)
+    ct = cu.to(torch.int32) - cd.to(torch.int32)
+    lsh = (-(rt[:, None] + ct[None, :])).clamp(min=0).to(torch.float32)
+    clip = ((i8mag.to(torch.float32) * torch.exp2(lsh)) > 127).sum().item()
+    _REB_STATS['calls'] += 1
+    _REB_STATS['tickup_dim'] += int(ru.sum() + cu.sum())
+    _REB_STATS['tickdown_dim'] += int(rd.sum() + cd.sum())
+    _REB_STATS['dim_total'] += N + K
+    _REB_STATS['clip_elems'] += clip
+    _REB_STATS['elem_total'] += N * K
+
+
+def rebalance_packed(packed_w, row_exp, col_exp, row_max, col_max, MAX_M=24000, EXP_MAX=7,
+                     EXP_MIN=-8, seed_buf=None, allow_tickdown=False, row_hwm=None,
+                     col_hwm=None, advance_seed=False):
+    """Exponent ratchet (concord/packed_b.py:1129-1190): tick a row/column
+    exponent up when its watermark exceeds MAX_M (down, if allowed, when the
+    median int8 magnitude is <= 31), SR-shifting the words.  Like the
+    reference, the seed is read, not advanced, unless advance_seed."""
+    N, K = _check_packed(packed_w, row_exp, col_exp)
+    if seed_buf is None:
+        seed_buf = _ensure_reb_seed_tensor(packed_w.device)
+    if _REB_STATS is not None:
+        _reb_stats_update(packed_w, row_exp, col_exp, row_max, col_max, MAX_M, EXP_MAX, EXP_MIN,
+                          allow_tickdown)
+    ws = _workspace(packed_w.device, N, K)
+    C.check(C.lib().concord_rebalance(
+        C.ptr(packed_w), packed_w.stride(0), C.ptr(row_exp), C.ptr(col_exp), C.ptr(row_max),
+        C.ptr(col_max), C.ptr(row_hwm), C.ptr(col_hwm), C.ptr(seed_buf), N, K, int(MAX_M),
+        int(EXP_MAX), int(EXP_MIN), int(bool(allow_tickdown)), int(bool(advance_seed)),
+        C.ptr(ws), ws.numel(), C.stream_of(packed_w.device)), "rebalance_packed")
+
+
+def load_packed(W, packed_w, row_exp, col_exp, exp_min=-8, exp_max=7, mantissa_bias=15,
+                finetune=False):
+    """fp32 weights -> packed state (concord/packed_b.py:1570-1603, 1816-1856)."""
+    N, K = _check_packed(packed_w, row_exp, col_exp)
+    W = W.to(device=packed_w.device, dtype=torch.float32).contiguous()
+    assert tuple(W.shape) == (N, K)
+    C.check(C.lib().concord_load_weights(
+        C.ptr(W), W.stride(0), N, K, int(exp_min), int(exp_max), int(mantissa_bias),
+        int(bool(finetune)), C.ptr(packed_w), packed_w.stride(0), C.ptr(row_exp),
+        C.ptr(col_exp), C.stream_of(packed_w.device)), "load_weights")
+
+
+# ---------------------------------------------------------------------------
+# autograd Function (concord/packed_b.py:1197-1353)
+# ---------------------------------------------------------------------------
+# When set to a list, each backward appends a copy of its bf16 grad_W: lets a
+# checker replay the update from the identical gradient.
+_DEBUG_CAPTURE = None
+
+
+def _gemm_fwd(x2, packed_w, row_exp, col_exp, mantissa_bias, bias, weight_buf):
+    M, K = x2.shape
+    N = (weight_buf if weight_buf is not None else packed_w).shape[0]
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=x2.device)
+    st = C.stream_of(x2.device)
+    if weight_buf is None:
+        C.check(C.lib().concord_dqgemm_fwd(
+            C.ptr(x2), x2.stride(0), C.ptr(packed_w), packed_w.stride(0), C.ptr(row_exp),
+            C.ptr(col_exp), int(mantissa_bias), C.ptr(bias), C.ptr(y), y.stride(0), M, N, K, st),
+            "dqgemm_fwd")
+    else:
+        C.check(C.lib().concord_gemm_bf16_fwd(
+            C.ptr(x2), x2.stride(0), C.ptr(weight_buf), weight_buf.stride(0), C.ptr(bias),
+            C.ptr(y), y.stride(0), M, N, K, st), "gemm_bf16_fwd")
+    return y
+
+
+def _gemm_dgrad(dy, packed_w, row_exp, col_exp, mantissa_bias, weight_buf):
+    M, N = dy.shape
+    K = (weight_buf if weight_buf is not None else packed_w).shape[1]
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dy.device)
+    st = C.stream_of(dy.device)
+    if weight_buf is None:
+        C.check(C.lib().concord_dqgemm_dgrad(
+            C.ptr(dy), dy.stride(0), C.ptr(packed_w), packed_w.stride(0), C.ptr(row_exp),
+            C.ptr(col_exp), int(mantissa_bias), C.ptr(dx), dx.stride(0), M, N, K, st),
+            "dqgemm_dgrad")
+    else:
+        C.check(C.lib().concord_gemm_bf16_dgrad(
+            C.ptr(dy), dy.stride(0), C.ptr(weight_buf), weight_buf.stride(0), C.ptr(dx),
+            dx.stride(0), M, N, K, st), "gemm_bf16_dgrad")
+    return dx
+
+
+def _wgrad(dy, x2):
+    M, N = dy.shape
+    K = x2.shape[1]
+    gw = torch.empty((N, K), dtype=torch.bfloat16, device=dy.device)
+    C.check(C.lib().concord_wgrad(C.ptr(dy), dy.stride(0), C.ptr(x2), x2.stride(0), C.ptr(gw),
+                                  gw.stride(0), M, N, K, C.stream_of(dy.device)), "wgrad")
+    return gw
+
+
+def _bias_grad(dy):
+    M, N = dy.shape
+    need = int(C.lib().concord_workspace_bytes(N, 1, M))
+    scratch = torch.empty(need, dtype=torch.uint8, device=dy.device)
+    out = torch.empty(N, dtype=torch.bfloat16, device=dy.device)
+    C.check(C.lib().concord_bias_grad(C.ptr(dy), dy.stride(0), M, N, C.ptr(out), C.ptr(scratch),
+                                      scratch.numel(), C.stream_of(dy.device)), "bias_grad")
+    return out
+
+
+class FusedConcordLinearPackedB(torch.autograd.Function):
+    """Linear forward; backward = dgrad + wgrad + v-hat EMA + packed update.
+    Same 33 forward arguments as the reference (concord/packed_b.py:1201-1211).
+    weight_buf = None selects the fused dequant-GEMM mode."""
+
+    @staticmethod
+    def forward(ctx, x, packed_w, row_exp, col_exp, bias,
+                lr, alpha, beta1, mantissa_bias,
+                optimizer_kind,
+                weight_decay, eps, step_cap,
+                v_scale, precond_p, gf_consol, drift_cancel_C, alpha_v_fast,
+                wd_sv, wd_sf,
+                mass_preserve, apply_chase, track_rebalance,
+                weight_buf, row_max_buf, col_max_buf,
+                v_row, v_col, sum_v_inv,
+                adafactor_beta2, track_adafactor_v,
+                gf_trust_delta_sq, coh_pre):
+        K = packed_w.shape[1]
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, K)
+        if x2.dtype != torch.bfloat16:
+            x2 = x2.to(torch.bfloat16)
+        x2 = x2.contiguous()
+        bias_bf16 = None
+        if bias is not None:
+            bias_bf16 = bias if bias.dtype == torch.bfloat16 else bias.to(torch.bfloat16)
+            bias_bf16 = bias_bf16.contiguous()
+        y = _gemm_fwd(x2, packed_w, row_exp, col_exp, mantissa_bias, bias_bf16, weight_buf)
+        ctx.save_for_backward(x2)
+        ctx.lead = lead
+        ctx.packed_w, ctx.row_exp, ctx.col_exp = packed_w, row_exp, col_exp
+        ctx.lr, ctx.alpha, ctx.beta1, ctx.mantissa_bias = lr, alpha, beta1, mantissa_bias
+        ctx.optimizer_kind = optimizer_kind
+        ctx.weight_decay, ctx.eps, ctx.step_cap = weight_decay, eps, step_cap
+        ctx.v_scale, ctx.precond_p, ctx.gf_consol = v_scale, precond_p, gf_consol
+        ctx.drift_cancel_C, ctx.alpha_v_fast = drift_cancel_C, alpha_v_fast
+        ctx.wd_sv, ctx.wd_sf = wd_sv, wd_sf
+        ctx.mass_preserve, ctx.apply_chase = mass_preserve, apply_chase
+        ctx.track_rebalance = track_rebalance
+        ctx.has_bias = bias is not None
+        ctx.weight_buf, ctx.row_max_buf, ctx.col_max_buf = weight_buf, row_max_buf, col_max_buf
+        ctx.v_row, ctx.v_col, ctx.sum_v_inv = v_row, v_col, sum_v_inv
+        ctx.adafactor_beta2, ctx.track_adafactor_v = adafactor_beta2, track_adafactor_v
+        ctx.gf_trust_delta_sq, ctx.coh_pre = gf_trust_delta_sq, coh_pre
+        return y.reshape(*lead, y.shape[-1])
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        (x2,) = ctx.saved_tensors
+        N, K = ctx.packed_w.shape
+        dy = grad_y.reshape(-1, N)
+        if dy.dtype != torch.bfloat16:
+            dy = dy.to(torch.bfloat16)
+        dy = dy.contiguous()
+        dev = dy.device
+        # dgrad on the pre-update weight (1263), before the update below
+        grad_x = _gemm_dgrad(dy, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias,
+                             ctx.weight_buf).reshape(*ctx.lead, K)
+        grad_W = _wgrad(dy, x2)
+        if _DEBUG_CAPTURE is not None:
+            _DEBUG_CAPTURE.append(grad_W.clone())
+        salt = _get_step_counter(dev)
+        prebumped = False
+        if ctx.track_adafactor_v and ctx.v_row is not None:
+            # zeroes the watermarks (1281-1283), v-hat EMA (1288-1303), salt + 1 (910-911)
+            vhat_ema(grad_W, ctx.v_row, ctx.v_col, ctx.sum_v_inv, ctx.adafactor_beta2,
+                     ctx.row_max_buf if ctx.track_rebalance else None,
+                     ctx.col_max_buf if ctx.track_rebalance else None, salt)
+            prebumped = True
+        elif ctx.track_rebalance:
+            ctx.row_max_buf.zero_()
+            ctx.col_max_buf.zero_()
+        if ctx.optimizer_kind == 'adamw':
+            apply_packed_adamw(
+                ctx.packed_w, grad_W, ctx.weight_buf, ctx.row_exp, ctx.col_exp,
+                ctx.row_max_buf, ctx.col_max_buf, lr=ctx.lr, mantissa_bias=ctx.mantissa_bias,
+                alpha=ctx.alpha, beta1=ctx.beta1, weight_decay=ctx.weight_decay, eps=ctx.eps,
+                step_cap=ctx.step_cap, v_scale=ctx.v_scale, precond_p=ctx.precond_p,
+                gf_consol=ctx.gf_consol, drift_cancel_C=ctx.drift_cancel_C,
+                alpha_v_fast=ctx.alpha_v_fast, wd_sv=ctx.wd_sv, wd_sf=ctx.wd_sf,
+                mass_preserve=ctx.mass_preserve, apply_chase=ctx.apply_chase,
+                track_rebalance=ctx.track_rebalance, v_row=ctx.v_row, v_col=ctx.v_col,
+                sum_v_inv=ctx.sum_v_inv, gf_trust_delta_sq=ctx.gf_trust_delta_sq,
+                coh_pre=ctx.coh_pre, salt_prebumped=prebumped)
+        else:
+            apply_packed_sgd(
+                ctx.packed_w, grad_W, ctx.weight_buf, ctx.row_exp, ctx.col_exp,
+                ctx.row_max_buf, ctx.col_max_buf, lr=ctx.lr, mantissa_bias=ctx.mantissa_bias,
+                alpha=ctx.alpha, beta1=ctx.beta1, alpha_v_fast=ctx.alpha_v_fast,
+                mass_preserve=ctx.mass_preserve, track_rebalance=ctx.track_rebalance,
+                salt_prebumped=prebumped)
+        grad_bias = _bias_grad(dy) if ctx.has_bias else None
+        return (grad_x, None, None, None, grad_bias,
+                None, None, None, None,
+                None,
+                None, None, None,
+                None, None, None, None, None,
+                None, None,
+                None, None, None,
+                None, None, None,
+                None, None, None,
+                None, None, None, None)
+
+
+# ---------------------------------------------------------------------------
+# nn.Module (concord/packed_b.py:1356-1856)
+# ---------------------------------------------------------------------------
+class ConcordLinearPackedB(nn.Module):
+    """int32 packed weight (int16 s_fast + int8x128 s_slow + int8x128 v_slow) on
+    shared row/column exponents; the optimizer step runs in backward.
+
+    Defaults = the reference's validated production optimizer: adamw, rank-1
+    v-hat (v_scale=0, gf_trust_delta_sq=1, eps=1e-10, precond_p=0.5), fixed
+    coherence gate with coh_pre allocated.  Extra argument: weight_cache
+    (False = fused dequant-GEMM forward/dgrad, no bf16 weight copy)."""
+
+    MANTISSA_BIAS = 15
+    EXP_MIN = -8
+    EXP_MAX = 7
+    MAX_M = 24000
+
+    def __init__(self, in_features, out_features, bias=True, device='cuda', alpha=0.1,
+                 beta1=0.0, lr=0.01, weight_cache=False):
+        super().__init__()
+        device = torch.device(device)
+        if device.type != 'cuda':
+            raise RuntimeError(
+                "concord_amd.ConcordLinearPackedB runs on a ROCm GPU; got device "
+                f"{device}.  There is no CPU implementation of the packed path.")
+        C.lib()
+        self.in_features = in_features
+        self.out_features = out_features
+        self.alpha = alpha
+        self.beta1 = beta1
+        self.weight_cache = bool(weight_cache)
+        self._lr_value = float(lr)
+        self.optimizer_kind = 'adamw'
+        self.weight_decay = 0.0
+        self._eps_value = 1e-10
+        self.step_cap = 10.0
+        self.v_scale = 0.0
+        self.precond_p = 0.5
+        self.gf_consol = 0.0
+        self._coh_pre = None
+        self.fast_gain = 1.0
+        self.alpha_v_fast = 0.001
+        self.drift_cancel_C = compute_drift_cancel_C(alpha, self.alpha_v_fast, mass_preserve=True)
+        self.track_adafactor_v = True
+        self.adafactor_beta2 = 0.999
+        self.gf_trust_delta_sq = 1.0
+        self.allow_tickdown = False
+        self.wd_sv = 0.0
+        self.wd_sf = 0.0
+        self.mass_preserve_v = True
+        self.apply_chase = True
+        self.track_rebalance = True
+        self.register_buffer('_reb_seed', torch.zeros(1, dtype=torch.int32, device=device))
+        self.register_buffer('packed_w', torch.zeros(out_features, in_features, dtype=torch.int32,
+                                                     device=device))
+        self.register_buffer('row_exp', torch.zeros(out_features, dtype=torch.int8, device=device))
+        self.register_buffer('col_exp', torch.zeros(in_features, dtype=torch.int8, device=device))
+        self.register_buffer('v_row', torch.zeros(out_features, dtype=torch.float32, device=device))
+        self.register_buffer('v_col', torch.zeros(in_features, dtype=torch.float32, device=device))
+        self.register_buffer('_sum_v_inv', torch.ones(1, dtype=torch.float32, device=device))
+        self._coh_pre = torch.ones_like(self.packed_w, dtype=torch.float32)
+        self.register_buffer('_row_max_hwm', torch.zeros(out_features, dtype=torch.int32,
+                                                         device=device))
+        self.register_buffer('_col_max_hwm', torch.zeros(in_features, dtype=torch.int32,
+                                                         device=device))
+        self.register_buffer('_lr_buf', torch.full((1,), self._lr_value, dtype=torch.float32,
+                                                   device=device))
+        self.register_buffer('_eps_buf', torch.full((1,), self._eps_value, dtype=torch.float32,
+                                                    device=device))
+        if bias:
+            self.bias = nn.Parameter(torch.zeros(out_features, dtype=torch.bfloat16, device=device))
+        else:
+            self.register_parameter('bias', None)
+        _workspace(device, out_features, in_features)
+        self._init_weight()
+        self._ensure_buffers()
+
+    # -- properties (concord/packed_b.py:1500-1537) --
+    @property
+    def weight(self):
+        """bf16 weight for code that inspects nn.Linear.weight.  With
+        weight_cache=True this is the live buffer the update keeps fresh; in
+        the fused mode it is a snapshot decoded on each access."""
+        wbuf = getattr(self, '_bf16_weight_buf', None)
+        if wbuf is not None:
+            return wbuf
+        return self.get_weight()
+
+    @property
+    def lr(self):
+        return self._lr_value
+
+    @lr.setter
+    def lr(self, value):
+        v = float(value)
+        self._lr_value = v
+        buf = getattr(self, '_lr_buf', None)
+        if buf is not None:
+            buf.fill_(v)
+
+    @property
+    def eps(self):
+        return self._eps_value
+
+    @eps.setter
+    def eps(self, value):
+        v = float(value)
+        self._eps_value = v
+        buf = getattr(self, '_eps_buf', None)
+        if buf is not None:
+            buf.fill_(v)
+
+    # -- knobs (concord/packed_b.py:1539-1568) --
+    @torch.no_grad()
+    def enable_cohpre(self):
+        self._coh_pre = torch.ones_like(self.packed_w, dtype=torch.float32)
+        return self._coh_pre
+
+    @torch.no_grad()
+    def disable_cohpre(self):
+        self._coh_pre = None
+
+    def set_optimizer_kind(self, kind, weight_decay=0.0, eps=1.0, step_cap=10.0):
+        if kind not in ('sgd', 'adamw'):
+            raise ValueError("optimizer kind must be 'sgd' or 'adamw'")
+        self.optimizer_kind = kind
+        self.weight_decay = float(weight_decay)
+        self.eps = float(eps)
+        self.step_cap = float(step_cap)
+
+    def _init_weight(self):
+        std = (2.0 / (self.in_features + self.out_features)) ** 0.5
+        w = torch.randn(self.out_features, self.in_features, device=self.packed_w.device) * std
+        self.load_weights(w)
+
+    @torch.no_grad()
+    def load_weights(self, W):
+        """Whole mantissa into s_fast, row exponents from the row max
+        (concord/packed_b.py:1570-1603)."""
+        load_packed(W, self.packed_w, self.row_exp, self.col_exp, self.EXP_MIN, self.EXP_MAX,
+                    self.MANTISSA_BIAS, finetune=False)
+        self._resync_weight_buf()
+
+    @torch.no_grad()
+    def load_weights_finetune(self, W):
+        """Zero-gradient steady state: half the mantissa in v_slow, the rest in
+        s_slow, the residual in s_fast (concord/packed_b.py:1816-1856)."""
+        load_packed(W, self.packed_w, self.row_exp, self.col_exp, self.EXP_MIN, self.EXP_MAX,
+                    self.MANTISSA_BIAS, finetune=True)
+        self._resync_weight_buf()
+
+    @torch.no_grad()
+    def _resync_weight_buf(self):
+        wbuf = getattr(self, '_bf16_weight_buf', None)
+        if wbuf is not None:
+            materialize_packed_bf16(self.packed_w, self.row_exp, self.col_exp, wbuf,
+                                    self.MANTISSA_BIAS)
+
+    @torch.no_grad()
+    def get_weight(self):
+        """Live bf16 weight decoded from the packed state (1617-1630)."""
+        out = torch.empty(self.packed_w.shape, dtype=torch.bfloat16, device=self.packed_w.device)
+        return materialize_packed_bf16(self.packed_w, self.row_exp, self.col_exp, out,
+                                       self.MANTISSA_BIAS)
+
+    @torch.no_grad()
+    def consolidated_weight(self):
+        """Deploy weight (128 s_slow + 128 v_slow) * 2^exp, s_fast dropped (1632-1649)."""
+        out = torch.empty(self.packed_w.shape, dtype=torch.bfloat16, device=self.packed_w.device)
+        return materialize_packed_bf16(self.packed_w, self.row_exp, self.col_exp, out,
+                                       self.MANTISSA_BIAS, consolidated=True)
+
+    @torch.no_grad()
+    def get_state(self):
+        p = self.packed_w
+        return p >> 16, (p << 16) >> 24, (p << 24) >> 24
+
+    @torch.no_grad()
+    def get_rebalance_watermark_stats(self):
+        if getattr(self, '_row_max_buf', None) is None or not self.track_rebalance:
+            return None, None
+        return self._row_max_hwm.clone(), self._col_max_hwm.clone()
+
+    @torch.no_grad()
+    def get_garbage_fraction_stats(self):
+        """Per-weight garbage fraction quantiles (diagnostic, 1676-1730)."""
+        if float(self.v_row.sum().item()) <= 0.0:
+            return None
+        s_fast, s_slow, v_slow = (t.to(torch.float32) for t in self.get_state())
+        noise = s_fast - float(self.drift_cancel_C) * (s_slow - v_slow) * 128.0
+        exp = (self.row_exp[:, None].to(torch.float32) + self.col_exp[None, :].to(torch.float32)
+               - self.MANTISSA_BIAS)
+        var_W = (noise * torch.pow(2.0, exp)) ** 2
+        sum_v = self.v_row.float().sum().clamp(min=1e-30)
+        v_hat = self.v_row.float()[:, None] * self.v_col.float()[None, :] / sum_v
+        flat = (var_W / (v_hat + 1e-30)).clamp(0.0, 1.0).flatten()
+        q = torch.quantile(flat, torch.tensor([0.25, 0.5, 0.75], device=flat.device))
+        return {'mean': flat.mean().item(), 'p25': q[0].item(), 'median': q[1].item(),
+                'p75': q[2].item(),
+                'frac_signal_dominated': (flat < 0.1).float().mean().item(),
+                'frac_noise_dominated': (flat > 0.9).float().mean().item()}
+
+    def _ensure_buffers(self):
+        N, K = self.packed_w.shape
+        dev = self.packed_w.device
+        wbuf = getattr(self, '_bf16_weight_buf', None)
+        if self.weight_cache and (wbuf is None or wbuf.shape != self.packed_w.shape):
+            wbuf = torch.empty(self.packed_w.shape, dtype=torch.bfloat16, device=dev)
+            self._bf16_weight_buf = wbuf
+            materialize_packed_bf16(self.packed_w, self.row_exp, self.col_exp, wbuf,
+                                    self.MANTISSA_BIAS)
+        if not self.weight_cache:
+            self._bf16_weight_buf = None
+            wbuf = None
+        rmbuf = getattr(self, '_row_max_buf', None)
+        if rmbuf is None or rmbuf.shape[0] != N:
+            self._row_max_buf = rmbuf = torch.zeros(N, dtype=torch.int32, device=dev)
+        cmbuf = getattr(self, '_col_max_buf', None)
+        if cmbuf is None or cmbuf.shape[0] != K:
+            self._col_max_buf = cmbuf = torch.zeros(K, dtype=torch.int32, device=dev)
+        return wbuf, rmbuf, cmbuf
+
+    def forward(self, x):
+        in_dtype = x.dtype
+        if x.dtype != torch.bfloat16:
+            x = x.to(torch.bfloat16)
+        wbuf, rmbuf, cmbuf = self._ensure_buffers()
+        if self.fast_gain < 1.0:
+            # gate s_fast out of the forward weight (1762-1772); the GEMMs then read
+            # the gated bf16 copy, the packed state keeps the full s_fast
+            with torch.no_grad():
+                pw = self.packed_w
+                sf = (pw >> 16).to(torch.float32)
+                ss = ((pw << 16) >> 24).to(torch.float32)
+                vs = ((pw << 24) >> 24).to(torch.float32)
+                exp = (self.row_exp.float()[:, None] + self.col_exp.float()[None, :]
+                       - self.MANTISSA_BIAS)
+                m_gated = (ss * 128.0 + self.fast_gain * sf + vs * 128.0) * torch.exp2(exp)
+                if wbuf is None:
+                    wbuf = torch.empty(pw.shape, dtype=torch.bfloat16, device=pw.device)
+                wbuf.copy_(m_gated.to(torch.bfloat16))
+        y = FusedConcordLinearPackedB.apply(
+            x, self.packed_w, self.row_exp, self.col_exp, self.bias,
+            self._lr_buf, self.alpha, self.beta1, self.MANTISSA_BIAS,
+            self.optimizer_kind,
+            self.weight_decay, self._eps_buf, self.step_cap,
+            self.v_scale, self.precond_p, self.gf_consol, self.drift_cancel_C, self.alpha_v_fast,
+            self.wd_sv, self.wd_sf,
+            self.mass_preserve_v, self.apply_chase, self.track_rebalance,
+            wbuf, rmbuf, cmbuf,
+            self.v_row, self.v_col, self._sum_v_inv,
+            float(self.adafactor_beta2), bool(self.track_adafactor_v),
+            float(self.gf_trust_delta_sq), self._coh_pre)
+        return y.to(in_dtype)
+
+    @torch.no_grad()
+    def rebalance(self):
+        """Watermarks -> high-watermarks, seed + 1, exponent ratchet (1792-1814).
+        Entirely on device; no host synchronisation."""
+        rmbuf = getattr(self, '_row_max_buf', None)
+        cmbuf = getattr(self, '_col_max_buf', None)
+        if rmbuf is None or cmbuf is None:
+            return
+        rebalance_packed(self.packed_w, self.row_exp, self.col_exp, rmbuf, cmbuf,
+                         MAX_M=self.MAX_M, EXP_MAX=self.EXP_MAX, EXP_MIN=self.EXP_MIN,
+                         seed_buf=self._reb_seed, allow_tickdown=self.allow_tickdown,
+                         row_hwm=self._row_max_hwm, col_hwm=self._col_max_hwm,
+                         advance_seed=True)

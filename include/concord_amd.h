@@ -1,0 +1,192 @@
+/*
+ * concord_amd.h -- C ABI of the MI355X (gfx950) packed-weight linear path.
+ *
+ * Every entry point takes raw device pointers, sizes and leading dimensions,
+ * plus the hipStream_t (passed as void*) to enqueue on.  No entry point
+ * allocates device memory, synchronises the host or reads device values back
+ * to the host, so every call is asynchronous and can be captured into a HIP
+ * graph.  Scratch space is a caller-owned workspace (concord_workspace_bytes).
+ *
+ * Tensors are row-major with an explicit leading dimension (elements):
+ *   packed  int32 [N, ld_p]   one word per weight: s_fast int16 in bits 31..16,
+ *                             s_slow int8 in 15..8, v_slow int8 in 7..0
+ *   row_exp int8  [N], col_exp int8 [K]
+ *   live weight  W[n,k] = (s_fast + 128 s_slow + 128 v_slow) * 2^(row_exp[n] + col_exp[k] - mantissa_bias)
+ *   bf16 tensors are passed as uint16_t bit patterns.
+ *
+ * Return value: CONCORD_OK (0) or a negative CONCORD_E* code; the message of
+ * the last failure on the calling thread is returned by concord_last_error().
+ *
+ * Reference citations are relative to the reference repository root.
+ */
+#ifndef CONCORD_AMD_H
+#define CONCORD_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CONCORD_OK 0
+#define CONCORD_EINVAL (-1)     /* bad argument (null pointer, size, stride, flag) */
+#define CONCORD_ELAUNCH (-2)    /* a kernel launch failed */
+#define CONCORD_EWORKSPACE (-3) /* workspace missing or too small */
+
+/* Update flags (concord/packed_b.py:451-458 constexprs, plus this build's). */
+#define CONCORD_MASS_PRESERVE (1u << 0)
+#define CONCORD_APPLY_CHASE (1u << 1)
+#define CONCORD_TRACK_REBALANCE (1u << 2)
+#define CONCORD_GF_TRUST_REGION (1u << 3)
+#define CONCORD_GF_CONSOLIDATION (1u << 4)
+#define CONCORD_COHPRE (1u << 5)
+#define CONCORD_FIXED_COH (1u << 6)
+#define CONCORD_RATIO_COH (1u << 7)
+#define CONCORD_EMIT_WEIGHT (1u << 8)   /* write the bf16 live weight (materialize-merge) */
+#define CONCORD_PROTO_CONSF (1u << 9)   /* notebook/src/prototype_packed_b.py:454-778 semantics */
+#define CONCORD_MUON (1u << 10)         /* step = supplied drive (docs/MUON_IMPLEMENTATION.md:87-119) */
+#define CONCORD_SALT_PREBUMPED (1u << 16) /* the caller already advanced the salt counter */
+
+/* Launch-time scalars of the update (concord/packed_b.py:436-445). */
+typedef struct concord_update_params {
+  float alpha, beta1, weight_decay, step_cap, v_scale, precond_p;
+  float gf_consol, drift_cancel_C, alpha_v_fast, wd_sv, wd_sf;
+  float gf_trust_delta_sq, gate_gain;
+  int32_t mantissa_bias;
+} concord_update_params;
+
+/* Per-step scalars read from device memory so that a captured graph sees
+ * their current values (concord/packed_b.py:462-468; prototype 474-485).
+ * lr, eps: fp32[1]; chase_floor, leak_floor, v_bc: fp32[1] (may be NULL when
+ * RATIO_COH / PROTO_CONSF are off); salt_counter: int32[1], advanced by one on
+ * device before each update unless CONCORD_SALT_PREBUMPED; consolidate:
+ * int32[1] (NULL = 1). */
+typedef struct concord_device_scalars {
+  const float* lr;
+  const float* eps;
+  const float* chase_floor;
+  const float* leak_floor;
+  const float* v_bc;
+  int32_t* salt_counter;
+  const int32_t* consolidate;
+} concord_device_scalars;
+
+const char* concord_last_error(void);
+int concord_version(void);
+
+/* Bytes of caller-owned workspace the entry points below need for a layer of
+ * N x K weights and M activation rows.  The workspace must be zero-filled
+ * once when allocated; every call leaves its counters at zero again. */
+size_t concord_workspace_bytes(int64_t N, int64_t K, int64_t M);
+
+/* salt_counter[0] += 1 on device.  Replaces step_counter.add_(1),
+ * concord/packed_b.py:910-911. */
+int concord_salt_bump(int32_t* salt_counter, void* stream);
+
+/* bf16 decode of the packed state.  consolidated = 0: live weight
+ * (_materialize_packed_bf16_kernel, concord/packed_b.py:120-170; get_weight
+ * 1617-1630).  consolidated = 1: deploy weight without s_fast
+ * (consolidated_weight, concord/packed_b.py:1632-1649). */
+int concord_materialize(const int32_t* packed, int64_t ld_p, const int8_t* row_exp,
+                        const int8_t* col_exp, int64_t N, int64_t K, int32_t mantissa_bias,
+                        int consolidated, uint16_t* out, int64_t ld_out, void* stream);
+
+/* The packed optimizer update with a supplied bf16 gradient: apply_packed_adamw
+ * + _apply_packed_adamw_kernel, concord/packed_b.py:863-951 and 422-703
+ * (prototype extension notebook/src/prototype_packed_b.py:454-778 under
+ * CONCORD_PROTO_CONSF).  Mutates packed (and coh_pre, weight_buf, row_max,
+ * col_max) in place; row_max/col_max receive atomic maxima and must be
+ * zeroed by the caller (or by concord_vhat_ema). */
+int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t* grad, int64_t ld_g,
+                        uint16_t* weight_buf, int64_t ld_w, const int8_t* row_exp,
+                        const int8_t* col_exp, int32_t* row_max, int32_t* col_max,
+                        const float* v_row, const float* v_col, const float* sum_v_inv,
+                        float* coh_pre, int64_t ld_c, int64_t N, int64_t K,
+                        const concord_update_params* params,
+                        const concord_device_scalars* scalars, uint32_t flags, void* stream);
+
+/* SGD path: apply_packed_sgd + _apply_packed_sgd_kernel,
+ * concord/packed_b.py:362-394 and 173-312.  flags: MASS_PRESERVE,
+ * TRACK_REBALANCE, EMIT_WEIGHT, SALT_PREBUMPED. */
+int concord_apply_sgd(int32_t* packed, int64_t ld_p, const uint16_t* grad, int64_t ld_g,
+                      uint16_t* weight_buf, int64_t ld_w, const int8_t* row_exp,
+                      const int8_t* col_exp, int32_t* row_max, int32_t* col_max, int64_t N,
+                      int64_t K, const float* lr, int32_t mantissa_bias, float alpha,
+                      float beta1, float alpha_v_fast, int32_t* salt_counter, uint32_t flags,
+                      void* stream);
+
+/* AdaFactor rank-1 second moment of a bf16 gradient, in place:
+ * v_row = b2 v_row + (1-b2) sum_k g^2, v_col likewise, sum_v_inv =
+ * 1/max(sum v_row, 1e-30) (FusedConcordLinearPackedB.backward,
+ * concord/packed_b.py:1288-1303), in the fixed reduction order of
+ * oracle_vhat_ema; b2 = (float)beta2 and 1-b2 = (float)(1 - beta2) as torch
+ * forms them from a Python float.  When row_max/col_max are non-NULL they are zeroed
+ * (1281-1283); when salt_counter is non-NULL it is advanced by one, so the
+ * following concord_apply_adamw takes CONCORD_SALT_PREBUMPED. */
+int concord_vhat_ema(const uint16_t* grad, int64_t ld_g, int64_t N, int64_t K, double beta2,
+                     float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max,
+                     int32_t* col_max, int32_t* salt_counter, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* rebalance(): ConcordLinearPackedB.rebalance + rebalance_packed +
+ * _rebalance_packed_decide_kernel, concord/packed_b.py:1792-1814, 1129-1190,
+ * 959-1095.  Folds row_max/col_max into the high-watermarks (when non-NULL),
+ * advances seed[0] when advance_seed != 0 (rebalance() does, rebalance_packed
+ * does not: concord/packed_b.py:1808), decides per-row/column exponent ticks from the
+ * pre-call exponents, SR-shifts the fired words and updates the exponents.
+ * A call where nothing fires touches O(N + K) memory. */
+int concord_rebalance(int32_t* packed, int64_t ld_p, int8_t* row_exp, int8_t* col_exp,
+                      const int32_t* row_max, const int32_t* col_max, int32_t* row_hwm,
+                      int32_t* col_hwm, int32_t* seed, int64_t N, int64_t K, int32_t max_m,
+                      int32_t exp_max, int32_t exp_min, int allow_tickdown, int advance_seed,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
+/* load_weights / load_weights_finetune (concord/packed_b.py:1570-1603,
+ * 1816-1856): fp32 W[N, ld_w] -> packed state, row_exp, col_exp = 0. */
+int concord_load_weights(const float* W, int64_t ld_w, int64_t N, int64_t K, int32_t exp_min,
+                         int32_t exp_max, int32_t mantissa_bias, int finetune, int32_t* packed,
+                         int64_t ld_p, int8_t* row_exp, int8_t* col_exp, void* stream);
+
+/* Dequant-GEMM forward: y[M,N] = x[M,K] . decode(packed)[N,K]^T (+ bias[N]),
+ * bf16 in/out, fp32 accumulation on bf16 MFMA.  Replaces
+ * F.linear(x, weight_buf, bias), concord/packed_b.py:1216-1219.  bias may be
+ * NULL. */
+int concord_dqgemm_fwd(const uint16_t* x, int64_t ld_x, const int32_t* packed, int64_t ld_p,
+                       const int8_t* row_exp, const int8_t* col_exp, int32_t mantissa_bias,
+                       const uint16_t* bias, uint16_t* y, int64_t ld_y, int64_t M, int64_t N,
+                       int64_t K, void* stream);
+
+/* Dequant-GEMM dgrad: dx[M,K] = dy[M,N] . decode(packed)[N,K], on the
+ * pre-update weight.  Replaces grad_y @ weight, concord/packed_b.py:1263. */
+int concord_dqgemm_dgrad(const uint16_t* dy, int64_t ld_dy, const int32_t* packed, int64_t ld_p,
+                         const int8_t* row_exp, const int8_t* col_exp, int32_t mantissa_bias,
+                         uint16_t* dx, int64_t ld_dx, int64_t M, int64_t N, int64_t K,
+                         void* stream);
+
+/* wgrad: grad_w[N,K] = bf16(dy[M,N]^T . x[M,K]) with fp32 accumulation.
+ * Replaces grad_y_flat.T @ x_flat, concord/packed_b.py:1269-1277. */
+int concord_wgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t ld_x,
+                  uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
+                  void* stream);
+
+/* The forward and dgrad products over a materialised bf16 weight w[N,K]: the
+ * reference's cached weight_buf path, F.linear(x, weight_buf, bias) and
+ * grad_y @ weight_buf (concord/packed_b.py:1219, 1263). */
+int concord_gemm_bf16_fwd(const uint16_t* x, int64_t ld_x, const uint16_t* w, int64_t ld_w,
+                          const uint16_t* bias, uint16_t* y, int64_t ld_y, int64_t M, int64_t N,
+                          int64_t K, void* stream);
+int concord_gemm_bf16_dgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* w, int64_t ld_w,
+                            uint16_t* dx, int64_t ld_dx, int64_t M, int64_t N, int64_t K,
+                            void* stream);
+
+/* grad_bias[N] = bf16(sum_m dy[m, n]) with fp32 accumulation.  Replaces
+ * grad_y_flat.sum(0), concord/packed_b.py:1338-1340. */
+int concord_bias_grad(const uint16_t* dy, int64_t ld_dy, int64_t M, int64_t N,
+                      uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,625 @@
+"""GPU parity of every kernel of the packed path, through the C ABI.
+
+Integer / byte results (packed words, exponents, watermarks, bf16 decodes,
+coh_pre, v-hat) must be bit-exact against the CPU oracle and, where the
+reference's own golden vectors exist, against those.  GEMM outputs must be
+within rel-L2 <= 1e-2 of an fp32 dense product on the same bf16 operands.
+"""
+import glob
+import os
+import zlib
+
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import DEV, dev, host, rand_grad_bits, rand_state, rel_l2, sync
+
+pytestmark = pytest.mark.gpu
+
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(autouse=True)
+def _reset_globals():
+    from concord_amd import packed_b as pb
+    yield
+    pb.set_fixed_coh(True)
+    pb.set_gate_gain(1.0)
+    pb.set_ratio_coh(False)
+    pb.set_ratio_coh_floors(0.9, 0.999)
+    pb.set_prototype_semantics(False)
+    for t in pb._CONSOLIDATE_FLAGS.values():
+        t.fill_(1)
+    for t in pb._V_BC_BUFS.values():
+        t.fill_(1.0)
+
+
+def _set_salt(salt_next):
+    from concord_amd import packed_b as pb
+    pb._get_step_counter(DEV).fill_(int(salt_next) - 1)
+
+
+# ---------------------------------------------------------------- decode
+
+
+@pytest.mark.parametrize("N,K", [(37, 93), (256, 2048), (5, 2049), (300, 130)])
+@pytest.mark.parametrize("consolidated", [False, True])
+def test_materialize(oracle, N, K, consolidated):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(N * 7 + K)
+    packed, re, ce = rand_state(rng, N, K, sf=(-32768, 32768), exp=(-8, 7), col=(-8, 7))
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=DEV)
+    pb.materialize_packed_bf16(dev(packed), dev(re), dev(ce), out, consolidated=consolidated)
+    np.testing.assert_array_equal(host(out), oracle.materialize(packed, re, ce, consolidated=consolidated))
+
+
+def test_materialize_strided(oracle):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(1)
+    N, K = 40, 100
+    big, re, ce = rand_state(rng, N, K + 13, exp=(-8, 7), col=(-8, 7))
+    ce = ce[:K].copy()
+    pk = dev(big)[:, :K]
+    out_full = torch.zeros((N, K + 5), dtype=torch.bfloat16, device=DEV)
+    out = out_full[:, :K]
+    from concord_amd import _lib as C
+    C.check(C.lib().concord_materialize(C.ptr(pk), pk.stride(0), C.ptr(dev(re)), C.ptr(dev(ce)), N, K,
+                                        15, 0, C.ptr(out), out.stride(0), C.stream_of(DEV)), "mat")
+    sync()
+    np.testing.assert_array_equal(host(out), oracle.materialize(np.ascontiguousarray(big[:, :K]), re, ce))
+
+
+# ---------------------------------------------------------------- update
+
+
+def _adamw_flags_from_fixture(pb, z):
+    s = lambda k: int(z["s_" + k])  # noqa: E731
+    pb.set_fixed_coh(bool(s("fixed_coh")))
+    pb.set_gate_gain(float(z["s_gate_gain"]))
+    pb.set_ratio_coh(bool(s("ratio_coh")))
+    pb.set_ratio_coh_floors(float(z["s_chase_floor"]), float(z["s_leak_floor"]))
+    pb.set_prototype_semantics(bool(s("proto")))
+    pb._get_consolidate_flag(DEV).fill_(s("consolidate"))
+    pb._v_bc_buf(DEV).fill_(float(z["s_v_bc"]))
+
+
+ADAMW_CASES = sorted(os.path.basename(p)[6:-4] for p in glob.glob(os.path.join(GOLD, "adamw_*.npz")))
+
+
+@pytest.mark.parametrize("case", ADAMW_CASES)
+def test_apply_adamw_matches_reference_golden(oracle, case):
+    """GPU update on the reference's own inputs == the reference's own outputs."""
+    from concord_amd import packed_b as pb
+    z = np.load(os.path.join(GOLD, f"adamw_{case}.npz"))
+    N, K = z["packed"].shape
+    _adamw_flags_from_fixture(pb, z)
+    _set_salt(int(z["s_salt"]))
+    pk = dev(z["packed"])
+    wbuf = torch.zeros((N, K), dtype=torch.bfloat16, device=DEV)
+    rm = torch.zeros(N, dtype=torch.int32, device=DEV)
+    cm = torch.zeros(K, dtype=torch.int32, device=DEV)
+    cp = dev(z["coh_pre"].reshape(N, K)) if z["coh_pre"].size else None
+    pb.apply_packed_adamw(
+        pk, dev(z["grad"]), wbuf, dev(z["row_exp"]), dev(z["col_exp"]), rm, cm,
+        lr=float(z["s_lr"]), alpha=float(z["s_alpha"]), beta1=float(z["s_beta1"]),
+        weight_decay=float(z["s_weight_decay"]), eps=float(z["s_eps"]), step_cap=float(z["s_step_cap"]),
+        v_scale=float(z["s_v_scale"]), gf_consol=float(z["s_gf_consol"]),
+        drift_cancel_C=float(z["s_drift_cancel_C"]), alpha_v_fast=float(z["s_alpha_v_fast"]),
+        wd_sv=float(z["s_wd_sv"]), wd_sf=float(z["s_wd_sf"]),
+        mass_preserve=bool(int(z["s_mass_preserve"])), apply_chase=bool(int(z["s_apply_chase"])),
+        track_rebalance=bool(int(z["s_track"])), v_row=dev(z["v_row"]), v_col=dev(z["v_col"]),
+        sum_v_inv=dev(z["sum_v_inv"]), gf_trust_delta_sq=float(z["s_gf_trust_delta_sq"]), coh_pre=cp)
+    sync()
+    np.testing.assert_array_equal(host(pk), z["packed_out"])
+    np.testing.assert_array_equal(host(rm), z["row_max"])
+    np.testing.assert_array_equal(host(cm), z["col_max"])
+    if cp is not None:
+        np.testing.assert_array_equal(host(cp), z["coh_pre_out"].reshape(N, K))
+    if int(z["s_consolidate"]) == 1 or not int(z["s_proto"]):
+        want = oracle.materialize(z["packed_out"], z["row_exp"], z["col_exp"])
+        np.testing.assert_array_equal(host(wbuf), want)
+    else:
+        assert not host(wbuf).any()
+
+
+FLAG_SETS = {
+    "bare": dict(cohpre=True),
+    "winner": dict(ratio=True, gf_consol=50.0),
+    "proto_accum": dict(ratio=True, gf_consol=50.0, proto=True, consolidate=0, beta1=0.1),
+    "proto_cons": dict(ratio=True, gf_consol=30.0, proto=True, consolidate=1, beta1=0.1, v_bc=1.5),
+    "wd_all": dict(cohpre=True, fixed=False, weight_decay=0.02, wd_sv=0.3, wd_sf=0.2, beta1=0.05,
+                   v_scale=1.0, gate_gain=0.7, eps=1.0),
+    "muon": dict(ratio=True, gf_consol=10.0, muon=True),
+    "pow": dict(cohpre=True, precond_p=0.3),
+    "sgdlike": dict(precond_p=0.0, trust=0.0, chase=False, track=False, mp=False),
+}
+
+
+@pytest.mark.parametrize("name", sorted(FLAG_SETS))
+@pytest.mark.parametrize("N,K", [(130, 300), (512, 1280), (33, 1030)])
+def test_apply_adamw_matches_oracle(oracle, name, N, K):
+    from concord_amd import packed_b as pb
+    O = oracle
+    f = FLAG_SETS[name]
+    rng = np.random.default_rng(zlib.crc32(f"{name}-{N}-{K}".encode()))
+    packed, re, ce = rand_state(rng, N, K, exp=(-8, 7), col=(-3, 3))
+    g = rand_grad_bits(rng, N, K)
+    vr = (rng.random(N) * 1e-3 + 1e-7).astype(np.float32)
+    vc = (rng.random(K) * 1e-3 + 1e-7).astype(np.float32)
+    svi = np.array([1.0 / vr.sum()], np.float32)
+    cp = rng.random((N, K)).astype(np.float32) if f.get("cohpre") else None
+    salt = int(rng.integers(-2 ** 31 + 1, 2 ** 31))
+    lr = 7e-4
+    pb.set_fixed_coh(f.get("fixed", True))
+    pb.set_gate_gain(f.get("gate_gain", 1.0))
+    pb.set_ratio_coh(f.get("ratio", False))
+    pb.set_ratio_coh_floors(0.6, 0.8)
+    pb.set_prototype_semantics(f.get("proto", False))
+    pb._get_consolidate_flag(DEV).fill_(f.get("consolidate", 1))
+    pb._v_bc_buf(DEV).fill_(f.get("v_bc", 1.0))
+    _set_salt(salt)
+    kw = dict(alpha=0.1, beta1=f.get("beta1", 0.0), weight_decay=f.get("weight_decay", 0.0),
+              eps=f.get("eps", 1e-10), step_cap=10.0, v_scale=f.get("v_scale", 0.0),
+              precond_p=f.get("precond_p", 0.5), gf_consol=f.get("gf_consol", 0.0),
+              drift_cancel_C=0.018036072144288578, alpha_v_fast=0.001, wd_sv=f.get("wd_sv", 0.0),
+              wd_sf=f.get("wd_sf", 0.0), mass_preserve=f.get("mp", True),
+              apply_chase=f.get("chase", True), track_rebalance=f.get("track", True),
+              gf_trust_delta_sq=f.get("trust", 1.0))
+    pk, wb = dev(packed), torch.zeros((N, K), dtype=torch.bfloat16, device=DEV)
+    rm = torch.zeros(N, dtype=torch.int32, device=DEV)
+    cm = torch.zeros(K, dtype=torch.int32, device=DEV)
+    cpd = dev(cp) if cp is not None else None
+    pb.apply_packed_adamw(pk, dev(g), wb, dev(re), dev(ce), rm, cm, lr=lr, v_row=dev(vr),
+                          v_col=dev(vc), sum_v_inv=dev(svi), coh_pre=cpd,
+                          drive_muon=f.get("muon", False), **kw)
+    sync()
+    # oracle
+    flags = O.EMIT_WEIGHT
+    for key, bit in [("mp", O.MASS_PRESERVE), ("chase", O.APPLY_CHASE), ("track", O.TRACK_REBALANCE)]:
+        if f.get(key, True):
+            flags |= bit
+    if kw["gf_trust_delta_sq"] > 0:
+        flags |= O.GF_TRUST_REGION
+    if kw["gf_consol"] > 0:
+        flags |= O.GF_CONSOLIDATION
+    if cp is not None:
+        flags |= O.COHPRE
+    if f.get("fixed", True):
+        flags |= O.FIXED_COH
+    if f.get("ratio", False):
+        flags |= O.RATIO_COH
+    if f.get("proto", False):
+        flags |= O.PROTO_CONSF
+    if f.get("muon", False):
+        flags |= O.MUON
+    P = O.UpdateParams(alpha=kw["alpha"], beta1=kw["beta1"], weight_decay=kw["weight_decay"],
+                       step_cap=10.0, v_scale=kw["v_scale"], precond_p=kw["precond_p"],
+                       gf_consol=kw["gf_consol"], drift_cancel_C=kw["drift_cancel_C"],
+                       alpha_v_fast=0.001, wd_sv=kw["wd_sv"], wd_sf=kw["wd_sf"],
+                       gf_trust_delta_sq=kw["gf_trust_delta_sq"], gate_gain=f.get("gate_gain", 1.0),
+                       mantissa_bias=15)
+    S = O.UpdateScalars(lr=lr, eps=kw["eps"], chase_floor=0.6, leak_floor=0.8, v_bc=f.get("v_bc", 1.0),
+                        salt=salt, consolidate=f.get("consolidate", 1))
+    opk = packed.copy()
+    ow = np.zeros((N, K), np.uint16)
+    orm = np.zeros(N, np.int32)
+    ocm = np.zeros(K, np.int32)
+    ocp = cp.copy() if cp is not None else None
+    O.apply_adamw(opk, g, ow, re, ce, orm, ocm, vr, vc, float(svi[0]), ocp, P, S, flags)
+    np.testing.assert_array_equal(host(pk), opk)
+    np.testing.assert_array_equal(host(wb), ow)
+    np.testing.assert_array_equal(host(rm), orm)
+    np.testing.assert_array_equal(host(cm), ocm)
+    if cp is not None:
+        np.testing.assert_array_equal(host(cpd), ocp)
+    assert (opk != packed).any()
+
+
+def test_apply_adamw_extreme_values(oracle):
+    """Overflowing ticks: saturating float->int, int32 wrap, int16/int8 clamps."""
+    from concord_amd import packed_b as pb
+    O = oracle
+    N, K = 64, 256
+    rng = np.random.default_rng(5)
+    packed, re, ce = rand_state(rng, N, K, sf=(-32768, 32768), exp=(-8, -8), col=(-8, -8), big_frac=0.5)
+    g = O.f32_to_bf16_bits_array((rng.standard_normal((N, K)) * 1e3).astype(np.float32))
+    vr = np.full(N, 1e-30, np.float32)
+    vc = np.full(K, 1e-30, np.float32)
+    svi = np.array([1e-10], np.float32)
+    _set_salt(99)
+    pk = dev(packed)
+    rm = torch.zeros(N, dtype=torch.int32, device=DEV)
+    cm = torch.zeros(K, dtype=torch.int32, device=DEV)
+    pb.apply_packed_adamw(pk, dev(g), None, dev(re), dev(ce), rm, cm, lr=50.0, eps=1e-30,
+                          step_cap=1e30, v_scale=0.0, gf_consol=0.0, mass_preserve=True,
+                          v_row=dev(vr), v_col=dev(vc), sum_v_inv=dev(svi), gf_trust_delta_sq=1.0,
+                          wd_sv=3.0, wd_sf=5.0)
+    sync()
+    P = O.UpdateParams(alpha=0.1, beta1=0.0, weight_decay=0.0, step_cap=1e30, v_scale=0.0,
+                       precond_p=0.5, gf_consol=0.0, drift_cancel_C=0.018036072144288578,
+                       alpha_v_fast=0.001, wd_sv=3.0, wd_sf=5.0, gf_trust_delta_sq=1.0,
+                       gate_gain=1.0, mantissa_bias=15)
+    S = O.UpdateScalars(lr=50.0, eps=1e-30, chase_floor=0.9, leak_floor=0.999, v_bc=1.0, salt=99,
+                        consolidate=1)
+    opk = packed.copy()
+    orm = np.zeros(N, np.int32)
+    ocm = np.zeros(K, np.int32)
+    O.apply_adamw(opk, g, None, re, ce, orm, ocm, vr, vc, float(svi[0]), None, P, S,
+                  O.MASS_PRESERVE | O.APPLY_CHASE | O.TRACK_REBALANCE | O.GF_TRUST_REGION | O.FIXED_COH)
+    np.testing.assert_array_equal(host(pk), opk)
+    np.testing.assert_array_equal(host(rm), orm)
+    np.testing.assert_array_equal(host(cm), ocm)
+
+
+@pytest.mark.parametrize("case", ["mp", "nomp"])
+def test_apply_sgd_matches_reference_golden(oracle, case):
+    from concord_amd import packed_b as pb
+    z = np.load(os.path.join(GOLD, f"sgd_{case}.npz"))
+    N, K = z["packed"].shape
+    _set_salt(int(z["s_salt"]))
+    pk = dev(z["packed"])
+    wb = torch.zeros((N, K), dtype=torch.bfloat16, device=DEV)
+    rm = torch.zeros(N, dtype=torch.int32, device=DEV)
+    cm = torch.zeros(K, dtype=torch.int32, device=DEV)
+    pb.apply_packed_sgd(pk, dev(z["grad"]), wb, dev(z["row_exp"]), dev(z["col_exp"]), rm, cm,
+                        lr=float(z["s_lr"]), alpha=float(z["s_alpha"]), beta1=float(z["s_beta1"]),
+                        alpha_v_fast=float(z["s_alpha_v_fast"]),
+                        mass_preserve=bool(int(z["s_mass_preserve"])), track_rebalance=True)
+    sync()
+    np.testing.assert_array_equal(host(pk), z["packed_out"])
+    np.testing.assert_array_equal(host(rm), z["row_max"])
+    np.testing.assert_array_equal(host(cm), z["col_max"])
+    np.testing.assert_array_equal(host(wb), oracle.materialize(z["packed_out"], z["row_exp"], z["col_exp"]))
+
+
+# ---------------------------------------------------------------- rebalance
+
+
+@pytest.mark.parametrize("case", ["up", "up_td", "tickdown"])
+def test_rebalance_matches_reference_golden(case):
+    from concord_amd import packed_b as pb
+    z = np.load(os.path.join(GOLD, f"rebalance_{case}.npz"))
+    pk, re, ce = dev(z["packed"]), dev(z["row_exp"]), dev(z["col_exp"])
+    seed = torch.tensor([int(z["s_seed"])], dtype=torch.int32, device=DEV)
+    pb.rebalance_packed(pk, re, ce, dev(z["row_max"]), dev(z["col_max"]), seed_buf=seed,
+                        allow_tickdown=bool(int(z["s_allow_tickdown"])))
+    sync()
+    np.testing.assert_array_equal(host(pk), z["packed_out"])
+    np.testing.assert_array_equal(host(re), z["row_exp_out"])
+    np.testing.assert_array_equal(host(ce), z["col_exp_out"])
+    assert int(host(seed)[0]) == int(z["s_seed"])
+
+
+@pytest.mark.parametrize("N,K,tickdown", [(200, 700, False), (200, 700, True), (1024, 256, True),
+                                          (70, 70, False)])
+def test_rebalance_matches_oracle(oracle, N, K, tickdown):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(N + K + tickdown)
+    sf = rng.integers(-3000, 3000, (N, K))
+    small = rng.random(N) < 0.5
+    ss = np.where(small[:, None], rng.integers(-20, 20, (N, K)), rng.integers(-100, 100, (N, K)))
+    vs = np.where(small[:, None], rng.integers(-20, 20, (N, K)), rng.integers(-100, 100, (N, K)))
+    for r in rng.choice(N, 5, replace=False):
+        c = rng.integers(0, K)
+        ss[r, c], vs[r, c] = 120, 125
+    packed = oracle.pack(sf, ss, vs)
+    re = rng.integers(-6, 8, N).astype(np.int8)
+    ce = rng.integers(-6, 8, K).astype(np.int8)
+    m = ss * 128 + sf + vs * 128
+    rmax = np.abs(m).max(1).astype(np.int32)
+    cmax = np.abs(m).max(0).astype(np.int32)
+    hw_r = rng.integers(0, 30000, N).astype(np.int32)
+    hw_c = rng.integers(0, 30000, K).astype(np.int32)
+    pk, red, ced = dev(packed), dev(re), dev(ce)
+    seed = torch.tensor([41], dtype=torch.int32, device=DEV)
+    hr, hc = dev(hw_r), dev(hw_c)
+    pb.rebalance_packed(pk, red, ced, dev(rmax), dev(cmax), seed_buf=seed, allow_tickdown=tickdown,
+                        row_hwm=hr, col_hwm=hc, advance_seed=True)
+    sync()
+    opk, ore, oce = packed.copy(), re.copy(), ce.copy()
+    oracle.rebalance(opk, ore, oce, rmax, cmax, seed=42, allow_tickdown=tickdown)
+    np.testing.assert_array_equal(host(pk), opk)
+    np.testing.assert_array_equal(host(red), ore)
+    np.testing.assert_array_equal(host(ced), oce)
+    np.testing.assert_array_equal(host(hr), np.maximum(hw_r, rmax))
+    np.testing.assert_array_equal(host(hc), np.maximum(hw_c, cmax))
+    assert int(host(seed)[0]) == 42
+    assert (opk != packed).any()
+
+
+def test_rebalance_no_fire_leaves_words(oracle):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(3)
+    packed, re, ce = rand_state(rng, 300, 500, sf=(-1000, 1000))
+    pk = dev(packed)
+    z = torch.zeros(300, dtype=torch.int32, device=DEV)
+    zc = torch.zeros(500, dtype=torch.int32, device=DEV)
+    pb.rebalance_packed(pk, dev(re), dev(ce), z, zc, allow_tickdown=False)
+    sync()
+    np.testing.assert_array_equal(host(pk), packed)
+
+
+# ---------------------------------------------------------------- v-hat, load
+
+
+@pytest.mark.parametrize("N,K", [(70, 130), (5120, 1280), (33, 1000), (1, 1)])
+def test_vhat_matches_oracle(oracle, N, K):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(N * K)
+    g = rand_grad_bits(rng, N, K)
+    vr = (rng.random(N) * 1e-4).astype(np.float32)
+    vc = (rng.random(K) * 1e-4).astype(np.float32)
+    vrd, vcd = dev(vr), dev(vc)
+    svi = torch.zeros(1, dtype=torch.float32, device=DEV)
+    rm = torch.full((N,), 7, dtype=torch.int32, device=DEV)
+    cm = torch.full((K,), 7, dtype=torch.int32, device=DEV)
+    salt = torch.tensor([5], dtype=torch.int32, device=DEV)
+    for _ in range(2):   # twice: the completion counter must re-arm itself
+        pb.vhat_ema(dev(g), vrd, vcd, svi, 0.999, rm, cm, salt)
+        s = oracle.vhat_ema(g, vr, vc, 0.999)
+    sync()
+    np.testing.assert_array_equal(host(vrd), vr)
+    np.testing.assert_array_equal(host(vcd), vc)
+    assert host(svi)[0] == s
+    assert not host(rm).any() and not host(cm).any()
+    assert int(host(salt)[0]) == 7
+
+
+def test_load_weights_matches_reference_golden():
+    from concord_amd import packed_b as pb
+    z = np.load(os.path.join(GOLD, "load_weights.npz"))
+    N, K = z["W"].shape
+    for ft, sfx in [(False, ""), (True, "_ft")]:
+        pk = torch.zeros((N, K), dtype=torch.int32, device=DEV)
+        re = torch.zeros(N, dtype=torch.int8, device=DEV)
+        ce = torch.ones(K, dtype=torch.int8, device=DEV)
+        pb.load_packed(torch.from_numpy(z["W"]), pk, re, ce, finetune=ft)
+        sync()
+        np.testing.assert_array_equal(host(pk), z["packed" + sfx])
+        np.testing.assert_array_equal(host(re), z["row_exp" + sfx])
+        np.testing.assert_array_equal(host(ce), z["col_exp" + sfx])
+
+
+def test_load_weights_matches_oracle(oracle):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(11)
+    N, K = 1000, 777
+    W = (rng.standard_normal((N, K)) * 10.0 ** rng.uniform(-5, 2, (N, 1))).astype(np.float32)
+    W[0] = 0
+    W[1, 5] = 0.5
+    for ft in (False, True):
+        pk = torch.zeros((N, K), dtype=torch.int32, device=DEV)
+        re = torch.zeros(N, dtype=torch.int8, device=DEV)
+        ce = torch.zeros(K, dtype=torch.int8, device=DEV)
+        pb.load_packed(torch.from_numpy(W), pk, re, ce, finetune=ft)
+        sync()
+        p, r, c = oracle.load_weights(W, finetune=ft)
+        np.testing.assert_array_equal(host(pk), p)
+        np.testing.assert_array_equal(host(re), r)
+
+
+# ---------------------------------------------------------------- GEMMs
+
+GEMM_SHAPES = [(64, 128, 64), (77, 130, 200), (256, 384, 1280), (1, 5, 3), (130, 1000, 70),
+               (2048, 1280, 1280)]
+
+
+def _decoded(oracle, packed, re, ce):
+    return oracle.bf16_bits_to_f32(oracle.materialize(packed, re, ce)).astype(np.float64)
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_dqgemm_fwd(oracle, M, N, K):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(M + N + K)
+    packed, re, ce = rand_state(rng, N, K, exp=(-2, 2), col=(-2, 2))
+    x = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32))
+    b = oracle.f32_to_bf16_bits_array(rng.standard_normal(N).astype(np.float32))
+    y = pb._gemm_fwd(dev(x), dev(packed), dev(re), dev(ce), 15, dev(b), None)
+    sync()
+    W = _decoded(oracle, packed, re, ce)
+    ref = oracle.bf16_bits_to_f32(x).astype(np.float64) @ W.T + oracle.bf16_bits_to_f32(b)
+    got = oracle.bf16_bits_to_f32(host(y))
+    assert rel_l2(got, ref) < 5e-3
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_dqgemm_dgrad(oracle, M, N, K):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(M * 3 + N + K)
+    packed, re, ce = rand_state(rng, N, K, exp=(-2, 2), col=(-2, 2))
+    dy = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, N)).astype(np.float32))
+    dx = pb._gemm_dgrad(dev(dy), dev(packed), dev(re), dev(ce), 15, None)
+    sync()
+    W = _decoded(oracle, packed, re, ce)
+    ref = oracle.bf16_bits_to_f32(dy).astype(np.float64) @ W
+    assert rel_l2(oracle.bf16_bits_to_f32(host(dx)), ref) < 5e-3
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_wgrad(oracle, M, N, K):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(M * 5 + N + K)
+    dy = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, N)).astype(np.float32))
+    x = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32))
+    gw = pb._wgrad(dev(dy), dev(x))
+    sync()
+    ref = oracle.bf16_bits_to_f32(dy).astype(np.float64).T @ oracle.bf16_bits_to_f32(x)
+    assert rel_l2(oracle.bf16_bits_to_f32(host(gw)), ref) < 5e-3
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES[:4])
+def test_bf16_weight_gemms(oracle, M, N, K):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(M * 7 + N + K)
+    w = oracle.f32_to_bf16_bits_array((rng.standard_normal((N, K)) * 0.05).astype(np.float32))
+    x = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32))
+    dy = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, N)).astype(np.float32))
+    wd = dev(w)
+    y = pb._gemm_fwd(dev(x), None, None, None, 15, None, wd)
+    dx = pb._gemm_dgrad(dev(dy), torch.empty((N, K), dtype=torch.int32, device=DEV), None, None, 15, wd)
+    sync()
+    Wf = oracle.bf16_bits_to_f32(w).astype(np.float64)
+    assert rel_l2(oracle.bf16_bits_to_f32(host(y)), oracle.bf16_bits_to_f32(x) @ Wf.T) < 5e-3
+    assert rel_l2(oracle.bf16_bits_to_f32(host(dx)), oracle.bf16_bits_to_f32(dy) @ Wf) < 5e-3
+
+
+def test_bias_grad(oracle):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(17)
+    for M, N in [(300, 70), (4096, 1280), (1, 3)]:
+        dy = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, N)).astype(np.float32))
+        db = pb._bias_grad(dev(dy))
+        sync()
+        ref = oracle.bf16_bits_to_f32(dy).astype(np.float64).sum(0)
+        assert rel_l2(oracle.bf16_bits_to_f32(host(db)), ref) < 5e-3
+
+
+# ---------------------------------------------------------------- layer
+
+
+def _oracle_step(oracle, layer_state, grad_bits, lr, salt, flags, coh_pre=None, chase=0.9, leak=0.999,
+                 gf_consol=0.0):
+    O = oracle
+    pk, re, ce, vr, vc = layer_state
+    N, K = pk.shape
+    svi = O.vhat_ema(grad_bits, vr, vc, 0.999)
+    rm = np.zeros(N, np.int32)
+    cm = np.zeros(K, np.int32)
+    P = O.UpdateParams(alpha=0.1, beta1=0.0, weight_decay=0.0, step_cap=10.0, v_scale=0.0,
+                       precond_p=0.5, gf_consol=gf_consol, drift_cancel_C=0.018036072144288578,
+                       alpha_v_fast=0.001, wd_sv=0.0, wd_sf=0.0, gf_trust_delta_sq=1.0,
+                       gate_gain=1.0, mantissa_bias=15)
+    S = O.UpdateScalars(lr=lr, eps=1e-10, chase_floor=chase, leak_floor=leak, v_bc=1.0, salt=salt,
+                        consolidate=1)
+    O.apply_adamw(pk, grad_bits, None, re, ce, rm, cm, vr, vc, svi, coh_pre, P, S, flags)
+    return rm, cm
+
+
+@pytest.mark.parametrize("winner", [False, True])
+def test_layer_config1_bit_exact(oracle, winner):
+    """Config 1: 768->768 layer, Kaiming-uniform init (seed 0), x ~ N(0,1) [4096, 768],
+    grad_y ~ N(0, 1e-2) (std), lr 5e-4: forward, backward (fused update), rebalance;
+    packed words and consolidated_weight() bit-exact vs the oracle fed the same
+    bf16 gradient."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    O = oracle
+    torch.manual_seed(0)
+    W0 = torch.nn.init.kaiming_uniform_(torch.empty(768, 768), a=5 ** 0.5)
+    x = torch.randn(4096, 768)
+    gy = torch.randn(4096, 768) * 1e-2
+    layer = ca.ConcordLinearPackedB(768, 768, bias=True, device=DEV, lr=5e-4)
+    flags = O.MASS_PRESERVE | O.APPLY_CHASE | O.TRACK_REBALANCE | O.GF_TRUST_REGION | O.FIXED_COH
+    if winner:
+        pb.set_ratio_coh(True)
+        pb.set_ratio_coh_floors(0.9, 0.999)
+        layer.disable_cohpre()
+        layer.gf_consol = 50.0
+        flags |= O.RATIO_COH | O.GF_CONSOLIDATION
+    else:
+        flags |= O.COHPRE
+    layer.load_weights(W0)
+    p0, r0, c0 = O.load_weights(W0.numpy())
+    np.testing.assert_array_equal(host(layer.packed_w), p0)
+    state = [p0.copy(), r0.copy(), c0.copy(), np.zeros(768, np.float32), np.zeros(768, np.float32)]
+    coh = None if winner else np.ones((768, 768), np.float32)
+    for step in range(3):
+        salt_next = int(host(pb._get_step_counter(DEV))[0]) + 1
+        xd = x.to(DEV).requires_grad_(True)
+        cap = []
+        pb._DEBUG_CAPTURE = cap
+        try:
+            y = layer(xd)
+            y.backward(gy.to(DEV))
+        finally:
+            pb._DEBUG_CAPTURE = None
+        layer.rebalance()
+        sync()
+        rm, cm = _oracle_step(O, state, host(cap[0]), 5e-4, salt_next, flags, coh,
+                              gf_consol=50.0 if winner else 0.0)
+        O.rebalance(state[0], state[1], state[2], rm, cm, seed=step + 1)
+        np.testing.assert_array_equal(host(layer.packed_w), state[0])
+        np.testing.assert_array_equal(host(layer.row_exp), state[1])
+        np.testing.assert_array_equal(host(layer.v_row), state[3])
+        np.testing.assert_array_equal(host(layer.v_col), state[4])
+    np.testing.assert_array_equal(host(layer.consolidated_weight()),
+                                  O.materialize(state[0], state[1], state[2], consolidated=True))
+    np.testing.assert_array_equal(host(layer.get_weight()), O.materialize(state[0], state[1], state[2]))
+
+
+def test_layer_weight_cache_mode_matches_fused():
+    """The two forward modes feed identical bf16 operands: same y, dx, state."""
+    import concord_amd as ca
+    torch.manual_seed(3)
+    W0 = torch.randn(384, 256) * 0.05
+    x = torch.randn(512, 256)
+    gy = torch.randn(512, 384) * 1e-2
+    outs = []
+    from concord_amd import packed_b as pb
+    for cache in (False, True):
+        pb._get_step_counter(DEV).fill_(100)
+        layer = ca.ConcordLinearPackedB(256, 384, bias=True, device=DEV, lr=1e-3, weight_cache=cache)
+        layer.load_weights(W0)
+        xd = x.to(DEV).requires_grad_(True)
+        y = layer(xd)
+        y.backward(gy.to(DEV))
+        y2 = layer(xd.detach())
+        sync()
+        outs.append((host(y.to(torch.bfloat16)), host(xd.grad.to(torch.bfloat16)), host(layer.packed_w),
+                     host(y2.to(torch.bfloat16))))
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_determinism_run_twice():
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    res = []
+    for _ in range(2):
+        torch.manual_seed(9)
+        pb._get_step_counter(DEV).fill_(0)
+        layer = ca.ConcordLinearPackedB(640, 320, bias=False, device=DEV, lr=2e-3)
+        for _ in range(3):
+            x = torch.randn(300, 640, device=DEV).requires_grad_(True)
+            layer(x).square().mean().backward()
+            layer.rebalance()
+        sync()
+        res.append(host(layer.packed_w))
+    np.testing.assert_array_equal(res[0], res[1])
+
+
+def test_bare_default_trains():
+    """concord/test_baked_defaults.py:34-46: a bare layer fits a toy regression."""
+    import concord_amd as ca
+    torch.manual_seed(1)
+    W = ca.ConcordLinearPackedB(32, 32, bias=False, device=DEV)
+    W.lr = 0.02
+    tgt = torch.randn(32, 32, device=DEV) * 0.3
+    x = torch.randn(256, 32, device=DEV)
+    y = x @ tgt.T
+    losses = []
+    for _ in range(80):
+        xb = x.detach().requires_grad_(True)
+        loss = torch.nn.functional.mse_loss(W(xb).float(), y)
+        loss.backward()
+        W.rebalance()
+        losses.append(loss.item())
+    assert losses[-1] < 0.9 * losses[0]
+    W.disable_cohpre()
+    assert W._coh_pre is None
+    loss = torch.nn.functional.mse_loss(W(x.requires_grad_(True)).float(), y)
+    loss.backward()
+    W.rebalance()
+
+
+def test_3d_input_and_fp32_dtype():
+    import concord_amd as ca
+    torch.manual_seed(2)
+    layer = ca.ConcordLinearPackedB(96, 48, bias=True, device=DEV)
+    x = torch.randn(4, 25, 96, device=DEV, requires_grad=True)
+    y = layer(x)
+    assert y.shape == (4, 25, 48) and y.dtype == torch.float32
+    y.sum().backward()
+    assert x.grad.shape == x.shape and layer.bias.grad is not None
