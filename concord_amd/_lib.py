@@ -60,11 +60,14 @@ _SIGS = {
                                          ctypes.c_int, ctypes.c_int, _P, _Z, _P]),
     "concord_load_weights": (ctypes.c_int, [_P, _I, _I, _I, _i, _i, _i, ctypes.c_int, _P, _I, _P,
                                             _P, _P]),
-    "concord_dqgemm_fwd": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _i, _P, _P, _I, _I, _I, _I, _P]),
-    "concord_dqgemm_dgrad": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _i, _P, _I, _I, _I, _I, _P]),
-    "concord_wgrad": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P]),
-    "concord_gemm_bf16_fwd": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _P]),
-    "concord_gemm_bf16_dgrad": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P]),
+    "concord_gemm_workspace_bytes": (_Z, [_I, _I, _I]),
+    "concord_dqgemm_fwd": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _i, _P, _P, _I, _I, _I, _I, _P, _Z,
+                                          _P]),
+    "concord_dqgemm_dgrad": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _i, _P, _I, _I, _I, _I, _P, _Z,
+                                            _P]),
+    "concord_wgrad": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _Z, _P]),
+    "concord_gemm_bf16_fwd": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _P, _Z, _P]),
+    "concord_gemm_bf16_dgrad": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _Z, _P]),
     "concord_bias_grad": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _Z, _P]),
 }
 

@@ -159,8 +159,12 @@ CONCORD_DEV float det_exp2(float y) {
   return __fmul_rn(__fmul_rn(p, exp2i(a)), exp2i(b));
 }
 
+// correctly rounded sqrt: __builtin_sqrtf expands to v_sqrt_f32 plus the
+// +-1 ulp fma correction (__fsqrt_rn lowers to the bare ~1 ulp v_sqrt_f32).
+CONCORD_DEV float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+
 CONCORD_DEV float pow_p(float x, float p) {
-  if (p == 0.5f) return __fsqrt_rn(x);
+  if (p == 0.5f) return sqrt_rn(x);
   if (p == 0.0f) return 1.0f;
   return det_exp2(__fmul_rn(p, det_log2(x)));
 }

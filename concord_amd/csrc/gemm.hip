@@ -6,31 +6,36 @@
 //   FWD_BF16 / DGRAD_BF16: the same products over a materialised bf16 W
 //   (the reference's cached weight_buf path).
 //
-// All are C[i][j] = sum_r A(i,r) B(r,j) with fp32 accumulation on
-// v_mfma_f32_32x32x16_bf16.  Packed words are decoded to bf16 on the way into
-// LDS: bf16(m_eff * 2^(row_exp + col_exp - bias)), bit-identical to the
+// All are C[i][j] = sum_r A(i,r) B(r,j), fp32 accumulation on
+// v_mfma_f32_16x16x32_bf16.  Packed words are decoded to bf16 on the way into
+// LDS, bf16(m_eff * 2^(row_exp + col_exp - bias)): bit-identical to the
 // materialised weight.
 //
-// Block: 256 threads (4 waves as 2 x 2), tile 128 (i) x 128 (j) x 64 (r), LDS
-// double-buffered, next tile's global loads in flight during the MFMAs.  Both
-// LDS operands are stored r-contiguous ([i][r] and [j][r], 144 B row stride),
-// so each lane's MFMA operand is one ds_read_b128.  Operands whose global
-// layout is r-strided are transposed in registers in 8 (r) x 4 blocks.
+// Block = 256 threads (4 waves).  Tile BI x BJ x 64, LDS double-buffered
+// ([i][r] and [j][r], r-contiguous, 144 B row stride: each MFMA operand is one
+// conflict-free ds_read_b128), next tile's global loads in flight during the
+// MFMAs.  The MFMA computes C^T blocks (its A operand is the j-tile), so each
+// lane holds 4 consecutive j of one i: one 8-byte store per block.
+// Tile shapes are picked per problem so that about one tile lands on each of
+// the 256 CUs; a too-small grid is split 2-way along r with a deterministic
+// fixup (the second finisher adds the first's fp32 partial: a + b = b + a).
+// Tiles are mapped XCD-aware: workgroup w runs on XCD w % 8, and each XCD
+// gets a compact block of the tile grid so its L2 serves shared operands.
 #include "common.h"
+#include "workspace.h"
 
 namespace concord {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 enum { MODE_FWD = 0, MODE_DGRAD = 1, MODE_WGRAD = 2, MODE_FWD_BF16 = 3, MODE_DGRAD_BF16 = 4 };
 
-constexpr int TI = 128, TJ = 128, TR = 64;
-constexpr int LDS_STRIDE = 72;  // bf16 elements per LDS row (64 + 8 pad)
-constexpr int LDS_TILE = 128 * LDS_STRIDE;
+constexpr int TR = 64;          // reduction depth per LDS stage
+constexpr int LDS_STRIDE = 72;  // bf16 per LDS row (64 + 8 pad)
 
 struct GemmArgs {
-  const uint16_t* a;      // FWD: x[M,K]; DGRAD, WGRAD, *_BF16 dgrad: dy[M,N]
+  const uint16_t* a;      // FWD: x[M,K]; DGRAD*, WGRAD: dy[M,N]
   const void* b;          // packed[N,K] int32 | x[M,K] bf16 (WGRAD) | W[N,K] bf16 (*_BF16)
   int64_t lda, ldb;
   const int8_t* row_exp;  // packed rows (n)
@@ -40,6 +45,11 @@ struct GemmArgs {
   uint16_t* c;
   int64_t ldc;
   int64_t I, J, R;        // C is I x J, reduction R
+  int64_t r_split;        // reduction length per split (multiple of TR)
+  float* part;            // split-K: 2 x I x J fp32 partials
+  uint32_t* tile_cnt;     // split-K: one counter per (i, j) tile, zero between calls
+  int tiles_i, tiles_j, splits;
+  int vec_a, vec_b, vec_c;  // base pointers and leading dimensions allow 16 B / 8 B accesses
 };
 
 CONCORD_DEV float decode_word(int32_t w, int32_t e) {
@@ -60,193 +70,228 @@ CONCORD_DEV void transpose_8x4(const uint32_t (&in)[8][2], uint4 (&out)[4]) {
   }
 }
 
-// ---- tile loaders -------------------------------------------------------------
-// rows-copy: bf16 [rows][R] r-contiguous -> 4 x 16 B per thread
-// (rows t/8 + 32q, r chunk (t%8)*8), stored to LDS [row][r].
+// ---- tile loaders (256 threads; work split in chunks, ceil(chunks / 256) each) ----
+
+// bf16 [rows][R] r-contiguous -> LDS [row][r]; chunk = 8 bf16 (16 B)
+template <int ROWS>
 struct RowsCopy {
-  uint4 v[4];
-  CONCORD_DEV void load(const uint16_t* base, int64_t ld, int64_t rows, int64_t R, int64_t i0,
-                        int64_t r0, int t) {
+  static constexpr int NCH = ROWS * (TR / 8);
+  static constexpr int PER = (NCH + 255) / 256;
+  uint4 v[PER];
+  CONCORD_DEV void load(const uint16_t* base, int64_t ld, int64_t nrows, int64_t i0, int64_t r0,
+                        int64_t r_end, int t, int vec) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int64_t i = i0 + t / 8 + 32 * q, r = r0 + (t % 8) * 8;
+    for (int q = 0; q < PER; ++q) {
+      const int ch = t + 256 * q;
+      const int64_t i = i0 + ch / 8, r = r0 + (ch % 8) * 8;
       const uint16_t* p = base + i * ld + r;
-      if (i < rows && r + 8 <= R && (ld % 8) == 0) {
-        v[q] = *reinterpret_cast<const uint4*>(p);
-      } else {
-        uint32_t w[4] = {0, 0, 0, 0};
-        if (i < rows) {
+      uint32_t w[4] = {0, 0, 0, 0};
+      if (ch < NCH && i < nrows) {
+        if (r + 8 <= r_end && vec) {
+          const uint4 x = *reinterpret_cast<const uint4*>(p);
+          w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+        } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e)
-            if (r + e < R) w[e / 2] |= (uint32_t)p[e] << (16 * (e & 1));
+            if (r + e < r_end) w[e / 2] |= (uint32_t)p[e] << (16 * (e & 1));
         }
-        v[q] = make_uint4(w[0], w[1], w[2], w[3]);
       }
+      v[q] = make_uint4(w[0], w[1], w[2], w[3]);
     }
   }
   CONCORD_DEV void store(uint16_t* lds, int t) const {
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
-      *reinterpret_cast<uint4*>(lds + (t / 8 + 32 * q) * LDS_STRIDE + (t % 8) * 8) = v[q];
+    for (int q = 0; q < PER; ++q) {
+      const int ch = t + 256 * q;
+      if (ch < NCH) *reinterpret_cast<uint4*>(lds + (ch / 8) * LDS_STRIDE + (ch % 8) * 8) = v[q];
+    }
   }
 };
 
-// transposed: bf16 [R][cols] col-contiguous -> thread owns 4 columns (4*(t%32))
-// x 8 r (8*(t/32)), stored to LDS [col][r] as 4 x 16 B.
+// bf16 [R][cols] col-contiguous -> LDS [col][r]; block = 8 r x 4 cols
+template <int COLS>
 struct ColsTranspose {
-  uint4 v[4];
-  CONCORD_DEV void load(const uint16_t* base, int64_t ld, int64_t cols, int64_t R, int64_t c0,
-                        int64_t r0, int t) {
-    const int64_t c = c0 + 4 * (t % 32), rb = r0 + 8 * (t / 32);
-    uint32_t blk[8][2];
+  static constexpr int NB = (TR / 8) * (COLS / 4);
+  static constexpr int PER = (NB + 255) / 256;
+  uint4 v[PER][4];
+  CONCORD_DEV void load(const uint16_t* base, int64_t ld, int64_t ncols, int64_t c0, int64_t r0,
+                        int64_t r_end, int t, int vec) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int64_t r = rb + e;
-      const uint16_t* p = base + r * ld + c;
-      if (r < R && c + 4 <= cols && (ld % 4) == 0) {
-        const uint2 w = *reinterpret_cast<const uint2*>(p);
-        blk[e][0] = w.x;
-        blk[e][1] = w.y;
-      } else {
+    for (int q = 0; q < PER; ++q) {
+      const int b = t + 256 * q;
+      const int64_t c = c0 + 4 * (b % (COLS / 4)), rb = r0 + 8 * (b / (COLS / 4));
+      uint32_t blk[8][2];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t r = rb + e;
+        const uint16_t* p = base + r * ld + c;
         uint32_t w[2] = {0, 0};
-        if (r < R) {
+        if (b < NB && r < r_end) {
+          if (c + 4 <= ncols && vec) {
+            const uint2 x = *reinterpret_cast<const uint2*>(p);
+            w[0] = x.x; w[1] = x.y;
+          } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (c + q < cols) w[q / 2] |= (uint32_t)p[q] << (16 * (q & 1));
+            for (int q2 = 0; q2 < 4; ++q2)
+              if (c + q2 < ncols) w[q2 / 2] |= (uint32_t)p[q2] << (16 * (q2 & 1));
+          }
         }
         blk[e][0] = w[0];
         blk[e][1] = w[1];
       }
+      transpose_8x4(blk, v[q]);
     }
-    transpose_8x4(blk, v);
   }
   CONCORD_DEV void store(uint16_t* lds, int t) const {
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *reinterpret_cast<uint4*>(lds + (4 * (t % 32) + c) * LDS_STRIDE + 8 * (t / 32)) = v[c];
+    for (int q = 0; q < PER; ++q) {
+      const int b = t + 256 * q;
+      if (b < NB) {
+        const int c = 4 * (b % (COLS / 4)), r = 8 * (b / (COLS / 4));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) *reinterpret_cast<uint4*>(lds + (c + k) * LDS_STRIDE + r) = v[q][k];
+      }
+    }
   }
 };
 
-// packed W as B(r=k, j=n) = W[n][k]: [J][R] r-contiguous.  thread -> rows
-// t/16 + 16q (8 rows), r chunk (t%16)*4; decode with row_exp[n] + col_exp[k].
+// packed W as B(r=k, j=n): [J][R] r-contiguous; chunk = 4 words
+template <int ROWS>
 struct PackedRows {
-  uint4 v[8];
-  int32_t ce[4];
-  int32_t re[8];  // row_exp - bias of the thread's 8 rows (fixed per block)
-  CONCORD_DEV void init(const GemmArgs& g, int64_t j0, int t) {
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int64_t j = j0 + t / 16 + 16 * q;
-      re[q] = ((j < g.J) ? (int32_t)g.row_exp[j] : 0) - g.bias;
-    }
-  }
-  CONCORD_DEV void load(const GemmArgs& g, int64_t j0, int64_t r0, int t) {
+  static constexpr int NCH = ROWS * (TR / 4);
+  static constexpr int PER = (NCH + 255) / 256;
+  uint4 v[PER];
+  int32_t re[PER];  // row exponent - bias per chunk
+  int32_t ce[4];    // column exponents: ch % 16 == t % 16 for every chunk of a thread
+  CONCORD_DEV void load(const GemmArgs& g, int64_t j0, int64_t r0, int64_t r_end, int t) {
     const int32_t* pk = reinterpret_cast<const int32_t*>(g.b);
     const int64_t r = r0 + (t % 16) * 4;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int64_t j = j0 + t / 16 + 16 * q;
+    for (int k = 0; k < 4; ++k) ce[k] = (r + k < r_end) ? (int32_t)g.col_exp[r + k] : 0;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int ch = t + 256 * q;
+      const int64_t j = j0 + ch / 16;
       const int32_t* p = pk + j * g.ldb + r;
-      if (j < g.J && r + 4 <= g.R && (g.ldb % 4) == 0) {
-        v[q] = *reinterpret_cast<const uint4*>(p);
-      } else {
-        uint32_t w[4] = {0, 0, 0, 0};
-        if (j < g.J) {
+      uint32_t w[4] = {0, 0, 0, 0};
+      int32_t e = 0;
+      if (ch < NCH && j < g.J) {
+        e = (int32_t)g.row_exp[j];
+        if (r + 4 <= r_end && g.vec_b) {
+          const uint4 x = *reinterpret_cast<const uint4*>(p);
+          w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+        } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (r + e < g.R) w[e] = (uint32_t)p[e];
+          for (int k = 0; k < 4; ++k)
+            if (r + k < r_end) w[k] = (uint32_t)p[k];
         }
-        v[q] = make_uint4(w[0], w[1], w[2], w[3]);
       }
+      v[q] = make_uint4(w[0], w[1], w[2], w[3]);
+      re[q] = e - g.bias;
     }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) ce[e] = (r + e < g.R) ? (int32_t)g.col_exp[r + e] : 0;
   }
   CONCORD_DEV void store(uint16_t* lds, int t) const {
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const uint4 w = v[q];
-      uint2 o;
-      o.x = pack_bf16x2(decode_word((int32_t)w.x, re[q] + ce[0]), decode_word((int32_t)w.y, re[q] + ce[1]));
-      o.y = pack_bf16x2(decode_word((int32_t)w.z, re[q] + ce[2]), decode_word((int32_t)w.w, re[q] + ce[3]));
-      *reinterpret_cast<uint2*>(lds + (t / 16 + 16 * q) * LDS_STRIDE + (t % 16) * 4) = o;
+    for (int q = 0; q < PER; ++q) {
+      const int ch = t + 256 * q;
+      if (ch < NCH) {
+        uint2 o;
+        o.x = pack_bf16x2(decode_word((int32_t)v[q].x, re[q] + ce[0]), decode_word((int32_t)v[q].y, re[q] + ce[1]));
+        o.y = pack_bf16x2(decode_word((int32_t)v[q].z, re[q] + ce[2]), decode_word((int32_t)v[q].w, re[q] + ce[3]));
+        *reinterpret_cast<uint2*>(lds + (ch / 16) * LDS_STRIDE + (ch % 16) * 4) = o;
+      }
     }
   }
 };
 
-// packed W as B(r=n, j=k) = W[n][k]: [R][J] j-contiguous.  thread -> 4 columns
-// 4*(t%32) x 8 rows 8*(t/32); decode, transpose, store [j][r].
+// packed W as B(r=n, j=k): [R][J] j-contiguous; block = 8 r x 4 cols
+template <int COLS>
 struct PackedCols {
-  uint4 v[8];
-  int32_t re[8];
-  int32_t ce[4];  // col_exp - bias of the thread's 4 columns (fixed per block)
-  CONCORD_DEV void init(const GemmArgs& g, int64_t j0, int t) {
-    const int64_t j = j0 + 4 * (t % 32);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) ce[c] = ((j + c < g.J) ? (int32_t)g.col_exp[j + c] : 0) - g.bias;
-  }
-  CONCORD_DEV void load(const GemmArgs& g, int64_t j0, int64_t r0, int t) {
+  static constexpr int NB = (TR / 8) * (COLS / 4);
+  static constexpr int PER = (NB + 255) / 256;
+  uint4 v[PER][8];
+  int32_t re[PER][8];
+  int32_t ce[PER][4];
+  CONCORD_DEV void load(const GemmArgs& g, int64_t j0, int64_t r0, int64_t r_end, int t) {
     const int32_t* pk = reinterpret_cast<const int32_t*>(g.b);
-    const int64_t j = j0 + 4 * (t % 32), rb = r0 + 8 * (t / 32);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int64_t r = rb + e;
-      const int32_t* p = pk + r * g.ldb + j;
-      if (r < g.R && j + 4 <= g.J && (g.ldb % 4) == 0) {
-        v[e] = *reinterpret_cast<const uint4*>(p);
-      } else {
+    for (int q = 0; q < PER; ++q) {
+      const int b = t + 256 * q;
+      const int64_t j = j0 + 4 * (b % (COLS / 4)), rb = r0 + 8 * (b / (COLS / 4));
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        ce[q][c] = ((b < NB && j + c < g.J) ? (int32_t)g.col_exp[j + c] : 0) - g.bias;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t r = rb + e;
+        const int32_t* p = pk + r * g.ldb + j;
         uint32_t w[4] = {0, 0, 0, 0};
-        if (r < g.R) {
+        int32_t rexp = 0;
+        if (b < NB && r < r_end) {
+          rexp = (int32_t)g.row_exp[r];
+          if (j + 4 <= g.J && g.vec_b) {
+            const uint4 x = *reinterpret_cast<const uint4*>(p);
+            w[0] = x.x; w[1] = x.y; w[2] = x.z; w[3] = x.w;
+          } else {
 #pragma unroll
-          for (int c = 0; c < 4; ++c)
-            if (j + c < g.J) w[c] = (uint32_t)p[c];
+            for (int c = 0; c < 4; ++c)
+              if (j + c < g.J) w[c] = (uint32_t)p[c];
+          }
         }
-        v[e] = make_uint4(w[0], w[1], w[2], w[3]);
+        v[q][e] = make_uint4(w[0], w[1], w[2], w[3]);
+        re[q][e] = rexp;
       }
-      re[e] = (r < g.R) ? (int32_t)g.row_exp[r] : 0;
     }
   }
   CONCORD_DEV void store(uint16_t* lds, int t) const {
-    uint32_t blk[8][2];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint4 w = v[e];
-      blk[e][0] = pack_bf16x2(decode_word((int32_t)w.x, re[e] + ce[0]), decode_word((int32_t)w.y, re[e] + ce[1]));
-      blk[e][1] = pack_bf16x2(decode_word((int32_t)w.z, re[e] + ce[2]), decode_word((int32_t)w.w, re[e] + ce[3]));
+    for (int q = 0; q < PER; ++q) {
+      const int b = t + 256 * q;
+      if (b < NB) {
+        uint32_t blk[8][2];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          blk[e][0] = pack_bf16x2(decode_word((int32_t)v[q][e].x, re[q][e] + ce[q][0]),
+                                  decode_word((int32_t)v[q][e].y, re[q][e] + ce[q][1]));
+          blk[e][1] = pack_bf16x2(decode_word((int32_t)v[q][e].z, re[q][e] + ce[q][2]),
+                                  decode_word((int32_t)v[q][e].w, re[q][e] + ce[q][3]));
+        }
+        uint4 o[4];
+        transpose_8x4(blk, o);
+        const int c = 4 * (b % (COLS / 4)), r = 8 * (b / (COLS / 4));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) *reinterpret_cast<uint4*>(lds + (c + k) * LDS_STRIDE + r) = o[k];
+      }
     }
-    uint4 o[4];
-    transpose_8x4(blk, o);
-#pragma unroll
-    for (int c = 0; c < 4; ++c)
-      *reinterpret_cast<uint4*>(lds + (4 * (t % 32) + c) * LDS_STRIDE + 8 * (t / 32)) = o[c];
   }
 };
 
-template <int MODE>
-struct Tiles {
-  RowsCopy ar;        // A for all but WGRAD
-  ColsTranspose at;   // A for WGRAD
-  PackedRows bpr;     // B for FWD
-  PackedCols bpc;     // B for DGRAD
-  ColsTranspose bt;   // B for WGRAD, DGRAD_BF16
-  RowsCopy br;        // B for FWD_BF16
+// A operand loader (i side) and B operand loader (j side) per mode
+template <int MODE, int BI> struct ALoad;
+template <int BI> struct ALoad<MODE_FWD, BI> : RowsCopy<BI> {};
+template <int BI> struct ALoad<MODE_DGRAD, BI> : RowsCopy<BI> {};
+template <int BI> struct ALoad<MODE_FWD_BF16, BI> : RowsCopy<BI> {};
+template <int BI> struct ALoad<MODE_DGRAD_BF16, BI> : RowsCopy<BI> {};
+template <int BI> struct ALoad<MODE_WGRAD, BI> : ColsTranspose<BI> {};
 
-  CONCORD_DEV void init(const GemmArgs& g, int64_t j0, int t) {
-    if (MODE == MODE_FWD) bpr.init(g, j0, t);
-    if (MODE == MODE_DGRAD) bpc.init(g, j0, t);
-  }
-  CONCORD_DEV void load(const GemmArgs& g, int64_t i0, int64_t j0, int64_t r0, int t) {
-    if (MODE == MODE_WGRAD) at.load(g.a, g.lda, g.I, g.R, i0, r0, t);
-    else ar.load(g.a, g.lda, g.I, g.R, i0, r0, t);
+template <int MODE, int BI, int BJ>
+struct Tiles {
+  ALoad<MODE, BI> a;
+  PackedRows<BJ> bpr;       // FWD
+  PackedCols<BJ> bpc;       // DGRAD
+  ColsTranspose<BJ> bt;     // WGRAD, DGRAD_BF16
+  RowsCopy<BJ> br;          // FWD_BF16
+
+  CONCORD_DEV void load(const GemmArgs& g, int64_t i0, int64_t j0, int64_t r0, int64_t r_end, int t) {
+    a.load(g.a, g.lda, g.I, i0, r0, r_end, t, g.vec_a);
     const uint16_t* bb = reinterpret_cast<const uint16_t*>(g.b);
-    if (MODE == MODE_FWD) bpr.load(g, j0, r0, t);
-    if (MODE == MODE_DGRAD) bpc.load(g, j0, r0, t);
-    if (MODE == MODE_WGRAD || MODE == MODE_DGRAD_BF16) bt.load(bb, g.ldb, g.J, g.R, j0, r0, t);
-    if (MODE == MODE_FWD_BF16) br.load(bb, g.ldb, g.J, g.R, j0, r0, t);
+    if (MODE == MODE_FWD) bpr.load(g, j0, r0, r_end, t);
+    if (MODE == MODE_DGRAD) bpc.load(g, j0, r0, r_end, t);
+    if (MODE == MODE_WGRAD || MODE == MODE_DGRAD_BF16) bt.load(bb, g.ldb, g.J, j0, r0, r_end, t, g.vec_b);
+    if (MODE == MODE_FWD_BF16) br.load(bb, g.ldb, g.J, j0, r0, r_end, t, g.vec_b);
   }
   CONCORD_DEV void store(uint16_t* la, uint16_t* lb, int t) const {
-    if (MODE == MODE_WGRAD) at.store(la, t);
-    else ar.store(la, t);
+    a.store(la, t);
     if (MODE == MODE_FWD) bpr.store(lb, t);
     if (MODE == MODE_DGRAD) bpc.store(lb, t);
     if (MODE == MODE_WGRAD || MODE == MODE_DGRAD_BF16) bt.store(lb, t);
@@ -254,85 +299,208 @@ struct Tiles {
   }
 };
 
-template <int MODE>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t lds[2][2][LDS_TILE];
+// XCD-aware tile order: workgroup w runs on XCD w % 8.  XCD x owns tile
+// indices [x*T/8, (x+1)*T/8) of a grouped row-major order (groups of GI
+// i-tiles), so the CUs of one XCD share i- and j-tiles in their L2.
+CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
+  // XCD x owns q + (x < rem) consecutive indices starting at x*q + min(x, rem):
+  // a bijection of [0, total) for any total
+  const int xcd = w % 8, slot = w / 8;
+  const int q = total / 8, rem = total % 8;
+  const int lin = xcd * q + min(xcd, rem) + slot;
+  const int GI = 8;
+  const int group = lin / (GI * tj);
+  const int first_i = group * GI;
+  const int gsize = min(ti - first_i, GI);
+  const int in = lin % (GI * tj);
+  bi = first_i + in % gsize;
+  bj = in / gsize;
+}
+
+template <int MODE, int BI, int BJ, int WI, int WJ>
+__global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
+  constexpr int WTI = BI / WI, WTJ = BJ / WJ;   // wave tile
+  constexpr int NI = WTI / 16, NJ = WTJ / 16;   // 16x16 blocks per wave
+  static_assert(WI * WJ == 4, "4 waves");
+  static_assert(WTI % 16 == 0 && WTJ % 16 == 0, "wave tile must be a multiple of 16");
+  __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][BI * LDS_STRIDE];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][BJ * LDS_STRIDE];
+  __shared__ uint32_t s_old;
+
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int wi = wave >> 1, wj = wave & 1;
-  const int64_t i0 = (int64_t)blockIdx.x * TI;
-  const int64_t j0 = (int64_t)blockIdx.y * TJ;
+  const int wi = wave / WJ, wj = wave % WJ;
+  const int tiles = g.tiles_i * g.tiles_j;
+  const int wg = blockIdx.x;
+  const int split = wg / tiles;
+  int bi, bj;
+  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
+  const int64_t r_begin = (int64_t)split * g.r_split;
+  const int64_t r_end = min(g.R, r_begin + g.r_split);
 
-  Tiles<MODE> T;
-  T.init(g, j0, t);
+  Tiles<MODE, BI, BJ> T;
+  f32x4 acc[NI][NJ];
+#pragma unroll
+  for (int x = 0; x < NI; ++x)
+#pragma unroll
+    for (int y = 0; y < NJ; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  f32x16 acc[2][2];
-#pragma unroll
-  for (int x = 0; x < 2; ++x)
-#pragma unroll
-    for (int y = 0; y < 2; ++y)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[x][y][e] = 0.0f;
-
-  const int64_t nr = (g.R + TR - 1) / TR;
+  const int64_t nr = (r_end > r_begin) ? (r_end - r_begin + TR - 1) / TR : 0;
   if (nr > 0) {
-    T.load(g, i0, j0, 0, t);
-    T.store(lds[0][0], lds[0][1], t);
+    T.load(g, i0, j0, r_begin, r_end, t);
+    T.store(lds_a[0], lds_b[0], t);
   }
   __syncthreads();
 
-  const int lrow = lane & 31, lk = (lane >> 5) * 8;
+  const int lrow = lane & 15, lk = (lane >> 4) * 8;
   for (int64_t rt = 0; rt < nr; ++rt) {
     const int cur = (int)(rt & 1);
-    if (rt + 1 < nr) T.load(g, i0, j0, (rt + 1) * TR, t);
-    const uint16_t* la = lds[cur][0];
-    const uint16_t* lb = lds[cur][1];
+    if (rt + 1 < nr) T.load(g, i0, j0, r_begin + (rt + 1) * TR, r_end, t);
+    const uint16_t* la = lds_a[cur];
+    const uint16_t* lb = lds_b[cur];
 #pragma unroll
-    for (int kk = 0; kk < TR / 16; ++kk) {
-      bf16x8 af[2], bfr[2];
+    for (int kk = 0; kk < TR / 32; ++kk) {
+      bf16x8 fa[NI], fb[NJ];
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
-        af[x] = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const uint4*>(la + (wi * 64 + x * 32 + lrow) * LDS_STRIDE + kk * 16 + lk));
+      for (int x = 0; x < NI; ++x)
+        fa[x] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                               la + (wi * WTI + x * 16 + lrow) * LDS_STRIDE + kk * 32 + lk));
 #pragma unroll
-      for (int y = 0; y < 2; ++y)
-        bfr[y] = __builtin_bit_cast(
-            bf16x8, *reinterpret_cast<const uint4*>(lb + (wj * 64 + y * 32 + lrow) * LDS_STRIDE + kk * 16 + lk));
+      for (int y = 0; y < NJ; ++y)
+        fb[y] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(
+                                               lb + (wj * WTJ + y * 16 + lrow) * LDS_STRIDE + kk * 32 + lk));
+      // D^T: MFMA rows = j (from the B tile), columns = i (from the A tile)
 #pragma unroll
-      for (int x = 0; x < 2; ++x)
+      for (int x = 0; x < NI; ++x)
 #pragma unroll
-        for (int y = 0; y < 2; ++y)
-          acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[x], bfr[y], acc[x][y], 0, 0, 0);
+        for (int y = 0; y < NJ; ++y)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[y], fa[x], acc[x][y], 0, 0, 0);
     }
-    if (rt + 1 < nr) T.store(lds[cur ^ 1][0], lds[cur ^ 1][1], t);
+    if (rt + 1 < nr) T.store(lds_a[cur ^ 1], lds_b[cur ^ 1], t);
     __syncthreads();
   }
 
-  // epilogue: lane holds column j = lane % 32 and rows 8*(e/4) + 4*(lane/32) + e%4
+  // lane holds C[i0 + wi*WTI + x*16 + lane%16][j0 + wj*WTJ + y*16 + 4*(lane/16) + e], e = 0..3
+  const int64_t ib = i0 + wi * WTI + (lane & 15);
+  const int64_t jb = j0 + wj * WTJ + 4 * (lane >> 4);
+  if (g.splits == 2) {
+    // deterministic 2-way fixup: both halves publish, the second finisher sums
+    float* mine = g.part + (int64_t)split * g.I * g.J;
+    const float* other = g.part + (int64_t)(split ^ 1) * g.I * g.J;
 #pragma unroll
-  for (int y = 0; y < 2; ++y) {
-    const int64_t j = j0 + wj * 64 + y * 32 + (lane & 31);
-    if (j >= g.J) continue;
-    const float bj = g.vbias ? bf16_to_f32(g.vbias[j]) : 0.0f;
+    for (int x = 0; x < NI; ++x)
 #pragma unroll
-    for (int x = 0; x < 2; ++x) {
+      for (int y = 0; y < NJ; ++y) {
+        const int64_t i = ib + x * 16, j = jb + y * 16;
+        if (i < g.I)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t i = i0 + wi * 64 + x * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e & 3);
-        if (i < g.I) {
-          const float v = __fadd_rn(acc[x][y][e], bj);
-          g.c[i * g.ldc + j] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
-        }
+          for (int e = 0; e < 4; ++e)
+            if (j + e < g.J) mine[i * g.J + j + e] = acc[x][y][e];
+      }
+    __threadfence();
+    __syncthreads();
+    if (t == 0) s_old = atomicAdd(g.tile_cnt + (wg % tiles), 1u);
+    __syncthreads();
+    if (s_old == 0) return;
+    __threadfence();
+#pragma unroll
+    for (int x = 0; x < NI; ++x)
+#pragma unroll
+      for (int y = 0; y < NJ; ++y) {
+        const int64_t i = ib + x * 16, j = jb + y * 16;
+        if (i < g.I)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (j + e < g.J) acc[x][y][e] = __fadd_rn(acc[x][y][e], other[i * g.J + j + e]);
+      }
+    if (t == 0) g.tile_cnt[wg % tiles] = 0u;
+  }
+#pragma unroll
+  for (int x = 0; x < NI; ++x) {
+    const int64_t i = ib + x * 16;
+    if (i >= g.I) continue;
+#pragma unroll
+    for (int y = 0; y < NJ; ++y) {
+      const int64_t j = jb + y * 16;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float bj = (g.vbias && j + e < g.J) ? bf16_to_f32(g.vbias[j + e]) : 0.0f;
+        v[e] = __fadd_rn(acc[x][y][e], bj);
+      }
+      uint16_t* out = g.c + i * g.ldc + j;
+      if (j + 4 <= g.J && g.vec_c) {
+        *reinterpret_cast<uint2*>(out) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (j + e < g.J) out[e] = (uint16_t)(pack_bf16x2(v[e], 0.0f) & 0xFFFFu);
       }
     }
   }
 }
 
+// ---- tile shape selection -------------------------------------------------------
+enum Shape { SH_256x160 = 0, SH_128x160 = 1, SH_160x160 = 2, SH_128x128 = 3 };
+struct ShapeDims { int bi, bj; };
+static const ShapeDims kShapes[4] = {{256, 160}, {128, 160}, {160, 160}, {128, 128}};
+constexpr int kCUs = 256;
+
+struct Plan {
+  int shape, splits, ti, tj;
+  int64_t r_split;
+};
+
+// Estimated time ~ waves of tiles x work per tile (plus a fixup charge for a
+// split), over the four shapes and splits {1, 2}.
+static Plan plan_gemm(int64_t I, int64_t J, int64_t R, bool allow_split) {
+  Plan best{SH_128x128, 1, 0, 0, R};
+  double best_cost = 1e300;
+  for (int s = 0; s < 4; ++s) {
+    for (int sp = 1; sp <= (allow_split ? 2 : 1); ++sp) {
+      const int64_t ti = cdiv(I, kShapes[s].bi), tj = cdiv(J, kShapes[s].bj);
+      const int64_t blocks = ti * tj * sp;
+      const int64_t rs = cdiv(cdiv(R, sp), TR) * TR;
+      const double waves = (double)cdiv(blocks, kCUs);
+      const double eff = (kShapes[s].bi * kShapes[s].bj >= 256 * 160) ? 1.0
+                         : (kShapes[s].bi * kShapes[s].bj >= 160 * 160) ? 0.93 : 0.85;
+      double cost = waves * (double)kShapes[s].bi * kShapes[s].bj * (double)rs / eff;
+      if (sp == 2) cost += 2.0 * (double)I * J * 4.0 / 64.0;   // fixup traffic
+      if (cost < best_cost) {
+        best_cost = cost;
+        best = Plan{s, sp, (int)ti, (int)tj, rs};
+      }
+    }
+  }
+  return best;
+}
+
 template <int MODE>
-static int launch_gemm(const GemmArgs& g, hipStream_t st, const char* what) {
+static int launch_gemm(GemmArgs g, void* workspace, size_t ws_bytes, hipStream_t st,
+                       const char* what) {
   if (g.I == 0 || g.J == 0) return CONCORD_OK;
-  dim3 grid((unsigned)cdiv(g.I, TI), (unsigned)cdiv(g.J, TJ));
-  hipLaunchKernelGGL(gemm_kernel<MODE>, grid, dim3(256), 0, st, g);
+  const bool can_split = workspace != nullptr;
+  Plan p = plan_gemm(g.I, g.J, g.R, can_split);
+  if (p.splits == 2 &&
+      (ws_bytes < gemm_splitk_bytes(g.I, g.J) || !gemm_splitk_fits((int64_t)p.ti * p.tj)))
+    p = plan_gemm(g.I, g.J, g.R, false);
+  g.splits = p.splits;
+  g.r_split = p.r_split;
+  g.tiles_i = p.ti;
+  g.tiles_j = p.tj;
+  if (p.splits == 2) {
+    char* base = (char*)workspace;
+    g.tile_cnt = (uint32_t*)base;
+    g.part = (float*)(base + kSplitkCounterBytes);
+  }
+  const dim3 grid((unsigned)((int64_t)p.ti * p.tj * p.splits)), block(256);
+  switch (p.shape) {
+    case SH_256x160: hipLaunchKernelGGL((gemm_kernel<MODE, 256, 160, 4, 1>), grid, block, 0, st, g); break;
+    case SH_128x160: hipLaunchKernelGGL((gemm_kernel<MODE, 128, 160, 2, 2>), grid, block, 0, st, g); break;
+    case SH_160x160: hipLaunchKernelGGL((gemm_kernel<MODE, 160, 160, 2, 2>), grid, block, 0, st, g); break;
+    default: hipLaunchKernelGGL((gemm_kernel<MODE, 128, 128, 2, 2>), grid, block, 0, st, g); break;
+  }
   return launch_status(what);
 }
 
@@ -340,63 +508,89 @@ static bool sizes_ok(int64_t M, int64_t N, int64_t K) {
   return M >= 0 && N >= 0 && K >= 0 && M < (1LL << 31) && N < (1LL << 31) && K < (1LL << 31);
 }
 
+static GemmArgs make_args(const uint16_t* a, const void* b, int64_t lda, int64_t ldb,
+                          const int8_t* re, const int8_t* ce, int32_t bias, const uint16_t* vb,
+                          uint16_t* c, int64_t ldc, int64_t I, int64_t J, int64_t R, bool b_packed) {
+  GemmArgs g{};
+  g.a = a; g.b = b; g.lda = lda; g.ldb = ldb; g.row_exp = re; g.col_exp = ce; g.bias = bias;
+  g.vbias = vb; g.c = c; g.ldc = ldc; g.I = I; g.J = J; g.R = R;
+  auto al = [](const void* p, int n) { return ((uintptr_t)p % n) == 0; };
+  g.vec_a = al(a, 16) && (lda % 8) == 0;
+  g.vec_b = al(b, 16) && (ldb % (b_packed ? 4 : 8)) == 0;
+  g.vec_c = al(c, 8) && (ldc % 4) == 0;
+  return g;
+}
+
 }  // namespace concord
 
 using namespace concord;
 
+extern "C" size_t concord_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  // split-K partials of the largest of the three outputs: y [M,N], dx [M,K], gw [N,K]
+  if (M < 1) M = 1;
+  if (N < 1) N = 1;
+  if (K < 1) K = 1;
+  size_t a = gemm_splitk_bytes(M, N), b = gemm_splitk_bytes(M, K), c = gemm_splitk_bytes(N, K);
+  return a > b ? (a > c ? a : c) : (b > c ? b : c);
+}
+
 extern "C" int concord_dqgemm_fwd(const uint16_t* x, int64_t ld_x, const int32_t* packed,
                                   int64_t ld_p, const int8_t* row_exp, const int8_t* col_exp,
                                   int32_t mantissa_bias, const uint16_t* bias, uint16_t* y,
-                                  int64_t ld_y, int64_t M, int64_t N, int64_t K, void* stream) {
+                                  int64_t ld_y, int64_t M, int64_t N, int64_t K, void* workspace,
+                                  size_t workspace_bytes, void* stream) {
   CONCORD_CHECK(sizes_ok(M, N, K), "concord_dqgemm_fwd: bad size");
   if (M == 0 || N == 0) return CONCORD_OK;
   CONCORD_CHECK(x && packed && row_exp && col_exp && y, "concord_dqgemm_fwd: NULL argument");
   CONCORD_CHECK(ld_x >= K && ld_p >= K && ld_y >= N, "concord_dqgemm_fwd: bad leading dimension");
-  GemmArgs g{x, packed, ld_x, ld_p, row_exp, col_exp, mantissa_bias, bias, y, ld_y, M, N, K};
-  return launch_gemm<MODE_FWD>(g, (hipStream_t)stream, "dqgemm_fwd");
+  GemmArgs g = make_args(x, packed, ld_x, ld_p, row_exp, col_exp, mantissa_bias, bias, y, ld_y, M, N, K, true);
+  return launch_gemm<MODE_FWD>(g, workspace, workspace_bytes, (hipStream_t)stream, "dqgemm_fwd");
 }
 
 extern "C" int concord_dqgemm_dgrad(const uint16_t* dy, int64_t ld_dy, const int32_t* packed,
                                     int64_t ld_p, const int8_t* row_exp, const int8_t* col_exp,
                                     int32_t mantissa_bias, uint16_t* dx, int64_t ld_dx, int64_t M,
-                                    int64_t N, int64_t K, void* stream) {
+                                    int64_t N, int64_t K, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
   CONCORD_CHECK(sizes_ok(M, N, K), "concord_dqgemm_dgrad: bad size");
   if (M == 0 || K == 0) return CONCORD_OK;
   CONCORD_CHECK(dy && packed && row_exp && col_exp && dx, "concord_dqgemm_dgrad: NULL argument");
   CONCORD_CHECK(ld_dy >= N && ld_p >= K && ld_dx >= K, "concord_dqgemm_dgrad: bad leading dimension");
-  GemmArgs g{dy, packed, ld_dy, ld_p, row_exp, col_exp, mantissa_bias, nullptr, dx, ld_dx, M, K, N};
-  return launch_gemm<MODE_DGRAD>(g, (hipStream_t)stream, "dqgemm_dgrad");
+  GemmArgs g = make_args(dy, packed, ld_dy, ld_p, row_exp, col_exp, mantissa_bias, nullptr, dx, ld_dx, M, K, N, true);
+  return launch_gemm<MODE_DGRAD>(g, workspace, workspace_bytes, (hipStream_t)stream, "dqgemm_dgrad");
 }
 
 extern "C" int concord_wgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t ld_x,
                              uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
-                             void* stream) {
+                             void* workspace, size_t workspace_bytes, void* stream) {
   CONCORD_CHECK(sizes_ok(M, N, K), "concord_wgrad: bad size");
   if (N == 0 || K == 0) return CONCORD_OK;
   CONCORD_CHECK(dy && x && grad_w, "concord_wgrad: NULL argument");
   CONCORD_CHECK(ld_dy >= N && ld_x >= K && ld_gw >= K, "concord_wgrad: bad leading dimension");
-  GemmArgs g{dy, x, ld_dy, ld_x, nullptr, nullptr, 0, nullptr, grad_w, ld_gw, N, K, M};
-  return launch_gemm<MODE_WGRAD>(g, (hipStream_t)stream, "wgrad");
+  GemmArgs g = make_args(dy, x, ld_dy, ld_x, nullptr, nullptr, 0, nullptr, grad_w, ld_gw, N, K, M, false);
+  return launch_gemm<MODE_WGRAD>(g, workspace, workspace_bytes, (hipStream_t)stream, "wgrad");
 }
 
 extern "C" int concord_gemm_bf16_fwd(const uint16_t* x, int64_t ld_x, const uint16_t* w,
                                      int64_t ld_w, const uint16_t* bias, uint16_t* y, int64_t ld_y,
-                                     int64_t M, int64_t N, int64_t K, void* stream) {
+                                     int64_t M, int64_t N, int64_t K, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
   CONCORD_CHECK(sizes_ok(M, N, K), "concord_gemm_bf16_fwd: bad size");
   if (M == 0 || N == 0) return CONCORD_OK;
   CONCORD_CHECK(x && w && y, "concord_gemm_bf16_fwd: NULL argument");
   CONCORD_CHECK(ld_x >= K && ld_w >= K && ld_y >= N, "concord_gemm_bf16_fwd: bad leading dimension");
-  GemmArgs g{x, w, ld_x, ld_w, nullptr, nullptr, 0, bias, y, ld_y, M, N, K};
-  return launch_gemm<MODE_FWD_BF16>(g, (hipStream_t)stream, "gemm_bf16_fwd");
+  GemmArgs g = make_args(x, w, ld_x, ld_w, nullptr, nullptr, 0, bias, y, ld_y, M, N, K, false);
+  return launch_gemm<MODE_FWD_BF16>(g, workspace, workspace_bytes, (hipStream_t)stream, "gemm_bf16_fwd");
 }
 
 extern "C" int concord_gemm_bf16_dgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* w,
                                        int64_t ld_w, uint16_t* dx, int64_t ld_dx, int64_t M,
-                                       int64_t N, int64_t K, void* stream) {
+                                       int64_t N, int64_t K, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
   CONCORD_CHECK(sizes_ok(M, N, K), "concord_gemm_bf16_dgrad: bad size");
   if (M == 0 || K == 0) return CONCORD_OK;
   CONCORD_CHECK(dy && w && dx, "concord_gemm_bf16_dgrad: NULL argument");
   CONCORD_CHECK(ld_dy >= N && ld_w >= K && ld_dx >= K, "concord_gemm_bf16_dgrad: bad leading dimension");
-  GemmArgs g{dy, w, ld_dy, ld_w, nullptr, nullptr, 0, nullptr, dx, ld_dx, M, K, N};
-  return launch_gemm<MODE_DGRAD_BF16>(g, (hipStream_t)stream, "gemm_bf16_dgrad");
+  GemmArgs g = make_args(dy, w, ld_dy, ld_w, nullptr, nullptr, 0, nullptr, dx, ld_dx, M, K, N, false);
+  return launch_gemm<MODE_DGRAD_BF16>(g, workspace, workspace_bytes, (hipStream_t)stream, "gemm_bf16_dgrad");
 }

@@ -146,6 +146,194 @@ CONCORD_DEV int32_t adamw_element(int32_t word, float g, int32_t te, float vr, f
 // The wd_sv/wd_sf terms are skipped only when both rates are zero: then both
 // SR deltas are +-0 and their ticks are exactly 0 (floor(+-0) + (u < 0) = 0).
 
+// Specialised element for the two production configurations, chosen by the
+// host only when every dropped term is an exact no-op:
+//   RATIO (winner): ratio-coherence gates + gf evaporation, no coh_pre;
+//   !RATIO (bare default): coh_pre-gated chase, no evaporation.
+// Preconditions: FIXED_COH, TRUST with delta^2 = 1, v_scale = 0, p = 0.5,
+// beta1 = 0, weight_decay = wd_sv = wd_sf = 0, gate_gain = 1, APPLY_CHASE,
+// MASS_PRESERVE, no PROTO/MUON.  Then v_proxy = nw^2 * 0 + 1 * v_hat = v_hat
+// exactly; the beta1 and weight-decay terms add +-0 (the SR tick of a +-0
+// delta is 0 whatever the zero's sign); the Wiener gain sig2/(sig2+nw2+1e-30)
+// already lies in [0, 1], so its clamp is the identity.
+template <bool RATIO>
+CONCORD_DEV int32_t adamw_element_fast(int32_t word, float g, float scale_fwd, float scale_inv,
+                                       float vr, float vc, float* coh_pre, int32_t ps,
+                                       float C, float alpha, float avf, float lr_kappa,
+                                       const Uniform& U, int32_t* m_out) {
+  const Fields f = unpack(word);
+  int32_t sf = f.sf, ss = f.ss;
+  const int32_t vs = f.vs, vsf = f.vs * 128;
+  const float d_fs = (float)sf;
+  const float d_sv = (float)(ss * 128 - vsf);
+  const float cd = __fmul_rn(C, d_sv);
+  const float nw = __fmul_rn(__fsub_rn(d_fs, cd), scale_fwd);
+  const float v_hat = __fmul_rn(__fmul_rn(vr, vc), U.svi);
+  const float sig_w = __fmul_rn(cd, scale_fwd);
+  const float sig2 = __fmul_rn(sig_w, sig_w);
+  const float coh = __fdiv_rn(sig2, __fadd_rn(__fadd_rn(sig2, __fmul_rn(nw, nw)), 1e-30f));
+  float step = __fdiv_rn(g, sqrt_rn(__fadd_rn(v_hat, U.eps)));
+  step = fminf(fmaxf(step, -10.0f), 10.0f);
+  float delta_t = __fmul_rn(__fmul_rn(-U.lr, step), scale_inv);
+  if (RATIO) delta_t = __fsub_rn(delta_t, __fmul_rn(__fmul_rn(lr_kappa, __fsub_rn(1.0f, coh)), d_fs));
+  sf = wadd(sf, sr_tick(delta_t, hash_uniform(sf, ps)));
+
+  float gate;
+  if (RATIO) {
+    gate = __fadd_rn(U.chase_floor, __fmul_rn(__fsub_rn(1.0f, U.chase_floor), coh));
+  } else {
+    const float cp = *coh_pre;
+    gate = __fadd_rn(coh, __fmul_rn(cp, __fsub_rn(1.0f, coh)));
+    *coh_pre = __fadd_rn(__fmul_rn(__fsub_rn(1.0f, avf), cp), __fmul_rn(avf, coh));
+  }
+  const float chase = __fmul_rn(__fmul_rn(alpha, gate), (float)sf);
+  const int32_t t2 = sr_tick(__fmul_rn(chase, 0.0078125f), hash_uniform(sf, ps ^ 0x5A5A5A5A));
+  ss = wadd(ss, t2);
+  sf = wsub(sf, wshl(t2, 7));
+  float dv8 = __fmul_rn(__fmul_rn(avf, (float)wsub(wshl(ss, 7), vsf)), 0.0078125f);
+  if (RATIO) dv8 = __fmul_rn(dv8, __fadd_rn(U.leak_floor, __fmul_rn(__fsub_rn(1.0f, U.leak_floor), coh)));
+  const int32_t t3 = sr_tick(dv8, hash_uniform(sf, ps ^ 0x33335555));
+  const int32_t new_v = clampi(wadd(vs, t3), -128, 127);
+  ss = wsub(ss, wsub(new_v, vs));
+  const int32_t sfc = clampi(sf, -32768, 32767);
+  const int32_t ssc = clampi(ss, -128, 127);
+  *m_out = ssc * 128 + sfc + new_v * 128;
+  return pack(sfc, ssc, new_v);
+}
+
+template <bool RATIO>
+__global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
+  __shared__ int32_t s_cmax[4][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t kb = (int64_t)blockIdx.x * 256;
+  const int64_t k0 = kb + lane * 4;
+  const int64_t nb = (int64_t)blockIdx.y * a.tn;
+  Uniform U;
+  U.lr = *a.s.lr;
+  U.eps = *a.s.eps;
+  U.chase_floor = RATIO ? *a.s.chase_floor : 0.0f;
+  U.leak_floor = RATIO ? *a.s.leak_floor : 0.0f;
+  U.v_bc = 1.0f;
+  U.cons = 1;
+  U.consf = 1.0f;
+  U.salt = *a.s.salt_counter;
+  U.svi = *a.sum_v_inv;
+  const bool track = a.flags & CONCORD_TRACK_REBALANCE;
+  const bool emit = a.flags & CONCORD_EMIT_WEIGHT;
+  const float C = a.p.drift_cancel_C, alpha = a.p.alpha, avf = a.p.alpha_v_fast;
+  const float lr_kappa = __fmul_rn(U.lr, a.p.gf_consol);
+
+  const bool full = k0 + 4 <= a.K;
+  int32_t ce[4], cmax[4];
+  float vc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bool ok = k0 + j < a.K;
+    ce[j] = ok ? (int32_t)a.col_exp[k0 + j] : 0;
+    vc[j] = ok ? a.v_col[k0 + j] : 0.0f;
+    cmax[j] = 0;
+  }
+  for (int r = wave; r < a.tn; r += 4) {
+    const int64_t n = nb + r;
+    if (n >= a.N) break;
+    const int32_t te_row = (int32_t)a.row_exp[n] - a.p.mantissa_bias;
+    const float vr = a.v_row[n];
+    const int32_t psr = wshl((int32_t)n, 16) ^ U.salt;
+    int32_t w[4];
+    float g[4], cp[4];
+    int32_t* pp = a.packed + n * a.ld_p + k0;
+    const uint16_t* gp = a.grad + n * a.ld_g + k0;
+    float* cpp = RATIO ? nullptr : a.coh_pre + n * a.ld_c + k0;
+    if (full) {
+      const int4 wv = *reinterpret_cast<const int4*>(pp);
+      const uint2 gv = *reinterpret_cast<const uint2*>(gp);
+      w[0] = wv.x; w[1] = wv.y; w[2] = wv.z; w[3] = wv.w;
+      g[0] = __uint_as_float(gv.x << 16);
+      g[1] = __uint_as_float(gv.x & 0xFFFF0000u);
+      g[2] = __uint_as_float(gv.y << 16);
+      g[3] = __uint_as_float(gv.y & 0xFFFF0000u);
+      if (!RATIO) {
+        const float4 cv = *reinterpret_cast<const float4*>(cpp);
+        cp[0] = cv.x; cp[1] = cv.y; cp[2] = cv.z; cp[3] = cv.w;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool ok = k0 + j < a.K;
+        w[j] = ok ? pp[j] : 0;
+        g[j] = ok ? bf16_to_f32(gp[j]) : 0.0f;
+        cp[j] = (!RATIO && ok) ? cpp[j] : 1.0f;
+      }
+    }
+    int32_t out[4], m[4];
+    int32_t rmax = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int32_t te = te_row + ce[j];
+      out[j] = adamw_element_fast<RATIO>(w[j], g[j], exp2i(te), exp2i(-te), vr, vc[j], &cp[j],
+                                         psr ^ (int32_t)(k0 + j), C, alpha, avf, lr_kappa, U, &m[j]);
+      const int32_t am = (full || k0 + j < a.K) ? abs(m[j]) : 0;
+      rmax = max(rmax, am);
+      cmax[j] = max(cmax[j], am);
+    }
+    if (full) {
+      *reinterpret_cast<int4*>(pp) = make_int4(out[0], out[1], out[2], out[3]);
+      if (!RATIO) *reinterpret_cast<float4*>(cpp) = make_float4(cp[0], cp[1], cp[2], cp[3]);
+      if (emit) {
+        uint2 wv;
+        wv.x = pack_bf16x2(__fmul_rn((float)m[0], exp2i(te_row + ce[0])),
+                           __fmul_rn((float)m[1], exp2i(te_row + ce[1])));
+        wv.y = pack_bf16x2(__fmul_rn((float)m[2], exp2i(te_row + ce[2])),
+                           __fmul_rn((float)m[3], exp2i(te_row + ce[3])));
+        *reinterpret_cast<uint2*>(a.wbuf + n * a.ld_w + k0) = wv;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if (k0 + j < a.K) {
+          pp[j] = out[j];
+          if (!RATIO) cpp[j] = cp[j];
+          if (emit)
+            a.wbuf[n * a.ld_w + k0 + j] =
+                (uint16_t)(pack_bf16x2(__fmul_rn((float)m[j], exp2i(te_row + ce[j])), 0.0f) & 0xFFFFu);
+        }
+      }
+    }
+    if (track) {
+      rmax = wave_max(rmax);
+      if (lane == 0) atomicMax(a.row_max + n, rmax);
+    }
+  }
+  if (track) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s_cmax[wave][lane * 4 + j] = cmax[j];
+    __syncthreads();
+    const int64_t k = kb + threadIdx.x;
+    if (k < a.K) {
+      const int32_t v = max(max(s_cmax[0][threadIdx.x], s_cmax[1][threadIdx.x]),
+                            max(s_cmax[2][threadIdx.x], s_cmax[3][threadIdx.x]));
+      atomicMax(a.col_max + k, v);
+    }
+  }
+}
+
+// 0 = generic kernel, 1 = bare fast path, 2 = winner fast path
+static int fast_path(const concord_update_params& p, uint32_t flags) {
+  const uint32_t need = CONCORD_FIXED_COH | CONCORD_GF_TRUST_REGION | CONCORD_APPLY_CHASE |
+                        CONCORD_MASS_PRESERVE;
+  if ((flags & need) != need) return 0;
+  if (flags & (CONCORD_PROTO_CONSF | CONCORD_MUON)) return 0;
+  if (!(p.v_scale == 0.0f && p.gf_trust_delta_sq == 1.0f && p.precond_p == 0.5f &&
+        p.beta1 == 0.0f && p.weight_decay == 0.0f && p.wd_sv == 0.0f && p.wd_sf == 0.0f &&
+        p.gate_gain == 1.0f && p.step_cap == 10.0f))
+    return 0;
+  const bool ratio = flags & CONCORD_RATIO_COH, consol = flags & CONCORD_GF_CONSOLIDATION,
+             cohpre = flags & CONCORD_COHPRE;
+  if (ratio && consol) return 2;
+  if (!ratio && !consol && cohpre) return 1;
+  return 0;
+}
+
 template <int VEC>
 __global__ __launch_bounds__(256) void apply_adamw_kernel(AdamwArgs a) {
   __shared__ int32_t s_cmax[4][256];
@@ -418,7 +606,12 @@ extern "C" int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t
   if (vec4) {
     const int64_t cb = cdiv(K, 256);
     a.tn = choose_tn(N, cb);
-    hipLaunchKernelGGL(apply_adamw_kernel<4>, dim3(cb, cdiv(N, a.tn)), dim3(256), 0, st, a);
+    const dim3 grid(cb, cdiv(N, a.tn));
+    switch (fast_path(*params, flags)) {
+      case 2: hipLaunchKernelGGL(apply_adamw_fast_kernel<true>, grid, dim3(256), 0, st, a); break;
+      case 1: hipLaunchKernelGGL(apply_adamw_fast_kernel<false>, grid, dim3(256), 0, st, a); break;
+      default: hipLaunchKernelGGL(apply_adamw_kernel<4>, grid, dim3(256), 0, st, a); break;
+    }
   } else {
     const int64_t cb = cdiv(K, 64);
     a.tn = choose_tn(N, cb);

@@ -1,5 +1,6 @@
-// workspace.h -- layout of the caller-owned workspace.
+// workspace.h -- layout of the caller-owned workspaces.
 //
+// Update-side workspace:
 // [0, 256)       counters: the v-hat "blocks done" counter and the rebalance
 //                "fired" flag; zero when the workspace is created and zero
 //                again after every call that uses them.
@@ -21,7 +22,8 @@ inline Workspace workspace_layout(int64_t N, int64_t K, int64_t M) {
   w.vhat_counter = 0;
   w.reb_fired = 64;
   w.scratch = 256;
-  const size_t vhat = (size_t)(cd(K, 64) * N + cd(N, 32) * K) * sizeof(float);
+  // v-hat: row partials per 64-column chunk, column partials per 128-row slab
+  const size_t vhat = (size_t)(cd(K, 64) * N + cd(N, 128) * K) * sizeof(float);
   const size_t reb = (size_t)(2 * (N + K)) * sizeof(int32_t);
   const size_t bias = (size_t)(cd(M, 256) * (N > K ? N : K)) * sizeof(float);
   size_t s = vhat;
@@ -29,6 +31,17 @@ inline Workspace workspace_layout(int64_t N, int64_t K, int64_t M) {
   if (bias > s) s = bias;
   w.total = w.scratch + ((s + 255) / 256) * 256;
   return w;
+}
+
+// GEMM split-K workspace (its own buffer): a fixed region of tile counters
+// (the same offsets for every problem, so one call's fp32 partials can never
+// sit where a later call expects zeroed counters), then two fp32 partial
+// outputs [I][J].  Split-K is only used when the tile grid fits the counters.
+constexpr int64_t kSplitkMaxTiles = 4096;
+constexpr size_t kSplitkCounterBytes = (size_t)kSplitkMaxTiles * sizeof(uint32_t);
+inline bool gemm_splitk_fits(int64_t tiles) { return tiles <= kSplitkMaxTiles; }
+inline size_t gemm_splitk_bytes(int64_t I, int64_t J) {
+  return kSplitkCounterBytes + (size_t)2 * (size_t)I * (size_t)J * sizeof(float);
 }
 
 }  // namespace concord

@@ -212,6 +212,21 @@ def _ensure_reb_seed_tensor(device):
     return _REB_SEED_CACHE[key]
 
 
+_GEMM_WORKSPACES = {}
+
+
+def _gemm_workspace(device, M, N, K):
+    """Zero-initialised per-device split-K workspace of the GEMMs, grown to the
+    largest problem seen (grow it eagerly, before any graph capture)."""
+    key = _dev_key(device)
+    need = int(C.lib().concord_gemm_workspace_bytes(int(M), int(N), int(K)))
+    ws = _GEMM_WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=key)
+        _GEMM_WORKSPACES[key] = ws
+    return ws
+
+
 def _workspace(device, N, K):
     """Zero-initialised per-device workspace, grown to the largest layer."""
     key = _dev_key(device)
@@ -453,15 +468,16 @@ def _gemm_fwd(x2, packed_w, row_exp, col_exp, mantissa_bias, bias, weight_buf):
     N = (weight_buf if weight_buf is not None else packed_w).shape[0]
     y = torch.empty((M, N), dtype=torch.bfloat16, device=x2.device)
     st = C.stream_of(x2.device)
+    ws = _gemm_workspace(x2.device, M, N, K)
     if weight_buf is None:
         C.check(C.lib().concord_dqgemm_fwd(
             C.ptr(x2), x2.stride(0), C.ptr(packed_w), packed_w.stride(0), C.ptr(row_exp),
-            C.ptr(col_exp), int(mantissa_bias), C.ptr(bias), C.ptr(y), y.stride(0), M, N, K, st),
-            "dqgemm_fwd")
+            C.ptr(col_exp), int(mantissa_bias), C.ptr(bias), C.ptr(y), y.stride(0), M, N, K,
+            C.ptr(ws), ws.numel(), st), "dqgemm_fwd")
     else:
         C.check(C.lib().concord_gemm_bf16_fwd(
             C.ptr(x2), x2.stride(0), C.ptr(weight_buf), weight_buf.stride(0), C.ptr(bias),
-            C.ptr(y), y.stride(0), M, N, K, st), "gemm_bf16_fwd")
+            C.ptr(y), y.stride(0), M, N, K, C.ptr(ws), ws.numel(), st), "gemm_bf16_fwd")
     return y
 
 
@@ -470,15 +486,16 @@ def _gemm_dgrad(dy, packed_w, row_exp, col_exp, mantissa_bias, weight_buf):
     K = (weight_buf if weight_buf is not None else packed_w).shape[1]
     dx = torch.empty((M, K), dtype=torch.bfloat16, device=dy.device)
     st = C.stream_of(dy.device)
+    ws = _gemm_workspace(dy.device, M, N, K)
     if weight_buf is None:
         C.check(C.lib().concord_dqgemm_dgrad(
             C.ptr(dy), dy.stride(0), C.ptr(packed_w), packed_w.stride(0), C.ptr(row_exp),
-            C.ptr(col_exp), int(mantissa_bias), C.ptr(dx), dx.stride(0), M, N, K, st),
-            "dqgemm_dgrad")
+            C.ptr(col_exp), int(mantissa_bias), C.ptr(dx), dx.stride(0), M, N, K,
+            C.ptr(ws), ws.numel(), st), "dqgemm_dgrad")
     else:
         C.check(C.lib().concord_gemm_bf16_dgrad(
             C.ptr(dy), dy.stride(0), C.ptr(weight_buf), weight_buf.stride(0), C.ptr(dx),
-            dx.stride(0), M, N, K, st), "gemm_bf16_dgrad")
+            dx.stride(0), M, N, K, C.ptr(ws), ws.numel(), st), "gemm_bf16_dgrad")
     return dx
 
 
@@ -486,8 +503,10 @@ def _wgrad(dy, x2):
     M, N = dy.shape
     K = x2.shape[1]
     gw = torch.empty((N, K), dtype=torch.bfloat16, device=dy.device)
+    ws = _gemm_workspace(dy.device, M, N, K)
     C.check(C.lib().concord_wgrad(C.ptr(dy), dy.stride(0), C.ptr(x2), x2.stride(0), C.ptr(gw),
-                                  gw.stride(0), M, N, K, C.stream_of(dy.device)), "wgrad")
+                                  gw.stride(0), M, N, K, C.ptr(ws), ws.numel(),
+                                  C.stream_of(dy.device)), "wgrad")
     return gw
 
 

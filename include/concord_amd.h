@@ -148,6 +148,14 @@ int concord_load_weights(const float* W, int64_t ld_w, int64_t N, int64_t K, int
                          int32_t exp_max, int32_t mantissa_bias, int finetune, int32_t* packed,
                          int64_t ld_p, int8_t* row_exp, int8_t* col_exp, void* stream);
 
+/* The GEMM entry points below take an optional split-K workspace (NULL /
+ * 0 = never split): concord_gemm_workspace_bytes(M, N, K) bytes, zero-filled
+ * once when allocated; each call leaves its tile counters at zero again.
+ * With a workspace, a GEMM whose tile grid is too small for the chip is split
+ * 2-way along the reduction and the halves are added in a fixed way
+ * (bit-identical whichever half finishes first). */
+size_t concord_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K);
+
 /* Dequant-GEMM forward: y[M,N] = x[M,K] . decode(packed)[N,K]^T (+ bias[N]),
  * bf16 in/out, fp32 accumulation on bf16 MFMA.  Replaces
  * F.linear(x, weight_buf, bias), concord/packed_b.py:1216-1219.  bias may be
@@ -155,30 +163,31 @@ int concord_load_weights(const float* W, int64_t ld_w, int64_t N, int64_t K, int
 int concord_dqgemm_fwd(const uint16_t* x, int64_t ld_x, const int32_t* packed, int64_t ld_p,
                        const int8_t* row_exp, const int8_t* col_exp, int32_t mantissa_bias,
                        const uint16_t* bias, uint16_t* y, int64_t ld_y, int64_t M, int64_t N,
-                       int64_t K, void* stream);
+                       int64_t K, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Dequant-GEMM dgrad: dx[M,K] = dy[M,N] . decode(packed)[N,K], on the
  * pre-update weight.  Replaces grad_y @ weight, concord/packed_b.py:1263. */
 int concord_dqgemm_dgrad(const uint16_t* dy, int64_t ld_dy, const int32_t* packed, int64_t ld_p,
                          const int8_t* row_exp, const int8_t* col_exp, int32_t mantissa_bias,
                          uint16_t* dx, int64_t ld_dx, int64_t M, int64_t N, int64_t K,
+                         void* workspace, size_t workspace_bytes,
                          void* stream);
 
 /* wgrad: grad_w[N,K] = bf16(dy[M,N]^T . x[M,K]) with fp32 accumulation.
  * Replaces grad_y_flat.T @ x_flat, concord/packed_b.py:1269-1277. */
 int concord_wgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t ld_x,
                   uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
-                  void* stream);
+                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* The forward and dgrad products over a materialised bf16 weight w[N,K]: the
  * reference's cached weight_buf path, F.linear(x, weight_buf, bias) and
  * grad_y @ weight_buf (concord/packed_b.py:1219, 1263). */
 int concord_gemm_bf16_fwd(const uint16_t* x, int64_t ld_x, const uint16_t* w, int64_t ld_w,
                           const uint16_t* bias, uint16_t* y, int64_t ld_y, int64_t M, int64_t N,
-                          int64_t K, void* stream);
+                          int64_t K, void* workspace, size_t workspace_bytes, void* stream);
 int concord_gemm_bf16_dgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* w, int64_t ld_w,
                             uint16_t* dx, int64_t ld_dx, int64_t M, int64_t N, int64_t K,
-                            void* stream);
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /* grad_bias[N] = bf16(sum_m dy[m, n]) with fp32 accumulation.  Replaces
  * grad_y_flat.sum(0), concord/packed_b.py:1338-1340. */

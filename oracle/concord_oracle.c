@@ -540,7 +540,7 @@ void oracle_rebalance(int32_t* packed, int8_t* row_exp, int8_t* col_exp,
  * sum_v_inv = 1 / max(sum_n v_row, 1e-30).
  * Reduction order (this build's definition; the reference leaves it to torch):
  *   row partial  P_r[c][n] = sum over k in [64c, 64c+64) ascending, from 0.0f
- *   col partial  P_c[r][k] = sum over n in [32r, 32r+32) ascending, from 0.0f
+ *   col partial  P_c[r][k] = sum over n in [128r, 128r+128) ascending, from 0.0f
  *   g2_row[n] = sum over c ascending of P_r[c][n]; g2_col[k] likewise over r
  *   sum_v: 256 strided partials s_t = sum_{n = t mod 256} v_row[n] (ascending
  *   n), then the tree s_t += s_{t+h} for h = 128, 64, ..., 1. */
@@ -549,7 +549,7 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
                      double beta2) {
     const float b2 = (float)beta2;
     const float omb2 = (float)(1.0 - beta2);
-    const int64_t nc = (K + 63) / 64, nr = (N + 31) / 32;
+    const int64_t nc = (K + 63) / 64, nr = (N + 127) / 128;
     float* pr = (float*)malloc((size_t)(nc * N) * sizeof(float));
     float* pc = (float*)malloc((size_t)(nr * K) * sizeof(float));
 #pragma omp parallel for schedule(static)
@@ -567,7 +567,7 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
     for (int64_t r = 0; r < nr; ++r) {
         for (int64_t k = 0; k < K; ++k) {
             float s = 0.0f;
-            for (int64_t n = 32 * r; n < 32 * r + 32 && n < N; ++n) {
+            for (int64_t n = 128 * r; n < 128 * r + 128 && n < N; ++n) {
                 float g = bf16_to_f32(grad_bf16[n * K + k]);
                 s = s + g * g;
             }

@@ -64,7 +64,8 @@ def test_materialize_strided(oracle):
     out_full = torch.zeros((N, K + 5), dtype=torch.bfloat16, device=DEV)
     out = out_full[:, :K]
     from concord_amd import _lib as C
-    C.check(C.lib().concord_materialize(C.ptr(pk), pk.stride(0), C.ptr(dev(re)), C.ptr(dev(ce)), N, K,
+    red, ced = dev(re), dev(ce)   # keep the device copies alive across the launch
+    C.check(C.lib().concord_materialize(C.ptr(pk), pk.stride(0), C.ptr(red), C.ptr(ced), N, K,
                                         15, 0, C.ptr(out), out.stride(0), C.stream_of(DEV)), "mat")
     sync()
     np.testing.assert_array_equal(host(out), oracle.materialize(np.ascontiguousarray(big[:, :K]), re, ce))
@@ -402,7 +403,7 @@ def test_load_weights_matches_oracle(oracle):
 # ---------------------------------------------------------------- GEMMs
 
 GEMM_SHAPES = [(64, 128, 64), (77, 130, 200), (256, 384, 1280), (1, 5, 3), (130, 1000, 70),
-               (2048, 1280, 1280)]
+               (2048, 1280, 1280), (2048, 5120, 1280), (300, 2050, 645)]
 
 
 def _decoded(oracle, packed, re, ce):
@@ -447,6 +448,21 @@ def test_wgrad(oracle, M, N, K):
     sync()
     ref = oracle.bf16_bits_to_f32(dy).astype(np.float64).T @ oracle.bf16_bits_to_f32(x)
     assert rel_l2(oracle.bf16_bits_to_f32(host(gw)), ref) < 5e-3
+
+
+def test_gemm_splitk_workspace_reuse(oracle):
+    """Back-to-back split-K GEMMs of different tile grids share one workspace:
+    each call must find its counters zeroed whatever the previous call's
+    partials overwrote (small grid first, then larger ones, then small again)."""
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(99)
+    for (M, N, K) in [(300, 200, 130), (300, 2050, 645), (77, 130, 200), (300, 2050, 645)]:
+        dy = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, N)).astype(np.float32))
+        x = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32))
+        gw = pb._wgrad(dev(dy), dev(x))
+        sync()
+        ref = oracle.bf16_bits_to_f32(dy).astype(np.float64).T @ oracle.bf16_bits_to_f32(x)
+        assert rel_l2(oracle.bf16_bits_to_f32(host(gw)), ref) < 5e-3, (M, N, K)
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES[:4])
