@@ -1,0 +1,60 @@
+// gemm.h -- shared definitions of the GEMM kernels (gemm.hip: generic
+// kernel for any strides; gemm_fast.hip: branch-free kernels for aligned
+// operands).
+#pragma once
+#include "common.h"
+
+namespace concord {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+enum { MODE_FWD = 0, MODE_DGRAD = 1, MODE_WGRAD = 2, MODE_FWD_BF16 = 3, MODE_DGRAD_BF16 = 4 };
+
+constexpr int TR = 64;          // reduction depth per LDS stage
+constexpr int LDS_STRIDE = 72;  // bf16 per LDS row (64 + 8 pad)
+
+struct GemmArgs {
+  const uint16_t* a;      // FWD: x[M,K]; DGRAD*, WGRAD: dy[M,N]
+  const void* b;          // packed[N,K] int32 | x[M,K] bf16 (WGRAD) | W[N,K] bf16 (*_BF16)
+  int64_t lda, ldb;
+  const int8_t* row_exp;  // packed rows (n)
+  const int8_t* col_exp;  // packed cols (k)
+  int32_t bias;           // mantissa bias
+  const uint16_t* vbias;  // bias[J] added in the epilogue, or NULL
+  uint16_t* c;
+  int64_t ldc;
+  int64_t I, J, R;        // C is I x J, reduction R
+  int64_t r_split;        // reduction length per split (multiple of TR)
+  float* part;            // split-K: 2 x I x J fp32 partials
+  uint32_t* tile_cnt;     // split-K: one counter per (i, j) tile, zero between calls
+  int tiles_i, tiles_j, splits;
+  int vec_a, vec_b, vec_c;  // base pointers and leading dimensions allow 16 B / 8 B accesses
+};
+
+// XCD-aware tile order: workgroup w runs on XCD w % 8.  XCD x owns tile
+// indices [x*T/8, (x+1)*T/8) of a grouped row-major order (groups of GI
+// i-tiles), so the CUs of one XCD share i- and j-tiles in their L2.
+CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
+  // XCD x owns q + (x < rem) consecutive indices starting at x*q + min(x, rem):
+  // a bijection of [0, total) for any total
+  const int xcd = w % 8, slot = w / 8;
+  const int q = total / 8, rem = total % 8;
+  const int lin = xcd * q + min(xcd, rem) + slot;
+  const int GI = 8;
+  const int group = lin / (GI * tj);
+  const int first_i = group * GI;
+  const int gsize = min(ti - first_i, GI);
+  const int in = lin % (GI * tj);
+  bi = first_i + in % gsize;
+  bj = in / gsize;
+}
+
+// launch a fast-path kernel when the operands satisfy its alignment rules;
+// returns CONCORD_OK, an error code, or -1 when the generic kernel must run
+int gemm_fast_launch(int mode, const GemmArgs& g, void* workspace, size_t ws_bytes,
+                     hipStream_t st, const char* what);
+// number of split-K ways the fast kernels plan for an I x J x R problem
+int gemm_fast_splits(int mode, int64_t I, int64_t J, int64_t R);
+
+}  // namespace concord

@@ -21,36 +21,10 @@
 // fixup (the second finisher adds the first's fp32 partial: a + b = b + a).
 // Tiles are mapped XCD-aware: workgroup w runs on XCD w % 8, and each XCD
 // gets a compact block of the tile grid so its L2 serves shared operands.
-#include "common.h"
+#include "gemm.h"
 #include "workspace.h"
 
 namespace concord {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-enum { MODE_FWD = 0, MODE_DGRAD = 1, MODE_WGRAD = 2, MODE_FWD_BF16 = 3, MODE_DGRAD_BF16 = 4 };
-
-constexpr int TR = 64;          // reduction depth per LDS stage
-constexpr int LDS_STRIDE = 72;  // bf16 per LDS row (64 + 8 pad)
-
-struct GemmArgs {
-  const uint16_t* a;      // FWD: x[M,K]; DGRAD*, WGRAD: dy[M,N]
-  const void* b;          // packed[N,K] int32 | x[M,K] bf16 (WGRAD) | W[N,K] bf16 (*_BF16)
-  int64_t lda, ldb;
-  const int8_t* row_exp;  // packed rows (n)
-  const int8_t* col_exp;  // packed cols (k)
-  int32_t bias;           // mantissa bias
-  const uint16_t* vbias;  // bias[J] added in the epilogue, or NULL
-  uint16_t* c;
-  int64_t ldc;
-  int64_t I, J, R;        // C is I x J, reduction R
-  int64_t r_split;        // reduction length per split (multiple of TR)
-  float* part;            // split-K: 2 x I x J fp32 partials
-  uint32_t* tile_cnt;     // split-K: one counter per (i, j) tile, zero between calls
-  int tiles_i, tiles_j, splits;
-  int vec_a, vec_b, vec_c;  // base pointers and leading dimensions allow 16 B / 8 B accesses
-};
 
 CONCORD_DEV float decode_word(int32_t w, int32_t e) {
   const Fields f = unpack(w);
@@ -299,24 +273,6 @@ struct Tiles {
   }
 };
 
-// XCD-aware tile order: workgroup w runs on XCD w % 8.  XCD x owns tile
-// indices [x*T/8, (x+1)*T/8) of a grouped row-major order (groups of GI
-// i-tiles), so the CUs of one XCD share i- and j-tiles in their L2.
-CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
-  // XCD x owns q + (x < rem) consecutive indices starting at x*q + min(x, rem):
-  // a bijection of [0, total) for any total
-  const int xcd = w % 8, slot = w / 8;
-  const int q = total / 8, rem = total % 8;
-  const int lin = xcd * q + min(xcd, rem) + slot;
-  const int GI = 8;
-  const int group = lin / (GI * tj);
-  const int first_i = group * GI;
-  const int gsize = min(ti - first_i, GI);
-  const int in = lin % (GI * tj);
-  bi = first_i + in % gsize;
-  bj = in / gsize;
-}
-
 template <int MODE, int BI, int BJ, int WI, int WJ>
 __global__ __launch_bounds__(256, 1) void gemm_kernel(GemmArgs g) {
   constexpr int WTI = BI / WI, WTJ = BJ / WJ;   // wave tile
@@ -480,6 +436,8 @@ template <int MODE>
 static int launch_gemm(GemmArgs g, void* workspace, size_t ws_bytes, hipStream_t st,
                        const char* what) {
   if (g.I == 0 || g.J == 0) return CONCORD_OK;
+  const int fast = gemm_fast_launch(MODE, g, workspace, ws_bytes, st, what);
+  if (fast != -1) return fast;
   const bool can_split = workspace != nullptr;
   Plan p = plan_gemm(g.I, g.J, g.R, can_split);
   if (p.splits == 2 &&
@@ -525,13 +483,24 @@ static GemmArgs make_args(const uint16_t* a, const void* b, int64_t lda, int64_t
 
 using namespace concord;
 
+// split-K partial bytes one GEMM may use (fast or generic kernel), 0 if unsplit
+static size_t splitk_partials(int mode, int64_t I, int64_t J, int64_t R) {
+  const int sf = gemm_fast_splits(mode, I, J, R);
+  const int sg = plan_gemm(I, J, R, true).splits;
+  const int s = sf > sg ? sf : sg;
+  return s > 1 ? (size_t)s * (size_t)I * (size_t)J * sizeof(float) : 0;
+}
+
 extern "C" size_t concord_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
-  // split-K partials of the largest of the three outputs: y [M,N], dx [M,K], gw [N,K]
+  // tile counters + the split-K partials of the largest need among the layer's
+  // three products: y [M,N] (reduce K), dx [M,K] (reduce N), gw [N,K] (reduce M)
   if (M < 1) M = 1;
   if (N < 1) N = 1;
   if (K < 1) K = 1;
-  size_t a = gemm_splitk_bytes(M, N), b = gemm_splitk_bytes(M, K), c = gemm_splitk_bytes(N, K);
-  return a > b ? (a > c ? a : c) : (b > c ? b : c);
+  const size_t a = splitk_partials(MODE_FWD, M, N, K), b = splitk_partials(MODE_DGRAD, M, K, N),
+               c = splitk_partials(MODE_WGRAD, N, K, M);
+  const size_t m = a > b ? (a > c ? a : c) : (b > c ? b : c);
+  return kSplitkCounterBytes + ((m + 255) / 256) * 256;
 }
 
 extern "C" int concord_dqgemm_fwd(const uint16_t* x, int64_t ld_x, const int32_t* packed,

@@ -1,0 +1,1055 @@
+// gemm_fast.hip -- branch-free bf16 MFMA GEMM kernels for aligned operands
+// (the problem statement and modes are in gemm.h; gemm.hip holds the generic
+// kernel that serves every other stride and alignment).
+//
+// What makes these kernels fast on gfx950:
+//  * every global read is a buffer load; a lane whose element lies outside the
+//    operand gets an offset past the buffer end and the hardware returns zero.
+//    Edge tiles and the reduction tail need no branches, so one pipeline stage
+//    is one basic block the scheduler can interleave freely.
+//  * a packed word decodes with plain integer/float VALU ops only (the matrix
+//    core runs them alongside the MFMAs; v_dot4 and v_cvt_f32_i32 would
+//    stall it): m_eff = sf + 128 (ss + vs) is added to the bit pattern M of
+//    1.5 * 2^(23+e), and subtracting that float leaves m_eff * 2^e exactly,
+//    e being the exponent that varies along the reduction.  The exponent of
+//    the other side is constant along each output column and is applied in
+//    the epilogue: scaling by a power of two commutes with fp32 rounding, so
+//    the result equals the product with the fully decoded weight
+//    bf16(m_eff * 2^(row_exp + col_exp - bias)).
+//  * the large tiles split each block into compute waves (LDS fragments ->
+//    MFMA, and the activation operand moved straight from global memory into
+//    LDS by buffer-load DMA) and producer waves (weight loads two stages
+//    ahead, decode, LDS writes).
+//  * split-K over S ways is deterministic: the last block of a tile to finish
+//    sums the S fp32 partials in split order.
+#include <algorithm>
+#include <cmath>
+
+#include "gemm.h"
+#include "workspace.h"
+
+namespace concord {
+namespace {
+
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
+
+// a voffset at or past every buffer's num_records (which stay below 2^31)
+constexpr uint32_t kOOB = 0x80000000u;
+constexpr int kMaxSplits = 4;
+
+CONCORD_DEV Rsrc make_rsrc(const void* p, uint32_t bytes) {
+  // dword 3 = 0x00020000: 32-bit data format, raw (stride 0) addressing
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+// soffset is the stage offset, the same for the whole wave; readfirstlane
+// states that to the compiler, which otherwise may wrap each load in a
+// per-lane loop when it cannot prove the value uniform
+CONCORD_DEV uint32_t uni(uint32_t v) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)v); }
+CONCORD_DEV i32x4 ld128(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, uni(soff), 0);
+}
+CONCORD_DEV i32x2 ld64(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, voff, uni(soff), 0);
+}
+CONCORD_DEV int32_t ld32(Rsrc r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, uni(soff), 0);
+}
+
+// m_eff * 2^e of one packed word, exactly, with plain integer/float VALU ops
+// only (they co-execute with MFMAs; v_dot4 and v_cvt_f32_i32 do not):
+// with M = bits of 1.5 * 2^(23+e), the float whose bits are M + m is
+// 1.5 * 2^(23+e) + m * 2^e for |m| < 2^22, so subtracting 1.5 * 2^(23+e)
+// leaves m * 2^e.  m_eff = sf + 128 (ss + vs) lies in [-65536, 65279].
+CONCORD_DEV uint32_t magic(int32_t e) { return ((uint32_t)(150 + e) << 23) | 0x400000u; }
+CONCORD_DEV float dec(int32_t w, uint32_t M) {
+  const int32_t t = (int32_t)(int8_t)(w >> 8) + (int32_t)(int8_t)w;   // ss + vs
+  const uint32_t b = ((uint32_t)t << 7) + M + (uint32_t)(w >> 16);    // + 128 (ss + vs) + sf
+  return __fsub_rn(__uint_as_float(b), __uint_as_float(M));
+}
+
+CONCORD_DEV int32_t sbyte(int32_t v, int i) { return __builtin_amdgcn_sbfe(v, 8 * i, 8); }
+
+// Redefine raw load registers at the point of their decode.  The decode is
+// pure arithmetic, which the compiler would otherwise hoist across the LDS
+// barrier into the previous pipeline stage, forcing that stage to wait for
+// loads issued only just before it.
+template <typename T> CONCORD_DEV void pin(T& v) { asm volatile("" : "+v"(v)); }
+
+// ---- operand loaders --------------------------------------------------------
+// Each loader owns per-thread byte offsets (fixed for the whole reduction; a
+// lane outside the operand holds kOOB) and moves one TR-deep stage of its tile
+// from global memory into a Raw register set (load) and from there into LDS as
+// bf16 [row][r] with r contiguous (store).  `rem` = reduction elements left
+// from the stage start; r >= rem reads zero.  NT = threads per block.
+
+// bf16 [rows][R], r contiguous; chunk = 8 bf16.  Thread t: r = 8 (t % 8),
+// rows t/8 + (NT/8) q.  When the rows do not split evenly, the surplus rows
+// read zeros into LDS padding rows (LROWS >= ROWS).
+template <int ROWS, int NT>
+struct RowsBf16 {
+  static constexpr int PER = (ROWS * 8 + NT - 1) / NT;
+  static constexpr int LROWS = PER * NT / 8;
+  static constexpr int NLOADS = PER, NWRITES = PER, NVALU = PER;
+  struct Raw { i32x4 v[PER]; };
+  uint32_t voff[PER];
+  int32_t kc;
+  Rsrc rs;
+  CONCORD_DEV void init(const uint16_t* band, int64_t ld, int64_t rows_left, int64_t R, int t) {
+    kc = (t % 8) * 8;
+    rs = make_rsrc(band, (uint32_t)(((rows_left - 1) * ld + R) * 2));
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int64_t row = t / 8 + (NT / 8) * q;
+      voff[q] = (row < rows_left && row < ROWS) ? (uint32_t)((row * ld + kc) * 2) : kOOB;
+    }
+  }
+  CONCORD_DEV void load(Raw& r, int64_t r0, int64_t rem) const {
+    const bool ok = kc < rem;
+    const uint32_t so = (uint32_t)(r0 * 2);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) r.v[q] = ld128(rs, ok ? voff[q] : kOOB, so);
+  }
+  CONCORD_DEV void store(Raw& r, uint16_t* lds, int t) const {
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+      *reinterpret_cast<i32x4*>(lds + (t / 8 + (NT / 8) * q) * LDS_STRIDE + kc) = r.v[q];
+  }
+};
+
+// packed [rows][R] int32, r contiguous (the forward's W[n][k]); chunk = 4
+// words.  Thread t: r = 4 (t % 16), rows t/16 + (NT/16) q.  The per-r
+// column exponents are applied while decoding.
+template <int ROWS, int NT>
+struct RowsPacked {
+  static constexpr int PER = ROWS * 16 / NT;
+  static constexpr int LROWS = ROWS;
+  static constexpr int NLOADS = PER + 1, NWRITES = PER, NVALU = 19 * PER + 4;
+  static_assert(PER * NT == ROWS * 16, "tile rows must split evenly over the threads");
+  struct Raw { i32x4 v[PER]; int32_t ex; };
+  uint32_t voff[PER];
+  int32_t kc;
+  Rsrc rs, es;
+  CONCORD_DEV void init(const int32_t* band, int64_t ld, int64_t rows_left, int64_t R,
+                        const int8_t* exps, int t) {
+    kc = (t % 16) * 4;
+    rs = make_rsrc(band, (uint32_t)(((rows_left - 1) * ld + R) * 4));
+    es = make_rsrc(exps, (uint32_t)R);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int64_t row = t / 16 + (NT / 16) * q;
+      voff[q] = row < rows_left ? (uint32_t)((row * ld + kc) * 4) : kOOB;
+    }
+  }
+  CONCORD_DEV void load(Raw& r, int64_t r0, int64_t rem) const {
+    const bool ok = kc < rem;
+    const uint32_t so = (uint32_t)(r0 * 4);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) r.v[q] = ld128(rs, ok ? voff[q] : kOOB, so);
+    r.ex = ld32(es, ok ? (uint32_t)kc : kOOB, (uint32_t)r0);
+  }
+  CONCORD_DEV void store(Raw& r, uint16_t* lds, int t) const {
+    pin(r.ex);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) pin(r.v[q]);
+    const uint32_t e0 = magic(sbyte(r.ex, 0)), e1 = magic(sbyte(r.ex, 1)), e2 = magic(sbyte(r.ex, 2)),
+                   e3 = magic(sbyte(r.ex, 3));
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      uint2 o;
+      o.x = pack_bf16x2(dec(r.v[q].x, e0), dec(r.v[q].y, e1));
+      o.y = pack_bf16x2(dec(r.v[q].z, e2), dec(r.v[q].w, e3));
+      *reinterpret_cast<uint2*>(lds + (t / 16 + (NT / 16) * q) * LDS_STRIDE + kc) = o;
+    }
+  }
+};
+
+// Column loaders: [R][cols] with cols contiguous, moved in blocks of RB r x 4
+// cols.  Thread t: r = RB (t % (TR/RB)) .. +RB-1, cols 4 (t / (TR/RB) +
+// (NT / (TR/RB)) q).  RB = 8 when the tile has enough blocks for every
+// thread, else 4.
+template <int COLS, int NT>
+struct ColGeom {
+  static constexpr int RB = (TR / 8) * (COLS / 4) >= NT ? 8 : 4;
+  static constexpr int NRB = TR / RB;   // row blocks per stage
+  static constexpr int PER = NRB * (COLS / 4) / NT;
+  static_assert(PER >= 1 && PER * NT == NRB * (COLS / 4), "column tile must split evenly over the threads");
+  static CONCORD_DEV int rb(int t) { return (t % NRB) * RB; }
+  static CONCORD_DEV int col(int t, int q) { return 4 * (t / NRB + (NT / NRB) * q); }
+};
+
+// packed int32 (the dgrad's W[n][k] with r = n).  Per-r row exponents are
+// applied while decoding, and the bf16 pairs are formed along r, so the
+// transpose costs nothing.
+template <int COLS, int NT>
+struct ColsPacked {
+  typedef ColGeom<COLS, NT> G;
+  static constexpr int PER = G::PER, RB = G::RB, LROWS = COLS;
+  static constexpr int NLOADS = PER * RB + RB / 4, NWRITES = 4 * PER, NVALU = PER * (RB * 18 + RB) + RB;
+  struct Raw { i32x4 v[PER][RB]; int32_t ex[RB / 4]; };
+  uint32_t voff[PER];
+  uint32_t ld4;
+  int32_t rb;
+  Rsrc rs, es;
+  CONCORD_DEV void init(const int32_t* band, int64_t ld, int64_t cols_left, int64_t R,
+                        const int8_t* exps, int t) {
+    rb = G::rb(t);
+    ld4 = (uint32_t)(ld * 4);
+    rs = make_rsrc(band, (uint32_t)(((R - 1) * ld + cols_left) * 4));
+    es = make_rsrc(exps, (uint32_t)R);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int64_t col = G::col(t, q);
+      voff[q] = col < cols_left ? (uint32_t)((rb * ld + col) * 4) : kOOB;
+    }
+  }
+  CONCORD_DEV void load(Raw& r, int64_t r0, int64_t rem) const {
+    const uint32_t so = (uint32_t)(r0 * (int64_t)ld4);
+#pragma unroll
+    for (int e = 0; e < RB; ++e) {
+      const bool ok = rb + e < rem;
+#pragma unroll
+      for (int q = 0; q < PER; ++q) r.v[q][e] = ld128(rs, ok ? voff[q] + e * ld4 : kOOB, so);
+    }
+#pragma unroll
+    for (int h = 0; h < RB / 4; ++h)
+      r.ex[h] = ld32(es, rb + 4 * h < rem ? (uint32_t)(rb + 4 * h) : kOOB, (uint32_t)r0);
+  }
+  CONCORD_DEV void store(Raw& r, uint16_t* lds, int t) const {
+#pragma unroll
+    for (int h = 0; h < RB / 4; ++h) pin(r.ex[h]);
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+#pragma unroll
+      for (int e = 0; e < RB; ++e) pin(r.v[q][e]);
+    uint32_t ex[RB];
+#pragma unroll
+    for (int e = 0; e < RB; ++e) ex[e] = magic(sbyte(r.ex[e / 4], e % 4));
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int col = G::col(t, q);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        int32_t o[RB / 2];
+#pragma unroll
+        for (int p = 0; p < RB / 2; ++p)
+          o[p] = (int32_t)pack_bf16x2(dec(r.v[q][2 * p][c], ex[2 * p]), dec(r.v[q][2 * p + 1][c], ex[2 * p + 1]));
+        uint16_t* dst = lds + (col + c) * LDS_STRIDE + rb;
+        if (RB == 8) *reinterpret_cast<i32x4*>(dst) = i32x4{o[0], o[1], o[2 % (RB / 2)], o[3 % (RB / 2)]};
+        else *reinterpret_cast<i32x2*>(dst) = i32x2{o[0], o[1]};
+      }
+    }
+  }
+};
+
+// bf16 (wgrad's dy and x, dgrad's bf16 W): 8-byte loads, transposed with
+// byte permutes.
+template <int COLS, int NT>
+struct ColsBf16 {
+  typedef ColGeom<COLS, NT> G;
+  static constexpr int PER = G::PER, RB = G::RB, LROWS = COLS;
+  static constexpr int NLOADS = PER * RB, NWRITES = 4 * PER, NVALU = PER * (2 * RB + RB);
+  struct Raw { i32x2 v[PER][RB]; };
+  uint32_t voff[PER];
+  uint32_t ld2;
+  int32_t rb;
+  Rsrc rs;
+  CONCORD_DEV void init(const uint16_t* band, int64_t ld, int64_t cols_left, int64_t R, int t) {
+    rb = G::rb(t);
+    ld2 = (uint32_t)(ld * 2);
+    rs = make_rsrc(band, (uint32_t)(((R - 1) * ld + cols_left) * 2));
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int64_t col = G::col(t, q);
+      voff[q] = col < cols_left ? (uint32_t)((rb * ld + col) * 2) : kOOB;
+    }
+  }
+  CONCORD_DEV void load(Raw& r, int64_t r0, int64_t rem) const {
+    const uint32_t so = (uint32_t)(r0 * (int64_t)ld2);
+#pragma unroll
+    for (int e = 0; e < RB; ++e) {
+      const bool ok = rb + e < rem;
+#pragma unroll
+      for (int q = 0; q < PER; ++q) r.v[q][e] = ld64(rs, ok ? voff[q] + e * ld2 : kOOB, so);
+    }
+  }
+  CONCORD_DEV void store(Raw& r, uint16_t* lds, int t) const {
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+#pragma unroll
+      for (int e = 0; e < RB; ++e) pin(r.v[q][e]);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int col = G::col(t, q);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        // column c of the RB x 4 block: rows (2p, 2p+1) -> dword p
+        const int dw = c >> 1;
+        const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+        int32_t o[RB / 2];
+#pragma unroll
+        for (int p = 0; p < RB / 2; ++p)
+          o[p] = (int32_t)__builtin_amdgcn_perm((uint32_t)r.v[q][2 * p + 1][dw],
+                                                (uint32_t)r.v[q][2 * p][dw], sel);
+        uint16_t* dst = lds + (col + c) * LDS_STRIDE + rb;
+        if (RB == 8) *reinterpret_cast<i32x4*>(dst) = i32x4{o[0], o[1], o[2 % (RB / 2)], o[3 % (RB / 2)]};
+        else *reinterpret_cast<i32x2*>(dst) = i32x2{o[0], o[1]};
+      }
+    }
+  }
+};
+
+// ---- per-mode operand pairs -------------------------------------------------
+template <int MODE, int BI, int BJ, int NT> struct Ops;
+
+template <int BI, int BJ, int NT> struct Ops<MODE_FWD, BI, BJ, NT> {
+  RowsBf16<BI, NT> a;
+  RowsPacked<BJ, NT> b;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t i0, int64_t j0, int t) {
+    a.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, t);
+    b.init(reinterpret_cast<const int32_t*>(g.b) + j0 * g.ldb, g.ldb, g.J - j0, g.R, g.col_exp, t);
+  }
+};
+template <int BI, int BJ, int NT> struct Ops<MODE_FWD_BF16, BI, BJ, NT> {
+  RowsBf16<BI, NT> a;
+  RowsBf16<BJ, NT> b;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t i0, int64_t j0, int t) {
+    a.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, t);
+    b.init(reinterpret_cast<const uint16_t*>(g.b) + j0 * g.ldb, g.ldb, g.J - j0, g.R, t);
+  }
+};
+template <int BI, int BJ, int NT> struct Ops<MODE_DGRAD, BI, BJ, NT> {
+  RowsBf16<BI, NT> a;
+  ColsPacked<BJ, NT> b;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t i0, int64_t j0, int t) {
+    a.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, t);
+    b.init(reinterpret_cast<const int32_t*>(g.b) + j0, g.ldb, g.J - j0, g.R, g.row_exp, t);
+  }
+};
+template <int BI, int BJ, int NT> struct Ops<MODE_DGRAD_BF16, BI, BJ, NT> {
+  RowsBf16<BI, NT> a;
+  ColsBf16<BJ, NT> b;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t i0, int64_t j0, int t) {
+    a.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, t);
+    b.init(reinterpret_cast<const uint16_t*>(g.b) + j0, g.ldb, g.J - j0, g.R, t);
+  }
+};
+template <int BI, int BJ, int NT> struct Ops<MODE_WGRAD, BI, BJ, NT> {
+  ColsBf16<BI, NT> a;
+  ColsBf16<BJ, NT> b;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t i0, int64_t j0, int t) {
+    a.init(g.a + i0, g.lda, g.I - i0, g.R, t);
+    b.init(reinterpret_cast<const uint16_t*>(g.b) + j0, g.ldb, g.J - j0, g.R, t);
+  }
+};
+
+// Workgroup barrier that orders LDS only.  __syncthreads() also acquires
+// global memory, which waits for every outstanding buffer load (vmcnt(0)) and
+// so would cap the prefetch distance at one stage.
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
+// memory operations are outstanding and leaves the other counters alone
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | (0x7 << 4) | (0xF << 8) | (((n >> 4) & 3) << 14); }
+
+CONCORD_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// ---- instruction schedule of one pipeline stage -------------------------------
+// Per wave and stage: NRD fragment reads per 32-deep sub-step, NM MFMAs, NLD
+// buffer loads of stage s+2, NWR LDS writes of stage s+1 and NV decode VALU
+// ops.  The order handed to the scheduler: the first sub-step's fragment
+// reads; then the first half of the MFMAs, each followed by one buffer load
+// (with the VALU op that picks its offset) and one fragment read of the
+// second sub-step; then the second half of the MFMAs, each followed by its
+// share of the decode and the LDS writes.  The decode of stage s+1 thereby
+// starts half a stage after the loads of stage s+2 are on their way, and the
+// matrix core, the VALU, the LDS and the memory pipeline overlap.
+template <int NM, int NRD, int NLD, int NWR, int NV>
+CONCORD_DEV void sched_stage() {
+  constexpr int H = NM / 2;
+  constexpr int VPM = (NV + (NM - H) - 1) / (NM - H);
+  __builtin_amdgcn_sched_group_barrier(0x100, NRD, 0);   // DS read: sub-step 0 fragments
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+    if (i < NLD) {
+      __builtin_amdgcn_sched_group_barrier(0x002, 1, 0);   // VALU: the load's offset
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // VMEM read
+    }
+    if (i >= 1 && i < 1 + NRD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // DS read: sub-step 1
+  }
+#pragma unroll
+  for (int i = H; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);  // VALU: decode
+    if (((i - H) % 2) == 1 && (i - H) / 2 < NWR) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // DS write
+  }
+}
+
+// ---- epilogue shared by the kernels ------------------------------------------
+// Split-K fixup (every thread of the block takes part in its barriers; only
+// threads with `active` accumulators write) and the store: the column scale
+// 2^(exp - bias) of the side not decoded in the loop, the bias, bf16 rounding
+// and 8-byte stores (J % 4 == 0 and ldc % 4 == 0).
+// lane holds C[ib + 16x][jb + 16y + e], e = 0..3
+template <int MODE, int NI, int NJ>
+CONCORD_DEV void epilogue(const GemmArgs& g, f32x4 (&acc)[NI][NJ], int64_t ib, int64_t jb, int split,
+                          int tile, bool active, int t, uint32_t* s_old) {
+  if (g.splits > 1) {
+    const int64_t IJ = g.I * g.J;
+    if (active) {
+      float* mine = g.part + (int64_t)split * IJ;
+#pragma unroll
+      for (int x = 0; x < NI; ++x)
+#pragma unroll
+        for (int y = 0; y < NJ; ++y) {
+          const int64_t i = ib + x * 16, j = jb + y * 16;
+          if (i < g.I && j < g.J) *reinterpret_cast<f32x4*>(mine + i * g.J + j) = acc[x][y];
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (t == 0) *s_old = atomicAdd(g.tile_cnt + tile, 1u);
+    __syncthreads();
+    if (*s_old != (uint32_t)(g.splits - 1)) return;
+    __threadfence();
+    if (t == 0) g.tile_cnt[tile] = 0u;
+    if (!active) return;
+    // sum the partials in split order: ((p0 + p1) + p2) + ...
+#pragma unroll
+    for (int x = 0; x < NI; ++x)
+#pragma unroll
+      for (int y = 0; y < NJ; ++y) {
+        const int64_t i = ib + x * 16, j = jb + y * 16;
+        if (i < g.I && j < g.J) {
+          f32x4 sum = split == 0 ? acc[x][y] : *reinterpret_cast<const f32x4*>(g.part + i * g.J + j);
+          for (int s2 = 1; s2 < g.splits; ++s2) {
+            const f32x4 p = s2 == split ? acc[x][y]
+                                        : *reinterpret_cast<const f32x4*>(g.part + s2 * IJ + i * g.J + j);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sum[e] = __fadd_rn(sum[e], p[e]);
+          }
+          acc[x][y] = sum;
+        }
+      }
+  }
+  if (!active) return;
+  const int8_t* cexp = MODE == MODE_FWD ? g.row_exp : MODE == MODE_DGRAD ? g.col_exp : nullptr;
+#pragma unroll
+  for (int y = 0; y < NJ; ++y) {
+    const int64_t j = jb + y * 16;
+    if (j >= g.J) continue;
+    float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
+    if (cexp) {
+      const int32_t e4 = *reinterpret_cast<const int32_t*>(cexp + j);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sc[e] = exp2i(sbyte(e4, e) - g.bias);
+    }
+    if (g.vbias) {
+      const uint2 b4 = *reinterpret_cast<const uint2*>(g.vbias + j);
+      bs[0] = __uint_as_float(b4.x << 16);
+      bs[1] = __uint_as_float(b4.x & 0xFFFF0000u);
+      bs[2] = __uint_as_float(b4.y << 16);
+      bs[3] = __uint_as_float(b4.y & 0xFFFF0000u);
+    }
+#pragma unroll
+    for (int x = 0; x < NI; ++x) {
+      const int64_t i = ib + x * 16;
+      if (i >= g.I) continue;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(__fmul_rn(acc[x][y][e], sc[e]), bs[e]);
+      *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) =
+          make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+  }
+}
+
+// MFMAs of one TR-deep stage for a wave tile of NI x NJ 16x16 blocks whose
+// rows start at LDS rows ra (A) and rb (B).
+template <int NI, int NJ>
+CONCORD_DEV void stage_mfma(f32x4 (&acc)[NI][NJ], const uint16_t* la, const uint16_t* lb, int ra, int rb,
+                            int lane) {
+  const int lrow = lane & 15, lk = (lane >> 4) * 8;
+#pragma unroll
+  for (int kk = 0; kk < TR / 32; ++kk) {
+    bf16x8 fa[NI], fb[NJ];
+#pragma unroll
+    for (int x = 0; x < NI; ++x)
+      fa[x] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(
+                                             la + (ra + x * 16 + lrow) * LDS_STRIDE + kk * 32 + lk));
+#pragma unroll
+    for (int y = 0; y < NJ; ++y)
+      fb[y] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(
+                                             lb + (rb + y * 16 + lrow) * LDS_STRIDE + kk * 32 + lk));
+    // D^T: MFMA rows = j (B tile), columns = i (A tile)
+#pragma unroll
+    for (int x = 0; x < NI; ++x)
+#pragma unroll
+      for (int y = 0; y < NJ; ++y)
+        acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[y], fa[x], acc[x][y], 0, 0, 0);
+  }
+}
+
+// ---- the kernel -------------------------------------------------------------
+// DB: two raw register sets (loads two stages ahead) or one (one stage ahead,
+// for tiles whose raw footprint would not fit twice)
+template <int MODE, int BI, int BJ, int WI, int WJ, int MINB, bool DB, bool SCHED>
+__global__ __launch_bounds__(64 * WI * WJ, MINB) void gemm_fast_kernel(GemmArgs g) {
+  constexpr int NT = 64 * WI * WJ;
+  constexpr int WTI = BI / WI, WTJ = BJ / WJ;   // wave tile
+  constexpr int NI = WTI / 16, NJ = WTJ / 16;
+  static_assert(WTI % 16 == 0 && WTJ % 16 == 0, "wave tile must be a multiple of 16");
+  typedef Ops<MODE, BI, BJ, NT> OpsT;
+  constexpr int LA = decltype(OpsT::a)::LROWS, LB = decltype(OpsT::b)::LROWS;
+  static_assert(LA >= BI && LB >= BJ, "LDS tile rows");
+  __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][LA * LDS_STRIDE];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][LB * LDS_STRIDE];
+  __shared__ uint32_t s_old;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int wi = wave / WJ, wj = wave % WJ;
+  const int tiles = g.tiles_i * g.tiles_j;
+  const int wg = blockIdx.x;
+  const int split = wg / tiles;
+  int bi, bj;
+  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
+  const int64_t r_begin = (int64_t)split * g.r_split;
+  const int64_t r_end = min(g.R, r_begin + g.r_split);
+  const int nst = r_end > r_begin ? (int)((r_end - r_begin + TR - 1) / TR) : 0;
+
+  OpsT op;
+  op.init(g, i0, j0, t);
+  // per-stage instruction counts for the schedule hint
+  constexpr int NLD = decltype(OpsT::a)::NLOADS + decltype(OpsT::b)::NLOADS;
+  constexpr int NWR = decltype(OpsT::a)::NWRITES + decltype(OpsT::b)::NWRITES;
+  constexpr int NV = decltype(OpsT::a)::NVALU + decltype(OpsT::b)::NVALU;
+  typename decltype(op.a)::Raw ra0, ra1;
+  typename decltype(op.b)::Raw rb0, rb1;
+
+  f32x4 acc[NI][NJ];
+#pragma unroll
+  for (int x = 0; x < NI; ++x)
+#pragma unroll
+    for (int y = 0; y < NJ; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int lrow = lane & 15, lk = (lane >> 4) * 8;
+  auto compute = [&](const uint16_t* la, const uint16_t* lb) {
+#pragma unroll
+    for (int kk = 0; kk < TR / 32; ++kk) {
+      bf16x8 fa[NI], fb[NJ];
+#pragma unroll
+      for (int x = 0; x < NI; ++x)
+        fa[x] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(
+                                               la + (wi * WTI + x * 16 + lrow) * LDS_STRIDE + kk * 32 + lk));
+#pragma unroll
+      for (int y = 0; y < NJ; ++y)
+        fb[y] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(
+                                               lb + (wj * WTJ + y * 16 + lrow) * LDS_STRIDE + kk * 32 + lk));
+      // D^T: MFMA rows = j (B tile), columns = i (A tile)
+#pragma unroll
+      for (int x = 0; x < NI; ++x)
+#pragma unroll
+        for (int y = 0; y < NJ; ++y)
+          acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[y], fa[x], acc[x][y], 0, 0, 0);
+    }
+  };
+
+  if (!DB) {
+    if (nst > 0) {
+      op.a.load(ra0, r_begin, r_end - r_begin);
+      op.b.load(rb0, r_begin, r_end - r_begin);
+      op.a.store(ra0, lds_a[0], t);
+      op.b.store(rb0, lds_b[0], t);
+      op.a.load(ra0, r_begin + TR, r_end - r_begin - TR);
+      op.b.load(rb0, r_begin + TR, r_end - r_begin - TR);
+    }
+    lds_barrier();
+    for (int s = 0; s < nst; ++s) {
+      // stage s from LDS buffer s&1; stage s+1 (registers) -> the other
+      // buffer; then stage s+2 -> registers
+      const int cur = s & 1;
+      compute(lds_a[cur], lds_b[cur]);
+      op.a.store(ra0, lds_a[cur ^ 1], t);
+      op.b.store(rb0, lds_b[cur ^ 1], t);
+      const int64_t r2 = r_begin + (int64_t)(s + 2) * TR;
+      op.a.load(ra0, r2, r_end - r2);
+      op.b.load(rb0, r2, r_end - r2);
+      lds_barrier();
+    }
+  } else {
+  if (nst > 0) {
+    op.a.load(ra0, r_begin, r_end - r_begin);
+    op.b.load(rb0, r_begin, r_end - r_begin);
+    op.a.load(ra1, r_begin + TR, r_end - r_begin - TR);
+    op.b.load(rb1, r_begin + TR, r_end - r_begin - TR);
+    op.a.store(ra0, lds_a[0], t);
+    op.b.store(rb0, lds_b[0], t);
+  }
+  lds_barrier();
+  for (int s = 0; s < nst; s += 2) {
+    // stage s from LDS buffer 0; stage s+1 (register set 1) -> LDS buffer 1;
+    // stage s+2 -> register set 0
+    int64_t r2 = r_begin + (int64_t)(s + 2) * TR;
+    op.a.load(ra0, r2, r_end - r2);
+    op.b.load(rb0, r2, r_end - r2);
+    compute(lds_a[0], lds_b[0]);
+    op.a.store(ra1, lds_a[1], t);
+    op.b.store(rb1, lds_b[1], t);
+    if (SCHED) sched_stage<2 * NI * NJ, NI + NJ, NLD, NWR, NV>();
+    lds_barrier();
+    if (s + 1 >= nst) break;
+    r2 += TR;
+    op.a.load(ra1, r2, r_end - r2);
+    op.b.load(rb1, r2, r_end - r2);
+    compute(lds_a[1], lds_b[1]);
+    op.a.store(ra0, lds_a[0], t);
+    op.b.store(rb0, lds_b[0], t);
+    if (SCHED) sched_stage<2 * NI * NJ, NI + NJ, NLD, NWR, NV>();
+    lds_barrier();
+  }
+  }
+
+  const int64_t ib = i0 + wi * WTI + (lane & 15);
+  const int64_t jb = j0 + wj * WTJ + 4 * (lane >> 4);
+  epilogue<MODE, NI, NJ>(g, acc, ib, jb, split, wg % tiles, true, t, &s_old);
+}
+
+// ---- the role-split kernel ----------------------------------------------------
+// 8 waves: waves 0-3 compute (LDS fragments -> MFMA, a 2 x 2 grid of
+// BI/2 x BJ/2 wave tiles), waves 4-7 produce (global loads two stages ahead,
+// decode, LDS writes).  A compute wave and a producer wave share each SIMD,
+// so the producer's VALU work runs while the compute wave's MFMAs execute.
+// One LDS-only barrier per stage; both roles pass the same number of them.
+template <int MODE, int BI, int BJ>
+__global__ __launch_bounds__(512, 1) void gemm_ws_kernel(GemmArgs g) {
+  constexpr int NP = 256;   // producer threads
+  constexpr int WTI = BI / 2, WTJ = BJ / 2;
+  constexpr int NI = WTI / 16, NJ = WTJ / 16;
+  static_assert(WTI % 16 == 0 && WTJ % 16 == 0, "wave tile must be a multiple of 16");
+  typedef Ops<MODE, BI, BJ, NP> OpsT;
+  constexpr int LA = decltype(OpsT::a)::LROWS, LB = decltype(OpsT::b)::LROWS;
+  static_assert(LA >= BI && LB >= BJ, "LDS tile rows");
+  __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][LA * LDS_STRIDE];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][LB * LDS_STRIDE];
+  __shared__ uint32_t s_old;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const bool producer = wave >= 4;
+  const int tiles = g.tiles_i * g.tiles_j;
+  const int wg = blockIdx.x;
+  const int split = wg / tiles;
+  int bi, bj;
+  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
+  const int64_t r_begin = (int64_t)split * g.r_split;
+  const int64_t r_end = min(g.R, r_begin + g.r_split);
+  const int nst = r_end > r_begin ? (int)((r_end - r_begin + TR - 1) / TR) : 0;
+
+  f32x4 acc[NI][NJ];
+#pragma unroll
+  for (int x = 0; x < NI; ++x)
+#pragma unroll
+    for (int y = 0; y < NJ; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int wi = (wave & 3) >> 1, wj = wave & 1;
+
+  if (producer) {
+    const int tp = t - NP;
+    OpsT op;
+    op.init(g, i0, j0, tp);
+    typename decltype(op.a)::Raw ra0, ra1;
+    typename decltype(op.b)::Raw rb0, rb1;
+    // stage 0 -> set 0 -> LDS 0; stage 1 -> set 1; stage 2 -> set 0
+    op.a.load(ra0, r_begin, r_end - r_begin);
+    op.b.load(rb0, r_begin, r_end - r_begin);
+    op.a.load(ra1, r_begin + TR, r_end - r_begin - TR);
+    op.b.load(rb1, r_begin + TR, r_end - r_begin - TR);
+    op.a.store(ra0, lds_a[0], tp);
+    op.b.store(rb0, lds_b[0], tp);
+    op.a.load(ra0, r_begin + 2 * TR, r_end - r_begin - 2 * TR);
+    op.b.load(rb0, r_begin + 2 * TR, r_end - r_begin - 2 * TR);
+    lds_barrier();
+    for (int s = 0; s < nst; s += 2) {
+      // while stage s is computed: stage s+1 (set 1) -> LDS 1, stage s+3 -> set 1
+      int64_t r3 = r_begin + (int64_t)(s + 3) * TR;
+      op.a.store(ra1, lds_a[1], tp);
+      op.b.store(rb1, lds_b[1], tp);
+      op.a.load(ra1, r3, r_end - r3);
+      op.b.load(rb1, r3, r_end - r3);
+      lds_barrier();
+      if (s + 1 >= nst) break;
+      // while stage s+1 is computed: stage s+2 (set 0) -> LDS 0, stage s+4 -> set 0
+      r3 += TR;
+      op.a.store(ra0, lds_a[0], tp);
+      op.b.store(rb0, lds_b[0], tp);
+      op.a.load(ra0, r3, r_end - r3);
+      op.b.load(rb0, r3, r_end - r3);
+      lds_barrier();
+    }
+  } else {
+    lds_barrier();
+    for (int s = 0; s < nst; ++s) {
+      stage_mfma<NI, NJ>(acc, lds_a[s & 1], lds_b[s & 1], wi * WTI, wj * WTJ, lane);
+      lds_barrier();
+    }
+  }
+
+  const int64_t ib = i0 + wi * WTI + (lane & 15);
+  const int64_t jb = j0 + wj * WTJ + 4 * (lane >> 4);
+  epilogue<MODE, NI, NJ>(g, acc, ib, jb, split, wg % tiles, !producer, t, &s_old);
+}
+
+// ---- LDS-DMA kernel ------------------------------------------------------------
+// The A operand (bf16 rows, r contiguous) goes from global memory straight
+// into LDS (buffer_load ... lds, 16 bytes per lane: lane l of a wave
+// instruction writes LDS bytes [16 l, 16 l + 16) above the instruction's base;
+// an out-of-range lane writes zeros).  A stage of A is an unpadded LDS tile of
+// 128-byte rows; chunk c (8 bf16) of row r sits in slot c ^ ((r >> 1) & 7), so
+// the 16 rows of one MFMA fragment read fall in 16 distinct bank groups.  The
+// loads need no VGPRs, so the compute waves issue them themselves, three
+// stages ahead in a ring of three LDS tiles.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// One LDS-DMA buffer load, issued as inline assembly so the compiler does not
+// track it: it cannot tell which ring slot a DMA writes and would otherwise
+// wait for every outstanding DMA before any LDS read.  The kernel waits for
+// its DMAs itself (vmcnt) before each barrier and before it ends.
+CONCORD_DEV void dma16(i32x4 rsrc, uint32_t voff, uint32_t soff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %3\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+               :
+               : "v"(voff), "s"(rsrc), "s"(soff), "s"(lds_base)
+               : "memory", "m0");
+}
+CONCORD_DEV uint32_t lds_addr(const void* p) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(uintptr_t)(lds_ptr_t)p);
+}
+
+template <int ROWS, int NW>
+struct RowsDma {
+  static constexpr int INSTR = ROWS / 8;   // wave instructions per stage (8 rows each)
+  static constexpr int PER = INSTR / NW;   // per issuing wave
+  static_assert(PER * NW == INSTR, "rows must split evenly over the issuing waves");
+  uint32_t voff[PER];
+  int32_t kcq[PER];   // r offset of this lane's chunk, for the reduction tail
+  i32x4 rs;
+  int w;
+  CONCORD_DEV void init(const uint16_t* band, int64_t ld, int64_t rows_left, int64_t R, int wave, int lane) {
+    w = wave;
+    // raw buffer descriptor: base address, stride 0, num_records, dword 3
+    const uint64_t base = (uint64_t)(uintptr_t)band;
+    rs = i32x4{(int32_t)(uint32_t)base, (int32_t)(uint32_t)((base >> 32) & 0xFFFF),
+               (int32_t)(uint32_t)(((rows_left - 1) * ld + R) * 2), 0x00020000};
+    for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(rs[e]);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int r = (w * PER + q) * 8 + lane / 8;
+      const int c = (lane % 8) ^ ((r >> 1) & 7);
+      kcq[q] = c * 8;
+      voff[q] = r < rows_left ? (uint32_t)((r * ld + c * 8) * 2) : kOOB;
+    }
+  }
+  // tile = LDS tile of this stage (ROWS x 64 bf16)
+  CONCORD_DEV void load(uint16_t* tile, int64_t r0, int64_t rem) const {
+    const uint32_t so = uni((uint32_t)(r0 * 2));
+    const uint32_t base = lds_addr(tile);
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+      dma16(rs, kcq[q] < rem ? voff[q] : kOOB, so, uni(base + (uint32_t)((w * PER + q) * 1024)));
+  }
+};
+
+// MFMAs of one stage: A from a swizzled DMA tile, B from a padded tile.
+template <int NI, int NJ>
+CONCORD_DEV void stage_mfma_swz(f32x4 (&acc)[NI][NJ], const uint16_t* la, const uint16_t* lb, int ra, int rb,
+                                int lane) {
+  const int lrow = lane & 15, lk = (lane >> 4) * 8;
+  const int sw = (lane & 14) >> 1;   // (row >> 1) & 7 for row = ra + 16x + lrow
+#pragma unroll
+  for (int kk = 0; kk < TR / 32; ++kk) {
+    const int aoff = lrow * 64 + (((kk * 4 + (lane >> 4)) ^ sw) * 8);
+    bf16x8 fa[NI], fb[NJ];
+#pragma unroll
+    for (int x = 0; x < NI; ++x)
+      fa[x] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(la + (ra + x * 16) * 64 + aoff));
+#pragma unroll
+    for (int y = 0; y < NJ; ++y)
+      fb[y] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(
+                                             lb + (rb + y * 16 + lrow) * LDS_STRIDE + kk * 32 + lk));
+#pragma unroll
+    for (int x = 0; x < NI; ++x)
+#pragma unroll
+      for (int y = 0; y < NJ; ++y)
+        acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[y], fa[x], acc[x][y], 0, 0, 0);
+  }
+}
+
+// B-side loader per mode (the A side is RowsDma for every mode here)
+template <int MODE, int BJ, int NT> struct BSide;
+template <int BJ, int NT> struct BSide<MODE_FWD, BJ, NT> {
+  RowsPacked<BJ, NT> b;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t j0, int t) {
+    b.init(reinterpret_cast<const int32_t*>(g.b) + j0 * g.ldb, g.ldb, g.J - j0, g.R, g.col_exp, t);
+  }
+};
+template <int BJ, int NT> struct BSide<MODE_FWD_BF16, BJ, NT> {
+  RowsBf16<BJ, NT> b;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t j0, int t) {
+    b.init(reinterpret_cast<const uint16_t*>(g.b) + j0 * g.ldb, g.ldb, g.J - j0, g.R, t);
+  }
+};
+template <int BJ, int NT> struct BSide<MODE_DGRAD, BJ, NT> {
+  ColsPacked<BJ, NT> b;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t j0, int t) {
+    b.init(reinterpret_cast<const int32_t*>(g.b) + j0, g.ldb, g.J - j0, g.R, g.row_exp, t);
+  }
+};
+template <int BJ, int NT> struct BSide<MODE_DGRAD_BF16, BJ, NT> {
+  ColsBf16<BJ, NT> b;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t j0, int t) {
+    b.init(reinterpret_cast<const uint16_t*>(g.b) + j0, g.ldb, g.J - j0, g.R, t);
+  }
+};
+
+// 8 waves: waves 0-3 compute and move A by DMA (stage s+2 while computing s),
+// waves 4-7 load B three stages ahead in registers, decode it and write it
+// into a double-buffered padded LDS tile.  One LDS barrier per stage; before
+// it every compute wave waits until its own DMA of the next stage has landed.
+template <int MODE, int BI, int BJ>
+__global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
+  constexpr int NP = 256;
+  constexpr int WTI = BI / 2, WTJ = BJ / 2;
+  constexpr int NI = WTI / 16, NJ = WTJ / 16;
+  typedef BSide<MODE, BJ, NP> BS;
+  typedef RowsDma<BI, 4> AD;
+  constexpr int LB = decltype(BS::b)::LROWS;
+  static_assert(LB >= BJ, "LDS tile rows");
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
+  __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][LB * LDS_STRIDE];
+  __shared__ uint32_t s_old;
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const bool producer = wave >= 4;
+  const int tiles = g.tiles_i * g.tiles_j;
+  const int wg = blockIdx.x;
+  const int split = wg / tiles;
+  int bi, bj;
+  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
+  const int64_t r_begin = (int64_t)split * g.r_split;
+  const int64_t r_end = min(g.R, r_begin + g.r_split);
+  const int nst = r_end > r_begin ? (int)((r_end - r_begin + TR - 1) / TR) : 0;
+  // both roles pass an even number of stage barriers; the producers' extra
+  // stage reads zeros (out-of-range loads) and the compute waves skip it
+  const int nst2 = (nst + 1) & ~1;
+
+  f32x4 acc[NI][NJ];
+#pragma unroll
+  for (int x = 0; x < NI; ++x)
+#pragma unroll
+    for (int y = 0; y < NJ; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int wi = (wave & 3) >> 1, wj = wave & 1;
+
+  if (producer) {
+    const int tp = t - NP;
+    BS bs;
+    bs.init(g, j0, tp);
+    typename decltype(bs.b)::Raw r0, r1;
+    auto stage_r = [&](int st) { return r_begin + (int64_t)st * TR; };
+    bs.b.load(r0, stage_r(0), r_end - stage_r(0));
+    bs.b.load(r1, stage_r(1), r_end - stage_r(1));
+    bs.b.store(r0, lds_b[0], tp);
+    bs.b.load(r0, stage_r(2), r_end - stage_r(2));
+    lds_barrier();
+    // iteration s: stage s+1 -> LDS buffer (s+1)&1, then stage s+3 into its
+    // registers.  Two sets in flight measured faster than three (deeper
+    // prefetch only adds L2 pressure).  One back-edge and no early exit, so
+    // the compiler sees the same order of outstanding loads from the prologue
+    // and from the loop.
+    for (int s = 0; s < nst2; s += 2) {
+      bs.b.store(r1, lds_b[1], tp);
+      bs.b.load(r1, stage_r(s + 3), r_end - stage_r(s + 3));
+      lds_barrier();
+      bs.b.store(r0, lds_b[0], tp);
+      bs.b.load(r0, stage_r(s + 4), r_end - stage_r(s + 4));
+      lds_barrier();
+    }
+  } else {
+    AD ad;
+    ad.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, wave, lane);
+    ad.load(lds_a[0], r_begin, r_end - r_begin);
+    ad.load(lds_a[1], r_begin + TR, r_end - r_begin - TR);
+    // own DMA of stage 0 landed (stage 1's PER loads may still fly)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(AD::PER));
+    lds_barrier();
+    for (int s = 0; s < nst2; ++s) {
+      const int64_t r2 = r_begin + (int64_t)(s + 2) * TR;
+      ad.load(lds_a[(s + 2) % 3], r2, r_end - r2);
+      if (s < nst) stage_mfma_swz<NI, NJ>(acc, lds_a[s % 3], lds_b[s & 1], wi * WTI, wj * WTJ, lane);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(AD::PER));
+      lds_barrier();
+    }
+    // no DMA may still be writing LDS when the block ends
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  }
+
+  const int64_t ib = i0 + wi * WTI + (lane & 15);
+  const int64_t jb = j0 + wj * WTJ + 4 * (lane >> 4);
+  epilogue<MODE, NI, NJ>(g, acc, ib, jb, split, wg % tiles, !producer, t, &s_old);
+}
+
+// ---- planning -----------------------------------------------------------------
+struct FastShape { int bi, bj, waves, minb; };
+
+// tile shapes per mode (index into the launch switch below); 8-wave tiles run
+// two waves per SIMD, 4-wave 128 x 128 tiles two blocks per CU
+constexpr FastShape kFwdShapes[] = {{256, 160, 8, 1}, {256, 128, 8, 1}, {128, 128, 4, 2}};
+constexpr FastShape kColShapes[] = {{256, 128, 8, 1}, {128, 128, 4, 2}};
+constexpr FastShape kWgrShapes[] = {{256, 128, 8, 1}, {128, 128, 4, 2}};
+constexpr int kCUs = 256;
+
+struct FastPlan { int shape, splits, ti, tj; int64_t r_split; };
+
+template <int NS>
+static FastPlan plan(const FastShape (&shapes)[NS], int64_t I, int64_t J, int64_t R, int max_splits) {
+  FastPlan best{0, 1, 0, 0, R};
+  double best_cost = 1e300;
+  for (int s = 0; s < NS; ++s) {
+    const int64_t ti = cdiv(I, shapes[s].bi), tj = cdiv(J, shapes[s].bj);
+    for (int sp = 1; sp <= max_splits; ++sp) {
+      if (sp > 1 && (!gemm_splitk_fits(ti * tj) || ti * tj * (sp - 1) >= kCUs * shapes[s].minb)) break;
+      const int64_t rs = cdiv(cdiv(R, sp), TR) * TR;
+      if (sp > 1 && (sp - 1) * rs >= R) break;
+      const double slots = (double)kCUs * shapes[s].minb;
+      const double waves = std::ceil((double)(ti * tj * sp) / slots);
+      // a resident block's MFMA rate falls when two share a CU
+      const double per_block = (double)shapes[s].bi * shapes[s].bj * (double)(rs + 2 * TR) * shapes[s].minb;
+      double cost = waves * per_block;
+      if (sp > 1) cost += (double)sp * I * J * 8.0 / kCUs;   // partial write + read, spread over CUs
+      if (cost < best_cost * 0.999) {
+        best_cost = cost;
+        best = FastPlan{s, sp, (int)ti, (int)tj, rs};
+      }
+    }
+  }
+  return best;
+}
+
+static bool al(const void* p, int n) { return ((uintptr_t)p % n) == 0; }
+// operand extents stay below 2^30 bytes, so kOOB plus any in-tile offset plus
+// the stage's soffset never wraps 32 bits
+static bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 30); }
+
+// alignment and extent rules of the fast kernels, per mode
+static bool eligible(int mode, const GemmArgs& g) {
+  if (!(g.ldc % 4 == 0 && g.J % 4 == 0 && al(g.c, 8))) return false;
+  if (g.vbias && !al(g.vbias, 8)) return false;
+  switch (mode) {
+    case MODE_FWD:
+      return g.lda % 8 == 0 && g.R % 8 == 0 && al(g.a, 16) && g.ldb % 4 == 0 && al(g.b, 16) &&
+             al(g.col_exp, 4) && al(g.row_exp, 4) && fits31(((g.I - 1) * g.lda + g.R) * 2) &&
+             fits31(((g.J - 1) * g.ldb + g.R) * 4);
+    case MODE_FWD_BF16:
+      return g.lda % 8 == 0 && g.R % 8 == 0 && al(g.a, 16) && g.ldb % 8 == 0 && al(g.b, 16) &&
+             fits31(((g.I - 1) * g.lda + g.R) * 2) && fits31(((g.J - 1) * g.ldb + g.R) * 2);
+    case MODE_DGRAD:
+      return g.lda % 8 == 0 && g.R % 8 == 0 && al(g.a, 16) && g.ldb % 4 == 0 && al(g.b, 16) &&
+             al(g.row_exp, 4) && al(g.col_exp, 4) && fits31(((g.I - 1) * g.lda + g.R) * 2) &&
+             fits31(((g.R - 1) * g.ldb + g.J) * 4);
+    case MODE_DGRAD_BF16:
+      return g.lda % 8 == 0 && g.R % 8 == 0 && al(g.a, 16) && g.ldb % 4 == 0 && al(g.b, 8) &&
+             fits31(((g.I - 1) * g.lda + g.R) * 2) && fits31(((g.R - 1) * g.ldb + g.J) * 2);
+    case MODE_WGRAD:
+      return g.lda % 4 == 0 && g.I % 4 == 0 && al(g.a, 8) && g.ldb % 4 == 0 && al(g.b, 8) &&
+             fits31(((g.R - 1) * g.lda + g.I) * 2) && fits31(((g.R - 1) * g.ldb + g.J) * 2);
+  }
+  return false;
+}
+
+template <int MODE, int BI, int BJ>
+static void launch_dma(const GemmArgs& g, int blocks, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_dma_kernel<MODE, BI, BJ>), dim3(blocks), dim3(512), 0, st, g);
+}
+
+template <int MODE, int BI, int BJ>
+static void launch_ws(const GemmArgs& g, int blocks, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_ws_kernel<MODE, BI, BJ>), dim3(blocks), dim3(512), 0, st, g);
+}
+
+template <int MODE, int BI, int BJ, int WI, int WJ, int MINB, bool DB = true, bool SCHED = true>
+static void launch(const GemmArgs& g, int blocks, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_fast_kernel<MODE, BI, BJ, WI, WJ, MINB, DB, SCHED>), dim3(blocks),
+                     dim3(64 * WI * WJ), 0, st, g);
+}
+
+static FastPlan plan_mode(int mode, int64_t I, int64_t J, int64_t R, int max_splits) {
+  if (mode == MODE_FWD || mode == MODE_FWD_BF16) return plan(kFwdShapes, I, J, R, max_splits);
+  if (mode == MODE_WGRAD) return plan(kWgrShapes, I, J, R, max_splits);
+  return plan(kColShapes, I, J, R, max_splits);
+}
+
+}  // namespace
+
+int gemm_fast_splits(int mode, int64_t I, int64_t J, int64_t R) {
+  if (I <= 0 || J <= 0) return 1;
+  return plan_mode(mode, I, J, R, kMaxSplits).splits;
+}
+
+int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_bytes,
+                     hipStream_t st, const char* what) {
+  if (!eligible(mode, g0)) return -1;
+  GemmArgs g = g0;
+  // split-K needs room for its partials behind the counters
+  int max_splits = 1;
+  if (workspace) {
+    const size_t room = ws_bytes > kSplitkCounterBytes ? ws_bytes - kSplitkCounterBytes : 0;
+    const size_t per = (size_t)g.I * (size_t)g.J * sizeof(float);
+    max_splits = (int)std::min<size_t>(kMaxSplits, per ? room / per : 1);
+    if (max_splits < 1) max_splits = 1;
+  }
+  const FastPlan p = plan_mode(mode, g.I, g.J, g.R, max_splits);
+  g.splits = p.splits;
+  g.r_split = p.r_split;
+  g.tiles_i = p.ti;
+  g.tiles_j = p.tj;
+  if (p.splits > 1) {
+    g.tile_cnt = (uint32_t*)workspace;
+    g.part = (float*)((char*)workspace + kSplitkCounterBytes);
+  }
+  const int blocks = p.ti * p.tj * p.splits;
+  switch (mode) {
+    case MODE_FWD:
+      if (p.shape == 0) launch_dma<MODE_FWD, 256, 160>(g, blocks, st);
+      else if (p.shape == 1) launch_dma<MODE_FWD, 256, 128>(g, blocks, st);
+      else launch<MODE_FWD, 128, 128, 2, 2, 2>(g, blocks, st);
+      break;
+    case MODE_FWD_BF16:
+      if (p.shape == 0) launch_dma<MODE_FWD_BF16, 256, 160>(g, blocks, st);
+      else if (p.shape == 1) launch_dma<MODE_FWD_BF16, 256, 128>(g, blocks, st);
+      else launch<MODE_FWD_BF16, 128, 128, 2, 2, 2>(g, blocks, st);
+      break;
+    case MODE_DGRAD:
+      if (p.shape == 0) launch_dma<MODE_DGRAD, 256, 128>(g, blocks, st);
+      else launch<MODE_DGRAD, 128, 128, 2, 2, 2>(g, blocks, st);
+      break;
+    case MODE_DGRAD_BF16:
+      if (p.shape == 0) launch_dma<MODE_DGRAD_BF16, 256, 128>(g, blocks, st);
+      else launch<MODE_DGRAD_BF16, 128, 128, 2, 2, 2>(g, blocks, st);
+      break;
+    case MODE_WGRAD:
+      if (p.shape == 0) launch_ws<MODE_WGRAD, 256, 128>(g, blocks, st);
+      else launch<MODE_WGRAD, 128, 128, 2, 2, 2>(g, blocks, st);
+      break;
+    default:
+      return -1;
+  }
+  return launch_status(what);
+}
+
+}  // namespace concord

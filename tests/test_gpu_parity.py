@@ -402,8 +402,12 @@ def test_load_weights_matches_oracle(oracle):
 
 # ---------------------------------------------------------------- GEMMs
 
+# (M, N, K).  Misaligned shapes run the generic kernel; shapes whose
+# contiguous dimensions are multiples of 8 run the branch-free kernels, with
+# ragged tile edges, a reduction tail, and (64, 136, 4096) a 4-way split-K.
 GEMM_SHAPES = [(64, 128, 64), (77, 130, 200), (256, 384, 1280), (1, 5, 3), (130, 1000, 70),
-               (2048, 1280, 1280), (2048, 5120, 1280), (300, 2050, 645)]
+               (2048, 1280, 1280), (2048, 5120, 1280), (300, 2050, 645),
+               (77, 136, 200), (300, 2056, 648), (1, 8, 8), (129, 1000, 72), (64, 136, 4096)]
 
 
 def _decoded(oracle, packed, re, ce):
@@ -450,6 +454,23 @@ def test_wgrad(oracle, M, N, K):
     assert rel_l2(oracle.bf16_bits_to_f32(host(gw)), ref) < 5e-3
 
 
+@pytest.mark.parametrize("M,N,K", [(96, 264, 320), (96, 130, 320)])
+def test_dqgemm_extreme_exponents(oracle, M, N, K):
+    """Row/column exponents at both ends of [EXP_MIN, EXP_MAX] (the fast
+    kernels apply one side in the epilogue, the other while decoding)."""
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(M + N + 7 * K)
+    packed, re, ce = rand_state(rng, N, K, exp=(-8, 7), col=(-8, 7))
+    x = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32))
+    dy = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, N)).astype(np.float32))
+    y = pb._gemm_fwd(dev(x), dev(packed), dev(re), dev(ce), 15, None, None)
+    dx = pb._gemm_dgrad(dev(dy), dev(packed), dev(re), dev(ce), 15, None)
+    sync()
+    W = _decoded(oracle, packed, re, ce)
+    assert rel_l2(oracle.bf16_bits_to_f32(host(y)), oracle.bf16_bits_to_f32(x).astype(np.float64) @ W.T) < 5e-3
+    assert rel_l2(oracle.bf16_bits_to_f32(host(dx)), oracle.bf16_bits_to_f32(dy).astype(np.float64) @ W) < 5e-3
+
+
 def test_gemm_splitk_workspace_reuse(oracle):
     """Back-to-back split-K GEMMs of different tile grids share one workspace:
     each call must find its counters zeroed whatever the previous call's
@@ -465,7 +486,7 @@ def test_gemm_splitk_workspace_reuse(oracle):
         assert rel_l2(oracle.bf16_bits_to_f32(host(gw)), ref) < 5e-3, (M, N, K)
 
 
-@pytest.mark.parametrize("M,N,K", GEMM_SHAPES[:4])
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES[:4] + GEMM_SHAPES[8:])
 def test_bf16_weight_gemms(oracle, M, N, K):
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(M * 7 + N + K)

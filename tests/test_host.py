@@ -76,7 +76,10 @@ def test_invalid_arguments_rejected_without_launch(L):
     # empty problems are valid no-ops
     assert L.concord_materialize(P, 0, P, P, 0, 0, 15, 0, P, 0, P) == C.OK
     assert L.concord_wgrad(P, 0, P, 0, P, 0, 5, 0, 7, P, 0, P) == C.OK
-    assert L.concord_gemm_workspace_bytes(2048, 5120, 1280) >= 2 * 2048 * 5120 * 4
+    # tile counters always; split-K partials only for products with few tiles
+    ws = L.concord_gemm_workspace_bytes(2048, 5120, 1280)
+    assert ws >= 16384 and ws % 256 == 0
+    assert L.concord_gemm_workspace_bytes(128, 128, 1 << 16) >= 16384 + 2 * 128 * 128 * 4
 
 
 def test_apply_rejects_missing_vhat_inputs(L):
