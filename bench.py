@@ -8,10 +8,19 @@ fused dequant-GEMM mode.  One step = forward (dequant-GEMM) + backward
 synthetic x ~ N(0,1) and dy ~ N(0, 1e-3), random-init weights.
 
 Prints one JSON line.  value = dequant-matmul throughput of the whole step,
-6 M N K / step time (TFLOP/s).  roofline = the forward dequant-GEMM kernel
-against dense bf16 MFMA peak; roofline_update = the packed update kernel
-against HBM peak at 10 algorithmic B/param.  cpu_baseline = the same step on
-the host: torch fp32 GEMMs + the CPU oracle's v-hat / update / rebalance.
+6 M N K / step time (TFLOP/s).  roofline = the step's dominant kernel (the
+longest per-kernel time) against its roofline: a GEMM against dense bf16
+MFMA peak at 2 M N K algorithmic FLOP, the packed update against HBM peak at
+10 algorithmic B/param; rooflines = the same for every kernel of the step;
+traffic = HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+WRITE_SIZE summary (profiles/traffic_sdxl_1280x5120.txt) when present.
+cpu_baseline = the same step on the host: torch fp32 GEMMs + the CPU oracle's
+v-hat / update / rebalance.
+
+`--only KERNEL` runs one kernel of the step `--reps` times and exits (the
+command the committed rocprofv3 summaries were taken with); KERNEL = fwd,
+dgrad, wgrad, vhat, update, materialize, or copy (a 256 MiB device copy, the
+counter calibration).
 """
 import argparse
 import json
@@ -55,6 +64,23 @@ def _event_time_ms(fn, reps, torch):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / (n * reps)
+
+
+def _read_traffic():
+    """HBM bytes per launch per kernel from the committed PMC summary:
+    lines `kernel_key  fetch_bytes  write_bytes`."""
+    path = os.path.join(ROOT, "profiles", "traffic_sdxl_1280x5120.txt")
+    out = {}
+    if not os.path.exists(path):
+        return out
+    for line in open(path):
+        f = line.split()
+        if len(f) == 3 and not line.startswith("#"):
+            try:
+                out[f[0]] = int(f[1]) + int(f[2])
+            except ValueError:
+                pass
+    return out
 
 
 def cpu_baseline(threads):
@@ -109,6 +135,40 @@ def cpu_baseline(threads):
                       f"(fwd, dgrad, wgrad) + oracle v-hat, update, rebalance"}
 
 
+def _only(which, reps, layer, xb, dy, torch, pb):
+    """Run one kernel of the step `reps` times (profiling entry)."""
+    st = (layer.packed_w, layer.row_exp, layer.col_exp)
+    dev = xb.device
+    if which == "copy":
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+        b = torch.empty_like(a)
+        fn = lambda: b.copy_(a)  # noqa: E731
+    elif which == "fwd":
+        fn = lambda: pb._gemm_fwd(xb, *st, 15, layer.bias, None)  # noqa: E731
+    elif which == "dgrad":
+        fn = lambda: pb._gemm_dgrad(dy, *st, 15, None)  # noqa: E731
+    elif which == "wgrad":
+        fn = lambda: pb._wgrad(dy, xb)  # noqa: E731
+    else:
+        gw = pb._wgrad(dy, xb)
+        if which == "vhat":
+            fn = lambda: pb.vhat_ema(gw, layer.v_row, layer.v_col, layer._sum_v_inv)  # noqa: E731
+        elif which == "update":
+            pk = layer.packed_w.clone()
+            fn = lambda: pb.apply_packed_adamw(  # noqa: E731
+                pk, gw, None, layer.row_exp, layer.col_exp, layer._row_max_buf, layer._col_max_buf,
+                lr=layer._lr_buf, eps=layer._eps_buf, gf_consol=50.0, v_scale=0.0, mass_preserve=True,
+                v_row=layer.v_row, v_col=layer.v_col, sum_v_inv=layer._sum_v_inv, gf_trust_delta_sq=1.0,
+                coh_pre=None, salt_prebumped=True)
+        else:
+            wbuf = torch.empty((N_OUT, K_IN), dtype=torch.bfloat16, device=dev)
+            fn = lambda: pb.materialize_packed_bf16(*st, wbuf)  # noqa: E731
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    print(json.dumps({"only": which, "reps": reps}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -116,6 +176,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--only", default=None,
+                    choices=["fwd", "dgrad", "wgrad", "vhat", "update", "materialize", "copy"])
+    ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -145,6 +208,10 @@ def main():
     for _ in range(3):
         step()
     torch.cuda.synchronize()
+
+    if args.only:
+        _only(args.only, args.reps, layer, x.detach(), dy, torch, pb)
+        return
 
     mode = "eager"
     run = step
@@ -217,6 +284,32 @@ def main():
     fwd_tflops = gemm_flop / (t_fwd * 1e-3) / 1e12
     params = N_OUT * K_IN
     upd_gbps = UPDATE_BYTES_PER_PARAM * params / (t_upd * 1e-3) / 1e9
+    traffic = _read_traffic()
+
+    def gemm_roof(key, name, t_ms):
+        a = gemm_flop / (t_ms * 1e-3) / 1e12
+        return {"bound": "mfma", "kernel": name, "achieved": round(a, 2), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(a / PEAK_BF16_TFLOPS, 4), "traffic": traffic.get(key),
+                "us": round(t_ms * 1e3, 2)}
+
+    def hbm_roof(key, name, t_ms, nbytes):
+        a = nbytes / (t_ms * 1e-3) / 1e9
+        return {"bound": "hbm", "kernel": name, "achieved": round(a, 1), "peak": PEAK_HBM_GBPS,
+                "unit": "GB/s", "frac": round(a / PEAK_HBM_GBPS, 4), "traffic": traffic.get(key),
+                "us": round(t_ms * 1e3, 2)}
+
+    roofs = {
+        "dqgemm_fwd": gemm_roof("dqgemm_fwd", "gemm_dma_kernel<FWD, 256, 160> (fused dequant-GEMM forward)",
+                                t_fwd),
+        "dqgemm_dgrad": gemm_roof("dqgemm_dgrad", "gemm_dma_kernel<DGRAD, 256, 128> + split-K reduce "
+                                  "(fused dequant-GEMM dgrad)", t_dgrad),
+        "wgrad": gemm_roof("wgrad", "wgrad GEMM dy^T x", t_wgrad),
+        "apply_adamw": hbm_roof("apply_adamw", "apply_adamw_fast_kernel<ratio> (packed update, winner flags)",
+                                t_upd, UPDATE_BYTES_PER_PARAM * params),
+        "vhat_ema": hbm_roof("vhat_ema", "vhat_partials + vhat_finalize (reads bf16 grad)", t_vhat,
+                             2 * params),
+    }
+    dominant = max(roofs, key=lambda k: roofs[k]["us"])
 
     out = {
         "metric": "dequant-matmul TFLOP/s (%MFMA peak) + packed-update GB/s (%HBM), SDXL linears",
@@ -234,13 +327,8 @@ def main():
         "config": {"workload": "sdxl_linear_1280to5120_M2048_fwd_dgrad_wgrad_update_rebalance",
                    "N": N_OUT, "K": K_IN, "M": M_TOK, "optimizer": "winner (ratio_coh, gf_consol=50)",
                    "forward": "fused dequant-GEMM", "timing": mode},
-        "roofline": {"bound": "mfma", "kernel": "gemm_kernel<FWD> (dequant-GEMM forward)",
-                     "achieved": round(fwd_tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(fwd_tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
-        "roofline_update": {"bound": "hbm", "kernel": "apply_adamw_kernel<4>",
-                            "achieved": round(upd_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                            "frac": round(upd_gbps / PEAK_HBM_GBPS, 4), "traffic": None,
-                            "bytes_per_param": UPDATE_BYTES_PER_PARAM},
+        "roofline": dict(roofs[dominant], step_kernel=dominant),
+        "rooflines": roofs,
         "kernel_us": {"dqgemm_fwd": round(t_fwd * 1e3, 2), "dqgemm_dgrad": round(t_dgrad * 1e3, 2),
                       "wgrad": round(t_wgrad * 1e3, 2), "vhat_ema": round(t_vhat * 1e3, 2),
                       "apply_adamw": round(t_upd * 1e3, 2), "materialize": round(t_mat * 1e3, 2),

@@ -54,7 +54,8 @@ CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
 // returns CONCORD_OK, an error code, or -1 when the generic kernel must run
 int gemm_fast_launch(int mode, const GemmArgs& g, void* workspace, size_t ws_bytes,
                      hipStream_t st, const char* what);
-// number of split-K ways the fast kernels plan for an I x J x R problem
-int gemm_fast_splits(int mode, int64_t I, int64_t J, int64_t R);
+// split-K partial bytes the fast kernels plan for an I x J x R problem
+// given unlimited workspace (0 when they do not split it)
+size_t gemm_fast_partial_bytes(int mode, int64_t I, int64_t J, int64_t R);
 
 }  // namespace concord

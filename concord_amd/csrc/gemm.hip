@@ -485,10 +485,9 @@ using namespace concord;
 
 // split-K partial bytes one GEMM may use (fast or generic kernel), 0 if unsplit
 static size_t splitk_partials(int mode, int64_t I, int64_t J, int64_t R) {
-  const int sf = gemm_fast_splits(mode, I, J, R);
-  const int sg = plan_gemm(I, J, R, true).splits;
-  const int s = sf > sg ? sf : sg;
-  return s > 1 ? (size_t)s * (size_t)I * (size_t)J * sizeof(float) : 0;
+  const size_t fast = gemm_fast_partial_bytes(mode, I, J, R);
+  const size_t generic = plan_gemm(I, J, R, true).splits > 1 ? (size_t)2 * I * J * sizeof(float) : 0;
+  return fast > generic ? fast : generic;
 }
 
 extern "C" size_t concord_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {

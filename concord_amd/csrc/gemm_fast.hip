@@ -390,82 +390,140 @@ CONCORD_DEV void sched_stage() {
 }
 
 // ---- epilogue shared by the kernels ------------------------------------------
-// Split-K fixup (every thread of the block takes part in its barriers; only
-// threads with `active` accumulators write) and the store: the column scale
-// 2^(exp - bias) of the side not decoded in the loop, the bias, bf16 rounding
-// and 8-byte stores (J % 4 == 0 and ldc % 4 == 0).
-// lane holds C[ib + 16x][jb + 16y + e], e = 0..3
-template <int MODE, int NI, int NJ>
-CONCORD_DEV void epilogue(const GemmArgs& g, f32x4 (&acc)[NI][NJ], int64_t ib, int64_t jb, int split,
-                          int tile, bool active, int t, uint32_t* s_old) {
+// NAW waves hold accumulators (aw = this wave's index among them, -1 for a
+// wave without); lane holds C[i0 + ra + 16x + lane%16][j0 + rb + 16y + 4(lane/16) + e].
+// Split-K: each split stores its accumulators in register order (one
+// contiguous 1 KB per wave instruction) into its slot of the partial buffer
+// and is done; splitk_reduce_kernel sums the slots in split order afterwards
+// (a device-scope fence here would write back a whole XCD's L2).
+// Otherwise the column scale 2^(exp - bias) of the side not decoded in the
+// loop and the bias are applied, the tile is rounded to bf16 into LDS
+// (`stage`, at least BI x (BJ + 8) bf16, free once the main loop is done)
+// and written out row-contiguous.
+template <int NAW, int NI, int NJ>
+CONCORD_DEV float* partial_slot(const GemmArgs& g, int tile, int split, int aw) {
+  return g.part + ((int64_t)tile * g.splits + split) * ((int64_t)NAW * NI * NJ * 256) + (int64_t)aw * NI * NJ * 256;
+}
+
+template <int MODE, int NI, int NJ, int BI, int BJ, int NAW>
+CONCORD_DEV void epilogue(const GemmArgs& g, f32x4 (&acc)[NI][NJ], int64_t i0, int64_t j0, int ra, int rb,
+                          int split, int tile, int aw, int t, int nthreads, uint16_t* stage) {
+  constexpr int LDO = BJ + 8;   // bf16 per staged row (16-byte multiple, shifts banks by 4)
+  static_assert((int64_t)NAW * NI * NJ * 256 == (int64_t)BI * BJ, "accumulator waves must cover the tile");
+  const int lane = t & 63;
   if (g.splits > 1) {
-    const int64_t IJ = g.I * g.J;
-    if (active) {
-      float* mine = g.part + (int64_t)split * IJ;
+    if (aw >= 0) {
+      float* mine = partial_slot<NAW, NI, NJ>(g, tile, split, aw) + lane * 4;
 #pragma unroll
       for (int x = 0; x < NI; ++x)
 #pragma unroll
-        for (int y = 0; y < NJ; ++y) {
-          const int64_t i = ib + x * 16, j = jb + y * 16;
-          if (i < g.I && j < g.J) *reinterpret_cast<f32x4*>(mine + i * g.J + j) = acc[x][y];
-        }
+        for (int y = 0; y < NJ; ++y) *reinterpret_cast<f32x4*>(mine + (x * NJ + y) * 256) = acc[x][y];
     }
-    __threadfence();
-    __syncthreads();
-    if (t == 0) *s_old = atomicAdd(g.tile_cnt + tile, 1u);
-    __syncthreads();
-    if (*s_old != (uint32_t)(g.splits - 1)) return;
-    __threadfence();
-    if (t == 0) g.tile_cnt[tile] = 0u;
-    if (!active) return;
-    // sum the partials in split order: ((p0 + p1) + p2) + ...
+    return;
+  }
+  // column scale and bias in registers, bf16 tile into LDS
+  __syncthreads();
+  if (aw >= 0) {
+    const int8_t* cexp = MODE == MODE_FWD ? g.row_exp : MODE == MODE_DGRAD ? g.col_exp : nullptr;
 #pragma unroll
-    for (int x = 0; x < NI; ++x)
+    for (int y = 0; y < NJ; ++y) {
+      const int cl = rb + y * 16 + 4 * (lane >> 4);   // tile-local column
+      const int64_t j = j0 + cl;
+      float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
+      if (j < g.J) {
+        if (cexp) {
+          const int32_t e4 = *reinterpret_cast<const int32_t*>(cexp + j);
 #pragma unroll
-      for (int y = 0; y < NJ; ++y) {
-        const int64_t i = ib + x * 16, j = jb + y * 16;
-        if (i < g.I && j < g.J) {
-          f32x4 sum = split == 0 ? acc[x][y] : *reinterpret_cast<const f32x4*>(g.part + i * g.J + j);
-          for (int s2 = 1; s2 < g.splits; ++s2) {
-            const f32x4 p = s2 == split ? acc[x][y]
-                                        : *reinterpret_cast<const f32x4*>(g.part + s2 * IJ + i * g.J + j);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sum[e] = __fadd_rn(sum[e], p[e]);
-          }
-          acc[x][y] = sum;
+          for (int e = 0; e < 4; ++e) sc[e] = exp2i(sbyte(e4, e) - g.bias);
+        }
+        if (g.vbias) {
+          const uint2 b4 = *reinterpret_cast<const uint2*>(g.vbias + j);
+          bs[0] = __uint_as_float(b4.x << 16);
+          bs[1] = __uint_as_float(b4.x & 0xFFFF0000u);
+          bs[2] = __uint_as_float(b4.y << 16);
+          bs[3] = __uint_as_float(b4.y & 0xFFFF0000u);
         }
       }
+#pragma unroll
+      for (int x = 0; x < NI; ++x) {
+        const int rl = ra + x * 16 + (lane & 15);
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(__fmul_rn(acc[x][y][e], sc[e]), bs[e]);
+        *reinterpret_cast<uint2*>(stage + rl * LDO + cl) =
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      }
+    }
   }
-  if (!active) return;
+  __syncthreads();
+  // row-contiguous stores: 8 bf16 (16 bytes) per thread when the output
+  // allows, else 4 (J % 4 == 0, ldc % 4 == 0, 8-byte aligned base)
+  const bool v16 = (g.ldc % 8 == 0) && (g.J % 8 == 0) && (((uintptr_t)g.c % 16) == 0);
+  if (v16) {
+    constexpr int CPR = BJ / 8;
+    for (int c = t; c < BI * CPR; c += nthreads) {
+      const int rl = c / CPR, cl = (c % CPR) * 8;
+      const int64_t i = i0 + rl, j = j0 + cl;
+      if (i < g.I && j < g.J)
+        *reinterpret_cast<uint4*>(g.c + i * g.ldc + j) = *reinterpret_cast<const uint4*>(stage + rl * LDO + cl);
+    }
+  } else {
+    constexpr int CPR = BJ / 4;
+    for (int c = t; c < BI * CPR; c += nthreads) {
+      const int rl = c / CPR, cl = (c % CPR) * 4;
+      const int64_t i = i0 + rl, j = j0 + cl;
+      if (i < g.I && j < g.J)
+        *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = *reinterpret_cast<const uint2*>(stage + rl * LDO + cl);
+    }
+  }
+}
+
+// Split-K reduction: one thread per (tile, accumulator wave, 16x16 block,
+// lane) sums the splits' partials in split order, applies the column scale
+// and bias, and stores 4 bf16.
+template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
+  constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int tiles = g.tiles_i * g.tiles_j;
+  if (idx >= (int64_t)tiles * NAW * NI * NJ * 64) return;
+  const int lane = (int)(idx % 64);
+  int64_t r = idx / 64;
+  const int y = (int)(r % NJ); r /= NJ;
+  const int x = (int)(r % NI); r /= NI;
+  const int aw = (int)(r % NAW);
+  const int tile = (int)(r / NAW);
+  int bi, bj;
+  tile_of(tile, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  const int64_t i = (int64_t)bi * BI + (aw / WJ) * WTI + x * 16 + (lane & 15);
+  const int64_t j = (int64_t)bj * BJ + (aw % WJ) * WTJ + y * 16 + 4 * (lane >> 4);
+  if (i >= g.I || j >= g.J) return;
+  const int64_t PT = (int64_t)NAW * NI * NJ * 256;
+  const float* p = g.part + (int64_t)tile * g.splits * PT + (int64_t)aw * NI * NJ * 256 + (x * NJ + y) * 256 + lane * 4;
+  f32x4 sum = *reinterpret_cast<const f32x4*>(p);
+  for (int s2 = 1; s2 < g.splits; ++s2) {
+    const f32x4 q = *reinterpret_cast<const f32x4*>(p + s2 * PT);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum[e] = __fadd_rn(sum[e], q[e]);
+  }
   const int8_t* cexp = MODE == MODE_FWD ? g.row_exp : MODE == MODE_DGRAD ? g.col_exp : nullptr;
+  float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
+  if (cexp) {
+    const int32_t e4 = *reinterpret_cast<const int32_t*>(cexp + j);
 #pragma unroll
-  for (int y = 0; y < NJ; ++y) {
-    const int64_t j = jb + y * 16;
-    if (j >= g.J) continue;
-    float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
-    if (cexp) {
-      const int32_t e4 = *reinterpret_cast<const int32_t*>(cexp + j);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sc[e] = exp2i(sbyte(e4, e) - g.bias);
-    }
-    if (g.vbias) {
-      const uint2 b4 = *reinterpret_cast<const uint2*>(g.vbias + j);
-      bs[0] = __uint_as_float(b4.x << 16);
-      bs[1] = __uint_as_float(b4.x & 0xFFFF0000u);
-      bs[2] = __uint_as_float(b4.y << 16);
-      bs[3] = __uint_as_float(b4.y & 0xFFFF0000u);
-    }
-#pragma unroll
-    for (int x = 0; x < NI; ++x) {
-      const int64_t i = ib + x * 16;
-      if (i >= g.I) continue;
-      float v[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(__fmul_rn(acc[x][y][e], sc[e]), bs[e]);
-      *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) =
-          make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-    }
+    for (int e = 0; e < 4; ++e) sc[e] = exp2i(sbyte(e4, e) - g.bias);
   }
+  if (g.vbias) {
+    const uint2 b4 = *reinterpret_cast<const uint2*>(g.vbias + j);
+    bs[0] = __uint_as_float(b4.x << 16);
+    bs[1] = __uint_as_float(b4.x & 0xFFFF0000u);
+    bs[2] = __uint_as_float(b4.y << 16);
+    bs[3] = __uint_as_float(b4.y & 0xFFFF0000u);
+  }
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(__fmul_rn(sum[e], sc[e]), bs[e]);
+  *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
 }
 
 // MFMAs of one TR-deep stage for a wave tile of NI x NJ 16x16 blocks whose
@@ -508,7 +566,6 @@ __global__ __launch_bounds__(64 * WI * WJ, MINB) void gemm_fast_kernel(GemmArgs 
   static_assert(LA >= BI && LB >= BJ, "LDS tile rows");
   __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][LA * LDS_STRIDE];
   __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][LB * LDS_STRIDE];
-  __shared__ uint32_t s_old;
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -615,9 +672,9 @@ __global__ __launch_bounds__(64 * WI * WJ, MINB) void gemm_fast_kernel(GemmArgs 
   }
   }
 
-  const int64_t ib = i0 + wi * WTI + (lane & 15);
-  const int64_t jb = j0 + wj * WTJ + 4 * (lane >> 4);
-  epilogue<MODE, NI, NJ>(g, acc, ib, jb, split, wg % tiles, true, t, &s_old);
+  static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
+  epilogue<MODE, NI, NJ, BI, BJ, WI * WJ>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, wave, t, NT,
+                                           &lds_a[0][0]);
 }
 
 // ---- the role-split kernel ----------------------------------------------------
@@ -637,7 +694,6 @@ __global__ __launch_bounds__(512, 1) void gemm_ws_kernel(GemmArgs g) {
   static_assert(LA >= BI && LB >= BJ, "LDS tile rows");
   __shared__ __attribute__((aligned(16))) uint16_t lds_a[2][LA * LDS_STRIDE];
   __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][LB * LDS_STRIDE];
-  __shared__ uint32_t s_old;
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -700,9 +756,9 @@ __global__ __launch_bounds__(512, 1) void gemm_ws_kernel(GemmArgs g) {
     }
   }
 
-  const int64_t ib = i0 + wi * WTI + (lane & 15);
-  const int64_t jb = j0 + wj * WTJ + 4 * (lane >> 4);
-  epilogue<MODE, NI, NJ>(g, acc, ib, jb, split, wg % tiles, !producer, t, &s_old);
+  static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
+  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, producer ? -1 : wave,
+                                     t, 512, &lds_a[0][0]);
 }
 
 // ---- LDS-DMA kernel ------------------------------------------------------------
@@ -831,7 +887,6 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
   static_assert(LB >= BJ, "LDS tile rows");
   __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
   __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][LB * LDS_STRIDE];
-  __shared__ uint32_t s_old;
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -899,9 +954,9 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   }
 
-  const int64_t ib = i0 + wi * WTI + (lane & 15);
-  const int64_t jb = j0 + wj * WTJ + 4 * (lane >> 4);
-  epilogue<MODE, NI, NJ>(g, acc, ib, jb, split, wg % tiles, !producer, t, &s_old);
+  static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
+  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, producer ? -1 : wave,
+                                     t, 512, &lds_a[0][0]);
 }
 
 // ---- planning -----------------------------------------------------------------
@@ -916,12 +971,16 @@ constexpr int kCUs = 256;
 
 struct FastPlan { int shape, splits, ti, tj; int64_t r_split; };
 
+// room = bytes available for split-K partials (each split of each tile
+// takes a full BI x BJ fp32 slot)
 template <int NS>
-static FastPlan plan(const FastShape (&shapes)[NS], int64_t I, int64_t J, int64_t R, int max_splits) {
+static FastPlan plan(const FastShape (&shapes)[NS], int64_t I, int64_t J, int64_t R, size_t room) {
   FastPlan best{0, 1, 0, 0, R};
   double best_cost = 1e300;
   for (int s = 0; s < NS; ++s) {
     const int64_t ti = cdiv(I, shapes[s].bi), tj = cdiv(J, shapes[s].bj);
+    const size_t slot = (size_t)ti * tj * shapes[s].bi * shapes[s].bj * sizeof(float);
+    const int max_splits = (int)std::min<size_t>(kMaxSplits, std::max<size_t>(1, room / slot));
     for (int sp = 1; sp <= max_splits; ++sp) {
       if (sp > 1 && (!gemm_splitk_fits(ti * tj) || ti * tj * (sp - 1) >= kCUs * shapes[s].minb)) break;
       const int64_t rs = cdiv(cdiv(R, sp), TR) * TR;
@@ -972,33 +1031,55 @@ static bool eligible(int mode, const GemmArgs& g) {
   return false;
 }
 
+// split-K: sum the partials once every split has stored them
+template <int MODE, int BI, int BJ, int WI, int WJ>
+static void launch_reduce(const GemmArgs& g, hipStream_t st) {
+  if (g.splits <= 1) return;
+  constexpr int NI = BI / WI / 16, NJ = BJ / WJ / 16;
+  const int64_t threads = (int64_t)g.tiles_i * g.tiles_j * WI * WJ * NI * NJ * 64;
+  hipLaunchKernelGGL((splitk_reduce_kernel<MODE, NI, NJ, BI, BJ, WI, WJ>), dim3((unsigned)cdiv(threads, 256)),
+                     dim3(256), 0, st, g);
+}
+
 template <int MODE, int BI, int BJ>
 static void launch_dma(const GemmArgs& g, int blocks, hipStream_t st) {
   hipLaunchKernelGGL((gemm_dma_kernel<MODE, BI, BJ>), dim3(blocks), dim3(512), 0, st, g);
+  launch_reduce<MODE, BI, BJ, 2, 2>(g, st);
 }
 
 template <int MODE, int BI, int BJ>
 static void launch_ws(const GemmArgs& g, int blocks, hipStream_t st) {
   hipLaunchKernelGGL((gemm_ws_kernel<MODE, BI, BJ>), dim3(blocks), dim3(512), 0, st, g);
+  launch_reduce<MODE, BI, BJ, 2, 2>(g, st);
 }
 
 template <int MODE, int BI, int BJ, int WI, int WJ, int MINB, bool DB = true, bool SCHED = true>
 static void launch(const GemmArgs& g, int blocks, hipStream_t st) {
   hipLaunchKernelGGL((gemm_fast_kernel<MODE, BI, BJ, WI, WJ, MINB, DB, SCHED>), dim3(blocks),
                      dim3(64 * WI * WJ), 0, st, g);
+  launch_reduce<MODE, BI, BJ, WI, WJ>(g, st);
 }
 
-static FastPlan plan_mode(int mode, int64_t I, int64_t J, int64_t R, int max_splits) {
-  if (mode == MODE_FWD || mode == MODE_FWD_BF16) return plan(kFwdShapes, I, J, R, max_splits);
-  if (mode == MODE_WGRAD) return plan(kWgrShapes, I, J, R, max_splits);
-  return plan(kColShapes, I, J, R, max_splits);
+static FastPlan plan_mode(int mode, int64_t I, int64_t J, int64_t R, size_t room) {
+  if (mode == MODE_FWD || mode == MODE_FWD_BF16) return plan(kFwdShapes, I, J, R, room);
+  if (mode == MODE_WGRAD) return plan(kWgrShapes, I, J, R, room);
+  return plan(kColShapes, I, J, R, room);
+}
+
+static const FastShape& shape_of(int mode, int idx) {
+  if (mode == MODE_FWD || mode == MODE_FWD_BF16) return kFwdShapes[idx];
+  if (mode == MODE_WGRAD) return kWgrShapes[idx];
+  return kColShapes[idx];
 }
 
 }  // namespace
 
-int gemm_fast_splits(int mode, int64_t I, int64_t J, int64_t R) {
-  if (I <= 0 || J <= 0) return 1;
-  return plan_mode(mode, I, J, R, kMaxSplits).splits;
+size_t gemm_fast_partial_bytes(int mode, int64_t I, int64_t J, int64_t R) {
+  if (I <= 0 || J <= 0) return 0;
+  const FastPlan p = plan_mode(mode, I, J, R, (size_t)-1 / 2);
+  if (p.splits <= 1) return 0;
+  const FastShape& sh = shape_of(mode, p.shape);
+  return (size_t)p.ti * p.tj * sh.bi * sh.bj * sizeof(float) * p.splits;
 }
 
 int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_bytes,
@@ -1006,22 +1087,13 @@ int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
   if (!eligible(mode, g0)) return -1;
   GemmArgs g = g0;
   // split-K needs room for its partials behind the counters
-  int max_splits = 1;
-  if (workspace) {
-    const size_t room = ws_bytes > kSplitkCounterBytes ? ws_bytes - kSplitkCounterBytes : 0;
-    const size_t per = (size_t)g.I * (size_t)g.J * sizeof(float);
-    max_splits = (int)std::min<size_t>(kMaxSplits, per ? room / per : 1);
-    if (max_splits < 1) max_splits = 1;
-  }
-  const FastPlan p = plan_mode(mode, g.I, g.J, g.R, max_splits);
+  const size_t room = (workspace && ws_bytes > kSplitkCounterBytes) ? ws_bytes - kSplitkCounterBytes : 0;
+  const FastPlan p = plan_mode(mode, g.I, g.J, g.R, room);
   g.splits = p.splits;
   g.r_split = p.r_split;
   g.tiles_i = p.ti;
   g.tiles_j = p.tj;
-  if (p.splits > 1) {
-    g.tile_cnt = (uint32_t*)workspace;
-    g.part = (float*)((char*)workspace + kSplitkCounterBytes);
-  }
+  if (p.splits > 1) g.part = (float*)((char*)workspace + kSplitkCounterBytes);
   const int blocks = p.ti * p.tj * p.splits;
   switch (mode) {
     case MODE_FWD:
