@@ -7,6 +7,10 @@ linked into concord_amd/_lib/libconcord_amd.so.  Flags:
   -ffp-contract=off   the numerical contract forbids FMA contraction;
   -Xclang -target-feature -Xclang -packed-fp32-ops
                       no v_pk_*_f32 instructions in device code.
+Per-file extras (FILE_FLAGS): gemm_fast.hip keeps MFMA accumulators in
+ordinary VGPRs (-amdgpu-mfma-vgpr-form); its kernels are written to fit them,
+and the accumulator-register form made the compiler copy accumulators
+around the main loops.
 """
 import glob
 import os
@@ -29,6 +33,8 @@ CFLAGS = [
     "-I" + os.path.join(ROOT, "include"), "-I" + CSRC,
 ]
 
+FILE_FLAGS = {"gemm_fast.hip": ["-mllvm", "--amdgpu-mfma-vgpr-form"]}
+
 
 def _run(cmd):
     r = subprocess.run(cmd, capture_output=True, text=True)
@@ -47,7 +53,7 @@ def build(verbose=False, jobs=8):
 
     def compile_one(so):
         s, o = so
-        return _run([HIPCC] + CFLAGS + ["-c", s, "-o", o])
+        return _run([HIPCC] + CFLAGS + FILE_FLAGS.get(os.path.basename(s), []) + ["-c", s, "-o", o])
 
     with ThreadPoolExecutor(max_workers=jobs) as ex:
         for msg in ex.map(compile_one, zip(srcs, objs)):

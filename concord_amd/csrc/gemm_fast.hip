@@ -959,6 +959,173 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
                                      t, 512, &lds_a[0][0]);
 }
 
+// ---- WGRAD: both operands by DMA, fragments by transpose reads -------------
+// Both WGRAD operands are r-major (dy[m][n], x[m][k]), and an MFMA fragment
+// needs 8 consecutive r of one column per lane.  A stage of each operand goes
+// from global memory straight into LDS by DMA as a row-major [r][col] tile,
+// and ds_read_b64_tr_b16 turns it around: in each 16-lane group, lane p
+// addresses row r0 + (p >> 2), columns c0 + 4 (p & 3) .. +3, and receives
+// column c0 + p of rows r0 .. r0 + 3.  Two such reads make one fragment.
+// LDS layout of a stage tile (ROWB bytes per row): the 32-byte window w of
+// row r is stored at window w ^ trf(r), trf(r) = (r & 3) | ((r >> 1) & 4), so
+// the 8 rows one half-wave touches (r0 .. r0+3 and r0+8 .. r0+11, r0 a
+// multiple of 4) fall in 8 distinct 32-byte bank groups.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+CONCORD_DEV int trf(int r) { return (r & 3) | ((r >> 1) & 4); }
+
+// DMA of one operand's stage: TR rows x COLS bf16 (COLS >= 128 so that the
+// window swizzle stays inside a row)
+template <int COLS, int NW>
+struct TrDma {
+  static constexpr int ROWB = COLS * 2;        // bytes per LDS row
+  static constexpr int RPI = 1024 / ROWB;      // rows per wave instruction (1 KB)
+  static constexpr int INSTR = TR / RPI;
+  static constexpr int PER = INSTR / NW;       // per wave
+  static_assert(COLS >= 128 && COLS <= 512 && PER * NW == INSTR, "TrDma tile");
+  uint32_t voff[PER];   // kOOB for chunks past the operand's last column
+  int32_t lrow;         // this lane's row within an instruction
+  i32x4 rs;
+  int64_t ld2;
+  int w;
+  // band = operand + first column of the tile; cols_left = columns from there
+  CONCORD_DEV void init(const uint16_t* band, int64_t ld, int64_t cols_left, int64_t R, int wave, int lane) {
+    w = wave;
+    ld2 = ld * 2;
+    lrow = lane / (ROWB / 16);
+    const uint64_t base = (uint64_t)(uintptr_t)band;
+    const int64_t bytes = ((R - 1) * ld + (cols_left < COLS ? cols_left : COLS)) * 2;
+    rs = i32x4{(int32_t)(uint32_t)base, (int32_t)(uint32_t)((base >> 32) & 0xFFFF), (int32_t)(uint32_t)bytes,
+               0x00020000};
+    for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(rs[e]);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int r = (w * PER + q) * RPI + lrow;
+      const int c = (lane % (ROWB / 16)) ^ (trf(r) << 1);   // 16-byte chunk this lane's slot holds
+      voff[q] = c * 8 < cols_left ? (uint32_t)((r * ld + c * 8) * 2) : kOOB;
+    }
+  }
+  // tile = LDS byte address of this operand's stage tile; rows r0 + [0, TR)
+  CONCORD_DEV void load(uint32_t tile, int64_t r0, int64_t rem) const {
+    const uint32_t so = uni(rem > 0 ? (uint32_t)(r0 * ld2) : 0u);
+    const int rem32 = (int)(rem < TR ? rem : TR);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int row0 = (w * PER + q) * RPI;
+      dma16(rs, lrow < rem32 - row0 ? voff[q] : kOOB, so, uni(tile + (uint32_t)((w * PER + q) * 1024)));
+    }
+  }
+};
+
+typedef __attribute__((address_space(3))) char lds_char;
+
+// fragments of reduction step kk (32 r) of a stage tile for the 16-column
+// groups cw0 .. cw0 + NF - 1.  lbase = (8 (lane >> 4) + (lane & 15) / 4) ROWB
+// + 8 (lane & 3); fsw = trf of every row this lane reads, times 32.
+template <int NF, int ROWB>
+CONCORD_DEV void tr_frags(bf16x8 (&fr)[NF], const lds_char* tile, uint32_t lbase, uint32_t fsw, int cw0, int kk) {
+#pragma unroll
+  for (int x = 0; x < NF; ++x) {
+    const lds_char* q = tile + (lbase + ((uint32_t)((cw0 + x) * 32) ^ fsw)) + kk * 32 * ROWB;
+    const v4i16 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)q);
+    const v4i16 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(q + 4 * ROWB));
+    fr[x] = __builtin_bit_cast(bf16x8, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+}
+
+template <int NI, int NJ>
+CONCORD_DEV void mfma_block(f32x4 (&acc)[NI][NJ], const bf16x8 (&fa)[NI], const bf16x8 (&fb)[NJ]) {
+#pragma unroll
+  for (int x = 0; x < NI; ++x)
+#pragma unroll
+    for (int y = 0; y < NJ; ++y)
+      acc[x][y] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[y], fa[x], acc[x][y], 0, 0, 0);
+}
+
+// WI x WJ waves, each BI/WI x BJ/WJ; every wave computes and issues its share
+// of both operands' DMA.  Ring of three stages: stage s + 3 is loaded into
+// the slot of stage s as soon as every wave has finished reading stage s.
+// Per stage: fragments of the second half-stage are read while the first
+// half-stage's MFMAs issue, then (after the barrier) the next stage's first
+// half is read while the second half's MFMAs issue.
+template <int BI, int BJ, int WI, int WJ>
+__global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
+  constexpr int NW = WI * WJ, NT = 64 * NW, WTI = BI / WI, WTJ = BJ / WJ;
+  constexpr int NI = WTI / 16, NJ = WTJ / 16;
+  typedef TrDma<BI, NW> DA;
+  typedef TrDma<BJ, NW> DB;
+  constexpr int ABYTES = TR * BI * 2, STAGE = ABYTES + TR * BJ * 2;
+  constexpr int PERT = DA::PER + DB::PER;
+  static_assert(TR == 64, "two 32-deep MFMA steps per stage");
+  __shared__ __attribute__((aligned(1024))) uint16_t ring[3 * STAGE / 2];
+  static_assert(sizeof(ring) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the ring");
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const int tiles = g.tiles_i * g.tiles_j;
+  const int wg = blockIdx.x;
+  const int split = wg / tiles;
+  int bi, bj;
+  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
+  const int64_t r_begin = (int64_t)split * g.r_split;
+  const int64_t r_end = min(g.R, r_begin + g.r_split);
+  const int nst = r_end > r_begin ? (int)((r_end - r_begin + TR - 1) / TR) : 0;
+  const int wi = wave / WJ, wj = wave % WJ;
+
+  f32x4 acc[NI][NJ];
+#pragma unroll
+  for (int x = 0; x < NI; ++x)
+#pragma unroll
+    for (int y = 0; y < NJ; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  DA da;
+  DB db;
+  da.init(g.a + i0, g.lda, g.I - i0, g.R, wave, lane);
+  db.init(reinterpret_cast<const uint16_t*>(g.b) + j0, g.ldb, g.J - j0, g.R, wave, lane);
+  const uint32_t ring_lds = lds_addr(ring);
+  const lds_char* ring_p = (const lds_char*)ring;
+  auto dma_stage = [&](int s) {
+    const int64_t r0 = r_begin + (int64_t)s * TR;
+    const uint32_t slot = ring_lds + (uint32_t)((s % 3) * STAGE);
+    da.load(slot, r0, r_end - r0);
+    db.load(slot + ABYTES, r0, r_end - r0);
+  };
+  const int p = lane & 15, gq = lane >> 4;
+  const uint32_t fsw = (uint32_t)(((p >> 2) | ((gq & 1) << 2)) * 32);
+  const uint32_t la = (uint32_t)((8 * gq + (p >> 2)) * DA::ROWB + 8 * (p & 3));
+  const uint32_t lb = (uint32_t)(ABYTES + (8 * gq + (p >> 2)) * DB::ROWB + 8 * (p & 3));
+  const int cwa = wi * WTI / 16, cwb = wj * WTJ / 16;
+
+  dma_stage(0);
+  dma_stage(1);
+  dma_stage(2);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PERT));   // own stage-0 DMA landed
+  lds_barrier();
+  bf16x8 fa0[NI], fb0[NJ], fa1[NI], fb1[NJ];
+  tr_frags<NI, DA::ROWB>(fa0, ring_p, la, fsw, cwa, 0);
+  tr_frags<NJ, DB::ROWB>(fb0, ring_p, lb, fsw, cwb, 0);
+  for (int s = 0; s < nst; ++s) {
+    const lds_char* cur = ring_p + (s % 3) * STAGE;
+    tr_frags<NI, DA::ROWB>(fa1, cur, la, fsw, cwa, 1);
+    tr_frags<NJ, DB::ROWB>(fb1, cur, lb, fsw, cwb, 1);
+    mfma_block<NI, NJ>(acc, fa0, fb0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(PERT));     // own stage s+1 DMA landed
+    lds_barrier();                                    // stage s fully read by every wave
+    dma_stage(s + 3);
+    // after the last stage this reads a ring slot no MFMA uses (in bounds)
+    const lds_char* nxt = ring_p + ((s + 1) % 3) * STAGE;
+    tr_frags<NI, DA::ROWB>(fa0, nxt, la, fsw, cwa, 0);
+    tr_frags<NJ, DB::ROWB>(fb0, nxt, lb, fsw, cwb, 0);
+    mfma_block<NI, NJ>(acc, fa1, fb1);
+  }
+  // no DMA may still be writing LDS when the ring is reused for the output
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  epilogue<MODE_WGRAD, NI, NJ, BI, BJ, NW>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, wave, t, NT,
+                                           ring);
+}
+
 // ---- planning -----------------------------------------------------------------
 struct FastShape { int bi, bj, waves, minb; };
 
@@ -1031,6 +1198,11 @@ static bool eligible(int mode, const GemmArgs& g) {
   return false;
 }
 
+// the transpose-read WGRAD kernel moves 16-byte chunks of both operands
+static bool tr_eligible(const GemmArgs& g) {
+  return g.lda % 8 == 0 && g.I % 8 == 0 && al(g.a, 16) && g.ldb % 8 == 0 && g.J % 8 == 0 && al(g.b, 16);
+}
+
 // split-K: sum the partials once every split has stored them
 template <int MODE, int BI, int BJ, int WI, int WJ>
 static void launch_reduce(const GemmArgs& g, hipStream_t st) {
@@ -1045,6 +1217,12 @@ template <int MODE, int BI, int BJ>
 static void launch_dma(const GemmArgs& g, int blocks, hipStream_t st) {
   hipLaunchKernelGGL((gemm_dma_kernel<MODE, BI, BJ>), dim3(blocks), dim3(512), 0, st, g);
   launch_reduce<MODE, BI, BJ, 2, 2>(g, st);
+}
+
+template <int BI, int BJ, int WI, int WJ>
+static void launch_tr(const GemmArgs& g, int blocks, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_tr_kernel<BI, BJ, WI, WJ>), dim3(blocks), dim3(64 * WI * WJ), 0, st, g);
+  launch_reduce<MODE_WGRAD, BI, BJ, WI, WJ>(g, st);
 }
 
 template <int MODE, int BI, int BJ>
@@ -1115,7 +1293,9 @@ int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
       else launch<MODE_DGRAD_BF16, 128, 128, 2, 2, 2>(g, blocks, st);
       break;
     case MODE_WGRAD:
-      if (p.shape == 0) launch_ws<MODE_WGRAD, 256, 128>(g, blocks, st);
+      // 8 waves of 64 x 64 (measured faster than 4 waves of 128 x 64)
+      if (p.shape == 0 && tr_eligible(g)) launch_tr<256, 128, 4, 2>(g, blocks, st);
+      else if (p.shape == 0) launch_ws<MODE_WGRAD, 256, 128>(g, blocks, st);
       else launch<MODE_WGRAD, 128, 128, 2, 2, 2>(g, blocks, st);
       break;
     default:

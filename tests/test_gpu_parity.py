@@ -454,6 +454,20 @@ def test_wgrad(oracle, M, N, K):
     assert rel_l2(oracle.bf16_bits_to_f32(host(gw)), ref) < 5e-3
 
 
+@pytest.mark.parametrize("M,N,K", [(4096, 136, 200), (2048, 264, 256), (1000, 512, 128), (130, 8, 8)])
+def test_wgrad_split_reduction(oracle, M, N, K):
+    """Few output tiles and a long reduction: the planner splits the
+    reduction and a second kernel adds the partial tiles."""
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(M + 3 * N + K)
+    dy = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, N)).astype(np.float32))
+    x = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32))
+    gw = pb._wgrad(dev(dy), dev(x))
+    sync()
+    ref = oracle.bf16_bits_to_f32(dy).astype(np.float64).T @ oracle.bf16_bits_to_f32(x)
+    assert rel_l2(oracle.bf16_bits_to_f32(host(gw)), ref) < 5e-3
+
+
 @pytest.mark.parametrize("M,N,K", [(96, 264, 320), (96, 130, 320)])
 def test_dqgemm_extreme_exponents(oracle, M, N, K):
     """Row/column exponents at both ends of [EXP_MIN, EXP_MAX] (the fast
@@ -477,7 +491,8 @@ def test_gemm_splitk_workspace_reuse(oracle):
     partials overwrote (small grid first, then larger ones, then small again)."""
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(99)
-    for (M, N, K) in [(300, 200, 130), (300, 2050, 645), (77, 130, 200), (300, 2050, 645)]:
+    for (M, N, K) in [(300, 200, 130), (300, 2050, 645), (77, 130, 200), (300, 2050, 645),
+                      (3000, 136, 200), (300, 2056, 648), (4096, 264, 256), (3000, 136, 200)]:
         dy = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, N)).astype(np.float32))
         x = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32))
         gw = pb._wgrad(dev(dy), dev(x))
