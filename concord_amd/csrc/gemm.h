@@ -30,6 +30,8 @@ struct GemmArgs {
   uint32_t* tile_cnt;     // split-K: one counter per (i, j) tile, zero between calls
   int tiles_i, tiles_j, splits;
   int vec_a, vec_b, vec_c;  // base pointers and leading dimensions allow 16 B / 8 B accesses
+  float* vh_pr;           // WGRAD with v-hat partials: row / column partial sums of g^2
+  float* vh_pc;
 };
 
 // XCD-aware tile order: workgroup w runs on XCD w % 8.  XCD x owns tile
@@ -54,6 +56,12 @@ CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
 // returns CONCORD_OK, an error code, or -1 when the generic kernel must run
 int gemm_fast_launch(int mode, const GemmArgs& g, void* workspace, size_t ws_bytes,
                      hipStream_t st, const char* what);
+// WGRAD whose epilogue also writes the v-hat partial sums of the bf16 output
+// (vhat_tile.h order) into vh_pr / vh_pc; -1 when the shape or its alignment
+// does not run the transpose-read kernel, or when the plan given split_room
+// bytes of split-K workspace would split it (the caller then runs the plain
+// WGRAD and the separate partials kernel)
+int gemm_wgrad_vhat_launch(const GemmArgs& g, size_t split_room, hipStream_t st, const char* what);
 // split-K partial bytes the fast kernels plan for an I x J x R problem
 // given unlimited workspace (0 when they do not split it)
 size_t gemm_fast_partial_bytes(int mode, int64_t I, int64_t J, int64_t R);

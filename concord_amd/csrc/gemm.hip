@@ -22,6 +22,7 @@
 // Tiles are mapped XCD-aware: workgroup w runs on XCD w % 8, and each XCD
 // gets a compact block of the tile grid so its L2 serves shared operands.
 #include "gemm.h"
+#include "vhat.h"
 #include "workspace.h"
 
 namespace concord {
@@ -537,6 +538,40 @@ extern "C" int concord_wgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* 
   CONCORD_CHECK(ld_dy >= N && ld_x >= K && ld_gw >= K, "concord_wgrad: bad leading dimension");
   GemmArgs g = make_args(dy, x, ld_dy, ld_x, nullptr, nullptr, 0, nullptr, grad_w, ld_gw, N, K, M, false);
   return launch_gemm<MODE_WGRAD>(g, workspace, workspace_bytes, (hipStream_t)stream, "wgrad");
+}
+
+extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t ld_x,
+                                  uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
+                                  double beta2, float* v_row, float* v_col, float* sum_v_inv,
+                                  int32_t* row_max, int32_t* col_max, int32_t* salt_counter,
+                                  void* workspace, size_t workspace_bytes, void* gemm_workspace,
+                                  size_t gemm_workspace_bytes, void* stream) {
+  CONCORD_CHECK(sizes_ok(M, N, K) && N > 0 && K > 0, "concord_wgrad_vhat: bad size");
+  CONCORD_CHECK(dy && x && grad_w && v_row && v_col && sum_v_inv, "concord_wgrad_vhat: NULL argument");
+  CONCORD_CHECK(ld_dy >= N && ld_x >= K && ld_gw >= K, "concord_wgrad_vhat: bad leading dimension");
+  const Workspace ws = workspace_layout(N, K, 0);
+  if (!workspace || workspace_bytes < ws.total) {
+    set_error("concord_wgrad_vhat: workspace of %zu bytes needed", ws.total);
+    return CONCORD_EWORKSPACE;
+  }
+  const VhatScratch v = vhat_scratch(N, K);
+  float* pr = (float*)((char*)workspace + ws.scratch);
+  float* pc = pr + v.pr;
+  float* bsum = pc + v.pc;
+  hipStream_t st = (hipStream_t)stream;
+  GemmArgs g = make_args(dy, x, ld_dy, ld_x, nullptr, nullptr, 0, nullptr, grad_w, ld_gw, N, K, M, false);
+  g.vh_pr = pr;
+  g.vh_pc = pc;
+  int rc = gemm_wgrad_vhat_launch(g, gemm_workspace ? gemm_workspace_bytes : 0, st, "wgrad_vhat");
+  if (rc == -1) {   // split or unaligned WGRAD: the plain product, then the partials kernel
+    rc = launch_gemm<MODE_WGRAD>(g, gemm_workspace, gemm_workspace_bytes, st, "wgrad");
+    if (rc != CONCORD_OK) return rc;
+    vhat_partials_launch(grad_w, ld_gw, N, K, pr, pc, st);
+  } else if (rc != CONCORD_OK) {
+    return rc;
+  }
+  vhat_finish_launch(pr, pc, bsum, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter, st);
+  return launch_status("wgrad_vhat");
 }
 
 extern "C" int concord_gemm_bf16_fwd(const uint16_t* x, int64_t ld_x, const uint16_t* w,

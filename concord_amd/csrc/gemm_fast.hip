@@ -26,6 +26,7 @@
 #include <cmath>
 
 #include "gemm.h"
+#include "vhat_tile.h"
 #include "workspace.h"
 
 namespace concord {
@@ -1049,7 +1050,9 @@ CONCORD_DEV void mfma_block(f32x4 (&acc)[NI][NJ], const bf16x8 (&fa)[NI], const 
 // Per stage: fragments of the second half-stage are read while the first
 // half-stage's MFMAs issue, then (after the barrier) the next stage's first
 // half is read while the second half's MFMAs issue.
-template <int BI, int BJ, int WI, int WJ>
+// VH: also write the v-hat partials of the bf16-rounded output (64 x 64 wave
+// tiles, vhat_tile.h order); only without split-K.
+template <int BI, int BJ, int WI, int WJ, bool VH>
 __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
   constexpr int NW = WI * WJ, NT = 64 * NW, WTI = BI / WI, WTJ = BJ / WJ;
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
@@ -1122,6 +1125,23 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
   }
   // no DMA may still be writing LDS when the ring is reused for the output
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if constexpr (VH) {
+    static_assert(NI == 4 && NJ == 4, "v-hat partials take 64 x 64 wave tiles");
+    float g2[4][4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        // the values the epilogue stores: acc rounded to bf16
+        const uint32_t lo = pack_bf16x2(acc[x][y][0], acc[x][y][1]);
+        const uint32_t hi = pack_bf16x2(acc[x][y][2], acc[x][y][3]);
+        const float v[4] = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xFFFF0000u),
+                            __uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g2[x][y][e] = __fmul_rn(v[e], v[e]);
+      }
+    vhat_tile_partials(g2, lane, i0 + wi * WTI, j0 + wj * WTJ, g.I, g.J, g.vh_pr, g.vh_pc);
+  }
   epilogue<MODE_WGRAD, NI, NJ, BI, BJ, NW>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, wave, t, NT,
                                            ring);
 }
@@ -1221,7 +1241,7 @@ static void launch_dma(const GemmArgs& g, int blocks, hipStream_t st) {
 
 template <int BI, int BJ, int WI, int WJ>
 static void launch_tr(const GemmArgs& g, int blocks, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_tr_kernel<BI, BJ, WI, WJ>), dim3(blocks), dim3(64 * WI * WJ), 0, st, g);
+  hipLaunchKernelGGL((gemm_tr_kernel<BI, BJ, WI, WJ, false>), dim3(blocks), dim3(64 * WI * WJ), 0, st, g);
   launch_reduce<MODE_WGRAD, BI, BJ, WI, WJ>(g, st);
 }
 
@@ -1258,6 +1278,20 @@ size_t gemm_fast_partial_bytes(int mode, int64_t I, int64_t J, int64_t R) {
   if (p.splits <= 1) return 0;
   const FastShape& sh = shape_of(mode, p.shape);
   return (size_t)p.ti * p.tj * sh.bi * sh.bj * sizeof(float) * p.splits;
+}
+
+int gemm_wgrad_vhat_launch(const GemmArgs& g0, size_t split_room, hipStream_t st, const char* what) {
+  if (!eligible(MODE_WGRAD, g0) || !tr_eligible(g0)) return -1;
+  const size_t room = split_room > kSplitkCounterBytes ? split_room - kSplitkCounterBytes : 0;
+  const FastPlan p = plan_mode(MODE_WGRAD, g0.I, g0.J, g0.R, room);
+  if (p.shape != 0 || p.splits != 1) return -1;
+  GemmArgs g = g0;
+  g.splits = 1;
+  g.r_split = p.r_split;
+  g.tiles_i = p.ti;
+  g.tiles_j = p.tj;
+  hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true>), dim3(p.ti * p.tj), dim3(512), 0, st, g);
+  return launch_status(what);
 }
 
 int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_bytes,

@@ -4,129 +4,132 @@
 //                    (zero row/col watermarks, v_row/v_col EMA of grad^2, 1/sum v_row).
 // concord_bias_grad: grad_y_flat.sum(0), concord/packed_b.py:1338-1340.
 //
-// Reduction order (fixed, also restated by oracle_vhat_ema):
-//   P_r[c][n] = sum_{k in [64c, 64c+64)} g^2 ascending; P_c[r][k] = sum_{n in
-//   [128r, 128r+128)} g^2 ascending; g2_row[n] = sum_c P_r[c][n] ascending c;
-//   g2_col[k] = sum_r P_c[r][k] ascending r; sum v_row by 256 strided lanes
-//   followed by the halving tree.
+// Reduction order: the tile order of vhat_tile.h (also restated by
+// oracle_vhat_ema); g2_row[n] = sum of the row partials over column tiles
+// ascending, g2_col[k] likewise over row tiles; sum v_row: halving tree per
+// block of 256 rows, then the block totals ascending.
 #include "common.h"
+#include "vhat.h"
+#include "vhat_tile.h"
 #include "workspace.h"
 
 namespace concord {
 
-constexpr int VH_ROWS = 128;   // rows per column partial
-constexpr int VH_SUB = 32;     // rows staged in LDS at a time
-
-// One block: a slab of 128 rows x 256 columns, staged 32 rows at a time as
-// g^2 in LDS (257-float row stride: both walks are bank-conflict free).
+// One wave per 64 x 64 tile of g, loaded in the MFMA accumulator layout of
+// vhat_tile.h (lane 16 q + p: rows 16 x + p, columns 16 y + 4 q .. + 3).
 __global__ __launch_bounds__(256) void vhat_partials_kernel(const uint16_t* __restrict__ g,
                                                             int64_t ld, int64_t N, int64_t K,
                                                             float* __restrict__ pr,
                                                             float* __restrict__ pc) {
-  __shared__ float t[VH_SUB * 257];
-  const int64_t kb = (int64_t)blockIdx.x * 256, nb0 = (int64_t)blockIdx.y * VH_ROWS;
-  const int tid = threadIdx.x;
-  const int64_t nc = cdiv(K, 64);
-  const bool vec = (ld % 8) == 0;
-  float colsum = 0.0f;
-  for (int sub = 0; sub < VH_ROWS / VH_SUB; ++sub) {
-    const int64_t nb = nb0 + sub * VH_SUB;
-    if (nb >= N) break;
-    // load: thread -> (row = tid / 32 + 8 i, 8 columns at (tid % 32) * 8)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t ntc = cdiv(K, 64), nt = cdiv(N, 64) * ntc;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  if (tile >= nt) return;
+  const int64_t row0 = (tile / ntc) * 64, col0 = (tile % ntc) * 64;
+  const int p = lane & 15, q = lane >> 4;
+  const bool vec = (ld % 4) == 0 && ((uintptr_t)g % 8) == 0;
+  float g2[4][4][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = tid / 32 + 8 * i, c = (tid % 32) * 8;
-      const int64_t n = nb + r, k = kb + c;
-      float v[8];
-      if (n < N && k + 8 <= K && vec) {
-        const uint4 q = *reinterpret_cast<const uint4*>(g + n * ld + k);
-        const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  for (int x = 0; x < 4; ++x) {
+    const int64_t n = row0 + 16 * x + p;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          v[2 * j] = __uint_as_float(w[j] << 16);
-          v[2 * j + 1] = __uint_as_float(w[j] & 0xFFFF0000u);
-        }
+    for (int y = 0; y < 4; ++y) {
+      const int64_t k = col0 + 16 * y + 4 * q;
+      float v[4];
+      if (n < N && k + 4 <= K && vec) {
+        const uint2 w = *reinterpret_cast<const uint2*>(g + n * ld + k);
+        v[0] = __uint_as_float(w.x << 16);
+        v[1] = __uint_as_float(w.x & 0xFFFF0000u);
+        v[2] = __uint_as_float(w.y << 16);
+        v[3] = __uint_as_float(w.y & 0xFFFF0000u);
       } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          v[j] = (n < N && k + j < K) ? bf16_to_f32(g[n * ld + k + j]) : 0.0f;
+        for (int e = 0; e < 4; ++e) v[e] = (n < N && k + e < K) ? bf16_to_f32(g[n * ld + k + e]) : 0.0f;
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) t[r * 257 + c + j] = __fmul_rn(v[j], v[j]);
+      for (int e = 0; e < 4; ++e) g2[x][y][e] = __fmul_rn(v[e], v[e]);
     }
-    __syncthreads();
-    if (tid < 128) {
-      const int r = tid % 32, ch = tid / 32;
-      const int64_t n = nb + r, cg = (int64_t)blockIdx.x * 4 + ch;
-      if (n < N && cg < nc) {
-        float s = 0.0f;
-        const float* row = t + r * 257 + ch * 64;
-#pragma unroll 16
-        for (int j = 0; j < 64; ++j) s = __fadd_rn(s, row[j]);
-        pr[cg * N + n] = s;
-      }
-    }
-#pragma unroll 8
-    for (int r = 0; r < VH_SUB; ++r) colsum = __fadd_rn(colsum, t[r * 257 + tid]);
-    __syncthreads();
   }
-  const int64_t k = kb + tid;
-  if (k < K) pc[(int64_t)blockIdx.y * K + k] = colsum;
+  vhat_tile_partials(g2, lane, row0, col0, N, K, pr, pc);
 }
 
-// Row/column EMA and watermark zeroing; the last block to finish computes
-// 1/sum(v_row), advances the salt and re-arms the counter.
+// Row/column EMA and watermark zeroing.  Blocks [0, cdiv(N, 256)) take rows
+// and also leave the halving-tree total of their 256 new v_row values in
+// bsum; the remaining blocks take columns.
 __global__ __launch_bounds__(256) void vhat_finalize_kernel(
     const float* __restrict__ pr, const float* __restrict__ pc, int64_t N, int64_t K, float b2,
-    float omb2, float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max, int32_t* col_max,
-    int32_t* salt, uint32_t* counter) {
+    float omb2, float* v_row, float* v_col, int32_t* row_max, int32_t* col_max, float* bsum) {
   __shared__ float s_part[256];
-  __shared__ bool s_last;
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int64_t nc = cdiv(K, 64), nr = cdiv(N, VH_ROWS);
-  if (i < N) {
-    float s = 0.0f;
-    int64_t c = 0;
-    for (; c + 4 <= nc; c += 4) {   // loads issued ahead, adds in ascending c
-      const float a0 = pr[c * N + i], a1 = pr[(c + 1) * N + i];
-      const float a2 = pr[(c + 2) * N + i], a3 = pr[(c + 3) * N + i];
-      s = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(s, a0), a1), a2), a3);
+  const int64_t rb = cdiv(N, 256);
+  const int64_t nc = cdiv(K, 64), nr = cdiv(N, 64);
+  if ((int64_t)blockIdx.x < rb) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    float vn = 0.0f;
+    if (i < N) {
+      float s = 0.0f;
+      int64_t c = 0;
+      for (; c + 4 <= nc; c += 4) {   // loads issued ahead, adds in ascending c
+        const float a0 = pr[c * N + i], a1 = pr[(c + 1) * N + i];
+        const float a2 = pr[(c + 2) * N + i], a3 = pr[(c + 3) * N + i];
+        s = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(s, a0), a1), a2), a3);
+      }
+      for (; c < nc; ++c) s = __fadd_rn(s, pr[c * N + i]);
+      vn = __fadd_rn(__fmul_rn(v_row[i], b2), __fmul_rn(omb2, s));
+      v_row[i] = vn;
+      if (row_max) row_max[i] = 0;
     }
-    for (; c < nc; ++c) s = __fadd_rn(s, pr[c * N + i]);
-    v_row[i] = __fadd_rn(__fmul_rn(v_row[i], b2), __fmul_rn(omb2, s));
-    if (row_max) row_max[i] = 0;
-  } else if (i < N + K) {
-    const int64_t k = i - N;
+    s_part[threadIdx.x] = vn;
+    __syncthreads();
+    for (int h = 128; h >= 1; h >>= 1) {
+      if (threadIdx.x < h) s_part[threadIdx.x] = __fadd_rn(s_part[threadIdx.x], s_part[threadIdx.x + h]);
+      __syncthreads();
+    }
+    if (threadIdx.x == 0) bsum[blockIdx.x] = s_part[0];
+  } else {
+    const int64_t k = ((int64_t)blockIdx.x - rb) * 256 + threadIdx.x;
+    if (k >= K) return;
     float s = 0.0f;
     int64_t r = 0;
-    for (; r + 4 <= nr; r += 4) {
-      const float a0 = pc[r * K + k], a1 = pc[(r + 1) * K + k];
-      const float a2 = pc[(r + 2) * K + k], a3 = pc[(r + 3) * K + k];
-      s = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(s, a0), a1), a2), a3);
+    for (; r + 8 <= nr; r += 8) {
+      float a[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a[e] = pc[(r + e) * K + k];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s = __fadd_rn(s, a[e]);
     }
     for (; r < nr; ++r) s = __fadd_rn(s, pc[r * K + k]);
     v_col[k] = __fadd_rn(__fmul_rn(v_col[k], b2), __fmul_rn(omb2, s));
     if (col_max) col_max[k] = 0;
   }
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) s_last = atomicAdd(counter, 1u) == gridDim.x - 1;
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
+}
+
+// 1 / max(sum of the block totals ascending, 1e-30) and the salt advance.
+// A kernel of its own, so it sees every block total without a device fence.
+__global__ __launch_bounds__(64) void vhat_sum_kernel(const float* __restrict__ bsum, int64_t nb,
+                                                      float* sum_v_inv, int32_t* salt) {
+  if (threadIdx.x != 0) return;
   float s = 0.0f;
-  for (int64_t n = threadIdx.x; n < N; n += 256) s = __fadd_rn(s, v_row[n]);
-  s_part[threadIdx.x] = s;
-  __syncthreads();
-  for (int h = 128; h >= 1; h >>= 1) {
-    if (threadIdx.x < h) s_part[threadIdx.x] = __fadd_rn(s_part[threadIdx.x], s_part[threadIdx.x + h]);
-    __syncthreads();
-  }
-  if (threadIdx.x == 0) {
-    *sum_v_inv = __fdiv_rn(1.0f, fmaxf(s_part[0], 1e-30f));
-    if (salt) salt[0] = wadd(salt[0], 1);
-    *counter = 0u;
-  }
+  for (int64_t b = 0; b < nb; ++b) s = __fadd_rn(s, bsum[b]);
+  *sum_v_inv = __fdiv_rn(1.0f, fmaxf(s, 1e-30f));
+  if (salt) salt[0] = wadd(salt[0], 1);
+}
+
+void vhat_partials_launch(const uint16_t* grad, int64_t ld, int64_t N, int64_t K, float* pr, float* pc,
+                          hipStream_t st) {
+  const int64_t nt = cdiv(N, 64) * cdiv(K, 64);
+  hipLaunchKernelGGL(vhat_partials_kernel, dim3((unsigned)cdiv(nt, 4)), dim3(256), 0, st, grad, ld, N, K,
+                     pr, pc);
+}
+
+void vhat_finish_launch(const float* pr, const float* pc, float* bsum, int64_t N, int64_t K, double beta2,
+                        float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max, int32_t* col_max,
+                        int32_t* salt, hipStream_t st) {
+  const float b2 = (float)beta2;
+  const float omb2 = (float)(1.0 - beta2);
+  const int64_t rb = cdiv(N, 256);
+  hipLaunchKernelGGL(vhat_finalize_kernel, dim3((unsigned)(rb + cdiv(K, 256))), dim3(256), 0, st, pr, pc,
+                     N, K, b2, omb2, v_row, v_col, row_max, col_max, bsum);
+  hipLaunchKernelGGL(vhat_sum_kernel, dim3(1), dim3(64), 0, st, bsum, rb, sum_v_inv, salt);
 }
 
 // bias gradient: a thread sums two adjacent columns over a 256-row slab
@@ -188,19 +191,13 @@ extern "C" int concord_vhat_ema(const uint16_t* grad, int64_t ld_g, int64_t N, i
     set_error("concord_vhat_ema: workspace of %zu bytes needed", ws.total);
     return CONCORD_EWORKSPACE;
   }
-  char* base = (char*)workspace;
-  float* pr = (float*)(base + ws.scratch);
-  float* pc = pr + cdiv(K, 64) * N;
-  uint32_t* counter = (uint32_t*)(base + ws.vhat_counter);
+  const VhatScratch v = vhat_scratch(N, K);
+  float* pr = (float*)((char*)workspace + ws.scratch);
+  float* pc = pr + v.pr;
+  float* bsum = pc + v.pc;
   hipStream_t st = (hipStream_t)stream;
-  const float b2 = (float)beta2;
-  const float omb2 = (float)(1.0 - beta2);
-  hipLaunchKernelGGL(vhat_partials_kernel,
-                     dim3((unsigned)cdiv(K, 256), (unsigned)cdiv(N, VH_ROWS)), dim3(256), 0, st,
-                     grad, ld_g, N, K, pr, pc);
-  hipLaunchKernelGGL(vhat_finalize_kernel, dim3((unsigned)cdiv(N + K, 256)), dim3(256), 0, st, pr,
-                     pc, N, K, b2, omb2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter,
-                     counter);
+  vhat_partials_launch(grad, ld_g, N, K, pr, pc, st);
+  vhat_finish_launch(pr, pc, bsum, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter, st);
   return launch_status("vhat_ema");
 }
 

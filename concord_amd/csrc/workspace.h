@@ -1,9 +1,8 @@
 // workspace.h -- layout of the caller-owned workspaces.
 //
 // Update-side workspace:
-// [0, 256)       counters: the v-hat "blocks done" counter and the rebalance
-//                "fired" flag; zero when the workspace is created and zero
-//                again after every call that uses them.
+// [0, 256)       counters: the rebalance "fired" flag; zero when the
+//                workspace is created and zero again after every call.
 // [256, total)   scratch shared by the entry points (they run in stream order):
 //                v-hat partials, rebalance decisions, bias-gradient partials.
 #pragma once
@@ -13,17 +12,27 @@
 namespace concord {
 
 struct Workspace {
-  size_t vhat_counter, reb_fired, scratch, total;
+  size_t reb_fired, scratch, total;
 };
+
+// v-hat scratch (floats, each region a multiple of 64 so the next stays
+// 256-byte aligned): row partials per 64-column tile, column partials per
+// 64-row tile, one total per 256-row block of v_row
+struct VhatScratch {
+  int64_t pr, pc, bsum;
+};
+inline VhatScratch vhat_scratch(int64_t N, int64_t K) {
+  auto cd = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
+  return VhatScratch{cd(cd(K, 64) * N, 64) * 64, cd(cd(N, 64) * K, 64) * 64, cd(cd(N, 256), 64) * 64};
+}
 
 inline Workspace workspace_layout(int64_t N, int64_t K, int64_t M) {
   auto cd = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
   Workspace w;
-  w.vhat_counter = 0;
   w.reb_fired = 64;
   w.scratch = 256;
-  // v-hat: row partials per 64-column chunk, column partials per 128-row slab
-  const size_t vhat = (size_t)(cd(K, 64) * N + cd(N, 128) * K) * sizeof(float);
+  const VhatScratch v = vhat_scratch(N, K);
+  const size_t vhat = (size_t)(v.pr + v.pc + v.bsum) * sizeof(float);
   const size_t reb = (size_t)(2 * (N + K)) * sizeof(int32_t);
   const size_t bias = (size_t)(cd(M, 256) * (N > K ? N : K)) * sizeof(float);
   size_t s = vhat;

@@ -510,6 +510,22 @@ def _wgrad(dy, x2):
     return gw
 
 
+def _wgrad_vhat(dy, x2, v_row, v_col, sum_v_inv, beta2, row_max, col_max, salt_counter):
+    """wgrad with the v-hat partials formed in its epilogue, then the EMA
+    (concord/packed_b.py:1269-1303); same results as _wgrad + vhat_ema."""
+    M, N = dy.shape
+    K = x2.shape[1]
+    gw = torch.empty((N, K), dtype=torch.bfloat16, device=dy.device)
+    gws = _gemm_workspace(dy.device, M, N, K)
+    ws = _workspace(dy.device, N, K)
+    C.check(C.lib().concord_wgrad_vhat(
+        C.ptr(dy), dy.stride(0), C.ptr(x2), x2.stride(0), C.ptr(gw), gw.stride(0), M, N, K,
+        float(beta2), C.ptr(v_row), C.ptr(v_col), C.ptr(sum_v_inv), C.ptr(row_max), C.ptr(col_max),
+        C.ptr(salt_counter), C.ptr(ws), ws.numel(), C.ptr(gws), gws.numel(),
+        C.stream_of(dy.device)), "wgrad_vhat")
+    return gw
+
+
 def _bias_grad(dy):
     M, N = dy.shape
     need = int(C.lib().concord_workspace_bytes(N, 1, M))
@@ -578,18 +594,20 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
         # dgrad on the pre-update weight (1263), before the update below
         grad_x = _gemm_dgrad(dy, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias,
                              ctx.weight_buf).reshape(*ctx.lead, K)
-        grad_W = _wgrad(dy, x2)
-        if _DEBUG_CAPTURE is not None:
-            _DEBUG_CAPTURE.append(grad_W.clone())
         salt = _get_step_counter(dev)
         prebumped = False
         if ctx.track_adafactor_v and ctx.v_row is not None:
-            # zeroes the watermarks (1281-1283), v-hat EMA (1288-1303), salt + 1 (910-911)
-            vhat_ema(grad_W, ctx.v_row, ctx.v_col, ctx.sum_v_inv, ctx.adafactor_beta2,
-                     ctx.row_max_buf if ctx.track_rebalance else None,
-                     ctx.col_max_buf if ctx.track_rebalance else None, salt)
+            # wgrad (1269-1277), watermark zeroing (1281-1283), v-hat EMA (1288-1303),
+            # salt + 1 (910-911)
+            grad_W = _wgrad_vhat(dy, x2, ctx.v_row, ctx.v_col, ctx.sum_v_inv, ctx.adafactor_beta2,
+                                 ctx.row_max_buf if ctx.track_rebalance else None,
+                                 ctx.col_max_buf if ctx.track_rebalance else None, salt)
             prebumped = True
-        elif ctx.track_rebalance:
+        else:
+            grad_W = _wgrad(dy, x2)
+        if _DEBUG_CAPTURE is not None:
+            _DEBUG_CAPTURE.append(grad_W.clone())
+        if not prebumped and ctx.track_rebalance:
             ctx.row_max_buf.zero_()
             ctx.col_max_buf.zero_()
         if ctx.optimizer_kind == 'adamw':

@@ -179,6 +179,20 @@ int concord_wgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t 
                   uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* wgrad followed by the v-hat EMA, with the v-hat partial sums formed in the
+ * wgrad epilogue from the bf16 values it stores (no re-read of grad_w):
+ * grad_y_flat.T @ x_flat, the watermark zeroing and the v_row/v_col EMA of
+ * FusedConcordLinearPackedB.backward, concord/packed_b.py:1269-1303.  Results
+ * are bit-identical to concord_wgrad followed by concord_vhat_ema with the
+ * same arguments.  workspace: concord_workspace_bytes(N, K, M) bytes;
+ * gemm_workspace (optional): concord_gemm_workspace_bytes(M, N, K) bytes. */
+int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t ld_x,
+                       uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
+                       double beta2, float* v_row, float* v_col, float* sum_v_inv,
+                       int32_t* row_max, int32_t* col_max, int32_t* salt_counter, void* workspace,
+                       size_t workspace_bytes, void* gemm_workspace, size_t gemm_workspace_bytes,
+                       void* stream);
+
 /* The forward and dgrad products over a materialised bf16 weight w[N,K]: the
  * reference's cached weight_buf path, F.linear(x, weight_buf, bias) and
  * grad_y @ weight_buf (concord/packed_b.py:1219, 1263). */

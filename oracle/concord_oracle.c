@@ -538,40 +538,74 @@ void oracle_rebalance(int32_t* packed, int8_t* row_exp, int8_t* col_exp,
 /* ---- A5 v-hat EMA: concord/packed_b.py:1288-1303 ---------------------------
  * g2 = f32(grad)^2; v_row = b2*v_row + (1-b2)*sum_k g2; v_col likewise;
  * sum_v_inv = 1 / max(sum_n v_row, 1e-30).
- * Reduction order (this build's definition; the reference leaves it to torch):
- *   row partial  P_r[c][n] = sum over k in [64c, 64c+64) ascending, from 0.0f
- *   col partial  P_c[r][k] = sum over n in [128r, 128r+128) ascending, from 0.0f
- *   g2_row[n] = sum over c ascending of P_r[c][n]; g2_col[k] likewise over r
- *   sum_v: 256 strided partials s_t = sum_{n = t mod 256} v_row[n] (ascending
- *   n), then the tree s_t += s_{t+h} for h = 128, 64, ..., 1. */
+ * Reduction order (this build's definition; the reference leaves it to torch).
+ * The grad is cut into 64 x 64 tiles (zeros past N and K); inside a tile,
+ * with g2[r][c] for tile row r and column c:
+ *   row partial of row r (P_r[col tile][n]):
+ *     s(y, q) = ((g2[r][16y+4q] + g2[r][16y+4q+1]) + g2[r][16y+4q+2]) + g2[r][16y+4q+3]
+ *     t(y)    = (s(y,0) + s(y,1)) + (s(y,2) + s(y,3))
+ *     P       = ((t(0) + t(1)) + t(2)) + t(3)
+ *   column partial of column c (P_c[row tile][k]):
+ *     for each block x of 16 rows, a(p) = g2[16x+p][c], p = 0..15:
+ *       u1(p) = a(p) + a(p+8), p < 8;  u2(p) = u1(p) + u1(p+4), p < 4;
+ *       u3(p) = u2(p) + u2(p+2), p < 2;  u(x) = u3(0) + u3(1)
+ *     P = ((u(0) + u(1)) + u(2)) + u(3)
+ *   g2_row[n] = sum over column tiles ascending of P_r, from 0.0f; g2_col[k]
+ *   likewise over row tiles;
+ *   sum_v: per block of 256 rows the halving tree s_t += s_{t+h}, h = 128 ..
+ *   1, over v_row (zeros past N); then the block totals ascending from 0.0f.
+ * (The GPU forms these partials in the wgrad epilogue from the MFMA
+ * accumulator layout: lane (p, q) of a wave holds tile rows 16x+p, columns
+ * 16y+4q..16y+4q+3.) */
+static float vh_row_tile(const float* g2r /* 64 values */) {
+    float t[4];
+    for (int y = 0; y < 4; ++y) {
+        float sq[4];
+        for (int q = 0; q < 4; ++q) {
+            const float* v = g2r + 16 * y + 4 * q;
+            sq[q] = ((v[0] + v[1]) + v[2]) + v[3];
+        }
+        t[y] = (sq[0] + sq[1]) + (sq[2] + sq[3]);
+    }
+    return ((t[0] + t[1]) + t[2]) + t[3];
+}
+
+static float vh_col_tile(const float* g2c /* 64 values, one per tile row */) {
+    float u[4];
+    for (int x = 0; x < 4; ++x) {
+        const float* a = g2c + 16 * x;
+        float u1[8], u2[4], u3[2];
+        for (int p = 0; p < 8; ++p) u1[p] = a[p] + a[p + 8];
+        for (int p = 0; p < 4; ++p) u2[p] = u1[p] + u1[p + 4];
+        for (int p = 0; p < 2; ++p) u3[p] = u2[p] + u2[p + 2];
+        u[x] = u3[0] + u3[1];
+    }
+    return ((u[0] + u[1]) + u[2]) + u[3];
+}
+
 void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
                      float* v_row, float* v_col, float* sum_v_inv,
                      double beta2) {
     const float b2 = (float)beta2;
     const float omb2 = (float)(1.0 - beta2);
-    const int64_t nc = (K + 63) / 64, nr = (N + 127) / 128;
+    const int64_t nc = (K + 63) / 64, nr = (N + 63) / 64;
     float* pr = (float*)malloc((size_t)(nc * N) * sizeof(float));
     float* pc = (float*)malloc((size_t)(nr * K) * sizeof(float));
 #pragma omp parallel for schedule(static)
-    for (int64_t n = 0; n < N; ++n) {
-        for (int64_t c = 0; c < nc; ++c) {
-            float s = 0.0f;
-            for (int64_t k = 64 * c; k < 64 * c + 64 && k < K; ++k) {
-                float g = bf16_to_f32(grad_bf16[n * K + k]);
-                s = s + g * g;
+    for (int64_t t = 0; t < nr * nc; ++t) {
+        const int64_t n0 = (t / nc) * 64, k0 = (t % nc) * 64;
+        float g2[64][64];
+        for (int r = 0; r < 64; ++r)
+            for (int c = 0; c < 64; ++c) {
+                const int64_t n = n0 + r, k = k0 + c;
+                float g = (n < N && k < K) ? bf16_to_f32(grad_bf16[n * K + k]) : 0.0f;
+                g2[r][c] = g * g;
             }
-            pr[c * N + n] = s;
-        }
-    }
-#pragma omp parallel for schedule(static)
-    for (int64_t r = 0; r < nr; ++r) {
-        for (int64_t k = 0; k < K; ++k) {
-            float s = 0.0f;
-            for (int64_t n = 128 * r; n < 128 * r + 128 && n < N; ++n) {
-                float g = bf16_to_f32(grad_bf16[n * K + k]);
-                s = s + g * g;
-            }
-            pc[r * K + k] = s;
+        for (int r = 0; r < 64 && n0 + r < N; ++r) pr[(k0 / 64) * N + n0 + r] = vh_row_tile(g2[r]);
+        for (int c = 0; c < 64 && k0 + c < K; ++c) {
+            float col[64];
+            for (int r = 0; r < 64; ++r) col[r] = g2[r][c];
+            pc[(n0 / 64) * K + k0 + c] = vh_col_tile(col);
         }
     }
     for (int64_t n = 0; n < N; ++n) {
@@ -584,15 +618,15 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
         for (int64_t r = 0; r < nr; ++r) s = s + pc[r * K + k];
         v_col[k] = v_col[k] * b2 + omb2 * s;
     }
-    float part[256];
-    for (int t = 0; t < 256; ++t) {
-        float s = 0.0f;
-        for (int64_t n = t; n < N; n += 256) s = s + v_row[n];
-        part[t] = s;
+    float total = 0.0f;
+    for (int64_t b0 = 0; b0 < N; b0 += 256) {
+        float part[256];
+        for (int t = 0; t < 256; ++t) part[t] = (b0 + t < N) ? v_row[b0 + t] : 0.0f;
+        for (int h = 128; h >= 1; h >>= 1)
+            for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
+        total = total + part[0];
     }
-    for (int h = 128; h >= 1; h >>= 1)
-        for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
-    const float sv = fmaxf(part[0], 1e-30f);
+    const float sv = fmaxf(total, 1e-30f);
     *sum_v_inv = 1.0f / sv;
     free(pr);
     free(pc);

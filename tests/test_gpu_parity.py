@@ -356,7 +356,7 @@ def test_vhat_matches_oracle(oracle, N, K):
     rm = torch.full((N,), 7, dtype=torch.int32, device=DEV)
     cm = torch.full((K,), 7, dtype=torch.int32, device=DEV)
     salt = torch.tensor([5], dtype=torch.int32, device=DEV)
-    for _ in range(2):   # twice: the completion counter must re-arm itself
+    for _ in range(2):   # twice: workspace reuse
         pb.vhat_ema(dev(g), vrd, vcd, svi, 0.999, rm, cm, salt)
         s = oracle.vhat_ema(g, vr, vc, 0.999)
     sync()
@@ -365,6 +365,43 @@ def test_vhat_matches_oracle(oracle, N, K):
     assert host(svi)[0] == s
     assert not host(rm).any() and not host(cm).any()
     assert int(host(salt)[0]) == 7
+
+
+@pytest.mark.parametrize("M,N,K", [(300, 2056, 648), (2048, 5120, 1280), (2048, 1280, 1280), (77, 130, 200),
+                                   (64, 136, 4096)])
+def test_wgrad_vhat_matches_separate_calls(oracle, M, N, K):
+    """wgrad with the v-hat partials formed in its epilogue (fused path when
+    the product runs unsplit on the transpose-read kernel, else the separate
+    partials kernel) equals wgrad followed by vhat_ema bit for bit, and the
+    v-hat equals the oracle's on the same bf16 gradient."""
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(M + N + K + 11)
+    dy = dev(oracle.f32_to_bf16_bits_array((rng.standard_normal((M, N)) * 1e-2).astype(np.float32)))
+    x = dev(oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32)))
+    vr = (rng.random(N) * 1e-6).astype(np.float32)
+    vc = (rng.random(K) * 1e-6).astype(np.float32)
+    outs = []
+    for fused in (True, False):
+        vrd, vcd = dev(vr), dev(vc)
+        svi = torch.zeros(1, dtype=torch.float32, device=DEV)
+        rm = torch.full((N,), 7, dtype=torch.int32, device=DEV)
+        cm = torch.full((K,), 7, dtype=torch.int32, device=DEV)
+        salt = torch.tensor([5], dtype=torch.int32, device=DEV)
+        if fused:
+            gw = pb._wgrad_vhat(dy, x, vrd, vcd, svi, 0.999, rm, cm, salt)
+        else:
+            gw = pb._wgrad(dy, x)
+            pb.vhat_ema(gw, vrd, vcd, svi, 0.999, rm, cm, salt)
+        sync()
+        assert not host(rm).any() and not host(cm).any() and int(host(salt)[0]) == 6
+        outs.append((host(gw), host(vrd), host(vcd), host(svi)))
+    for a, b in zip(outs[0], outs[1]):
+        np.testing.assert_array_equal(a, b)
+    g = outs[0][0]
+    s = oracle.vhat_ema(g, vr, vc, 0.999)
+    np.testing.assert_array_equal(outs[0][1], vr)
+    np.testing.assert_array_equal(outs[0][2], vc)
+    assert outs[0][3][0] == s
 
 
 def test_load_weights_matches_reference_golden():
