@@ -62,6 +62,13 @@ int gemm_fast_launch(int mode, const GemmArgs& g, void* workspace, size_t ws_byt
 // bytes of split-K workspace would split it (the caller then runs the plain
 // WGRAD and the separate partials kernel)
 int gemm_wgrad_vhat_launch(const GemmArgs& g, size_t split_room, hipStream_t st, const char* what);
+// a plain bf16 product through the fast or generic kernels: MODE_FWD_BF16
+// (C[I][J] = sum_r a[i][r] b[j][r]) or MODE_DGRAD_BF16 (sum_r a[i][r] b[r][j])
+int gemm_bf16_run(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
+                  int64_t ldc, int64_t I, int64_t J, int64_t R, void* ws, size_t ws_bytes, hipStream_t st,
+                  const char* what);
+// split-K workspace bytes (counters + partials) one such product may use
+size_t gemm_splitk_need(int mode, int64_t I, int64_t J, int64_t R);
 // split-K partial bytes the fast kernels plan for an I x J x R problem
 // given unlimited workspace (0 when they do not split it)
 size_t gemm_fast_partial_bytes(int mode, int64_t I, int64_t J, int64_t R);

@@ -491,6 +491,24 @@ static size_t splitk_partials(int mode, int64_t I, int64_t J, int64_t R) {
   return fast > generic ? fast : generic;
 }
 
+namespace concord {
+
+int gemm_bf16_run(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
+                  int64_t ldc, int64_t I, int64_t J, int64_t R, void* ws, size_t ws_bytes, hipStream_t st,
+                  const char* what) {
+  GemmArgs g = make_args(a, b, lda, ldb, nullptr, nullptr, 0, nullptr, c, ldc, I, J, R, false);
+  if (mode == MODE_FWD_BF16) return launch_gemm<MODE_FWD_BF16>(g, ws, ws_bytes, st, what);
+  if (mode == MODE_DGRAD_BF16) return launch_gemm<MODE_DGRAD_BF16>(g, ws, ws_bytes, st, what);
+  set_error("%s: unsupported product", what);
+  return CONCORD_EINVAL;
+}
+
+size_t gemm_splitk_need(int mode, int64_t I, int64_t J, int64_t R) {
+  return kSplitkCounterBytes + ((splitk_partials(mode, I, J, R) + 255) / 256) * 256;
+}
+
+}  // namespace concord
+
 extern "C" size_t concord_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K) {
   // tile counters + the split-K partials of the largest need among the layer's
   // three products: y [M,N] (reduce K), dx [M,K] (reduce N), gw [N,K] (reduce M)

@@ -1,0 +1,210 @@
+// muon.hip -- the Muon drive: O = gamma * NS5(g / ||g||_F) in bf16.
+//
+// experiments/cpu_dynamics/exp9_muon.py:44-55 (ns5) and 58-100 (the drive
+// sqrt(max(N, K)) * ns5(g / ||g||)); docs/MUON_IMPLEMENTATION.md:27-40 (bf16
+// NS on the backward's grad_W) and 87-119 (O is the apply kernel's step).
+//
+// Numerics (oracle_muon_ns5 restates them):
+//   ||g||^2  blocks of 8192 elements of the row-major flattening; lane t of a
+//            block sums elements t, t + 256, ... ascending, then the halving
+//            tree over 256 lanes; block totals ascending.  norm = sqrt (RN).
+//   X0 = bf16(g / (norm + 1e-7)), transposed when N > K (X is m x n, m <= n)
+//   5 x:  A = bf16(X X^T); AA = bf16(A A); B = bf16(b A + c AA);
+//         BX = bf16(B X); X = bf16(a X + BX)      (products: bf16 MFMA, fp32 acc)
+//   out = bf16(gamma X), transposed back.
+// The three products run on the library's bf16 GEMM kernels; the elementwise
+// steps are small bandwidth kernels.
+#include "common.h"
+#include "gemm.h"
+#include "workspace.h"
+
+namespace concord {
+
+constexpr int kFrobBlock = 8192;
+
+// per-block partial of sum g^2 in the order above
+__global__ __launch_bounds__(256) void frob_partials_kernel(const uint16_t* __restrict__ g, int64_t ld,
+                                                            int64_t N, int64_t K, float* __restrict__ part) {
+  __shared__ float s[256];
+  const int64_t total = N * K;
+  const int64_t b0 = (int64_t)blockIdx.x * kFrobBlock;
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int i = 0; i < kFrobBlock / 256; ++i) {
+    const int64_t e = b0 + threadIdx.x + 256 * i;
+    float v = 0.0f;
+    if (e < total) v = bf16_to_f32(ld == K ? g[e] : g[(e / K) * ld + e % K]);
+    acc = __fadd_rn(acc, __fmul_rn(v, v));
+  }
+  s[threadIdx.x] = acc;
+  __syncthreads();
+  for (int h = 128; h >= 1; h >>= 1) {
+    if (threadIdx.x < h) s[threadIdx.x] = __fadd_rn(s[threadIdx.x], s[threadIdx.x + h]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = s[0];
+}
+
+// den = sqrt(sum of the block partials ascending) + 1e-7
+__global__ __launch_bounds__(64) void frob_den_kernel(const float* __restrict__ part, int64_t nb, float* den) {
+  if (threadIdx.x != 0) return;
+  float s = 0.0f;
+  for (int64_t b = 0; b < nb; ++b) s = __fadd_rn(s, part[b]);
+  *den = __fadd_rn(sqrt_rn(s), 1e-7f);
+}
+
+// dst[r][c] = bf16(op(src)) over a 64 x 64 tile, where the destination is
+// R x C; with TRANS the source element of dst[r][c] is src[c][r].
+// DIV: src / *den (the first NS input); else gamma * src (the output).
+template <bool TRANS, bool DIV>
+__global__ __launch_bounds__(256) void ns5_copy_kernel(const uint16_t* __restrict__ src, int64_t lds,
+                                                       uint16_t* __restrict__ dst, int64_t ldd, int64_t R,
+                                                       int64_t C, const float* den, float gamma) {
+  __shared__ float t[64][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+  const float d = DIV ? *den : gamma;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    // read coalesced along the source's rows
+    if (TRANS) {
+      const int64_t sr = c0 + i, sc = r0 + tx;   // src[sr][sc] -> dst[sc][sr]
+      float v = 0.0f;
+      if (sr < C && sc < R) v = bf16_to_f32(src[sr * lds + sc]);
+      t[tx][i] = v;
+    } else {
+      const int64_t sr = r0 + i, sc = c0 + tx;
+      float v = 0.0f;
+      if (sr < R && sc < C) v = bf16_to_f32(src[sr * lds + sc]);
+      t[i][tx] = v;
+    }
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t r = r0 + i, c = c0 + tx;
+    if (r < R && c < C) {
+      const float v = t[i][tx];
+      const float o = DIV ? __fdiv_rn(v, d) : __fmul_rn(d, v);
+      dst[r * ldd + c] = (uint16_t)(pack_bf16x2(o, 0.0f) & 0xFFFFu);
+    }
+  }
+}
+
+// y = bf16(s * y + t * x), elementwise over n values (B from A and AA with
+// s = b, t = c; the new X from X and BX with s = a, t = 1)
+__global__ __launch_bounds__(256) void ns5_axpby_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
+                                                        int64_t n, float s, float t) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (i >= n) return;
+  if (i + 4 <= n) {
+    const uint2 yv = *reinterpret_cast<const uint2*>(y + i);
+    const uint2 xv = *reinterpret_cast<const uint2*>(x + i);
+    const uint32_t yw[2] = {yv.x, yv.y}, xw[2] = {xv.x, xv.y};
+    uint32_t o[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float y0 = __uint_as_float(yw[h] << 16), y1 = __uint_as_float(yw[h] & 0xFFFF0000u);
+      const float x0 = __uint_as_float(xw[h] << 16), x1 = __uint_as_float(xw[h] & 0xFFFF0000u);
+      const float r0 = t == 1.0f ? __fadd_rn(__fmul_rn(s, y0), x0) : __fadd_rn(__fmul_rn(s, y0), __fmul_rn(t, x0));
+      const float r1 = t == 1.0f ? __fadd_rn(__fmul_rn(s, y1), x1) : __fadd_rn(__fmul_rn(s, y1), __fmul_rn(t, x1));
+      o[h] = pack_bf16x2(r0, r1);
+    }
+    *reinterpret_cast<uint2*>(y + i) = make_uint2(o[0], o[1]);
+  } else {
+    for (int64_t j = i; j < n; ++j) {
+      const float yv = bf16_to_f32(y[j]), xv = bf16_to_f32(x[j]);
+      const float r = t == 1.0f ? __fadd_rn(__fmul_rn(s, yv), xv) : __fadd_rn(__fmul_rn(s, yv), __fmul_rn(t, xv));
+      y[j] = (uint16_t)(pack_bf16x2(r, 0.0f) & 0xFFFFu);
+    }
+  }
+}
+
+struct MuonLayout {
+  size_t x, bx, a, aa, part, den, gemm, total;
+};
+
+static MuonLayout muon_layout(int64_t N, int64_t K) {
+  const int64_t m = N < K ? N : K, n = N < K ? K : N;
+  auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
+  MuonLayout L;
+  size_t o = 0;
+  L.x = o; o += r256((size_t)m * n * 2);
+  L.bx = o; o += r256((size_t)m * n * 2);
+  L.a = o; o += r256((size_t)m * m * 2);
+  L.aa = o; o += r256((size_t)m * m * 2);
+  L.part = o; o += r256((size_t)cdiv(N * K, kFrobBlock) * 4);
+  L.den = o; o += 256;
+  // split-K region of the three products (tile counters first, zeroed once)
+  size_t g = gemm_splitk_need(MODE_FWD_BF16, m, m, n);
+  const size_t g2 = gemm_splitk_need(MODE_DGRAD_BF16, m, m, m), g3 = gemm_splitk_need(MODE_DGRAD_BF16, m, n, m);
+  if (g2 > g) g = g2;
+  if (g3 > g) g = g3;
+  L.gemm = o; o += r256(g);
+  L.total = o;
+  return L;
+}
+
+}  // namespace concord
+
+using namespace concord;
+
+extern "C" size_t concord_muon_workspace_bytes(int64_t N, int64_t K) {
+  if (N <= 0 || K <= 0) return 256;
+  return muon_layout(N, K).total;
+}
+
+extern "C" int concord_muon_ns5(const uint16_t* g, int64_t ld_g, int64_t N, int64_t K, float gamma,
+                                uint16_t* out, int64_t ld_out, void* workspace, size_t workspace_bytes,
+                                void* stream) {
+  CONCORD_CHECK(N > 0 && K > 0 && N < (1LL << 30) && K < (1LL << 30) && N * K < (1LL << 40),
+                "concord_muon_ns5: bad size N=%lld K=%lld", (long long)N, (long long)K);
+  CONCORD_CHECK(g && out, "concord_muon_ns5: NULL argument");
+  CONCORD_CHECK(ld_g >= K && ld_out >= K, "concord_muon_ns5: leading dimension < K");
+  const MuonLayout L = muon_layout(N, K);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("concord_muon_ns5: workspace of %zu bytes needed", L.total);
+    return CONCORD_EWORKSPACE;
+  }
+  char* base = (char*)workspace;
+  uint16_t* X = (uint16_t*)(base + L.x);
+  uint16_t* BX = (uint16_t*)(base + L.bx);
+  uint16_t* A = (uint16_t*)(base + L.a);
+  uint16_t* AA = (uint16_t*)(base + L.aa);
+  float* part = (float*)(base + L.part);
+  float* den = (float*)(base + L.den);
+  void* gws = base + L.gemm;
+  const size_t gws_bytes = L.total - L.gemm;
+  hipStream_t st = (hipStream_t)stream;
+  const bool tr = N > K;
+  const int64_t m = tr ? K : N, n = tr ? N : K;
+  const int64_t nb = cdiv(N * K, kFrobBlock);
+
+  hipLaunchKernelGGL(frob_partials_kernel, dim3((unsigned)nb), dim3(256), 0, st, g, ld_g, N, K, part);
+  hipLaunchKernelGGL(frob_den_kernel, dim3(1), dim3(64), 0, st, part, nb, den);
+  const dim3 gx((unsigned)cdiv(n, 64), (unsigned)cdiv(m, 64));
+  if (tr)
+    hipLaunchKernelGGL((ns5_copy_kernel<true, true>), gx, dim3(256), 0, st, g, ld_g, X, n, m, n, den, 0.0f);
+  else
+    hipLaunchKernelGGL((ns5_copy_kernel<false, true>), gx, dim3(256), 0, st, g, ld_g, X, n, m, n, den, 0.0f);
+  int rc = launch_status("muon_ns5");
+  if (rc != CONCORD_OK) return rc;
+  const float a = 3.4445f, b = -4.7750f, c = 2.0315f;
+  for (int it = 0; it < 5; ++it) {
+    rc = gemm_bf16_run(MODE_FWD_BF16, X, n, X, n, A, m, m, m, n, gws, gws_bytes, st, "muon_ns5 X X^T");
+    if (rc != CONCORD_OK) return rc;
+    rc = gemm_bf16_run(MODE_DGRAD_BF16, A, m, A, m, AA, m, m, m, m, gws, gws_bytes, st, "muon_ns5 A A");
+    if (rc != CONCORD_OK) return rc;
+    hipLaunchKernelGGL(ns5_axpby_kernel, dim3((unsigned)cdiv(cdiv(m * m, 4), 256)), dim3(256), 0, st, A, AA,
+                       m * m, b, c);
+    rc = gemm_bf16_run(MODE_DGRAD_BF16, A, m, X, n, BX, n, m, n, m, gws, gws_bytes, st, "muon_ns5 B X");
+    if (rc != CONCORD_OK) return rc;
+    hipLaunchKernelGGL(ns5_axpby_kernel, dim3((unsigned)cdiv(cdiv(m * n, 4), 256)), dim3(256), 0, st, X, BX,
+                       m * n, a, 1.0f);
+  }
+  // out[N][K] = bf16(gamma X) (X^T when transposed)
+  const dim3 go((unsigned)cdiv(K, 64), (unsigned)cdiv(N, 64));
+  if (tr)
+    hipLaunchKernelGGL((ns5_copy_kernel<true, false>), go, dim3(256), 0, st, X, n, out, ld_out, N, K, den, gamma);
+  else
+    hipLaunchKernelGGL((ns5_copy_kernel<false, false>), go, dim3(256), 0, st, X, n, out, ld_out, N, K, den, gamma);
+  return launch_status("muon_ns5");
+}

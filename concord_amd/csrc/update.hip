@@ -15,6 +15,17 @@
 
 namespace concord {
 
+// v-hat enters the update through the trust-region denominator (not under
+// the Muon drive, whose step is the supplied drive) and through the
+// non-fixed coherence gate; otherwise v_row / v_col / sum_v_inv are not read
+// (docs/MUON_IMPLEMENTATION.md:75-80: the Muon path needs no v-hat).
+__host__ __device__ inline bool update_needs_vhat(uint32_t flags) {
+  const bool denom = (flags & CONCORD_GF_TRUST_REGION) && !(flags & CONCORD_MUON);
+  const bool gate = !(flags & CONCORD_FIXED_COH) &&
+                    (flags & (CONCORD_GF_CONSOLIDATION | CONCORD_COHPRE | CONCORD_RATIO_COH));
+  return denom || gate;
+}
+
 struct AdamwArgs {
   int32_t* packed;
   const uint16_t* grad;
@@ -353,8 +364,7 @@ __global__ __launch_bounds__(256) void apply_adamw_kernel(AdamwArgs a) {
   U.cons = (proto && a.s.consolidate) ? *a.s.consolidate : 1;
   U.consf = (float)U.cons;
   U.salt = *a.s.salt_counter;
-  const bool need_vhat = flags & (CONCORD_GF_TRUST_REGION | CONCORD_GF_CONSOLIDATION |
-                                  CONCORD_COHPRE | CONCORD_RATIO_COH);
+  const bool need_vhat = update_needs_vhat(flags);
   U.svi = need_vhat ? *a.sum_v_inv : 0.0f;
   const bool track = (flags & CONCORD_TRACK_REBALANCE) && U.cons == 1;
   const bool emit = (flags & CONCORD_EMIT_WEIGHT) && U.cons == 1;
@@ -577,8 +587,7 @@ extern "C" int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t
   CONCORD_CHECK(ld_p >= K && ld_g >= K, "concord_apply_adamw: leading dimension < K");
   CONCORD_CHECK(scalars->lr && scalars->eps && scalars->salt_counter,
                 "concord_apply_adamw: lr/eps/salt_counter NULL");
-  const bool need_vhat = flags & (CONCORD_GF_TRUST_REGION | CONCORD_GF_CONSOLIDATION |
-                                  CONCORD_COHPRE | CONCORD_RATIO_COH);
+  const bool need_vhat = update_needs_vhat(flags);
   CONCORD_CHECK(!need_vhat || (v_row && v_col && sum_v_inv),
                 "concord_apply_adamw: gf_trust/gf_consol/coh_pre/ratio_coh need v_row, v_col, sum_v_inv");
   CONCORD_CHECK(!(flags & CONCORD_RATIO_COH) || (scalars->chase_floor && scalars->leak_floor),

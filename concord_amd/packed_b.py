@@ -345,7 +345,10 @@ def apply_packed_adamw(packed_w, grad_W, weight_buf, row_exp, col_exp, row_max, 
     N, K = _check_packed(packed_w, row_exp, col_exp)
     assert grad_W.dtype == torch.bfloat16 and tuple(grad_W.shape) == (N, K) and grad_W.stride(1) == 1
     dev = packed_w.device
-    use_vhat = gf_trust_delta_sq > 0 or gf_consol > 0 or coh_pre is not None or _RATIO_COH
+    # v-hat feeds the trust-region denominator (not under the Muon drive) and
+    # the non-fixed coherence gate (docs/MUON_IMPLEMENTATION.md:75-80)
+    use_vhat = ((gf_trust_delta_sq > 0 and not drive_muon)
+                or (not _USE_FIXED_COH and (gf_consol > 0 or coh_pre is not None or _RATIO_COH)))
     if use_vhat:
         assert v_row is not None and v_col is not None and sum_v_inv is not None, \
             "gf_trust/gf_consol/coh_pre/ratio_coh require v_row, v_col, sum_v_inv"
@@ -526,6 +529,32 @@ def _wgrad_vhat(dy, x2, v_row, v_col, sum_v_inv, beta2, row_max, col_max, salt_c
     return gw
 
 
+_MUON_WORKSPACES = {}
+
+
+def muon_ns5(grad_W, out=None, gamma=None):
+    """The Muon drive O = bf16(gamma NS5(grad_W / ||grad_W||_F)), gamma =
+    sqrt(max(N, K)) (experiments/cpu_dynamics/exp9_muon.py:44-55, 58-100;
+    docs/MUON_IMPLEMENTATION.md:27-40)."""
+    C.require_device_tensor(grad_W, "grad_W")
+    assert grad_W.dtype == torch.bfloat16 and grad_W.dim() == 2 and grad_W.stride(1) == 1
+    N, K = grad_W.shape
+    if gamma is None:
+        gamma = math.sqrt(max(N, K))
+    if out is None:
+        out = torch.empty((N, K), dtype=torch.bfloat16, device=grad_W.device)
+    key = _dev_key(grad_W.device)
+    need = int(C.lib().concord_muon_workspace_bytes(N, K))
+    ws = _MUON_WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=key)
+        _MUON_WORKSPACES[key] = ws
+    C.check(C.lib().concord_muon_ns5(C.ptr(grad_W), grad_W.stride(0), N, K, float(gamma), C.ptr(out),
+                                     out.stride(0), C.ptr(ws), ws.numel(),
+                                     C.stream_of(grad_W.device)), "muon_ns5")
+    return out
+
+
 def _bias_grad(dy):
     M, N = dy.shape
     need = int(C.lib().concord_workspace_bytes(N, 1, M))
@@ -552,7 +581,11 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
                 weight_buf, row_max_buf, col_max_buf,
                 v_row, v_col, sum_v_inv,
                 adafactor_beta2, track_adafactor_v,
-                gf_trust_delta_sq, coh_pre):
+                gf_trust_delta_sq, coh_pre, *extra):
+        # extra[0] (optional): the drive, 'vhat' (the reference's) or 'muon'
+        # (docs/MUON_IMPLEMENTATION.md:56-67)
+        ctx.n_extra = len(extra)
+        ctx.drive = extra[0] if extra else 'vhat'
         K = packed_w.shape[1]
         lead = x.shape[:-1]
         x2 = x.reshape(-1, K)
@@ -596,7 +629,12 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
                              ctx.weight_buf).reshape(*ctx.lead, K)
         salt = _get_step_counter(dev)
         prebumped = False
-        if ctx.track_adafactor_v and ctx.v_row is not None:
+        muon = ctx.drive == 'muon' and ctx.optimizer_kind == 'adamw'
+        if muon:
+            # O = sqrt(max(N, K)) NS5(grad_W / ||grad_W||); no v-hat
+            # (docs/MUON_IMPLEMENTATION.md:45-67)
+            grad_W = muon_ns5(_wgrad(dy, x2))
+        elif ctx.track_adafactor_v and ctx.v_row is not None:
             # wgrad (1269-1277), watermark zeroing (1281-1283), v-hat EMA (1288-1303),
             # salt + 1 (910-911)
             grad_W = _wgrad_vhat(dy, x2, ctx.v_row, ctx.v_col, ctx.sum_v_inv, ctx.adafactor_beta2,
@@ -621,7 +659,7 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
                 mass_preserve=ctx.mass_preserve, apply_chase=ctx.apply_chase,
                 track_rebalance=ctx.track_rebalance, v_row=ctx.v_row, v_col=ctx.v_col,
                 sum_v_inv=ctx.sum_v_inv, gf_trust_delta_sq=ctx.gf_trust_delta_sq,
-                coh_pre=ctx.coh_pre, salt_prebumped=prebumped)
+                coh_pre=ctx.coh_pre, salt_prebumped=prebumped, drive_muon=muon)
         else:
             apply_packed_sgd(
                 ctx.packed_w, grad_W, ctx.weight_buf, ctx.row_exp, ctx.col_exp,
@@ -639,7 +677,7 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
                 None, None, None,
                 None, None, None,
                 None, None, None,
-                None, None, None, None)
+                None, None, None, None) + (None,) * ctx.n_extra
 
 
 # ---------------------------------------------------------------------------
@@ -660,7 +698,7 @@ class ConcordLinearPackedB(nn.Module):
     MAX_M = 24000
 
     def __init__(self, in_features, out_features, bias=True, device='cuda', alpha=0.1,
-                 beta1=0.0, lr=0.01, weight_cache=False):
+                 beta1=0.0, lr=0.01, weight_cache=False, drive='vhat'):
         super().__init__()
         device = torch.device(device)
         if device.type != 'cuda':
@@ -673,6 +711,7 @@ class ConcordLinearPackedB(nn.Module):
         self.alpha = alpha
         self.beta1 = beta1
         self.weight_cache = bool(weight_cache)
+        self.set_drive(drive)
         self._lr_value = float(lr)
         self.optimizer_kind = 'adamw'
         self.weight_decay = 0.0
@@ -763,6 +802,14 @@ class ConcordLinearPackedB(nn.Module):
     @torch.no_grad()
     def disable_cohpre(self):
         self._coh_pre = None
+
+    def set_drive(self, drive):
+        """'vhat' (default: clip(g / sqrt(v-hat + eps))) or 'muon' (the step is
+        sqrt(max(N, K)) NS5(grad / ||grad||); no v-hat, eps or cap), after
+        docs/MUON_IMPLEMENTATION.md:56-67."""
+        if drive not in ('vhat', 'muon'):
+            raise ValueError("drive must be 'vhat' or 'muon'")
+        self.drive = drive
 
     def set_optimizer_kind(self, kind, weight_decay=0.0, eps=1.0, step_cap=10.0):
         if kind not in ('sgd', 'adamw'):
@@ -894,7 +941,7 @@ class ConcordLinearPackedB(nn.Module):
             wbuf, rmbuf, cmbuf,
             self.v_row, self.v_col, self._sum_v_inv,
             float(self.adafactor_beta2), bool(self.track_adafactor_v),
-            float(self.gf_trust_delta_sq), self._coh_pre)
+            float(self.gf_trust_delta_sq), self._coh_pre, self.drive)
         return y.to(in_dtype)
 
     @torch.no_grad()

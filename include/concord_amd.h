@@ -193,6 +193,18 @@ int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int
                        size_t workspace_bytes, void* gemm_workspace, size_t gemm_workspace_bytes,
                        void* stream);
 
+/* Muon drive (A13): out[N,K] = bf16(gamma * NS5(g / ||g||_F)), the quintic
+ * Newton-Schulz orthogonalisation of experiments/cpu_dynamics/exp9_muon.py:44-55
+ * used as the drive of MuonConcord.step (58-100; gamma = sqrt(max(N, K))) and
+ * specified for the packed layer in docs/MUON_IMPLEMENTATION.md:27-40, 87-119.
+ * bf16 iterates and products with fp32 accumulation; the result is the step
+ * the update takes under CONCORD_MUON.  workspace:
+ * concord_muon_workspace_bytes(N, K) bytes, zero-filled once when allocated. */
+size_t concord_muon_workspace_bytes(int64_t N, int64_t K);
+int concord_muon_ns5(const uint16_t* g, int64_t ld_g, int64_t N, int64_t K, float gamma,
+                     uint16_t* out, int64_t ld_out, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
 /* The forward and dgrad products over a materialised bf16 weight w[N,K]: the
  * reference's cached weight_buf path, F.linear(x, weight_buf, bias) and
  * grad_y @ weight_buf (concord/packed_b.py:1219, 1263). */

@@ -248,8 +248,12 @@ void oracle_apply_adamw(int32_t* packed, const uint16_t* grad_bf16,
     const float consf = (float)cons;
     const float lr = S->lr, eps = S->eps;
     const int32_t salt = S->salt;
-    const int need_vhat = (flags & (OR_GF_TRUST_REGION | OR_GF_CONSOLIDATION |
-                                    OR_COHPRE | OR_RATIO_COH)) != 0;
+    /* v-hat only feeds the trust-region denominator (not under the Muon
+     * drive) and the non-fixed coherence gate; otherwise it is not read
+     * (docs/MUON_IMPLEMENTATION.md:75-80) and v_row / v_col may be NULL */
+    const int need_vhat = ((flags & OR_GF_TRUST_REGION) && !(flags & OR_MUON)) ||
+                          (!(flags & OR_FIXED_COH) &&
+                           (flags & (OR_GF_CONSOLIDATION | OR_COHPRE | OR_RATIO_COH)));
     const int need_coh = (flags & (OR_GF_CONSOLIDATION | OR_COHPRE | OR_RATIO_COH)) != 0;
     const int track = (flags & OR_TRACK_REBALANCE) != 0 && cons == 1;
     const int emit = (flags & OR_EMIT_WEIGHT) != 0 && cons == 1;
@@ -630,6 +634,89 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
     *sum_v_inv = 1.0f / sv;
     free(pr);
     free(pc);
+}
+
+/* ---- A13 Muon drive: experiments/cpu_dynamics/exp9_muon.py:44-55 (ns5),
+ * 58-100 (MuonConcord.step: drive = sqrt(max(N,K)) * ns5(g / ||g||));
+ * docs/MUON_IMPLEMENTATION.md:27-40 (bf16 NS, O fed to the apply as the step).
+ * This build's numerics (the GPU path follows them):
+ *   ||g||^2: the row-major flattening of g cut into blocks of 8192 elements;
+ *     in a block, lane t (0..255) sums elements t, t+256, ... (32 of them)
+ *     ascending from 0.0f, then the halving tree over the 256 lane sums;
+ *     block totals ascending from 0.0f.  norm = sqrtf(sum).
+ *   X0 = bf16(g / (norm + 1e-7)), transposed when N > K so X is m x n, m <= n.
+ *   per iteration (a, b, c = 3.4445, -4.7750, 2.0315):
+ *     A = bf16(X X^T), AA = bf16(A A), B = bf16(b A + c AA), BX = bf16(B X),
+ *     X = bf16(a X + BX); the products accumulate in fp32 over ascending r.
+ *   out = bf16(gamma * X), transposed back to N x K.
+ * The GPU's products accumulate in MFMA order, so GPU and oracle agree to the
+ * bf16 rounding of the products, not bit for bit; the norm and X0 are exact. */
+float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K) {
+    const int64_t total = N * K;
+    float acc = 0.0f;
+    for (int64_t b0 = 0; b0 < total; b0 += 8192) {
+        float part[256];
+        for (int t = 0; t < 256; ++t) {
+            float s = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                const int64_t e = b0 + t + 256 * i;
+                float v = e < total ? bf16_to_f32(g[e]) : 0.0f;
+                s = s + v * v;
+            }
+            part[t] = s;
+        }
+        for (int h = 128; h >= 1; h >>= 1)
+            for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
+        acc = acc + part[0];
+    }
+    return acc;
+}
+
+static inline float rbf(float f) { return bf16_to_f32(oracle_f32_to_bf16(f)); }
+
+/* C[I][J] = bf16(sum_r A(i,r) B(r,j)); A(i,r) = a[i*lda_i + r*lda_r], likewise B */
+static void gemm_bf16(const float* a, int64_t lai, int64_t lar, const float* b, int64_t lbr, int64_t lbj,
+                      float* c, int64_t I, int64_t J, int64_t R) {
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < I; ++i)
+        for (int64_t j = 0; j < J; ++j) {
+            float s = 0.0f;
+            for (int64_t r = 0; r < R; ++r) s = s + a[i * lai + r * lar] * b[r * lbr + j * lbj];
+            c[i * J + j] = rbf(s);
+        }
+}
+
+void oracle_muon_ns5(const uint16_t* g, int64_t N, int64_t K, float gamma, uint16_t* out) {
+    const float na = 3.4445f, nb = -4.7750f, nc = 2.0315f;
+    const int tr = N > K;
+    const int64_t m = tr ? K : N, n = tr ? N : K;
+    const float norm = sqrtf(oracle_frob_sumsq(g, N, K));
+    const float den = norm + 1e-7f;
+    float* X = (float*)malloc((size_t)(m * n) * sizeof(float));
+    float* BX = (float*)malloc((size_t)(m * n) * sizeof(float));
+    float* A = (float*)malloc((size_t)(m * m) * sizeof(float));
+    float* AA = (float*)malloc((size_t)(m * m) * sizeof(float));
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            const float v = tr ? bf16_to_f32(g[j * K + i]) : bf16_to_f32(g[i * K + j]);
+            X[i * n + j] = rbf(v / den);
+        }
+    for (int it = 0; it < 5; ++it) {
+        gemm_bf16(X, n, 1, X, 1, n, A, m, m, n);          /* X X^T */
+        gemm_bf16(A, m, 1, A, m, 1, AA, m, m, m);         /* A A */
+        for (int64_t e = 0; e < m * m; ++e) A[e] = rbf(nb * A[e] + nc * AA[e]);   /* B */
+        gemm_bf16(A, m, 1, X, n, 1, BX, m, n, m);         /* B X */
+        for (int64_t e = 0; e < m * n; ++e) X[e] = rbf(na * X[e] + BX[e]);
+    }
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            const uint16_t v = oracle_f32_to_bf16(gamma * X[i * n + j]);
+            if (tr) out[j * K + i] = v; else out[i * K + j] = v;
+        }
+    free(X);
+    free(BX);
+    free(A);
+    free(AA);
 }
 
 /* ---- A11 load_weights / load_weights_finetune ------------------------------

@@ -106,6 +106,9 @@ void oracle_load_weights(const float* W, int64_t N, int64_t K,
                          int32_t mantissa_bias, int finetune,
                          int32_t* packed, int8_t* row_exp, int8_t* col_exp);
 
+float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K);
+void oracle_muon_ns5(const uint16_t* g, int64_t N, int64_t K, float gamma, uint16_t* out);
+
 void oracle_set_threads(int n);
 
 #ifdef __cplusplus

@@ -78,6 +78,9 @@ def lib():
         L.oracle_apply_sgd.argtypes = [P, P, P, P, P, P, P, i64, i64, f32, i32, f32,
                                        f32, f32, i32, u32]
         L.oracle_i8_medians.argtypes = [P, i64, i64, P, P]
+        L.oracle_frob_sumsq.restype = f32
+        L.oracle_frob_sumsq.argtypes = [P, i64, i64]
+        L.oracle_muon_ns5.argtypes = [P, i64, i64, f32, P]
         L.oracle_rebalance.argtypes = [P, P, P, P, P, P, P, i64, i64, i32, i32, i32,
                                        i32, ctypes.c_int]
         L.oracle_vhat_ema.argtypes = [P, i64, i64, P, P, P, f64]
@@ -184,6 +187,22 @@ def vhat_ema(grad_bf16, v_row, v_col, beta2=0.999):
     s = np.zeros(1, np.float32)
     lib().oracle_vhat_ema(_p(grad_bf16), N, K, _p(v_row), _p(v_col), _p(s), float(beta2))
     return s[0]
+
+
+def frob_sumsq(grad_bf16):
+    g = np.ascontiguousarray(grad_bf16, dtype=np.uint16)
+    return np.float32(lib().oracle_frob_sumsq(_p(g), g.shape[0], g.shape[1]))
+
+
+def muon_ns5(grad_bf16, gamma=None):
+    """O = bf16(gamma * NS5(g / ||g||)) as bf16 bits (gamma = sqrt(max(N, K)))."""
+    g = np.ascontiguousarray(grad_bf16, dtype=np.uint16)
+    N, K = g.shape
+    if gamma is None:
+        gamma = float(np.float32(np.sqrt(np.float32(max(N, K)))))
+    out = np.zeros((N, K), np.uint16)
+    lib().oracle_muon_ns5(_p(g), N, K, float(gamma), _p(out))
+    return out
 
 
 def load_weights(W, exp_min=-8, exp_max=7, mantissa_bias=15, finetune=False):

@@ -712,3 +712,100 @@ def test_3d_input_and_fp32_dtype():
     assert y.shape == (4, 25, 48) and y.dtype == torch.float32
     y.sum().backward()
     assert x.grad.shape == x.shape and layer.bias.grad is not None
+
+
+# ---------------------------------------------------------------- Muon drive
+
+@pytest.mark.parametrize("N,K", [(96, 160), (160, 96), (256, 1024), (1024, 256), (200, 333), (1, 8)])
+def test_muon_ns5_matches_oracle(oracle, N, K):
+    """O = gamma NS5(g / ||g||) on the GPU (bf16 MFMA products) against the
+    oracle's bf16 restatement.  Tolerance 2e-2 rel-L2: the chain has 15 bf16
+    products and 10 bf16 roundings, and two restatements of the same bf16
+    method already differ by up to ~7e-3 where the accumulation order flips
+    a rounding (tests/test_oracle_math.py)."""
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(N * 3 + K)
+    g = oracle.f32_to_bf16_bits_array((rng.standard_normal((N, K)) * 1e-3).astype(np.float32))
+    gamma = float(np.float32(np.sqrt(np.float32(max(N, K)))))
+    o = pb.muon_ns5(dev(g), gamma=gamma)
+    sync()
+    ref = oracle.bf16_bits_to_f32(oracle.muon_ns5(g, gamma)).astype(np.float64)
+    got = oracle.bf16_bits_to_f32(host(o)).astype(np.float64)
+    assert rel_l2(got, ref) < 2e-2
+
+
+def test_muon_ns5_full_size_properties(oracle):
+    """Config 5 shape (1280 x 5120): the drive's singular values lie in the
+    quintic's band times gamma, a power-of-two rescale of g leaves the drive
+    bit-identical, and two calls agree bit for bit (fixed reduction order)."""
+    from concord_amd import packed_b as pb
+    N, K = 1280, 5120
+    g = torch.randn(N, K, generator=torch.Generator().manual_seed(3)) * 1e-3
+    gd = g.to(torch.bfloat16).to(DEV)
+    o1 = pb.muon_ns5(gd)
+    o2 = pb.muon_ns5(gd)
+    o4 = pb.muon_ns5((gd.float() * 4.0).to(torch.bfloat16))
+    sync()
+    a1 = host(o1)
+    np.testing.assert_array_equal(a1, host(o2))
+    np.testing.assert_array_equal(a1, host(o4))
+    X = oracle.bf16_bits_to_f32(a1).astype(np.float64) / np.sqrt(K)
+    ev = np.linalg.eigvalsh(X @ X.T)
+    sv = np.sqrt(np.clip(ev, 0, None))
+    assert sv.min() > 0.6 and sv.max() < 1.25, (sv.min(), sv.max())
+
+
+def test_layer_muon_drive_bit_exact(oracle):
+    """drive='muon': the backward feeds O = sqrt(max(N,K)) NS5(grad_W) to the
+    update as its step (CONCORD_MUON: no v-hat, eps or cap); packed words and
+    exponents bit-exact vs the oracle's update fed the same O."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    O = oracle
+    N, K, M = 384, 256, 512
+    torch.manual_seed(1)
+    W0 = torch.nn.init.kaiming_uniform_(torch.empty(N, K), a=5 ** 0.5)
+    x = torch.randn(M, K)
+    gy = torch.randn(M, N) * 1e-2
+    layer = ca.ConcordLinearPackedB(K, N, bias=False, device=DEV, lr=1e-3, drive='muon')
+    pb.set_ratio_coh(True)
+    pb.set_ratio_coh_floors(0.9, 0.999)
+    try:
+        layer.disable_cohpre()
+        layer.gf_consol = 10.0
+        layer.load_weights(W0)
+        p0, r0, c0 = O.load_weights(W0.numpy())
+        pk, re, ce = p0.copy(), r0.copy(), c0.copy()
+        flags = (O.MASS_PRESERVE | O.APPLY_CHASE | O.TRACK_REBALANCE | O.GF_TRUST_REGION | O.FIXED_COH
+                 | O.RATIO_COH | O.GF_CONSOLIDATION | O.MUON)
+        for step in range(3):
+            salt_next = int(host(pb._get_step_counter(DEV))[0]) + 1
+            cap = []
+            pb._DEBUG_CAPTURE = cap
+            try:
+                y = layer(x.to(DEV).requires_grad_(True))
+                y.backward(gy.to(DEV))
+            finally:
+                pb._DEBUG_CAPTURE = None
+            layer.rebalance()
+            sync()
+            drive = host(cap[0])
+            rm = np.zeros(N, np.int32)
+            cm = np.zeros(K, np.int32)
+            P = O.UpdateParams(alpha=0.1, beta1=0.0, weight_decay=0.0, step_cap=10.0, v_scale=0.0,
+                               precond_p=0.5, gf_consol=10.0, drift_cancel_C=0.018036072144288578,
+                               alpha_v_fast=0.001, wd_sv=0.0, wd_sf=0.0, gf_trust_delta_sq=1.0,
+                               gate_gain=1.0, mantissa_bias=15)
+            S = O.UpdateScalars(lr=1e-3, eps=1e-10, chase_floor=0.9, leak_floor=0.999, v_bc=1.0,
+                                salt=salt_next, consolidate=1)
+            z = np.zeros(1, np.float32)
+            O.apply_adamw(pk, drive, None, re, ce, rm, cm, np.zeros(N, np.float32), np.zeros(K, np.float32),
+                          z[0], None, P, S, flags)
+            O.rebalance(pk, re, ce, rm, cm, seed=step + 1)
+            np.testing.assert_array_equal(host(layer.packed_w), pk)
+            np.testing.assert_array_equal(host(layer.row_exp), re)
+            # the drive is the NS5 of this step's gradient: unit-RMS scale, gamma-sized
+            dv = O.bf16_bits_to_f32(drive).astype(np.float64)
+            assert 0.4 < np.sqrt((dv * dv).mean()) < 1.2
+    finally:
+        pb.set_ratio_coh(False)

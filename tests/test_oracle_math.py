@@ -452,3 +452,96 @@ def test_load_weights_edges(oracle):
     assert re[4] == -8 and (sf[4] == 320).all()
     # round half to even: row 5 max 0.75 -> exp 1 -> scale 2^-14; W = 0.75 -> 12288
     assert re[5] == 1 and sf[5, 1] == -12288
+
+
+# ------------------------------------------------------------ Muon NS5 drive
+
+
+def _ns5_float64(G):
+    """experiments/cpu_dynamics/exp9_muon.py:44-55 in float64 (no bf16 rounding)."""
+    a, b, c = 3.4445, -4.7750, 2.0315
+    X = G / (np.linalg.norm(G) + 1e-7)
+    tr = X.shape[0] > X.shape[1]
+    if tr:
+        X = X.T
+    for _ in range(5):
+        A = X @ X.T
+        B = b * A + c * (A @ A)
+        X = a * X + B @ X
+    return X.T if tr else X
+
+
+def test_frob_sumsq(oracle):
+    rng = np.random.default_rng(21)
+    g = oracle.f32_to_bf16_bits_array((rng.standard_normal((70, 300)) * 1e-2).astype(np.float32))
+    gd = oracle.bf16_bits_to_f32(g).astype(np.float64)
+    assert abs(oracle.frob_sumsq(g) - (gd * gd).sum()) <= 1e-6 * (gd * gd).sum()
+    # dyadic: exact whatever the order
+    d = oracle.f32_to_bf16_bits_array(np.full((33, 500), -2.0 ** -5, np.float32))
+    assert oracle.frob_sumsq(d) == np.float32(33 * 500 * 2.0 ** -10)
+
+
+def _ns5_bf16_numpy(oracle, G, gamma):
+    """The same bf16 rounding points as the oracle, written independently in
+    numpy (float64 products, float32 elementwise)."""
+    def rb(x):
+        return oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits_array(np.asarray(x, np.float32))).astype(np.float64)
+    a, b, c = np.float32(3.4445), np.float32(-4.7750), np.float32(2.0315)
+    norm = np.float32(np.sqrt(np.float32((G * G).sum())))
+    X = rb(G.astype(np.float32) / (norm + np.float32(1e-7)))
+    tr = X.shape[0] > X.shape[1]
+    if tr:
+        X = X.T.copy()
+    for _ in range(5):
+        A = rb(X @ X.T)
+        AA = rb(A @ A)
+        B = rb(b * A.astype(np.float32) + c * AA.astype(np.float32))
+        X = rb(a * X.astype(np.float32) + rb(B @ X).astype(np.float32))
+    out = rb(np.float32(gamma) * X.astype(np.float32))
+    return out.T if tr else out
+
+
+@pytest.mark.parametrize("N,K", [(96, 160), (160, 96), (128, 128), (40, 300)])
+def test_ns5_matches_independent_iterations(oracle, N, K):
+    """The oracle's bf16 NS5 against (1) the same rounding points restated in
+    numpy, to the products' accumulation order, and (2) the reference
+    iteration in float64, to the bf16 NS5's own error (~2%).  A wrong
+    coefficient, sign, operand order or missing transpose fails both."""
+    rng = np.random.default_rng(N * 7 + K)
+    g = oracle.f32_to_bf16_bits_array((rng.standard_normal((N, K)) * 1e-3).astype(np.float32))
+    gd = oracle.bf16_bits_to_f32(g).astype(np.float64)
+    gamma = np.float32(np.sqrt(np.float32(max(N, K))))
+    got = oracle.bf16_bits_to_f32(oracle.muon_ns5(g, gamma)).astype(np.float64)
+    em = _ns5_bf16_numpy(oracle, gd, gamma)
+    # two restatements of one bf16 method differ only where a product's
+    # accumulation order flips a bf16 rounding; five iterations amplify
+    # such flips to ~7e-3 at most here
+    assert np.linalg.norm(got - em) / np.linalg.norm(em) < 1.5e-2
+    ref = gamma * _ns5_float64(gd)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 4e-2
+
+
+def test_ns5_singular_values_in_quintic_band(oracle):
+    """NS5 with the Muon quintic maps every singular value of a full-rank
+    input into roughly [0.68, 1.14] (semi-orthogonal up to that band);
+    the spectral norm of the drive is then ~gamma."""
+    rng = np.random.default_rng(5)
+    for N, K in [(64, 256), (256, 64)]:
+        g = oracle.f32_to_bf16_bits_array(rng.standard_normal((N, K)).astype(np.float32))
+        gamma = np.sqrt(max(N, K))
+        X = oracle.bf16_bits_to_f32(oracle.muon_ns5(g, gamma)).astype(np.float64) / gamma
+        sv = np.linalg.svd(X, compute_uv=False)
+        assert sv.min() > 0.6 and sv.max() < 1.25, (sv.min(), sv.max())
+
+
+def test_ns5_transpose_and_scale(oracle):
+    rng = np.random.default_rng(8)
+    g = rng.standard_normal((48, 200)).astype(np.float32) * 1e-3
+    gb = oracle.f32_to_bf16_bits_array(g)
+    gt = oracle.f32_to_bf16_bits_array(np.ascontiguousarray(g.T))
+    o = oracle.bf16_bits_to_f32(oracle.muon_ns5(gb, 1.0)).astype(np.float64)
+    ot = oracle.bf16_bits_to_f32(oracle.muon_ns5(gt, 1.0)).astype(np.float64)
+    assert np.linalg.norm(o - ot.T) / np.linalg.norm(o) < 1e-2
+    # a power-of-two scale of g changes nothing but the norm's exponent
+    g4 = oracle.f32_to_bf16_bits_array(g * 4.0)
+    np.testing.assert_array_equal(oracle.muon_ns5(g4, 1.0), oracle.muon_ns5(gb, 1.0))
