@@ -32,6 +32,7 @@ struct GemmArgs {
   int vec_a, vec_b, vec_c;  // base pointers and leading dimensions allow 16 B / 8 B accesses
   float* vh_pr;           // WGRAD with v-hat partials: row / column partial sums of g^2
   float* vh_pc;
+  float* bpart;           // WGRAD with v-hat partials: bias-gradient partials [tiles_j][I], or NULL
 };
 
 // XCD-aware tile order: workgroup w runs on XCD w % 8.  XCD x owns tile
@@ -61,7 +62,10 @@ int gemm_fast_launch(int mode, const GemmArgs& g, void* workspace, size_t ws_byt
 // does not run the transpose-read kernel, or when the plan given split_room
 // bytes of split-K workspace would split it (the caller then runs the plain
 // WGRAD and the separate partials kernel)
-int gemm_wgrad_vhat_launch(const GemmArgs& g, size_t split_room, hipStream_t st, const char* what);
+int gemm_wgrad_vhat_launch(const GemmArgs& g, size_t split_room, hipStream_t st, const char* what,
+                           int* tiles_j);
+// tiles along J of the WGRAD launch above (the bias partials' row count)
+int64_t gemm_wgrad_vhat_tiles_j(int64_t J);
 // a plain bf16 product through the fast or generic kernels: MODE_FWD_BF16
 // (C[I][J] = sum_r a[i][r] b[j][r]) or MODE_DGRAD_BF16 (sum_r a[i][r] b[r][j])
 int gemm_bf16_run(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,

@@ -562,12 +562,12 @@ extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint1
                                   uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
                                   double beta2, float* v_row, float* v_col, float* sum_v_inv,
                                   int32_t* row_max, int32_t* col_max, int32_t* salt_counter,
-                                  void* workspace, size_t workspace_bytes, void* gemm_workspace,
-                                  size_t gemm_workspace_bytes, void* stream) {
+                                  uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
+                                  void* gemm_workspace, size_t gemm_workspace_bytes, void* stream) {
   CONCORD_CHECK(sizes_ok(M, N, K) && N > 0 && K > 0, "concord_wgrad_vhat: bad size");
   CONCORD_CHECK(dy && x && grad_w && v_row && v_col && sum_v_inv, "concord_wgrad_vhat: NULL argument");
   CONCORD_CHECK(ld_dy >= N && ld_x >= K && ld_gw >= K, "concord_wgrad_vhat: bad leading dimension");
-  const Workspace ws = workspace_layout(N, K, 0);
+  const Workspace ws = workspace_layout(N, K, grad_bias ? M : 0);
   if (!workspace || workspace_bytes < ws.total) {
     set_error("concord_wgrad_vhat: workspace of %zu bytes needed", ws.total);
     return CONCORD_EWORKSPACE;
@@ -576,19 +576,27 @@ extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint1
   float* pr = (float*)((char*)workspace + ws.scratch);
   float* pc = pr + v.pr;
   float* bsum = pc + v.pc;
+  float* bpart = bsum + v.bsum;
   hipStream_t st = (hipStream_t)stream;
   GemmArgs g = make_args(dy, x, ld_dy, ld_x, nullptr, nullptr, 0, nullptr, grad_w, ld_gw, N, K, M, false);
   g.vh_pr = pr;
   g.vh_pc = pc;
-  int rc = gemm_wgrad_vhat_launch(g, gemm_workspace ? gemm_workspace_bytes : 0, st, "wgrad_vhat");
-  if (rc == -1) {   // split or unaligned WGRAD: the plain product, then the partials kernel
+  g.bpart = grad_bias ? bpart : nullptr;
+  int tiles_j = 0;
+  int rc = gemm_wgrad_vhat_launch(g, gemm_workspace ? gemm_workspace_bytes : 0, st, "wgrad_vhat", &tiles_j);
+  if (rc == -1) {   // split or unaligned WGRAD: the plain product, then the partials kernels
+    g.bpart = nullptr;
     rc = launch_gemm<MODE_WGRAD>(g, gemm_workspace, gemm_workspace_bytes, st, "wgrad");
     if (rc != CONCORD_OK) return rc;
     vhat_partials_launch(grad_w, ld_gw, N, K, pr, pc, st);
+    if (grad_bias) bias_grad_launch(dy, ld_dy, M, N, grad_bias, bpart, st);
+    vhat_finish_launch(pr, pc, bsum, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter, st);
   } else if (rc != CONCORD_OK) {
     return rc;
+  } else {
+    vhat_finish_launch(pr, pc, bsum, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter, st,
+                       bpart, tiles_j, grad_bias);
   }
-  vhat_finish_launch(pr, pc, bsum, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter, st);
   return launch_status("wgrad_vhat");
 }
 

@@ -23,6 +23,7 @@
 //  * split-K over S ways is deterministic: the last block of a tile to finish
 //    sums the S fp32 partials in split order.
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 
 #include "gemm.h"
@@ -1050,8 +1051,23 @@ CONCORD_DEV void mfma_block(f32x4 (&acc)[NI][NJ], const bf16x8 (&fa)[NI], const 
 // Per stage: fragments of the second half-stage are read while the first
 // half-stage's MFMAs issue, then (after the barrier) the next stage's first
 // half is read while the second half's MFMAs issue.
+// bias-gradient partial of one wave: for each of its i-fragments, the sum of
+// the 8 r-values this lane holds, added in ascending r
+template <int NI>
+CONCORD_DEV void bias_acc(float (&b)[NI], const bf16x8 (&fa)[NI]) {
+#pragma unroll
+  for (int x = 0; x < NI; ++x)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b[x] = __fadd_rn(b[x], (float)fa[x][e]);
+}
+
 // VH: also write the v-hat partials of the bf16-rounded output (64 x 64 wave
-// tiles, vhat_tile.h order); only without split-K.
+// tiles, vhat_tile.h order); only without split-K.  With g.bpart set, the
+// waves wj = 0 of block (bi, bj) also sum the A operand over the stages
+// s = bj, bj + tiles_j, ...: lane (p, q) chains its r = 8 q .. 8 q + 7
+// (mod 32) values of column p in ascending r, the four q are then added as
+// (q0 + q1) + (q2 + q3), and the fp32 result is bpart[bj][i]; the bias
+// gradient is the sum of the partials over bj ascending (vhat_finalize).
 template <int BI, int BJ, int WI, int WJ, bool VH>
 __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
   constexpr int NW = WI * WJ, NT = 64 * NW, WTI = BI / WI, WTJ = BJ / WJ;
@@ -1107,6 +1123,10 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PERT));   // own stage-0 DMA landed
   lds_barrier();
   bf16x8 fa0[NI], fb0[NJ], fa1[NI], fb1[NJ];
+  const bool bg = VH && g.bpart != nullptr && wj == 0;   // uniform per wave
+  float bsum[NI];
+#pragma unroll
+  for (int x = 0; x < NI; ++x) bsum[x] = 0.0f;
   tr_frags<NI, DA::ROWB>(fa0, ring_p, la, fsw, cwa, 0);
   tr_frags<NJ, DB::ROWB>(fb0, ring_p, lb, fsw, cwb, 0);
   for (int s = 0; s < nst; ++s) {
@@ -1114,6 +1134,8 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
     tr_frags<NI, DA::ROWB>(fa1, cur, la, fsw, cwa, 1);
     tr_frags<NJ, DB::ROWB>(fb1, cur, lb, fsw, cwb, 1);
     mfma_block<NI, NJ>(acc, fa0, fb0);
+    const bool bgs = bg && (s % g.tiles_j) == bj;
+    if (bgs) bias_acc<NI>(bsum, fa0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(PERT));     // own stage s+1 DMA landed
     lds_barrier();                                    // stage s fully read by every wave
     dma_stage(s + 3);
@@ -1122,6 +1144,16 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
     tr_frags<NI, DA::ROWB>(fa0, nxt, la, fsw, cwa, 0);
     tr_frags<NJ, DB::ROWB>(fb0, nxt, lb, fsw, cwb, 0);
     mfma_block<NI, NJ>(acc, fa1, fb1);
+    if (bgs) bias_acc<NI>(bsum, fa1);
+  }
+  if (bg) {
+#pragma unroll
+    for (int x = 0; x < NI; ++x) {
+      const float h = __fadd_rn(bsum[x], __shfl_xor(bsum[x], 16, 64));
+      const float tot = __fadd_rn(h, __shfl_xor(h, 32, 64));
+      const int64_t i = i0 + wi * WTI + 16 * x + (lane & 15);
+      if (lane < 16 && i < g.I) g.bpart[(int64_t)bj * g.I + i] = tot;
+    }
   }
   // no DMA may still be writing LDS when the ring is reused for the output
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
@@ -1144,6 +1176,166 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
   }
   epilogue<MODE_WGRAD, NI, NJ, BI, BJ, NW>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, wave, t, NT,
                                            ring);
+}
+
+// ---- DGRAD with a row-major weight tile and transpose reads -------------------
+// DGRAD's weight operand W[n][k] is r-major (r = n).  The producer waves load
+// two full rows of the tile per wave instruction (lane: 4 consecutive columns
+// of one row), decode them with their row's exponent and write bf16 rows into
+// a row-major [r][col] tile (ds_write_b64, the 32-byte windows swizzled as in
+// TrDma); the compute waves read the MFMA fragments with ds_read_b64_tr_b16.
+// Thread t: columns 4 (t % (COLS / 4)), rows 8 (t / (COLS / 4)) .. + 7.
+template <int COLS, int NT, bool PACKED>
+struct TrRowsB {
+  static constexpr int CG = COLS / 4, RG = NT / CG;
+  static_assert(CG * RG == NT && 8 * RG == TR, "one 8-row group per thread covers the stage");
+  static constexpr int ROWB = COLS * 2;
+  static constexpr int LBYTES = TR * ROWB;   // bytes of one LDS stage tile
+  typedef typename std::conditional<PACKED, i32x4, i32x2>::type Chunk;
+  struct Raw { Chunk v[8]; i32x2 ex; };
+  uint32_t voff;   // row 8 rg, this thread's 4 columns (kOOB past the last column)
+  uint32_t ldb;    // row stride in bytes
+  int32_t rg, col;
+  Rsrc rs, es;
+  CONCORD_DEV void init(const void* band, int64_t ld, int64_t cols_left, int64_t R, const int8_t* exps, int t) {
+    constexpr int ES = PACKED ? 4 : 2;
+    col = 4 * (t % CG);
+    rg = t / CG;
+    ldb = (uint32_t)(ld * ES);
+    rs = make_rsrc(band, (uint32_t)(((R - 1) * ld + cols_left) * ES));
+    if (PACKED) es = make_rsrc(exps, (uint32_t)R);
+    voff = col < cols_left ? (uint32_t)((8 * rg * ld + col) * ES) : kOOB;
+  }
+  CONCORD_DEV void load(Raw& r, int64_t r0, int64_t rem) const {
+    const uint32_t so = (uint32_t)(r0 * (int64_t)ldb);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t o = 8 * rg + e < rem ? voff + e * ldb : kOOB;
+      if constexpr (PACKED) r.v[e] = ld128(rs, o, so);
+      else r.v[e] = ld64(rs, o, so);
+    }
+    // the 8 rows' exponents (R % 8 == 0: the 8 bytes are all in range or all out)
+    if constexpr (PACKED) r.ex = ld64(es, 8 * rg < rem ? (uint32_t)(8 * rg) : kOOB, (uint32_t)r0);
+  }
+  // tile = LDS byte address of the stage tile
+  CONCORD_DEV void store(Raw& r, char* tile) const {
+    if constexpr (PACKED) pin(r.ex);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pin(r.v[e]);
+    const int cw = col / 16, cb = 2 * (col % 16);   // 32-byte window, byte in window
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int row = 8 * rg + e;
+      i32x2 o;
+      if constexpr (PACKED) {
+        const uint32_t M = magic(sbyte(r.ex[e / 4], e % 4));
+        o[0] = (int32_t)pack_bf16x2(dec(r.v[e][0], M), dec(r.v[e][1], M));
+        o[1] = (int32_t)pack_bf16x2(dec(r.v[e][2], M), dec(r.v[e][3], M));
+      } else {
+        o = r.v[e];
+      }
+      *reinterpret_cast<i32x2*>(tile + row * ROWB + ((cw ^ trf(row)) * 32) + cb) = o;
+    }
+  }
+};
+
+// MFMAs of one stage: A from a swizzled DMA tile (ds_read_b128), B from a
+// row-major tile by transpose reads.
+template <int NI, int NJ, int ROWB>
+CONCORD_DEV void stage_mfma_swz_tr(f32x4 (&acc)[NI][NJ], const uint16_t* la, const lds_char* lb, int ra,
+                                   int rb, int lane) {
+  const int lrow = lane & 15;
+  const int sw = (lane & 14) >> 1;
+  const int p = lane & 15, gq = lane >> 4;
+  const uint32_t fsw = (uint32_t)(((p >> 2) | ((gq & 1) << 2)) * 32);
+  const uint32_t lbase = (uint32_t)((8 * gq + (p >> 2)) * ROWB + 8 * (p & 3));
+#pragma unroll
+  for (int kk = 0; kk < TR / 32; ++kk) {
+    const int aoff = lrow * 64 + (((kk * 4 + (lane >> 4)) ^ sw) * 8);
+    bf16x8 fa[NI], fb[NJ];
+#pragma unroll
+    for (int x = 0; x < NI; ++x)
+      fa[x] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(la + (ra + x * 16) * 64 + aoff));
+    tr_frags<NJ, ROWB>(fb, lb, lbase, fsw, rb / 16, kk);
+    mfma_block<NI, NJ>(acc, fa, fb);
+  }
+}
+
+// 8 waves: waves 0-3 compute and move A (dy) by DMA, waves 4-7 load W rows
+// two stages ahead, decode them and write the row-major B tile.
+template <int MODE, int BI, int BJ>
+__global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
+  constexpr int NP = 256;
+  constexpr int WTI = BI / 2, WTJ = BJ / 2;
+  constexpr int NI = WTI / 16, NJ = WTJ / 16;
+  typedef TrRowsB<BJ, NP, MODE == MODE_DGRAD> BL;
+  typedef RowsDma<BI, 4> AD;
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
+  __shared__ __attribute__((aligned(1024))) char lds_b[2][BL::LBYTES];
+
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  const bool producer = wave >= 4;
+  const int tiles = g.tiles_i * g.tiles_j;
+  const int wg = blockIdx.x;
+  const int split = wg / tiles;
+  int bi, bj;
+  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
+  const int64_t r_begin = (int64_t)split * g.r_split;
+  const int64_t r_end = min(g.R, r_begin + g.r_split);
+  const int nst = r_end > r_begin ? (int)((r_end - r_begin + TR - 1) / TR) : 0;
+  const int nst2 = (nst + 1) & ~1;
+
+  f32x4 acc[NI][NJ];
+#pragma unroll
+  for (int x = 0; x < NI; ++x)
+#pragma unroll
+    for (int y = 0; y < NJ; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const int wi = (wave & 3) >> 1, wj = wave & 1;
+
+  if (producer) {
+    const int tp = t - NP;
+    BL bl;
+    const int esz = MODE == MODE_DGRAD ? 4 : 2;
+    bl.init(reinterpret_cast<const char*>(g.b) + j0 * esz, g.ldb, g.J - j0, g.R, g.row_exp, tp);
+    typename BL::Raw r0, r1;
+    auto stage_r = [&](int st) { return r_begin + (int64_t)st * TR; };
+    bl.load(r0, stage_r(0), r_end - stage_r(0));
+    bl.load(r1, stage_r(1), r_end - stage_r(1));
+    bl.store(r0, lds_b[0]);
+    bl.load(r0, stage_r(2), r_end - stage_r(2));
+    lds_barrier();
+    for (int s = 0; s < nst2; s += 2) {
+      bl.store(r1, lds_b[1]);
+      bl.load(r1, stage_r(s + 3), r_end - stage_r(s + 3));
+      lds_barrier();
+      bl.store(r0, lds_b[0]);
+      bl.load(r0, stage_r(s + 4), r_end - stage_r(s + 4));
+      lds_barrier();
+    }
+  } else {
+    AD ad;
+    ad.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, wave, lane);
+    ad.load(lds_a[0], r_begin, r_end - r_begin);
+    ad.load(lds_a[1], r_begin + TR, r_end - r_begin - TR);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(AD::PER));
+    lds_barrier();
+    for (int s = 0; s < nst2; ++s) {
+      const int64_t r2 = r_begin + (int64_t)(s + 2) * TR;
+      ad.load(lds_a[(s + 2) % 3], r2, r_end - r2);
+      if (s < nst)
+        stage_mfma_swz_tr<NI, NJ, BL::ROWB>(acc, lds_a[s % 3], (const lds_char*)lds_b[s & 1], wi * WTI,
+                                             wj * WTJ, lane);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(AD::PER));
+      lds_barrier();
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  }
+
+  static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
+  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, producer ? -1 : wave,
+                                     t, 512, &lds_a[0][0]);
 }
 
 // ---- planning -----------------------------------------------------------------
@@ -1234,6 +1426,12 @@ static void launch_reduce(const GemmArgs& g, hipStream_t st) {
 }
 
 template <int MODE, int BI, int BJ>
+static void launch_dgt(const GemmArgs& g, int blocks, hipStream_t st) {
+  hipLaunchKernelGGL((gemm_dgt_kernel<MODE, BI, BJ>), dim3(blocks), dim3(512), 0, st, g);
+  launch_reduce<MODE, BI, BJ, 2, 2>(g, st);
+}
+
+template <int MODE, int BI, int BJ>
 static void launch_dma(const GemmArgs& g, int blocks, hipStream_t st) {
   hipLaunchKernelGGL((gemm_dma_kernel<MODE, BI, BJ>), dim3(blocks), dim3(512), 0, st, g);
   launch_reduce<MODE, BI, BJ, 2, 2>(g, st);
@@ -1280,11 +1478,15 @@ size_t gemm_fast_partial_bytes(int mode, int64_t I, int64_t J, int64_t R) {
   return (size_t)p.ti * p.tj * sh.bi * sh.bj * sizeof(float) * p.splits;
 }
 
-int gemm_wgrad_vhat_launch(const GemmArgs& g0, size_t split_room, hipStream_t st, const char* what) {
+int64_t gemm_wgrad_vhat_tiles_j(int64_t J) { return cdiv(J, 128); }
+
+int gemm_wgrad_vhat_launch(const GemmArgs& g0, size_t split_room, hipStream_t st, const char* what,
+                           int* tiles_j) {
   if (!eligible(MODE_WGRAD, g0) || !tr_eligible(g0)) return -1;
   const size_t room = split_room > kSplitkCounterBytes ? split_room - kSplitkCounterBytes : 0;
   const FastPlan p = plan_mode(MODE_WGRAD, g0.I, g0.J, g0.R, room);
   if (p.shape != 0 || p.splits != 1) return -1;
+  *tiles_j = p.tj;
   GemmArgs g = g0;
   g.splits = 1;
   g.r_split = p.r_split;
@@ -1319,11 +1521,11 @@ int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
       else launch<MODE_FWD_BF16, 128, 128, 2, 2, 2>(g, blocks, st);
       break;
     case MODE_DGRAD:
-      if (p.shape == 0) launch_dma<MODE_DGRAD, 256, 128>(g, blocks, st);
+      if (p.shape == 0) launch_dgt<MODE_DGRAD, 256, 128>(g, blocks, st);
       else launch<MODE_DGRAD, 128, 128, 2, 2, 2>(g, blocks, st);
       break;
     case MODE_DGRAD_BF16:
-      if (p.shape == 0) launch_dma<MODE_DGRAD_BF16, 256, 128>(g, blocks, st);
+      if (p.shape == 0) launch_dgt<MODE_DGRAD_BF16, 256, 128>(g, blocks, st);
       else launch<MODE_DGRAD_BF16, 128, 128, 2, 2, 2>(g, blocks, st);
       break;
     case MODE_WGRAD:

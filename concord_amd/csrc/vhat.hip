@@ -53,12 +53,36 @@ __global__ __launch_bounds__(256) void vhat_partials_kernel(const uint16_t* __re
   vhat_tile_partials(g2, lane, row0, col0, N, K, pr, pc);
 }
 
+// sum of v[0], v[stride], ..., v[(count - 1) stride] ascending from 0.0f,
+// with the loads of 32 terms in flight at a time
+CONCORD_DEV float ordered_sum(const float* __restrict__ v, int64_t stride, int64_t count) {
+  float s = 0.0f;
+  int64_t b = 0;
+  for (; b + 32 <= count; b += 32) {
+    float a[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) a[e] = v[(b + e) * stride];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) s = __fadd_rn(s, a[e]);
+  }
+  if (b < count) {
+    float a[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) a[e] = b + e < count ? v[(b + e) * stride] : 0.0f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e)
+      if (b + e < count) s = __fadd_rn(s, a[e]);
+  }
+  return s;
+}
+
 // Row/column EMA and watermark zeroing.  Blocks [0, cdiv(N, 256)) take rows
 // and also leave the halving-tree total of their 256 new v_row values in
 // bsum; the remaining blocks take columns.
 __global__ __launch_bounds__(256) void vhat_finalize_kernel(
     const float* __restrict__ pr, const float* __restrict__ pc, int64_t N, int64_t K, float b2,
-    float omb2, float* v_row, float* v_col, int32_t* row_max, int32_t* col_max, float* bsum) {
+    float omb2, float* v_row, float* v_col, int32_t* row_max, int32_t* col_max, float* bsum,
+    const float* __restrict__ bpart, int64_t nbp, uint16_t* grad_bias) {
   __shared__ float s_part[256];
   const int64_t rb = cdiv(N, 256);
   const int64_t nc = cdiv(K, 64), nr = cdiv(N, 64);
@@ -66,17 +90,11 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     float vn = 0.0f;
     if (i < N) {
-      float s = 0.0f;
-      int64_t c = 0;
-      for (; c + 4 <= nc; c += 4) {   // loads issued ahead, adds in ascending c
-        const float a0 = pr[c * N + i], a1 = pr[(c + 1) * N + i];
-        const float a2 = pr[(c + 2) * N + i], a3 = pr[(c + 3) * N + i];
-        s = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(s, a0), a1), a2), a3);
-      }
-      for (; c < nc; ++c) s = __fadd_rn(s, pr[c * N + i]);
+      const float s = ordered_sum(pr + i, N, nc);
       vn = __fadd_rn(__fmul_rn(v_row[i], b2), __fmul_rn(omb2, s));
       v_row[i] = vn;
       if (row_max) row_max[i] = 0;
+      if (grad_bias) grad_bias[i] = (uint16_t)(pack_bf16x2(ordered_sum(bpart + i, N, nbp), 0.0f) & 0xFFFFu);
     }
     s_part[threadIdx.x] = vn;
     __syncthreads();
@@ -88,30 +106,28 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
   } else {
     const int64_t k = ((int64_t)blockIdx.x - rb) * 256 + threadIdx.x;
     if (k >= K) return;
-    float s = 0.0f;
-    int64_t r = 0;
-    for (; r + 8 <= nr; r += 8) {
-      float a[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) a[e] = pc[(r + e) * K + k];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s = __fadd_rn(s, a[e]);
-    }
-    for (; r < nr; ++r) s = __fadd_rn(s, pc[r * K + k]);
+    const float s = ordered_sum(pc + k, K, nr);
     v_col[k] = __fadd_rn(__fmul_rn(v_col[k], b2), __fmul_rn(omb2, s));
     if (col_max) col_max[k] = 0;
   }
 }
 
 // 1 / max(sum of the block totals ascending, 1e-30) and the salt advance.
-// A kernel of its own, so it sees every block total without a device fence.
+// One wave: the totals are loaded 64 at a time and chained in order.  A kernel
+// of its own, so it sees every block total without a device-scope fence.
 __global__ __launch_bounds__(64) void vhat_sum_kernel(const float* __restrict__ bsum, int64_t nb,
                                                       float* sum_v_inv, int32_t* salt) {
-  if (threadIdx.x != 0) return;
+  const int lane = threadIdx.x;
   float s = 0.0f;
-  for (int64_t b = 0; b < nb; ++b) s = __fadd_rn(s, bsum[b]);
-  *sum_v_inv = __fdiv_rn(1.0f, fmaxf(s, 1e-30f));
-  if (salt) salt[0] = wadd(salt[0], 1);
+  for (int64_t c0 = 0; c0 < nb; c0 += 64) {
+    const float v = c0 + lane < nb ? bsum[c0 + lane] : 0.0f;
+    const int cnt = (int)min((int64_t)64, nb - c0);
+    for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, __shfl(v, j, 64));
+  }
+  if (lane == 0) {
+    *sum_v_inv = __fdiv_rn(1.0f, fmaxf(s, 1e-30f));
+    if (salt) salt[0] = wadd(salt[0], 1);
+  }
 }
 
 void vhat_partials_launch(const uint16_t* grad, int64_t ld, int64_t N, int64_t K, float* pr, float* pc,
@@ -123,45 +139,59 @@ void vhat_partials_launch(const uint16_t* grad, int64_t ld, int64_t N, int64_t K
 
 void vhat_finish_launch(const float* pr, const float* pc, float* bsum, int64_t N, int64_t K, double beta2,
                         float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max, int32_t* col_max,
-                        int32_t* salt, hipStream_t st) {
+                        int32_t* salt, hipStream_t st, const float* bpart, int64_t nbp, uint16_t* grad_bias) {
   const float b2 = (float)beta2;
   const float omb2 = (float)(1.0 - beta2);
   const int64_t rb = cdiv(N, 256);
   hipLaunchKernelGGL(vhat_finalize_kernel, dim3((unsigned)(rb + cdiv(K, 256))), dim3(256), 0, st, pr, pc,
-                     N, K, b2, omb2, v_row, v_col, row_max, col_max, bsum);
+                     N, K, b2, omb2, v_row, v_col, row_max, col_max, bsum, bpart, nbp, grad_bias);
   hipLaunchKernelGGL(vhat_sum_kernel, dim3(1), dim3(64), 0, st, bsum, rb, sum_v_inv, salt);
 }
 
-// bias gradient: a thread sums two adjacent columns over a 256-row slab
-// (rows ascending, 8 loads in flight), then the slabs are combined in order.
+// bias gradient: a thread sums 4 adjacent columns over a slab of 64 rows
+// (rows ascending; 8-byte loads, a wave reads 512 contiguous bytes per row),
+// then the slabs are combined in order.
+constexpr int BG_ROWS = 64;
+
 __global__ __launch_bounds__(256) void colsum_partials_kernel(const uint16_t* __restrict__ dy,
                                                               int64_t ld, int64_t M, int64_t N,
                                                               float* __restrict__ part) {
-  const int64_t n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 2;
+  const int64_t n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (n >= N) return;
-  const int64_t m0 = (int64_t)blockIdx.y * 256;
-  const int64_t m1 = min(M, m0 + 256);
-  const bool pair = (n + 1 < N) && (ld % 2 == 0);
-  float s0 = 0.0f, s1 = 0.0f;
-  int64_t m = m0;
-  if (pair) {
+  const int64_t m0 = (int64_t)blockIdx.y * BG_ROWS;
+  const int64_t m1 = min(M, m0 + BG_ROWS);
+  const bool vec = (n + 4 <= N) && (ld % 4 == 0) && (((uintptr_t)dy % 8) == 0);
+  float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (vec) {
+    int64_t m = m0;
     for (; m + 8 <= m1; m += 8) {
-      uint32_t w[8];
+      uint2 w[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) w[e] = *reinterpret_cast<const uint32_t*>(dy + (m + e) * ld + n);
+      for (int e = 0; e < 8; ++e) w[e] = *reinterpret_cast<const uint2*>(dy + (m + e) * ld + n);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        s0 = __fadd_rn(s0, __uint_as_float(w[e] << 16));
-        s1 = __fadd_rn(s1, __uint_as_float(w[e] & 0xFFFF0000u));
+        s[0] = __fadd_rn(s[0], __uint_as_float(w[e].x << 16));
+        s[1] = __fadd_rn(s[1], __uint_as_float(w[e].x & 0xFFFF0000u));
+        s[2] = __fadd_rn(s[2], __uint_as_float(w[e].y << 16));
+        s[3] = __fadd_rn(s[3], __uint_as_float(w[e].y & 0xFFFF0000u));
       }
     }
+    for (; m < m1; ++m) {
+      const uint2 w = *reinterpret_cast<const uint2*>(dy + m * ld + n);
+      s[0] = __fadd_rn(s[0], __uint_as_float(w.x << 16));
+      s[1] = __fadd_rn(s[1], __uint_as_float(w.x & 0xFFFF0000u));
+      s[2] = __fadd_rn(s[2], __uint_as_float(w.y << 16));
+      s[3] = __fadd_rn(s[3], __uint_as_float(w.y & 0xFFFF0000u));
+    }
+  } else {
+    for (int64_t m = m0; m < m1; ++m)
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        if (n + c < N) s[c] = __fadd_rn(s[c], bf16_to_f32(dy[m * ld + n + c]));
   }
-  for (; m < m1; ++m) {
-    s0 = __fadd_rn(s0, bf16_to_f32(dy[m * ld + n]));
-    if (n + 1 < N) s1 = __fadd_rn(s1, bf16_to_f32(dy[m * ld + n + 1]));
-  }
-  part[(int64_t)blockIdx.y * N + n] = s0;
-  if (n + 1 < N) part[(int64_t)blockIdx.y * N + n + 1] = s1;
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+    if (n + c < N) part[(int64_t)blockIdx.y * N + n + c] = s[c];
 }
 
 __global__ __launch_bounds__(256) void colsum_finalize_kernel(const float* __restrict__ part,
@@ -169,9 +199,18 @@ __global__ __launch_bounds__(256) void colsum_finalize_kernel(const float* __res
                                                               uint16_t* out) {
   const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= N) return;
-  float s = 0.0f;
-  for (int64_t b = 0; b < slabs; ++b) s = __fadd_rn(s, part[b * N + n]);
+  const float s = ordered_sum(part + n, N, slabs);
   out[n] = (uint16_t)(pack_bf16x2(s, 0.0f) & 0xFFFFu);
+}
+
+void bias_grad_launch(const uint16_t* dy, int64_t ld, int64_t M, int64_t N, uint16_t* grad_bias, float* part,
+                      hipStream_t st) {
+  const int64_t slabs = cdiv(M, BG_ROWS);  // 0 when M == 0: the combine writes zeros
+  if (slabs > 0)
+    hipLaunchKernelGGL(colsum_partials_kernel, dim3((unsigned)cdiv(N, 1024), (unsigned)slabs), dim3(256), 0,
+                       st, dy, ld, M, N, part);
+  hipLaunchKernelGGL(colsum_finalize_kernel, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, part, slabs, N,
+                     grad_bias);
 }
 
 }  // namespace concord
@@ -207,18 +246,11 @@ extern "C" int concord_bias_grad(const uint16_t* dy, int64_t ld_dy, int64_t M, i
   CONCORD_CHECK(M >= 0 && N > 0, "concord_bias_grad: bad size");
   CONCORD_CHECK(dy && grad_bias, "concord_bias_grad: NULL argument");
   CONCORD_CHECK(ld_dy >= N, "concord_bias_grad: leading dimension < N");
-  const int64_t slabs = cdiv(M, 256);  // 0 when M == 0: the combine writes zeros
   const Workspace ws = workspace_layout(N, 1, M);
   if (!workspace || workspace_bytes < ws.total) {
     set_error("concord_bias_grad: workspace of %zu bytes needed", ws.total);
     return CONCORD_EWORKSPACE;
   }
-  float* part = (float*)((char*)workspace + ws.scratch);
-  hipStream_t st = (hipStream_t)stream;
-  if (slabs > 0)
-    hipLaunchKernelGGL(colsum_partials_kernel, dim3((unsigned)cdiv(N, 512), (unsigned)slabs),
-                       dim3(256), 0, st, dy, ld_dy, M, N, part);
-  hipLaunchKernelGGL(colsum_finalize_kernel, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, part,
-                     slabs, N, grad_bias);
+  bias_grad_launch(dy, ld_dy, M, N, grad_bias, (float*)((char*)workspace + ws.scratch), (hipStream_t)stream);
   return launch_status("bias_grad");
 }

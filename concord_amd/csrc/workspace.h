@@ -1,10 +1,10 @@
 // workspace.h -- layout of the caller-owned workspaces.
 //
 // Update-side workspace:
-// [0, 256)       counters: the rebalance "fired" flag; zero when the
-//                workspace is created and zero again after every call.
+// [0, 256)       reserved
 // [256, total)   scratch shared by the entry points (they run in stream order):
 //                v-hat partials, rebalance decisions, bias-gradient partials.
+//                No entry point needs its contents to survive between calls.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
@@ -12,7 +12,7 @@
 namespace concord {
 
 struct Workspace {
-  size_t reb_fired, scratch, total;
+  size_t scratch, total;
 };
 
 // v-hat scratch (floats, each region a multiple of 64 so the next stays
@@ -29,15 +29,20 @@ inline VhatScratch vhat_scratch(int64_t N, int64_t K) {
 inline Workspace workspace_layout(int64_t N, int64_t K, int64_t M) {
   auto cd = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
   Workspace w;
-  w.reb_fired = 64;
   w.scratch = 256;
   const VhatScratch v = vhat_scratch(N, K);
   const size_t vhat = (size_t)(v.pr + v.pc + v.bsum) * sizeof(float);
-  const size_t reb = (size_t)(2 * (N + K)) * sizeof(int32_t);
-  const size_t bias = (size_t)(cd(M, 256) * (N > K ? N : K)) * sizeof(float);
-  size_t s = vhat;
+  // rebalance: ticks and tick-down counts per row and column, decide-block flags
+  const size_t reb = (size_t)(2 * (N + K) + cd(N, 256) + cd(K, 256)) * sizeof(int32_t);
+  // bias gradient partials (concord_wgrad_vhat places them after the v-hat
+  // partials, which are still live when they are written)
+  // (slab partials of the bias-gradient kernels, or [cdiv(K, 128)][N] partials
+  // of the wgrad epilogue)
+  size_t bias = (size_t)(cd(M, 64) * (N > K ? N : K)) * sizeof(float);
+  const size_t bias_w = M > 0 ? (size_t)(cd(K, 128) * N) * sizeof(float) : 0;
+  if (bias_w > bias) bias = bias_w;
+  size_t s = vhat + bias;
   if (reb > s) s = reb;
-  if (bias > s) s = bias;
   w.total = w.scratch + ((s + 255) / 256) * 256;
   return w;
 }

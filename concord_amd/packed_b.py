@@ -227,10 +227,10 @@ def _gemm_workspace(device, M, N, K):
     return ws
 
 
-def _workspace(device, N, K):
+def _workspace(device, N, K, M=0):
     """Zero-initialised per-device workspace, grown to the largest layer."""
     key = _dev_key(device)
-    need = int(C.lib().concord_workspace_bytes(int(N), int(K), 0))
+    need = int(C.lib().concord_workspace_bytes(int(N), int(K), int(M)))
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < need:
         ws = torch.zeros(need, dtype=torch.uint8, device=key)
@@ -513,20 +513,24 @@ def _wgrad(dy, x2):
     return gw
 
 
-def _wgrad_vhat(dy, x2, v_row, v_col, sum_v_inv, beta2, row_max, col_max, salt_counter):
+def _wgrad_vhat(dy, x2, v_row, v_col, sum_v_inv, beta2, row_max, col_max, salt_counter,
+                with_bias=False):
     """wgrad with the v-hat partials formed in its epilogue, then the EMA
-    (concord/packed_b.py:1269-1303); same results as _wgrad + vhat_ema."""
+    (concord/packed_b.py:1269-1303); same results as _wgrad + vhat_ema.
+    with_bias: also returns grad_y.sum(0) (1338-1340), formed from the same
+    dy fragments.  Returns (grad_W, grad_bias or None)."""
     M, N = dy.shape
     K = x2.shape[1]
     gw = torch.empty((N, K), dtype=torch.bfloat16, device=dy.device)
+    gb = torch.empty(N, dtype=torch.bfloat16, device=dy.device) if with_bias else None
     gws = _gemm_workspace(dy.device, M, N, K)
-    ws = _workspace(dy.device, N, K)
+    ws = _workspace(dy.device, N, K, M if with_bias else 0)
     C.check(C.lib().concord_wgrad_vhat(
         C.ptr(dy), dy.stride(0), C.ptr(x2), x2.stride(0), C.ptr(gw), gw.stride(0), M, N, K,
         float(beta2), C.ptr(v_row), C.ptr(v_col), C.ptr(sum_v_inv), C.ptr(row_max), C.ptr(col_max),
-        C.ptr(salt_counter), C.ptr(ws), ws.numel(), C.ptr(gws), gws.numel(),
+        C.ptr(salt_counter), C.ptr(gb), C.ptr(ws), ws.numel(), C.ptr(gws), gws.numel(),
         C.stream_of(dy.device)), "wgrad_vhat")
-    return gw
+    return gw, gb
 
 
 _MUON_WORKSPACES = {}
@@ -629,6 +633,7 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
                              ctx.weight_buf).reshape(*ctx.lead, K)
         salt = _get_step_counter(dev)
         prebumped = False
+        grad_bias = None
         muon = ctx.drive == 'muon' and ctx.optimizer_kind == 'adamw'
         if muon:
             # O = sqrt(max(N, K)) NS5(grad_W / ||grad_W||); no v-hat
@@ -637,9 +642,11 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
         elif ctx.track_adafactor_v and ctx.v_row is not None:
             # wgrad (1269-1277), watermark zeroing (1281-1283), v-hat EMA (1288-1303),
             # salt + 1 (910-911)
-            grad_W = _wgrad_vhat(dy, x2, ctx.v_row, ctx.v_col, ctx.sum_v_inv, ctx.adafactor_beta2,
-                                 ctx.row_max_buf if ctx.track_rebalance else None,
-                                 ctx.col_max_buf if ctx.track_rebalance else None, salt)
+            grad_W, grad_bias = _wgrad_vhat(dy, x2, ctx.v_row, ctx.v_col, ctx.sum_v_inv,
+                                            ctx.adafactor_beta2,
+                                            ctx.row_max_buf if ctx.track_rebalance else None,
+                                            ctx.col_max_buf if ctx.track_rebalance else None, salt,
+                                            with_bias=ctx.has_bias)
             prebumped = True
         else:
             grad_W = _wgrad(dy, x2)
@@ -667,7 +674,8 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
                 alpha=ctx.alpha, beta1=ctx.beta1, alpha_v_fast=ctx.alpha_v_fast,
                 mass_preserve=ctx.mass_preserve, track_rebalance=ctx.track_rebalance,
                 salt_prebumped=prebumped)
-        grad_bias = _bias_grad(dy) if ctx.has_bias else None
+        if ctx.has_bias and grad_bias is None:
+            grad_bias = _bias_grad(dy)
         return (grad_x, None, None, None, grad_bias,
                 None, None, None, None,
                 None,

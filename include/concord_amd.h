@@ -182,16 +182,19 @@ int concord_wgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t 
 /* wgrad followed by the v-hat EMA, with the v-hat partial sums formed in the
  * wgrad epilogue from the bf16 values it stores (no re-read of grad_w):
  * grad_y_flat.T @ x_flat, the watermark zeroing and the v_row/v_col EMA of
- * FusedConcordLinearPackedB.backward, concord/packed_b.py:1269-1303.  Results
- * are bit-identical to concord_wgrad followed by concord_vhat_ema with the
- * same arguments.  workspace: concord_workspace_bytes(N, K, M) bytes;
- * gemm_workspace (optional): concord_gemm_workspace_bytes(M, N, K) bytes. */
+ * FusedConcordLinearPackedB.backward, concord/packed_b.py:1269-1303.  The
+ * grad_w / v_row / v_col / sum_v_inv results are bit-identical to
+ * concord_wgrad followed by concord_vhat_ema with the same arguments.  When
+ * grad_bias is non-NULL it receives bf16(sum_m dy[m, n]) (grad_y_flat.sum(0),
+ * 1338-1340), formed from the dy fragments the product already reads.
+ * workspace: concord_workspace_bytes(N, K, M) bytes; gemm_workspace
+ * (optional): concord_gemm_workspace_bytes(M, N, K) bytes. */
 int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t ld_x,
                        uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
                        double beta2, float* v_row, float* v_col, float* sum_v_inv,
-                       int32_t* row_max, int32_t* col_max, int32_t* salt_counter, void* workspace,
-                       size_t workspace_bytes, void* gemm_workspace, size_t gemm_workspace_bytes,
-                       void* stream);
+                       int32_t* row_max, int32_t* col_max, int32_t* salt_counter,
+                       uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
+                       void* gemm_workspace, size_t gemm_workspace_bytes, void* stream);
 
 /* Muon drive (A13): out[N,K] = bf16(gamma * NS5(g / ||g||_F)), the quintic
  * Newton-Schulz orthogonalisation of experiments/cpu_dynamics/exp9_muon.py:44-55

@@ -388,7 +388,10 @@ def test_wgrad_vhat_matches_separate_calls(oracle, M, N, K):
         cm = torch.full((K,), 7, dtype=torch.int32, device=DEV)
         salt = torch.tensor([5], dtype=torch.int32, device=DEV)
         if fused:
-            gw = pb._wgrad_vhat(dy, x, vrd, vcd, svi, 0.999, rm, cm, salt)
+            gw, gb = pb._wgrad_vhat(dy, x, vrd, vcd, svi, 0.999, rm, cm, salt, with_bias=True)
+            # bias gradient formed from the same dy fragments (fp32 sums, bf16 out)
+            ref_b = oracle.bf16_bits_to_f32(host(dy)).astype(np.float64).sum(0)
+            assert rel_l2(oracle.bf16_bits_to_f32(host(gb)), ref_b) < 5e-3
         else:
             gw = pb._wgrad(dy, x)
             pb.vhat_ema(gw, vrd, vcd, svi, 0.999, rm, cm, salt)
