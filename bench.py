@@ -8,19 +8,22 @@ fused dequant-GEMM mode.  One step = forward (dequant-GEMM) + backward
 synthetic x ~ N(0,1) and dy ~ N(0, 1e-3), random-init weights.
 
 Prints one JSON line.  value = dequant-matmul throughput of the whole step,
-6 M N K / step time (TFLOP/s).  roofline = the step's dominant kernel (the
-longest per-kernel time) against its roofline: a GEMM against dense bf16
-MFMA peak at 2 M N K algorithmic FLOP, the packed update against HBM peak at
-10 algorithmic B/param; rooflines = the same for every kernel of the step;
-traffic = HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
-WRITE_SIZE summary (profiles/traffic_sdxl_1280x5120.txt) when present.
-cpu_baseline = the same step on the host: torch fp32 GEMMs + the CPU oracle's
-v-hat / update / rebalance.
+6 M N K / step time (TFLOP/s).  The step's entries are timed one by one (HIP
+events around a HIP graph of back-to-back calls): forward, dgrad (main kernel
++ split reduction), wgrad with the v-hat partials and bias gradient in its
+epilogue (+ the v-hat EMA kernels), packed update.  roofline = the longest
+entry against its roofline: a GEMM against dense bf16 MFMA peak at 2 M N K
+algorithmic FLOP, the packed update against HBM peak at 10 algorithmic
+B/param; rooflines = the same for every entry; traffic = HBM bytes per call
+from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+(profiles/traffic_sdxl_1280x5120.txt) when present.  cpu_baseline = the same
+step on the host: torch fp32 GEMMs + the CPU oracle's v-hat / update /
+rebalance.
 
-`--only KERNEL` runs one kernel of the step `--reps` times and exits (the
+`--only KERNEL` runs one entry of the step `--reps` times and exits (the
 command the committed rocprofv3 summaries were taken with); KERNEL = fwd,
-dgrad, wgrad, vhat, update, materialize, or copy (a 256 MiB device copy, the
-counter calibration).
+dgrad, wgrad, wgrad_vhat, vhat, update, materialize, or copy (a 256 MiB
+device copy, the counter calibration).
 """
 import argparse
 import json
@@ -149,6 +152,9 @@ def _only(which, reps, layer, xb, dy, torch, pb):
         fn = lambda: pb._gemm_dgrad(dy, *st, 15, None)  # noqa: E731
     elif which == "wgrad":
         fn = lambda: pb._wgrad(dy, xb)  # noqa: E731
+    elif which == "wgrad_vhat":
+        fn = lambda: pb._wgrad_vhat(dy, xb, layer.v_row, layer.v_col, layer._sum_v_inv, 0.999,  # noqa: E731
+                                    layer._row_max_buf, layer._col_max_buf, None, with_bias=True)
     else:
         gw = pb._wgrad(dy, xb)
         if which == "vhat":
@@ -177,7 +183,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only", default=None,
-                    choices=["fwd", "dgrad", "wgrad", "vhat", "update", "materialize", "copy"])
+                    choices=["fwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
+                             "copy"])
     ap.add_argument("--reps", type=int, default=20)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -252,12 +259,16 @@ def main():
     flops_step = 6.0 * M_TOK * N_OUT * K_IN
     value = flops_step / (ms_step * 1e-3) / 1e12
 
-    # per-kernel averages (HIP events on the stream the kernels run on)
+    # per-entry averages (HIP events on the stream the kernels run on), each the
+    # call the step makes: forward, dgrad, wgrad + v-hat + bias gradient, update
     xb = x.detach()
     st = (layer.packed_w, layer.row_exp, layer.col_exp)
     reps = 20
     t_fwd = _event_time_ms(lambda: pb._gemm_fwd(xb, *st, 15, layer.bias, None), reps, torch)
     t_dgrad = _event_time_ms(lambda: pb._gemm_dgrad(dy, *st, 15, None), reps, torch)
+    t_wgv = _event_time_ms(lambda: pb._wgrad_vhat(dy, xb, layer.v_row, layer.v_col, layer._sum_v_inv, 0.999,
+                                                  layer._row_max_buf, layer._col_max_buf, None,
+                                                  with_bias=True), reps, torch)
     t_wgrad = _event_time_ms(lambda: pb._wgrad(dy, xb), reps, torch)
     gw = pb._wgrad(dy, xb)
     pk_copy = layer.packed_w.clone()
@@ -307,13 +318,13 @@ def main():
     roofs = {
         "dqgemm_fwd": gemm_roof("dqgemm_fwd", "gemm_dma_kernel<FWD, 256, 160> (fused dequant-GEMM forward)",
                                 t_fwd),
-        "dqgemm_dgrad": gemm_roof("dqgemm_dgrad", "gemm_dma_kernel<DGRAD, 256, 128> + split-K reduce "
-                                  "(fused dequant-GEMM dgrad)", t_dgrad),
-        "wgrad": gemm_roof("wgrad", "wgrad GEMM dy^T x", t_wgrad),
+        "dqgemm_dgrad": gemm_roof("dqgemm_dgrad", "gemm_dgt_kernel<DGRAD, 256, 128> + splitk_reduce_kernel "
+                                  "(fused dequant-GEMM dgrad, 3-way split reduction)", t_dgrad),
+        "wgrad_vhat": gemm_roof("wgrad_vhat", "gemm_tr_kernel<256, 128, 4, 2, VH> + vhat_finalize_kernel + "
+                                "vhat_sum_kernel (wgrad with v-hat partials and bias gradient in the "
+                                "epilogue, then the v-hat EMA)", t_wgv),
         "apply_adamw": hbm_roof("apply_adamw", "apply_adamw_fast_kernel<ratio> (packed update, winner flags)",
                                 t_upd, UPDATE_BYTES_PER_PARAM * params),
-        "vhat_ema": hbm_roof("vhat_ema", "vhat_partials + vhat_finalize (reads bf16 grad)", t_vhat,
-                             2 * params),
     }
     dominant = max(roofs, key=lambda k: roofs[k]["us"])
 
@@ -336,12 +347,14 @@ def main():
         "roofline": dict(roofs[dominant], step_kernel=dominant),
         "rooflines": roofs,
         "kernel_us": {"dqgemm_fwd": round(t_fwd * 1e3, 2), "dqgemm_dgrad": round(t_dgrad * 1e3, 2),
-                      "wgrad": round(t_wgrad * 1e3, 2), "vhat_ema": round(t_vhat * 1e3, 2),
+                      "wgrad_vhat": round(t_wgv * 1e3, 2), "wgrad_alone": round(t_wgrad * 1e3, 2),
+                      "vhat_ema_alone": round(t_vhat * 1e3, 2),
                       "apply_adamw": round(t_upd * 1e3, 2), "materialize": round(t_mat * 1e3, 2),
                       "rebalance_nofire": round(t_reb * 1e3, 2)},
         "gemm_tflops": {"fwd": round(fwd_tflops, 1),
                         "dgrad": round(gemm_flop / (t_dgrad * 1e-3) / 1e12, 1),
-                        "wgrad": round(gemm_flop / (t_wgrad * 1e-3) / 1e12, 1)},
+                        "wgrad_vhat": round(gemm_flop / (t_wgv * 1e-3) / 1e12, 1),
+                        "wgrad_alone": round(gemm_flop / (t_wgrad * 1e-3) / 1e12, 1)},
         "materialize_GBps": round(DECODE_BYTES_PER_PARAM * params / (t_mat * 1e-3) / 1e9, 1),
         "library_bf16_gemm_tflops": {
             "note": "torch.matmul (hipBLASLt) on a pre-decoded bf16 W, same shapes; context only",
