@@ -189,7 +189,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the packed path is single-GPU; sharding is described in DESIGN.md)", file=sys.stderr)
+              "(the packed path runs on one GPU; it has no multi-GPU mode)", file=sys.stderr)
         sys.exit(2)
 
     import torch
