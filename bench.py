@@ -285,6 +285,11 @@ def main():
     wbuf = torch.empty((N_OUT, K_IN), dtype=torch.bfloat16, device=dev)
     t_mat = _event_time_ms(lambda: pb.materialize_packed_bf16(layer.packed_w, layer.row_exp,
                                                               layer.col_exp, wbuf), reps, torch)
+    # config 5's Muon drive on this layer's gradient (context: NS5 = 5 x
+    # (2 m^2 n + 2 m^3 + 2 m^2 n) FLOP with m = 1280, n = 5120)
+    ns5_out = torch.empty_like(gw)
+    t_ns5 = _event_time_ms(lambda: pb.muon_ns5(gw, out=ns5_out), 3, torch)
+    ns5_flop = 5.0 * (4.0 * K_IN * K_IN * N_OUT + 2.0 * K_IN ** 3)
     # no-fire rebalance: zeroed watermarks, so no row or column ticks
     layer._row_max_buf.zero_()
     layer._col_max_buf.zero_()
@@ -356,6 +361,8 @@ def main():
                         "wgrad_vhat": round(gemm_flop / (t_wgv * 1e-3) / 1e12, 1),
                         "wgrad_alone": round(gemm_flop / (t_wgrad * 1e-3) / 1e12, 1)},
         "materialize_GBps": round(DECODE_BYTES_PER_PARAM * params / (t_mat * 1e-3) / 1e9, 1),
+        "muon_ns5": {"us": round(t_ns5 * 1e3, 1),
+                     "tflops": round(ns5_flop / (t_ns5 * 1e-3) / 1e12, 1)},
         "library_bf16_gemm_tflops": {
             "note": "torch.matmul (hipBLASLt) on a pre-decoded bf16 W, same shapes; context only",
             "fwd": round(gemm_flop / (t_lib_fwd * 1e-3) / 1e12, 1),
