@@ -325,9 +325,9 @@ def main():
                                 t_fwd),
         "dqgemm_dgrad": gemm_roof("dqgemm_dgrad", "gemm_dgt_kernel<DGRAD, 256, 128> + splitk_reduce_kernel "
                                   "(fused dequant-GEMM dgrad, 3-way split reduction)", t_dgrad),
-        "wgrad_vhat": gemm_roof("wgrad_vhat", "gemm_tr_kernel<256, 128, 4, 2, VH> + vhat_finalize_kernel + "
-                                "vhat_sum_kernel (wgrad with v-hat partials and bias gradient in the "
-                                "epilogue, then the v-hat EMA)", t_wgv),
+        "wgrad_vhat": gemm_roof("wgrad_vhat", "gemm_tr_kernel<256, 128, 4, 2, VH> + vhat_finalize_kernel "
+                                "(wgrad with v-hat partials and bias gradient in the epilogue, then the "
+                                "v-hat EMA and its row sum)", t_wgv),
         "apply_adamw": hbm_roof("apply_adamw", "apply_adamw_fast_kernel<ratio> (packed update, winner flags)",
                                 t_upd, UPDATE_BYTES_PER_PARAM * params),
     }

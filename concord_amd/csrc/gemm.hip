@@ -577,6 +577,7 @@ extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint1
   float* pc = pr + v.pr;
   float* bsum = pc + v.pc;
   float* bpart = bsum + v.bsum;
+  uint32_t* ticket = (uint32_t*)((char*)workspace + ws.vhat_ticket);
   hipStream_t st = (hipStream_t)stream;
   GemmArgs g = make_args(dy, x, ld_dy, ld_x, nullptr, nullptr, 0, nullptr, grad_w, ld_gw, N, K, M, false);
   g.vh_pr = pr;
@@ -590,12 +591,13 @@ extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint1
     if (rc != CONCORD_OK) return rc;
     vhat_partials_launch(grad_w, ld_gw, N, K, pr, pc, st);
     if (grad_bias) bias_grad_launch(dy, ld_dy, M, N, grad_bias, bpart, st);
-    vhat_finish_launch(pr, pc, bsum, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter, st);
+    vhat_finish_launch(pr, pc, bsum, ticket, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max,
+                       salt_counter, st);
   } else if (rc != CONCORD_OK) {
     return rc;
   } else {
-    vhat_finish_launch(pr, pc, bsum, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter, st,
-                       bpart, tiles_j, grad_bias);
+    vhat_finish_launch(pr, pc, bsum, ticket, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max,
+                       salt_counter, st, bpart, tiles_j, grad_bias);
   }
   return launch_status("wgrad_vhat");
 }

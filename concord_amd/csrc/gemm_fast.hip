@@ -1051,23 +1051,23 @@ CONCORD_DEV void mfma_block(f32x4 (&acc)[NI][NJ], const bf16x8 (&fa)[NI], const 
 // Per stage: fragments of the second half-stage are read while the first
 // half-stage's MFMAs issue, then (after the barrier) the next stage's first
 // half is read while the second half's MFMAs issue.
-// bias-gradient partial of one wave: for each of its i-fragments, the sum of
-// the 8 r-values this lane holds, added in ascending r
+// bias-gradient partial of one wave: sum_r a(i, r) for each of its
+// i-fragments, as an MFMA against an all-ones operand (every output column
+// j of the 16 x 16 block then holds the same column sum)
 template <int NI>
-CONCORD_DEV void bias_acc(float (&b)[NI], const bf16x8 (&fa)[NI]) {
+CONCORD_DEV void bias_acc(f32x4 (&b)[NI], const bf16x8 (&fa)[NI]) {
+  const bf16x8 ones = {(__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f,
+                       (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
-  for (int x = 0; x < NI; ++x)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) b[x] = __fadd_rn(b[x], (float)fa[x][e]);
+  for (int x = 0; x < NI; ++x) b[x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, fa[x], b[x], 0, 0, 0);
 }
 
 // VH: also write the v-hat partials of the bf16-rounded output (64 x 64 wave
 // tiles, vhat_tile.h order); only without split-K.  With g.bpart set, the
 // waves wj = 0 of block (bi, bj) also sum the A operand over the stages
-// s = bj, bj + tiles_j, ...: lane (p, q) chains its r = 8 q .. 8 q + 7
-// (mod 32) values of column p in ascending r, the four q are then added as
-// (q0 + q1) + (q2 + q3), and the fp32 result is bpart[bj][i]; the bias
-// gradient is the sum of the partials over bj ascending (vhat_finalize).
+// s = bj, bj + tiles_j, ... (an MFMA against ones per fragment, fp32
+// accumulation), giving bpart[bj][i]; the bias gradient is the sum of the
+// partials over bj ascending (vhat_finalize).
 template <int BI, int BJ, int WI, int WJ, bool VH>
 __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
   constexpr int NW = WI * WJ, NT = 64 * NW, WTI = BI / WI, WTJ = BJ / WJ;
@@ -1124,9 +1124,9 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
   lds_barrier();
   bf16x8 fa0[NI], fb0[NJ], fa1[NI], fb1[NJ];
   const bool bg = VH && g.bpart != nullptr && wj == 0;   // uniform per wave
-  float bsum[NI];
+  f32x4 bsum[NI];
 #pragma unroll
-  for (int x = 0; x < NI; ++x) bsum[x] = 0.0f;
+  for (int x = 0; x < NI; ++x) bsum[x] = f32x4{0.f, 0.f, 0.f, 0.f};
   tr_frags<NI, DA::ROWB>(fa0, ring_p, la, fsw, cwa, 0);
   tr_frags<NJ, DB::ROWB>(fb0, ring_p, lb, fsw, cwb, 0);
   for (int s = 0; s < nst; ++s) {
@@ -1149,10 +1149,8 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
   if (bg) {
 #pragma unroll
     for (int x = 0; x < NI; ++x) {
-      const float h = __fadd_rn(bsum[x], __shfl_xor(bsum[x], 16, 64));
-      const float tot = __fadd_rn(h, __shfl_xor(h, 32, 64));
       const int64_t i = i0 + wi * WTI + 16 * x + (lane & 15);
-      if (lane < 16 && i < g.I) g.bpart[(int64_t)bj * g.I + i] = tot;
+      if (lane < 16 && i < g.I) g.bpart[(int64_t)bj * g.I + i] = bsum[x][0];
     }
   }
   // no DMA may still be writing LDS when the ring is reused for the output

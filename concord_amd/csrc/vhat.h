@@ -12,10 +12,11 @@ void vhat_partials_launch(const uint16_t* grad, int64_t ld, int64_t N, int64_t K
 // salt advance (row_max, col_max, salt may be NULL)
 // bpart / nbp / grad_bias (optional): grad_bias[n] = bf16(sum over b < nbp
 // ascending of bpart[b][n])
-void vhat_finish_launch(const float* pr, const float* pc, float* bsum, int64_t N, int64_t K, double beta2,
-                        float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max, int32_t* col_max,
-                        int32_t* salt, hipStream_t st, const float* bpart = nullptr, int64_t nbp = 0,
-                        uint16_t* grad_bias = nullptr);
+// ticket: a zero-initialised counter the call leaves at zero again
+void vhat_finish_launch(const float* pr, const float* pc, float* bsum, uint32_t* ticket, int64_t N, int64_t K,
+                        double beta2, float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max,
+                        int32_t* col_max, int32_t* salt, hipStream_t st, const float* bpart = nullptr,
+                        int64_t nbp = 0, uint16_t* grad_bias = nullptr);
 
 // grad_bias[N] = bf16(sum_m dy[m][n]) (fp32, 64-row slabs, slabs ascending);
 // part: cdiv(M, 64) * N floats of scratch

@@ -77,13 +77,20 @@ CONCORD_DEV float ordered_sum(const float* __restrict__ v, int64_t stride, int64
 }
 
 // Row/column EMA and watermark zeroing.  Blocks [0, cdiv(N, 256)) take rows
-// and also leave the halving-tree total of their 256 new v_row values in
-// bsum; the remaining blocks take columns.
+// and leave the halving-tree total of their 256 new v_row values in bsum;
+// the remaining blocks take columns.  The last row block to finish (a
+// device-scope ticket) chains the totals in ascending order into
+// 1 / max(sum v_row, 1e-30) and advances the salt.  The totals and the
+// ticket are device-scope atomics (cache-coherent across the XCDs), each
+// total stored and complete before its block takes a ticket, so the last
+// block reads every total without a device-wide cache write-back.
 __global__ __launch_bounds__(256) void vhat_finalize_kernel(
     const float* __restrict__ pr, const float* __restrict__ pc, int64_t N, int64_t K, float b2,
     float omb2, float* v_row, float* v_col, int32_t* row_max, int32_t* col_max, float* bsum,
-    const float* __restrict__ bpart, int64_t nbp, uint16_t* grad_bias) {
+    const float* __restrict__ bpart, int64_t nbp, uint16_t* grad_bias, uint32_t* ticket,
+    float* sum_v_inv, int32_t* salt) {
   __shared__ float s_part[256];
+  __shared__ uint32_t s_ticket;
   const int64_t rb = cdiv(N, 256);
   const int64_t nc = cdiv(K, 64), nr = cdiv(N, 64);
   if ((int64_t)blockIdx.x < rb) {
@@ -102,31 +109,33 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
       if (threadIdx.x < h) s_part[threadIdx.x] = __fadd_rn(s_part[threadIdx.x], s_part[threadIdx.x + h]);
       __syncthreads();
     }
-    if (threadIdx.x == 0) bsum[blockIdx.x] = s_part[0];
+    if (threadIdx.x == 0) {
+      __hip_atomic_store(bsum + blockIdx.x, s_part[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);   // the total is stored before the ticket is taken
+      s_ticket = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (s_ticket != (uint32_t)(rb - 1) || threadIdx.x >= 64) return;
+    // last row block, one wave: totals 64 at a time, chained in order
+    const int lane = threadIdx.x;
+    float s = 0.0f;
+    for (int64_t c0 = 0; c0 < rb; c0 += 64) {
+      const float v = c0 + lane < rb ? __hip_atomic_load(bsum + c0 + lane, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
+      const int cnt = (int)min((int64_t)64, rb - c0);
+      for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, __shfl(v, j, 64));
+    }
+    if (lane == 0) {
+      *sum_v_inv = __fdiv_rn(1.0f, fmaxf(s, 1e-30f));
+      if (salt) salt[0] = wadd(salt[0], 1);
+      __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // re-armed
+    }
   } else {
     const int64_t k = ((int64_t)blockIdx.x - rb) * 256 + threadIdx.x;
     if (k >= K) return;
     const float s = ordered_sum(pc + k, K, nr);
     v_col[k] = __fadd_rn(__fmul_rn(v_col[k], b2), __fmul_rn(omb2, s));
     if (col_max) col_max[k] = 0;
-  }
-}
-
-// 1 / max(sum of the block totals ascending, 1e-30) and the salt advance.
-// One wave: the totals are loaded 64 at a time and chained in order.  A kernel
-// of its own, so it sees every block total without a device-scope fence.
-__global__ __launch_bounds__(64) void vhat_sum_kernel(const float* __restrict__ bsum, int64_t nb,
-                                                      float* sum_v_inv, int32_t* salt) {
-  const int lane = threadIdx.x;
-  float s = 0.0f;
-  for (int64_t c0 = 0; c0 < nb; c0 += 64) {
-    const float v = c0 + lane < nb ? bsum[c0 + lane] : 0.0f;
-    const int cnt = (int)min((int64_t)64, nb - c0);
-    for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, __shfl(v, j, 64));
-  }
-  if (lane == 0) {
-    *sum_v_inv = __fdiv_rn(1.0f, fmaxf(s, 1e-30f));
-    if (salt) salt[0] = wadd(salt[0], 1);
   }
 }
 
@@ -137,15 +146,16 @@ void vhat_partials_launch(const uint16_t* grad, int64_t ld, int64_t N, int64_t K
                      pr, pc);
 }
 
-void vhat_finish_launch(const float* pr, const float* pc, float* bsum, int64_t N, int64_t K, double beta2,
-                        float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max, int32_t* col_max,
-                        int32_t* salt, hipStream_t st, const float* bpart, int64_t nbp, uint16_t* grad_bias) {
+void vhat_finish_launch(const float* pr, const float* pc, float* bsum, uint32_t* ticket, int64_t N, int64_t K,
+                        double beta2, float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max,
+                        int32_t* col_max, int32_t* salt, hipStream_t st, const float* bpart, int64_t nbp,
+                        uint16_t* grad_bias) {
   const float b2 = (float)beta2;
   const float omb2 = (float)(1.0 - beta2);
   const int64_t rb = cdiv(N, 256);
   hipLaunchKernelGGL(vhat_finalize_kernel, dim3((unsigned)(rb + cdiv(K, 256))), dim3(256), 0, st, pr, pc,
-                     N, K, b2, omb2, v_row, v_col, row_max, col_max, bsum, bpart, nbp, grad_bias);
-  hipLaunchKernelGGL(vhat_sum_kernel, dim3(1), dim3(64), 0, st, bsum, rb, sum_v_inv, salt);
+                     N, K, b2, omb2, v_row, v_col, row_max, col_max, bsum, bpart, nbp, grad_bias, ticket,
+                     sum_v_inv, salt);
 }
 
 // bias gradient: a thread sums 4 adjacent columns over a slab of 64 rows
@@ -236,7 +246,8 @@ extern "C" int concord_vhat_ema(const uint16_t* grad, int64_t ld_g, int64_t N, i
   float* bsum = pc + v.pc;
   hipStream_t st = (hipStream_t)stream;
   vhat_partials_launch(grad, ld_g, N, K, pr, pc, st);
-  vhat_finish_launch(pr, pc, bsum, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter, st);
+  vhat_finish_launch(pr, pc, bsum, (uint32_t*)((char*)workspace + ws.vhat_ticket), N, K, beta2, v_row, v_col,
+                     sum_v_inv, row_max, col_max, salt_counter, st);
   return launch_status("vhat_ema");
 }
 

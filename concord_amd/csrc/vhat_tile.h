@@ -3,14 +3,14 @@
 //
 // Lane l = 16 q + p holds, for x, y in [0, 4) and v in [0, 4), the value of
 // tile row 16 x + p, column 16 y + 4 q + v.  The sums are taken in one fixed
-// order (oracle_vhat_ema restates it):
+// order (oracle_vhat_ema restates it); each lane first chains what it holds,
+// then one cross-lane tree per row or column:
 //   row partial    s(y, q) = ((g2_0 + g2_1) + g2_2) + g2_3 over the lane's 4 columns,
-//                  t(y) = (s(y,0) + s(y,1)) + (s(y,2) + s(y,3))   [lanes p, p+16, p+32, p+48]
-//                  P_r = ((t(0) + t(1)) + t(2)) + t(3)
-//   column partial u(x) = pairwise tree over the 16 rows of block x, pairs
-//                  (p, p+8), (p, p+4), (p, p+2), (p, p+1) [lanes of one 16-lane row]
-//                  P_c = ((u(0) + u(1)) + u(2)) + u(3)
-// Every butterfly step adds the same two values on both lanes of a pair
+//                  u(q) = ((s(0,q) + s(1,q)) + s(2,q)) + s(3,q),
+//                  P_r = (u(0) + u(1)) + (u(2) + u(3))     [lanes p, p+16, p+32, p+48]
+//   column partial w(p) = ((a(p) + a(16+p)) + a(32+p)) + a(48+p) over the lane's 4 rows,
+//                  P_c = pairwise tree over p, pairs (p, p+8), (p, p+4), (p, p+2), (p, p+1)
+// Every cross-lane step adds the same two values on both lanes of a pair
 // (a + b == b + a exactly), so all lanes of a group end with one value.
 #pragma once
 #include "common.h"
@@ -34,16 +34,16 @@ CONCORD_DEV void vhat_tile_partials(const float (&g2)[4][4][4], int lane, int64_
   // rows
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
-    float acc = 0.0f;
+    float u = 0.0f;
 #pragma unroll
     for (int y = 0; y < 4; ++y) {
       const float s = __fadd_rn(__fadd_rn(__fadd_rn(g2[x][y][0], g2[x][y][1]), g2[x][y][2]), g2[x][y][3]);
-      const float t1 = __fadd_rn(s, __shfl_xor(s, 16, 64));
-      const float t = __fadd_rn(t1, __shfl_xor(t1, 32, 64));
-      acc = y == 0 ? t : __fadd_rn(acc, t);
+      u = y == 0 ? s : __fadd_rn(u, s);
     }
+    const float h = __fadd_rn(u, __shfl_xor(u, 16, 64));
+    const float t = __fadd_rn(h, __shfl_xor(h, 32, 64));
     const int64_t n = row0 + 16 * x + p;
-    if (q == 0 && n < N) pr[(col0 / 64) * N + n] = acc;
+    if (q == 0 && n < N) pr[(col0 / 64) * N + n] = t;
   }
   // columns
   float cs[4][4];
@@ -51,17 +51,12 @@ CONCORD_DEV void vhat_tile_partials(const float (&g2)[4][4][4], int lane, int64_
   for (int y = 0; y < 4; ++y)
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        float u = g2[x][y][v];
-        u = __fadd_rn(u, row_ror<8>(u));
-        u = __fadd_rn(u, row_ror<4>(u));
-        u = __fadd_rn(u, row_ror<2>(u));
-        u = __fadd_rn(u, row_ror<1>(u));
-        acc = x == 0 ? u : __fadd_rn(acc, u);
-      }
-      cs[y][v] = acc;
+      float w = __fadd_rn(__fadd_rn(__fadd_rn(g2[0][y][v], g2[1][y][v]), g2[2][y][v]), g2[3][y][v]);
+      w = __fadd_rn(w, row_ror<8>(w));
+      w = __fadd_rn(w, row_ror<4>(w));
+      w = __fadd_rn(w, row_ror<2>(w));
+      w = __fadd_rn(w, row_ror<1>(w));
+      cs[y][v] = w;
     }
   if (p == 0) {
     float* dst = pc + (row0 / 64) * K;

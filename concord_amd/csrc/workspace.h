@@ -1,7 +1,8 @@
 // workspace.h -- layout of the caller-owned workspaces.
 //
 // Update-side workspace:
-// [0, 256)       reserved
+// [0, 256)       counters: the v-hat "row blocks done" ticket; zero when the
+//                workspace is created and zero again after every call.
 // [256, total)   scratch shared by the entry points (they run in stream order):
 //                v-hat partials, rebalance decisions, bias-gradient partials.
 //                No entry point needs its contents to survive between calls.
@@ -12,7 +13,7 @@
 namespace concord {
 
 struct Workspace {
-  size_t scratch, total;
+  size_t vhat_ticket, scratch, total;
 };
 
 // v-hat scratch (floats, each region a multiple of 64 so the next stays
@@ -29,6 +30,7 @@ inline VhatScratch vhat_scratch(int64_t N, int64_t K) {
 inline Workspace workspace_layout(int64_t N, int64_t K, int64_t M) {
   auto cd = [](int64_t a, int64_t b) { return (a + b - 1) / b; };
   Workspace w;
+  w.vhat_ticket = 0;
   w.scratch = 256;
   const VhatScratch v = vhat_scratch(N, K);
   const size_t vhat = (size_t)(v.pr + v.pc + v.bsum) * sizeof(float);

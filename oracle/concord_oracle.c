@@ -547,13 +547,12 @@ void oracle_rebalance(int32_t* packed, int8_t* row_exp, int8_t* col_exp,
  * with g2[r][c] for tile row r and column c:
  *   row partial of row r (P_r[col tile][n]):
  *     s(y, q) = ((g2[r][16y+4q] + g2[r][16y+4q+1]) + g2[r][16y+4q+2]) + g2[r][16y+4q+3]
- *     t(y)    = (s(y,0) + s(y,1)) + (s(y,2) + s(y,3))
- *     P       = ((t(0) + t(1)) + t(2)) + t(3)
+ *     u(q)    = ((s(0,q) + s(1,q)) + s(2,q)) + s(3,q)
+ *     P       = (u(0) + u(1)) + (u(2) + u(3))
  *   column partial of column c (P_c[row tile][k]):
- *     for each block x of 16 rows, a(p) = g2[16x+p][c], p = 0..15:
- *       u1(p) = a(p) + a(p+8), p < 8;  u2(p) = u1(p) + u1(p+4), p < 4;
- *       u3(p) = u2(p) + u2(p+2), p < 2;  u(x) = u3(0) + u3(1)
- *     P = ((u(0) + u(1)) + u(2)) + u(3)
+ *     w(p) = ((g2[p][c] + g2[16+p][c]) + g2[32+p][c]) + g2[48+p][c], p = 0..15
+ *     u1(p) = w(p) + w(p+8), p < 8;  u2(p) = u1(p) + u1(p+4), p < 4;
+ *     u3(p) = u2(p) + u2(p+2), p < 2;  P = u3(0) + u3(1)
  *   g2_row[n] = sum over column tiles ascending of P_r, from 0.0f; g2_col[k]
  *   likewise over row tiles;
  *   sum_v: per block of 256 rows the halving tree s_t += s_{t+h}, h = 128 ..
@@ -562,29 +561,26 @@ void oracle_rebalance(int32_t* packed, int8_t* row_exp, int8_t* col_exp,
  * accumulator layout: lane (p, q) of a wave holds tile rows 16x+p, columns
  * 16y+4q..16y+4q+3.) */
 static float vh_row_tile(const float* g2r /* 64 values */) {
-    float t[4];
-    for (int y = 0; y < 4; ++y) {
-        float sq[4];
-        for (int q = 0; q < 4; ++q) {
+    float u[4];
+    for (int q = 0; q < 4; ++q) {
+        float acc = 0.0f;
+        for (int y = 0; y < 4; ++y) {
             const float* v = g2r + 16 * y + 4 * q;
-            sq[q] = ((v[0] + v[1]) + v[2]) + v[3];
+            const float s = ((v[0] + v[1]) + v[2]) + v[3];
+            acc = y == 0 ? s : acc + s;
         }
-        t[y] = (sq[0] + sq[1]) + (sq[2] + sq[3]);
+        u[q] = acc;
     }
-    return ((t[0] + t[1]) + t[2]) + t[3];
+    return (u[0] + u[1]) + (u[2] + u[3]);
 }
 
 static float vh_col_tile(const float* g2c /* 64 values, one per tile row */) {
-    float u[4];
-    for (int x = 0; x < 4; ++x) {
-        const float* a = g2c + 16 * x;
-        float u1[8], u2[4], u3[2];
-        for (int p = 0; p < 8; ++p) u1[p] = a[p] + a[p + 8];
-        for (int p = 0; p < 4; ++p) u2[p] = u1[p] + u1[p + 4];
-        for (int p = 0; p < 2; ++p) u3[p] = u2[p] + u2[p + 2];
-        u[x] = u3[0] + u3[1];
-    }
-    return ((u[0] + u[1]) + u[2]) + u[3];
+    float w[16], u1[8], u2[4], u3[2];
+    for (int p = 0; p < 16; ++p) w[p] = ((g2c[p] + g2c[16 + p]) + g2c[32 + p]) + g2c[48 + p];
+    for (int p = 0; p < 8; ++p) u1[p] = w[p] + w[p + 8];
+    for (int p = 0; p < 4; ++p) u2[p] = u1[p] + u1[p + 4];
+    for (int p = 0; p < 2; ++p) u3[p] = u2[p] + u2[p + 2];
+    return u3[0] + u3[1];
 }
 
 void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
