@@ -138,6 +138,50 @@ def cpu_baseline(threads):
                       f"(fwd, dgrad, wgrad) + oracle v-hat, update, rebalance"}
 
 
+def _graph_ms(step, warmup, steps, torch):
+    """Average time of one step replayed from a HIP graph (events on the
+    launching stream)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
+
+
+def _weight_cache_step_ms(layer, x, dy, warmup, steps, torch, ca):
+    """The same step on a weight_cache=True copy of the layer."""
+    wl = ca.ConcordLinearPackedB(K_IN, N_OUT, bias=True, device=x.device, lr=5e-4, weight_cache=True)
+    wl.disable_cohpre()
+    wl.gf_consol = 50.0
+    with torch.no_grad():
+        wl.load_weights(layer.get_weight().float())
+
+    def step():
+        x.grad = None
+        wl.bias.grad = None
+        wl(x).backward(dy)
+        wl.rebalance()
+
+    for _ in range(3):
+        step()
+    return _graph_ms(step, warmup, steps, torch)
+
+
 def _only(which, reps, layer, xb, dy, torch, pb):
     """Run one kernel of the step `reps` times (profiling entry)."""
     st = (layer.packed_w, layer.row_exp, layer.col_exp)
@@ -295,6 +339,14 @@ def main():
     layer._col_max_buf.zero_()
     t_reb = _event_time_ms(layer.rebalance, reps, torch)
 
+    # the reference's own dataflow on the same workload, for context: the
+    # update emits the bf16 weight (materialize-merge) and the next step's
+    # forward and dgrad are bf16 GEMMs on it (this library's kernels)
+    Wd0 = layer.get_weight()
+    t_bf_fwd = _event_time_ms(lambda: pb._gemm_fwd(xb, None, None, None, 15, layer.bias, Wd0), reps, torch)
+    t_bf_dgrad = _event_time_ms(lambda: pb._gemm_dgrad(dy, None, None, None, 15, Wd0), reps, torch)
+    wc_ms = _weight_cache_step_ms(layer, x, dy, args.warmup, args.steps, torch, ca)
+
     # library reference (hipBLASLt through torch.matmul) on the same bf16 shapes,
     # for context only: W decoded once, not part of the measured path
     Wd = layer.get_weight()
@@ -363,6 +415,12 @@ def main():
         "materialize_GBps": round(DECODE_BYTES_PER_PARAM * params / (t_mat * 1e-3) / 1e9, 1),
         "muon_ns5": {"us": round(t_ns5 * 1e3, 1),
                      "tflops": round(ns5_flop / (t_ns5 * 1e-3) / 1e12, 1)},
+        "weight_cache_mode": {
+            "note": "the reference's dataflow (update emits the bf16 weight; forward and dgrad are bf16 "
+                    "GEMMs on it), same workload; context only",
+            "ms_per_step": round(wc_ms, 4),
+            "tflops": round(flops_step / (wc_ms * 1e-3) / 1e12, 2),
+            "fwd_us": round(t_bf_fwd * 1e3, 2), "dgrad_us": round(t_bf_dgrad * 1e3, 2)},
         "library_bf16_gemm_tflops": {
             "note": "torch.matmul (hipBLASLt) on a pre-decoded bf16 W, same shapes; context only",
             "fwd": round(gemm_flop / (t_lib_fwd * 1e-3) / 1e12, 1),

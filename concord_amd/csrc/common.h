@@ -69,20 +69,28 @@ CONCORD_DEV int32_t pack(int32_t sf, int32_t ss, int32_t vs) {
 }
 
 // ---- the SR hash: concord/packed_b.py:109-117 ------------------------------------
-CONCORD_DEV float hash_uniform(int32_t x, int32_t pos_salt) {
-  int32_t h = x ^ pos_salt;
+// u = hash(x ^ pos_salt) in [0, 1), 24 bits
+CONCORD_DEV float hash_mix(int32_t h) {
   h = h ^ wshl(h, 13);
   h = h ^ (h >> 17);
   h = h ^ wshl(h, 5);
   h = h ^ (h >> 7);
   return __fmul_rn((float)(h & 0xFFFFFF), 5.9604644775390625e-08f);
 }
+CONCORD_DEV float hash_uniform(int32_t x, int32_t pos_salt) { return hash_mix(x ^ pos_salt); }
+// hash_uniform(x, pos ^ c): the three-way xor is one v_bitop3_b32
+CONCORD_DEV float hash_uniform3(int32_t x, int32_t pos, int32_t c) {
+  return hash_mix((int32_t)__builtin_amdgcn_bitop3_b32((uint32_t)x, (uint32_t)pos, (uint32_t)c, 0x96));
+}
 
-// int(floor(d) + (u < d - floor(d))), concord/packed_b.py:596-598
+// int(floor(d) + (u < d - floor(d))), concord/packed_b.py:596-598.
+// Formed as int(floor(d)) + (u < fr): equal, because u < fr needs fr > 0,
+// so d is not an integer, |d| < 2^23 and floor(d) + 1 is exact; otherwise
+// both forms convert floor(d) alone (NaN -> 0, +-inf saturate alike).
 CONCORD_DEV int32_t sr_tick(float d, float u) {
   const float fl = floorf(d);
   const float fr = __fsub_rn(d, fl);
-  return f2i(__fadd_rn(fl, u < fr ? 1.0f : 0.0f));
+  return f2i(fl) + (int32_t)(u < fr);
 }
 
 // ---- Philox4x32-10 as tl.rand (triton/language/random.py:13-44, 127-157) ------
@@ -161,9 +169,28 @@ CONCORD_DEV float det_exp2(float y) {
   return __fmul_rn(__fmul_rn(p, exp2i(a)), exp2i(b));
 }
 
-// correctly rounded sqrt: __builtin_sqrtf expands to v_sqrt_f32 plus the
-// +-1 ulp fma correction (__fsqrt_rn lowers to the bare ~1 ulp v_sqrt_f32).
-CONCORD_DEV float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+// correctly rounded sqrt.  __builtin_sqrtf expands to v_sqrt_f32 plus the
+// +-1 ulp fma correction, wrapped in a 2^32 pre-scale for x < 2^-96 and a
+// class test that returns x itself for +-0 and +inf.  For x >= 2^-96
+// (and +inf, where the corrections leave v_sqrt's inf) the scale and the
+// class test change nothing, so only the correction runs; a wave with any
+// lane below 2^-96, zero, negative or NaN takes the full expansion.
+CONCORD_DEV float sqrt_rn(float x) {
+  float s = __builtin_amdgcn_sqrtf(x);
+  const float sdn = __int_as_float(__float_as_int(s) - 1);
+  const float sup = __int_as_float(__float_as_int(s) + 1);
+  const float rdn = __builtin_fmaf(-sdn, s, x);
+  const float rup = __builtin_fmaf(-sup, s, x);
+  s = rdn <= 0.0f ? sdn : s;
+  s = rup > 0.0f ? sup : s;
+  if (__builtin_amdgcn_ballot_w64(!(x >= 0x1p-96f))) {
+    float y = x;
+    asm volatile("" : "+v"(y));   // keep the full expansion behind the branch
+    const float full = __builtin_sqrtf(y);
+    s = x >= 0x1p-96f ? s : full;
+  }
+  return s;
+}
 
 CONCORD_DEV float pow_p(float x, float p) {
   if (p == 0.5f) return sqrt_rn(x);

@@ -125,7 +125,7 @@ CONCORD_DEV int32_t adamw_element(int32_t word, float g, int32_t te, float vr, f
     }
     float chase = __fmul_rn(__fmul_rn(__fmul_rn(P.alpha, gate), P.gate_gain), (float)sf);
     if (proto) chase = __fmul_rn(chase, U.consf);
-    const int32_t t2 = sr_tick(__fmul_rn(chase, 0.0078125f), hash_uniform(sf, ps ^ 0x5A5A5A5A));
+    const int32_t t2 = sr_tick(__fmul_rn(chase, 0.0078125f), hash_uniform3(sf, ps, 0x5A5A5A5A));
     ss = wadd(ss, t2);
     sf = wsub(sf, wshl(t2, 7));
 
@@ -133,7 +133,7 @@ CONCORD_DEV int32_t adamw_element(int32_t word, float g, int32_t te, float vr, f
     if (proto) dv8 = __fmul_rn(dv8, U.consf);
     if (flags & CONCORD_RATIO_COH)
       dv8 = __fmul_rn(dv8, __fadd_rn(U.leak_floor, __fmul_rn(__fsub_rn(1.0f, U.leak_floor), coh)));
-    const int32_t t3 = sr_tick(dv8, hash_uniform(sf, ps ^ 0x33335555));
+    const int32_t t3 = sr_tick(dv8, hash_uniform3(sf, ps, 0x33335555));
     new_v = clampi(wadd(vs, t3), -128, 127);
     if (flags & CONCORD_MASS_PRESERVE) ss = wsub(ss, wsub(new_v, vs));
 
@@ -142,10 +142,10 @@ CONCORD_DEV int32_t adamw_element(int32_t word, float g, int32_t te, float vr, f
       float wdsv = __fmul_rn(__fmul_rn(__fmul_rn(U.lr, P.wd_sv), (float)wsub(wshl(ss, 7), vpost)),
                              0.0078125f);
       if (proto) wdsv = __fmul_rn(wdsv, U.consf);
-      ss = wsub(ss, sr_tick(wdsv, hash_uniform(sf, ps ^ 0x66665555)));
+      ss = wsub(ss, sr_tick(wdsv, hash_uniform3(sf, ps, 0x66665555)));
       float wdsf = __fmul_rn(__fmul_rn(U.lr, P.wd_sf), (float)wsub(wadd(wshl(ss, 7), sf), vpost));
       if (proto) wdsf = __fmul_rn(wdsf, U.consf);
-      sf = wsub(sf, sr_tick(wdsf, hash_uniform(sf, ps ^ 0x77770000)));
+      sf = wsub(sf, sr_tick(wdsf, hash_uniform3(sf, ps, 0x77770000)));
     }
   }
   const int32_t sfc = clampi(sf, -32768, 32767);
@@ -198,12 +198,12 @@ CONCORD_DEV int32_t adamw_element_fast(int32_t word, float g, float scale_fwd, f
     *coh_pre = __fadd_rn(__fmul_rn(__fsub_rn(1.0f, avf), cp), __fmul_rn(avf, coh));
   }
   const float chase = __fmul_rn(__fmul_rn(alpha, gate), (float)sf);
-  const int32_t t2 = sr_tick(__fmul_rn(chase, 0.0078125f), hash_uniform(sf, ps ^ 0x5A5A5A5A));
+  const int32_t t2 = sr_tick(__fmul_rn(chase, 0.0078125f), hash_uniform3(sf, ps, 0x5A5A5A5A));
   ss = wadd(ss, t2);
   sf = wsub(sf, wshl(t2, 7));
   float dv8 = __fmul_rn(__fmul_rn(avf, (float)wsub(wshl(ss, 7), vsf)), 0.0078125f);
   if (RATIO) dv8 = __fmul_rn(dv8, __fadd_rn(U.leak_floor, __fmul_rn(__fsub_rn(1.0f, U.leak_floor), coh)));
-  const int32_t t3 = sr_tick(dv8, hash_uniform(sf, ps ^ 0x33335555));
+  const int32_t t3 = sr_tick(dv8, hash_uniform3(sf, ps, 0x33335555));
   const int32_t new_v = clampi(wadd(vs, t3), -128, 127);
   ss = wsub(ss, wsub(new_v, vs));
   const int32_t sfc = clampi(sf, -32768, 32767);
@@ -513,12 +513,12 @@ __global__ __launch_bounds__(256) void apply_sgd_kernel(SgdArgs a) {
       const int32_t ps = wshl((int32_t)n, 16) ^ (int32_t)k ^ salt;
       sf = wadd(sf, sr_tick(delta_t, hash_uniform(sf, ps)));
       const float c8 = __fmul_rn(__fmul_rn(a.alpha, (float)sf), 0.0078125f);
-      const int32_t t2 = sr_tick(c8, hash_uniform(sf, ps ^ 0x5A5A5A5A));
+      const int32_t t2 = sr_tick(c8, hash_uniform3(sf, ps, 0x5A5A5A5A));
       ss = wadd(ss, t2);
       sf = wsub(sf, wshl(t2, 7));
       const float dv8 =
           __fmul_rn(__fmul_rn(a.alpha_v_fast, (float)wsub(wshl(ss, 7), f.vs * 128)), 0.0078125f);
-      const int32_t t3 = sr_tick(dv8, hash_uniform(sf, ps ^ 0x33335555));
+      const int32_t t3 = sr_tick(dv8, hash_uniform3(sf, ps, 0x33335555));
       const int32_t new_v = clampi(wadd(f.vs, t3), -128, 127);
       if (a.flags & CONCORD_MASS_PRESERVE) ss = wsub(ss, wsub(new_v, f.vs));
       const int32_t sfc = clampi(sf, -32768, 32767), ssc = clampi(ss, -128, 127);

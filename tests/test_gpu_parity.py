@@ -134,6 +134,11 @@ FLAG_SETS = {
     "muon": dict(ratio=True, gf_consol=10.0, muon=True),
     "pow": dict(cohpre=True, precond_p=0.3),
     "sgdlike": dict(precond_p=0.0, trust=0.0, chase=False, track=False, mp=False),
+    # v-hat spread over 60 decades (and exact zeros) with eps = 1e-30: the
+    # square root's argument falls on both sides of 2^-96 within one wave
+    "winner_tiny_v": dict(ratio=True, gf_consol=50.0, eps=1e-30, vspread=True),
+    "bare_tiny_v": dict(cohpre=True, eps=1e-30, vspread=True),
+    "wd_tiny_v": dict(cohpre=True, fixed=False, weight_decay=0.02, wd_sv=0.3, eps=1e-30, vspread=True),
 }
 
 
@@ -148,6 +153,10 @@ def test_apply_adamw_matches_oracle(oracle, name, N, K):
     g = rand_grad_bits(rng, N, K)
     vr = (rng.random(N) * 1e-3 + 1e-7).astype(np.float32)
     vc = (rng.random(K) * 1e-3 + 1e-7).astype(np.float32)
+    if f.get("vspread"):
+        vr = (10.0 ** -rng.uniform(0, 30, N)).astype(np.float32)
+        vc = (10.0 ** -rng.uniform(0, 30, K)).astype(np.float32)
+        vc[::7] = 0.0
     svi = np.array([1.0 / vr.sum()], np.float32)
     cp = rng.random((N, K)).astype(np.float32) if f.get("cohpre") else None
     salt = int(rng.integers(-2 ** 31 + 1, 2 ** 31))
