@@ -821,3 +821,63 @@ def test_layer_muon_drive_bit_exact(oracle):
             assert 0.4 < np.sqrt((dv * dv).mean()) < 1.2
     finally:
         pb.set_ratio_coh(False)
+
+
+def _layer_state(layer):
+    return [host(t) for t in (layer.packed_w, layer.row_exp, layer.col_exp, layer.v_row, layer.v_col,
+                              layer._sum_v_inv, layer._row_max_buf, layer._col_max_buf, layer._reb_seed)]
+
+
+def test_graph_replay_matches_eager_steps():
+    """A HIP graph of one training step (forward, backward with the update,
+    rebalance), replayed with eager work and host syncs between replays,
+    tracks an eager twin bit for bit on every replay."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    torch.manual_seed(12)
+    W0 = torch.randn(1280, 1280) * 0.03
+    x = torch.randn(512, 1280, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    dy = (torch.randn(512, 1280, device=DEV) * 1e-3).to(torch.bfloat16)
+    xe = x.detach().clone().requires_grad_(True)
+    salt = pb._get_step_counter(DEV)
+
+    def make():
+        layer = ca.ConcordLinearPackedB(1280, 1280, bias=True, device=DEV, lr=2e-3)
+        layer.load_weights(W0)
+        return layer
+
+    def step(layer, xin):
+        xin.grad = None
+        layer.bias.grad = None
+        layer(xin).backward(dy)
+        layer.rebalance()
+
+    g_layer, e_layer = make(), make()
+    # the graph layer's warm-up runs on a side stream, as capture requires
+    salt.fill_(7)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            step(g_layer, x)
+    torch.cuda.current_stream().wait_stream(s)
+    sync()
+    salt.fill_(7)
+    for _ in range(2):
+        step(e_layer, xe)
+    sync()
+    for a, b in zip(_layer_state(g_layer), _layer_state(e_layer)):
+        np.testing.assert_array_equal(a, b)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step(g_layer, x)
+    for r in range(4):
+        salt.fill_(100 + r)
+        graph.replay()
+        sync()
+        salt.fill_(100 + r)
+        step(e_layer, xe)
+        sync()
+        for a, b in zip(_layer_state(g_layer) + [host(x.grad), host(g_layer.bias.grad)],
+                        _layer_state(e_layer) + [host(xe.grad), host(e_layer.bias.grad)]):
+            np.testing.assert_array_equal(a, b)
