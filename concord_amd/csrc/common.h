@@ -199,6 +199,12 @@ CONCORD_DEV float pow_p(float x, float p) {
 }
 
 // ---- reductions ------------------------------------------------------------------
+// lane j's value, j wave-uniform (a scalar read; a shuffle would take an LDS
+// round trip, which a serial chain pays once per term)
+CONCORD_DEV float lane_value(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
 CONCORD_DEV int32_t wave_max(int32_t v) {
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));

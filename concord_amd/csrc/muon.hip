@@ -45,12 +45,32 @@ __global__ __launch_bounds__(256) void frob_partials_kernel(const uint16_t* __re
   if (threadIdx.x == 0) part[blockIdx.x] = s[0];
 }
 
-// den = sqrt(sum of the block partials ascending) + 1e-7
+// den = sqrt(sum of the block partials ascending) + 1e-7.  One wave: 16 x 64
+// partials are loaded at a time, then chained in ascending order by reading
+// one lane after another (every lane carries the same running sum).
 __global__ __launch_bounds__(64) void frob_den_kernel(const float* __restrict__ part, int64_t nb, float* den) {
-  if (threadIdx.x != 0) return;
+  constexpr int B = 16;
+  const int lane = threadIdx.x;
   float s = 0.0f;
-  for (int64_t b = 0; b < nb; ++b) s = __fadd_rn(s, part[b]);
-  *den = __fadd_rn(sqrt_rn(s), 1e-7f);
+  for (int64_t c0 = 0; c0 < nb; c0 += 64 * B) {
+    float v[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int64_t i = c0 + 64 * b + lane;
+      v[b] = i < nb ? part[i] : 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int64_t cnt = min((int64_t)64, nb - (c0 + 64 * b));
+      if (cnt == 64) {
+#pragma unroll
+        for (int j = 0; j < 64; ++j) s = __fadd_rn(s, lane_value(v[b], j));
+      } else {
+        for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, lane_value(v[b], j));
+      }
+    }
+  }
+  if (lane == 0) *den = __fadd_rn(sqrt_rn(s), 1e-7f);
 }
 
 // dst[r][c] = bf16(op(src)) over a 64 x 64 tile, where the destination is

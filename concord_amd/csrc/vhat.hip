@@ -123,7 +123,7 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
       const float v = c0 + lane < rb ? __hip_atomic_load(bsum + c0 + lane, __ATOMIC_RELAXED,
                                                         __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
       const int cnt = (int)min((int64_t)64, rb - c0);
-      for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, __shfl(v, j, 64));
+      for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, lane_value(v, j));
     }
     if (lane == 0) {
       *sum_v_inv = __fdiv_rn(1.0f, fmaxf(s, 1e-30f));

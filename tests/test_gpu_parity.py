@@ -746,6 +746,26 @@ def test_muon_ns5_matches_oracle(oracle, N, K):
     assert rel_l2(got, ref) < 2e-2
 
 
+@pytest.mark.parametrize("N,K", [(2048, 5120), (1280, 5120), (333, 1001)])
+def test_muon_frobenius_denominator_bit_exact(oracle, N, K):
+    """The NS5 input scale ||g|| + 1e-7 (block partials, then one wave chaining
+    them in ascending order) equals the oracle's bit for bit; read back from
+    the workspace (layout: X, BX, A, AA, partials, then the denominator)."""
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(N + K)
+    g = oracle.f32_to_bf16_bits_array((rng.standard_normal((N, K)) * 1e-3).astype(np.float32))
+    pb.muon_ns5(dev(g))
+    sync()
+    ws = pb._MUON_WORKSPACES[pb._dev_key(torch.device(DEV))]
+    m, n = min(N, K), max(N, K)
+    r256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    off = 2 * r256(m * n * 2) + 2 * r256(m * m * 2) + r256(-(-N * K // 8192) * 4)
+    den = host(ws[off:off + 4].view(torch.float32))[0]
+    s = oracle.frob_sumsq(g)
+    want = np.float32(np.sqrt(np.float32(s))) + np.float32(1e-7)
+    assert den.view(np.uint32) == np.float32(want).view(np.uint32), (den, want)
+
+
 def test_muon_ns5_full_size_properties(oracle):
     """Config 5 shape (1280 x 5120): the drive's singular values lie in the
     quintic's band times gamma, a power-of-two rescale of g leaves the drive
