@@ -23,6 +23,7 @@ import math
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import _lib as C
 
@@ -869,6 +870,56 @@ class ConcordLinearPackedB(nn.Module):
         return materialize_packed_bf16(self.packed_w, self.row_exp, self.col_exp, out,
                                        self.MANTISSA_BIAS, consolidated=True)
 
+    # -- checkpoint (the buffers registered above travel in state_dict as in
+    # concord/packed_b.py:1445-1486; the extra state adds what the reference
+    # loses on save: the device salt counter of the SR streams, the coh_pre
+    # EMA, which is not a registered buffer, and the optimizer settings) --
+    _CHECKPOINT_FORMAT = 1
+    _CHECKPOINT_KNOBS = ('alpha', 'beta1', 'optimizer_kind', 'weight_decay', 'step_cap', 'v_scale',
+                         'precond_p', 'gf_consol', 'fast_gain', 'alpha_v_fast', 'drift_cancel_C',
+                         'track_adafactor_v', 'adafactor_beta2', 'gf_trust_delta_sq', 'allow_tickdown',
+                         'wd_sv', 'wd_sf', 'mass_preserve_v', 'apply_chase', 'track_rebalance', 'drive')
+
+    def get_extra_state(self):
+        """Resume state beyond the registered buffers: the per-device salt
+        counter (read back once, at save time), coh_pre and the optimizer
+        settings.  Plain tensors and Python scalars only, so the checkpoint
+        loads with torch.load(..., weights_only=True)."""
+        dev = self.packed_w.device
+        return {
+            'format': self._CHECKPOINT_FORMAT,
+            'salt_counter': int(_get_step_counter(dev).item()),
+            'coh_pre': None if self._coh_pre is None else self._coh_pre.detach().clone(),
+            'knobs': {k: getattr(self, k) for k in self._CHECKPOINT_KNOBS},
+        }
+
+    @torch.no_grad()
+    def set_extra_state(self, state):
+        """Restore get_extra_state()'s record after the buffers have loaded:
+        the device salt counter is set to the saved value (it is shared by the
+        device's layers, which all saved the same value), lr / eps follow the
+        loaded device scalars, and the bf16 weight copy is re-materialised."""
+        if not isinstance(state, dict) or state.get('format') != self._CHECKPOINT_FORMAT:
+            raise ValueError("ConcordLinearPackedB: unknown checkpoint extra-state format")
+        dev = self.packed_w.device
+        for k, v in state['knobs'].items():
+            if k in self._CHECKPOINT_KNOBS:
+                if k == 'drive':
+                    self.set_drive(v)
+                else:
+                    setattr(self, k, v)
+        cp = state['coh_pre']
+        if cp is None:
+            self._coh_pre = None
+        else:
+            if tuple(cp.shape) != tuple(self.packed_w.shape):
+                raise ValueError("ConcordLinearPackedB: coh_pre shape does not match the layer")
+            self._coh_pre = cp.to(device=dev, dtype=torch.float32).contiguous()
+        _get_step_counter(dev).fill_(int(state['salt_counter']))
+        self._lr_value = float(self._lr_buf.item())
+        self._eps_value = float(self._eps_buf.item())
+        self._resync_weight_buf()
+
     @torch.no_grad()
     def get_state(self):
         p = self.packed_w
@@ -965,3 +1016,93 @@ class ConcordLinearPackedB(nn.Module):
                          seed_buf=self._reb_seed, allow_tickdown=self.allow_tickdown,
                          row_hwm=self._row_max_hwm, col_hwm=self._col_max_hwm,
                          advance_seed=True)
+
+
+# ---------------------------------------------------------------------------
+# Conv2d on the packed path (concord/packed_b.py:1863-2065)
+# ---------------------------------------------------------------------------
+def _pair(v):
+    return (int(v), int(v)) if isinstance(v, int) else (int(v[0]), int(v[1]))
+
+
+class ConcordConv2dPackedB(ConcordLinearPackedB):
+    """Conv2d variant of ConcordLinearPackedB (concord/packed_b.py:2028-2065):
+    the same packed int32 state, an (out_channels, in_channels * kh * kw)
+    matrix in nn.Conv2d's (c, i, j) flattening.  Where the reference runs
+    cuDNN on the cached bf16 weight, this layer runs the linear layer's own
+    kernels on the patch matrix: the (B * Ho * Wo, in_channels * kh * kw)
+    patches are gathered with torch's unfold (a layout copy; for 1x1, stride
+    1, no padding a channels-last permute), and its autograd adjoint (fold)
+    scatters dx back.  Forward, dgrad, wgrad with v-hat and bias, and the
+    packed update are the HIP entries of the linear path."""
+
+    def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, bias=True,
+                 device='cuda', alpha=0.1, beta1=0.0, lr=0.01, weight_cache=False, drive='vhat'):
+        kh, kw = _pair(kernel_size)
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.kh, self.kw = kh, kw
+        self.stride = stride
+        self.padding = padding
+        super().__init__(in_features=in_channels * kh * kw, out_features=out_channels, bias=bias,
+                         device=device, alpha=alpha, beta1=beta1, lr=lr, weight_cache=weight_cache,
+                         drive=drive)
+
+    def _patches(self, x):
+        B, cin, H, W = x.shape
+        if cin != self.in_channels:
+            raise ValueError(f"ConcordConv2dPackedB: expected {self.in_channels} input channels, "
+                             f"got {cin}")
+        (sh, sw), (ph, pw) = _pair(self.stride), _pair(self.padding)
+        Ho = (H + 2 * ph - self.kh) // sh + 1
+        Wo = (W + 2 * pw - self.kw) // sw + 1
+        if (self.kh, self.kw, sh, sw, ph, pw) == (1, 1, 1, 1, 0, 0):
+            cols = x.permute(0, 2, 3, 1).reshape(B * H * W, cin)
+        else:
+            u = F.unfold(x, (self.kh, self.kw), padding=(ph, pw), stride=(sh, sw))
+            cols = u.transpose(1, 2).reshape(B * Ho * Wo, self.in_features)
+        return cols.contiguous(), Ho, Wo
+
+    def forward(self, x):
+        if x.dim() != 4:
+            raise ValueError("ConcordConv2dPackedB expects (B, C, H, W) input")
+        in_dtype = x.dtype
+        if x.dtype != torch.bfloat16:
+            x = x.to(torch.bfloat16)
+        cols, Ho, Wo = self._patches(x)
+        y = super().forward(cols)
+        B = x.shape[0]
+        y = y.view(B, Ho * Wo, self.out_channels).permute(0, 2, 1).reshape(B, self.out_channels, Ho, Wo)
+        return y.to(in_dtype)
+
+    @property
+    def weight(self):
+        """bf16 (out, in, kh, kw) weight, as nn.Conv2d.weight."""
+        return ConcordLinearPackedB.weight.fget(self).view(self.out_channels, self.in_channels,
+                                                          self.kh, self.kw)
+
+    @torch.no_grad()
+    def load_weights(self, W):
+        """W: (out, in, kh, kw) or its (out, in * kh * kw) flattening."""
+        super().load_weights(W.reshape(self.out_channels, -1))
+
+    @torch.no_grad()
+    def load_weights_finetune(self, W):
+        super().load_weights_finetune(W.reshape(self.out_channels, -1))
+
+
+@torch.no_grad()
+def consolidated_state_dict(layers, names):
+    """Deploy export (notebook/src/concord_winner.py:328-341): each layer's
+    consolidated_weight() (s_fast dropped) as name + '.weight', its bias as
+    name + '.bias'; conv weights as (out, in, kh, kw); plain bf16
+    tensors for safetensors / nn.Linear / nn.Conv2d."""
+    out = {}
+    for name, m in zip(names, layers):
+        W = m.consolidated_weight()
+        if isinstance(m, ConcordConv2dPackedB):
+            W = W.view(m.out_channels, m.in_channels, m.kh, m.kw)
+        out[name + '.weight'] = W
+        if getattr(m, 'bias', None) is not None:
+            out[name + '.bias'] = m.bias.detach().clone()
+    return out

@@ -901,3 +901,67 @@ def test_graph_replay_matches_eager_steps():
         for a, b in zip(_layer_state(g_layer) + [host(x.grad), host(g_layer.bias.grad)],
                         _layer_state(e_layer) + [host(xe.grad), host(e_layer.bias.grad)]):
             np.testing.assert_array_equal(a, b)
+
+
+@pytest.mark.parametrize("cohpre", [True, False])
+def test_checkpoint_resume_bit_exact(cohpre):
+    """state_dict -> torch.save -> torch.load(weights_only=True) -> a fresh
+    layer resumes bit for bit: packed words, exponents, v-hat, watermarks,
+    coh_pre and the SR salt counter all travel (the reference loses the salt
+    and coh_pre)."""
+    import io
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    torch.manual_seed(21)
+    W0 = torch.randn(384, 256) * 0.05
+    xs = [torch.randn(512, 256, device=DEV) for _ in range(5)]
+    salt = pb._get_step_counter(DEV)
+    salt.fill_(1234)
+
+    def steps(layer, batch):
+        for x in batch:
+            xd = x.clone().requires_grad_(True)
+            layer(xd).square().mean().backward()
+            layer.rebalance()
+
+    a = ca.ConcordLinearPackedB(256, 384, bias=True, device=DEV, lr=3e-3)
+    if not cohpre:
+        a.disable_cohpre()
+        a.gf_consol = 20.0
+    a.load_weights(W0)
+    a.lr = 4e-3
+    steps(a, xs[:3])
+    buf = io.BytesIO()
+    torch.save(a.state_dict(), buf)
+    steps(a, xs[3:])
+    sync()
+    want = _layer_state(a) + [host(a.bias)]
+    if cohpre:
+        want.append(host(a._coh_pre))
+
+    buf.seek(0)
+    sd = torch.load(buf, weights_only=True)
+    b = ca.ConcordLinearPackedB(256, 384, bias=True, device=DEV, lr=1e-1)
+    salt.fill_(0)
+    b.load_state_dict(sd)
+    assert b.lr == pytest.approx(4e-3) and b.gf_consol == a.gf_consol
+    assert (b._coh_pre is None) == (not cohpre)
+    steps(b, xs[3:])
+    sync()
+    got = _layer_state(b) + [host(b.bias)]
+    if cohpre:
+        got.append(host(b._coh_pre))
+    for u, v in zip(want, got):
+        np.testing.assert_array_equal(u, v)
+
+
+def test_consolidated_state_dict_matches_layers():
+    import concord_amd as ca
+    torch.manual_seed(22)
+    layers = [ca.ConcordLinearPackedB(128, 64, bias=True, device=DEV),
+              ca.ConcordLinearPackedB(64, 32, bias=False, device=DEV)]
+    sd = ca.consolidated_state_dict(layers, ["a", "b"])
+    assert set(sd) == {"a.weight", "a.bias", "b.weight"}
+    np.testing.assert_array_equal(host(sd["a.weight"]), host(layers[0].consolidated_weight()))
+    np.testing.assert_array_equal(host(sd["b.weight"]), host(layers[1].consolidated_weight()))
+    assert sd["a.weight"].dtype == torch.bfloat16 and sd["a.weight"].shape == (64, 128)
