@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "concord_amd.h"
 
 #define CONCORD_DEV __device__ __forceinline__

@@ -1091,6 +1091,109 @@ class ConcordConv2dPackedB(ConcordLinearPackedB):
         super().load_weights_finetune(W.reshape(self.out_channels, -1))
 
 
+# ---------------------------------------------------------------------------
+# Multi-layer statistics: gated rebalance and the coherence meter
+# (notebook/src/concord_winner.py:206-262, concord/packed_b.py:2081-2106)
+# ---------------------------------------------------------------------------
+_STATS_WORKSPACES = {}
+
+
+def _stats_workspace(device, n_watermarks, n_words):
+    key = _dev_key(device)
+    need = int(C.lib().concord_stats_workspace_bytes(int(n_watermarks), int(n_words)))
+    ws = _STATS_WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=key)
+        _STATS_WORKSPACES[key] = ws
+    return ws
+
+
+def gate_coherence_from_fields(s_fast, s_slow_i8, v_slow_i8, drift_cancel_C):
+    """The update's FIXED_COH Wiener gain from unpacked integer fields given
+    as float tensors (concord/packed_b.py:2081-2091); the exponents cancel.
+    Elementwise tensor helper, as in the reference."""
+    d_sv = (s_slow_i8 - v_slow_i8) * 128.0
+    sig = drift_cancel_C * d_sv
+    noise = s_fast - sig
+    sig2 = sig * sig
+    return sig2 / (sig2 + noise * noise + 1e-30)
+
+
+@torch.no_grad()
+def measure_coherence(layer):
+    """Mean gate coherence of one Concord layer read from its packed words
+    (concord/packed_b.py:2094-2106): one HIP reduction in a fixed order
+    (concord_coherence_sum) and one host read of the sum."""
+    p = layer.packed_w
+    N, K = p.shape
+    out = torch.empty(1, dtype=torch.float32, device=p.device)
+    ws = _stats_workspace(p.device, 0, N * K)
+    C.check(C.lib().concord_coherence_sum(C.ptr(p), p.stride(0), N, K, float(layer.drift_cancel_C),
+                                          C.ptr(out), C.ptr(ws), ws.numel(), C.stream_of(p.device)),
+            "coherence_sum")
+    return float(out.item()) / float(max(N * K, 1))
+
+
+class GatedRebalance:
+    """Fire rebalance only when some layer's mantissa crosses MAX_M
+    (notebook/src/concord_winner.py:206-262).  Every layer's row / column
+    watermark buffers become slices of two shared slabs; one call is one HIP
+    reduction over both slabs (concord_watermark_peak) and one host read, and
+    the per-layer rebalance launches run only when the peak exceeds MAX_M.
+    Drop-in for `for m in layers: m.rebalance()`: call the instance after
+    backward.  Returns True when it fired."""
+
+    def __init__(self, layers):
+        self.layers = [m for m in (layers or []) if hasattr(m, "rebalance")]
+        self.MAX_M = max((getattr(m, "MAX_M", 24000) for m in self.layers), default=24000)
+        self.row_all = None
+        self.col_all = None
+        self._peak = None
+        self.fires = 0
+        self.calls = 0
+
+    def _wire(self):
+        """Repoint the per-layer watermark buffers at slices of the shared
+        slabs (once, after the first backward; the slabs start at zero)."""
+        dev = self.layers[0].packed_w.device
+        rs = [m._row_max_buf.shape[0] for m in self.layers]
+        cs = [m._col_max_buf.shape[0] for m in self.layers]
+        self.row_all = torch.zeros(sum(rs), dtype=torch.int32, device=dev)
+        self.col_all = torch.zeros(sum(cs), dtype=torch.int32, device=dev)
+        self._peak = torch.zeros(1, dtype=torch.int32, device=dev)
+        ro = co = 0
+        for m, n, k in zip(self.layers, rs, cs):
+            m._row_max_buf = self.row_all[ro:ro + n]
+            ro += n
+            m._col_max_buf = self.col_all[co:co + k]
+            co += k
+        _stats_workspace(dev, ro + co, 0)
+
+    def peak(self):
+        """Device tensor with the largest watermark of every layer (no host read)."""
+        ws = _stats_workspace(self.row_all.device, self.row_all.numel() + self.col_all.numel(), 0)
+        C.check(C.lib().concord_watermark_peak(
+            C.ptr(self.row_all), self.row_all.numel(), C.ptr(self.col_all), self.col_all.numel(),
+            C.ptr(self._peak), C.ptr(ws), ws.numel(), C.stream_of(self.row_all.device)), "watermark_peak")
+        return self._peak
+
+    def __call__(self):
+        if not self.layers:
+            return False
+        self.calls += 1
+        if self.row_all is None:
+            if getattr(self.layers[0], "_row_max_buf", None) is None:
+                return False
+            self._wire()
+            return False
+        if int(self.peak().item()) > self.MAX_M:
+            for m in self.layers:
+                m.rebalance()
+            self.fires += 1
+            return True
+        return False
+
+
 @torch.no_grad()
 def consolidated_state_dict(layers, names):
     """Deploy export (notebook/src/concord_winner.py:328-341): each layer's

@@ -224,6 +224,29 @@ int concord_bias_grad(const uint16_t* dy, int64_t ld_dy, int64_t M, int64_t N,
                       uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* Multi-layer statistics over the packed state.  workspace:
+ * concord_stats_workspace_bytes(n_watermarks, n_words) bytes (no zeroing
+ * needed); each call is two launches and writes one scalar.
+ *
+ * concord_watermark_peak: *out = max of rows[0, n_rows) and cols[0, n_cols)
+ * (the update's |m_eff| watermarks, all >= 0).  This is the one reduction of
+ * GatedRebalance.__call__ over the shared row / column watermark slabs of every
+ * layer (notebook/src/concord_winner.py:206-262: torch.maximum(row_all.max(),
+ * col_all.max())); rebalance runs only when it exceeds MAX_M.
+ *
+ * concord_coherence_sum: *out_sum = sum over the N x K words of the gate's
+ * Wiener gain sig^2 / (sig^2 + noise^2 + 1e-30), sig = C * 128 (s_slow -
+ * v_slow), noise = s_fast - sig (gate_coherence_from_fields,
+ * concord/packed_b.py:2081-2091); the layer mean of measure_coherence
+ * (2094-2106) is out_sum / (N K).  Fixed order: 8192-word blocks, lanes
+ * chaining a stride-256 set each, a halving tree, blocks ascending. */
+size_t concord_stats_workspace_bytes(int64_t n_watermarks, int64_t n_words);
+int concord_watermark_peak(const int32_t* rows, int64_t n_rows, const int32_t* cols, int64_t n_cols,
+                           int32_t* out, void* workspace, size_t workspace_bytes, void* stream);
+int concord_coherence_sum(const int32_t* packed, int64_t ld_p, int64_t N, int64_t K,
+                          float drift_cancel_C, float* out_sum, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

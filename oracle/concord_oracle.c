@@ -668,6 +668,36 @@ float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K) {
     return acc;
 }
 
+/* concord/packed_b.py:2081-2091: sig = C * (s_slow - v_slow) * 128, noise =
+ * s_fast - sig, coh = sig^2 / (sig^2 + noise^2 + 1e-30) (left to right);
+ * summed like oracle_frob_sumsq: 8192-word blocks, lane t chains words
+ * b0 + t + 256 i, a halving tree over the 256 lanes, blocks ascending */
+float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C) {
+    const int64_t total = N * K;
+    float acc = 0.0f;
+    for (int64_t b0 = 0; b0 < total; b0 += 8192) {
+        float part[256];
+        for (int t = 0; t < 256; ++t) {
+            float s = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                const int64_t e = b0 + t + 256 * i;
+                if (e >= total) continue;
+                const int32_t w = packed[e];
+                const int32_t sf = w >> 16, ss = (int8_t)(w >> 8), vs = (int8_t)w;
+                const float sig = C * (float)((ss - vs) * 128);
+                const float noise = (float)sf - sig;
+                const float sig2 = sig * sig;
+                s = s + sig2 / ((sig2 + noise * noise) + 1e-30f);
+            }
+            part[t] = s;
+        }
+        for (int h = 128; h >= 1; h >>= 1)
+            for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
+        acc = acc + part[0];
+    }
+    return acc;
+}
+
 static inline float rbf(float f) { return bf16_to_f32(oracle_f32_to_bf16(f)); }
 
 /* C[I][J] = bf16(sum_r A(i,r) B(r,j)); A(i,r) = a[i*lda_i + r*lda_r], likewise B */

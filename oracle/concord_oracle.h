@@ -107,6 +107,9 @@ void oracle_load_weights(const float* W, int64_t N, int64_t K,
                          int32_t* packed, int8_t* row_exp, int8_t* col_exp);
 
 float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K);
+/* sum of gate_coherence_from_fields (concord/packed_b.py:2081-2091) over the
+ * N x K words, in the library's block / lane / tree order */
+float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C);
 void oracle_muon_ns5(const uint16_t* g, int64_t N, int64_t K, float gamma, uint16_t* out);
 
 void oracle_set_threads(int n);

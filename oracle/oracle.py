@@ -80,6 +80,8 @@ def lib():
         L.oracle_i8_medians.argtypes = [P, i64, i64, P, P]
         L.oracle_frob_sumsq.restype = f32
         L.oracle_frob_sumsq.argtypes = [P, i64, i64]
+        L.oracle_coherence_sum.restype = f32
+        L.oracle_coherence_sum.argtypes = [P, i64, i64, f32]
         L.oracle_muon_ns5.argtypes = [P, i64, i64, f32, P]
         L.oracle_rebalance.argtypes = [P, P, P, P, P, P, P, i64, i64, i32, i32, i32,
                                        i32, ctypes.c_int]
@@ -192,6 +194,12 @@ def vhat_ema(grad_bf16, v_row, v_col, beta2=0.999):
 def frob_sumsq(grad_bf16):
     g = np.ascontiguousarray(grad_bf16, dtype=np.uint16)
     return np.float32(lib().oracle_frob_sumsq(_p(g), g.shape[0], g.shape[1]))
+
+
+def coherence_sum(packed, drift_cancel_C):
+    """Sum of the gate's Wiener gain over the words (fixed library order)."""
+    p = np.ascontiguousarray(packed, dtype=np.int32)
+    return np.float32(lib().oracle_coherence_sum(_p(p), p.shape[0], p.shape[1], float(drift_cancel_C)))
 
 
 def muon_ns5(grad_bf16, gamma=None):

@@ -965,3 +965,114 @@ def test_consolidated_state_dict_matches_layers():
     np.testing.assert_array_equal(host(sd["a.weight"]), host(layers[0].consolidated_weight()))
     np.testing.assert_array_equal(host(sd["b.weight"]), host(layers[1].consolidated_weight()))
     assert sd["a.weight"].dtype == torch.bfloat16 and sd["a.weight"].shape == (64, 128)
+
+
+# ---------------------------------------------------------------- multi-layer statistics
+
+@pytest.mark.parametrize("N,K,ld", [(300, 777, 777), (5120, 1280, 1280), (33, 100, 128), (1, 5, 5)])
+def test_coherence_sum_bit_exact(oracle, N, K, ld):
+    from concord_amd import _lib as C
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(N + K)
+    words = rng.integers(-2 ** 31, 2 ** 31, (N, ld), dtype=np.int64).astype(np.int32)
+    Cc = 0.018036072144288578
+    p = dev(words)
+    out = torch.empty(1, dtype=torch.float32, device=DEV)
+    ws = pb._stats_workspace(torch.device(DEV), 0, N * K)
+    assert C.lib().concord_coherence_sum(C.ptr(p), ld, N, K, Cc, C.ptr(out), C.ptr(ws), ws.numel(),
+                                         C.stream_of(torch.device(DEV))) == 0
+    sync()
+    want = oracle.coherence_sum(np.ascontiguousarray(words[:, :K]), Cc)
+    assert host(out)[0].view(np.uint32) == np.float32(want).view(np.uint32)
+
+
+def test_measure_coherence_layer(oracle):
+    import concord_amd as ca
+    torch.manual_seed(5)
+    layer = ca.ConcordLinearPackedB(256, 384, device=DEV)
+    x = torch.randn(512, 256, device=DEV).requires_grad_(True)
+    for _ in range(3):
+        layer(x).square().mean().backward()
+    sync()
+    got = ca.measure_coherence(layer)
+    want = float(oracle.coherence_sum(host(layer.packed_w), layer.drift_cancel_C)) / (256 * 384)
+    assert got == want and 0.0 <= got <= 1.0
+
+
+@pytest.mark.parametrize("nr,nc", [(0, 0), (7, 0), (0, 9), (5000, 70000), (123457, 3)])
+def test_watermark_peak(nr, nc):
+    from concord_amd import _lib as C
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(nr * 7 + nc)
+    r = rng.integers(0, 30000, max(nr, 1)).astype(np.int32)[:nr]
+    c = rng.integers(0, 30000, max(nc, 1)).astype(np.int32)[:nc]
+    rd, cd = dev(r) if nr else torch.zeros(1, dtype=torch.int32, device=DEV), \
+        dev(c) if nc else torch.zeros(1, dtype=torch.int32, device=DEV)
+    out = torch.full((1,), -5, dtype=torch.int32, device=DEV)
+    ws = pb._stats_workspace(torch.device(DEV), nr + nc, 0)
+    assert C.lib().concord_watermark_peak(C.ptr(rd), nr, C.ptr(cd), nc, C.ptr(out), C.ptr(ws), ws.numel(),
+                                          C.stream_of(torch.device(DEV))) == 0
+    sync()
+    want = max([0] + ([int(r.max())] if nr else []) + ([int(c.max())] if nc else []))
+    assert int(host(out)[0]) == want
+
+
+def test_gated_rebalance_matches_host_gate():
+    """GatedRebalance (shared watermark slabs, one device reduction) takes the
+    same decisions and leaves every layer bit-identical to the same gate
+    evaluated on the host (max of every layer's watermarks > MAX_M, then the
+    per-layer rebalance loop), over several training steps."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    shapes = [(256, 384), (384, 128), (128, 256)]   # (in, out), chained
+    torch.manual_seed(31)
+    Ws = [torch.randn(n, k) / k ** 0.5 for k, n in shapes]
+    xs = [torch.randn(300, shapes[0][0], device=DEV) for _ in range(4)]
+    salt = pb._get_step_counter(DEV)
+    results, decisions = [], []
+    for gated in (True, False):
+        layers = [ca.ConcordLinearPackedB(k, n, bias=False, device=DEV, lr=5e-3) for k, n in shapes]
+        for m, W in zip(layers, Ws):
+            m.load_weights(W)
+        gate = ca.GatedRebalance(layers)
+        fired = []
+        for i, x in enumerate(xs):
+            salt.fill_(70 + i)
+            h = x.clone().requires_grad_(True)
+            for m in layers:
+                h = m(h)
+            h.square().mean().backward()
+            if gated:
+                fired.append(gate())
+            elif i == 0:
+                fired.append(False)   # the gate's first call only wires the slabs
+            else:
+                peak = max(int(t.max().item()) for m in layers for t in (m._row_max_buf, m._col_max_buf))
+                fired.append(peak > m.MAX_M)
+                if fired[-1]:
+                    for m in layers:
+                        m.rebalance()
+        sync()
+        decisions.append(fired)
+        results.append([host(t) for m in layers for t in (m.packed_w, m.row_exp, m.col_exp, m._reb_seed)])
+    assert decisions[0] == decisions[1]
+    for a, b in zip(*results):
+        np.testing.assert_array_equal(a, b)
+
+
+def test_gated_rebalance_gate_logic():
+    """Below MAX_M nothing runs (no seed advance); one watermark above it
+    fires the rebalance of every layer."""
+    import concord_amd as ca
+    layers = [ca.ConcordLinearPackedB(64, 96, bias=False, device=DEV),
+              ca.ConcordLinearPackedB(96, 32, bias=False, device=DEV)]
+    gate = ca.GatedRebalance(layers)
+    assert gate() is False and gate.row_all is not None
+    seeds = [int(host(m._reb_seed)[0]) for m in layers]
+    gate.row_all.fill_(gate.MAX_M)
+    gate.col_all.fill_(7)
+    assert gate() is False
+    assert [int(host(m._reb_seed)[0]) for m in layers] == seeds
+    gate.col_all[40] = gate.MAX_M + 1
+    assert gate() is True and gate.fires == 1
+    assert [int(host(m._reb_seed)[0]) for m in layers] == [v + 1 for v in seeds]

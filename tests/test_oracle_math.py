@@ -545,3 +545,50 @@ def test_ns5_transpose_and_scale(oracle):
     # a power-of-two scale of g changes nothing but the norm's exponent
     g4 = oracle.f32_to_bf16_bits_array(g * 4.0)
     np.testing.assert_array_equal(oracle.muon_ns5(g4, 1.0), oracle.muon_ns5(gb, 1.0))
+
+
+# ---------------------------------------------------------------- coherence meter
+
+def _coh_f32(packed, C):
+    p = packed.astype(np.int64)
+    sf = (packed >> 16).astype(np.float32)
+    ss = ((packed << 16) >> 24).astype(np.int64)
+    vs = ((packed << 24) >> 24).astype(np.int64)
+    sig = np.float32(C) * ((ss - vs) * 128).astype(np.float32)
+    noise = sf - sig
+    sig2 = sig * sig
+    return sig2 / ((sig2 + noise * noise) + np.float32(1e-30))
+
+
+def test_coherence_sum_closed_forms(oracle):
+    """Zero state -> 0; s_fast = 0 with s_slow != v_slow -> every word's gain
+    is exactly 1/2 (noise = -sig); s_slow == v_slow -> 0 whatever s_fast."""
+    C = 0.018036072144288578
+    assert oracle.coherence_sum(np.zeros((7, 300), np.int32), C) == 0.0
+    rng = np.random.default_rng(0)
+    ss = rng.integers(-128, 128, (64, 200))
+    vs = (ss + rng.integers(1, 100, (64, 200)) + 128) % 256 - 128
+    assert (ss != vs).all()
+    words = (((ss & 0xFF) << 8) | (vs & 0xFF)).astype(np.int32)
+    assert oracle.coherence_sum(words, C) == np.float32(0.5 * words.size)
+    sf = rng.integers(-32768, 32768, (64, 200))
+    words = (((sf & 0xFFFF) << 16) | ((ss & 0xFF) << 8) | (ss & 0xFF)).astype(np.uint32).view(np.int32)
+    assert oracle.coherence_sum(words, C) == 0.0
+
+
+def test_coherence_sum_order_and_value(oracle):
+    """A single block smaller than the lane count is the halving tree of the
+    per-word gains; larger inputs agree with a float64 sum of the same float32
+    gains (the association only moves low bits)."""
+    C = 0.018036072144288578
+    rng = np.random.default_rng(1)
+    small = rng.integers(-2 ** 31, 2 ** 31, (3, 50), dtype=np.int64).astype(np.int32)
+    g = np.zeros(256, np.float32)
+    g[:small.size] = _coh_f32(small, C).ravel()
+    for h in (128, 64, 32, 16, 8, 4, 2, 1):
+        g[:h] = g[:h] + g[h:2 * h]
+    assert oracle.coherence_sum(small, C) == g[0]
+    big = rng.integers(-2 ** 31, 2 ** 31, (300, 777), dtype=np.int64).astype(np.int32)
+    want = _coh_f32(big, C).astype(np.float64).sum()
+    got = float(oracle.coherence_sum(big, C))
+    assert abs(got - want) <= 1e-5 * want
