@@ -50,6 +50,7 @@ _SIGS = {
     "concord_workspace_bytes": (_Z, [_I, _I, _I]),
     "concord_salt_bump": (ctypes.c_int, [_P, _P]),
     "concord_materialize": (ctypes.c_int, [_P, _I, _P, _P, _I, _I, _i, ctypes.c_int, _P, _I, _P]),
+    "concord_materialize_gated": (ctypes.c_int, [_P, _I, _P, _P, _I, _I, _i, _F, _P, _I, _P]),
     "concord_apply_adamw": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
                                            _I, _I, _I, ctypes.POINTER(UpdateParams),
                                            ctypes.POINTER(DeviceScalars), ctypes.c_uint32, _P]),

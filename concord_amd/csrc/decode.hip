@@ -44,6 +44,24 @@ __global__ __launch_bounds__(256) void materialize_kernel(const int32_t* __restr
   }
 }
 
+// The forward weight with s_fast smoothly gated out (concord/packed_b.py:1763-1772):
+// bf16(((128 ss + g sf) + 128 vs) * 2^(row_exp + col_exp - bias)), fp32 ops in
+// that order.  One lane per word.
+__global__ __launch_bounds__(256) void materialize_gated_kernel(const int32_t* __restrict__ packed,
+                                                                int64_t ld_p, const int8_t* row_exp,
+                                                                const int8_t* col_exp, int64_t N,
+                                                                int64_t K, int32_t bias, float g,
+                                                                uint16_t* __restrict__ out,
+                                                                int64_t ld_o) {
+  const int64_t n = blockIdx.y;
+  const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (k >= K) return;
+  const Fields f = unpack(packed[n * ld_p + k]);
+  const float m = __fadd_rn(__fadd_rn((float)(f.ss * 128), __fmul_rn(g, (float)f.sf)), (float)(f.vs * 128));
+  const float v = __fmul_rn(m, exp2i((int32_t)row_exp[n] - bias + (int32_t)col_exp[k]));
+  out[n * ld_o + k] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+}
+
 // One block per row: row max |W| (exact), exponent, then quantise the row.
 // row_exp = clamp(ceil(log2(max) + 1)) evaluated exactly from the exponent
 // field: a power of two 2^q gives q + 1, anything in (2^q, 2^(q+1)) gives q + 2.
@@ -118,6 +136,20 @@ extern "C" int concord_materialize(const int32_t* packed, int64_t ld_p, const in
   }
 #undef LAUNCH
   return launch_status("materialize");
+}
+
+extern "C" int concord_materialize_gated(const int32_t* packed, int64_t ld_p, const int8_t* row_exp,
+                                         const int8_t* col_exp, int64_t N, int64_t K,
+                                         int32_t mantissa_bias, float fast_gain, uint16_t* out,
+                                         int64_t ld_out, void* stream) {
+  CONCORD_CHECK(N >= 0 && K >= 0 && N < (1LL << 31), "concord_materialize_gated: bad size");
+  if (N == 0 || K == 0) return CONCORD_OK;
+  CONCORD_CHECK(packed && row_exp && col_exp && out, "concord_materialize_gated: NULL argument");
+  CONCORD_CHECK(ld_p >= K && ld_out >= K, "concord_materialize_gated: leading dimension < K");
+  hipLaunchKernelGGL(materialize_gated_kernel, dim3((unsigned)cdiv(K, 256), (unsigned)N), dim3(256), 0,
+                     (hipStream_t)stream, packed, ld_p, row_exp, col_exp, N, K, mantissa_bias, fast_gain, out,
+                     ld_out);
+  return launch_status("materialize_gated");
 }
 
 extern "C" int concord_load_weights(const float* W, int64_t ld_w, int64_t N, int64_t K,

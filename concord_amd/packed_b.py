@@ -978,17 +978,13 @@ class ConcordLinearPackedB(nn.Module):
         if self.fast_gain < 1.0:
             # gate s_fast out of the forward weight (1762-1772); the GEMMs then read
             # the gated bf16 copy, the packed state keeps the full s_fast
-            with torch.no_grad():
-                pw = self.packed_w
-                sf = (pw >> 16).to(torch.float32)
-                ss = ((pw << 16) >> 24).to(torch.float32)
-                vs = ((pw << 24) >> 24).to(torch.float32)
-                exp = (self.row_exp.float()[:, None] + self.col_exp.float()[None, :]
-                       - self.MANTISSA_BIAS)
-                m_gated = (ss * 128.0 + self.fast_gain * sf + vs * 128.0) * torch.exp2(exp)
-                if wbuf is None:
-                    wbuf = torch.empty(pw.shape, dtype=torch.bfloat16, device=pw.device)
-                wbuf.copy_(m_gated.to(torch.bfloat16))
+            pw = self.packed_w
+            if wbuf is None:
+                wbuf = torch.empty(pw.shape, dtype=torch.bfloat16, device=pw.device)
+            C.check(C.lib().concord_materialize_gated(
+                C.ptr(pw), pw.stride(0), C.ptr(self.row_exp), C.ptr(self.col_exp), pw.shape[0],
+                pw.shape[1], self.MANTISSA_BIAS, float(self.fast_gain), C.ptr(wbuf), wbuf.stride(0),
+                C.stream_of(pw.device)), "materialize_gated")
         y = FusedConcordLinearPackedB.apply(
             x, self.packed_w, self.row_exp, self.col_exp, self.bias,
             self._lr_buf, self.alpha, self.beta1, self.MANTISSA_BIAS,

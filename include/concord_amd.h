@@ -92,6 +92,14 @@ int concord_materialize(const int32_t* packed, int64_t ld_p, const int8_t* row_e
                         const int8_t* col_exp, int64_t N, int64_t K, int32_t mantissa_bias,
                         int consolidated, uint16_t* out, int64_t ld_out, void* stream);
 
+/* The forward weight with s_fast gated by fast_gain in [0, 1):
+ * bf16(((128 s_slow + fast_gain s_fast) + 128 v_slow) * 2^(row_exp + col_exp -
+ * mantissa_bias)), fp32 ops in that order.  Replaces the torch re-materialise
+ * branch of ConcordLinearPackedB.forward, concord/packed_b.py:1763-1772. */
+int concord_materialize_gated(const int32_t* packed, int64_t ld_p, const int8_t* row_exp,
+                              const int8_t* col_exp, int64_t N, int64_t K, int32_t mantissa_bias,
+                              float fast_gain, uint16_t* out, int64_t ld_out, void* stream);
+
 /* The packed optimizer update with a supplied bf16 gradient: apply_packed_adamw
  * + _apply_packed_adamw_kernel, concord/packed_b.py:863-951 and 422-703
  * (prototype extension notebook/src/prototype_packed_b.py:454-778 under

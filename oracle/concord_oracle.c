@@ -229,6 +229,24 @@ void oracle_materialize(const int32_t* packed, const int8_t* row_exp,
     }
 }
 
+/* concord/packed_b.py:1763-1772 (fast_gain < 1): m_gated = (ss*128 + fg*sf +
+ * vs*128) * exp2(exp) in float32, left to right, then .to(bfloat16) */
+void oracle_materialize_gated(const int32_t* packed, const int8_t* row_exp,
+                              const int8_t* col_exp, int64_t N, int64_t K,
+                              int32_t mantissa_bias, float fast_gain,
+                              uint16_t* out) {
+#pragma omp parallel for schedule(static)
+    for (int64_t n = 0; n < N; ++n) {
+        for (int64_t k = 0; k < K; ++k) {
+            int32_t sf, ss, vs;
+            unpack(packed[n * K + k], &sf, &ss, &vs);
+            const float m = ((float)(ss * 128) + fast_gain * (float)sf) + (float)(vs * 128);
+            const float sc = exp2i((int32_t)row_exp[n] + (int32_t)col_exp[k] - mantissa_bias);
+            out[n * K + k] = oracle_f32_to_bf16(m * sc);
+        }
+    }
+}
+
 /* ---- A4: the packed optimizer update --------------------------------------
  * Canonical: concord/packed_b.py:422-703 (_apply_packed_adamw_kernel).
  * With OR_PROTO_CONSF: notebook/src/prototype_packed_b.py:454-778 (consf

@@ -72,6 +72,11 @@ void oracle_materialize(const int32_t* packed, const int8_t* row_exp,
                         const int8_t* col_exp, int64_t N, int64_t K,
                         int32_t mantissa_bias, int consolidated,
                         uint16_t* out_bf16);
+/* concord/packed_b.py:1763-1772: bf16(((ss*128 + g*sf) + vs*128) * 2^exp) */
+void oracle_materialize_gated(const int32_t* packed, const int8_t* row_exp,
+                              const int8_t* col_exp, int64_t N, int64_t K,
+                              int32_t mantissa_bias, float fast_gain,
+                              uint16_t* out_bf16);
 
 void oracle_apply_adamw(int32_t* packed, const uint16_t* grad_bf16,
                         uint16_t* weight_bf16, const int8_t* row_exp,

@@ -72,6 +72,7 @@ def lib():
         L.oracle_drift_cancel_C.restype = f64
         L.oracle_drift_cancel_C.argtypes = [f64, f64, f64, ctypes.c_int, ctypes.c_int]
         L.oracle_materialize.argtypes = [P, P, P, i64, i64, i32, ctypes.c_int, P]
+        L.oracle_materialize_gated.argtypes = [P, P, P, i64, i64, i32, f32, P]
         L.oracle_apply_adamw.argtypes = [P, P, P, P, P, P, P, P, P, f32, P, i64, i64,
                                          ctypes.POINTER(UpdateParams),
                                          ctypes.POINTER(UpdateScalars), u32]
@@ -138,6 +139,14 @@ def materialize(packed, row_exp, col_exp, mantissa_bias=15, consolidated=False):
     out = np.empty((N, K), dtype=np.uint16)
     lib().oracle_materialize(_p(packed), _p(row_exp), _p(col_exp), N, K,
                              int(mantissa_bias), int(bool(consolidated)), _p(out))
+    return out
+
+
+def materialize_gated(packed, row_exp, col_exp, fast_gain, mantissa_bias=15):
+    N, K = packed.shape
+    out = np.empty((N, K), dtype=np.uint16)
+    lib().oracle_materialize_gated(_p(np.ascontiguousarray(packed, dtype=np.int32)), _p(row_exp),
+                                   _p(col_exp), N, K, int(mantissa_bias), float(fast_gain), _p(out))
     return out
 
 

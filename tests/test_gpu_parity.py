@@ -1076,3 +1076,34 @@ def test_gated_rebalance_gate_logic():
     gate.col_all[40] = gate.MAX_M + 1
     assert gate() is True and gate.fires == 1
     assert [int(host(m._reb_seed)[0]) for m in layers] == [v + 1 for v in seeds]
+
+
+@pytest.mark.parametrize("gain", [0.0, 0.37, 0.999])
+def test_materialize_gated_bit_exact(oracle, gain):
+    from concord_amd import _lib as C
+    rng = np.random.default_rng(int(gain * 1000))
+    N, K = 97, 1030
+    packed = rng.integers(-2 ** 31, 2 ** 31, (N, K), dtype=np.int64).astype(np.int32)
+    re = rng.integers(-8, 8, N).astype(np.int8)
+    ce = rng.integers(-8, 8, K).astype(np.int8)
+    out = torch.empty((N, K), dtype=torch.bfloat16, device=DEV)
+    assert C.lib().concord_materialize_gated(C.ptr(dev(packed)), K, C.ptr(dev(re)), C.ptr(dev(ce)), N, K, 15,
+                                             gain, C.ptr(out), K, C.stream_of(torch.device(DEV))) == 0
+    sync()
+    np.testing.assert_array_equal(host(out).view(np.uint16), oracle.materialize_gated(packed, re, ce, gain))
+
+
+def test_layer_fast_gain_forward(oracle):
+    """fast_gain < 1: the forward multiplies by the gated weight (within the
+    GEMM tolerance of an fp32 product with the oracle's gated weight)."""
+    import concord_amd as ca
+    torch.manual_seed(8)
+    layer = ca.ConcordLinearPackedB(256, 192, bias=False, device=DEV)
+    layer.fast_gain = 0.25
+    x = torch.randn(300, 256, device=DEV)
+    y = layer(x)
+    sync()
+    Wg = oracle.bf16_bits_to_f32(oracle.materialize_gated(host(layer.packed_w), host(layer.row_exp),
+                                                          host(layer.col_exp), 0.25)).astype(np.float64)
+    ref = host(x.to(torch.bfloat16).float()).astype(np.float64) @ Wg.T
+    assert rel_l2(host(y.float()).astype(np.float64), ref) < 1e-2

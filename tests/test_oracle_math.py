@@ -592,3 +592,27 @@ def test_coherence_sum_order_and_value(oracle):
     want = _coh_f32(big, C).astype(np.float64).sum()
     got = float(oracle.coherence_sum(big, C))
     assert abs(got - want) <= 1e-5 * want
+
+
+def test_materialize_gated_closed_forms(oracle):
+    """fast_gain = 1 is the live weight and 0 the consolidated one exactly
+    (every partial sum is an integer below 2^24); other gains follow the
+    reference's float32 expression ((128 ss + g sf) + 128 vs) * 2^e, RNE."""
+    rng = np.random.default_rng(4)
+    N, K = 40, 70
+    packed = rng.integers(-2 ** 31, 2 ** 31, (N, K), dtype=np.int64).astype(np.int32)
+    re = rng.integers(-8, 8, N).astype(np.int8)
+    ce = rng.integers(-8, 8, K).astype(np.int8)
+    np.testing.assert_array_equal(oracle.materialize_gated(packed, re, ce, 1.0),
+                                  oracle.materialize(packed, re, ce))
+    np.testing.assert_array_equal(oracle.materialize_gated(packed, re, ce, 0.0),
+                                  oracle.materialize(packed, re, ce, consolidated=True))
+    g = np.float32(0.37)
+    sf = (packed >> 16).astype(np.float32)
+    ss = ((packed << 16) >> 24).astype(np.float32)
+    vs = ((packed << 24) >> 24).astype(np.float32)
+    m = (ss * np.float32(128) + g * sf) + vs * np.float32(128)
+    e = (re.astype(np.int32)[:, None] + ce.astype(np.int32)[None, :] - 15).astype(np.float32)
+    v = (m * np.exp2(e).astype(np.float32)).astype(np.float32)
+    want = oracle.f32_to_bf16_bits_array(v)
+    np.testing.assert_array_equal(oracle.materialize_gated(packed, re, ce, 0.37), want)
