@@ -20,6 +20,10 @@ from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
 step on the host: torch fp32 GEMMs + the CPU oracle's v-hat / update /
 rebalance.
 
+The step is timed from a HIP graph holding 5 consecutive steps (--graph-steps),
+replayed back to back; every step's kernels run, only the replay launch is
+shared by 5 steps.
+
 `--only KERNEL` runs one entry of the step `--reps` times and exits (the
 command the committed rocprofv3 summaries were taken with); KERNEL = fwd,
 dgrad, wgrad, wgrad_vhat, vhat, update, materialize, or copy (a 256 MiB
@@ -138,9 +142,9 @@ def cpu_baseline(threads):
                       f"(fwd, dgrad, wgrad) + oracle v-hat, update, rebalance"}
 
 
-def _graph_ms(step, warmup, steps, torch):
-    """Average time of one step replayed from a HIP graph (events on the
-    launching stream)."""
+def _graph_ms(step, warmup, steps, torch, per_graph=1):
+    """Average time of one step replayed from a HIP graph of per_graph steps
+    (events on the launching stream)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -149,21 +153,23 @@ def _graph_ms(step, warmup, steps, torch):
     torch.cuda.current_stream().wait_stream(s)
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        step()
-    for _ in range(warmup):
+        for _ in range(per_graph):
+            step()
+    for _ in range(max(1, warmup // per_graph)):
         g.replay()
     torch.cuda.synchronize()
+    reps = max(1, steps // per_graph)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
-    for _ in range(steps):
+    for _ in range(reps):
         g.replay()
     e1.record()
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / steps
+    return e0.elapsed_time(e1) / (reps * per_graph)
 
 
-def _weight_cache_step_ms(layer, x, dy, warmup, steps, torch, ca):
+def _weight_cache_step_ms(layer, x, dy, warmup, steps, torch, ca, per_graph=1):
     """The same step on a weight_cache=True copy of the layer."""
     wl = ca.ConcordLinearPackedB(K_IN, N_OUT, bias=True, device=x.device, lr=5e-4, weight_cache=True)
     wl.disable_cohpre()
@@ -179,7 +185,7 @@ def _weight_cache_step_ms(layer, x, dy, warmup, steps, torch, ca):
 
     for _ in range(3):
         step()
-    return _graph_ms(step, warmup, steps, torch)
+    return _graph_ms(step, warmup, steps, torch, per_graph)
 
 
 def _only(which, reps, layer, xb, dy, torch, pb):
@@ -230,6 +236,8 @@ def main():
                     choices=["fwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
                              "copy"])
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--graph-steps", type=int, default=5,
+                    help="training steps captured per HIP graph (1 = one graph replay per step)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -269,7 +277,14 @@ def main():
 
     mode = "eager"
     run = step
+    per_run = 1
     if not args.no_graph:
+        # G consecutive steps per graph (G divides the step counts), so the
+        # replay launch overhead is paid once per G steps, as a training loop
+        # that captures its inner steps does; every step's kernels all run
+        G = max(1, args.graph_steps)
+        while G > 1 and (args.steps % G or args.warmup % G):
+            G -= 1
         try:
             s = torch.cuda.Stream()
             s.wait_stream(torch.cuda.current_stream())
@@ -279,22 +294,24 @@ def main():
             torch.cuda.current_stream().wait_stream(s)
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
-                step()
+                for _ in range(G):
+                    step()
             torch.cuda.synchronize()
             run = g.replay
-            mode = "hipgraph"
+            per_run = G
+            mode = f"hipgraph ({G} steps per graph)" if G > 1 else "hipgraph"
         except Exception as exc:  # capture unsupported: time eagerly
             print(f"bench.py: graph capture failed ({exc}); timing eager steps", file=sys.stderr)
             torch.cuda.synchronize()
 
-    for _ in range(args.warmup):
+    for _ in range(args.warmup // per_run):
         run()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record()
-    for _ in range(args.steps):
+    for _ in range(args.steps // per_run):
         run()
     ev1.record()
     torch.cuda.synchronize()
@@ -345,7 +362,7 @@ def main():
     Wd0 = layer.get_weight()
     t_bf_fwd = _event_time_ms(lambda: pb._gemm_fwd(xb, None, None, None, 15, layer.bias, Wd0), reps, torch)
     t_bf_dgrad = _event_time_ms(lambda: pb._gemm_dgrad(dy, None, None, None, 15, Wd0), reps, torch)
-    wc_ms = _weight_cache_step_ms(layer, x, dy, args.warmup, args.steps, torch, ca)
+    wc_ms = _weight_cache_step_ms(layer, x, dy, args.warmup, args.steps, torch, ca, per_run)
 
     # library reference (hipBLASLt through torch.matmul) on the same bf16 shapes,
     # for context only: W decoded once, not part of the measured path
