@@ -69,6 +69,8 @@ _SIGS = {
     "concord_wgrad": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _Z, _P]),
     "concord_wgrad_vhat": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _D, _P, _P, _P, _P, _P,
                                           _P, _P, _P, _Z, _P, _Z, _P]),
+    "concord_dgrad_wgrad_vhat": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _i, _P, _I, _P, _I, _P, _I, _I, _I,
+                                                 _I, _D, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _P, _Z, _P]),
     "concord_muon_workspace_bytes": (_Z, [_I, _I]),
     "concord_muon_ns5": (ctypes.c_int, [_P, _I, _I, _I, _F, _P, _I, _P, _Z, _P]),
     "concord_gemm_bf16_fwd": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _P, _Z, _P]),

@@ -64,6 +64,12 @@ int gemm_fast_launch(int mode, const GemmArgs& g, void* workspace, size_t ws_byt
 // WGRAD and the separate partials kernel)
 int gemm_wgrad_vhat_launch(const GemmArgs& g, size_t split_room, hipStream_t st, const char* what,
                            int* tiles_j);
+// dgrad (split, its reduction deferred) then the VH WGRAD whose spare
+// workgroups run that reduction on the CUs the WGRAD tiles leave idle; -1
+// when the shapes do not take this path (the caller then issues the two
+// products separately).  The dgrad's split-K partials use `workspace`.
+int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd, void* workspace, size_t ws_bytes, const GemmArgs& gw,
+                                 hipStream_t st, const char* what, int* tiles_j);
 // tiles along J of the WGRAD launch above (the bias partials' row count)
 int64_t gemm_wgrad_vhat_tiles_j(int64_t J);
 // a plain bf16 product through the fast or generic kernels: MODE_FWD_BF16

@@ -558,18 +558,18 @@ extern "C" int concord_wgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* 
   return launch_gemm<MODE_WGRAD>(g, workspace, workspace_bytes, (hipStream_t)stream, "wgrad");
 }
 
-extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t ld_x,
-                                  uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
-                                  double beta2, float* v_row, float* v_col, float* sum_v_inv,
-                                  int32_t* row_max, int32_t* col_max, int32_t* salt_counter,
-                                  uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
-                                  void* gemm_workspace, size_t gemm_workspace_bytes, void* stream) {
-  CONCORD_CHECK(sizes_ok(M, N, K) && N > 0 && K > 0, "concord_wgrad_vhat: bad size");
-  CONCORD_CHECK(dy && x && grad_w && v_row && v_col && sum_v_inv, "concord_wgrad_vhat: NULL argument");
-  CONCORD_CHECK(ld_dy >= N && ld_x >= K && ld_gw >= K, "concord_wgrad_vhat: bad leading dimension");
+// wgrad with the v-hat EMA (and bias gradient); with gd, the dgrad product
+// `gd` first, its split-K reduction carried by the WGRAD launch when the
+// shapes allow (gemm_dgrad_wgrad_vhat_launch), else the two products in turn
+static int wgrad_vhat_impl(const GemmArgs* gd, const uint16_t* dy, int64_t ld_dy, const uint16_t* x,
+                           int64_t ld_x, uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
+                           double beta2, float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max,
+                           int32_t* col_max, int32_t* salt_counter, uint16_t* grad_bias, void* workspace,
+                           size_t workspace_bytes, void* gemm_workspace, size_t gemm_workspace_bytes,
+                           hipStream_t st, const char* what) {
   const Workspace ws = workspace_layout(N, K, grad_bias ? M : 0);
   if (!workspace || workspace_bytes < ws.total) {
-    set_error("concord_wgrad_vhat: workspace of %zu bytes needed", ws.total);
+    set_error("%s: workspace of %zu bytes needed", what, ws.total);
     return CONCORD_EWORKSPACE;
   }
   const VhatScratch v = vhat_scratch(N, K);
@@ -578,16 +578,25 @@ extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint1
   float* bsum = pc + v.pc;
   float* bpart = bsum + v.bsum;
   uint32_t* ticket = (uint32_t*)((char*)workspace + ws.vhat_ticket);
-  hipStream_t st = (hipStream_t)stream;
   GemmArgs g = make_args(dy, x, ld_dy, ld_x, nullptr, nullptr, 0, nullptr, grad_w, ld_gw, N, K, M, false);
   g.vh_pr = pr;
   g.vh_pc = pc;
   g.bpart = grad_bias ? bpart : nullptr;
   int tiles_j = 0;
-  int rc = gemm_wgrad_vhat_launch(g, gemm_workspace ? gemm_workspace_bytes : 0, st, "wgrad_vhat", &tiles_j);
+  int rc = -1;
+  if (gd && gd->I > 0 && gd->J > 0) {
+    rc = gemm_dgrad_wgrad_vhat_launch(*gd, gemm_workspace, gemm_workspace ? gemm_workspace_bytes : 0, g, st,
+                                      what, &tiles_j);
+    if (rc == -1) {   // the products in turn
+      rc = launch_gemm<MODE_DGRAD>(*gd, gemm_workspace, gemm_workspace_bytes, st, what);
+      if (rc != CONCORD_OK) return rc;
+      rc = -1;
+    }
+  }
+  if (rc == -1) rc = gemm_wgrad_vhat_launch(g, gemm_workspace ? gemm_workspace_bytes : 0, st, what, &tiles_j);
   if (rc == -1) {   // split or unaligned WGRAD: the plain product, then the partials kernels
     g.bpart = nullptr;
-    rc = launch_gemm<MODE_WGRAD>(g, gemm_workspace, gemm_workspace_bytes, st, "wgrad");
+    rc = launch_gemm<MODE_WGRAD>(g, gemm_workspace, gemm_workspace_bytes, st, what);
     if (rc != CONCORD_OK) return rc;
     vhat_partials_launch(grad_w, ld_gw, N, K, pr, pc, st);
     if (grad_bias) bias_grad_launch(dy, ld_dy, M, N, grad_bias, bpart, st);
@@ -599,7 +608,41 @@ extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint1
     vhat_finish_launch(pr, pc, bsum, ticket, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max,
                        salt_counter, st, bpart, tiles_j, grad_bias);
   }
-  return launch_status("wgrad_vhat");
+  return launch_status(what);
+}
+
+extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int64_t ld_x,
+                                  uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
+                                  double beta2, float* v_row, float* v_col, float* sum_v_inv,
+                                  int32_t* row_max, int32_t* col_max, int32_t* salt_counter,
+                                  uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
+                                  void* gemm_workspace, size_t gemm_workspace_bytes, void* stream) {
+  CONCORD_CHECK(sizes_ok(M, N, K) && N > 0 && K > 0, "concord_wgrad_vhat: bad size");
+  CONCORD_CHECK(dy && x && grad_w && v_row && v_col && sum_v_inv, "concord_wgrad_vhat: NULL argument");
+  CONCORD_CHECK(ld_dy >= N && ld_x >= K && ld_gw >= K, "concord_wgrad_vhat: bad leading dimension");
+  return wgrad_vhat_impl(nullptr, dy, ld_dy, x, ld_x, grad_w, ld_gw, M, N, K, beta2, v_row, v_col, sum_v_inv,
+                         row_max, col_max, salt_counter, grad_bias, workspace, workspace_bytes, gemm_workspace,
+                         gemm_workspace_bytes, (hipStream_t)stream, "wgrad_vhat");
+}
+
+extern "C" int concord_dgrad_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const int32_t* packed, int64_t ld_p,
+                                        const int8_t* row_exp, const int8_t* col_exp, int32_t mantissa_bias,
+                                        uint16_t* dx, int64_t ld_dx, const uint16_t* x, int64_t ld_x,
+                                        uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
+                                        double beta2, float* v_row, float* v_col, float* sum_v_inv,
+                                        int32_t* row_max, int32_t* col_max, int32_t* salt_counter,
+                                        uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
+                                        void* gemm_workspace, size_t gemm_workspace_bytes, void* stream) {
+  CONCORD_CHECK(sizes_ok(M, N, K) && N > 0 && K > 0, "concord_dgrad_wgrad_vhat: bad size");
+  CONCORD_CHECK(dy && packed && row_exp && col_exp && dx && x && grad_w && v_row && v_col && sum_v_inv,
+                "concord_dgrad_wgrad_vhat: NULL argument");
+  CONCORD_CHECK(ld_dy >= N && ld_p >= K && ld_dx >= K && ld_x >= K && ld_gw >= K,
+                "concord_dgrad_wgrad_vhat: bad leading dimension");
+  const GemmArgs gd =
+      make_args(dy, packed, ld_dy, ld_p, row_exp, col_exp, mantissa_bias, nullptr, dx, ld_dx, M, K, N, true);
+  return wgrad_vhat_impl(&gd, dy, ld_dy, x, ld_x, grad_w, ld_gw, M, N, K, beta2, v_row, v_col, sum_v_inv,
+                         row_max, col_max, salt_counter, grad_bias, workspace, workspace_bytes, gemm_workspace,
+                         gemm_workspace_bytes, (hipStream_t)stream, "dgrad_wgrad_vhat");
 }
 
 extern "C" int concord_gemm_bf16_fwd(const uint16_t* x, int64_t ld_x, const uint16_t* w,

@@ -484,11 +484,14 @@ CONCORD_DEV void epilogue(const GemmArgs& g, f32x4 (&acc)[NI][NJ], int64_t i0, i
 // lane) sums the splits' partials in split order, applies the column scale
 // and bias, and stores 4 bf16.
 template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
+CONCORD_DEV int64_t splitk_reduce_items(const GemmArgs& g) {
+  return (int64_t)g.tiles_i * g.tiles_j * WI * WJ * NI * NJ * 64;
+}
+
+template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
+CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
   constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ;
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int tiles = g.tiles_i * g.tiles_j;
-  if (idx >= (int64_t)tiles * NAW * NI * NJ * 64) return;
   const int lane = (int)(idx % 64);
   int64_t r = idx / 64;
   const int y = (int)(r % NJ); r /= NJ;
@@ -526,6 +529,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(__fmul_rn(sum[e], sc[e]), bs[e]);
   *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+}
+
+template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= splitk_reduce_items<MODE, NI, NJ, BI, BJ, WI, WJ>(g)) return;
+  splitk_reduce_item<MODE, NI, NJ, BI, BJ, WI, WJ>(g, idx);
 }
 
 // MFMAs of one TR-deep stage for a wave tile of NI x NJ 16x16 blocks whose
@@ -1068,9 +1078,24 @@ CONCORD_DEV void bias_acc(f32x4 (&b)[NI], const bf16x8 (&fa)[NI]) {
 // s = bj, bj + tiles_j, ... (an MFMA against ones per fragment, fp32
 // accumulation), giving bpart[bj][i]; the bias gradient is the sum of the
 // partials over bj ascending (vhat_finalize).
+// The split-K reduction shape of the dgrad kernel (gemm_dgt_kernel<DGRAD, 256,
+// 128>, 2 x 2 accumulator waves of 128 x 64), which a VH launch can carry.
+#define CONCORD_DGRAD_REDUCE MODE_DGRAD, 8, 4, 256, 128, 2, 2
+
+// Workgroups [0, tr_blocks) compute WGRAD tiles.  A VH launch may carry more:
+// workgroups from tr_blocks on run the split-K reduction `rd` of the dgrad
+// kernel issued just before on the stream, on the CUs the WGRAD grid leaves
+// idle (200 tiles on 256 CUs at 1280 -> 5120).
 template <int BI, int BJ, int WI, int WJ, bool VH>
-__global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g) {
+__global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, GemmArgs rd, int tr_blocks) {
   constexpr int NW = WI * WJ, NT = 64 * NW, WTI = BI / WI, WTJ = BJ / WJ;
+  if (VH && (int)blockIdx.x >= tr_blocks) {
+    const int64_t items = splitk_reduce_items<CONCORD_DGRAD_REDUCE>(rd);
+    const int64_t stride = (int64_t)(gridDim.x - tr_blocks) * NT;
+    for (int64_t idx = (int64_t)(blockIdx.x - tr_blocks) * NT + threadIdx.x; idx < items; idx += stride)
+      splitk_reduce_item<CONCORD_DGRAD_REDUCE>(rd, idx);
+    return;
+  }
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
   typedef TrDma<BI, NW> DA;
   typedef TrDma<BJ, NW> DB;
@@ -1437,7 +1462,8 @@ static void launch_dma(const GemmArgs& g, int blocks, hipStream_t st) {
 
 template <int BI, int BJ, int WI, int WJ>
 static void launch_tr(const GemmArgs& g, int blocks, hipStream_t st) {
-  hipLaunchKernelGGL((gemm_tr_kernel<BI, BJ, WI, WJ, false>), dim3(blocks), dim3(64 * WI * WJ), 0, st, g);
+  hipLaunchKernelGGL((gemm_tr_kernel<BI, BJ, WI, WJ, false>), dim3(blocks), dim3(64 * WI * WJ), 0, st, g,
+                     GemmArgs{}, blocks);
   launch_reduce<MODE_WGRAD, BI, BJ, WI, WJ>(g, st);
 }
 
@@ -1490,7 +1516,38 @@ int gemm_wgrad_vhat_launch(const GemmArgs& g0, size_t split_room, hipStream_t st
   g.r_split = p.r_split;
   g.tiles_i = p.ti;
   g.tiles_j = p.tj;
-  hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true>), dim3(p.ti * p.tj), dim3(512), 0, st, g);
+  hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true>), dim3(p.ti * p.tj), dim3(512), 0, st, g,
+                     GemmArgs{}, p.ti * p.tj);
+  return launch_status(what);
+}
+
+int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd0, void* workspace, size_t ws_bytes, const GemmArgs& gw0,
+                                 hipStream_t st, const char* what, int* tiles_j) {
+  if (!eligible(MODE_DGRAD, gd0) || !eligible(MODE_WGRAD, gw0) || !tr_eligible(gw0)) return -1;
+  const size_t room = (workspace && ws_bytes > kSplitkCounterBytes) ? ws_bytes - kSplitkCounterBytes : 0;
+  const FastPlan pd = plan_mode(MODE_DGRAD, gd0.I, gd0.J, gd0.R, room);
+  // the WGRAD plan of gemm_wgrad_vhat_launch with the same room, so that both
+  // routes take the same product (and so the same bits)
+  const FastPlan pw = plan_mode(MODE_WGRAD, gw0.I, gw0.J, gw0.R, room);
+  if (pd.shape != 0 || pd.splits < 2 || pw.shape != 0 || pw.splits != 1) return -1;
+  const int tw = pw.ti * pw.tj;
+  const int extra = kCUs - tw;
+  if (extra < 16) return -1;   // the WGRAD grid leaves too few CUs to carry the reduction
+  GemmArgs gd = gd0;
+  gd.splits = pd.splits;
+  gd.r_split = pd.r_split;
+  gd.tiles_i = pd.ti;
+  gd.tiles_j = pd.tj;
+  gd.part = (float*)((char*)workspace + kSplitkCounterBytes);
+  GemmArgs gw = gw0;
+  gw.splits = 1;
+  gw.r_split = pw.r_split;
+  gw.tiles_i = pw.ti;
+  gw.tiles_j = pw.tj;
+  *tiles_j = pw.tj;
+  hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD, 256, 128>), dim3(pd.ti * pd.tj * pd.splits), dim3(512), 0, st,
+                     gd);
+  hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true>), dim3(tw + extra), dim3(512), 0, st, gw, gd, tw);
   return launch_status(what);
 }
 

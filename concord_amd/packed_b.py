@@ -534,6 +534,27 @@ def _wgrad_vhat(dy, x2, v_row, v_col, sum_v_inv, beta2, row_max, col_max, salt_c
     return gw, gb
 
 
+def _dgrad_wgrad_vhat(dy, x2, packed_w, row_exp, col_exp, mantissa_bias, v_row, v_col, sum_v_inv,
+                      beta2, row_max, col_max, salt_counter, with_bias=False):
+    """_gemm_dgrad then _wgrad_vhat in one entry (concord_dgrad_wgrad_vhat):
+    the dgrad's split-K reduction runs on the CUs the WGRAD grid leaves idle.
+    Same results as the two calls.  Returns (grad_x, grad_W, grad_bias or None)."""
+    M, N = dy.shape
+    K = x2.shape[1]
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dy.device)
+    gw = torch.empty((N, K), dtype=torch.bfloat16, device=dy.device)
+    gb = torch.empty(N, dtype=torch.bfloat16, device=dy.device) if with_bias else None
+    gws = _gemm_workspace(dy.device, M, N, K)
+    ws = _workspace(dy.device, N, K, M if with_bias else 0)
+    C.check(C.lib().concord_dgrad_wgrad_vhat(
+        C.ptr(dy), dy.stride(0), C.ptr(packed_w), packed_w.stride(0), C.ptr(row_exp), C.ptr(col_exp),
+        int(mantissa_bias), C.ptr(dx), dx.stride(0), C.ptr(x2), x2.stride(0), C.ptr(gw), gw.stride(0),
+        M, N, K, float(beta2), C.ptr(v_row), C.ptr(v_col), C.ptr(sum_v_inv), C.ptr(row_max),
+        C.ptr(col_max), C.ptr(salt_counter), C.ptr(gb), C.ptr(ws), ws.numel(), C.ptr(gws), gws.numel(),
+        C.stream_of(dy.device)), "dgrad_wgrad_vhat")
+    return dx, gw, gb
+
+
 _MUON_WORKSPACES = {}
 
 
@@ -629,28 +650,40 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
             dy = dy.to(torch.bfloat16)
         dy = dy.contiguous()
         dev = dy.device
-        # dgrad on the pre-update weight (1263), before the update below
-        grad_x = _gemm_dgrad(dy, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias,
-                             ctx.weight_buf).reshape(*ctx.lead, K)
         salt = _get_step_counter(dev)
         prebumped = False
         grad_bias = None
         muon = ctx.drive == 'muon' and ctx.optimizer_kind == 'adamw'
-        if muon:
-            # O = sqrt(max(N, K)) NS5(grad_W / ||grad_W||); no v-hat
-            # (docs/MUON_IMPLEMENTATION.md:45-67)
-            grad_W = muon_ns5(_wgrad(dy, x2))
-        elif ctx.track_adafactor_v and ctx.v_row is not None:
-            # wgrad (1269-1277), watermark zeroing (1281-1283), v-hat EMA (1288-1303),
-            # salt + 1 (910-911)
-            grad_W, grad_bias = _wgrad_vhat(dy, x2, ctx.v_row, ctx.v_col, ctx.sum_v_inv,
-                                            ctx.adafactor_beta2,
-                                            ctx.row_max_buf if ctx.track_rebalance else None,
-                                            ctx.col_max_buf if ctx.track_rebalance else None, salt,
-                                            with_bias=ctx.has_bias)
+        vhat = ctx.track_adafactor_v and ctx.v_row is not None
+        if vhat and not muon and ctx.weight_buf is None:
+            # dgrad on the pre-update weight (1263), wgrad (1269-1277), watermark
+            # zeroing (1281-1283), v-hat EMA (1288-1303), salt + 1 (910-911) and
+            # grad_y.sum(0) (1338-1340) in one entry
+            grad_x, grad_W, grad_bias = _dgrad_wgrad_vhat(
+                dy, x2, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias, ctx.v_row, ctx.v_col,
+                ctx.sum_v_inv, ctx.adafactor_beta2, ctx.row_max_buf if ctx.track_rebalance else None,
+                ctx.col_max_buf if ctx.track_rebalance else None, salt, with_bias=ctx.has_bias)
+            grad_x = grad_x.reshape(*ctx.lead, K)
             prebumped = True
         else:
-            grad_W = _wgrad(dy, x2)
+            # dgrad on the pre-update weight (1263), before the update below
+            grad_x = _gemm_dgrad(dy, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias,
+                                 ctx.weight_buf).reshape(*ctx.lead, K)
+            if muon:
+                # O = sqrt(max(N, K)) NS5(grad_W / ||grad_W||); no v-hat
+                # (docs/MUON_IMPLEMENTATION.md:45-67)
+                grad_W = muon_ns5(_wgrad(dy, x2))
+            elif vhat:
+                # wgrad (1269-1277), watermark zeroing (1281-1283), v-hat EMA
+                # (1288-1303), salt + 1 (910-911)
+                grad_W, grad_bias = _wgrad_vhat(dy, x2, ctx.v_row, ctx.v_col, ctx.sum_v_inv,
+                                                ctx.adafactor_beta2,
+                                                ctx.row_max_buf if ctx.track_rebalance else None,
+                                                ctx.col_max_buf if ctx.track_rebalance else None, salt,
+                                                with_bias=ctx.has_bias)
+                prebumped = True
+            else:
+                grad_W = _wgrad(dy, x2)
         if _DEBUG_CAPTURE is not None:
             _DEBUG_CAPTURE.append(grad_W.clone())
         if not prebumped and ctx.track_rebalance:

@@ -204,6 +204,22 @@ int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint16_t* x, int
                        uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
                        void* gemm_workspace, size_t gemm_workspace_bytes, void* stream);
 
+/* concord_dqgemm_dgrad followed by concord_wgrad_vhat in one call, with the
+ * same results: the backward's two products of the fused-forward layer
+ * (concord/packed_b.py:1263, 1269-1303, 1338-1340).  When the dgrad splits
+ * its reduction and the WGRAD grid leaves CUs idle, the dgrad's split-K
+ * reduction runs in extra workgroups of the WGRAD launch instead of a launch
+ * of its own.  Workspaces as for the two calls (gemm_workspace holds the
+ * dgrad's partials). */
+int concord_dgrad_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const int32_t* packed, int64_t ld_p,
+                             const int8_t* row_exp, const int8_t* col_exp, int32_t mantissa_bias,
+                             uint16_t* dx, int64_t ld_dx, const uint16_t* x, int64_t ld_x,
+                             uint16_t* grad_w, int64_t ld_gw, int64_t M, int64_t N, int64_t K,
+                             double beta2, float* v_row, float* v_col, float* sum_v_inv,
+                             int32_t* row_max, int32_t* col_max, int32_t* salt_counter,
+                             uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
+                             void* gemm_workspace, size_t gemm_workspace_bytes, void* stream);
+
 /* Muon drive (A13): out[N,K] = bf16(gamma * NS5(g / ||g||_F)), the quintic
  * Newton-Schulz orthogonalisation of experiments/cpu_dynamics/exp9_muon.py:44-55
  * used as the drive of MuonConcord.step (58-100; gamma = sqrt(max(N, K))) and
