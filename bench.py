@@ -11,9 +11,11 @@ Prints one JSON line.  value = dequant-matmul throughput of the whole step,
 6 M N K / step time (TFLOP/s).  The step's entries are timed one by one (HIP
 events around a HIP graph of back-to-back calls): forward, dgrad (main kernel
 + split reduction), wgrad with the v-hat partials and bias gradient in its
-epilogue (+ the v-hat EMA kernels), packed update.  roofline = the longest
-entry against its roofline: a GEMM against dense bf16 MFMA peak at 2 M N K
-algorithmic FLOP, the packed update against HBM peak at 10 algorithmic
+epilogue (+ the v-hat EMA kernels), packed update; bwd_products = the entry
+the step's backward calls (dgrad, then the wgrad launch that also carries the
+dgrad's split-K reduction, then the v-hat EMA).  roofline = the longest entry
+the step calls against its roofline: a GEMM against dense bf16 MFMA peak at 2 M N K
+algorithmic FLOP per product (4 M N K for bwd_products), the packed update against HBM peak at 10 algorithmic
 B/param; rooflines = the same for every entry; traffic = HBM bytes per call
 from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
 (profiles/traffic_sdxl_1280x5120.txt) when present.  cpu_baseline = the same
@@ -26,7 +28,7 @@ shared by 5 steps.
 
 `--only KERNEL` runs one entry of the step `--reps` times and exits (the
 command the committed rocprofv3 summaries were taken with); KERNEL = fwd,
-dgrad, wgrad, wgrad_vhat, vhat, update, materialize, or copy (a 256 MiB
+bwd, dgrad, wgrad, wgrad_vhat, vhat, update, materialize, or copy (a 256 MiB
 device copy, the counter calibration).
 """
 import argparse
@@ -202,6 +204,10 @@ def _only(which, reps, layer, xb, dy, torch, pb):
         fn = lambda: pb._gemm_dgrad(dy, *st, 15, None)  # noqa: E731
     elif which == "wgrad":
         fn = lambda: pb._wgrad(dy, xb)  # noqa: E731
+    elif which == "bwd":
+        fn = lambda: pb._dgrad_wgrad_vhat(dy, xb, *st, 15, layer.v_row, layer.v_col,  # noqa: E731
+                                          layer._sum_v_inv, 0.999, layer._row_max_buf, layer._col_max_buf,
+                                          None, with_bias=True)
     elif which == "wgrad_vhat":
         fn = lambda: pb._wgrad_vhat(dy, xb, layer.v_row, layer.v_col, layer._sum_v_inv, 0.999,  # noqa: E731
                                     layer._row_max_buf, layer._col_max_buf, None, with_bias=True)
@@ -233,7 +239,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--only", default=None,
-                    choices=["fwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
+                    choices=["fwd", "bwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
                              "copy"])
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--graph-steps", type=int, default=5,
@@ -331,6 +337,10 @@ def main():
                                                   layer._row_max_buf, layer._col_max_buf, None,
                                                   with_bias=True), reps, torch)
     t_wgrad = _event_time_ms(lambda: pb._wgrad(dy, xb), reps, torch)
+    t_bwd = _event_time_ms(lambda: pb._dgrad_wgrad_vhat(dy, xb, *st, 15, layer.v_row, layer.v_col,
+                                                        layer._sum_v_inv, 0.999, layer._row_max_buf,
+                                                        layer._col_max_buf, None, with_bias=True),
+                           reps, torch)
     gw = pb._wgrad(dy, xb)
     pk_copy = layer.packed_w.clone()
     t_vhat = _event_time_ms(lambda: pb.vhat_ema(gw, layer.v_row, layer.v_col, layer._sum_v_inv),
@@ -389,9 +399,18 @@ def main():
                 "unit": "GB/s", "frac": round(a / PEAK_HBM_GBPS, 4), "traffic": traffic.get(key),
                 "us": round(t_ms * 1e3, 2)}
 
+    def bwd_roof(key, name, t_ms):
+        r = gemm_roof(key, name, t_ms)
+        a = 2.0 * gemm_flop / (t_ms * 1e-3) / 1e12
+        r.update(achieved=round(a, 2), frac=round(a / PEAK_BF16_TFLOPS, 4))
+        return r
+
     roofs = {
         "dqgemm_fwd": gemm_roof("dqgemm_fwd", "gemm_dma_kernel<FWD, 256, 160> (fused dequant-GEMM forward)",
                                 t_fwd),
+        "bwd_products": bwd_roof("bwd_products", "gemm_dgt_kernel<DGRAD, 256, 128> + gemm_tr_kernel<256, 128, "
+                                 "4, 2, VH> carrying the dgrad's split-K reduction + vhat_finalize_kernel "
+                                 "(the step's backward entry: dgrad and wgrad, 4 M N K FLOP)", t_bwd),
         "dqgemm_dgrad": gemm_roof("dqgemm_dgrad", "gemm_dgt_kernel<DGRAD, 256, 128> + splitk_reduce_kernel "
                                   "(fused dequant-GEMM dgrad, 3-way split reduction)", t_dgrad),
         "wgrad_vhat": gemm_roof("wgrad_vhat", "gemm_tr_kernel<256, 128, 4, 2, VH> + vhat_finalize_kernel "
@@ -400,7 +419,10 @@ def main():
         "apply_adamw": hbm_roof("apply_adamw", "apply_adamw_fast_kernel<ratio> (packed update, winner flags)",
                                 t_upd, UPDATE_BYTES_PER_PARAM * params),
     }
-    dominant = max(roofs, key=lambda k: roofs[k]["us"])
+    # the longest entry the step calls (dgrad and wgrad_vhat alone are context:
+    # the step runs them as bwd_products)
+    step_entries = ("dqgemm_fwd", "bwd_products", "apply_adamw")
+    dominant = max(step_entries, key=lambda k: roofs[k]["us"])
 
     out = {
         "metric": "dequant-matmul TFLOP/s (%MFMA peak) + packed-update GB/s (%HBM), SDXL linears",
@@ -420,12 +442,14 @@ def main():
                    "forward": "fused dequant-GEMM", "timing": mode},
         "roofline": dict(roofs[dominant], step_kernel=dominant),
         "rooflines": roofs,
-        "kernel_us": {"dqgemm_fwd": round(t_fwd * 1e3, 2), "dqgemm_dgrad": round(t_dgrad * 1e3, 2),
+        "kernel_us": {"dqgemm_fwd": round(t_fwd * 1e3, 2), "bwd_products": round(t_bwd * 1e3, 2),
+                      "dqgemm_dgrad": round(t_dgrad * 1e3, 2),
                       "wgrad_vhat": round(t_wgv * 1e3, 2), "wgrad_alone": round(t_wgrad * 1e3, 2),
                       "vhat_ema_alone": round(t_vhat * 1e3, 2),
                       "apply_adamw": round(t_upd * 1e3, 2), "materialize": round(t_mat * 1e3, 2),
                       "rebalance_nofire": round(t_reb * 1e3, 2)},
         "gemm_tflops": {"fwd": round(fwd_tflops, 1),
+                        "bwd_products": round(2.0 * gemm_flop / (t_bwd * 1e-3) / 1e12, 1),
                         "dgrad": round(gemm_flop / (t_dgrad * 1e-3) / 1e12, 1),
                         "wgrad_vhat": round(gemm_flop / (t_wgv * 1e-3) / 1e12, 1),
                         "wgrad_alone": round(gemm_flop / (t_wgrad * 1e-3) / 1e12, 1)},
