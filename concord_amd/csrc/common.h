@@ -95,10 +95,9 @@ CONCORD_DEV int32_t sr_tick(float d, float u) {
   return f2i(fl) + (int32_t)(u < fr);
 }
 
-// ---- Philox4x32-10 as tl.rand (triton/language/random.py:13-44, 127-157) ------
-CONCORD_DEV float tl_rand(int32_t seed, int32_t offset) {
-  uint32_t c0 = (uint32_t)offset, c1 = 0, c2 = 0, c3 = 0;
-  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 31);  // sign-extended seed
+// ---- Philox4x32-10 (triton/language/random.py:13-44) ------------------------
+CONCORD_DEV void philox4x32_10(uint32_t& c0, uint32_t& c1, uint32_t& c2, uint32_t& c3, uint32_t k0,
+                               uint32_t k1) {
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
     // one 32 x 32 -> 64-bit multiply gives both halves (v_mad_u64_u32)
@@ -112,6 +111,13 @@ CONCORD_DEV float tl_rand(int32_t seed, int32_t offset) {
     k0 += 0x9E3779B9u;
     k1 += 0xBB67AE85u;
   }
+}
+
+// tl.rand (triton/language/random.py:127-157): counter (offset, 0, 0, 0),
+// key = the sign-extended seed, word 0 mapped to [0, 1)
+CONCORD_DEV float tl_rand(int32_t seed, int32_t offset) {
+  uint32_t c0 = (uint32_t)offset, c1 = 0, c2 = 0, c3 = 0;
+  philox4x32_10(c0, c1, c2, c3, (uint32_t)seed, (uint32_t)(seed >> 31));
   int32_t x = (int32_t)c0;
   if (x < 0) x = wsub(-1, x);
   return __fmul_rn((float)x, 4.6566127342e-10f);
@@ -192,6 +198,48 @@ CONCORD_DEV float sqrt_rn(float x) {
     s = x >= 0x1p-96f ? s : full;
   }
   return s;
+}
+
+// cos(2 pi u) for u in [0, 1) on a 2^-24 grid: quadrant q = floor(4u) and
+// theta = (4u - q) pi/2 are exact up to the one product; cos and sin of
+// theta by Taylor polynomials in theta^2 (degree 10 and 11; |error| below
+// 1e-6 on [0, pi/2]), evaluated in a fixed order
+CONCORD_DEV float det_cos2pi(float u) {
+  const float t = __fmul_rn(u, 4.0f);
+  const float qf = floorf(t);
+  const int q = (int)qf;
+  const float th = __fmul_rn(__fsub_rn(t, qf), 1.57079632679489662f);
+  const float s = __fmul_rn(th, th);
+  float c = -1.0f / 3628800.0f;
+  c = __fadd_rn(__fmul_rn(c, s), 1.0f / 40320.0f);
+  c = __fadd_rn(__fmul_rn(c, s), -1.0f / 720.0f);
+  c = __fadd_rn(__fmul_rn(c, s), 1.0f / 24.0f);
+  c = __fadd_rn(__fmul_rn(c, s), -0.5f);
+  c = __fadd_rn(__fmul_rn(c, s), 1.0f);
+  float sn = -1.0f / 39916800.0f;
+  sn = __fadd_rn(__fmul_rn(sn, s), 1.0f / 362880.0f);
+  sn = __fadd_rn(__fmul_rn(sn, s), -1.0f / 5040.0f);
+  sn = __fadd_rn(__fmul_rn(sn, s), 1.0f / 120.0f);
+  sn = __fadd_rn(__fmul_rn(sn, s), -1.0f / 6.0f);
+  sn = __fadd_rn(__fmul_rn(sn, s), 1.0f);
+  sn = __fmul_rn(sn, th);
+  return q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+}
+
+// Standard normal draw `idx` of stream `seed` (Box-Muller on one Philox4x32-10
+// block; counter (idx, 0, 0, 0), key (seed, 0x6E6F6973)):
+//   u1 = ((c0 >> 8) + 1) 2^-24 in (0, 1],  u2 = (c1 >> 8) 2^-24 in [0, 1),
+//   z = sqrt(-2 ln u1) cos(2 pi u2), ln u1 = log2(u1) ln 2.
+// A fixed sequence of IEEE ops (det_log2, sqrt_rn, det_cos2pi), so the CPU
+// restatement draws the same bits.
+CONCORD_DEV float normal_draw(int32_t seed, uint32_t idx) {
+  uint32_t c0 = idx, c1 = 0, c2 = 0, c3 = 0;
+  philox4x32_10(c0, c1, c2, c3, (uint32_t)seed, 0x6E6F6973u);
+  const float u1 = __fmul_rn((float)((c0 >> 8) + 1u), 5.9604644775390625e-08f);
+  const float u2 = __fmul_rn((float)(c1 >> 8), 5.9604644775390625e-08f);
+  const float ln = __fmul_rn(det_log2(u1), 0.693147180559945309f);
+  const float r = sqrt_rn(__fmul_rn(-2.0f, ln));
+  return __fmul_rn(r, det_cos2pi(u2));
 }
 
 CONCORD_DEV float pow_p(float x, float p) {

@@ -655,7 +655,21 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
         grad_bias = None
         muon = ctx.drive == 'muon' and ctx.optimizer_kind == 'adamw'
         vhat = ctx.track_adafactor_v and ctx.v_row is not None
-        if vhat and not muon and ctx.weight_buf is None:
+        if _SIGMAG_NOISE:
+            # noise enters grad_W before the v-hat EMA and the update
+            # (prototype_packed_b.py:1484-1501): the products in turn, the
+            # injection, then the standalone v-hat entry
+            grad_x = _gemm_dgrad(dy, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias,
+                                 ctx.weight_buf).reshape(*ctx.lead, K)
+            grad_W = iso_noise_(_wgrad(dy, x2), salt_counter=salt)
+            if muon:
+                grad_W = muon_ns5(grad_W)
+            elif vhat:
+                vhat_ema(grad_W, ctx.v_row, ctx.v_col, ctx.sum_v_inv, ctx.adafactor_beta2,
+                         ctx.row_max_buf if ctx.track_rebalance else None,
+                         ctx.col_max_buf if ctx.track_rebalance else None, salt)
+                prebumped = True
+        elif vhat and not muon and ctx.weight_buf is None:
             # dgrad on the pre-update weight (1263), wgrad (1269-1277), watermark
             # zeroing (1281-1283), v-hat EMA (1288-1303), salt + 1 (910-911) and
             # grad_y.sum(0) (1338-1340) in one entry
@@ -1045,6 +1059,70 @@ class ConcordLinearPackedB(nn.Module):
                          seed_buf=self._reb_seed, allow_tickdown=self.allow_tickdown,
                          row_hwm=self._row_max_hwm, col_hwm=self._col_max_hwm,
                          advance_seed=True)
+
+
+# ---------------------------------------------------------------------------
+# Gradient-noise injection (notebook/src/prototype_packed_b.py:876-916, 1472-1501)
+# ---------------------------------------------------------------------------
+_SIGMAG_NOISE = False
+_SIGMAG_ISO = False
+_SIGMAG_SIGMA = 0.0
+_SIGMAG_SIGMA_T = {}
+_NOISE_WORKSPACES = {}
+
+
+def set_sigmag_noise(enabled, isotropic=False):
+    """Turn the gradient-noise injection on or off (a Python switch: a
+    captured graph keeps the choice made at capture, as in the reference).
+    Built: the isotropic draw, grad_W + sigma ||grad_W|| xi / ||xi||.  The
+    reference's default Sigma_g-shaped draw is not built and raises."""
+    global _SIGMAG_NOISE, _SIGMAG_ISO
+    if enabled and not isotropic:
+        raise NotImplementedError("concord_amd: only the isotropic gradient-noise draw is built "
+                                  "(set_sigmag_noise(True, isotropic=True))")
+    _SIGMAG_NOISE = bool(enabled)
+    _SIGMAG_ISO = bool(isotropic)
+
+
+def set_sigmag_sigma(sigma):
+    """Noise magnitude in units of ||grad_W||: the Python value and every
+    device-tensor copy (filled in place, so graph replays see it)."""
+    global _SIGMAG_SIGMA
+    _SIGMAG_SIGMA = float(sigma)
+    for t in _SIGMAG_SIGMA_T.values():
+        t.fill_(_SIGMAG_SIGMA)
+
+
+def _get_sigmag_sigma(device):
+    key = _dev_key(device)
+    t = _SIGMAG_SIGMA_T.get(key)
+    if t is None:
+        t = torch.full((1,), _SIGMAG_SIGMA, dtype=torch.float32, device=key)
+        _SIGMAG_SIGMA_T[key] = t
+    return t
+
+
+def iso_noise_(grad_W, sigma=None, salt_counter=None):
+    """grad_W <- bf16(g + xi sigma ||g|| / max(||xi||, 1e-12)) in place
+    (concord_iso_noise); xi is the library's counter-based normal stream keyed
+    by the device salt counter (read, not advanced)."""
+    C.require_device_tensor(grad_W, "grad_W")
+    N, K = grad_W.shape
+    dev = grad_W.device
+    if sigma is None:
+        sigma = _get_sigmag_sigma(dev)
+    if salt_counter is None:
+        salt_counter = _get_step_counter(dev)
+    key = _dev_key(dev)
+    need = int(C.lib().concord_noise_workspace_bytes(N, K))
+    ws = _NOISE_WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.empty(need, dtype=torch.uint8, device=key)
+        _NOISE_WORKSPACES[key] = ws
+    C.check(C.lib().concord_iso_noise(C.ptr(grad_W), grad_W.stride(0), N, K, C.ptr(sigma),
+                                      C.ptr(salt_counter), C.ptr(ws), ws.numel(), C.stream_of(dev)),
+            "iso_noise")
+    return grad_W
 
 
 # ---------------------------------------------------------------------------

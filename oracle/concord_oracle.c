@@ -716,6 +716,74 @@ float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C)
     return acc;
 }
 
+/* cos(2 pi u), u in [0, 1) on a 2^-24 grid: quadrant and Taylor polynomials
+ * in theta^2, the op order of the library's det_cos2pi */
+static float det_cos2pi(float u) {
+    const float t = u * 4.0f;
+    const float qf = floorf(t);
+    const int q = (int)qf;
+    const float th = (t - qf) * 1.57079632679489662f;
+    const float s = th * th;
+    float c = -1.0f / 3628800.0f;
+    c = c * s + 1.0f / 40320.0f;
+    c = c * s + -1.0f / 720.0f;
+    c = c * s + 1.0f / 24.0f;
+    c = c * s + -0.5f;
+    c = c * s + 1.0f;
+    float sn = -1.0f / 39916800.0f;
+    sn = sn * s + 1.0f / 362880.0f;
+    sn = sn * s + -1.0f / 5040.0f;
+    sn = sn * s + 1.0f / 120.0f;
+    sn = sn * s + -1.0f / 6.0f;
+    sn = sn * s + 1.0f;
+    sn = sn * th;
+    return q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+}
+
+float oracle_normal_draw(int32_t seed, uint32_t idx) {
+    uint32_t c[4] = {idx, 0u, 0u, 0u};
+    uint32_t k[2] = {(uint32_t)seed, 0x6E6F6973u};
+    oracle_philox4x32_10(c, k);
+    const float u1 = (float)((c[0] >> 8) + 1u) * 5.9604644775390625e-08f;
+    const float u2 = (float)(c[1] >> 8) * 5.9604644775390625e-08f;
+    const float ln = det_log2(u1) * 0.693147180559945309f;
+    const float r = sqrtf(-2.0f * ln);
+    return r * det_cos2pi(u2);
+}
+
+void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t salt) {
+    const int64_t total = N * K;
+    float sg = 0.0f, sx = 0.0f;
+    for (int64_t b0 = 0; b0 < total; b0 += 8192) {
+        float pg[256], px[256];
+        for (int t = 0; t < 256; ++t) {
+            float ag = 0.0f, ax = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                const int64_t e = b0 + t + 256 * i;
+                if (e >= total) continue;
+                const float v = bf16_to_f32(g[e]);
+                const float z = oracle_normal_draw(salt, (uint32_t)e);
+                ag = ag + v * v;
+                ax = ax + z * z;
+            }
+            pg[t] = ag;
+            px[t] = ax;
+        }
+        for (int h = 128; h >= 1; h >>= 1)
+            for (int t = 0; t < h; ++t) {
+                pg[t] = pg[t] + pg[t + h];
+                px[t] = px[t] + px[t + h];
+            }
+        sg = sg + pg[0];
+        sx = sx + px[0];
+    }
+    const float ng = sqrtf(sg);
+    const float nx = fmaxf(sqrtf(sx), 1e-12f);
+    const float scale = (sigma * ng) / nx;
+    for (int64_t e = 0; e < total; ++e)
+        g[e] = oracle_f32_to_bf16(bf16_to_f32(g[e]) + oracle_normal_draw(salt, (uint32_t)e) * scale);
+}
+
 static inline float rbf(float f) { return bf16_to_f32(oracle_f32_to_bf16(f)); }
 
 /* C[I][J] = bf16(sum_r A(i,r) B(r,j)); A(i,r) = a[i*lda_i + r*lda_r], likewise B */

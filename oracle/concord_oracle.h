@@ -115,6 +115,13 @@ float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K);
 /* sum of gate_coherence_from_fields (concord/packed_b.py:2081-2091) over the
  * N x K words, in the library's block / lane / tree order */
 float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C);
+/* standard normal draw idx of stream seed: Box-Muller on one Philox4x32-10
+ * block, with this build's fixed-order log2 / sqrt / cos(2 pi u) */
+float oracle_normal_draw(int32_t seed, uint32_t idx);
+/* isotropic gradient noise in place: g <- bf16(g + xi * (sigma * ||g|| /
+ * max(||xi||, 1e-12))), xi_e = oracle_normal_draw(salt, e)
+ * (notebook/src/prototype_packed_b.py:1484-1501, isotropic branch) */
+void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t salt);
 void oracle_muon_ns5(const uint16_t* g, int64_t N, int64_t K, float gamma, uint16_t* out);
 
 void oracle_set_threads(int n);

@@ -83,6 +83,9 @@ def lib():
         L.oracle_frob_sumsq.argtypes = [P, i64, i64]
         L.oracle_coherence_sum.restype = f32
         L.oracle_coherence_sum.argtypes = [P, i64, i64, f32]
+        L.oracle_normal_draw.restype = f32
+        L.oracle_normal_draw.argtypes = [i32, ctypes.c_uint32]
+        L.oracle_iso_noise.argtypes = [P, i64, i64, f32, i32]
         L.oracle_muon_ns5.argtypes = [P, i64, i64, f32, P]
         L.oracle_rebalance.argtypes = [P, P, P, P, P, P, P, i64, i64, i32, i32, i32,
                                        i32, ctypes.c_int]
@@ -209,6 +212,19 @@ def coherence_sum(packed, drift_cancel_C):
     """Sum of the gate's Wiener gain over the words (fixed library order)."""
     p = np.ascontiguousarray(packed, dtype=np.int32)
     return np.float32(lib().oracle_coherence_sum(_p(p), p.shape[0], p.shape[1], float(drift_cancel_C)))
+
+
+def normal_draws(seed, n, start=0):
+    """Draws start .. start + n - 1 of the library's normal stream `seed`."""
+    f = lib().oracle_normal_draw
+    return np.array([f(int(seed), (start + i) & 0xFFFFFFFF) for i in range(n)], dtype=np.float32)
+
+
+def iso_noise(grad_bf16, sigma, salt):
+    """Isotropic noise injection on bf16 bits (returns a new array)."""
+    g = np.ascontiguousarray(grad_bf16, dtype=np.uint16).copy()
+    lib().oracle_iso_noise(_p(g), g.shape[0], g.shape[1], float(sigma), int(salt))
+    return g
 
 
 def muon_ns5(grad_bf16, gamma=None):

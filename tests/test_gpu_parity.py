@@ -1139,3 +1139,53 @@ def test_dgrad_wgrad_vhat_matches_separate_calls(M, N, K):
     for a, b in zip(*outs):
         np.testing.assert_array_equal(a, b)
     assert (outs[0][6] == 0).all() and outs[0][8][0] == 6
+
+
+# ---------------------------------------------------------------- gradient noise
+
+@pytest.mark.parametrize("N,K,ld,sigma", [(384, 256, 256, 0.1), (5120, 1280, 1280, 0.5), (33, 100, 104, 2.0)])
+def test_iso_noise_bit_exact(oracle, N, K, ld, sigma):
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(N + K)
+    g = oracle.f32_to_bf16_bits_array((rng.standard_normal((N, ld)) * 1e-3).astype(np.float32))
+    gd = dev(g)
+    salt = torch.full((1,), 4242, dtype=torch.int32, device=DEV)
+    sig = torch.full((1,), sigma, dtype=torch.float32, device=DEV)
+    pb.iso_noise_(gd[:, :K], sigma=sig, salt_counter=salt)
+    sync()
+    out = host(gd).view(np.uint16)
+    np.testing.assert_array_equal(out[:, :K], oracle.iso_noise(np.ascontiguousarray(g[:, :K]), sigma, 4242))
+    np.testing.assert_array_equal(out[:, K:], g[:, K:])   # the row padding is untouched
+    assert int(host(salt)[0]) == 4242
+
+
+def test_layer_iso_noise_step(oracle):
+    """With the isotropic noise on, backward feeds the v-hat EMA and the
+    update the noisy gradient: the captured grad_W equals the oracle's
+    injection applied to the plain product, at the salt of the step."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    torch.manual_seed(13)
+    layer = ca.ConcordLinearPackedB(256, 384, bias=True, device=DEV, lr=1e-3)
+    x = torch.randn(512, 256, device=DEV).to(torch.bfloat16)
+    gy = (torch.randn(512, 384, device=DEV) * 1e-2).to(torch.bfloat16)
+    salt = pb._get_step_counter(DEV)
+    salt.fill_(900)
+    ca.set_sigmag_noise(True, isotropic=True)
+    ca.set_sigmag_sigma(0.2)
+    cap = []
+    pb._DEBUG_CAPTURE = cap
+    try:
+        xd = x.clone().requires_grad_(True)
+        layer(xd).backward(gy)
+    finally:
+        pb._DEBUG_CAPTURE = None
+        ca.set_sigmag_noise(False)
+        ca.set_sigmag_sigma(0.0)
+    sync()
+    plain = host(pb._wgrad(gy, x)).view(np.uint16)
+    want = oracle.iso_noise(plain, 0.2, 900)
+    np.testing.assert_array_equal(host(cap[0]).view(np.uint16), want)
+    assert int(host(salt)[0]) == 901 and layer.bias.grad is not None
+    with pytest.raises(NotImplementedError):
+        ca.set_sigmag_noise(True)

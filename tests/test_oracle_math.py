@@ -616,3 +616,44 @@ def test_materialize_gated_closed_forms(oracle):
     v = (m * np.exp2(e).astype(np.float32)).astype(np.float32)
     want = oracle.f32_to_bf16_bits_array(v)
     np.testing.assert_array_equal(oracle.materialize_gated(packed, re, ce, 0.37), want)
+
+
+# ---------------------------------------------------------------- gradient noise
+
+def test_normal_draw_matches_float64_box_muller(oracle):
+    """Each draw is Box-Muller on its own Philox4x32-10 block (counter (i, 0,
+    0, 0), key (seed, 0x6E6F6973)); the fixed-order float32 log2 / sqrt /
+    cos(2 pi u) agree with float64 to ~1e-6 of the draw's scale."""
+    seed = -12345
+    z = oracle.normal_draws(seed, 4000)
+    for i in range(0, 4000, 37):
+        c = oracle.philox4x32_10([i, 0, 0, 0], [seed & 0xFFFFFFFF, 0x6E6F6973])
+        u1 = ((int(c[0]) >> 8) + 1) * 2.0 ** -24
+        u2 = (int(c[1]) >> 8) * 2.0 ** -24
+        want = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+        assert abs(float(z[i]) - want) <= 4e-6 * max(1.0, abs(want)), (i, z[i], want)
+
+
+def test_normal_draw_statistics(oracle):
+    z = oracle.normal_draws(7, 400000).astype(np.float64)
+    assert abs(z.mean()) < 5e-3 and abs(z.std() - 1.0) < 5e-3
+    assert abs((np.abs(z) > 2.0).mean() - 0.0455) < 2e-3
+    assert abs(np.mean(z ** 4) - 3.0) < 5e-2          # Gaussian kurtosis
+    z2 = oracle.normal_draws(8, 400000).astype(np.float64)
+    assert abs(np.corrcoef(z, z2)[0, 1]) < 1e-2       # streams of different seeds
+
+
+def test_iso_noise_closed_forms(oracle):
+    rng = np.random.default_rng(2)
+    g = oracle.f32_to_bf16_bits_array((rng.standard_normal((37, 300)) * 1e-3).astype(np.float32))
+    np.testing.assert_array_equal(oracle.iso_noise(g, 0.0, 5), g)           # sigma = 0
+    zero = np.zeros((20, 50), np.uint16)
+    np.testing.assert_array_equal(oracle.iso_noise(zero, 0.3, 5), zero)     # ||g|| = 0
+    out = oracle.iso_noise(g, 0.1, 5)
+    gf = oracle.bf16_bits_to_f32(g).astype(np.float64)
+    d = oracle.bf16_bits_to_f32(out).astype(np.float64) - gf
+    # the added noise has norm sigma ||g|| (up to the bf16 rounding of g + noise)
+    assert abs(np.linalg.norm(d) / np.linalg.norm(gf) - 0.1) < 5e-3
+    # and follows the stream: the same salt draws the same noise, another does not
+    np.testing.assert_array_equal(oracle.iso_noise(g, 0.1, 5), out)
+    assert (oracle.iso_noise(g, 0.1, 6) != out).any()
