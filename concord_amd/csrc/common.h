@@ -226,15 +226,17 @@ CONCORD_DEV float det_cos2pi(float u) {
   return q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
 }
 
-// Standard normal draw `idx` of stream `seed` (Box-Muller on one Philox4x32-10
-// block; counter (idx, 0, 0, 0), key (seed, 0x6E6F6973)):
+// Standard normal draw `idx` of stream (seed, tag) (Box-Muller on one
+// Philox4x32-10 block; counter (idx, 0, 0, 0), key (seed, tag); the
+// isotropic noise uses tag 0x6E6F6973, the per-token draw 0x5369676D):
 //   u1 = ((c0 >> 8) + 1) 2^-24 in (0, 1],  u2 = (c1 >> 8) 2^-24 in [0, 1),
 //   z = sqrt(-2 ln u1) cos(2 pi u2), ln u1 = log2(u1) ln 2.
 // A fixed sequence of IEEE ops (det_log2, sqrt_rn, det_cos2pi), so the CPU
 // restatement draws the same bits.
-CONCORD_DEV float normal_draw(int32_t seed, uint32_t idx) {
+constexpr uint32_t kNoiseTagIso = 0x6E6F6973u, kNoiseTagToken = 0x5369676Du;
+CONCORD_DEV float normal_draw(int32_t seed, uint32_t idx, uint32_t tag = kNoiseTagIso) {
   uint32_t c0 = idx, c1 = 0, c2 = 0, c3 = 0;
-  philox4x32_10(c0, c1, c2, c3, (uint32_t)seed, 0x6E6F6973u);
+  philox4x32_10(c0, c1, c2, c3, (uint32_t)seed, tag);
   const float u1 = __fmul_rn((float)((c0 >> 8) + 1u), 5.9604644775390625e-08f);
   const float u2 = __fmul_rn((float)(c1 >> 8), 5.9604644775390625e-08f);
   const float ln = __fmul_rn(det_log2(u1), 0.693147180559945309f);

@@ -499,6 +499,7 @@ int gemm_bf16_run(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, i
   GemmArgs g = make_args(a, b, lda, ldb, nullptr, nullptr, 0, nullptr, c, ldc, I, J, R, false);
   if (mode == MODE_FWD_BF16) return launch_gemm<MODE_FWD_BF16>(g, ws, ws_bytes, st, what);
   if (mode == MODE_DGRAD_BF16) return launch_gemm<MODE_DGRAD_BF16>(g, ws, ws_bytes, st, what);
+  if (mode == MODE_WGRAD) return launch_gemm<MODE_WGRAD>(g, ws, ws_bytes, st, what);
   set_error("%s: unsupported product", what);
   return CONCORD_EINVAL;
 }

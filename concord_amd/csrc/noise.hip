@@ -6,6 +6,7 @@
 // changes).  xi is normal_draw(salt, element index): counter-based, so the
 // three passes regenerate the same draws instead of storing them.
 #include "common.h"
+#include "gemm.h"
 
 namespace concord {
 
@@ -78,9 +79,176 @@ __global__ __launch_bounds__(256) void noise_apply_kernel(uint16_t* __restrict__
   *p = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
 }
 
+// ---- the Sigma_g-shaped draw (prototype_packed_b.py:1489-1496) ---------------
+// noise = (eps * dy)^T x - (sum eps) * (g / M), eps_m = normal_draw(salt, m,
+// kNoiseTagToken): a draw whose covariance is the empirical per-token
+// gradient covariance, centred.  The product runs on the WGRAD kernels (bf16
+// operands, fp32 accumulation); everything around it is elementwise or a
+// fixed-order reduction.
+
+// dyt[m][n] = bf16(eps_m * dy[m][n])
+__global__ __launch_bounds__(256) void token_scale_kernel(const uint16_t* __restrict__ dy, int64_t ld, int64_t M,
+                                                          int64_t N, const int32_t* salt,
+                                                          uint16_t* __restrict__ out) {
+  const int64_t m = blockIdx.y;
+  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (n >= N) return;
+  const float e = normal_draw(*salt, (uint32_t)m, kNoiseTagToken);
+  out[m * N + n] = (uint16_t)(pack_bf16x2(__fmul_rn(e, bf16_to_f32(dy[m * ld + n])), 0.0f) & 0xFFFFu);
+}
+
+// sum of eps_0 .. eps_{M-1} in kNoiseBlock blocks (lane chains, halving tree);
+// the block partials are chained by token_sum_final_kernel
+__global__ __launch_bounds__(256) void token_sum_partials_kernel(int64_t M, const int32_t* salt,
+                                                                 float* __restrict__ part) {
+  __shared__ float s[256];
+  const int64_t b0 = (int64_t)blockIdx.x * kNoiseBlock;
+  const int32_t seed = *salt;
+  float a = 0.0f;
+  for (int i = 0; i < kNoiseBlock / 256; ++i) {
+    const int64_t m = b0 + threadIdx.x + 256 * i;
+    if (m < M) a = __fadd_rn(a, normal_draw(seed, (uint32_t)m, kNoiseTagToken));
+  }
+  s[threadIdx.x] = a;
+  __syncthreads();
+  for (int h = 128; h >= 1; h >>= 1) {
+    if (threadIdx.x < h) s[threadIdx.x] = __fadd_rn(s[threadIdx.x], s[threadIdx.x + h]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) part[blockIdx.x] = s[0];
+}
+
+__global__ __launch_bounds__(64) void token_sum_final_kernel(const float* __restrict__ part, int64_t nb,
+                                                             float* out) {
+  const int lane = threadIdx.x;
+  float s = 0.0f;
+  for (int64_t c0 = 0; c0 < nb; c0 += 64) {
+    const float v = c0 + lane < nb ? part[c0 + lane] : 0.0f;
+    const int cnt = (int)min((int64_t)64, nb - c0);
+    for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, lane_value(v, j));
+  }
+  if (lane == 0) *out = s;
+}
+
+// noise_e = f32(P_e) - S * (g_e / M)
+CONCORD_DEV float sigmag_noise(float p, float g, float S, float Mf) {
+  return __fsub_rn(p, __fmul_rn(S, __fdiv_rn(g, Mf)));
+}
+
+__global__ __launch_bounds__(256) void sigmag_partials_kernel(const uint16_t* __restrict__ g, int64_t ld,
+                                                              const uint16_t* __restrict__ P, int64_t N,
+                                                              int64_t K, const float* Ssum, float Mf,
+                                                              float* __restrict__ part) {
+  __shared__ float sg[256], sx[256];
+  const int64_t total = N * K;
+  const int64_t b0 = (int64_t)blockIdx.x * kNoiseBlock;
+  const float S = *Ssum;
+  float ag = 0.0f, ax = 0.0f;
+  for (int i = 0; i < kNoiseBlock / 256; ++i) {
+    const int64_t e = b0 + threadIdx.x + 256 * i;
+    if (e < total) {
+      const float v = bf16_to_f32(g[(e / K) * ld + e % K]);
+      const float z = sigmag_noise(bf16_to_f32(P[e]), v, S, Mf);
+      ag = __fadd_rn(ag, __fmul_rn(v, v));
+      ax = __fadd_rn(ax, __fmul_rn(z, z));
+    }
+  }
+  sg[threadIdx.x] = ag;
+  sx[threadIdx.x] = ax;
+  __syncthreads();
+  for (int h = 128; h >= 1; h >>= 1) {
+    if (threadIdx.x < h) {
+      sg[threadIdx.x] = __fadd_rn(sg[threadIdx.x], sg[threadIdx.x + h]);
+      sx[threadIdx.x] = __fadd_rn(sx[threadIdx.x], sx[threadIdx.x + h]);
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    part[2 * blockIdx.x] = sg[0];
+    part[2 * blockIdx.x + 1] = sx[0];
+  }
+}
+
+__global__ __launch_bounds__(256) void sigmag_apply_kernel(uint16_t* __restrict__ g, int64_t ld,
+                                                           const uint16_t* __restrict__ P, int64_t N, int64_t K,
+                                                           const float* Ssum, float Mf, const float* scale) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= N * K) return;
+  const float S = *Ssum, sc = *scale;
+  uint16_t* p = g + (e / K) * ld + e % K;
+  const float v = bf16_to_f32(*p);
+  const float r = __fadd_rn(v, __fmul_rn(sigmag_noise(bf16_to_f32(P[e]), v, S, Mf), sc));
+  *p = (uint16_t)(pack_bf16x2(r, 0.0f) & 0xFFFFu);
+}
+
+struct SigmagLayout {
+  size_t dyt, prod, part, tpart, ssum, scale, gemm, total;
+};
+static SigmagLayout sigmag_layout(int64_t M, int64_t N, int64_t K) {
+  auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
+  SigmagLayout L;
+  size_t o = 0;
+  L.dyt = o; o += r256((size_t)M * N * 2);
+  L.prod = o; o += r256((size_t)N * K * 2);
+  L.part = o; o += r256((size_t)2 * cdiv(N * K, kNoiseBlock) * 4);
+  L.tpart = o; o += r256((size_t)cdiv(M, kNoiseBlock) * 4);
+  L.ssum = o; o += 256;
+  L.scale = o; o += 256;
+  L.gemm = o; o += r256(gemm_splitk_need(MODE_WGRAD, N, K, M));
+  L.total = o;
+  return L;
+}
+
 }  // namespace concord
 
 using namespace concord;
+
+extern "C" size_t concord_sigmag_noise_workspace_bytes(int64_t M, int64_t N, int64_t K) {
+  return sigmag_layout(M > 0 ? M : 1, N > 0 ? N : 1, K > 0 ? K : 1).total;
+}
+
+extern "C" int concord_sigmag_noise(uint16_t* grad_w, int64_t ld_g, const uint16_t* dy, int64_t ld_dy,
+                                    const uint16_t* x, int64_t ld_x, int64_t M, int64_t N, int64_t K,
+                                    const float* sigma, const int32_t* salt_counter, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  CONCORD_CHECK(M >= 0 && N >= 0 && K >= 0 && N * K < (1LL << 32) && M * N < (1LL << 40) && M < (1LL << 31),
+                "concord_sigmag_noise: bad size");
+  if (N == 0 || K == 0) return CONCORD_OK;
+  CONCORD_CHECK(grad_w && dy && x && sigma && salt_counter, "concord_sigmag_noise: NULL argument");
+  CONCORD_CHECK(ld_g >= K && ld_dy >= N && ld_x >= K, "concord_sigmag_noise: bad leading dimension");
+  const SigmagLayout L = sigmag_layout(M > 0 ? M : 1, N, K);
+  if (!workspace || workspace_bytes < L.total) {
+    set_error("concord_sigmag_noise: workspace of %zu bytes needed", L.total);
+    return CONCORD_EWORKSPACE;
+  }
+  char* w = (char*)workspace;
+  uint16_t* dyt = (uint16_t*)(w + L.dyt);
+  uint16_t* prod = (uint16_t*)(w + L.prod);
+  float* part = (float*)(w + L.part);
+  float* tpart = (float*)(w + L.tpart);
+  float* ssum = (float*)(w + L.ssum);
+  float* scale = (float*)(w + L.scale);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t tb = M > 0 ? cdiv(M, kNoiseBlock) : 0;
+  if (M > 0) {
+    hipLaunchKernelGGL(token_scale_kernel, dim3((unsigned)cdiv(N, 256), (unsigned)M), dim3(256), 0, st, dy,
+                       ld_dy, M, N, salt_counter, dyt);
+    hipLaunchKernelGGL(token_sum_partials_kernel, dim3((unsigned)tb), dim3(256), 0, st, M, salt_counter, tpart);
+  }
+  hipLaunchKernelGGL(token_sum_final_kernel, dim3(1), dim3(64), 0, st, tpart, tb, ssum);
+  // P = dyt^T x (the WGRAD product of the scaled dy), bf16
+  const int rc = gemm_bf16_run(MODE_WGRAD, dyt, N, x, ld_x, prod, K, N, K, M, w + L.gemm,
+                               L.total - L.gemm, st, "sigmag_noise");
+  if (rc != CONCORD_OK) return rc;
+  const float Mf = (float)(M > 1 ? M : 1);
+  const int64_t nb = cdiv(N * K, kNoiseBlock);
+  hipLaunchKernelGGL(sigmag_partials_kernel, dim3((unsigned)nb), dim3(256), 0, st, grad_w, ld_g, prod, N, K, ssum,
+                     Mf, part);
+  hipLaunchKernelGGL(noise_scale_kernel, dim3(1), dim3(64), 0, st, part, nb, sigma, scale);
+  hipLaunchKernelGGL(sigmag_apply_kernel, dim3((unsigned)cdiv(N * K, 256)), dim3(256), 0, st, grad_w, ld_g, prod,
+                     N, K, ssum, Mf, scale);
+  return launch_status("sigmag_noise");
+}
 
 extern "C" size_t concord_noise_workspace_bytes(int64_t N, int64_t K) {
   const int64_t nb = N * K > 0 ? cdiv(N * K, kNoiseBlock) : 0;

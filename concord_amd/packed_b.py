@@ -661,7 +661,11 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
             # injection, then the standalone v-hat entry
             grad_x = _gemm_dgrad(dy, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias,
                                  ctx.weight_buf).reshape(*ctx.lead, K)
-            grad_W = iso_noise_(_wgrad(dy, x2), salt_counter=salt)
+            grad_W = _wgrad(dy, x2)
+            if _SIGMAG_ISO:
+                iso_noise_(grad_W, salt_counter=salt)
+            else:
+                sigmag_noise_(grad_W, dy, x2, salt_counter=salt)
             if muon:
                 grad_W = muon_ns5(grad_W)
             elif vhat:
@@ -1074,12 +1078,9 @@ _NOISE_WORKSPACES = {}
 def set_sigmag_noise(enabled, isotropic=False):
     """Turn the gradient-noise injection on or off (a Python switch: a
     captured graph keeps the choice made at capture, as in the reference).
-    Built: the isotropic draw, grad_W + sigma ||grad_W|| xi / ||xi||.  The
-    reference's default Sigma_g-shaped draw is not built and raises."""
+    Default: the centred Sigma_g-shaped draw (eps * dy)^T x - (sum eps) g / M;
+    isotropic=True: white noise.  Either is scaled to sigma ||grad_W||."""
     global _SIGMAG_NOISE, _SIGMAG_ISO
-    if enabled and not isotropic:
-        raise NotImplementedError("concord_amd: only the isotropic gradient-noise draw is built "
-                                  "(set_sigmag_noise(True, isotropic=True))")
     _SIGMAG_NOISE = bool(enabled)
     _SIGMAG_ISO = bool(isotropic)
 
@@ -1100,6 +1101,35 @@ def _get_sigmag_sigma(device):
         t = torch.full((1,), _SIGMAG_SIGMA, dtype=torch.float32, device=key)
         _SIGMAG_SIGMA_T[key] = t
     return t
+
+
+_SIGMAG_WORKSPACES = {}
+
+
+def sigmag_noise_(grad_W, dy, x2, sigma=None, salt_counter=None):
+    """grad_W <- bf16(g + n sigma ||g|| / max(||n||, 1e-12)) in place with the
+    centred Sigma_g-shaped draw n = (eps * dy)^T x - (sum eps) g / M
+    (prototype_packed_b.py:1489-1500; concord_sigmag_noise); eps_m is the
+    library's per-token normal stream keyed by the salt counter (read, not
+    advanced), and the product runs on the WGRAD kernels."""
+    C.require_device_tensor(grad_W, "grad_W")
+    N, K = grad_W.shape
+    M = dy.shape[0]
+    dev = grad_W.device
+    if sigma is None:
+        sigma = _get_sigmag_sigma(dev)
+    if salt_counter is None:
+        salt_counter = _get_step_counter(dev)
+    key = _dev_key(dev)
+    need = int(C.lib().concord_sigmag_noise_workspace_bytes(M, N, K))
+    ws = _SIGMAG_WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=key)
+        _SIGMAG_WORKSPACES[key] = ws
+    C.check(C.lib().concord_sigmag_noise(C.ptr(grad_W), grad_W.stride(0), C.ptr(dy), dy.stride(0), C.ptr(x2),
+                                         x2.stride(0), M, N, K, C.ptr(sigma), C.ptr(salt_counter), C.ptr(ws),
+                                         ws.numel(), C.stream_of(dev)), "sigmag_noise")
+    return grad_W
 
 
 def iso_noise_(grad_W, sigma=None, salt_counter=None):

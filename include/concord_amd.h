@@ -283,6 +283,22 @@ size_t concord_noise_workspace_bytes(int64_t N, int64_t K);
 int concord_iso_noise(uint16_t* grad_w, int64_t ld_g, int64_t N, int64_t K, const float* sigma,
                       const int32_t* salt_counter, void* workspace, size_t workspace_bytes, void* stream);
 
+/* The Sigma_g-shaped draw, the reference's default when its noise is on
+ * (notebook/src/prototype_packed_b.py:1489-1500): in place on the bf16
+ * gradient g of dy[M,N]^T x[M,K],
+ *   n = (eps * dy)^T x - (sum_m eps_m) * (g / M),   eps_m ~ N(0, 1) per token,
+ *   g <- bf16(g + n * (sigma * ||g|| / max(||n||, 1e-12))).
+ * eps_m is the counter-based normal stream of concord_iso_noise with its own
+ * key (second word 0x5369676D) at the salt counter's current value (read,
+ * not advanced); the product is this library's WGRAD on bf16(eps_m dy[m,:])
+ * with fp32 accumulation.  workspace: concord_sigmag_noise_workspace_bytes(M,
+ * N, K) bytes (the scaled dy, the product, reductions, a split-K region),
+ * zero-filled once when allocated. */
+size_t concord_sigmag_noise_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int concord_sigmag_noise(uint16_t* grad_w, int64_t ld_g, const uint16_t* dy, int64_t ld_dy, const uint16_t* x,
+                         int64_t ld_x, int64_t M, int64_t N, int64_t K, const float* sigma,
+                         const int32_t* salt_counter, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

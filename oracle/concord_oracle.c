@@ -740,9 +740,11 @@ static float det_cos2pi(float u) {
     return q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
 }
 
-float oracle_normal_draw(int32_t seed, uint32_t idx) {
+float oracle_normal_draw(int32_t seed, uint32_t idx) { return oracle_normal_draw_tag(seed, idx, 0x6E6F6973u); }
+
+float oracle_normal_draw_tag(int32_t seed, uint32_t idx, uint32_t tag) {
     uint32_t c[4] = {idx, 0u, 0u, 0u};
-    uint32_t k[2] = {(uint32_t)seed, 0x6E6F6973u};
+    uint32_t k[2] = {(uint32_t)seed, tag};
     oracle_philox4x32_10(c, k);
     const float u1 = (float)((c[0] >> 8) + 1u) * 5.9604644775390625e-08f;
     const float u2 = (float)(c[1] >> 8) * 5.9604644775390625e-08f;
@@ -782,6 +784,60 @@ void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t sa
     const float scale = (sigma * ng) / nx;
     for (int64_t e = 0; e < total; ++e)
         g[e] = oracle_f32_to_bf16(bf16_to_f32(g[e]) + oracle_normal_draw(salt, (uint32_t)e) * scale);
+}
+
+float oracle_token_sum(int32_t seed, int64_t M) {
+    float acc = 0.0f;
+    for (int64_t b0 = 0; b0 < M; b0 += 8192) {
+        float part[256];
+        for (int t = 0; t < 256; ++t) {
+            float a = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                const int64_t m = b0 + t + 256 * i;
+                if (m < M) a = a + oracle_normal_draw_tag(seed, (uint32_t)m, 0x5369676Du);
+            }
+            part[t] = a;
+        }
+        for (int h = 128; h >= 1; h >>= 1)
+            for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
+        acc = acc + part[0];
+    }
+    return acc;
+}
+
+void oracle_sigmag_combine(uint16_t* g, const uint16_t* P, int64_t N, int64_t K, float S, float Mf,
+                           float sigma) {
+    const int64_t total = N * K;
+    float sg = 0.0f, sx = 0.0f;
+    for (int64_t b0 = 0; b0 < total; b0 += 8192) {
+        float pg[256], px[256];
+        for (int t = 0; t < 256; ++t) {
+            float ag = 0.0f, ax = 0.0f;
+            for (int i = 0; i < 32; ++i) {
+                const int64_t e = b0 + t + 256 * i;
+                if (e >= total) continue;
+                const float v = bf16_to_f32(g[e]);
+                const float z = bf16_to_f32(P[e]) - S * (v / Mf);
+                ag = ag + v * v;
+                ax = ax + z * z;
+            }
+            pg[t] = ag;
+            px[t] = ax;
+        }
+        for (int h = 128; h >= 1; h >>= 1)
+            for (int t = 0; t < h; ++t) {
+                pg[t] = pg[t] + pg[t + h];
+                px[t] = px[t] + px[t + h];
+            }
+        sg = sg + pg[0];
+        sx = sx + px[0];
+    }
+    const float scale = (sigma * sqrtf(sg)) / fmaxf(sqrtf(sx), 1e-12f);
+    for (int64_t e = 0; e < total; ++e) {
+        const float v = bf16_to_f32(g[e]);
+        const float z = bf16_to_f32(P[e]) - S * (v / Mf);
+        g[e] = oracle_f32_to_bf16(v + z * scale);
+    }
 }
 
 static inline float rbf(float f) { return bf16_to_f32(oracle_f32_to_bf16(f)); }

@@ -118,6 +118,16 @@ float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C)
 /* standard normal draw idx of stream seed: Box-Muller on one Philox4x32-10
  * block, with this build's fixed-order log2 / sqrt / cos(2 pi u) */
 float oracle_normal_draw(int32_t seed, uint32_t idx);
+/* the same with the Philox key's second word = tag (0x6E6F6973 isotropic,
+ * 0x5369676D per-token) */
+float oracle_normal_draw_tag(int32_t seed, uint32_t idx, uint32_t tag);
+/* sum of the per-token draws 0 .. M-1 in the library's block / lane / tree order */
+float oracle_token_sum(int32_t seed, int64_t M);
+/* Sigma_g combine in place (prototype_packed_b.py:1489-1500), P the product
+ * (eps * dy)^T x as bf16: noise = P - S * (g / M), then
+ * g <- bf16(g + noise * (sigma * ||g|| / max(||noise||, 1e-12))) */
+void oracle_sigmag_combine(uint16_t* g, const uint16_t* P, int64_t N, int64_t K, float S, float Mf,
+                           float sigma);
 /* isotropic gradient noise in place: g <- bf16(g + xi * (sigma * ||g|| /
  * max(||xi||, 1e-12))), xi_e = oracle_normal_draw(salt, e)
  * (notebook/src/prototype_packed_b.py:1484-1501, isotropic branch) */

@@ -86,6 +86,11 @@ def lib():
         L.oracle_normal_draw.restype = f32
         L.oracle_normal_draw.argtypes = [i32, ctypes.c_uint32]
         L.oracle_iso_noise.argtypes = [P, i64, i64, f32, i32]
+        L.oracle_normal_draw_tag.restype = f32
+        L.oracle_normal_draw_tag.argtypes = [i32, ctypes.c_uint32, ctypes.c_uint32]
+        L.oracle_token_sum.restype = f32
+        L.oracle_token_sum.argtypes = [i32, i64]
+        L.oracle_sigmag_combine.argtypes = [P, P, i64, i64, f32, f32, f32]
         L.oracle_muon_ns5.argtypes = [P, i64, i64, f32, P]
         L.oracle_rebalance.argtypes = [P, P, P, P, P, P, P, i64, i64, i32, i32, i32,
                                        i32, ctypes.c_int]
@@ -218,6 +223,27 @@ def normal_draws(seed, n, start=0):
     """Draws start .. start + n - 1 of the library's normal stream `seed`."""
     f = lib().oracle_normal_draw
     return np.array([f(int(seed), (start + i) & 0xFFFFFFFF) for i in range(n)], dtype=np.float32)
+
+
+TAG_TOKEN = 0x5369676D
+
+
+def token_draws(seed, M):
+    """The per-token draws eps_0 .. eps_{M-1} of the Sigma_g noise."""
+    f = lib().oracle_normal_draw_tag
+    return np.array([f(int(seed), m, TAG_TOKEN) for m in range(M)], dtype=np.float32)
+
+
+def token_sum(seed, M):
+    return np.float32(lib().oracle_token_sum(int(seed), int(M)))
+
+
+def sigmag_combine(grad_bf16, P_bf16, S, M, sigma):
+    g = np.ascontiguousarray(grad_bf16, dtype=np.uint16).copy()
+    P = np.ascontiguousarray(P_bf16, dtype=np.uint16)
+    lib().oracle_sigmag_combine(_p(g), _p(P), g.shape[0], g.shape[1], float(S), float(max(M, 1)),
+                                float(sigma))
+    return g
 
 
 def iso_noise(grad_bf16, sigma, salt):

@@ -1187,5 +1187,69 @@ def test_layer_iso_noise_step(oracle):
     want = oracle.iso_noise(plain, 0.2, 900)
     np.testing.assert_array_equal(host(cap[0]).view(np.uint16), want)
     assert int(host(salt)[0]) == 901 and layer.bias.grad is not None
-    with pytest.raises(NotImplementedError):
-        ca.set_sigmag_noise(True)
+
+
+@pytest.mark.parametrize("M,N,K", [(512, 384, 256), (2048, 1280, 640), (77, 96, 40)])
+def test_sigmag_noise_parts(oracle, M, N, K):
+    """The Sigma_g draw: the scaled dy and the token sum bit-exact against
+    the oracle, the product (eps dy)^T x within 1e-2 of fp32, and the
+    combine bit-exact against the oracle given that product (all read back
+    from the workspace)."""
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(M + N)
+    dy = (torch.randn(M, N, device=DEV) * 1e-2).to(torch.bfloat16)
+    x = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    g0 = pb._wgrad(dy, x)
+    g = g0.clone()
+    salt = torch.full((1,), 313, dtype=torch.int32, device=DEV)
+    sig = torch.full((1,), 0.3, dtype=torch.float32, device=DEV)
+    pb.sigmag_noise_(g, dy, x, sigma=sig, salt_counter=salt)
+    sync()
+    ws = pb._SIGMAG_WORKSPACES[pb._dev_key(torch.device(DEV))]
+    r256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
+    o_prod = r256(M * N * 2)
+    o_ssum = o_prod + r256(N * K * 2) + r256(2 * -(-N * K // 8192) * 4) + r256(-(-M // 8192) * 4)
+    dyt = host(ws[:M * N * 2].view(torch.bfloat16)).view(np.uint16).reshape(M, N)
+    P = host(ws[o_prod:o_prod + N * K * 2].view(torch.bfloat16)).view(np.uint16).reshape(N, K)
+    S = host(ws[o_ssum:o_ssum + 4].view(torch.float32))[0]
+    eps = oracle.token_draws(313, M)
+    dyf = host(dy.float())
+    np.testing.assert_array_equal(dyt, oracle.f32_to_bf16_bits_array((eps[:, None] * dyf).astype(np.float32)))
+    assert S.view(np.uint32) == oracle.token_sum(313, M).view(np.uint32)
+    ref = oracle.bf16_bits_to_f32(dyt).astype(np.float64).T @ host(x.float()).astype(np.float64)
+    assert rel_l2(oracle.bf16_bits_to_f32(P).astype(np.float64), ref) < 1e-2
+    want = oracle.sigmag_combine(host(g0).view(np.uint16), P, S, M, 0.3)
+    np.testing.assert_array_equal(host(g).view(np.uint16), want)
+    assert int(host(salt)[0]) == 313
+
+
+def test_layer_sigmag_noise_step():
+    """The layer's backward with the default (Sigma_g) noise on: the update
+    sees a gradient whose added part has norm sigma ||grad_W||, and two runs
+    at the same salt inject the same noise."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    torch.manual_seed(14)
+    x = torch.randn(512, 256, device=DEV).to(torch.bfloat16)
+    gy = (torch.randn(512, 384, device=DEV) * 1e-2).to(torch.bfloat16)
+    plain = pb._wgrad(gy, x).float()
+    caps = []
+    ca.set_sigmag_noise(True)
+    ca.set_sigmag_sigma(0.25)
+    try:
+        for _ in range(2):
+            pb._get_step_counter(DEV).fill_(600)
+            layer = ca.ConcordLinearPackedB(256, 384, bias=False, device=DEV, lr=1e-3)
+            cap = []
+            pb._DEBUG_CAPTURE = cap
+            layer(x.clone().requires_grad_(True)).backward(gy)
+            pb._DEBUG_CAPTURE = None
+            caps.append(cap[0].float())
+    finally:
+        pb._DEBUG_CAPTURE = None
+        ca.set_sigmag_noise(False)
+        ca.set_sigmag_sigma(0.0)
+    sync()
+    np.testing.assert_array_equal(host(caps[0]), host(caps[1]))
+    d = (caps[0] - plain).norm().item() / plain.norm().item()
+    assert abs(d - 0.25) < 1e-2, d

@@ -657,3 +657,61 @@ def test_iso_noise_closed_forms(oracle):
     # and follows the stream: the same salt draws the same noise, another does not
     np.testing.assert_array_equal(oracle.iso_noise(g, 0.1, 5), out)
     assert (oracle.iso_noise(g, 0.1, 6) != out).any()
+
+
+def test_token_draws_are_the_tagged_stream(oracle):
+    """The per-token draws use the same Box-Muller on Philox block (m, 0, 0,
+    0) as the isotropic stream, under the second key word 0x5369676D, and
+    the token sum is their fixed-order float32 total."""
+    seed = 4242
+    eps = oracle.token_draws(seed, 3000)
+    for m in range(0, 3000, 53):
+        c = oracle.philox4x32_10([m, 0, 0, 0], [seed, oracle.TAG_TOKEN])
+        u1 = ((int(c[0]) >> 8) + 1) * 2.0 ** -24
+        u2 = (int(c[1]) >> 8) * 2.0 ** -24
+        want = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
+        assert abs(float(eps[m]) - want) <= 4e-6 * max(1.0, abs(want))
+    assert not np.array_equal(eps[:100], oracle.normal_draws(seed, 100))
+    for M in (1, 7, 8192, 8193, 20000):
+        e = oracle.token_draws(seed, M).astype(np.float64)
+        assert abs(float(oracle.token_sum(seed, M)) - e.sum()) < 1e-5 * max(1.0, np.abs(e).sum())
+    assert float(oracle.token_sum(seed, 1)) == float(oracle.token_draws(seed, 1)[0])
+
+
+def test_sigmag_combine_closed_forms(oracle):
+    rng = np.random.default_rng(3)
+    g = oracle.f32_to_bf16_bits_array((rng.standard_normal((40, 70)) * 1e-2).astype(np.float32))
+    P = oracle.f32_to_bf16_bits_array((rng.standard_normal((40, 70)) * 1e-2).astype(np.float32))
+    np.testing.assert_array_equal(oracle.sigmag_combine(g, P, 1.5, 64, 0.0), g)   # sigma = 0
+    # P = S g / M exactly (M a power of two, S = M): the centred draw is zero
+    np.testing.assert_array_equal(oracle.sigmag_combine(g, g, 64.0, 64, 0.3), g)
+    # otherwise the added part has norm sigma ||g|| along P - S g / M
+    out = oracle.sigmag_combine(g, P, 3.0, 16, 0.2)
+    gf = oracle.bf16_bits_to_f32(g).astype(np.float64)
+    d = oracle.bf16_bits_to_f32(out).astype(np.float64) - gf
+    z = oracle.bf16_bits_to_f32(P).astype(np.float64) - 3.0 * gf / 16
+    assert abs(np.linalg.norm(d) / np.linalg.norm(gf) - 0.2) < 5e-3
+    assert np.dot(d.ravel(), z.ravel()) / (np.linalg.norm(d) * np.linalg.norm(z)) > 0.999
+
+
+def test_sigmag_draw_is_centred_per_token_gradients(oracle):
+    """Brute force on a tiny layer: the draw the library forms from the
+    scaled dy, the bf16 product and the token sum points along
+    sum_m eps_m (g_m - mean_m g_m), g_m = dy_m^T x_m, the definition of a
+    Sigma_g-shaped sample."""
+    rng = np.random.default_rng(9)
+    M, N, K, seed, sigma = 24, 12, 10, 77, 0.5
+    dy = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits_array(rng.standard_normal((M, N)).astype(np.float32)))
+    x = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32)))
+    eps = oracle.token_draws(seed, M)
+    gm = np.einsum("mn,mk->mnk", dy.astype(np.float64), x.astype(np.float64))
+    want = np.einsum("m,mnk->nk", eps.astype(np.float64), gm - gm.mean(axis=0))
+    g_bits = oracle.f32_to_bf16_bits_array(gm.sum(axis=0).astype(np.float32))
+    dyt = oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits_array((eps[:, None] * dy).astype(np.float32)))
+    P_bits = oracle.f32_to_bf16_bits_array((dyt.astype(np.float64).T @ x.astype(np.float64)).astype(np.float32))
+    out = oracle.sigmag_combine(g_bits, P_bits, oracle.token_sum(seed, M), M, sigma)
+    gf = oracle.bf16_bits_to_f32(g_bits).astype(np.float64)
+    d = oracle.bf16_bits_to_f32(out).astype(np.float64) - gf
+    cos = np.dot(d.ravel(), want.ravel()) / (np.linalg.norm(d) * np.linalg.norm(want))
+    assert cos > 0.999, cos
+    assert abs(np.linalg.norm(d) / np.linalg.norm(gf) - sigma) < 1e-2
