@@ -76,9 +76,36 @@ CONCORD_DEV float ordered_sum(const float* __restrict__ v, int64_t stride, int64
   return s;
 }
 
+// two ordered sums (as ordered_sum) whose loads are issued together, 32 + 32
+// in flight: *s1 over v1[0 .. c1), *s2 over v2[0 .. c2)
+CONCORD_DEV void ordered_sum2(const float* __restrict__ v1, int64_t st1, int64_t c1, float* s1,
+                              const float* __restrict__ v2, int64_t st2, int64_t c2, float* s2) {
+  float x1 = 0.0f, x2 = 0.0f;
+  for (int64_t b = 0; b < c1 || b < c2; b += 32) {
+    float a[32], d[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      a[e] = b + e < c1 ? v1[(b + e) * st1] : 0.0f;
+      d[e] = b + e < c2 ? v2[(b + e) * st2] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < 32; ++e) {
+      if (b + e < c1) x1 = __fadd_rn(x1, a[e]);
+      if (b + e < c2) x2 = __fadd_rn(x2, d[e]);
+    }
+  }
+  *s1 = x1;
+  *s2 = x2;
+}
+
+constexpr int VH_COLS = 64;        // columns per column block of the finalize
+constexpr int VH_CHUNK = 128;      // row tiles of column partials staged at a time
+
 // Row/column EMA and watermark zeroing.  Blocks [0, cdiv(N, 256)) take rows
 // and leave the halving-tree total of their 256 new v_row values in bsum;
-// the remaining blocks take columns.  The last row block to finish (a
+// the remaining blocks take VH_COLS columns each: the four waves load the
+// column partials of interleaved row tiles into LDS, one thread per column
+// then sums them in row-tile order.  The last row block to finish (a
 // device-scope ticket) chains the totals in ascending order into
 // 1 / max(sum v_row, 1e-30) and advances the salt.  The totals and the
 // ticket are device-scope atomics (cache-coherent across the XCDs), each
@@ -90,6 +117,7 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
     const float* __restrict__ bpart, int64_t nbp, uint16_t* grad_bias, uint32_t* ticket,
     float* sum_v_inv, int32_t* salt) {
   __shared__ float s_part[256];
+  __shared__ float s_cols[VH_CHUNK * VH_COLS];
   __shared__ uint32_t s_ticket;
   const int64_t rb = cdiv(N, 256);
   const int64_t nc = cdiv(K, 64), nr = cdiv(N, 64);
@@ -97,11 +125,12 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
     float vn = 0.0f;
     if (i < N) {
-      const float s = ordered_sum(pr + i, N, nc);
+      float s, sb;
+      ordered_sum2(pr + i, N, nc, &s, bpart + i, N, grad_bias ? nbp : 0, &sb);
       vn = __fadd_rn(__fmul_rn(v_row[i], b2), __fmul_rn(omb2, s));
       v_row[i] = vn;
       if (row_max) row_max[i] = 0;
-      if (grad_bias) grad_bias[i] = (uint16_t)(pack_bf16x2(ordered_sum(bpart + i, N, nbp), 0.0f) & 0xFFFFu);
+      if (grad_bias) grad_bias[i] = (uint16_t)(pack_bf16x2(sb, 0.0f) & 0xFFFFu);
     }
     s_part[threadIdx.x] = vn;
     __syncthreads();
@@ -131,11 +160,28 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
       __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // re-armed
     }
   } else {
-    const int64_t k = ((int64_t)blockIdx.x - rb) * 256 + threadIdx.x;
-    if (k >= K) return;
-    const float s = ordered_sum(pc + k, K, nr);
-    v_col[k] = __fadd_rn(__fmul_rn(v_col[k], b2), __fmul_rn(omb2, s));
-    if (col_max) col_max[k] = 0;
+    const int c = threadIdx.x % VH_COLS, grp = threadIdx.x / VH_COLS;
+    const int64_t k = ((int64_t)blockIdx.x - rb) * VH_COLS + c;
+    float s = 0.0f;
+    for (int64_t r0 = 0; r0 < nr; r0 += VH_CHUNK) {
+      const int rows = (int)min((int64_t)VH_CHUNK, nr - r0);
+      __syncthreads();   // the previous chunk is consumed
+      float a[VH_CHUNK / 4];
+#pragma unroll
+      for (int e = 0; e < VH_CHUNK / 4; ++e) {
+        const int r = grp + 4 * e;
+        a[e] = r < rows && k < K ? pc[(r0 + r) * K + k] : 0.0f;
+      }
+#pragma unroll
+      for (int e = 0; e < VH_CHUNK / 4; ++e) s_cols[(grp + 4 * e) * VH_COLS + c] = a[e];
+      __syncthreads();
+      if (grp == 0 && k < K)
+        for (int r = 0; r < rows; ++r) s = __fadd_rn(s, s_cols[r * VH_COLS + c]);
+    }
+    if (grp == 0 && k < K) {
+      v_col[k] = __fadd_rn(__fmul_rn(v_col[k], b2), __fmul_rn(omb2, s));
+      if (col_max) col_max[k] = 0;
+    }
   }
 }
 
@@ -153,7 +199,7 @@ void vhat_finish_launch(const float* pr, const float* pc, float* bsum, uint32_t*
   const float b2 = (float)beta2;
   const float omb2 = (float)(1.0 - beta2);
   const int64_t rb = cdiv(N, 256);
-  hipLaunchKernelGGL(vhat_finalize_kernel, dim3((unsigned)(rb + cdiv(K, 256))), dim3(256), 0, st, pr, pc,
+  hipLaunchKernelGGL(vhat_finalize_kernel, dim3((unsigned)(rb + cdiv(K, VH_COLS))), dim3(256), 0, st, pr, pc,
                      N, K, b2, omb2, v_row, v_col, row_max, col_max, bsum, bpart, nbp, grad_bias, ticket,
                      sum_v_inv, salt);
 }

@@ -416,6 +416,36 @@ def test_wgrad_vhat_matches_separate_calls(oracle, M, N, K):
     assert outs[0][3][0] == s
 
 
+def test_wgrad_vhat_repeated_calls(oracle):
+    """Calls in a row over alternating shapes that share one workspace: the
+    launch's block and ticket counters are re-armed by every call and sit at
+    the same offsets for every shape, so each call's v-hat state, 1 / sum v_row
+    and salt equal the oracle's on its own gradient."""
+    from concord_amd import packed_b as pb
+    shapes = [(2048, 5120, 1280), (300, 2056, 648), (2048, 5120, 1280), (512, 10240, 1280), (300, 2056, 648)]
+    for it, (M, N, K) in enumerate(shapes):
+        rng = np.random.default_rng(100 + it)
+        dy = dev(oracle.f32_to_bf16_bits_array((rng.standard_normal((M, N)) * 1e-2).astype(np.float32)))
+        x = dev(oracle.f32_to_bf16_bits_array(rng.standard_normal((M, K)).astype(np.float32)))
+        vr = (rng.random(N) * 1e-6).astype(np.float32)
+        vc = (rng.random(K) * 1e-6).astype(np.float32)
+        vrd, vcd = dev(vr), dev(vc)
+        svi = torch.zeros(1, dtype=torch.float32, device=DEV)
+        rm = torch.full((N,), 7, dtype=torch.int32, device=DEV)
+        cm = torch.full((K,), 7, dtype=torch.int32, device=DEV)
+        salt = torch.tensor([it], dtype=torch.int32, device=DEV)
+        gw, gb = pb._wgrad_vhat(dy, x, vrd, vcd, svi, 0.999, rm, cm, salt, with_bias=it % 2 == 0)
+        sync()
+        s = oracle.vhat_ema(host(gw), vr, vc, 0.999)
+        np.testing.assert_array_equal(host(vrd), vr, err_msg=f"call {it}")
+        np.testing.assert_array_equal(host(vcd), vc, err_msg=f"call {it}")
+        assert host(svi)[0] == s, it
+        assert int(host(salt)[0]) == it + 1 and not host(rm).any() and not host(cm).any()
+        if gb is not None:
+            ref_b = oracle.bf16_bits_to_f32(host(dy)).astype(np.float64).sum(0)
+            assert rel_l2(oracle.bf16_bits_to_f32(host(gb)), ref_b) < 5e-3
+
+
 def test_load_weights_matches_reference_golden():
     from concord_amd import packed_b as pb
     z = np.load(os.path.join(GOLD, "load_weights.npz"))
