@@ -257,10 +257,20 @@ CONCORD_DEV float lane_value(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
+// max over the wave's 64 lanes, as a wave-uniform value.  DPP steps: prefix
+// maxima within each 16-lane row (row_shr 1, 2, 4, 8), then lane 15 of rows 0
+// and 2 into rows 1 and 3 (row_bcast:15) and lane 31 into rows 2 and 3
+// (row_bcast:31); lane 63 then holds the maximum.  A lane with no source
+// keeps its own value (bound_ctrl off, old = v), so any sign is fine.  A
+// shuffle butterfly would cost an LDS round trip per step.
 CONCORD_DEV int32_t wave_max(int32_t v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
-  return v;
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x111, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x112, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x114, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x118, 0xF, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false));
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
