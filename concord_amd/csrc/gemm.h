@@ -33,7 +33,23 @@ struct GemmArgs {
   float* vh_pr;           // WGRAD with v-hat partials: row / column partial sums of g^2
   float* vh_pc;
   float* bpart;           // WGRAD with v-hat partials: bias-gradient partials [tiles_j][I], or NULL
+  // optional combine (fast kernels only): C = bf16(as * ay + at * bf16(product)),
+  // ay[I][J] with leading dimension ldy, in combine_bf16x2's float order
+  const uint16_t* ay;
+  int64_t ldy;
+  float as, at;
 };
+
+// s * y + t * x as the Newton-Schulz combination steps take it (x is the
+// bf16-rounded product; the t = 1 case skips the multiply by t)
+CONCORD_DEV float combine1(float s, float y, float t, float x) {
+  return t == 1.0f ? __fadd_rn(__fmul_rn(s, y), x) : __fadd_rn(__fmul_rn(s, y), __fmul_rn(t, x));
+}
+// two bf16 lanes of y and x -> two bf16 lanes of bf16(s y + t x)
+CONCORD_DEV uint32_t combine_bf16x2(uint32_t yw, uint32_t xw, float s, float t) {
+  return pack_bf16x2(combine1(s, __uint_as_float(yw << 16), t, __uint_as_float(xw << 16)),
+                     combine1(s, __uint_as_float(yw & 0xFFFF0000u), t, __uint_as_float(xw & 0xFFFF0000u)));
+}
 
 // XCD-aware tile order: workgroup w runs on XCD w % 8.  XCD x owns tile
 // indices [x*T/8, (x+1)*T/8) of a grouped row-major order (groups of GI
@@ -72,6 +88,13 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd, void* workspace, size_t ws_
                                  hipStream_t st, const char* what, int* tiles_j);
 // tiles along J of the WGRAD launch above (the bias partials' row count)
 int64_t gemm_wgrad_vhat_tiles_j(int64_t J);
+// c = bf16(s * y + t * bf16(product)) for MODE_FWD_BF16 / MODE_DGRAD_BF16 on
+// the fast kernels (the combine applied in their epilogue or split-K
+// reduction); -1 when the operands do not take the fast kernels (the caller
+// then runs the product and the combination separately)
+int gemm_bf16_combine(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
+                      int64_t ldc, int64_t I, int64_t J, int64_t R, const uint16_t* y, int64_t ldy, float s,
+                      float t, void* ws, size_t ws_bytes, hipStream_t st, const char* what);
 // a plain bf16 product through the fast or generic kernels: MODE_FWD_BF16
 // (C[I][J] = sum_r a[i][r] b[j][r]) or MODE_DGRAD_BF16 (sum_r a[i][r] b[r][j])
 int gemm_bf16_run(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,

@@ -504,6 +504,19 @@ int gemm_bf16_run(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, i
   return CONCORD_EINVAL;
 }
 
+int gemm_bf16_combine(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
+                      int64_t ldc, int64_t I, int64_t J, int64_t R, const uint16_t* y, int64_t ldy, float s,
+                      float t, void* ws, size_t ws_bytes, hipStream_t st, const char* what) {
+  if (mode != MODE_FWD_BF16 && mode != MODE_DGRAD_BF16) return -1;
+  if (I == 0 || J == 0) return CONCORD_OK;
+  GemmArgs g = make_args(a, b, lda, ldb, nullptr, nullptr, 0, nullptr, c, ldc, I, J, R, false);
+  g.ay = y;
+  g.ldy = ldy;
+  g.as = s;
+  g.at = t;
+  return gemm_fast_launch(mode, g, ws, ws_bytes, st, what);
+}
+
 size_t gemm_splitk_need(int mode, int64_t I, int64_t J, int64_t R) {
   return kSplitkCounterBytes + ((splitk_partials(mode, I, J, R) + 255) / 256) * 256;
 }

@@ -466,16 +466,29 @@ CONCORD_DEV void epilogue(const GemmArgs& g, f32x4 (&acc)[NI][NJ], int64_t i0, i
     for (int c = t; c < BI * CPR; c += nthreads) {
       const int rl = c / CPR, cl = (c % CPR) * 8;
       const int64_t i = i0 + rl, j = j0 + cl;
-      if (i < g.I && j < g.J)
-        *reinterpret_cast<uint4*>(g.c + i * g.ldc + j) = *reinterpret_cast<const uint4*>(stage + rl * LDO + cl);
+      if (i < g.I && j < g.J) {
+        uint4 o = *reinterpret_cast<const uint4*>(stage + rl * LDO + cl);
+        if (g.ay) {
+          const uint4 yv = *reinterpret_cast<const uint4*>(g.ay + i * g.ldy + j);
+          o = make_uint4(combine_bf16x2(yv.x, o.x, g.as, g.at), combine_bf16x2(yv.y, o.y, g.as, g.at),
+                         combine_bf16x2(yv.z, o.z, g.as, g.at), combine_bf16x2(yv.w, o.w, g.as, g.at));
+        }
+        *reinterpret_cast<uint4*>(g.c + i * g.ldc + j) = o;
+      }
     }
   } else {
     constexpr int CPR = BJ / 4;
     for (int c = t; c < BI * CPR; c += nthreads) {
       const int rl = c / CPR, cl = (c % CPR) * 4;
       const int64_t i = i0 + rl, j = j0 + cl;
-      if (i < g.I && j < g.J)
-        *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = *reinterpret_cast<const uint2*>(stage + rl * LDO + cl);
+      if (i < g.I && j < g.J) {
+        uint2 o = *reinterpret_cast<const uint2*>(stage + rl * LDO + cl);
+        if (g.ay) {
+          const uint2 yv = *reinterpret_cast<const uint2*>(g.ay + i * g.ldy + j);
+          o = make_uint2(combine_bf16x2(yv.x, o.x, g.as, g.at), combine_bf16x2(yv.y, o.y, g.as, g.at));
+        }
+        *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = o;
+      }
     }
   }
 }
@@ -528,7 +541,12 @@ CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
   float v[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(__fmul_rn(sum[e], sc[e]), bs[e]);
-  *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  uint2 o = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+  if (g.ay) {
+    const uint2 yv = *reinterpret_cast<const uint2*>(g.ay + i * g.ldy + j);
+    o = make_uint2(combine_bf16x2(yv.x, o.x, g.as, g.at), combine_bf16x2(yv.y, o.y, g.as, g.at));
+  }
+  *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = o;
 }
 
 template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
@@ -1410,6 +1428,8 @@ static bool fits31(int64_t bytes) { return bytes < ((int64_t)1 << 30); }
 // alignment and extent rules of the fast kernels, per mode
 static bool eligible(int mode, const GemmArgs& g) {
   if (!(g.ldc % 4 == 0 && g.J % 4 == 0 && al(g.c, 8))) return false;
+  // the combine operand is read at the output's positions, 16 bytes at a time
+  if (g.ay && !(g.ldy % 8 == 0 && g.ldc % 8 == 0 && g.J % 8 == 0 && al(g.ay, 16) && al(g.c, 16))) return false;
   if (g.vbias && !al(g.vbias, 8)) return false;
   switch (mode) {
     case MODE_FWD:

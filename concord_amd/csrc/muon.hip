@@ -12,8 +12,14 @@
 //   5 x:  A = bf16(X X^T); AA = bf16(A A); B = bf16(b A + c AA);
 //         BX = bf16(B X); X = bf16(a X + BX)      (products: bf16 MFMA, fp32 acc)
 //   out = bf16(gamma X), transposed back.
-// The three products run on the library's bf16 GEMM kernels; the elementwise
-// steps are small bandwidth kernels.
+// The three products run on the library's bf16 GEMM kernels.  The two
+// combinations ride in the epilogue of the product they follow (A A -> B,
+// B X -> the new X; gemm_bf16_combine), which writes into a second buffer:
+// B goes to the AA buffer and X ping-pongs between two buffers.  Operands the
+// fast kernels do not take fall back to an elementwise combination kernel;
+// both routes round identically (combine_bf16x2).
+#include <utility>
+
 #include "common.h"
 #include "gemm.h"
 #include "workspace.h"
@@ -122,18 +128,12 @@ __global__ __launch_bounds__(256) void ns5_axpby_kernel(uint16_t* __restrict__ y
     uint32_t o[2];
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      const float y0 = __uint_as_float(yw[h] << 16), y1 = __uint_as_float(yw[h] & 0xFFFF0000u);
-      const float x0 = __uint_as_float(xw[h] << 16), x1 = __uint_as_float(xw[h] & 0xFFFF0000u);
-      const float r0 = t == 1.0f ? __fadd_rn(__fmul_rn(s, y0), x0) : __fadd_rn(__fmul_rn(s, y0), __fmul_rn(t, x0));
-      const float r1 = t == 1.0f ? __fadd_rn(__fmul_rn(s, y1), x1) : __fadd_rn(__fmul_rn(s, y1), __fmul_rn(t, x1));
-      o[h] = pack_bf16x2(r0, r1);
+      o[h] = combine_bf16x2(yw[h], xw[h], s, t);
     }
     *reinterpret_cast<uint2*>(y + i) = make_uint2(o[0], o[1]);
   } else {
     for (int64_t j = i; j < n; ++j) {
-      const float yv = bf16_to_f32(y[j]), xv = bf16_to_f32(x[j]);
-      const float r = t == 1.0f ? __fadd_rn(__fmul_rn(s, yv), xv) : __fadd_rn(__fmul_rn(s, yv), __fmul_rn(t, xv));
-      y[j] = (uint16_t)(pack_bf16x2(r, 0.0f) & 0xFFFFu);
+      y[j] = (uint16_t)(combine_bf16x2(y[j], x[j], s, t) & 0xFFFFu);
     }
   }
 }
@@ -211,14 +211,29 @@ extern "C" int concord_muon_ns5(const uint16_t* g, int64_t ld_g, int64_t N, int6
   for (int it = 0; it < 5; ++it) {
     rc = gemm_bf16_run(MODE_FWD_BF16, X, n, X, n, A, m, m, m, n, gws, gws_bytes, st, "muon_ns5 X X^T");
     if (rc != CONCORD_OK) return rc;
-    rc = gemm_bf16_run(MODE_DGRAD_BF16, A, m, A, m, AA, m, m, m, m, gws, gws_bytes, st, "muon_ns5 A A");
+    // AA buffer <- B = bf16(b A + c bf16(A A))
+    rc = gemm_bf16_combine(MODE_DGRAD_BF16, A, m, A, m, AA, m, m, m, m, A, m, b, c, gws, gws_bytes, st,
+                           "muon_ns5 A A");
+    if (rc == -1) {
+      rc = gemm_bf16_run(MODE_DGRAD_BF16, A, m, A, m, AA, m, m, m, m, gws, gws_bytes, st, "muon_ns5 A A");
+      if (rc != CONCORD_OK) return rc;
+      hipLaunchKernelGGL(ns5_axpby_kernel, dim3((unsigned)cdiv(cdiv(m * m, 4), 256)), dim3(256), 0, st, A, AA,
+                         m * m, b, c);
+      std::swap(A, AA);   // B now in the AA slot, as on the fused route
+    }
     if (rc != CONCORD_OK) return rc;
-    hipLaunchKernelGGL(ns5_axpby_kernel, dim3((unsigned)cdiv(cdiv(m * m, 4), 256)), dim3(256), 0, st, A, AA,
-                       m * m, b, c);
-    rc = gemm_bf16_run(MODE_DGRAD_BF16, A, m, X, n, BX, n, m, n, m, gws, gws_bytes, st, "muon_ns5 B X");
+    // BX buffer <- the new X = bf16(a X + bf16(B X)); then X and BX trade places
+    rc = gemm_bf16_combine(MODE_DGRAD_BF16, AA, m, X, n, BX, n, m, n, m, X, n, a, 1.0f, gws, gws_bytes, st,
+                           "muon_ns5 B X");
+    if (rc == -1) {
+      rc = gemm_bf16_run(MODE_DGRAD_BF16, AA, m, X, n, BX, n, m, n, m, gws, gws_bytes, st, "muon_ns5 B X");
+      if (rc != CONCORD_OK) return rc;
+      hipLaunchKernelGGL(ns5_axpby_kernel, dim3((unsigned)cdiv(cdiv(m * n, 4), 256)), dim3(256), 0, st, X, BX,
+                         m * n, a, 1.0f);
+      std::swap(X, BX);   // the new X now in the BX slot, as on the fused route
+    }
     if (rc != CONCORD_OK) return rc;
-    hipLaunchKernelGGL(ns5_axpby_kernel, dim3((unsigned)cdiv(cdiv(m * n, 4), 256)), dim3(256), 0, st, X, BX,
-                       m * n, a, 1.0f);
+    std::swap(X, BX);
   }
   // out[N][K] = bf16(gamma X) (X^T when transposed)
   const dim3 go((unsigned)cdiv(K, 64), (unsigned)cdiv(N, 64));

@@ -776,6 +776,55 @@ def test_muon_ns5_matches_oracle(oracle, N, K):
     assert rel_l2(got, ref) < 2e-2
 
 
+@pytest.mark.parametrize("N,K", [(1280, 5120), (5120, 1280)])
+def test_muon_ns5_fused_combines_match_two_step(oracle, N, K):
+    """NS5's two combinations ride in the epilogue of the product before them
+    (A A -> B = bf16(b A + c bf16(A A)), B X -> X = bf16(a X + bf16(B X))).
+    Re-running the two-step route -- the library's own bf16 GEMM entries
+    (same tile and split plans), the combinations in float32 on the host --
+    gives the same bits."""
+    from concord_amd import _lib as C
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(N + 7)
+    g = oracle.f32_to_bf16_bits_array((rng.standard_normal((N, K)) * 1e-3).astype(np.float32))
+    gamma = float(np.float32(np.sqrt(np.float32(max(N, K)))))
+    o = pb.muon_ns5(dev(g), gamma=gamma)
+    sync()
+    f32, bf = np.float32, oracle.f32_to_bf16_bits_array
+    den = f32(np.sqrt(oracle.frob_sumsq(g))) + f32(1e-7)
+    gf = oracle.bf16_bits_to_f32(g)
+    if N > K:
+        gf = np.ascontiguousarray(gf.T)
+    m, n = gf.shape
+    X = bf((gf / den).astype(np.float32))
+    ws = torch.zeros(int(C.lib().concord_muon_workspace_bytes(N, K)), dtype=torch.uint8, device=DEV)
+    st = C.stream_of(torch.device(DEV))
+    a, b, c = f32(3.4445), f32(-4.7750), f32(2.0315)
+    for _ in range(5):
+        Xd = dev(X).view(torch.bfloat16)
+        A = torch.empty((m, m), dtype=torch.bfloat16, device=DEV)
+        C.check(C.lib().concord_gemm_bf16_fwd(C.ptr(Xd), n, C.ptr(Xd), n, None, C.ptr(A), m, m, m, n,
+                                              C.ptr(ws), ws.numel(), st), "X X^T")
+        AA = torch.empty((m, m), dtype=torch.bfloat16, device=DEV)
+        C.check(C.lib().concord_gemm_bf16_dgrad(C.ptr(A), m, C.ptr(A), m, C.ptr(AA), m, m, m, m,
+                                                C.ptr(ws), ws.numel(), st), "A A")
+        sync()
+        Af = oracle.bf16_bits_to_f32(host(A).view(np.uint16))
+        AAf = oracle.bf16_bits_to_f32(host(AA).view(np.uint16))
+        B = bf((b * Af + c * AAf).astype(np.float32))
+        Bd = dev(B).view(torch.bfloat16)
+        BX = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+        C.check(C.lib().concord_gemm_bf16_dgrad(C.ptr(Bd), m, C.ptr(Xd), n, C.ptr(BX), n, m, m, n,
+                                                C.ptr(ws), ws.numel(), st), "B X")
+        sync()
+        BXf = oracle.bf16_bits_to_f32(host(BX).view(np.uint16))
+        X = bf((a * oracle.bf16_bits_to_f32(X) + BXf).astype(np.float32))
+    out = bf((f32(gamma) * oracle.bf16_bits_to_f32(X)).astype(np.float32))
+    if N > K:
+        out = np.ascontiguousarray(out.T)
+    np.testing.assert_array_equal(host(o).view(np.uint16), out)
+
+
 @pytest.mark.parametrize("N,K", [(2048, 5120), (1280, 5120), (333, 1001)])
 def test_muon_frobenius_denominator_bit_exact(oracle, N, K):
     """The NS5 input scale ||g|| + 1e-7 (block partials, then one wave chaining
@@ -876,6 +925,39 @@ def test_layer_muon_drive_bit_exact(oracle):
 def _layer_state(layer):
     return [host(t) for t in (layer.packed_w, layer.row_exp, layer.col_exp, layer.v_row, layer.v_col,
                               layer._sum_v_inv, layer._row_max_buf, layer._col_max_buf, layer._reb_seed)]
+
+
+def test_steps_reuse_buffers():
+    """Steady-state steps allocate no new layer state: the packed words,
+    exponents, v-hat state, watermark buffers and the per-device workspaces
+    keep their storage from the second step on (the reference checks the
+    same for its watermark buffers, notebook/src/test_prealloc_buffers.py:107-120)."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    torch.manual_seed(21)
+    layer = ca.ConcordLinearPackedB(256, 384, bias=True, device=DEV, lr=1e-3)
+    x = torch.randn(512, 256, device=DEV)
+    gy = torch.randn(512, 384, device=DEV) * 1e-2
+
+    def step():
+        layer(x.clone().requires_grad_(True)).backward(gy)
+        layer.rebalance()
+
+    def ptrs():
+        names = ("packed_w", "row_exp", "col_exp", "v_row", "v_col", "_sum_v_inv", "_row_max_buf",
+                 "_col_max_buf")
+        out = {n: getattr(layer, n).data_ptr() for n in names}
+        key = pb._dev_key(torch.device(DEV))
+        out["ws"] = pb._WORKSPACES[key].data_ptr()
+        out["gemm_ws"] = pb._GEMM_WORKSPACES[key].data_ptr()
+        return out
+
+    step()
+    first = ptrs()
+    for _ in range(3):
+        step()
+    sync()
+    assert ptrs() == first
 
 
 def test_graph_replay_matches_eager_steps():
