@@ -90,11 +90,14 @@ __global__ __launch_bounds__(256) void noise_apply_kernel(uint16_t* __restrict__
 __global__ __launch_bounds__(256) void token_scale_kernel(const uint16_t* __restrict__ dy, int64_t ld, int64_t M,
                                                           int64_t N, const int32_t* salt,
                                                           uint16_t* __restrict__ out) {
-  const int64_t m = blockIdx.y;
   const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (n >= N) return;
-  const float e = normal_draw(*salt, (uint32_t)m, kNoiseTagToken);
-  out[m * N + n] = (uint16_t)(pack_bf16x2(__fmul_rn(e, bf16_to_f32(dy[m * ld + n])), 0.0f) & 0xFFFFu);
+  const int32_t seed = *salt;
+  // rows strided by the grid's y extent (capped at the y-dimension limit)
+  for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
+    const float e = normal_draw(seed, (uint32_t)m, kNoiseTagToken);
+    out[m * N + n] = (uint16_t)(pack_bf16x2(__fmul_rn(e, bf16_to_f32(dy[m * ld + n])), 0.0f) & 0xFFFFu);
+  }
 }
 
 // sum of eps_0 .. eps_{M-1} in kNoiseBlock blocks (lane chains, halving tree);
@@ -231,8 +234,8 @@ extern "C" int concord_sigmag_noise(uint16_t* grad_w, int64_t ld_g, const uint16
   hipStream_t st = (hipStream_t)stream;
   const int64_t tb = M > 0 ? cdiv(M, kNoiseBlock) : 0;
   if (M > 0) {
-    hipLaunchKernelGGL(token_scale_kernel, dim3((unsigned)cdiv(N, 256), (unsigned)M), dim3(256), 0, st, dy,
-                       ld_dy, M, N, salt_counter, dyt);
+    hipLaunchKernelGGL(token_scale_kernel, dim3((unsigned)cdiv(N, 256), (unsigned)std::min<int64_t>(M, 65535)),
+                       dim3(256), 0, st, dy, ld_dy, M, N, salt_counter, dyt);
     hipLaunchKernelGGL(token_sum_partials_kernel, dim3((unsigned)tb), dim3(256), 0, st, M, salt_counter, tpart);
   }
   hipLaunchKernelGGL(token_sum_final_kernel, dim3(1), dim3(64), 0, st, tpart, tb, ssum);
