@@ -171,6 +171,97 @@ def _graph_ms(step, warmup, steps, torch, per_graph=1):
     return e0.elapsed_time(e1) / (reps * per_graph)
 
 
+# sum of (rows + columns) over config 4's 754 SDXL Linear and 1x1 weights: the
+# watermark slab a GatedRebalance over the whole UNet reduces
+CONFIG4_WATERMARKS = 2729216
+
+
+def _next_rows(layer, xb, dy, gw, reps, warmup, steps, torch, ca, pb):
+    """Context timings of the rows beside the step, on the same layer state:
+    gradient noise (isotropic and Sigma_g), the prototype accumulate update
+    (consf = 0), the coherence meter and the multi-layer watermark peak of the
+    gated rebalance, and one training step of a 3 x 3 Concord conv."""
+    from concord_amd import _lib as C
+    dev = xb.device
+    params = N_OUT * K_IN
+
+    def hbm(t_ms, nbytes, kernel):
+        a = nbytes / (t_ms * 1e-3) / 1e9
+        return {"kernel": kernel, "us": round(t_ms * 1e3, 2), "achieved": round(a, 1), "unit": "GB/s",
+                "frac": round(a / PEAK_HBM_GBPS, 4), "bytes_per_call": int(nbytes)}
+
+    def mfma(t_ms, flop, kernel):
+        a = flop / (t_ms * 1e-3) / 1e12
+        return {"kernel": kernel, "us": round(t_ms * 1e3, 2), "achieved": round(a, 1), "unit": "TFLOP/s",
+                "frac": round(a / PEAK_BF16_TFLOPS, 4), "flop_per_call": flop}
+
+    out = {}
+    sig = torch.full((1,), 0.6, dtype=torch.float32, device=dev)
+    salt = torch.full((1,), 7, dtype=torch.int32, device=dev)
+    g1 = gw.clone()
+    t = _event_time_ms(lambda: pb.iso_noise_(g1, sigma=sig, salt_counter=salt), reps, torch)
+    out["iso_noise"] = hbm(t, 6 * params, "noise_partials + noise_scale + noise_apply (6 B/param: the "
+                           "gradient read twice and written once; the draws are regenerated, not stored)")
+    g2 = gw.clone()
+    t = _event_time_ms(lambda: pb.sigmag_noise_(g2, dy, xb, sigma=sig, salt_counter=salt), reps, torch)
+    out["sigmag_noise"] = mfma(t, 2.0 * M_TOK * N_OUT * K_IN,
+                               "token_scale + token sum + WGRAD product (eps dy)^T x + sigmag partials / "
+                               "scale / apply (bound by the extra 2 M N K product)")
+    pk = layer.packed_w.clone()
+    pb.set_prototype_semantics(True)
+    pb.set_consolidate(dev, False)
+    try:
+        t = _event_time_ms(lambda: pb.apply_packed_adamw(
+            pk, gw, None, layer.row_exp, layer.col_exp, layer._row_max_buf, layer._col_max_buf,
+            lr=layer._lr_buf, eps=layer._eps_buf, gf_consol=50.0, v_scale=0.0, mass_preserve=True,
+            v_row=layer.v_row, v_col=layer.v_col, sum_v_inv=layer._sum_v_inv, gf_trust_delta_sq=1.0,
+            coh_pre=None, salt_prebumped=True), reps, torch)
+    finally:
+        pb.set_consolidate(dev, True)
+        pb.set_prototype_semantics(False)
+    out["proto_consf_update"] = hbm(t, UPDATE_BYTES_PER_PARAM * params,
+                                    "apply_adamw_kernel (prototype semantics, accumulate step consf = 0)")
+    cs = torch.empty(1, dtype=torch.float32, device=dev)
+    ws = pb._stats_workspace(dev, CONFIG4_WATERMARKS, params)
+    p = layer.packed_w
+    # the stream is read at call time: the timer captures on its own stream
+    t = _event_time_ms(lambda: C.check(C.lib().concord_coherence_sum(
+        C.ptr(p), p.stride(0), N_OUT, K_IN, float(layer.drift_cancel_C), C.ptr(cs), C.ptr(ws), ws.numel(),
+        C.stream_of(dev)), "coherence_sum"), reps, torch)
+    out["coherence_meter"] = hbm(t, 4 * params, "coherence_partials + coherence_final (4 B/param)")
+    nr = CONFIG4_WATERMARKS // 2
+    nc = CONFIG4_WATERMARKS - nr
+    wm = torch.randint(0, 30000, (CONFIG4_WATERMARKS,), dtype=torch.int32, device=dev)
+    peak = torch.empty(1, dtype=torch.int32, device=dev)
+    t = _event_time_ms(lambda: C.check(C.lib().concord_watermark_peak(
+        C.ptr(wm), nr, C.ptr(wm[nr:]), nc, C.ptr(peak), C.ptr(ws), ws.numel(), C.stream_of(dev)),
+        "watermark_peak"),
+        reps, torch)
+    out["watermark_peak"] = hbm(t, 4 * CONFIG4_WATERMARKS, "peak_partials + peak_final over config 4's "
+                                f"{CONFIG4_WATERMARKS} row and column watermarks (4 B each)")
+    # one training step of an SDXL 640-channel 3 x 3 conv at 64 x 64, batch 2:
+    # M = 8192 positions, K = 640 * 9, N = 640; patches by unfold, products on
+    # the packed GEMMs
+    conv = ca.ConcordConv2dPackedB(640, 640, 3, padding=1, bias=True, device=dev, lr=5e-4)
+    xc = torch.randn(2, 640, 64, 64, device=dev).to(torch.bfloat16).requires_grad_(True)
+    dyc = (torch.randn(2, 640, 64, 64, device=dev) * 1e-3).to(torch.bfloat16)
+
+    def cstep():
+        xc.grad = None
+        conv.bias.grad = None
+        conv(xc).backward(dyc)
+        conv.rebalance()
+
+    for _ in range(3):
+        cstep()
+    torch.cuda.synchronize()
+    t = _graph_ms(cstep, warmup, steps, torch)
+    out["conv2d_3x3_step"] = mfma(t, 6.0 * 8192 * 640 * 640 * 9,
+                                  "ConcordConv2dPackedB(640, 640, 3, padding 1) fwd + bwd + update + "
+                                  "rebalance on (2, 640, 64, 64); 6 M N K with M 8192, N 640, K 5760")
+    return out
+
+
 def _weight_cache_step_ms(layer, x, dy, warmup, steps, torch, ca, per_graph=1):
     """The same step on a weight_cache=True copy of the layer."""
     wl = ca.ConcordLinearPackedB(K_IN, N_OUT, bias=True, device=x.device, lr=5e-4, weight_cache=True)
@@ -365,6 +456,7 @@ def main():
     layer._row_max_buf.zero_()
     layer._col_max_buf.zero_()
     t_reb = _event_time_ms(layer.rebalance, reps, torch)
+    next_rows = _next_rows(layer, xb, dy, gw, reps, args.warmup, args.steps, torch, ca, pb)
 
     # the reference's own dataflow on the same workload, for context: the
     # update emits the bf16 weight (materialize-merge) and the next step's
@@ -456,6 +548,8 @@ def main():
         "materialize_GBps": round(DECODE_BYTES_PER_PARAM * params / (t_mat * 1e-3) / 1e9, 1),
         "muon_ns5": {"us": round(t_ns5 * 1e3, 1),
                      "tflops": round(ns5_flop / (t_ns5 * 1e-3) / 1e12, 1)},
+        "next_rows": dict(note="the rows beside the step, timed on the same state; context only",
+                          **next_rows),
         "weight_cache_mode": {
             "note": "the reference's dataflow (update emits the bf16 weight; forward and dgrad are bf16 "
                     "GEMMs on it), same workload; context only",

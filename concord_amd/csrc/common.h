@@ -257,6 +257,76 @@ CONCORD_DEV float lane_value(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
+// ((0 + v[0]) + v[stride]) + ... + v[(count - 1) stride], summed in that order
+// by one wave (every lane carries the same running sum).  The terms are
+// loaded 16 x 64 at a time, so a long chain pays one memory round trip per
+// 1024 terms rather than one per 64.
+CONCORD_DEV float wave_chain(const float* __restrict__ v, int64_t count, int64_t stride) {
+  constexpr int B = 16;
+  const int lane = threadIdx.x & 63;
+  float s = 0.0f;
+  for (int64_t c0 = 0; c0 < count; c0 += 64 * B) {
+    float a[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int64_t i = c0 + 64 * b + lane;
+      a[b] = i < count ? v[i * stride] : 0.0f;
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int64_t base = c0 + 64 * b;
+      if (base >= count) break;
+      const int cnt = (int)min((int64_t)64, count - base);
+      if (cnt == 64) {
+#pragma unroll
+        for (int j = 0; j < 64; ++j) s = __fadd_rn(s, lane_value(a[b], j));
+      } else {
+        for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, lane_value(a[b], j));
+      }
+    }
+  }
+  return s;
+}
+
+// Two chains at once over interleaved pairs (v[2i], v[2i + 1]), i ascending:
+// *s0 = ((0 + v[0]) + v[2]) + ..., *s1 = ((0 + v[1]) + v[3]) + ...  Each
+// chain keeps its own order; running both side by side halves the
+// dependent-add latency of two chains in turn.
+CONCORD_DEV void wave_chain2(const float* __restrict__ v, int64_t count, float* s0, float* s1) {
+  constexpr int B = 8;
+  const int lane = threadIdx.x & 63;
+  float x0 = 0.0f, x1 = 0.0f;
+  for (int64_t c0 = 0; c0 < count; c0 += 64 * B) {
+    float a[B], b[B];
+#pragma unroll
+    for (int q = 0; q < B; ++q) {
+      const int64_t i = c0 + 64 * q + lane;
+      a[q] = i < count ? v[2 * i] : 0.0f;
+      b[q] = i < count ? v[2 * i + 1] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < B; ++q) {
+      const int64_t base = c0 + 64 * q;
+      if (base >= count) break;
+      const int cnt = (int)min((int64_t)64, count - base);
+      if (cnt == 64) {
+#pragma unroll
+        for (int j = 0; j < 64; ++j) {
+          x0 = __fadd_rn(x0, lane_value(a[q], j));
+          x1 = __fadd_rn(x1, lane_value(b[q], j));
+        }
+      } else {
+        for (int j = 0; j < cnt; ++j) {
+          x0 = __fadd_rn(x0, lane_value(a[q], j));
+          x1 = __fadd_rn(x1, lane_value(b[q], j));
+        }
+      }
+    }
+  }
+  *s0 = x0;
+  *s1 = x1;
+}
+
 // max over the wave's 64 lanes, as a wave-uniform value.  DPP steps: prefix
 // maxima within each 16-lane row (row_shr 1, 2, 4, 8), then lane 15 of rows 0
 // and 2 into rows 1 and 3 (row_bcast:15) and lane 31 into rows 2 and 3

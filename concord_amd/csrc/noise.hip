@@ -3,12 +3,17 @@
 //   grad_W <- bf16(g + xi * (sigma * ||g|| / max(||xi||, 1e-12))),  xi ~ N(0, 1)
 // (notebook/src/prototype_packed_b.py:876-916 and the isotropic branch of
 // 1484-1501; sigma is a device scalar so a captured graph sees schedule
-// changes).  xi is normal_draw(salt, element index): counter-based, so the
-// three passes regenerate the same draws instead of storing them.
+// changes).  xi is normal_draw(salt, element index), counter-based: the
+// first pass draws it and keeps it (fp32, in the workspace) for the apply pass.
+//
+// Element e of an N x K gradient with row stride ld sits at (e / K) * ld + e % K;
+// with ld == K that is e itself (no division).
 #include "common.h"
 #include "gemm.h"
 
 namespace concord {
+
+CONCORD_DEV int64_t elem_off(int64_t e, int64_t K, int64_t ld) { return ld == K ? e : (e / K) * ld + e % K; }
 
 constexpr int kNoiseBlock = 8192;   // elements per partial
 
@@ -16,7 +21,7 @@ constexpr int kNoiseBlock = 8192;   // elements per partial
 // b0 + t + 256 i (i ascending), then a halving tree over the 256 lanes
 __global__ __launch_bounds__(256) void noise_partials_kernel(const uint16_t* __restrict__ g, int64_t ld,
                                                              int64_t N, int64_t K, const int32_t* salt,
-                                                             float* __restrict__ part) {
+                                                             float* __restrict__ part, float* __restrict__ xi) {
   __shared__ float sg[256], sx[256];
   const int64_t total = N * K;
   const int64_t b0 = (int64_t)blockIdx.x * kNoiseBlock;
@@ -25,8 +30,9 @@ __global__ __launch_bounds__(256) void noise_partials_kernel(const uint16_t* __r
   for (int i = 0; i < kNoiseBlock / 256; ++i) {
     const int64_t e = b0 + threadIdx.x + 256 * i;
     if (e < total) {
-      const float v = bf16_to_f32(g[(e / K) * ld + e % K]);
+      const float v = bf16_to_f32(g[elem_off(e, K, ld)]);
       const float z = normal_draw(seed, (uint32_t)e);
+      xi[e] = z;
       ag = __fadd_rn(ag, __fmul_rn(v, v));
       ax = __fadd_rn(ax, __fmul_rn(z, z));
     }
@@ -52,15 +58,8 @@ __global__ __launch_bounds__(256) void noise_partials_kernel(const uint16_t* __r
 __global__ __launch_bounds__(64) void noise_scale_kernel(const float* __restrict__ part, int64_t nb,
                                                          const float* sigma, float* scale) {
   const int lane = threadIdx.x;
-  float sg = 0.0f, sx = 0.0f;
-  for (int64_t c0 = 0; c0 < nb; c0 += 32) {
-    const float v = c0 + (lane >> 1) < nb ? part[2 * c0 + lane] : 0.0f;
-    const int cnt = (int)min((int64_t)32, nb - c0);
-    for (int j = 0; j < cnt; ++j) {
-      sg = __fadd_rn(sg, lane_value(v, 2 * j));
-      sx = __fadd_rn(sx, lane_value(v, 2 * j + 1));
-    }
-  }
+  float sg, sx;
+  wave_chain2(part, nb, &sg, &sx);
   if (lane == 0) {
     const float ng = sqrt_rn(sg);
     const float nx = fmaxf(sqrt_rn(sx), 1e-12f);
@@ -69,13 +68,13 @@ __global__ __launch_bounds__(64) void noise_scale_kernel(const float* __restrict
 }
 
 __global__ __launch_bounds__(256) void noise_apply_kernel(uint16_t* __restrict__ g, int64_t ld, int64_t N,
-                                                          int64_t K, const int32_t* salt, const float* scale) {
+                                                          int64_t K, const float* __restrict__ xi,
+                                                          const float* scale) {
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= N * K) return;
-  const int32_t seed = *salt;
   const float s = *scale;
-  uint16_t* p = g + (e / K) * ld + e % K;
-  const float v = __fadd_rn(bf16_to_f32(*p), __fmul_rn(normal_draw(seed, (uint32_t)e), s));
+  uint16_t* p = g + elem_off(e, K, ld);
+  const float v = __fadd_rn(bf16_to_f32(*p), __fmul_rn(xi[e], s));
   *p = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
 }
 
@@ -86,31 +85,50 @@ __global__ __launch_bounds__(256) void noise_apply_kernel(uint16_t* __restrict__
 // operands, fp32 accumulation); everything around it is elementwise or a
 // fixed-order reduction.
 
-// dyt[m][n] = bf16(eps_m * dy[m][n])
+// dyt[m][n] = bf16(eps_m * dy[m][n]), eps as drawn by token_sum_partials_kernel.
+// A thread takes 8 consecutive columns (16-byte accesses when the rows allow).
 __global__ __launch_bounds__(256) void token_scale_kernel(const uint16_t* __restrict__ dy, int64_t ld, int64_t M,
-                                                          int64_t N, const int32_t* salt,
+                                                          int64_t N, const float* __restrict__ eps,
                                                           uint16_t* __restrict__ out) {
-  const int64_t n = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (n >= N) return;
-  const int32_t seed = *salt;
+  const bool vec = n + 8 <= N && (ld % 8) == 0 && (N % 8) == 0 && ((uintptr_t)dy % 16) == 0 &&
+                   ((uintptr_t)out % 16) == 0;
   // rows strided by the grid's y extent (capped at the y-dimension limit)
   for (int64_t m = blockIdx.y; m < M; m += gridDim.y) {
-    const float e = normal_draw(seed, (uint32_t)m, kNoiseTagToken);
-    out[m * N + n] = (uint16_t)(pack_bf16x2(__fmul_rn(e, bf16_to_f32(dy[m * ld + n])), 0.0f) & 0xFFFFu);
+    const float e = eps[m];
+    if (vec) {
+      const uint4 d = *reinterpret_cast<const uint4*>(dy + m * ld + n);
+      const uint32_t dw[4] = {d.x, d.y, d.z, d.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        o[q] = pack_bf16x2(__fmul_rn(e, __uint_as_float(dw[q] << 16)),
+                           __fmul_rn(e, __uint_as_float(dw[q] & 0xFFFF0000u)));
+      *reinterpret_cast<uint4*>(out + m * N + n) = make_uint4(o[0], o[1], o[2], o[3]);
+    } else {
+      for (int64_t c = n; c < n + 8 && c < N; ++c)
+        out[m * N + c] = (uint16_t)(pack_bf16x2(__fmul_rn(e, bf16_to_f32(dy[m * ld + c])), 0.0f) & 0xFFFFu);
+    }
   }
 }
 
 // sum of eps_0 .. eps_{M-1} in kNoiseBlock blocks (lane chains, halving tree);
 // the block partials are chained by token_sum_final_kernel
 __global__ __launch_bounds__(256) void token_sum_partials_kernel(int64_t M, const int32_t* salt,
-                                                                 float* __restrict__ part) {
+                                                                 float* __restrict__ part,
+                                                                 float* __restrict__ eps) {
   __shared__ float s[256];
   const int64_t b0 = (int64_t)blockIdx.x * kNoiseBlock;
   const int32_t seed = *salt;
   float a = 0.0f;
   for (int i = 0; i < kNoiseBlock / 256; ++i) {
     const int64_t m = b0 + threadIdx.x + 256 * i;
-    if (m < M) a = __fadd_rn(a, normal_draw(seed, (uint32_t)m, kNoiseTagToken));
+    if (m < M) {
+      const float z = normal_draw(seed, (uint32_t)m, kNoiseTagToken);
+      eps[m] = z;   // each token's draw, once, for the scaling of dy
+      a = __fadd_rn(a, z);
+    }
   }
   s[threadIdx.x] = a;
   __syncthreads();
@@ -123,14 +141,8 @@ __global__ __launch_bounds__(256) void token_sum_partials_kernel(int64_t M, cons
 
 __global__ __launch_bounds__(64) void token_sum_final_kernel(const float* __restrict__ part, int64_t nb,
                                                              float* out) {
-  const int lane = threadIdx.x;
-  float s = 0.0f;
-  for (int64_t c0 = 0; c0 < nb; c0 += 64) {
-    const float v = c0 + lane < nb ? part[c0 + lane] : 0.0f;
-    const int cnt = (int)min((int64_t)64, nb - c0);
-    for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, lane_value(v, j));
-  }
-  if (lane == 0) *out = s;
+  const float s = wave_chain(part, nb, 1);
+  if (threadIdx.x == 0) *out = s;
 }
 
 // noise_e = f32(P_e) - S * (g_e / M)
@@ -150,7 +162,7 @@ __global__ __launch_bounds__(256) void sigmag_partials_kernel(const uint16_t* __
   for (int i = 0; i < kNoiseBlock / 256; ++i) {
     const int64_t e = b0 + threadIdx.x + 256 * i;
     if (e < total) {
-      const float v = bf16_to_f32(g[(e / K) * ld + e % K]);
+      const float v = bf16_to_f32(g[elem_off(e, K, ld)]);
       const float z = sigmag_noise(bf16_to_f32(P[e]), v, S, Mf);
       ag = __fadd_rn(ag, __fmul_rn(v, v));
       ax = __fadd_rn(ax, __fmul_rn(z, z));
@@ -178,14 +190,14 @@ __global__ __launch_bounds__(256) void sigmag_apply_kernel(uint16_t* __restrict_
   const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (e >= N * K) return;
   const float S = *Ssum, sc = *scale;
-  uint16_t* p = g + (e / K) * ld + e % K;
+  uint16_t* p = g + elem_off(e, K, ld);
   const float v = bf16_to_f32(*p);
   const float r = __fadd_rn(v, __fmul_rn(sigmag_noise(bf16_to_f32(P[e]), v, S, Mf), sc));
   *p = (uint16_t)(pack_bf16x2(r, 0.0f) & 0xFFFFu);
 }
 
 struct SigmagLayout {
-  size_t dyt, prod, part, tpart, ssum, scale, gemm, total;
+  size_t dyt, prod, part, tpart, ssum, scale, eps, gemm, total;
 };
 static SigmagLayout sigmag_layout(int64_t M, int64_t N, int64_t K) {
   auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
@@ -197,6 +209,7 @@ static SigmagLayout sigmag_layout(int64_t M, int64_t N, int64_t K) {
   L.tpart = o; o += r256((size_t)cdiv(M, kNoiseBlock) * 4);
   L.ssum = o; o += 256;
   L.scale = o; o += 256;
+  L.eps = o; o += r256((size_t)M * 4);
   L.gemm = o; o += r256(gemm_splitk_need(MODE_WGRAD, N, K, M));
   L.total = o;
   return L;
@@ -231,12 +244,14 @@ extern "C" int concord_sigmag_noise(uint16_t* grad_w, int64_t ld_g, const uint16
   float* tpart = (float*)(w + L.tpart);
   float* ssum = (float*)(w + L.ssum);
   float* scale = (float*)(w + L.scale);
+  float* eps = (float*)(w + L.eps);
   hipStream_t st = (hipStream_t)stream;
   const int64_t tb = M > 0 ? cdiv(M, kNoiseBlock) : 0;
   if (M > 0) {
-    hipLaunchKernelGGL(token_scale_kernel, dim3((unsigned)cdiv(N, 256), (unsigned)std::min<int64_t>(M, 65535)),
-                       dim3(256), 0, st, dy, ld_dy, M, N, salt_counter, dyt);
-    hipLaunchKernelGGL(token_sum_partials_kernel, dim3((unsigned)tb), dim3(256), 0, st, M, salt_counter, tpart);
+    hipLaunchKernelGGL(token_sum_partials_kernel, dim3((unsigned)tb), dim3(256), 0, st, M, salt_counter, tpart,
+                       eps);
+    hipLaunchKernelGGL(token_scale_kernel, dim3((unsigned)cdiv(N, 2048), (unsigned)std::min<int64_t>(M, 65535)),
+                       dim3(256), 0, st, dy, ld_dy, M, N, eps, dyt);
   }
   hipLaunchKernelGGL(token_sum_final_kernel, dim3(1), dim3(64), 0, st, tpart, tb, ssum);
   // P = dyt^T x (the WGRAD product of the scaled dy), bf16
@@ -253,10 +268,47 @@ extern "C" int concord_sigmag_noise(uint16_t* grad_w, int64_t ld_g, const uint16
   return launch_status("sigmag_noise");
 }
 
-extern "C" size_t concord_noise_workspace_bytes(int64_t N, int64_t K) {
-  const int64_t nb = N * K > 0 ? cdiv(N * K, kNoiseBlock) : 0;
-  return (size_t)((2 * nb * 4 + 255) / 256 * 256 + 256);
+namespace concord {
+
+// isotropic workspace: the block partials, the scale (256 bytes), then the
+// draws xi (fp32, one per element)
+struct IsoLayout {
+  size_t part, scale, xi, total;
+};
+static IsoLayout iso_layout(int64_t N, int64_t K) {
+  auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
+  const int64_t nk = N * K > 0 ? N * K : 0;
+  IsoLayout L;
+  L.part = 0;
+  L.scale = r256((size_t)2 * cdiv(nk, kNoiseBlock) * 4);
+  L.xi = L.scale + 256;
+  L.total = L.xi + r256((size_t)nk * 4);
+  return L;
 }
+
+}  // namespace concord
+
+extern "C" size_t concord_noise_workspace_bytes(int64_t N, int64_t K) { return iso_layout(N, K).total; }
+
+namespace concord {
+namespace {
+int iso_noise_launch(uint16_t* grad_w, int64_t ld_g, int64_t N, int64_t K, const float* sigma,
+                     const int32_t* salt_counter, void* workspace, hipStream_t st) {
+  const IsoLayout L = iso_layout(N, K);
+  const int64_t nb = cdiv(N * K, kNoiseBlock);
+  char* w = (char*)workspace;
+  float* part = (float*)(w + L.part);
+  float* scale = (float*)(w + L.scale);
+  float* xi = (float*)(w + L.xi);
+  hipLaunchKernelGGL(noise_partials_kernel, dim3((unsigned)nb), dim3(256), 0, st, grad_w, ld_g, N, K,
+                     salt_counter, part, xi);
+  hipLaunchKernelGGL(noise_scale_kernel, dim3(1), dim3(64), 0, st, part, nb, sigma, scale);
+  hipLaunchKernelGGL(noise_apply_kernel, dim3((unsigned)cdiv(N * K, 256)), dim3(256), 0, st, grad_w, ld_g, N,
+                     K, xi, scale);
+  return launch_status("iso_noise");
+}
+}  // namespace
+}  // namespace concord
 
 extern "C" int concord_iso_noise(uint16_t* grad_w, int64_t ld_g, int64_t N, int64_t K, const float* sigma,
                                  const int32_t* salt_counter, void* workspace, size_t workspace_bytes,
@@ -269,14 +321,5 @@ extern "C" int concord_iso_noise(uint16_t* grad_w, int64_t ld_g, int64_t N, int6
     set_error("concord_iso_noise: workspace of %zu bytes needed", concord_noise_workspace_bytes(N, K));
     return CONCORD_EWORKSPACE;
   }
-  const int64_t nb = cdiv(N * K, kNoiseBlock);
-  float* part = (float*)workspace;
-  float* scale = (float*)((char*)workspace + concord_noise_workspace_bytes(N, K) - 256);
-  hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(noise_partials_kernel, dim3((unsigned)nb), dim3(256), 0, st, grad_w, ld_g, N, K,
-                     salt_counter, part);
-  hipLaunchKernelGGL(noise_scale_kernel, dim3(1), dim3(64), 0, st, part, nb, sigma, scale);
-  hipLaunchKernelGGL(noise_apply_kernel, dim3((unsigned)cdiv(N * K, 256)), dim3(256), 0, st, grad_w, ld_g, N,
-                     K, salt_counter, scale);
-  return launch_status("iso_noise");
+  return iso_noise_launch(grad_w, ld_g, N, K, sigma, salt_counter, workspace, (hipStream_t)stream);
 }

@@ -60,12 +60,17 @@ __global__ __launch_bounds__(256) void coherence_partials_kernel(const int32_t* 
   __shared__ float s[256];
   const int64_t total = N * K;
   const int64_t b0 = (int64_t)blockIdx.x * kCohBlock;
-  float acc = 0.0f;
-#pragma unroll 8
+  // the block's 32 words per lane loaded first, then chained in order
+  int32_t w[kCohBlock / 256];
+#pragma unroll
   for (int i = 0; i < kCohBlock / 256; ++i) {
     const int64_t e = b0 + threadIdx.x + 256 * i;
-    if (e < total) acc = __fadd_rn(acc, word_coherence(ld == K ? p[e] : p[(e / K) * ld + e % K], C));
+    w[i] = e < total ? (ld == K ? p[e] : p[(e / K) * ld + e % K]) : 0;
   }
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kCohBlock / 256; ++i)
+    if (b0 + threadIdx.x + 256 * i < total) acc = __fadd_rn(acc, word_coherence(w[i], C));
   s[threadIdx.x] = acc;
   __syncthreads();
   for (int h = 128; h >= 1; h >>= 1) {
@@ -78,14 +83,8 @@ __global__ __launch_bounds__(256) void coherence_partials_kernel(const int32_t* 
 // the block partials chained in ascending order (one wave, lane reads)
 __global__ __launch_bounds__(64) void coherence_final_kernel(const float* __restrict__ part, int64_t nb,
                                                              float* out) {
-  const int lane = threadIdx.x;
-  float s = 0.0f;
-  for (int64_t c0 = 0; c0 < nb; c0 += 64) {
-    const float v = c0 + lane < nb ? part[c0 + lane] : 0.0f;
-    const int cnt = (int)min((int64_t)64, nb - c0);
-    for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, lane_value(v, j));
-  }
-  if (lane == 0) *out = s;
+  const float s = wave_chain(part, nb, 1);
+  if (threadIdx.x == 0) *out = s;
 }
 
 }  // namespace concord

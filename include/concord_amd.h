@@ -276,9 +276,11 @@ int concord_coherence_sum(const int32_t* packed, int64_t ld_p, int64_t N, int64_
  * 1484-1501): g <- bf16(g + xi * (sigma * ||g|| / max(||xi||, 1e-12))), sigma
  * read from device memory.  xi_e is a standard normal from a counter-based
  * stream (Philox4x32-10 block e keyed by the salt counter's current value,
- * Box-Muller with fixed-order log2 / sqrt / cos), so no draw is stored and
- * the result is reproducible.  The salt counter is read, not advanced.
- * workspace: concord_noise_workspace_bytes(N, K) bytes, no zeroing needed. */
+ * Box-Muller with fixed-order log2 / sqrt / cos), so the result is
+ * reproducible.  The salt counter is read, not advanced.
+ * workspace: concord_noise_workspace_bytes(N, K) bytes (block partials, and
+ * the draws, 4 B per element, kept between the norm and apply passes); no
+ * zeroing needed. */
 size_t concord_noise_workspace_bytes(int64_t N, int64_t K);
 int concord_iso_noise(uint16_t* grad_w, int64_t ld_g, int64_t N, int64_t K, const float* sigma,
                       const int32_t* salt_counter, void* workspace, size_t workspace_bytes, void* stream);
