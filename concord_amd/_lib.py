@@ -79,6 +79,9 @@ _SIGS = {
     "concord_stats_workspace_bytes": (_Z, [_I, _I]),
     "concord_noise_workspace_bytes": (_Z, [_I, _I]),
     "concord_iso_noise": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _P, _Z, _P]),
+    "concord_conv_im2col": (ctypes.c_int, [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "concord_conv_col2im": (ctypes.c_int, [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "concord_conv_col2im_fits": (ctypes.c_int, [_I, _I, _I, _I]),
     "concord_sigmag_noise_workspace_bytes": (_Z, [_I, _I, _I]),
     "concord_sigmag_noise": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _Z, _P]),
     "concord_watermark_peak": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _Z, _P]),

@@ -1,0 +1,297 @@
+// conv.hip -- the patch matrix of ConcordConv2dPackedB (concord/packed_b.py:
+// 2028-2065, a Conv2d over the packed (out, in * kh * kw) state).
+//
+// cols[m][k] = x[b][c][ho * sh - ph + i][wo * sw - pw + j] (0 outside the
+// image), m = (b * Ho + ho) * Wo + wo, k = (c * kh + i) * kw + j: the rows are
+// the output positions and the columns nn.Conv2d's (c, i, j) weight
+// flattening, so the layer's forward, dgrad and wgrad are the packed linear
+// products on cols.  This replaces torch's unfold followed by a transpose
+// copy (two passes over the patch matrix) with one.
+#include "common.h"
+
+namespace concord {
+
+struct ConvGeom {
+  int64_t B, C, H, W, kh, kw, sh, sw, ph, pw, Ho, Wo, K;
+};
+
+// A block fills a 64-row x 64-column tile of cols.  Loads: wave w takes
+// columns w, w + 4, ..., each lane one row (output position), so a wave reads
+// 64 consecutive positions of one input row -- contiguous along w for stride
+// 1 -- into LDS.  Stores: a thread writes 8 consecutive columns of one row
+// (16 bytes when K % 8 == 0).
+constexpr int kTileM = 64, kTileK = 64, kTileLd = kTileK + 2;
+
+__global__ __launch_bounds__(256) void im2col_kernel(const uint16_t* __restrict__ x, ConvGeom g,
+                                                     uint16_t* __restrict__ cols) {
+  __shared__ uint16_t tile[kTileM * kTileLd];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t M = g.B * g.Ho * g.Wo;
+  const int64_t m0 = (int64_t)blockIdx.x * kTileM, k0 = (int64_t)blockIdx.y * kTileK;
+  const int64_t m = m0 + lane;
+  const int64_t wo = m % g.Wo, r = m / g.Wo;
+  const int64_t ho = r % g.Ho, b = r / g.Ho;
+  const bool mok = m < M;
+  const uint16_t* xb = x + (mok ? b : 0) * g.C * g.H * g.W;
+  // this lane's window origin; (c, i, j) of the wave's first column, then
+  // stepped by 4 columns per iteration (wave-uniform, 32-bit)
+  const int hb = (int)(ho * g.sh - g.ph), wb = (int)(wo * g.sw - g.pw);
+  const int H = (int)g.H, W = (int)g.W, kh = (int)g.kh, kw = (int)g.kw;
+  const int64_t kfirst = k0 + wave;
+  int c = (int)(kfirst / (g.kh * g.kw));
+  int ij = (int)(kfirst % (g.kh * g.kw));
+  int i = ij / kw, j = ij - i * kw;
+  // the wave's 16 columns are loaded before any is stored
+  uint16_t v[kTileK / 4];
+#pragma unroll
+  for (int n = 0; n < kTileK / 4; ++n) {
+    const int q = wave + 4 * n;
+    v[n] = 0;
+    if (k0 + q < g.K && mok) {
+      const int h = hb + i, w = wb + j;
+      if (h >= 0 && h < H && w >= 0 && w < W) v[n] = xb[((int64_t)c * H + h) * W + w];
+    }
+    j += 4;
+    while (j >= kw) {
+      j -= kw;
+      if (++i == kh) {
+        i = 0;
+        ++c;
+      }
+    }
+  }
+#pragma unroll
+  for (int n = 0; n < kTileK / 4; ++n) tile[lane * kTileLd + wave + 4 * n] = v[n];
+  __syncthreads();
+  const bool vec = (g.K % 8) == 0 && ((uintptr_t)cols % 16) == 0;
+  for (int q = threadIdx.x; q < kTileM * (kTileK / 8); q += 256) {
+    const int ml = q / (kTileK / 8), kg = (q % (kTileK / 8)) * 8;
+    const int64_t mm = m0 + ml, kc = k0 + kg;
+    if (mm >= M || kc >= g.K) continue;
+    const uint16_t* src = tile + ml * kTileLd + kg;
+    uint16_t* dst = cols + mm * g.K + kc;
+    if (vec) {
+      *reinterpret_cast<uint4*>(dst) =
+          make_uint4(src[0] | ((uint32_t)src[1] << 16), src[2] | ((uint32_t)src[3] << 16),
+                     src[4] | ((uint32_t)src[5] << 16), src[6] | ((uint32_t)src[7] << 16));
+    } else {
+      for (int e = 0; e < 8 && kc + e < g.K; ++e) dst[e] = src[e];
+    }
+  }
+}
+
+// ---- col2im: the adjoint of im2col, a fixed-order gather -------------------
+// dx[b][c][h][w] = bf16(sum over i ascending, then j ascending, of
+// dcols[(b * Ho + ho) * Wo + wo][(c * kh + i) * kw + j]) over the (i, j) with
+// ho * sh = h + ph - i and wo * sw = w + pw - j exactly, 0 <= ho < Ho,
+// 0 <= wo < Wo; fp32 accumulation.
+// A block owns 4 rows x 64 columns of the image for `cc` channels.  It stages
+// the dcols segments those outputs read -- rows (ho, wo) of its window, the
+// cc * kh * kw contiguous columns of its channels -- in LDS (each (ho, wo)
+// segment padded to an odd number of dwords), then a lane per column w sums
+// and writes rows of dx along w.
+constexpr int kC2iH = 4, kC2iW = 64;
+
+struct Col2imTile {
+  int nho, nwo, cc, seg, ld;   // staged rows / columns, channels per block, segment, padded segment
+};
+
+__device__ __forceinline__ int64_t ceil_div_nn(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+__global__ __launch_bounds__(256) void col2im_kernel(const uint16_t* __restrict__ dcols, ConvGeom g, Col2imTile T,
+                                                     uint16_t* __restrict__ dx) {
+  extern __shared__ uint16_t stage[];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t hblocks = (g.H + kC2iH - 1) / kC2iH;
+  const int64_t w0 = (int64_t)blockIdx.x * kC2iW;
+  const int64_t b = blockIdx.y / hblocks, h0 = (blockIdx.y % hblocks) * kC2iH;
+  const int64_t c0 = (int64_t)blockIdx.z * T.cc;
+  const int ncl = (int)min((int64_t)T.cc, g.C - c0);
+  const int kk = (int)(g.kh * g.kw);
+  const int64_t ho_lo = ceil_div_nn(max(h0 + g.ph - (g.kh - 1), (int64_t)0), g.sh);
+  const int64_t wo_lo = ceil_div_nn(max(w0 + g.pw - (g.kw - 1), (int64_t)0), g.sw);
+  const int seg = ncl * kk;
+  const int npairs = T.nho * T.nwo;
+  // 8-byte staging when every segment starts 8-byte aligned in dcols and in
+  // LDS: lane l of a wave moves chunk l % cpp of row p0 + l / cpp
+  const int cpp = seg / 4;
+  const bool vec8 = (seg % 4) == 0 && (g.K % 4) == 0 && ((c0 * kk) % 4) == 0 && (T.ld % 4) == 0 &&
+                    ((uintptr_t)dcols % 8) == 0 && cpp > 0 && cpp <= 64;
+  if (vec8) {
+    const int per = 64 / cpp;            // rows per wave instruction
+    const int pl = lane / cpp, ch = lane - pl * cpp;
+    constexpr int U8 = 4;
+    for (int p0 = wave * per; p0 < npairs; p0 += 4 * per * U8) {
+      uint2 v[U8];
+#pragma unroll
+      for (int u = 0; u < U8; ++u) {
+        const int p = p0 + 4 * per * u + pl;
+        const int rl = p / T.nwo, cl = p - rl * T.nwo;
+        const int64_t ho = ho_lo + rl, wo = wo_lo + cl;
+        const bool ok = pl < per && p < npairs && ho < g.Ho && wo < g.Wo;
+        v[u] = ok ? *reinterpret_cast<const uint2*>(dcols + ((b * g.Ho + ho) * g.Wo + wo) * g.K + c0 * kk + 4 * ch)
+                  : make_uint2(0, 0);
+      }
+#pragma unroll
+      for (int u = 0; u < U8; ++u) {
+        const int p = p0 + 4 * per * u + pl;
+        if (pl < per && p < npairs) *reinterpret_cast<uint2*>(stage + p * T.ld + 4 * ch) = v[u];
+      }
+    }
+  }
+  // otherwise a wave per (ho, wo) row, the lanes along its segment (at most 3
+  // elements per lane); 8 rows' loads are issued before any is written
+  constexpr int U = 8;
+  for (int p0 = wave; !vec8 && p0 < npairs; p0 += 4 * U) {
+    uint16_t v[U][3];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int p = p0 + 4 * u;
+      const int rl = p / T.nwo, cl = p - rl * T.nwo;
+      const int64_t ho = ho_lo + rl, wo = wo_lo + cl;
+      const bool ok = p < npairs && ho < g.Ho && wo < g.Wo;
+      const uint16_t* src = dcols + (ok ? ((b * g.Ho + ho) * g.Wo + wo) * g.K + c0 * kk : 0);
+#pragma unroll
+      for (int r = 0; r < 3; ++r) {
+        const int e = lane + 64 * r;
+        v[u][r] = ok && e < seg ? src[e] : (uint16_t)0;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int p = p0 + 4 * u;
+      if (p >= npairs) break;
+#pragma unroll
+      for (int r = 0; r < 3; ++r) {
+        const int e = lane + 64 * r;
+        if (e < seg) stage[p * T.ld + e] = v[u][r];
+      }
+    }
+  }
+  __syncthreads();
+  // gather: 32-bit offsets relative to the staged window
+  const int w = (int)(w0 + lane);
+  const bool unit = g.sh == 1 && g.sw == 1;
+  const int kh = (int)g.kh, kw = (int)g.kw, sh = (int)g.sh, sw = (int)g.sw;
+  const int Ho = (int)g.Ho, Wo = (int)g.Wo, hol = (int)ho_lo, wol = (int)wo_lo;
+  const int ph = (int)g.ph, pw = (int)g.pw;
+  for (int q = wave; q < ncl * kC2iH; q += 4) {
+    const int cl = q / kC2iH;
+    const int h = (int)h0 + (q - cl * kC2iH);
+    if (h >= g.H || w >= g.W) continue;
+    const uint16_t* base = stage + cl * kk;
+    float acc = 0.0f;
+    if (unit) {
+      // the (i, j) with 0 <= h + ph - i < Ho and 0 <= w + pw - j < Wo, ascending
+      const int i1 = min(kh - 1, h + ph), i0 = max(0, h + ph - (Ho - 1));
+      const int j1 = min(kw - 1, w + pw), j0 = max(0, w + pw - (Wo - 1));
+      for (int i = i0; i <= i1; ++i) {
+        const uint16_t* row = base + (h + ph - i - hol) * T.nwo * T.ld + i * kw + (w + pw - wol) * T.ld;
+        for (int j = j0; j <= j1; ++j) acc = __fadd_rn(acc, bf16_to_f32(row[j - j * T.ld]));
+      }
+      dx[((b * g.C + c0 + cl) * g.H + h) * g.W + w] = (uint16_t)(pack_bf16x2(acc, 0.0f) & 0xFFFFu);
+      continue;
+    }
+    for (int i = 0; i < kh; ++i) {
+      const int hh = h + ph - i;
+      if (hh < 0) break;
+      if (!unit && hh % sh) continue;
+      const int ho = unit ? hh : hh / sh;
+      if (ho >= Ho) continue;
+      const uint16_t* row = base + (ho - hol) * T.nwo * T.ld + i * kw;
+      for (int j = 0; j < kw; ++j) {
+        const int ww = w + pw - j;
+        if (ww < 0) break;
+        if (!unit && ww % sw) continue;
+        const int wo = unit ? ww : ww / sw;
+        if (wo >= Wo) continue;
+        acc = __fadd_rn(acc, bf16_to_f32(row[(wo - wol) * T.ld + j]));
+      }
+    }
+    dx[((b * g.C + c0 + cl) * g.H + h) * g.W + w] = (uint16_t)(pack_bf16x2(acc, 0.0f) & 0xFFFFu);
+  }
+}
+
+constexpr size_t kCol2imLdsBudget = 64 * 1024;   // two blocks per CU
+
+// staged rows and columns a block needs at most, and the channels per block
+// that fit the LDS budget (cc = 0: the geometry does not fit)
+static Col2imTile col2im_tile(const ConvGeom& g) {
+  Col2imTile T;
+  T.nho = (int)((kC2iH - 1 + g.kh - 1) / g.sh + 1);
+  T.nwo = (int)((kC2iW - 1 + g.kw - 1) / g.sw + 1);
+  const int kk = (int)(g.kh * g.kw);
+  T.cc = 0;
+  for (int cc = 16; cc >= 1; cc /= 2) {
+    if (cc * kk > 3 * 64) continue;   // the staging moves at most 3 elements per lane per row
+    int ld = cc * kk;
+    // rows 8-byte aligned when the segment allows 8-byte staging, with a dword
+    // stride of 2 mod 4 (2-way LDS bank conflicts in the gather at most);
+    // otherwise an odd number of dwords per row
+    if (ld % 4 == 0) {
+      if ((ld / 2) % 4 != 2) ld += 4;
+    } else if ((ld & 1) == 0 && ((ld / 2) & 1) == 0) {
+      ld += 2;
+    }
+    if ((size_t)T.nho * T.nwo * ld * 2 <= kCol2imLdsBudget) {
+      T.cc = cc;
+      T.ld = ld;
+      break;
+    }
+  }
+  T.seg = T.cc * kk;
+  return T;
+}
+
+}  // namespace concord
+
+using namespace concord;
+
+extern "C" int concord_conv_im2col(const uint16_t* x, int64_t B, int64_t C, int64_t H, int64_t W, int64_t kh,
+                                   int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, uint16_t* cols,
+                                   void* stream) {
+  CONCORD_CHECK(B >= 0 && C > 0 && H > 0 && W > 0 && kh > 0 && kw > 0 && sh > 0 && sw > 0 && ph >= 0 &&
+                    pw >= 0,
+                "concord_conv_im2col: bad geometry");
+  CONCORD_CHECK(x && cols, "concord_conv_im2col: NULL argument");
+  ConvGeom g{B, C, H, W, kh, kw, sh, sw, ph, pw, (H + 2 * ph - kh) / sh + 1, (W + 2 * pw - kw) / sw + 1,
+             C * kh * kw};
+  CONCORD_CHECK(H + 2 * ph >= kh && W + 2 * pw >= kw, "concord_conv_im2col: kernel larger than the image");
+  CONCORD_CHECK(H + 2 * ph < ((int64_t)1 << 30) && W + 2 * pw < ((int64_t)1 << 30) && C * H * W < ((int64_t)1 << 40),
+                "concord_conv_im2col: image too large");
+  const int64_t M = B * g.Ho * g.Wo;
+  CONCORD_CHECK(cdiv(M, kTileM) < ((int64_t)1 << 31) && cdiv(g.K, kTileK) < 65536 && B * C * H * W < ((int64_t)1 << 40),
+                "concord_conv_im2col: size too large");
+  if (M == 0) return CONCORD_OK;
+  hipLaunchKernelGGL(im2col_kernel, dim3((unsigned)cdiv(M, kTileM), (unsigned)cdiv(g.K, kTileK)), dim3(256), 0,
+                     (hipStream_t)stream, x, g, cols);
+  return launch_status("conv_im2col");
+}
+
+extern "C" int concord_conv_col2im(const uint16_t* dcols, int64_t B, int64_t C, int64_t H, int64_t W, int64_t kh,
+                                   int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw, uint16_t* dx,
+                                   void* stream) {
+  CONCORD_CHECK(B >= 0 && C > 0 && H > 0 && W > 0 && kh > 0 && kw > 0 && sh > 0 && sw > 0 && ph >= 0 &&
+                    pw >= 0 && H + 2 * ph >= kh && W + 2 * pw >= kw,
+                "concord_conv_col2im: bad geometry");
+  CONCORD_CHECK(dcols && dx, "concord_conv_col2im: NULL argument");
+  CONCORD_CHECK(H + 2 * ph < ((int64_t)1 << 30) && W + 2 * pw < ((int64_t)1 << 30) && B * C * H * W < ((int64_t)1 << 40),
+                "concord_conv_col2im: image too large");
+  ConvGeom g{B, C, H, W, kh, kw, sh, sw, ph, pw, (H + 2 * ph - kh) / sh + 1, (W + 2 * pw - kw) / sw + 1,
+             C * kh * kw};
+  const Col2imTile T = col2im_tile(g);
+  CONCORD_CHECK(T.cc > 0, "concord_conv_col2im: kernel window too large for the staged tile");
+  if (B == 0) return CONCORD_OK;
+  const int64_t gy = B * ((H + kC2iH - 1) / kC2iH);
+  CONCORD_CHECK(gy < 65536 * 1024LL && cdiv(C, T.cc) < 65536, "concord_conv_col2im: grid too large");
+  const size_t lds = (size_t)T.nho * T.nwo * T.ld * 2;
+  hipLaunchKernelGGL(col2im_kernel, dim3((unsigned)cdiv(W, kC2iW), (unsigned)gy, (unsigned)cdiv(C, T.cc)),
+                     dim3(256), lds, (hipStream_t)stream, dcols, g, T, dx);
+  return launch_status("conv_col2im");
+}
+
+extern "C" int concord_conv_col2im_fits(int64_t kh, int64_t kw, int64_t sh, int64_t sw) {
+  ConvGeom g{};
+  g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw;
+  return kh > 0 && kw > 0 && sh > 0 && sw > 0 && col2im_tile(g).cc > 0;
+}

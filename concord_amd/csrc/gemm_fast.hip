@@ -1380,13 +1380,16 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
 }
 
 // ---- planning -----------------------------------------------------------------
-struct FastShape { int bi, bj, waves, minb; };
+// weight: measured time per FLOP relative to the 8-wave kernels; the 4-wave
+// 128 x 128 kernel ran at ~255 TFLOP/s against ~650 for the transpose-read
+// WGRAD on the same conv-shaped product (640 x 5760, reduction 8192)
+struct FastShape { int bi, bj, waves, minb; double weight; };
 
 // tile shapes per mode (index into the launch switch below); 8-wave tiles run
 // two waves per SIMD, 4-wave 128 x 128 tiles two blocks per CU
-constexpr FastShape kFwdShapes[] = {{256, 160, 8, 1}, {256, 128, 8, 1}, {128, 128, 4, 2}};
-constexpr FastShape kColShapes[] = {{256, 128, 8, 1}, {128, 128, 4, 2}};
-constexpr FastShape kWgrShapes[] = {{256, 128, 8, 1}, {128, 128, 4, 2}};
+constexpr FastShape kFwdShapes[] = {{256, 160, 8, 1, 1.0}, {256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0}};
+constexpr FastShape kColShapes[] = {{256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0}};
+constexpr FastShape kWgrShapes[] = {{256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0}};
 constexpr int kCUs = 256;
 
 struct FastPlan { int shape, splits, ti, tj; int64_t r_split; };
@@ -1402,14 +1405,16 @@ static FastPlan plan(const FastShape (&shapes)[NS], int64_t I, int64_t J, int64_
     const size_t slot = (size_t)ti * tj * shapes[s].bi * shapes[s].bj * sizeof(float);
     const int max_splits = (int)std::min<size_t>(kMaxSplits, std::max<size_t>(1, room / slot));
     for (int sp = 1; sp <= max_splits; ++sp) {
-      if (sp > 1 && (!gemm_splitk_fits(ti * tj) || ti * tj * (sp - 1) >= kCUs * shapes[s].minb)) break;
+      // split only a grid that leaves CUs idle (then up to kMaxSplits, the
+      // cost below deciding); a grid that fills the chip stays unsplit
+      if (sp > 1 && (!gemm_splitk_fits(ti * tj) || ti * tj >= kCUs * shapes[s].minb)) break;
       const int64_t rs = cdiv(cdiv(R, sp), TR) * TR;
       if (sp > 1 && (sp - 1) * rs >= R) break;
       const double slots = (double)kCUs * shapes[s].minb;
       const double waves = std::ceil((double)(ti * tj * sp) / slots);
       // a resident block's MFMA rate falls when two share a CU
       const double per_block = (double)shapes[s].bi * shapes[s].bj * (double)(rs + 2 * TR) * shapes[s].minb;
-      double cost = waves * per_block;
+      double cost = waves * per_block * shapes[s].weight;
       if (sp > 1) cost += (double)sp * I * J * 8.0 / kCUs;   // partial write + read, spread over CUs
       if (cost < best_cost * 0.999) {
         best_cost = cost;

@@ -1162,15 +1162,47 @@ def _pair(v):
     return (int(v), int(v)) if isinstance(v, int) else (int(v[0]), int(v[1]))
 
 
+class _Im2col(torch.autograd.Function):
+    """(B, C, H, W) bf16 -> the (B * Ho * Wo, C * kh * kw) patch matrix in one
+    HIP pass (concord_conv_im2col).  The adjoint gathers dx straight from the
+    patch gradient (concord_conv_col2im: fixed order, fp32 accumulation); a
+    window too large for its staged tile takes torch's fold instead."""
+
+    @staticmethod
+    def forward(ctx, x, kh, kw, sh, sw, ph, pw):
+        x = x.contiguous()
+        B, Cin, H, W = x.shape
+        Ho = (H + 2 * ph - kh) // sh + 1
+        Wo = (W + 2 * pw - kw) // sw + 1
+        cols = torch.empty((B * Ho * Wo, Cin * kh * kw), dtype=torch.bfloat16, device=x.device)
+        C.check(C.lib().concord_conv_im2col(C.ptr(x), B, Cin, H, W, kh, kw, sh, sw, ph, pw, C.ptr(cols),
+                                            C.stream_of(x.device)), "conv_im2col")
+        ctx.geom = (B, Cin, H, W, kh, kw, sh, sw, ph, pw, Ho * Wo)
+        return cols
+
+    @staticmethod
+    def backward(ctx, dcols):
+        B, Cin, H, W, kh, kw, sh, sw, ph, pw, L = ctx.geom
+        if dcols.dtype == torch.bfloat16 and C.lib().concord_conv_col2im_fits(kh, kw, sh, sw):
+            dcols = dcols.contiguous()
+            dx = torch.empty((B, Cin, H, W), dtype=torch.bfloat16, device=dcols.device)
+            C.check(C.lib().concord_conv_col2im(C.ptr(dcols), B, Cin, H, W, kh, kw, sh, sw, ph, pw, C.ptr(dx),
+                                                C.stream_of(dcols.device)), "conv_col2im")
+        else:
+            u = dcols.reshape(B, L, Cin * kh * kw).transpose(1, 2)
+            dx = F.fold(u, (H, W), (kh, kw), padding=(ph, pw), stride=(sh, sw))
+        return dx, None, None, None, None, None, None
+
+
 class ConcordConv2dPackedB(ConcordLinearPackedB):
     """Conv2d variant of ConcordLinearPackedB (concord/packed_b.py:2028-2065):
     the same packed int32 state, an (out_channels, in_channels * kh * kw)
     matrix in nn.Conv2d's (c, i, j) flattening.  Where the reference runs
     cuDNN on the cached bf16 weight, this layer runs the linear layer's own
     kernels on the patch matrix: the (B * Ho * Wo, in_channels * kh * kw)
-    patches are gathered with torch's unfold (a layout copy; for 1x1, stride
-    1, no padding a channels-last permute), and its autograd adjoint (fold)
-    scatters dx back.  Forward, dgrad, wgrad with v-hat and bias, and the
+    patches are gathered in one HIP pass (concord_conv_im2col; for 1x1,
+    stride 1, no padding a channels-last permute), and the adjoint gathers
+    dx back from the patch gradient in another (concord_conv_col2im).  Forward, dgrad, wgrad with v-hat and bias, and the
     packed update are the HIP entries of the linear path."""
 
     def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, bias=True,
@@ -1194,11 +1226,10 @@ class ConcordConv2dPackedB(ConcordLinearPackedB):
         Ho = (H + 2 * ph - self.kh) // sh + 1
         Wo = (W + 2 * pw - self.kw) // sw + 1
         if (self.kh, self.kw, sh, sw, ph, pw) == (1, 1, 1, 1, 0, 0):
-            cols = x.permute(0, 2, 3, 1).reshape(B * H * W, cin)
+            cols = x.permute(0, 2, 3, 1).reshape(B * H * W, cin).contiguous()
         else:
-            u = F.unfold(x, (self.kh, self.kw), padding=(ph, pw), stride=(sh, sw))
-            cols = u.transpose(1, 2).reshape(B * Ho * Wo, self.in_features)
-        return cols.contiguous(), Ho, Wo
+            cols = _Im2col.apply(x, self.kh, self.kw, sh, sw, ph, pw)
+        return cols, Ho, Wo
 
     def forward(self, x):
         if x.dim() != 4:

@@ -285,6 +285,28 @@ size_t concord_noise_workspace_bytes(int64_t N, int64_t K);
 int concord_iso_noise(uint16_t* grad_w, int64_t ld_g, int64_t N, int64_t K, const float* sigma,
                       const int32_t* salt_counter, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Patch matrix of the packed Conv2d (ConcordConv2dPackedB; reference class
+ * concord/packed_b.py:2028-2065, which runs the conv on its cached bf16
+ * weight): x is (B, C, H, W) bf16, contiguous; cols is
+ * (B * Ho * Wo, C * kh * kw) bf16 with
+ *   cols[(b * Ho + ho) * Wo + wo][(c * kh + i) * kw + j]
+ *     = x[b][c][ho * sh - ph + i][wo * sw - pw + j]   (0 outside the image),
+ * Ho = (H + 2 ph - kh) / sh + 1, Wo likewise: nn.Conv2d's (c, i, j) weight
+ * flattening, so the conv's products are the packed linear entries on cols. */
+int concord_conv_im2col(const uint16_t* x, int64_t B, int64_t C, int64_t H, int64_t W, int64_t kh, int64_t kw,
+                        int64_t sh, int64_t sw, int64_t ph, int64_t pw, uint16_t* cols, void* stream);
+/* Its adjoint, the input gradient of the conv from the patch gradient dcols
+ * (same layout as cols): dx[b][c][h][w] = bf16(sum over i ascending, then j
+ * ascending, of dcols[(b * Ho + ho) * Wo + wo][(c * kh + i) * kw + j]) over
+ * the (i, j) with ho * sh = h + ph - i, wo * sw = w + pw - j, 0 <= ho < Ho,
+ * 0 <= wo < Wo; fp32 accumulation.  Replaces the conv's input-gradient path
+ * of the reference's conv class (cuDNN there).  concord_conv_col2im_fits
+ * says whether the window fits the kernel's staged tile (non-zero) for the
+ * given kernel size and stride. */
+int concord_conv_col2im(const uint16_t* dcols, int64_t B, int64_t C, int64_t H, int64_t W, int64_t kh, int64_t kw,
+                        int64_t sh, int64_t sw, int64_t ph, int64_t pw, uint16_t* dx, void* stream);
+int concord_conv_col2im_fits(int64_t kh, int64_t kw, int64_t sh, int64_t sw);
+
 /* The Sigma_g-shaped draw, the reference's default when its noise is on
  * (notebook/src/prototype_packed_b.py:1489-1500): in place on the bf16
  * gradient g of dy[M,N]^T x[M,K],

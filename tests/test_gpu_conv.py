@@ -120,3 +120,54 @@ def test_conv_consolidated_export_shape():
     assert sd["c.weight"].shape == (24, 16, 3, 3)
     np.testing.assert_array_equal(host(sd["c.weight"].reshape(24, -1)), host(conv.consolidated_weight()))
     assert conv.weight.shape == (24, 16, 3, 3)
+
+
+@pytest.mark.parametrize("geom", [  # (B, C, H, W, kh, kw, sh, sw, ph, pw)
+    (2, 640, 64, 64, 3, 3, 1, 1, 1, 1),
+    (2, 13, 17, 15, 3, 3, 2, 2, 1, 1),     # K = 117: the scalar store path
+    (1, 8, 9, 11, 5, 3, 1, 2, 2, 0),       # non-square kernel, mixed stride and padding
+    (3, 16, 7, 7, 3, 3, 3, 3, 0, 0),
+])
+def test_im2col_matches_unfold(geom):
+    """The one-pass HIP patch matrix equals torch's unfold + transpose bit for
+    bit (a pure gather with zeros outside the image)."""
+    from concord_amd import _lib as C
+    B, Cin, H, W, kh, kw, sh, sw, ph, pw = geom
+    x = torch.randn(B, Cin, H, W, device=DEV).to(torch.bfloat16)
+    u = F.unfold(x, (kh, kw), padding=(ph, pw), stride=(sh, sw))
+    want = u.transpose(1, 2).reshape(-1, u.shape[1]).contiguous()
+    got = torch.empty_like(want)
+    C.check(C.lib().concord_conv_im2col(C.ptr(x), B, Cin, H, W, kh, kw, sh, sw, ph, pw, C.ptr(got),
+                                        C.stream_of(x.device)), "conv_im2col")
+    sync()
+    np.testing.assert_array_equal(host(got), host(want))
+
+
+@pytest.mark.parametrize("geom", [  # (B, C, H, W, kh, kw, sh, sw, ph, pw)
+    (2, 640, 64, 64, 3, 3, 1, 1, 1, 1),
+    (2, 13, 17, 15, 3, 3, 2, 2, 1, 1),
+    (1, 8, 9, 70, 5, 3, 1, 2, 2, 0),
+    (3, 16, 7, 7, 3, 3, 3, 3, 0, 0),
+    (1, 24, 5, 130, 3, 3, 1, 1, 1, 1),
+])
+def test_col2im_matches_fp32_fold(oracle, geom):
+    """The HIP adjoint of im2col against fold in float64 on the same bf16
+    patch gradient: each output is a sum of at most kh * kw terms in fp32
+    rounded once to bf16, so it is within half a bf16 ulp (2^-8 relative) of
+    the exact sum plus the fp32 accumulation error, which is below
+    2^-20 times the sum of the terms' magnitudes."""
+    from concord_amd import _lib as C
+    B, Cin, H, W, kh, kw, sh, sw, ph, pw = geom
+    assert C.lib().concord_conv_col2im_fits(kh, kw, sh, sw)
+    Ho, Wo = (H + 2 * ph - kh) // sh + 1, (W + 2 * pw - kw) // sw + 1
+    dcols = torch.randn(B * Ho * Wo, Cin * kh * kw, device=DEV).to(torch.bfloat16)
+    got = torch.empty((B, Cin, H, W), dtype=torch.bfloat16, device=DEV)
+    C.check(C.lib().concord_conv_col2im(C.ptr(dcols), B, Cin, H, W, kh, kw, sh, sw, ph, pw, C.ptr(got),
+                                        C.stream_of(got.device)), "conv_col2im")
+    sync()
+    u = dcols.double().cpu().reshape(B, Ho * Wo, -1).transpose(1, 2)
+    exact = F.fold(u, (H, W), (kh, kw), padding=(ph, pw), stride=(sh, sw)).numpy()
+    mag = F.fold(u.abs(), (H, W), (kh, kw), padding=(ph, pw), stride=(sh, sw)).numpy()
+    g = oracle.bf16_bits_to_f32(host(got)).astype(np.float64)
+    tol = 2.0 ** -8 * np.abs(exact) + 2.0 ** -20 * mag
+    assert np.all(np.abs(g - exact) <= tol), np.max(np.abs(g - exact) - tol)
