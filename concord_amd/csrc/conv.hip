@@ -5,8 +5,8 @@
 // image), m = (b * Ho + ho) * Wo + wo, k = (c * kh + i) * kw + j: the rows are
 // the output positions and the columns nn.Conv2d's (c, i, j) weight
 // flattening, so the layer's forward, dgrad and wgrad are the packed linear
-// products on cols.  This replaces torch's unfold followed by a transpose
-// copy (two passes over the patch matrix) with one.
+// products on cols.  im2col builds cols in one pass; col2im, its adjoint,
+// gathers dx from the patch gradient (see below).
 #include "common.h"
 
 namespace concord {
@@ -283,7 +283,8 @@ extern "C" int concord_conv_col2im(const uint16_t* dcols, int64_t B, int64_t C, 
   CONCORD_CHECK(T.cc > 0, "concord_conv_col2im: kernel window too large for the staged tile");
   if (B == 0) return CONCORD_OK;
   const int64_t gy = B * ((H + kC2iH - 1) / kC2iH);
-  CONCORD_CHECK(gy < 65536 * 1024LL && cdiv(C, T.cc) < 65536, "concord_conv_col2im: grid too large");
+  CONCORD_CHECK(gy < 65536 && cdiv(C, T.cc) < 65536 && cdiv(W, kC2iW) < ((int64_t)1 << 31),
+                "concord_conv_col2im: grid too large (batch x rows / 4 must stay below 65536)");
   const size_t lds = (size_t)T.nho * T.nwo * T.ld * 2;
   hipLaunchKernelGGL(col2im_kernel, dim3((unsigned)cdiv(W, kC2iW), (unsigned)gy, (unsigned)cdiv(C, T.cc)),
                      dim3(256), lds, (hipStream_t)stream, dcols, g, T, dx);
