@@ -329,6 +329,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--no-next-rows", action="store_true",
+                    help="skip the context timings of the rows beside the step (keeps a kernel profile to the "
+                         "step's own shapes)")
     ap.add_argument("--only", default=None,
                     choices=["fwd", "bwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
                              "copy"])
@@ -456,7 +459,8 @@ def main():
     layer._row_max_buf.zero_()
     layer._col_max_buf.zero_()
     t_reb = _event_time_ms(layer.rebalance, reps, torch)
-    next_rows = _next_rows(layer, xb, dy, gw, reps, args.warmup, args.steps, torch, ca, pb)
+    next_rows = {} if args.no_next_rows else _next_rows(layer, xb, dy, gw, reps, args.warmup, args.steps, torch,
+                                                           ca, pb)
 
     # the reference's own dataflow on the same workload, for context: the
     # update emits the bf16 weight (materialize-merge) and the next step's
