@@ -262,6 +262,42 @@ def _next_rows(layer, xb, dy, gw, reps, warmup, steps, torch, ca, pb):
     return out
 
 
+# config 3: SDXL-UNet linear shapes (out N, in K, tokens M) at their token
+# counts -- attention q/k/v/out, GEGLU in and out, the north-star shape, the
+# 640-channel set on 4096 x 2 tokens, cross-attention k/v on 77 x 2 tokens
+CONFIG3 = [(1280, 1280, 2048), (10240, 1280, 2048), (1280, 5120, 2048), (5120, 1280, 2048),
+           (640, 640, 8192), (5120, 640, 8192), (640, 2560, 8192), (1280, 2048, 154)]
+
+
+def _config3_steps(warmup, steps, torch, ca):
+    """The same training step (fwd, dgrad, wgrad with v-hat, update with the
+    winner flags, rebalance) on each config-3 shape; 6MNK FLOP per step."""
+    out = {}
+    dev = torch.device("cuda:0")
+    for N, K, M in CONFIG3:
+        torch.manual_seed(N + K + M)
+        ly = ca.ConcordLinearPackedB(K, N, bias=True, device=dev, lr=5e-4)
+        ly.disable_cohpre()
+        ly.gf_consol = 50.0
+        xs = torch.randn(M, K, device=dev).to(torch.bfloat16).requires_grad_(True)
+        dys = (torch.randn(M, N, device=dev) * 1e-3).to(torch.bfloat16)
+
+        def st():
+            xs.grad = None
+            ly.bias.grad = None
+            ly(xs).backward(dys)
+            ly.rebalance()
+
+        for _ in range(3):
+            st()
+        torch.cuda.synchronize()
+        t = _graph_ms(st, warmup, steps, torch)
+        a = 6.0 * M * N * K / (t * 1e-3) / 1e12
+        out[f"{K}to{N}_M{M}"] = {"ms_per_step": round(t, 4), "tflops": round(a, 1),
+                                 "frac": round(a / PEAK_BF16_TFLOPS, 4)}
+    return out
+
+
 def _weight_cache_step_ms(layer, x, dy, warmup, steps, torch, ca, per_graph=1):
     """The same step on a weight_cache=True copy of the layer."""
     wl = ca.ConcordLinearPackedB(K_IN, N_OUT, bias=True, device=x.device, lr=5e-4, weight_cache=True)
@@ -461,6 +497,7 @@ def main():
     t_reb = _event_time_ms(layer.rebalance, reps, torch)
     next_rows = {} if args.no_next_rows else _next_rows(layer, xb, dy, gw, reps, args.warmup, args.steps, torch,
                                                            ca, pb)
+    sdxl_shapes = {} if args.no_next_rows else _config3_steps(args.warmup, args.steps, torch, ca)
 
     # the reference's own dataflow on the same workload, for context: the
     # update emits the bf16 weight (materialize-merge) and the next step's
@@ -554,6 +591,8 @@ def main():
                      "tflops": round(ns5_flop / (t_ns5 * 1e-3) / 1e12, 1)},
         "next_rows": dict(note="the rows beside the step, timed on the same state; context only",
                           **next_rows),
+        "sdxl_shapes": dict(note="the same step on each config-3 SDXL linear shape (out N, in K, tokens M); "
+                                 "context only", **sdxl_shapes),
         "weight_cache_mode": {
             "note": "the reference's dataflow (update emits the bf16 weight; forward and dgrad are bf16 "
                     "GEMMs on it), same workload; context only",
