@@ -361,8 +361,10 @@ def _only(which, reps, layer, xb, dy, torch, pb):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # the untimed warmup runs the layer into its steady state: the first steps
+    # after init tick many exponents at once, and the clocks settle
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-next-rows", action="store_true",
