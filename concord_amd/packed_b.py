@@ -1194,15 +1194,41 @@ class _Im2col(torch.autograd.Function):
         return dx, None, None, None, None, None, None
 
 
+class _ToNCHW(torch.autograd.Function):
+    """(B * L, N) rows in (b, ho, wo) order -> (B, N, Ho, Wo), the 1 x 1 case
+    of concord_conv_col2im (a transpose through LDS); the adjoint is the 1 x 1
+    im2col."""
+
+    @staticmethod
+    def forward(ctx, y2, B, Ho, Wo):
+        y2 = y2.to(torch.bfloat16).contiguous()
+        N = y2.shape[1]
+        y = torch.empty((B, N, Ho, Wo), dtype=torch.bfloat16, device=y2.device)
+        C.check(C.lib().concord_conv_col2im(C.ptr(y2), B, N, Ho, Wo, 1, 1, 1, 1, 0, 0, C.ptr(y),
+                                            C.stream_of(y2.device)), "conv_col2im")
+        ctx.shape = (B, N, Ho, Wo)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        B, N, Ho, Wo = ctx.shape
+        dy = dy.to(torch.bfloat16).contiguous()
+        d2 = torch.empty((B * Ho * Wo, N), dtype=torch.bfloat16, device=dy.device)
+        C.check(C.lib().concord_conv_im2col(C.ptr(dy), B, N, Ho, Wo, 1, 1, 1, 1, 0, 0, C.ptr(d2),
+                                            C.stream_of(dy.device)), "conv_im2col")
+        return d2, None, None, None
+
+
 class ConcordConv2dPackedB(ConcordLinearPackedB):
     """Conv2d variant of ConcordLinearPackedB (concord/packed_b.py:2028-2065):
     the same packed int32 state, an (out_channels, in_channels * kh * kw)
     matrix in nn.Conv2d's (c, i, j) flattening.  Where the reference runs
     cuDNN on the cached bf16 weight, this layer runs the linear layer's own
     kernels on the patch matrix: the (B * Ho * Wo, in_channels * kh * kw)
-    patches are gathered in one HIP pass (concord_conv_im2col; for 1x1,
-    stride 1, no padding a channels-last permute), and the adjoint gathers
-    dx back from the patch gradient in another (concord_conv_col2im).  Forward, dgrad, wgrad with v-hat and bias, and the
+    patches are gathered in one HIP pass (concord_conv_im2col; for a 1x1
+    kernel a transpose to channels-last), the adjoint gathers dx back from the
+    patch gradient in another (concord_conv_col2im), and the (positions,
+    out_channels) product is transposed to NCHW by the 1x1 col2im.  Forward, dgrad, wgrad with v-hat and bias, and the
     packed update are the HIP entries of the linear path."""
 
     def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, bias=True,
@@ -1225,10 +1251,7 @@ class ConcordConv2dPackedB(ConcordLinearPackedB):
         (sh, sw), (ph, pw) = _pair(self.stride), _pair(self.padding)
         Ho = (H + 2 * ph - self.kh) // sh + 1
         Wo = (W + 2 * pw - self.kw) // sw + 1
-        if (self.kh, self.kw, sh, sw, ph, pw) == (1, 1, 1, 1, 0, 0):
-            cols = x.permute(0, 2, 3, 1).reshape(B * H * W, cin).contiguous()
-        else:
-            cols = _Im2col.apply(x, self.kh, self.kw, sh, sw, ph, pw)
+        cols = _Im2col.apply(x, self.kh, self.kw, sh, sw, ph, pw)
         return cols, Ho, Wo
 
     def forward(self, x):
@@ -1238,9 +1261,7 @@ class ConcordConv2dPackedB(ConcordLinearPackedB):
         if x.dtype != torch.bfloat16:
             x = x.to(torch.bfloat16)
         cols, Ho, Wo = self._patches(x)
-        y = super().forward(cols)
-        B = x.shape[0]
-        y = y.view(B, Ho * Wo, self.out_channels).permute(0, 2, 1).reshape(B, self.out_channels, Ho, Wo)
+        y = _ToNCHW.apply(super().forward(cols), x.shape[0], Ho, Wo)
         return y.to(in_dtype)
 
     @property
