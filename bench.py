@@ -201,7 +201,7 @@ def _next_rows(layer, xb, dy, gw, reps, warmup, steps, torch, ca, pb):
     g1 = gw.clone()
     t = _event_time_ms(lambda: pb.iso_noise_(g1, sigma=sig, salt_counter=salt), reps, torch)
     out["iso_noise"] = hbm(t, 6 * params, "noise_partials + noise_scale + noise_apply (6 B/param: the "
-                           "gradient read twice and written once; the draws are regenerated, not stored)")
+                           "gradient read twice and written once; the draws also pass through the workspace, 8 B/param more)")
     g2 = gw.clone()
     t = _event_time_ms(lambda: pb.sigmag_noise_(g2, dy, xb, sigma=sig, salt_counter=salt), reps, torch)
     out["sigmag_noise"] = mfma(t, 2.0 * M_TOK * N_OUT * K_IN,

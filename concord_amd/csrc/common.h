@@ -200,11 +200,12 @@ CONCORD_DEV float sqrt_rn(float x) {
   return s;
 }
 
-// cos(2 pi u) for u in [0, 1) on a 2^-24 grid: quadrant q = floor(4u) and
-// theta = (4u - q) pi/2 are exact up to the one product; cos and sin of
-// theta by Taylor polynomials in theta^2 (degree 10 and 11; |error| below
-// 1e-6 on [0, pi/2]), evaluated in a fixed order
-CONCORD_DEV float det_cos2pi(float u) {
+// cos(2 pi u) and sin(2 pi u) for u in [0, 1) on a 2^-24 grid: quadrant
+// q = floor(4u) and theta = (4u - q) pi/2 are exact up to the one product;
+// cos and sin of theta by Taylor polynomials in theta^2 (degree 10 and 11;
+// |error| below 1e-6 on [0, pi/2]), evaluated in a fixed order, then rotated
+// by q quarter turns
+CONCORD_DEV void det_sincos2pi(float u, float& cs, float& sn2) {
   const float t = __fmul_rn(u, 4.0f);
   const float qf = floorf(t);
   const int q = (int)qf;
@@ -223,25 +224,55 @@ CONCORD_DEV float det_cos2pi(float u) {
   sn = __fadd_rn(__fmul_rn(sn, s), -1.0f / 6.0f);
   sn = __fadd_rn(__fmul_rn(sn, s), 1.0f);
   sn = __fmul_rn(sn, th);
-  return q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+  cs = q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+  sn2 = q == 0 ? sn : q == 1 ? c : q == 2 ? -sn : -c;
 }
 
-// Standard normal draw `idx` of stream (seed, tag) (Box-Muller on one
-// Philox4x32-10 block; counter (idx, 0, 0, 0), key (seed, tag); the
-// isotropic noise uses tag 0x6E6F6973, the per-token draw 0x5369676D):
-//   u1 = ((c0 >> 8) + 1) 2^-24 in (0, 1],  u2 = (c1 >> 8) 2^-24 in [0, 1),
-//   z = sqrt(-2 ln u1) cos(2 pi u2), ln u1 = log2(u1) ln 2.
+CONCORD_DEV float det_cos2pi(float u) {
+  float c, s;
+  det_sincos2pi(u, c, s);
+  return c;
+}
+
+// Box-Muller radius sqrt(-2 ln u1) of a Philox word w, u1 = ((w >> 8) + 1)
+// 2^-24 in (0, 1], ln u1 = log2(u1) ln 2; and the angle's u2 = (w >> 8) 2^-24
+CONCORD_DEV float bm_radius(uint32_t w) {
+  const float u1 = __fmul_rn((float)((w >> 8) + 1u), 5.9604644775390625e-08f);
+  return sqrt_rn(__fmul_rn(-2.0f, __fmul_rn(det_log2(u1), 0.693147180559945309f)));
+}
+CONCORD_DEV float bm_angle(uint32_t w) { return __fmul_rn((float)(w >> 8), 5.9604644775390625e-08f); }
+
+// Standard normal draw `idx` of stream (seed, tag): Box-Muller on one
+// Philox4x32-10 block, counter (idx, 0, 0, 0), key (seed, tag); the per-token
+// draw of the Sigma_g noise uses tag 0x5369676D:
+//   z = sqrt(-2 ln u1) cos(2 pi u2), u1 from word 0, u2 from word 1.
 // A fixed sequence of IEEE ops (det_log2, sqrt_rn, det_cos2pi), so the CPU
 // restatement draws the same bits.
 constexpr uint32_t kNoiseTagIso = 0x6E6F6973u, kNoiseTagToken = 0x5369676Du;
-CONCORD_DEV float normal_draw(int32_t seed, uint32_t idx, uint32_t tag = kNoiseTagIso) {
+CONCORD_DEV float normal_draw(int32_t seed, uint32_t idx, uint32_t tag) {
   uint32_t c0 = idx, c1 = 0, c2 = 0, c3 = 0;
   philox4x32_10(c0, c1, c2, c3, (uint32_t)seed, tag);
-  const float u1 = __fmul_rn((float)((c0 >> 8) + 1u), 5.9604644775390625e-08f);
-  const float u2 = __fmul_rn((float)(c1 >> 8), 5.9604644775390625e-08f);
-  const float ln = __fmul_rn(det_log2(u1), 0.693147180559945309f);
-  const float r = sqrt_rn(__fmul_rn(-2.0f, ln));
-  return __fmul_rn(r, det_cos2pi(u2));
+  return __fmul_rn(bm_radius(c0), det_cos2pi(bm_angle(c1)));
+}
+
+// The isotropic stream (tag 0x6E6F6973): four draws per Philox block, counter
+// (blk, 0, 0, 0).  Words 0, 1 and words 2, 3 are two Box-Muller pairs, and
+// each pair gives both its cos and its sin draw:
+//   z[0] = r0 cos(2 pi a1), z[1] = r0 sin(2 pi a1),
+//   z[2] = r2 cos(2 pi a3), z[3] = r2 sin(2 pi a3)
+// (r_i = bm_radius(word i), a_i = bm_angle(word i)).  Element e of a gradient
+// takes z[e & 3] of block e >> 2; z[0] equals normal_draw(seed, blk, tag).
+CONCORD_DEV void normal_draw4(int32_t seed, uint32_t blk, float z[4]) {
+  uint32_t c0 = blk, c1 = 0, c2 = 0, c3 = 0;
+  philox4x32_10(c0, c1, c2, c3, (uint32_t)seed, kNoiseTagIso);
+  const float r0 = bm_radius(c0), r2 = bm_radius(c2);
+  float ca, sa, cb, sb;
+  det_sincos2pi(bm_angle(c1), ca, sa);
+  det_sincos2pi(bm_angle(c3), cb, sb);
+  z[0] = __fmul_rn(r0, ca);
+  z[1] = __fmul_rn(r0, sa);
+  z[2] = __fmul_rn(r2, cb);
+  z[3] = __fmul_rn(r2, sb);
 }
 
 CONCORD_DEV float pow_p(float x, float p) {

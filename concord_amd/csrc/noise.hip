@@ -3,11 +3,14 @@
 //   grad_W <- bf16(g + xi * (sigma * ||g|| / max(||xi||, 1e-12))),  xi ~ N(0, 1)
 // (notebook/src/prototype_packed_b.py:876-916 and the isotropic branch of
 // 1484-1501; sigma is a device scalar so a captured graph sees schedule
-// changes).  xi is normal_draw(salt, element index), counter-based: the
-// first pass draws it and keeps it (fp32, in the workspace) for the apply pass.
+// changes).  xi is counter-based: element e takes draw e & 3 of the Philox
+// block e >> 2 of normal_draw4(salt, .).  The first pass draws it and keeps
+// it (fp32, in the workspace) for the apply pass.
 //
 // Element e of an N x K gradient with row stride ld sits at (e / K) * ld + e % K;
-// with ld == K that is e itself (no division).
+// with ld == K that is e itself (no division).  A thread takes the four
+// elements of one Philox block; when K and ld are multiples of 4 they share a
+// row and move as one 8-byte access.
 #include "common.h"
 #include "gemm.h"
 
@@ -17,8 +20,9 @@ CONCORD_DEV int64_t elem_off(int64_t e, int64_t K, int64_t ld) { return ld == K 
 
 constexpr int kNoiseBlock = 8192;   // elements per partial
 
-// sums of g^2 and xi^2 over kNoiseBlock elements: lane t chains elements
-// b0 + t + 256 i (i ascending), then a halving tree over the 256 lanes
+// sums of g^2 and xi^2 over kNoiseBlock elements: lane t chains the quads
+// q = b0 / 4 + t + 256 i (i ascending), elements 4q .. 4q + 3 in turn, then a
+// halving tree over the 256 lanes
 __global__ __launch_bounds__(256) void noise_partials_kernel(const uint16_t* __restrict__ g, int64_t ld,
                                                              int64_t N, int64_t K, const int32_t* salt,
                                                              float* __restrict__ part, float* __restrict__ xi) {
@@ -26,15 +30,37 @@ __global__ __launch_bounds__(256) void noise_partials_kernel(const uint16_t* __r
   const int64_t total = N * K;
   const int64_t b0 = (int64_t)blockIdx.x * kNoiseBlock;
   const int32_t seed = *salt;
+  const bool vg = (K % 4) == 0 && (ld % 4) == 0 && ((uintptr_t)g % 8) == 0;
+  const bool vx = ((uintptr_t)xi % 16) == 0;
   float ag = 0.0f, ax = 0.0f;
-  for (int i = 0; i < kNoiseBlock / 256; ++i) {
-    const int64_t e = b0 + threadIdx.x + 256 * i;
-    if (e < total) {
-      const float v = bf16_to_f32(g[elem_off(e, K, ld)]);
-      const float z = normal_draw(seed, (uint32_t)e);
-      xi[e] = z;
-      ag = __fadd_rn(ag, __fmul_rn(v, v));
-      ax = __fadd_rn(ax, __fmul_rn(z, z));
+  for (int i = 0; i < kNoiseBlock / 1024; ++i) {
+    const int64_t e0 = b0 + 4 * (threadIdx.x + 256 * i);
+    if (e0 < total) {
+      float z[4], v[4];
+      normal_draw4(seed, (uint32_t)(e0 >> 2), z);
+      const bool full = e0 + 4 <= total;
+      if (full && vg) {
+        const uint2 w = *reinterpret_cast<const uint2*>(g + elem_off(e0, K, ld));
+        v[0] = __uint_as_float(w.x << 16);
+        v[1] = __uint_as_float(w.x & 0xFFFF0000u);
+        v[2] = __uint_as_float(w.y << 16);
+        v[3] = __uint_as_float(w.y & 0xFFFF0000u);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[r] = e0 + r < total ? bf16_to_f32(g[elem_off(e0 + r, K, ld)]) : 0.0f;
+      }
+      if (full && vx) {
+        *reinterpret_cast<float4*>(xi + e0) = make_float4(z[0], z[1], z[2], z[3]);
+      } else {
+        for (int r = 0; r < 4 && e0 + r < total; ++r) xi[e0 + r] = z[r];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        if (e0 + r < total) {
+          ag = __fadd_rn(ag, __fmul_rn(v[r], v[r]));
+          ax = __fadd_rn(ax, __fmul_rn(z[r], z[r]));
+        }
+      }
     }
   }
   sg[threadIdx.x] = ag;
@@ -70,12 +96,26 @@ __global__ __launch_bounds__(64) void noise_scale_kernel(const float* __restrict
 __global__ __launch_bounds__(256) void noise_apply_kernel(uint16_t* __restrict__ g, int64_t ld, int64_t N,
                                                           int64_t K, const float* __restrict__ xi,
                                                           const float* scale) {
-  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= N * K) return;
+  const int64_t total = N * K;
+  const int64_t e0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+  if (e0 >= total) return;
   const float s = *scale;
-  uint16_t* p = g + elem_off(e, K, ld);
-  const float v = __fadd_rn(bf16_to_f32(*p), __fmul_rn(xi[e], s));
-  *p = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+  if (e0 + 4 <= total && (K % 4) == 0 && (ld % 4) == 0 && ((uintptr_t)g % 8) == 0 && ((uintptr_t)xi % 16) == 0) {
+    uint2* p = reinterpret_cast<uint2*>(g + elem_off(e0, K, ld));
+    const uint2 w = *p;
+    const float4 z = *reinterpret_cast<const float4*>(xi + e0);
+    const float v0 = __fadd_rn(__uint_as_float(w.x << 16), __fmul_rn(z.x, s));
+    const float v1 = __fadd_rn(__uint_as_float(w.x & 0xFFFF0000u), __fmul_rn(z.y, s));
+    const float v2 = __fadd_rn(__uint_as_float(w.y << 16), __fmul_rn(z.z, s));
+    const float v3 = __fadd_rn(__uint_as_float(w.y & 0xFFFF0000u), __fmul_rn(z.w, s));
+    *p = make_uint2(pack_bf16x2(v0, v1), pack_bf16x2(v2, v3));
+  } else {
+    for (int64_t e = e0; e < e0 + 4 && e < total; ++e) {
+      uint16_t* p = g + elem_off(e, K, ld);
+      const float v = __fadd_rn(bf16_to_f32(*p), __fmul_rn(xi[e], s));
+      *p = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+    }
+  }
 }
 
 // ---- the Sigma_g-shaped draw (prototype_packed_b.py:1489-1496) ---------------
@@ -303,7 +343,7 @@ int iso_noise_launch(uint16_t* grad_w, int64_t ld_g, int64_t N, int64_t K, const
   hipLaunchKernelGGL(noise_partials_kernel, dim3((unsigned)nb), dim3(256), 0, st, grad_w, ld_g, N, K,
                      salt_counter, part, xi);
   hipLaunchKernelGGL(noise_scale_kernel, dim3(1), dim3(64), 0, st, part, nb, sigma, scale);
-  hipLaunchKernelGGL(noise_apply_kernel, dim3((unsigned)cdiv(N * K, 256)), dim3(256), 0, st, grad_w, ld_g, N,
+  hipLaunchKernelGGL(noise_apply_kernel, dim3((unsigned)cdiv(N * K, 1024)), dim3(256), 0, st, grad_w, ld_g, N,
                      K, xi, scale);
   return launch_status("iso_noise");
 }

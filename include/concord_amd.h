@@ -275,9 +275,10 @@ int concord_coherence_sum(const int32_t* packed, int64_t ld_p, int64_t N, int64_
  * (notebook/src/prototype_packed_b.py:876-916 and the isotropic branch of
  * 1484-1501): g <- bf16(g + xi * (sigma * ||g|| / max(||xi||, 1e-12))), sigma
  * read from device memory.  xi_e is a standard normal from a counter-based
- * stream (Philox4x32-10 block e keyed by the salt counter's current value,
- * Box-Muller with fixed-order log2 / sqrt / cos), so the result is
- * reproducible.  The salt counter is read, not advanced.
+ * stream keyed by the salt counter's current value: draw e & 3 of
+ * Philox4x32-10 block e >> 2, whose words (0, 1) and (2, 3) are two
+ * Box-Muller pairs giving cos then sin, with fixed-order log2 / sqrt /
+ * sincos.  So the result is reproducible.  The salt counter is read, not advanced.
  * workspace: concord_noise_workspace_bytes(N, K) bytes (block partials, and
  * the draws, 4 B per element, kept between the norm and apply passes); no
  * zeroing needed. */

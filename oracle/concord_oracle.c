@@ -716,9 +716,9 @@ float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C)
     return acc;
 }
 
-/* cos(2 pi u), u in [0, 1) on a 2^-24 grid: quadrant and Taylor polynomials
- * in theta^2, the op order of the library's det_cos2pi */
-static float det_cos2pi(float u) {
+/* cos(2 pi u) and sin(2 pi u), u in [0, 1) on a 2^-24 grid: quadrant and
+ * Taylor polynomials in theta^2, the op order of the library's det_sincos2pi */
+static void det_sincos2pi(float u, float* cs, float* sn2) {
     const float t = u * 4.0f;
     const float qf = floorf(t);
     const int q = (int)qf;
@@ -737,20 +737,46 @@ static float det_cos2pi(float u) {
     sn = sn * s + -1.0f / 6.0f;
     sn = sn * s + 1.0f;
     sn = sn * th;
-    return q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+    *cs = q == 0 ? c : q == 1 ? -sn : q == 2 ? -c : sn;
+    *sn2 = q == 0 ? sn : q == 1 ? c : q == 2 ? -sn : -c;
 }
 
-float oracle_normal_draw(int32_t seed, uint32_t idx) { return oracle_normal_draw_tag(seed, idx, 0x6E6F6973u); }
+/* Box-Muller radius sqrt(-2 ln u1), u1 = ((w >> 8) + 1) 2^-24, and angle
+ * fraction u2 = (w >> 8) 2^-24 of a Philox word */
+static float bm_radius(uint32_t w) {
+    const float u1 = (float)((w >> 8) + 1u) * 5.9604644775390625e-08f;
+    const float ln = det_log2(u1) * 0.693147180559945309f;
+    return sqrtf(-2.0f * ln);
+}
+static float bm_angle(uint32_t w) { return (float)(w >> 8) * 5.9604644775390625e-08f; }
 
 float oracle_normal_draw_tag(int32_t seed, uint32_t idx, uint32_t tag) {
     uint32_t c[4] = {idx, 0u, 0u, 0u};
     uint32_t k[2] = {(uint32_t)seed, tag};
     oracle_philox4x32_10(c, k);
-    const float u1 = (float)((c[0] >> 8) + 1u) * 5.9604644775390625e-08f;
-    const float u2 = (float)(c[1] >> 8) * 5.9604644775390625e-08f;
-    const float ln = det_log2(u1) * 0.693147180559945309f;
-    const float r = sqrtf(-2.0f * ln);
-    return r * det_cos2pi(u2);
+    float cs, sn;
+    det_sincos2pi(bm_angle(c[1]), &cs, &sn);
+    return bm_radius(c[0]) * cs;
+}
+
+void oracle_iso_draw4(int32_t seed, uint32_t blk, float z[4]) {
+    uint32_t c[4] = {blk, 0u, 0u, 0u};
+    uint32_t k[2] = {(uint32_t)seed, 0x6E6F6973u};
+    oracle_philox4x32_10(c, k);
+    const float r0 = bm_radius(c[0]), r2 = bm_radius(c[2]);
+    float ca, sa, cb, sb;
+    det_sincos2pi(bm_angle(c[1]), &ca, &sa);
+    det_sincos2pi(bm_angle(c[3]), &cb, &sb);
+    z[0] = r0 * ca;
+    z[1] = r0 * sa;
+    z[2] = r2 * cb;
+    z[3] = r2 * sb;
+}
+
+float oracle_iso_draw(int32_t seed, int64_t e) {
+    float z[4];
+    oracle_iso_draw4(seed, (uint32_t)(e >> 2), z);
+    return z[e & 3];
 }
 
 void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t salt) {
@@ -760,13 +786,16 @@ void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t sa
         float pg[256], px[256];
         for (int t = 0; t < 256; ++t) {
             float ag = 0.0f, ax = 0.0f;
-            for (int i = 0; i < 32; ++i) {
-                const int64_t e = b0 + t + 256 * i;
-                if (e >= total) continue;
-                const float v = bf16_to_f32(g[e]);
-                const float z = oracle_normal_draw(salt, (uint32_t)e);
-                ag = ag + v * v;
-                ax = ax + z * z;
+            for (int i = 0; i < 8; ++i) {
+                const int64_t e0 = b0 + 4 * (t + 256 * i);
+                if (e0 >= total) continue;
+                float z[4];
+                oracle_iso_draw4(salt, (uint32_t)(e0 >> 2), z);
+                for (int r = 0; r < 4 && e0 + r < total; ++r) {
+                    const float v = bf16_to_f32(g[e0 + r]);
+                    ag = ag + v * v;
+                    ax = ax + z[r] * z[r];
+                }
             }
             pg[t] = ag;
             px[t] = ax;
@@ -783,7 +812,7 @@ void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t sa
     const float nx = fmaxf(sqrtf(sx), 1e-12f);
     const float scale = (sigma * ng) / nx;
     for (int64_t e = 0; e < total; ++e)
-        g[e] = oracle_f32_to_bf16(bf16_to_f32(g[e]) + oracle_normal_draw(salt, (uint32_t)e) * scale);
+        g[e] = oracle_f32_to_bf16(bf16_to_f32(g[e]) + oracle_iso_draw(salt, e) * scale);
 }
 
 float oracle_token_sum(int32_t seed, int64_t M) {

@@ -115,12 +115,16 @@ float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K);
 /* sum of gate_coherence_from_fields (concord/packed_b.py:2081-2091) over the
  * N x K words, in the library's block / lane / tree order */
 float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C);
-/* standard normal draw idx of stream seed: Box-Muller on one Philox4x32-10
- * block, with this build's fixed-order log2 / sqrt / cos(2 pi u) */
-float oracle_normal_draw(int32_t seed, uint32_t idx);
-/* the same with the Philox key's second word = tag (0x6E6F6973 isotropic,
- * 0x5369676D per-token) */
+/* standard normal draw idx of stream (seed, tag): Box-Muller on one
+ * Philox4x32-10 block (counter (idx, 0, 0, 0), key (seed, tag)), words 0 and
+ * 1, cos output, with this build's fixed-order log2 / sqrt / cos(2 pi u); the
+ * per-token draws of the Sigma_g noise use tag 0x5369676D */
 float oracle_normal_draw_tag(int32_t seed, uint32_t idx, uint32_t tag);
+/* the isotropic stream: the four draws of Philox block blk under key (seed,
+ * 0x6E6F6973), words (0, 1) and (2, 3) as two Box-Muller pairs, cos then sin
+ * of each; element e of a gradient takes draw e & 3 of block e >> 2 */
+void oracle_iso_draw4(int32_t seed, uint32_t blk, float z[4]);
+float oracle_iso_draw(int32_t seed, int64_t e);
 /* sum of the per-token draws 0 .. M-1 in the library's block / lane / tree order */
 float oracle_token_sum(int32_t seed, int64_t M);
 /* Sigma_g combine in place (prototype_packed_b.py:1489-1500), P the product
@@ -129,7 +133,7 @@ float oracle_token_sum(int32_t seed, int64_t M);
 void oracle_sigmag_combine(uint16_t* g, const uint16_t* P, int64_t N, int64_t K, float S, float Mf,
                            float sigma);
 /* isotropic gradient noise in place: g <- bf16(g + xi * (sigma * ||g|| /
- * max(||xi||, 1e-12))), xi_e = oracle_normal_draw(salt, e)
+ * max(||xi||, 1e-12))), xi_e = oracle_iso_draw(salt, e)
  * (notebook/src/prototype_packed_b.py:1484-1501, isotropic branch) */
 void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t salt);
 void oracle_muon_ns5(const uint16_t* g, int64_t N, int64_t K, float gamma, uint16_t* out);

@@ -83,8 +83,8 @@ def lib():
         L.oracle_frob_sumsq.argtypes = [P, i64, i64]
         L.oracle_coherence_sum.restype = f32
         L.oracle_coherence_sum.argtypes = [P, i64, i64, f32]
-        L.oracle_normal_draw.restype = f32
-        L.oracle_normal_draw.argtypes = [i32, ctypes.c_uint32]
+        L.oracle_iso_draw.restype = f32
+        L.oracle_iso_draw.argtypes = [i32, i64]
         L.oracle_iso_noise.argtypes = [P, i64, i64, f32, i32]
         L.oracle_normal_draw_tag.restype = f32
         L.oracle_normal_draw_tag.argtypes = [i32, ctypes.c_uint32, ctypes.c_uint32]
@@ -219,10 +219,19 @@ def coherence_sum(packed, drift_cancel_C):
     return np.float32(lib().oracle_coherence_sum(_p(p), p.shape[0], p.shape[1], float(drift_cancel_C)))
 
 
-def normal_draws(seed, n, start=0):
-    """Draws start .. start + n - 1 of the library's normal stream `seed`."""
-    f = lib().oracle_normal_draw
-    return np.array([f(int(seed), (start + i) & 0xFFFFFFFF) for i in range(n)], dtype=np.float32)
+def iso_draws(seed, n, start=0):
+    """Draws start .. start + n - 1 of the isotropic noise stream `seed`
+    (element e: draw e & 3 of Philox block e >> 2)."""
+    f = lib().oracle_iso_draw
+    return np.array([f(int(seed), start + i) for i in range(n)], dtype=np.float32)
+
+
+TAG_ISO = 0x6E6F6973
+
+
+def normal_draw_tag(seed, idx, tag):
+    """One Box-Muller draw (cos output) on Philox block idx under key (seed, tag)."""
+    return np.float32(lib().oracle_normal_draw_tag(int(seed), int(idx) & 0xFFFFFFFF, int(tag)))
 
 
 TAG_TOKEN = 0x5369676D

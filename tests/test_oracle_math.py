@@ -620,26 +620,40 @@ def test_materialize_gated_closed_forms(oracle):
 
 # ---------------------------------------------------------------- gradient noise
 
-def test_normal_draw_matches_float64_box_muller(oracle):
-    """Each draw is Box-Muller on its own Philox4x32-10 block (counter (i, 0,
-    0, 0), key (seed, 0x6E6F6973)); the fixed-order float32 log2 / sqrt /
-    cos(2 pi u) agree with float64 to ~1e-6 of the draw's scale."""
+def test_iso_draws_match_float64_box_muller(oracle):
+    """The isotropic stream takes four draws from each Philox4x32-10 block
+    (counter (b, 0, 0, 0), key (seed, 0x6E6F6973)): words (0, 1) and (2, 3)
+    are Box-Muller pairs, each giving its cos and then its sin draw.  The
+    fixed-order float32 log2 / sqrt / sincos(2 pi u) agree with float64 to
+    ~1e-6 of the draw's scale, in all four quadrants of the angle."""
     seed = -12345
-    z = oracle.normal_draws(seed, 4000)
-    for i in range(0, 4000, 37):
-        c = oracle.philox4x32_10([i, 0, 0, 0], [seed & 0xFFFFFFFF, 0x6E6F6973])
-        u1 = ((int(c[0]) >> 8) + 1) * 2.0 ** -24
-        u2 = (int(c[1]) >> 8) * 2.0 ** -24
-        want = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
-        assert abs(float(z[i]) - want) <= 4e-6 * max(1.0, abs(want)), (i, z[i], want)
+    z = oracle.iso_draws(seed, 4 * 1200)
+    quads = set()
+    for b in range(0, 1200, 7):
+        c = oracle.philox4x32_10([b, 0, 0, 0], [seed & 0xFFFFFFFF, oracle.TAG_ISO])
+        for p in (0, 1):
+            u1 = ((int(c[2 * p]) >> 8) + 1) * 2.0 ** -24
+            u2 = (int(c[2 * p + 1]) >> 8) * 2.0 ** -24
+            quads.add(int(u2 * 4))
+            r = np.sqrt(-2.0 * np.log(u1))
+            for k, want in enumerate((r * np.cos(2.0 * np.pi * u2), r * np.sin(2.0 * np.pi * u2))):
+                got = float(z[4 * b + 2 * p + k])
+                assert abs(got - want) <= 4e-6 * max(1.0, abs(want)), (b, p, k, got, want)
+        # the block's first draw is the one-draw form on the same block
+        assert z[4 * b] == oracle.normal_draw_tag(seed, b, oracle.TAG_ISO)
+    assert quads == {0, 1, 2, 3}
 
 
-def test_normal_draw_statistics(oracle):
-    z = oracle.normal_draws(7, 400000).astype(np.float64)
+def test_iso_draw_statistics(oracle):
+    z = oracle.iso_draws(7, 400000).astype(np.float64)
     assert abs(z.mean()) < 5e-3 and abs(z.std() - 1.0) < 5e-3
     assert abs((np.abs(z) > 2.0).mean() - 0.0455) < 2e-3
     assert abs(np.mean(z ** 4) - 3.0) < 5e-2          # Gaussian kurtosis
-    z2 = oracle.normal_draws(8, 400000).astype(np.float64)
+    q = z.reshape(-1, 4)
+    for a, b in ((0, 1), (2, 3), (0, 2), (1, 3)):     # the cos/sin pairs and the two pairs
+        assert abs(np.corrcoef(q[:, a], q[:, b])[0, 1]) < 1e-2
+        assert abs(np.corrcoef(q[:, a] ** 2, q[:, b] ** 2)[0, 1]) < 2e-2
+    z2 = oracle.iso_draws(8, 400000).astype(np.float64)
     assert abs(np.corrcoef(z, z2)[0, 1]) < 1e-2       # streams of different seeds
 
 
@@ -660,9 +674,9 @@ def test_iso_noise_closed_forms(oracle):
 
 
 def test_token_draws_are_the_tagged_stream(oracle):
-    """The per-token draws use the same Box-Muller on Philox block (m, 0, 0,
-    0) as the isotropic stream, under the second key word 0x5369676D, and
-    the token sum is their fixed-order float32 total."""
+    """The per-token draws are Box-Muller (words 0 and 1, cos output) on
+    Philox block (m, 0, 0, 0) under the second key word 0x5369676D, and the
+    token sum is their fixed-order float32 total."""
     seed = 4242
     eps = oracle.token_draws(seed, 3000)
     for m in range(0, 3000, 53):
@@ -671,7 +685,7 @@ def test_token_draws_are_the_tagged_stream(oracle):
         u2 = (int(c[1]) >> 8) * 2.0 ** -24
         want = np.sqrt(-2.0 * np.log(u1)) * np.cos(2.0 * np.pi * u2)
         assert abs(float(eps[m]) - want) <= 4e-6 * max(1.0, abs(want))
-    assert not np.array_equal(eps[:100], oracle.normal_draws(seed, 100))
+    assert not np.array_equal(eps[:100], oracle.iso_draws(seed, 400)[::4])
     for M in (1, 7, 8192, 8193, 20000):
         e = oracle.token_draws(seed, M).astype(np.float64)
         assert abs(float(oracle.token_sum(seed, M)) - e.sum()) < 1e-5 * max(1.0, np.abs(e).sum())
