@@ -288,12 +288,100 @@ CONCORD_DEV float lane_value(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
-// ((0 + v[0]) + v[stride]) + ... + v[(count - 1) stride], summed in that order
-// by one wave (every lane carries the same running sum).  The terms are
-// loaded 16 x 64 at a time, so a long chain pays one memory round trip per
-// 1024 terms rather than one per 64.
+// Lane 0 adds buf[0 .. cnt) to s in index order (buf 16-byte aligned).  The
+// LDS reads of the next 16 values go out before the adds of the current 16,
+// so each term costs one dependent add.
+CONCORD_DEV float lds_chain(const float* buf, int cnt, float s) {
+  const float4* b4 = reinterpret_cast<const float4*>(buf);
+  int j = 0;
+  if (cnt >= 16) {
+    float4 cur[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) cur[t] = b4[t];
+    for (j = 16; j + 16 <= cnt; j += 16) {
+      float4 nxt[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) nxt[t] = b4[j / 4 + t];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        s = __fadd_rn(s, cur[t].x);
+        s = __fadd_rn(s, cur[t].y);
+        s = __fadd_rn(s, cur[t].z);
+        s = __fadd_rn(s, cur[t].w);
+        cur[t] = nxt[t];
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      s = __fadd_rn(s, cur[t].x);
+      s = __fadd_rn(s, cur[t].y);
+      s = __fadd_rn(s, cur[t].z);
+      s = __fadd_rn(s, cur[t].w);
+    }
+  }
+  for (; j < cnt; ++j) s = __fadd_rn(s, buf[j]);
+  return s;
+}
+
+// The same for two chains over a[] and b[], term j of both in turn.
+CONCORD_DEV void lds_chain2(const float* a, const float* b, int cnt, float& x0, float& x1) {
+  const float4* a4 = reinterpret_cast<const float4*>(a);
+  const float4* b4 = reinterpret_cast<const float4*>(b);
+  int j = 0;
+  if (cnt >= 8) {
+    float4 ca[2], cb[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      ca[t] = a4[t];
+      cb[t] = b4[t];
+    }
+    for (j = 8; j + 8 <= cnt; j += 8) {
+      float4 na[2], nb[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        na[t] = a4[j / 4 + t];
+        nb[t] = b4[j / 4 + t];
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        x0 = __fadd_rn(x0, ca[t].x);
+        x1 = __fadd_rn(x1, cb[t].x);
+        x0 = __fadd_rn(x0, ca[t].y);
+        x1 = __fadd_rn(x1, cb[t].y);
+        x0 = __fadd_rn(x0, ca[t].z);
+        x1 = __fadd_rn(x1, cb[t].z);
+        x0 = __fadd_rn(x0, ca[t].w);
+        x1 = __fadd_rn(x1, cb[t].w);
+        ca[t] = na[t];
+        cb[t] = nb[t];
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      x0 = __fadd_rn(x0, ca[t].x);
+      x1 = __fadd_rn(x1, cb[t].x);
+      x0 = __fadd_rn(x0, ca[t].y);
+      x1 = __fadd_rn(x1, cb[t].y);
+      x0 = __fadd_rn(x0, ca[t].z);
+      x1 = __fadd_rn(x1, cb[t].z);
+      x0 = __fadd_rn(x0, ca[t].w);
+      x1 = __fadd_rn(x1, cb[t].w);
+    }
+  }
+  for (; j < cnt; ++j) {
+    x0 = __fadd_rn(x0, a[j]);
+    x1 = __fadd_rn(x1, b[j]);
+  }
+}
+
+// Serial sum ((0 + v[0]) + v[stride]) + ... over `count` terms, in index
+// order, as a wave-uniform value.  The wave loads 16 x 64 terms per memory
+// round trip and stages them in LDS; lane 0 chains them (lds_chain).  Called
+// by every lane of a block's only wave (it holds a block-private LDS buffer
+// and synchronises the block).
 CONCORD_DEV float wave_chain(const float* __restrict__ v, int64_t count, int64_t stride) {
   constexpr int B = 16;
+  __shared__ __align__(16) float buf[64 * B];
   const int lane = threadIdx.x & 63;
   float s = 0.0f;
   for (int64_t c0 = 0; c0 < count; c0 += 64 * B) {
@@ -303,28 +391,24 @@ CONCORD_DEV float wave_chain(const float* __restrict__ v, int64_t count, int64_t
       const int64_t i = c0 + 64 * b + lane;
       a[b] = i < count ? v[i * stride] : 0.0f;
     }
+    __syncthreads();   // lane 0 is done with the previous round's values
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const int64_t base = c0 + 64 * b;
-      if (base >= count) break;
-      const int cnt = (int)min((int64_t)64, count - base);
-      if (cnt == 64) {
-#pragma unroll
-        for (int j = 0; j < 64; ++j) s = __fadd_rn(s, lane_value(a[b], j));
-      } else {
-        for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, lane_value(a[b], j));
-      }
-    }
+    for (int b = 0; b < B; ++b) buf[64 * b + lane] = a[b];
+    __syncthreads();
+    if (lane == 0) s = lds_chain(buf, (int)min((int64_t)(64 * B), count - c0), s);
   }
-  return s;
+  return lane_value(s, 0);
 }
 
 // Two chains at once over interleaved pairs (v[2i], v[2i + 1]), i ascending:
 // *s0 = ((0 + v[0]) + v[2]) + ..., *s1 = ((0 + v[1]) + v[3]) + ...  Each
 // chain keeps its own order; running both side by side halves the
-// dependent-add latency of two chains in turn.
+// dependent-add latency of two chains in turn.  Same calling rule as
+// wave_chain.
 CONCORD_DEV void wave_chain2(const float* __restrict__ v, int64_t count, float* s0, float* s1) {
   constexpr int B = 8;
+  __shared__ __align__(16) float bufa[64 * B];
+  __shared__ __align__(16) float bufb[64 * B];
   const int lane = threadIdx.x & 63;
   float x0 = 0.0f, x1 = 0.0f;
   for (int64_t c0 = 0; c0 < count; c0 += 64 * B) {
@@ -335,27 +419,17 @@ CONCORD_DEV void wave_chain2(const float* __restrict__ v, int64_t count, float* 
       a[q] = i < count ? v[2 * i] : 0.0f;
       b[q] = i < count ? v[2 * i + 1] : 0.0f;
     }
+    __syncthreads();
 #pragma unroll
     for (int q = 0; q < B; ++q) {
-      const int64_t base = c0 + 64 * q;
-      if (base >= count) break;
-      const int cnt = (int)min((int64_t)64, count - base);
-      if (cnt == 64) {
-#pragma unroll
-        for (int j = 0; j < 64; ++j) {
-          x0 = __fadd_rn(x0, lane_value(a[q], j));
-          x1 = __fadd_rn(x1, lane_value(b[q], j));
-        }
-      } else {
-        for (int j = 0; j < cnt; ++j) {
-          x0 = __fadd_rn(x0, lane_value(a[q], j));
-          x1 = __fadd_rn(x1, lane_value(b[q], j));
-        }
-      }
+      bufa[64 * q + lane] = a[q];
+      bufb[64 * q + lane] = b[q];
     }
+    __syncthreads();
+    if (lane == 0) lds_chain2(bufa, bufb, (int)min((int64_t)(64 * B), count - c0), x0, x1);
   }
-  *s0 = x0;
-  *s1 = x1;
+  *s0 = lane_value(x0, 0);
+  *s1 = lane_value(x1, 0);
 }
 
 // max over the wave's 64 lanes, as a wave-uniform value.  DPP steps: prefix
