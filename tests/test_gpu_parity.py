@@ -1081,7 +1081,9 @@ def test_consolidated_state_dict_matches_layers():
 
 # ---------------------------------------------------------------- multi-layer statistics
 
-@pytest.mark.parametrize("N,K,ld", [(300, 777, 777), (5120, 1280, 1280), (33, 100, 128), (1, 5, 5)])
+# (4096, 2112): 1056 block partials, so the final chain takes two staging rounds of up to 1024
+@pytest.mark.parametrize("N,K,ld", [(300, 777, 777), (5120, 1280, 1280), (33, 100, 128), (1, 5, 5),
+                                    (4096, 2112, 2112)])
 def test_coherence_sum_bit_exact(oracle, N, K, ld):
     from concord_amd import _lib as C
     from concord_amd import packed_b as pb
