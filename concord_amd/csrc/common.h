@@ -288,11 +288,39 @@ CONCORD_DEV float lane_value(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
-// Lane 0 adds buf[0 .. cnt) to s in index order (buf 16-byte aligned).  The
-// LDS reads of the next 16 values go out before the adds of the current 16,
-// so each term costs one dependent add.
+// Lane 0 adds buf[0 .. cnt) to s in index order (buf 16-byte aligned).  A
+// full chunk of kFull terms (a multiple of 32) is one unrolled, software-
+// pipelined run; a shorter one issues the LDS reads of the next 16 values
+// before the adds of the current 16.
+template <int kFull>
 CONCORD_DEV float lds_chain(const float* buf, int cnt, float s) {
   const float4* b4 = reinterpret_cast<const float4*>(buf);
+  if (cnt == kFull) {
+    // a full chunk, unrolled: the reads of batch g + 1 (8 x 16 bytes) go out
+    // before the 32 adds of batch g; the scheduling barriers keep them there
+    constexpr int G = 8, NG = kFull / (4 * G);
+    float4 r[2][G];
+#pragma unroll
+    for (int t = 0; t < G; ++t) r[0][t] = b4[t];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g + 1 < NG) {
+#pragma unroll
+        for (int t = 0; t < G; ++t) r[(g + 1) & 1][t] = b4[(g + 1) * G + t];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < G; ++t) {
+        const float4 q = r[g & 1][t];
+        s = __fadd_rn(s, q.x);
+        s = __fadd_rn(s, q.y);
+        s = __fadd_rn(s, q.z);
+        s = __fadd_rn(s, q.w);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return s;
+  }
   int j = 0;
   if (cnt >= 16) {
     float4 cur[4];
@@ -324,9 +352,44 @@ CONCORD_DEV float lds_chain(const float* buf, int cnt, float s) {
 }
 
 // The same for two chains over a[] and b[], term j of both in turn.
+template <int kFull>
 CONCORD_DEV void lds_chain2(const float* a, const float* b, int cnt, float& x0, float& x1) {
   const float4* a4 = reinterpret_cast<const float4*>(a);
   const float4* b4 = reinterpret_cast<const float4*>(b);
+  if (cnt == kFull) {
+    constexpr int G = 8, NG = kFull / (4 * G);
+    float4 ra[2][G], rb[2][G];
+#pragma unroll
+    for (int t = 0; t < G; ++t) {
+      ra[0][t] = a4[t];
+      rb[0][t] = b4[t];
+    }
+#pragma unroll
+    for (int g = 0; g < NG; ++g) {
+      if (g + 1 < NG) {
+#pragma unroll
+        for (int t = 0; t < G; ++t) {
+          ra[(g + 1) & 1][t] = a4[(g + 1) * G + t];
+          rb[(g + 1) & 1][t] = b4[(g + 1) * G + t];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < G; ++t) {
+        const float4 p = ra[g & 1][t], q = rb[g & 1][t];
+        x0 = __fadd_rn(x0, p.x);
+        x1 = __fadd_rn(x1, q.x);
+        x0 = __fadd_rn(x0, p.y);
+        x1 = __fadd_rn(x1, q.y);
+        x0 = __fadd_rn(x0, p.z);
+        x1 = __fadd_rn(x1, q.z);
+        x0 = __fadd_rn(x0, p.w);
+        x1 = __fadd_rn(x1, q.w);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return;
+  }
   int j = 0;
   if (cnt >= 8) {
     float4 ca[2], cb[2];
@@ -395,7 +458,7 @@ CONCORD_DEV float wave_chain(const float* __restrict__ v, int64_t count, int64_t
 #pragma unroll
     for (int b = 0; b < B; ++b) buf[64 * b + lane] = a[b];
     __syncthreads();
-    if (lane == 0) s = lds_chain(buf, (int)min((int64_t)(64 * B), count - c0), s);
+    if (lane == 0) s = lds_chain<64 * B>(buf, (int)min((int64_t)(64 * B), count - c0), s);
   }
   return lane_value(s, 0);
 }
@@ -426,7 +489,7 @@ CONCORD_DEV void wave_chain2(const float* __restrict__ v, int64_t count, float* 
       bufb[64 * q + lane] = b[q];
     }
     __syncthreads();
-    if (lane == 0) lds_chain2(bufa, bufb, (int)min((int64_t)(64 * B), count - c0), x0, x1);
+    if (lane == 0) lds_chain2<64 * B>(bufa, bufb, (int)min((int64_t)(64 * B), count - c0), x0, x1);
   }
   *s0 = lane_value(x0, 0);
   *s1 = lane_value(x1, 0);
