@@ -290,8 +290,8 @@ CONCORD_DEV float lane_value(float v, int j) {
 
 // Lane 0 adds buf[0 .. cnt) to s in index order (buf 16-byte aligned).  A
 // full chunk of kFull terms (a multiple of 32) is one unrolled, software-
-// pipelined run; a shorter one issues the LDS reads of the next 16 values
-// before the adds of the current 16.
+// pipelined run; a shorter one runs batches of 32 whose LDS reads go out one
+// batch ahead, then the remaining terms one by one.
 template <int kFull>
 CONCORD_DEV float lds_chain(const float* buf, int cnt, float s) {
   const float4* b4 = reinterpret_cast<const float4*>(buf);
@@ -321,31 +321,44 @@ CONCORD_DEV float lds_chain(const float* buf, int cnt, float s) {
     }
     return s;
   }
+  // batches of 32 terms, alternating between two register sets; then the tail
   int j = 0;
-  if (cnt >= 16) {
-    float4 cur[4];
+  const int nb = cnt / 32;
+  if (nb > 0) {
+    float4 r0[8], r1[8];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) cur[t] = b4[t];
-    for (j = 16; j + 16 <= cnt; j += 16) {
-      float4 nxt[4];
+    for (int t = 0; t < 8; ++t) r0[t] = b4[t];
+    for (int g = 0;;) {
+      if (g + 1 < nb) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t) nxt[t] = b4[j / 4 + t];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        s = __fadd_rn(s, cur[t].x);
-        s = __fadd_rn(s, cur[t].y);
-        s = __fadd_rn(s, cur[t].z);
-        s = __fadd_rn(s, cur[t].w);
-        cur[t] = nxt[t];
+        for (int t = 0; t < 8; ++t) r1[t] = b4[(g + 1) * 8 + t];
       }
-    }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      s = __fadd_rn(s, cur[t].x);
-      s = __fadd_rn(s, cur[t].y);
-      s = __fadd_rn(s, cur[t].z);
-      s = __fadd_rn(s, cur[t].w);
+      for (int t = 0; t < 8; ++t) {
+        s = __fadd_rn(s, r0[t].x);
+        s = __fadd_rn(s, r0[t].y);
+        s = __fadd_rn(s, r0[t].z);
+        s = __fadd_rn(s, r0[t].w);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (++g == nb) break;
+      if (g + 1 < nb) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) r0[t] = b4[(g + 1) * 8 + t];
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        s = __fadd_rn(s, r1[t].x);
+        s = __fadd_rn(s, r1[t].y);
+        s = __fadd_rn(s, r1[t].z);
+        s = __fadd_rn(s, r1[t].w);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (++g == nb) break;
     }
+    j = nb * 32;
   }
   for (; j < cnt; ++j) s = __fadd_rn(s, buf[j]);
   return s;
@@ -390,46 +403,61 @@ CONCORD_DEV void lds_chain2(const float* a, const float* b, int cnt, float& x0, 
     }
     return;
   }
+  // batches of 16 pairs, alternating between two register sets; then the tail
   int j = 0;
-  if (cnt >= 8) {
-    float4 ca[2], cb[2];
+  const int nb = cnt / 16;
+  if (nb > 0) {
+    float4 a0[4], b0[4], a1[4], b1[4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      ca[t] = a4[t];
-      cb[t] = b4[t];
+    for (int t = 0; t < 4; ++t) {
+      a0[t] = a4[t];
+      b0[t] = b4[t];
     }
-    for (j = 8; j + 8 <= cnt; j += 8) {
-      float4 na[2], nb[2];
+    for (int g = 0;;) {
+      if (g + 1 < nb) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        na[t] = a4[j / 4 + t];
-        nb[t] = b4[j / 4 + t];
+        for (int t = 0; t < 4; ++t) {
+          a1[t] = a4[(g + 1) * 4 + t];
+          b1[t] = b4[(g + 1) * 4 + t];
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        x0 = __fadd_rn(x0, ca[t].x);
-        x1 = __fadd_rn(x1, cb[t].x);
-        x0 = __fadd_rn(x0, ca[t].y);
-        x1 = __fadd_rn(x1, cb[t].y);
-        x0 = __fadd_rn(x0, ca[t].z);
-        x1 = __fadd_rn(x1, cb[t].z);
-        x0 = __fadd_rn(x0, ca[t].w);
-        x1 = __fadd_rn(x1, cb[t].w);
-        ca[t] = na[t];
-        cb[t] = nb[t];
+      for (int t = 0; t < 4; ++t) {
+        x0 = __fadd_rn(x0, a0[t].x);
+        x1 = __fadd_rn(x1, b0[t].x);
+        x0 = __fadd_rn(x0, a0[t].y);
+        x1 = __fadd_rn(x1, b0[t].y);
+        x0 = __fadd_rn(x0, a0[t].z);
+        x1 = __fadd_rn(x1, b0[t].z);
+        x0 = __fadd_rn(x0, a0[t].w);
+        x1 = __fadd_rn(x1, b0[t].w);
       }
-    }
+      __builtin_amdgcn_sched_barrier(0);
+      if (++g == nb) break;
+      if (g + 1 < nb) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      x0 = __fadd_rn(x0, ca[t].x);
-      x1 = __fadd_rn(x1, cb[t].x);
-      x0 = __fadd_rn(x0, ca[t].y);
-      x1 = __fadd_rn(x1, cb[t].y);
-      x0 = __fadd_rn(x0, ca[t].z);
-      x1 = __fadd_rn(x1, cb[t].z);
-      x0 = __fadd_rn(x0, ca[t].w);
-      x1 = __fadd_rn(x1, cb[t].w);
+        for (int t = 0; t < 4; ++t) {
+          a0[t] = a4[(g + 1) * 4 + t];
+          b0[t] = b4[(g + 1) * 4 + t];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        x0 = __fadd_rn(x0, a1[t].x);
+        x1 = __fadd_rn(x1, b1[t].x);
+        x0 = __fadd_rn(x0, a1[t].y);
+        x1 = __fadd_rn(x1, b1[t].y);
+        x0 = __fadd_rn(x0, a1[t].z);
+        x1 = __fadd_rn(x1, b1[t].z);
+        x0 = __fadd_rn(x0, a1[t].w);
+        x1 = __fadd_rn(x1, b1[t].w);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (++g == nb) break;
     }
+    j = nb * 16;
   }
   for (; j < cnt; ++j) {
     x0 = __fadd_rn(x0, a[j]);
