@@ -92,9 +92,22 @@ def _read_traffic():
     return out
 
 
-def cpu_baseline(threads):
-    """One step of the same workload on the host cores: torch fp32 GEMMs and
-    the CPU oracle's v-hat EMA, packed update and rebalance."""
+def _cpu_model():
+    """The host CPU's model name from /proc/cpuinfo (what lscpu prints)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline_leg(threads, max_s, max_steps):
+    """Steps of the same workload on the host cores with `threads` threads:
+    torch fp32 GEMMs and the CPU oracle's v-hat EMA, packed update and
+    rebalance.  One untimed step, then steps until max_s seconds or
+    max_steps steps."""
     import numpy as np
     import torch
     from oracle import oracle as O
@@ -135,13 +148,25 @@ def cpu_baseline(threads):
         step(2 + reps)
         reps += 1
         el = time.perf_counter() - t0
-        if el > 10.0 or reps >= 10:
+        if el > max_s or reps >= max_steps:
             break
     sec = el / reps
-    return {"value": 6.0 * M_TOK * N_OUT * K_IN / sec / 1e12, "unit": "TFLOP/s", "cores": threads,
-            "kind": "port", "ms_per_step": sec * 1e3,
-            "sample": f"{reps} full steps of the 1280->5120 M=2048 workload: torch fp32 GEMMs "
-                      f"(fwd, dgrad, wgrad) + oracle v-hat, update, rebalance"}
+    return {"value": round(6.0 * M_TOK * N_OUT * K_IN / sec / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+            "ms_per_step": round(sec * 1e3, 2), "steps_timed": reps}
+
+
+def cpu_baseline():
+    """The step on the GPU box's host cores, twice: with every CPU this
+    process may run on (the reported value) and with one thread."""
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    full = cpu_baseline_leg(avail, 10.0, 10)
+    one = cpu_baseline_leg(1, 12.0, 4)
+    return dict(full, kind="port",
+                sample=f"{full['steps_timed']} full steps of the 1280->5120 M=2048 workload on {avail} threads "
+                       f"(and {one['steps_timed']} on 1 thread): torch fp32 GEMMs (fwd, dgrad, wgrad) + oracle "
+                       "v-hat, update, rebalance",
+                single_thread=one, os_cpu_count=os.cpu_count(), affinity_cpus=avail, cpu_model=_cpu_model(),
+                omp_num_threads=os.environ.get("OMP_NUM_THREADS"))
 
 
 def _graph_ms(step, warmup, steps, torch, per_graph=1):
@@ -609,8 +634,7 @@ def main():
         "wall_s_timed": round(wall, 3),
     }
     if not args.no_cpu_baseline:
-        threads = min(16, os.cpu_count() or 1)
-        out["cpu_baseline"] = cpu_baseline(threads)
+        out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out))
 
 

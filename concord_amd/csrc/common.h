@@ -541,4 +541,11 @@ CONCORD_DEV int32_t wave_max(int32_t v) {
 
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Every launch of this library keeps grid.y and grid.z at or below
+// kMaxGridY.  A kernel whose row-block count can exceed it is launched with
+// grid.y = grid_y(count) and strides over the row blocks by gridDim.y; the
+// entry points of the others reject sizes whose grid would exceed it.
+constexpr int64_t kMaxGridY = 65535;
+inline unsigned grid_y(int64_t blocks) { return (unsigned)(blocks < kMaxGridY ? blocks : kMaxGridY); }
+
 }  // namespace concord

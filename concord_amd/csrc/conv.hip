@@ -260,7 +260,7 @@ extern "C" int concord_conv_im2col(const uint16_t* x, int64_t B, int64_t C, int6
   CONCORD_CHECK(H + 2 * ph < ((int64_t)1 << 30) && W + 2 * pw < ((int64_t)1 << 30) && C * H * W < ((int64_t)1 << 40),
                 "concord_conv_im2col: image too large");
   const int64_t M = B * g.Ho * g.Wo;
-  CONCORD_CHECK(cdiv(M, kTileM) < ((int64_t)1 << 31) && cdiv(g.K, kTileK) < 65536 && B * C * H * W < ((int64_t)1 << 40),
+  CONCORD_CHECK(cdiv(M, kTileM) < ((int64_t)1 << 31) && cdiv(g.K, kTileK) <= kMaxGridY && B * C * H * W < ((int64_t)1 << 40),
                 "concord_conv_im2col: size too large");
   if (M == 0) return CONCORD_OK;
   hipLaunchKernelGGL(im2col_kernel, dim3((unsigned)cdiv(M, kTileM), (unsigned)cdiv(g.K, kTileK)), dim3(256), 0,
@@ -283,7 +283,7 @@ extern "C" int concord_conv_col2im(const uint16_t* dcols, int64_t B, int64_t C, 
   CONCORD_CHECK(T.cc > 0, "concord_conv_col2im: kernel window too large for the staged tile");
   if (B == 0) return CONCORD_OK;
   const int64_t gy = B * ((H + kC2iH - 1) / kC2iH);
-  CONCORD_CHECK(gy < 65536 && cdiv(C, T.cc) < 65536 && cdiv(W, kC2iW) < ((int64_t)1 << 31),
+  CONCORD_CHECK(gy <= kMaxGridY && cdiv(C, T.cc) <= kMaxGridY && cdiv(W, kC2iW) < ((int64_t)1 << 31),
                 "concord_conv_col2im: grid too large (batch x rows / 4 must stay below 65536)");
   const size_t lds = (size_t)T.nho * T.nwo * T.ld * 2;
   hipLaunchKernelGGL(col2im_kernel, dim3((unsigned)cdiv(W, kC2iW), (unsigned)gy, (unsigned)cdiv(C, T.cc)),

@@ -10,7 +10,8 @@
 namespace concord {
 
 // A lane decodes 8 consecutive words (two 16 B loads, one 16 B store); a
-// block of 256 lanes covers 2048 columns of one row (grid.y = rows).
+// block of 256 lanes covers 2048 columns of rows blockIdx.y, blockIdx.y +
+// gridDim.y, ...
 template <bool CONSOLIDATED, bool VEC>
 __global__ __launch_bounds__(256) void materialize_kernel(const int32_t* __restrict__ packed,
                                                           int64_t ld_p, const int8_t* row_exp,
@@ -18,48 +19,50 @@ __global__ __launch_bounds__(256) void materialize_kernel(const int32_t* __restr
                                                           int64_t K, int32_t bias,
                                                           uint16_t* __restrict__ out,
                                                           int64_t ld_o) {
-  const int64_t n = blockIdx.y;
   const int64_t k0 = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
   if (k0 >= K) return;
-  const int32_t te_row = (int32_t)row_exp[n] - bias;
-  const int32_t* src = packed + n * ld_p + k0;
-  uint16_t* dst = out + n * ld_o + k0;
-  auto decode = [&](int32_t w, int64_t k) -> float {
-    const Fields f = unpack(w);
-    const int32_t m = CONSOLIDATED ? (f.ss + f.vs) * 128 : f.ss * 128 + f.sf + f.vs * 128;
-    return __fmul_rn((float)m, exp2i(te_row + (int32_t)col_exp[k]));
-  };
-  if (VEC && k0 + 8 <= K) {
-    const int4 a = *reinterpret_cast<const int4*>(src);
-    const int4 b = *reinterpret_cast<const int4*>(src + 4);
-    uint4 o;
-    o.x = pack_bf16x2(decode(a.x, k0 + 0), decode(a.y, k0 + 1));
-    o.y = pack_bf16x2(decode(a.z, k0 + 2), decode(a.w, k0 + 3));
-    o.z = pack_bf16x2(decode(b.x, k0 + 4), decode(b.y, k0 + 5));
-    o.w = pack_bf16x2(decode(b.z, k0 + 6), decode(b.w, k0 + 7));
-    *reinterpret_cast<uint4*>(dst) = o;
-  } else {
-    for (int j = 0; j < 8 && k0 + j < K; ++j)
-      dst[j] = (uint16_t)(pack_bf16x2(decode(src[j], k0 + j), 0.0f) & 0xFFFFu);
+  for (int64_t n = blockIdx.y; n < N; n += gridDim.y) {
+    const int32_t te_row = (int32_t)row_exp[n] - bias;
+    const int32_t* src = packed + n * ld_p + k0;
+    uint16_t* dst = out + n * ld_o + k0;
+    auto decode = [&](int32_t w, int64_t k) -> float {
+      const Fields f = unpack(w);
+      const int32_t m = CONSOLIDATED ? (f.ss + f.vs) * 128 : f.ss * 128 + f.sf + f.vs * 128;
+      return __fmul_rn((float)m, exp2i(te_row + (int32_t)col_exp[k]));
+    };
+    if (VEC && k0 + 8 <= K) {
+      const int4 a = *reinterpret_cast<const int4*>(src);
+      const int4 b = *reinterpret_cast<const int4*>(src + 4);
+      uint4 o;
+      o.x = pack_bf16x2(decode(a.x, k0 + 0), decode(a.y, k0 + 1));
+      o.y = pack_bf16x2(decode(a.z, k0 + 2), decode(a.w, k0 + 3));
+      o.z = pack_bf16x2(decode(b.x, k0 + 4), decode(b.y, k0 + 5));
+      o.w = pack_bf16x2(decode(b.z, k0 + 6), decode(b.w, k0 + 7));
+      *reinterpret_cast<uint4*>(dst) = o;
+    } else {
+      for (int j = 0; j < 8 && k0 + j < K; ++j)
+        dst[j] = (uint16_t)(pack_bf16x2(decode(src[j], k0 + j), 0.0f) & 0xFFFFu);
+    }
   }
 }
 
 // The forward weight with s_fast smoothly gated out (concord/packed_b.py:1763-1772):
 // bf16(((128 ss + g sf) + 128 vs) * 2^(row_exp + col_exp - bias)), fp32 ops in
-// that order.  One lane per word.
+// that order.  One lane per word; rows strided by gridDim.y.
 __global__ __launch_bounds__(256) void materialize_gated_kernel(const int32_t* __restrict__ packed,
                                                                 int64_t ld_p, const int8_t* row_exp,
                                                                 const int8_t* col_exp, int64_t N,
                                                                 int64_t K, int32_t bias, float g,
                                                                 uint16_t* __restrict__ out,
                                                                 int64_t ld_o) {
-  const int64_t n = blockIdx.y;
   const int64_t k = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (k >= K) return;
-  const Fields f = unpack(packed[n * ld_p + k]);
-  const float m = __fadd_rn(__fadd_rn((float)(f.ss * 128), __fmul_rn(g, (float)f.sf)), (float)(f.vs * 128));
-  const float v = __fmul_rn(m, exp2i((int32_t)row_exp[n] - bias + (int32_t)col_exp[k]));
-  out[n * ld_o + k] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+  for (int64_t n = blockIdx.y; n < N; n += gridDim.y) {
+    const Fields f = unpack(packed[n * ld_p + k]);
+    const float m = __fadd_rn(__fadd_rn((float)(f.ss * 128), __fmul_rn(g, (float)f.sf)), (float)(f.vs * 128));
+    const float v = __fmul_rn(m, exp2i((int32_t)row_exp[n] - bias + (int32_t)col_exp[k]));
+    out[n * ld_o + k] = (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+  }
 }
 
 // One block per row: row max |W| (exact), exponent, then quantise the row.
@@ -124,7 +127,7 @@ extern "C" int concord_materialize(const int32_t* packed, int64_t ld_p, const in
   CONCORD_CHECK(ld_p >= K && ld_out >= K, "concord_materialize: leading dimension < K");
   const bool vec = (ld_p % 4 == 0) && (ld_out % 8 == 0) && ((uintptr_t)packed % 16 == 0) &&
                    ((uintptr_t)out % 16 == 0);
-  dim3 grid((unsigned)cdiv(K, 2048), (unsigned)N);
+  dim3 grid((unsigned)cdiv(K, 2048), grid_y(N));
   hipStream_t st = (hipStream_t)stream;
 #define LAUNCH(C, V)                                                                       \
   hipLaunchKernelGGL((materialize_kernel<C, V>), grid, dim3(256), 0, st, packed, ld_p, row_exp, \
@@ -146,7 +149,7 @@ extern "C" int concord_materialize_gated(const int32_t* packed, int64_t ld_p, co
   if (N == 0 || K == 0) return CONCORD_OK;
   CONCORD_CHECK(packed && row_exp && col_exp && out, "concord_materialize_gated: NULL argument");
   CONCORD_CHECK(ld_p >= K && ld_out >= K, "concord_materialize_gated: leading dimension < K");
-  hipLaunchKernelGGL(materialize_gated_kernel, dim3((unsigned)cdiv(K, 256), (unsigned)N), dim3(256), 0,
+  hipLaunchKernelGGL(materialize_gated_kernel, dim3((unsigned)cdiv(K, 256), grid_y(N)), dim3(256), 0,
                      (hipStream_t)stream, packed, ld_p, row_exp, col_exp, N, K, mantissa_bias, fast_gain, out,
                      ld_out);
   return launch_status("materialize_gated");

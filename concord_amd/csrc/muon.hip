@@ -8,7 +8,8 @@
 //   ||g||^2  blocks of 8192 elements of the row-major flattening; lane t of a
 //            block sums elements t, t + 256, ... ascending, then the halving
 //            tree over 256 lanes; block totals ascending.  norm = sqrt (RN).
-//   X0 = bf16(g / (norm + 1e-7)), transposed when N > K (X is m x n, m <= n)
+//   X0 = bf16(g / (max(norm, 1e-12) * fl(1 + 1e-7))), transposed when N > K
+//   (X is m x n, m <= n)
 //   5 x:  A = bf16(X X^T); AA = bf16(A A); B = bf16(b A + c AA);
 //         BX = bf16(B X); X = bf16(a X + BX)      (products: bf16 MFMA, fp32 acc)
 //   out = bf16(gamma X), transposed back.
@@ -51,7 +52,10 @@ __global__ __launch_bounds__(256) void frob_partials_kernel(const uint16_t* __re
   if (threadIdx.x == 0) part[blockIdx.x] = s[0];
 }
 
-// den = sqrt(sum of the block partials ascending) + 1e-7.  One wave: 16 x 64
+// den = max(sqrt(sum of the block partials ascending), 1e-12) * fl(1 + 1e-7):
+// the drive normalises g by max(||g||, 1e-12) and ns5 then divides the unit
+// matrix by (its norm + 1e-7) (exp9_muon.py:75, 82, 47), one fp32 product
+// here.  One wave: 16 x 64
 // partials are loaded at a time, then chained in ascending order by reading
 // one lane after another (every lane carries the same running sum).
 __global__ __launch_bounds__(64) void frob_den_kernel(const float* __restrict__ part, int64_t nb, float* den) {
@@ -76,7 +80,7 @@ __global__ __launch_bounds__(64) void frob_den_kernel(const float* __restrict__ 
       }
     }
   }
-  if (lane == 0) *den = __fadd_rn(sqrt_rn(s), 1e-7f);
+  if (lane == 0) *den = __fmul_rn(fmaxf(sqrt_rn(s), 1e-12f), 1.00000011920928955078125f);
 }
 
 // dst[r][c] = bf16(op(src)) over a 64 x 64 tile, where the destination is
@@ -179,6 +183,9 @@ extern "C" int concord_muon_ns5(const uint16_t* g, int64_t ld_g, int64_t N, int6
                 "concord_muon_ns5: bad size N=%lld K=%lld", (long long)N, (long long)K);
   CONCORD_CHECK(g && out, "concord_muon_ns5: NULL argument");
   CONCORD_CHECK(ld_g >= K && ld_out >= K, "concord_muon_ns5: leading dimension < K");
+  CONCORD_CHECK(cdiv(N, 64) <= kMaxGridY && cdiv(K, 64) <= kMaxGridY,
+                "concord_muon_ns5: N=%lld K=%lld exceed the transpose kernel's grid (at most %lld per side)",
+                (long long)N, (long long)K, (long long)(kMaxGridY * 64));
   const MuonLayout L = muon_layout(N, K);
   if (!workspace || workspace_bytes < L.total) {
     set_error("concord_muon_ns5: workspace of %zu bytes needed", L.total);

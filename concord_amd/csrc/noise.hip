@@ -290,7 +290,7 @@ extern "C" int concord_sigmag_noise(uint16_t* grad_w, int64_t ld_g, const uint16
   if (M > 0) {
     hipLaunchKernelGGL(token_sum_partials_kernel, dim3((unsigned)tb), dim3(256), 0, st, M, salt_counter, tpart,
                        eps);
-    hipLaunchKernelGGL(token_scale_kernel, dim3((unsigned)cdiv(N, 2048), (unsigned)std::min<int64_t>(M, 65535)),
+    hipLaunchKernelGGL(token_scale_kernel, dim3((unsigned)cdiv(N, 2048), grid_y(M)),
                        dim3(256), 0, st, dy, ld_dy, M, N, eps, dyt);
   }
   hipLaunchKernelGGL(token_sum_final_kernel, dim3(1), dim3(64), 0, st, tpart, tb, ssum);

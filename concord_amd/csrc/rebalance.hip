@@ -202,6 +202,9 @@ extern "C" int concord_rebalance(int32_t* packed, int64_t ld_p, int8_t* row_exp,
   CONCORD_CHECK(packed && row_exp && col_exp && row_max && col_max && seed,
                 "concord_rebalance: NULL argument");
   CONCORD_CHECK(ld_p >= K, "concord_rebalance: leading dimension < K");
+  CONCORD_CHECK(cdiv(N, 32) <= kMaxGridY,
+                "concord_rebalance: N=%lld rows exceed the shift kernel's grid (at most %lld rows)",
+                (long long)N, (long long)(kMaxGridY * 32));
   const Workspace ws = workspace_layout(N, K, 0);
   if (!workspace || workspace_bytes < ws.total) {
     set_error("concord_rebalance: workspace of %zu bytes needed", ws.total);

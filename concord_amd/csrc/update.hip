@@ -218,7 +218,6 @@ __global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t kb = (int64_t)blockIdx.x * 256;
   const int64_t k0 = kb + lane * 4;
-  const int64_t nb = (int64_t)blockIdx.y * a.tn;
   Uniform U;
   U.lr = *a.s.lr;
   U.eps = *a.s.eps;
@@ -244,6 +243,8 @@ __global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
     vc[j] = ok ? a.v_col[k0 + j] : 0.0f;
     cmax[j] = 0;
   }
+  // row blocks blockIdx.y, blockIdx.y + gridDim.y, ... (grid.y <= kMaxGridY)
+  for (int64_t nb = (int64_t)blockIdx.y * a.tn; nb < a.N; nb += (int64_t)gridDim.y * a.tn)
   for (int r = wave; r < a.tn; r += 4) {
     const int64_t n = nb + r;
     if (n >= a.N) break;
@@ -351,7 +352,6 @@ __global__ __launch_bounds__(256) void apply_adamw_kernel(AdamwArgs a) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t kb = (int64_t)blockIdx.x * (64 * VEC);
   const int64_t k0 = kb + lane * VEC;
-  const int64_t nb = (int64_t)blockIdx.y * a.tn;
   const uint32_t flags = a.flags;
 
   Uniform U;
@@ -384,6 +384,8 @@ __global__ __launch_bounds__(256) void apply_adamw_kernel(AdamwArgs a) {
   }
   const bool full = k0 + VEC <= a.K;
 
+  // row blocks blockIdx.y, blockIdx.y + gridDim.y, ... (grid.y <= kMaxGridY)
+  for (int64_t nb = (int64_t)blockIdx.y * a.tn; nb < a.N; nb += (int64_t)gridDim.y * a.tn)
   for (int r = wave; r < a.tn; r += 4) {
     const int64_t n = nb + r;
     if (n >= a.N) break;
@@ -491,7 +493,6 @@ __global__ __launch_bounds__(256) void apply_sgd_kernel(SgdArgs a) {
   __shared__ int32_t s_cmax[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t k = (int64_t)blockIdx.x * 64 + lane;
-  const int64_t nb = (int64_t)blockIdx.y * a.tn;
   const float lr = *a.lr;
   const int32_t salt = *a.salt;
   const bool track = a.flags & CONCORD_TRACK_REBALANCE;
@@ -499,6 +500,8 @@ __global__ __launch_bounds__(256) void apply_sgd_kernel(SgdArgs a) {
   const bool kok = k < a.K;
   const int32_t ce = kok ? (int32_t)a.col_exp[k] : 0;
   int32_t cmax = 0;
+  // row blocks blockIdx.y, blockIdx.y + gridDim.y, ... (grid.y <= kMaxGridY)
+  for (int64_t nb = (int64_t)blockIdx.y * a.tn; nb < a.N; nb += (int64_t)gridDim.y * a.tn)
   for (int r = wave; r < a.tn; r += 4) {
     const int64_t n = nb + r;
     if (n >= a.N) break;
@@ -615,7 +618,7 @@ extern "C" int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t
   if (vec4) {
     const int64_t cb = cdiv(K, 256);
     a.tn = choose_tn(N, cb);
-    const dim3 grid(cb, cdiv(N, a.tn));
+    const dim3 grid((unsigned)cb, grid_y(cdiv(N, a.tn)));
     switch (fast_path(*params, flags)) {
       case 2: hipLaunchKernelGGL(apply_adamw_fast_kernel<true>, grid, dim3(256), 0, st, a); break;
       case 1: hipLaunchKernelGGL(apply_adamw_fast_kernel<false>, grid, dim3(256), 0, st, a); break;
@@ -624,7 +627,7 @@ extern "C" int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t
   } else {
     const int64_t cb = cdiv(K, 64);
     a.tn = choose_tn(N, cb);
-    hipLaunchKernelGGL(apply_adamw_kernel<1>, dim3(cb, cdiv(N, a.tn)), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(apply_adamw_kernel<1>, dim3((unsigned)cb, grid_y(cdiv(N, a.tn))), dim3(256), 0, st, a);
   }
   return launch_status("apply_adamw");
 }
@@ -656,6 +659,6 @@ extern "C" int concord_apply_sgd(int32_t* packed, int64_t ld_p, const uint16_t* 
   a.flags = flags;
   const int64_t cb = cdiv(K, 64);
   a.tn = choose_tn(N, cb);
-  hipLaunchKernelGGL(apply_sgd_kernel, dim3(cb, cdiv(N, a.tn)), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(apply_sgd_kernel, dim3((unsigned)cb, grid_y(cdiv(N, a.tn))), dim3(256), 0, st, a);
   return launch_status("apply_sgd");
 }

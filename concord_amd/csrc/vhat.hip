@@ -214,9 +214,11 @@ __global__ __launch_bounds__(256) void colsum_partials_kernel(const uint16_t* __
                                                               float* __restrict__ part) {
   const int64_t n = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
   if (n >= N) return;
-  const int64_t m0 = (int64_t)blockIdx.y * BG_ROWS;
-  const int64_t m1 = min(M, m0 + BG_ROWS);
   const bool vec = (n + 4 <= N) && (ld % 4 == 0) && (((uintptr_t)dy % 8) == 0);
+  // slabs blockIdx.y, blockIdx.y + gridDim.y, ... (grid.y <= kMaxGridY)
+  for (int64_t slab = blockIdx.y; slab * BG_ROWS < M; slab += gridDim.y) {
+  const int64_t m0 = slab * BG_ROWS;
+  const int64_t m1 = min(M, m0 + BG_ROWS);
   float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   if (vec) {
     int64_t m = m0;
@@ -247,7 +249,8 @@ __global__ __launch_bounds__(256) void colsum_partials_kernel(const uint16_t* __
   }
 #pragma unroll
   for (int c = 0; c < 4; ++c)
-    if (n + c < N) part[(int64_t)blockIdx.y * N + n + c] = s[c];
+    if (n + c < N) part[slab * N + n + c] = s[c];
+  }
 }
 
 __global__ __launch_bounds__(256) void colsum_finalize_kernel(const float* __restrict__ part,
@@ -263,7 +266,7 @@ void bias_grad_launch(const uint16_t* dy, int64_t ld, int64_t M, int64_t N, uint
                       hipStream_t st) {
   const int64_t slabs = cdiv(M, BG_ROWS);  // 0 when M == 0: the combine writes zeros
   if (slabs > 0)
-    hipLaunchKernelGGL(colsum_partials_kernel, dim3((unsigned)cdiv(N, 1024), (unsigned)slabs), dim3(256), 0,
+    hipLaunchKernelGGL(colsum_partials_kernel, dim3((unsigned)cdiv(N, 1024), grid_y(slabs)), dim3(256), 0,
                        st, dy, ld, M, N, part);
   hipLaunchKernelGGL(colsum_finalize_kernel, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, part, slabs, N,
                      grad_bias);

@@ -655,7 +655,15 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
         grad_bias = None
         muon = ctx.drive == 'muon' and ctx.optimizer_kind == 'adamw'
         vhat = ctx.track_adafactor_v and ctx.v_row is not None
-        if _SIGMAG_NOISE:
+        if _SIGMAG_NOISE and muon:
+            # the Muon drive's fluctuation is post-NS and isotropic,
+            # O <- O + sigma ||O|| xi / ||xi|| (docs/MUON_IMPLEMENTATION.md:21,
+            # 64-66): NS5 of the clean gradient, then the draw scaled to O
+            grad_x = _gemm_dgrad(dy, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias,
+                                 ctx.weight_buf).reshape(*ctx.lead, K)
+            grad_W = muon_ns5(_wgrad(dy, x2))
+            iso_noise_(grad_W, salt_counter=salt)
+        elif _SIGMAG_NOISE:
             # noise enters grad_W before the v-hat EMA and the update
             # (prototype_packed_b.py:1484-1501): the products in turn, the
             # injection, then the standalone v-hat entry
@@ -666,9 +674,7 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
                 iso_noise_(grad_W, salt_counter=salt)
             else:
                 sigmag_noise_(grad_W, dy, x2, salt_counter=salt)
-            if muon:
-                grad_W = muon_ns5(grad_W)
-            elif vhat:
+            if vhat:
                 vhat_ema(grad_W, ctx.v_row, ctx.v_col, ctx.sum_v_inv, ctx.adafactor_beta2,
                          ctx.row_max_buf if ctx.track_rebalance else None,
                          ctx.col_max_buf if ctx.track_rebalance else None, salt)
@@ -971,6 +977,25 @@ class ConcordLinearPackedB(nn.Module):
         self._eps_value = float(self._eps_buf.item())
         self._resync_weight_buf()
 
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        """A state_dict without the extra-state entry (the reference class
+        writes none: its keys are the registered buffers of
+        concord/packed_b.py:1445-1492) loads under strict=True too: the salt
+        counter and coh_pre keep their current values, lr / eps follow the
+        loaded device scalars."""
+        key = prefix + '_extra_state'
+        absent = key not in state_dict
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
+        if absent:
+            while key in missing_keys:
+                missing_keys.remove(key)
+            if getattr(self, '_lr_buf', None) is not None and self._lr_buf.numel() == 1:
+                self._lr_value = float(self._lr_buf.item())
+                self._eps_value = float(self._eps_buf.item())
+            self._resync_weight_buf()
+
     @torch.no_grad()
     def get_state(self):
         p = self.packed_w
@@ -1079,7 +1104,9 @@ def set_sigmag_noise(enabled, isotropic=False):
     """Turn the gradient-noise injection on or off (a Python switch: a
     captured graph keeps the choice made at capture, as in the reference).
     Default: the centred Sigma_g-shaped draw (eps * dy)^T x - (sum eps) g / M;
-    isotropic=True: white noise.  Either is scaled to sigma ||grad_W||."""
+    isotropic=True: white noise.  Either is scaled to sigma ||grad_W||.
+    Layers with drive='muon' always take the isotropic draw after NS5,
+    scaled to sigma ||O|| (docs/MUON_IMPLEMENTATION.md:21, 64-66)."""
     global _SIGMAG_NOISE, _SIGMAG_ISO
     _SIGMAG_NOISE = bool(enabled)
     _SIGMAG_ISO = bool(isotropic)
@@ -1381,6 +1408,14 @@ class GatedRebalance:
             self.fires += 1
             return True
         return False
+
+
+def reference_state_dict(module):
+    """module.state_dict() without this build's '_extra_state' entries: the
+    key set of the reference classes (their registered buffers and bias,
+    concord/packed_b.py:1445-1492), loadable into them with strict=True."""
+    return {k: v for k, v in module.state_dict().items()
+            if not (k == '_extra_state' or k.endswith('._extra_state'))}
 
 
 @torch.no_grad()

@@ -658,7 +658,8 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
  *     in a block, lane t (0..255) sums elements t, t+256, ... (32 of them)
  *     ascending from 0.0f, then the halving tree over the 256 lane sums;
  *     block totals ascending from 0.0f.  norm = sqrtf(sum).
- *   X0 = bf16(g / (norm + 1e-7)), transposed when N > K so X is m x n, m <= n.
+ *   X0 = bf16(g / (max(norm, 1e-12) * fl(1 + 1e-7))), transposed when N > K so
+ *   X is m x n, m <= n.
  *   per iteration (a, b, c = 3.4445, -4.7750, 2.0315):
  *     A = bf16(X X^T), AA = bf16(A A), B = bf16(b A + c AA), BX = bf16(B X),
  *     X = bf16(a X + BX); the products accumulate in fp32 over ascending r.
@@ -888,7 +889,9 @@ void oracle_muon_ns5(const uint16_t* g, int64_t N, int64_t K, float gamma, uint1
     const int tr = N > K;
     const int64_t m = tr ? K : N, n = tr ? N : K;
     const float norm = sqrtf(oracle_frob_sumsq(g, N, K));
-    const float den = norm + 1e-7f;
+    /* g / max(||g||, 1e-12), then / (||unit|| + 1e-7) with ||unit|| = 1:
+     * exp9_muon.py:75, 82 (drive) and 47 (ns5), one fp32 product */
+    const float den = fmaxf(norm, 1e-12f) * 1.00000011920928955078125f;
     float* X = (float*)malloc((size_t)(m * n) * sizeof(float));
     float* BX = (float*)malloc((size_t)(m * n) * sizeof(float));
     float* A = (float*)malloc((size_t)(m * m) * sizeof(float));

@@ -8,7 +8,10 @@
 * config 2 - the char-level GPT stack of Concord linears trains on i.i.d.
   uniform synthetic tokens towards the unigram entropy ln 65;
 * config 4 - the full SDXL-sized set of linear and 1x1 weights held packed on
-  one GPU, one step per layer with rebalance(): finite outputs and state.
+  one GPU, one step per layer with rebalance(): finite outputs and state, and
+  one layer of each distinct shape bit-exact against the oracle;
+* config 5 - a 1280 x 5120 weight on the Muon drive for 100 steps: the first
+  steps bit-exact against the oracle fed the GPU's drive, then properties.
 """
 import math
 
@@ -122,11 +125,11 @@ def test_config2_gpt_stack_trains():
     every Linear (c_attn, c_proj, c_fc, mlp c_proj, lm_head), norms and
     embeddings on SGD momentum 0.9.  Tokens i.i.d. uniform over 65 from a
     seed: over the 200 steps the loss must fall from its initial value to
-    within 0.1 of the unigram entropy ln 65.  (Batch 16 here, not 64, to keep
-    the test short.)"""
+    within 0.1 of the unigram entropy ln 65.  Batch 64 (M = 16384 tokens per
+    Concord linear), as the configuration states."""
     import concord_amd as ca
     torch.manual_seed(0)
-    V, d, H, L, T, B = 65, 384, 6, 6, 256, 16
+    V, d, H, L, T, B = 65, 384, 6, 6, 256, 64
     mk = lambda i, o: ca.ConcordLinearPackedB(i, o, bias=False, device=DEV, lr=3e-3)  # noqa: E731
     wte = torch.nn.Embedding(V, d, device=DEV)
     wpe = torch.nn.Embedding(T, d, device=DEV)
@@ -175,15 +178,32 @@ SDXL_1X1 = [((1280, 2560), 2, 4096), ((1280, 1920), 1, 4096), ((640, 1920), 1, 1
             ((320, 640), 2, 65536), ((320, 960), 1, 65536), ((640, 320), 1, 16384)]
 
 
-def test_config4_full_sdxl_set_one_step():
+def _winner_oracle_params(O, layer):
+    return O.UpdateParams(alpha=0.1, beta1=0.0, weight_decay=0.0, step_cap=10.0, v_scale=0.0,
+                          precond_p=0.5, gf_consol=50.0, drift_cancel_C=layer.drift_cancel_C,
+                          alpha_v_fast=0.001, wd_sv=0.0, wd_sf=0.0, gf_trust_delta_sq=1.0,
+                          gate_gain=1.0, mantissa_bias=15)
+
+
+WINNER_FLAGS = ("MASS_PRESERVE", "APPLY_CHASE", "TRACK_REBALANCE", "GF_TRUST_REGION", "FIXED_COH",
+                "RATIO_COH", "GF_CONSOLIDATION")
+
+
+def test_config4_full_sdxl_set_one_step(oracle):
     """Config 4: the 754 Linear + 1x1 weights (2.25 B parameters, 9.0 GB
     packed) resident on one GPU; one synthetic fwd + bwd + fused update +
-    rebalance per layer (winner flags).  Checks that every layer keeps a
-    finite state and output; the per-step time is printed."""
+    rebalance per layer (winner flags).  Every layer keeps a finite state and
+    output, and the first layer of each of the 21 distinct shapes is checked
+    bit for bit against the oracle fed that layer's own bf16 gradient:
+    v-hat, packed words after the update, then the rebalanced words and
+    exponents, which must have ticked in some of them (the first step after
+    load_weights carries row maxima above MAX_M).  The per-step time is
+    printed."""
     import time
 
     import concord_amd as ca
     from concord_amd import packed_b as pb
+    O = oracle
     torch.manual_seed(4)
     layers, total = [], 0
     pb.set_ratio_coh(True)
@@ -206,24 +226,148 @@ def test_config4_full_sdxl_set_one_step():
             if key not in xs:
                 xs[key] = torch.randn(m, la.in_features, device=DEV).to(torch.bfloat16)
                 dys[key] = (torch.randn(m, la.out_features, device=DEV) * 1e-3).to(torch.bfloat16)
+        # the first layer of each distinct (shape, tokens): its pre-step state
+        sample, seen = {}, set()
+        for i, (la, m) in enumerate(layers):
+            key = (m, la.in_features, la.out_features)
+            if key not in seen:
+                seen.add(key)
+                sample[i] = [host(t).copy() for t in (la.packed_w, la.row_exp, la.col_exp, la.v_row, la.v_col)]
+        assert len(sample) == 21
         sync()
         t0 = time.perf_counter()
-        outs = []
-        for la, m in layers:
+        outs, grads, salts = [], {}, {}
+        for i, (la, m) in enumerate(layers):
             key = (m, la.in_features, la.out_features)
             x = xs[key].requires_grad_(True)
-            y = la(x)
-            y.backward(dys[key])
+            cap = None
+            if i in sample:
+                cap = []
+                salts[i] = int(host(pb._get_step_counter(DEV))[0]) + 1
+                pb._DEBUG_CAPTURE = cap
+            try:
+                y = la(x)
+                y.backward(dys[key])
+            finally:
+                pb._DEBUG_CAPTURE = None
+            if cap is not None:
+                grads[i] = cap[0]
             la.rebalance()
             x.grad = None
             la.bias.grad = None
             outs.append(y.detach()[:1].float().abs().max())
         sync()
         dt = time.perf_counter() - t0
-        print(f"config 4: {len(layers)} layers, {total / 1e9:.3f} B params, one step {dt * 1e3:.1f} ms")
+        print(f"config 4: {len(layers)} layers, {total / 1e9:.3f} B params, one step {dt * 1e3:.1f} ms "
+              f"(eager, with {len(sample)} gradient captures)")
         assert all(torch.isfinite(v).item() for v in outs)
         for la, _ in layers[::50]:
             w = la.get_weight().float()
             assert torch.isfinite(w).all().item()
+        flags = 0
+        for f in WINNER_FLAGS:
+            flags |= getattr(O, f)
+        ticked = 0
+        for i, (pk0, re0, ce0, vr0, vc0) in sample.items():
+            la = layers[i][0]
+            N, K = pk0.shape
+            gbits = host(grads[i])
+            vr, vc = vr0.copy(), vc0.copy()
+            svi = O.vhat_ema(gbits, vr, vc, 0.999)
+            np.testing.assert_array_equal(host(la.v_row), vr)
+            np.testing.assert_array_equal(host(la.v_col), vc)
+            pk, re, ce = pk0.copy(), re0.copy(), ce0.copy()
+            rm = np.zeros(N, np.int32)
+            cm = np.zeros(K, np.int32)
+            S = O.UpdateScalars(lr=5e-4, eps=1e-10, chase_floor=0.9, leak_floor=0.999, v_bc=1.0,
+                                salt=salts[i], consolidate=1)
+            O.apply_adamw(pk, gbits, None, re, ce, rm, cm, vr, vc, svi, None, _winner_oracle_params(O, la), S,
+                          flags)
+            O.rebalance(pk, re, ce, rm, cm, max_m=la.MAX_M, exp_max=la.EXP_MAX, exp_min=la.EXP_MIN, seed=1)
+            np.testing.assert_array_equal(host(la.packed_w), pk, err_msg=f"layer {i} {N}x{K}")
+            np.testing.assert_array_equal(host(la.row_exp), re)
+            np.testing.assert_array_equal(host(la.col_exp), ce)
+            ticked += int((re != re0).any() or (ce != ce0).any())
+        assert ticked >= 1, "no sampled layer's rebalance fired"
+    finally:
+        pb.set_ratio_coh(False)
+
+
+def test_config5_muon_drive_100_steps(oracle):
+    """Config 5: a 1280 x 5120 packed weight (out 1280, in 5120; NS5 runs on
+    the 1280 x 5120 gradient without a transpose) on the Muon drive for 100
+    steps.  Each step's gradient is g ~ N(0, 1e-3) from a seeded generator,
+    delivered through the layer's own backward (x = I of 5120 tokens and
+    dy = g^T, so dy^T x = g exactly in bf16); the layer forms O = sqrt(5120)
+    NS5(g / ||g||), the packed update takes O as its step (winner flags), and
+    rebalance() runs.  Steps 1-3: packed words and exponents bit-exact against
+    the oracle's update + rebalance fed the GPU's O.  Every step: the drive's
+    RMS lies in the quintic band (NS5 maps the singular values into about
+    [0.68, 1.14]), the live weight stays finite, and the salt counter and
+    rebalance seed advance by one each."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    O = oracle
+    N, K = 1280, 5120
+    torch.manual_seed(5)
+    layer = ca.ConcordLinearPackedB(K, N, bias=False, device=DEV, lr=1e-3, drive='muon')
+    pb.set_ratio_coh(True)
+    pb.set_ratio_coh_floors(0.9, 0.999)
+    try:
+        layer.disable_cohpre()
+        layer.gf_consol = 10.0
+        x = torch.eye(K, device=DEV, dtype=torch.bfloat16)
+        gen = torch.Generator(device="cpu").manual_seed(55)
+        salt = pb._get_step_counter(DEV)
+        flags = O.MUON
+        for f in WINNER_FLAGS:
+            flags |= getattr(O, f)
+        P = O.UpdateParams(alpha=0.1, beta1=0.0, weight_decay=0.0, step_cap=10.0, v_scale=0.0, precond_p=0.5,
+                           gf_consol=10.0, drift_cancel_C=layer.drift_cancel_C, alpha_v_fast=0.001, wd_sv=0.0,
+                           wd_sf=0.0, gf_trust_delta_sq=1.0, gate_gain=1.0, mantissa_bias=15)
+        rms = []
+        for step in range(100):
+            g = (torch.randn(N, K, generator=gen) * 1e-3).to(torch.bfloat16)
+            dy = g.t().contiguous().to(DEV)
+            s0 = int(host(salt)[0])
+            seed0 = int(host(layer._reb_seed)[0])
+            check = step < 3
+            if check:
+                pk0, re0, ce0 = (host(t).copy() for t in (layer.packed_w, layer.row_exp, layer.col_exp))
+            cap = []
+            pb._DEBUG_CAPTURE = cap
+            try:
+                layer(x.clone().requires_grad_(True)).backward(dy)
+            finally:
+                pb._DEBUG_CAPTURE = None
+            layer.rebalance()
+            sync()
+            drive = host(cap[0])
+            dv = O.bf16_bits_to_f32(drive).astype(np.float64)
+            rms.append(float(np.sqrt((dv * dv).mean())))
+            assert 0.6 < rms[-1] < 1.2, (step, rms[-1])
+            assert int(host(salt)[0]) == s0 + 1 and int(host(layer._reb_seed)[0]) == seed0 + 1
+            if check:
+                if step == 0:
+                    # the layer's product delivered g itself
+                    np.testing.assert_array_equal(host(pb._wgrad(dy, x)), host(g))
+                    X = dv / np.sqrt(K)
+                    sv = np.sqrt(np.clip(np.linalg.eigvalsh(X @ X.T), 0, None))
+                    assert sv.min() > 0.6 and sv.max() < 1.25, (sv.min(), sv.max())
+                rm = np.zeros(N, np.int32)
+                cm = np.zeros(K, np.int32)
+                S = O.UpdateScalars(lr=1e-3, eps=1e-10, chase_floor=0.9, leak_floor=0.999, v_bc=1.0,
+                                    salt=s0 + 1, consolidate=1)
+                z = np.float32(0.0)
+                O.apply_adamw(pk0, drive, None, re0, ce0, rm, cm, np.zeros(N, np.float32),
+                              np.zeros(K, np.float32), z, None, P, S, flags)
+                O.rebalance(pk0, re0, ce0, rm, cm, max_m=layer.MAX_M, exp_max=layer.EXP_MAX,
+                            exp_min=layer.EXP_MIN, seed=seed0 + 1)
+                np.testing.assert_array_equal(host(layer.packed_w), pk0, err_msg=f"step {step}")
+                np.testing.assert_array_equal(host(layer.row_exp), re0)
+                np.testing.assert_array_equal(host(layer.col_exp), ce0)
+            if step % 25 == 24:
+                assert torch.isfinite(layer.get_weight().float()).all().item()
+        print("config 5 drive RMS:", " ".join(f"{v:.3f}" for v in rms[::10]))
     finally:
         pb.set_ratio_coh(False)

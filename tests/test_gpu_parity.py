@@ -226,6 +226,50 @@ def test_apply_adamw_matches_oracle(oracle, name, N, K):
     assert (opk != packed).any()
 
 
+def test_tall_layer_beyond_grid_y(oracle):
+    """A layer of 65537 x 64 words: launches keep grid.y at most 65535 (the
+    materialize kernels stride their rows over it), and materialize and the
+    packed update stay bit-exact against the oracle on every row."""
+    from concord_amd import packed_b as pb
+    O = oracle
+    N, K = 65537, 64
+    rng = np.random.default_rng(65537)
+    packed, re, ce = rand_state(rng, N, K, exp=(-8, 7), col=(-2, 2))
+    pk, red, ced = dev(packed), dev(re), dev(ce)
+    for cons in (False, True):
+        w = torch.empty((N, K), dtype=torch.bfloat16, device=DEV)
+        pb.materialize_packed_bf16(pk, red, ced, w, consolidated=cons)
+        sync()
+        np.testing.assert_array_equal(host(w), O.materialize(packed, re, ce, consolidated=cons))
+    g = rand_grad_bits(rng, N, K)
+    vr = (rng.random(N) * 1e-3 + 1e-7).astype(np.float32)
+    vc = (rng.random(K) * 1e-3 + 1e-7).astype(np.float32)
+    svi = np.array([1.0 / vr.sum()], np.float32)
+    _set_salt(77)
+    pb.set_ratio_coh(True)
+    pb.set_ratio_coh_floors(0.9, 0.999)
+    rm = torch.zeros(N, dtype=torch.int32, device=DEV)
+    cm = torch.zeros(K, dtype=torch.int32, device=DEV)
+    pb.apply_packed_adamw(pk, dev(g), None, red, ced, rm, cm, lr=5e-4, eps=1e-10, gf_consol=50.0,
+                          v_scale=0.0, mass_preserve=True, v_row=dev(vr), v_col=dev(vc), sum_v_inv=dev(svi),
+                          gf_trust_delta_sq=1.0, coh_pre=None)
+    sync()
+    P = O.UpdateParams(alpha=0.1, beta1=0.0, weight_decay=0.0, step_cap=10.0, v_scale=0.0, precond_p=0.5,
+                       gf_consol=50.0, drift_cancel_C=0.018036072144288578, alpha_v_fast=0.001, wd_sv=0.0,
+                       wd_sf=0.0, gf_trust_delta_sq=1.0, gate_gain=1.0, mantissa_bias=15)
+    S = O.UpdateScalars(lr=5e-4, eps=1e-10, chase_floor=0.9, leak_floor=0.999, v_bc=1.0, salt=77,
+                        consolidate=1)
+    flags = (O.MASS_PRESERVE | O.APPLY_CHASE | O.TRACK_REBALANCE | O.GF_TRUST_REGION | O.FIXED_COH
+             | O.RATIO_COH | O.GF_CONSOLIDATION)
+    opk = packed.copy()
+    orm = np.zeros(N, np.int32)
+    ocm = np.zeros(K, np.int32)
+    O.apply_adamw(opk, g, None, re, ce, orm, ocm, vr, vc, float(svi[0]), None, P, S, flags)
+    np.testing.assert_array_equal(host(pk), opk)
+    np.testing.assert_array_equal(host(rm), orm)
+    np.testing.assert_array_equal(host(cm), ocm)
+
+
 def test_apply_adamw_extreme_values(oracle):
     """Overflowing ticks: saturating float->int, int32 wrap, int16/int8 clamps."""
     from concord_amd import packed_b as pb
@@ -827,9 +871,10 @@ def test_muon_ns5_fused_combines_match_two_step(oracle, N, K):
 
 @pytest.mark.parametrize("N,K", [(2048, 5120), (1280, 5120), (333, 1001)])
 def test_muon_frobenius_denominator_bit_exact(oracle, N, K):
-    """The NS5 input scale ||g|| + 1e-7 (block partials, then one wave chaining
-    them in ascending order) equals the oracle's bit for bit; read back from
-    the workspace (layout: X, BX, A, AA, partials, then the denominator)."""
+    """The NS5 input scale max(||g||, 1e-12) * fl(1 + 1e-7) (block partials,
+    then one wave chaining them in ascending order) equals the oracle's bit
+    for bit; read back from the workspace (layout: X, BX, A, AA, partials,
+    then the denominator)."""
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(N + K)
     g = oracle.f32_to_bf16_bits_array((rng.standard_normal((N, K)) * 1e-3).astype(np.float32))
@@ -841,7 +886,7 @@ def test_muon_frobenius_denominator_bit_exact(oracle, N, K):
     off = 2 * r256(m * n * 2) + 2 * r256(m * m * 2) + r256(-(-N * K // 8192) * 4)
     den = host(ws[off:off + 4].view(torch.float32))[0]
     s = oracle.frob_sumsq(g)
-    want = np.float32(np.sqrt(np.float32(s))) + np.float32(1e-7)
+    want = np.float32(max(np.float32(np.sqrt(np.float32(s))), np.float32(1e-12)) * np.float32(1.0 + 1e-7))
     assert den.view(np.uint32) == np.float32(want).view(np.uint32), (den, want)
 
 
@@ -1065,6 +1110,71 @@ def test_checkpoint_resume_bit_exact(cohpre):
         got.append(host(b._coh_pre))
     for u, v in zip(want, got):
         np.testing.assert_array_equal(u, v)
+
+
+# the reference class's state_dict keys: its registered buffers and the bias
+# parameter (concord/packed_b.py:1445-1492)
+REFERENCE_KEYS = ['_reb_seed', 'packed_w', 'row_exp', 'col_exp', 'v_row', 'v_col', '_sum_v_inv',
+                  '_row_max_hwm', '_col_max_hwm', '_lr_buf', '_eps_buf', 'bias']
+
+
+class _ReferenceShaped(torch.nn.Module):
+    """A module with exactly the reference class's buffers and parameter."""
+
+    def __init__(self, N, K, bias=True):
+        super().__init__()
+        z = lambda *s, dt=torch.float32: torch.zeros(*s, dtype=dt, device=DEV)  # noqa: E731
+        self.register_buffer('_reb_seed', z(1, dt=torch.int32))
+        self.register_buffer('packed_w', z(N, K, dt=torch.int32))
+        self.register_buffer('row_exp', z(N, dt=torch.int8))
+        self.register_buffer('col_exp', z(K, dt=torch.int8))
+        self.register_buffer('v_row', z(N))
+        self.register_buffer('v_col', z(K))
+        self.register_buffer('_sum_v_inv', z(1))
+        self.register_buffer('_row_max_hwm', z(N, dt=torch.int32))
+        self.register_buffer('_col_max_hwm', z(K, dt=torch.int32))
+        self.register_buffer('_lr_buf', z(1))
+        self.register_buffer('_eps_buf', z(1))
+        self.bias = torch.nn.Parameter(z(N, dt=torch.bfloat16)) if bias else None
+
+
+def test_state_dict_interchanges_with_reference_key_set():
+    """Checkpoints cross between this class and the reference's in both
+    directions under strict loading: a state_dict with only the reference's
+    keys loads here (the salt counter and coh_pre keep their values, lr / eps
+    follow the loaded device scalars), and reference_state_dict() strips the
+    extra-state entry so the result loads into a module with the
+    reference's buffers."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    torch.manual_seed(23)
+    a = ca.ConcordLinearPackedB(96, 64, bias=True, device=DEV, lr=2e-3)
+    x = torch.randn(128, 96, device=DEV).requires_grad_(True)
+    a(x).square().mean().backward()
+    a.rebalance()
+    a.lr = 7e-4
+    sd = ca.reference_state_dict(a)
+    assert sorted(sd) == sorted(REFERENCE_KEYS)
+    assert '_extra_state' in a.state_dict()
+    # this build -> the reference's key set
+    r = _ReferenceShaped(64, 96)
+    r.load_state_dict(sd, strict=True)
+    np.testing.assert_array_equal(host(r.packed_w), host(a.packed_w))
+    # the reference's key set -> this build
+    salt = pb._get_step_counter(DEV)
+    salt.fill_(555)
+    b = ca.ConcordLinearPackedB(96, 64, bias=True, device=DEV, lr=1e-1)
+    cp = b._coh_pre
+    res = b.load_state_dict(r.state_dict(), strict=True)
+    assert not res.missing_keys and not res.unexpected_keys
+    sync()
+    for k in REFERENCE_KEYS:
+        np.testing.assert_array_equal(host(getattr(b, k)), host(getattr(a, k)))
+    assert b.lr == pytest.approx(7e-4) and int(host(salt)[0]) == 555 and b._coh_pre is cp
+    # a checkpoint of this build still needs its extra state under strict
+    # loading only through the key it wrote: a foreign key still fails
+    with pytest.raises(RuntimeError):
+        b.load_state_dict(dict(sd, stray=torch.zeros(1)), strict=True)
 
 
 def test_consolidated_state_dict_matches_layers():
@@ -1301,6 +1411,49 @@ def test_layer_iso_noise_step(oracle):
     want = oracle.iso_noise(plain, 0.2, 900)
     np.testing.assert_array_equal(host(cap[0]).view(np.uint16), want)
     assert int(host(salt)[0]) == 901 and layer.bias.grad is not None
+
+
+def test_layer_muon_noise_is_post_ns(oracle):
+    """drive='muon' with the noise on: NS5 runs on the clean gradient and the
+    isotropic draw is added after it, scaled to sigma ||O||
+    (docs/MUON_IMPLEMENTATION.md:21, 64-66), whichever draw was selected.
+    The captured drive equals the oracle's injection applied to the GPU's
+    NS5 of the plain product; at sigma = 0 the step is bit-identical to the
+    step with the noise off."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    torch.manual_seed(17)
+    x = torch.randn(512, 256, device=DEV).to(torch.bfloat16)
+    gy = (torch.randn(512, 384, device=DEV) * 1e-2).to(torch.bfloat16)
+    salt = pb._get_step_counter(DEV)
+
+    def run(noise, sigma, isotropic=False):
+        torch.manual_seed(5)
+        layer = ca.ConcordLinearPackedB(256, 384, bias=False, device=DEV, lr=1e-3, drive='muon')
+        salt.fill_(700)
+        ca.set_sigmag_noise(noise, isotropic=isotropic)
+        ca.set_sigmag_sigma(sigma)
+        cap = []
+        pb._DEBUG_CAPTURE = cap
+        try:
+            layer(x.clone().requires_grad_(True)).backward(gy)
+        finally:
+            pb._DEBUG_CAPTURE = None
+            ca.set_sigmag_noise(False)
+            ca.set_sigmag_sigma(0.0)
+        sync()
+        return host(cap[0]).view(np.uint16), host(layer.packed_w)
+
+    clean = host(pb.muon_ns5(pb._wgrad(gy, x))).view(np.uint16)
+    for isotropic in (False, True):
+        drive, _ = run(True, 0.3, isotropic)
+        np.testing.assert_array_equal(drive, oracle.iso_noise(clean, 0.3, 700))
+    d_off, p_off = run(False, 0.0)
+    d_zero, p_zero = run(True, 0.0)
+    np.testing.assert_array_equal(d_off, clean)
+    np.testing.assert_array_equal(d_zero, clean)
+    np.testing.assert_array_equal(p_zero, p_off)
+    assert int(host(salt)[0]) == 701
 
 
 @pytest.mark.parametrize("M,N,K", [(512, 384, 256), (2048, 1280, 640), (77, 96, 40)])

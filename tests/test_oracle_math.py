@@ -326,6 +326,57 @@ def test_update_expectation_matches_real_valued_rule(oracle):
     assert (np.abs(mean[1] - (S - lk) / 128) / sem[1]).max() < 6.0
 
 
+def test_muon_update_expectation_matches_real_valued_rule(oracle):
+    """CONCORD_MUON: E over SR salts of the integer update == the tick of
+    MuonConcord.step (experiments/cpu_dynamics/exp9_muon.py:58-100), in
+    mantissa units, with the drive supplied as its step_:
+        u <- u - lr O 2^-(row_exp + col_exp - 15) - lr kappa (1 - coh) u.
+    No denominator and no clip (drive entries up to 40 pass whole: a clip
+    at the v-hat arm's 10, or a division by sqrt(v-hat + eps), fails), and
+    v-hat is never read (NaN v_row / v_col / sum_v_inv change nothing).
+    The chase and the leak downstream are the v-hat arm's, pinned above."""
+    O = oracle
+    rng = np.random.default_rng(19)
+    N, K = 8, 16
+    sf0 = rng.integers(-1500, 1500, (N, K))
+    ss0 = rng.integers(-50, 50, (N, K))
+    vs0 = rng.integers(-50, 50, (N, K))
+    packed = O.pack(sf0, ss0, vs0)
+    re = np.full(N, 2, np.int8)
+    ce = np.zeros(K, np.int8)
+    drive = np.clip(rng.standard_normal((N, K)) * 15.0, -40.0, 40.0).astype(np.float32)
+    drive[0, :4] = [40.0, -40.0, 25.0, -12.5]
+    d = O.f32_to_bf16_bits_array(drive)
+    v_row = np.full(N, 2e-6, np.float32)
+    v_col = np.full(K, 2e-6, np.float32)
+    svi = np.float32(1.0 / (N * 2e-6))
+    lr, kappa, C = 1e-4, 30.0, 0.018036072144288578
+    base = (O.MASS_PRESERVE | O.GF_TRUST_REGION | O.GF_CONSOLIDATION | O.RATIO_COH | O.FIXED_COH
+            | O.MUON)
+    u, S, A = sf0.astype(np.float64), 128.0 * ss0, 128.0 * vs0
+    mu = C * (S - A)
+    nse = u - mu
+    coh = mu * mu / (mu * mu + nse * nse + 1e-30)
+    Od = O.bf16_bits_to_f32(d).astype(np.float64)      # the update consumes bf16(O)
+    P = _params(O, alpha=0.1, alpha_v_fast=0.05, gf_consol=kappa, drift_cancel_C=C)
+    sc = dict(chase_floor=0.6, leak_floor=0.4)
+    mean, sem = _salt_mean(O, packed, d, re, ce, P, base, v_row, v_col, svi, lr=lr, **sc)
+    want = u - lr * Od * 2.0 ** 13 - lr * kappa * (1 - coh) * u
+    assert (np.abs(mean[0] - want) / sem[0]).max() < 6.0
+    np.testing.assert_array_equal(mean[1:], np.stack([ss0, vs0]))
+    # the clipped and the preconditioned drives are far outside that band
+    for wrong in (u - lr * np.clip(Od, -10, 10) * 2.0 ** 13 - lr * kappa * (1 - coh) * u,
+                  u - lr * Od / np.sqrt(v_row[0] * v_col[0] * svi + 1e-10) * 2.0 ** 13):
+        assert (np.abs(mean[0] - wrong) / sem[0]).max() > 50.0
+    nan = np.full(N, np.nan, np.float32), np.full(K, np.nan, np.float32)
+    flags = base | O.APPLY_CHASE | O.TRACK_REBALANCE
+    a = _apply(O, packed, d, re, ce, P, _scalars(O, lr=lr, salt=5, **sc), flags, v_row, v_col, svi)
+    b = _apply(O, packed, d, re, ce, P, _scalars(O, lr=lr, salt=5, **sc), flags, nan[0], nan[1],
+               float("nan"))
+    for x, y in zip(a, b):
+        np.testing.assert_array_equal(x, y)
+
+
 def test_sr_streams_are_xor_linked(oracle):
     """The property behind the stage-wise test above, shown directly:
     hash(x, pos, s) XOR hash(y, pos, s ^ c) is independent of the salt s."""
@@ -458,8 +509,11 @@ def test_load_weights_edges(oracle):
 
 
 def _ns5_float64(G):
-    """experiments/cpu_dynamics/exp9_muon.py:44-55 in float64 (no bf16 rounding)."""
+    """The Muon drive's orthogonalisation in float64 (no bf16 rounding):
+    g / max(||g||, 1e-12) (exp9_muon.py:75, 82), then ns5 of that unit
+    matrix (44-55), which divides by its norm + 1e-7 once more."""
     a, b, c = 3.4445, -4.7750, 2.0315
+    G = G / max(np.linalg.norm(G), 1e-12)
     X = G / (np.linalg.norm(G) + 1e-7)
     tr = X.shape[0] > X.shape[1]
     if tr:
@@ -488,7 +542,8 @@ def _ns5_bf16_numpy(oracle, G, gamma):
         return oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits_array(np.asarray(x, np.float32))).astype(np.float64)
     a, b, c = np.float32(3.4445), np.float32(-4.7750), np.float32(2.0315)
     norm = np.float32(np.sqrt(np.float32((G * G).sum())))
-    X = rb(G.astype(np.float32) / (norm + np.float32(1e-7)))
+    den = np.float32(max(norm, np.float32(1e-12)) * np.float32(1.0 + 1e-7))
+    X = rb(G.astype(np.float32) / den)
     tr = X.shape[0] > X.shape[1]
     if tr:
         X = X.T.copy()
@@ -519,6 +574,28 @@ def test_ns5_matches_independent_iterations(oracle, N, K):
     assert np.linalg.norm(got - em) / np.linalg.norm(em) < 1.5e-2
     ref = gamma * _ns5_float64(gd)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 4e-2
+
+
+def test_ns5_small_norm_input_is_normalised(oracle):
+    """A gradient of norm ~1e-7 still enters NS5 as a unit matrix: the drive
+    divides by max(||g||, 1e-12) before ns5 adds its 1e-7 (exp9_muon.py:75,
+    82, 47).  Dividing once by ||g|| + 1e-7 would halve the input here and
+    leave the five iterations short of the quintic's band."""
+    rng = np.random.default_rng(31)
+    N, K = 64, 192
+    g = rng.standard_normal((N, K))
+    g *= 1e-7 / np.linalg.norm(g)
+    gb = oracle.f32_to_bf16_bits_array(g.astype(np.float32))
+    gd = oracle.bf16_bits_to_f32(gb).astype(np.float64)
+    assert 0.9e-7 < np.linalg.norm(gd) < 1.1e-7
+    gamma = np.float32(np.sqrt(np.float32(K)))
+    got = oracle.bf16_bits_to_f32(oracle.muon_ns5(gb, gamma)).astype(np.float64)
+    ref = gamma * _ns5_float64(gd)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 4e-2
+    # and it is the same drive as for the same direction at unit scale
+    g1 = oracle.f32_to_bf16_bits_array((gd / np.linalg.norm(gd)).astype(np.float32))
+    one = oracle.bf16_bits_to_f32(oracle.muon_ns5(g1, gamma)).astype(np.float64)
+    assert np.linalg.norm(got - one) / np.linalg.norm(one) < 2e-2
 
 
 def test_ns5_singular_values_in_quintic_band(oracle):
