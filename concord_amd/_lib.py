@@ -59,6 +59,8 @@ _SIGS = {
     "concord_vhat_ema": (ctypes.c_int, [_P, _I, _I, _I, _D, _P, _P, _P, _P, _P, _P, _P, _Z, _P]),
     "concord_rebalance": (ctypes.c_int, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _i, _i, _i,
                                          ctypes.c_int, ctypes.c_int, _P, _Z, _P]),
+    "concord_rebalance_noalloc": (ctypes.c_int, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _i, _i, _i,
+                                                 ctypes.c_int, ctypes.c_int, _P]),
     "concord_load_weights": (ctypes.c_int, [_P, _I, _I, _I, _i, _i, _i, ctypes.c_int, _P, _I, _P,
                                             _P, _P]),
     "concord_gemm_workspace_bytes": (_Z, [_I, _I, _I]),

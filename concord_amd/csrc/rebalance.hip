@@ -14,6 +14,8 @@
 // The decisions of every tile come from the same pre-call exponents.  (In the
 // reference the tiles with pid_k == 0 store the new row exponents while other
 // tiles of the same launch may still be loading them.)
+#include <mutex>
+
 #include "common.h"
 #include "workspace.h"
 
@@ -189,6 +191,66 @@ __global__ __launch_bounds__(256) void rebalance_shift_kernel(int32_t* __restric
 
 }  // namespace concord
 
+namespace concord {
+
+// The launches of one rebalance call; `scr` holds 2 (N + K) + cdiv(N, 256) +
+// cdiv(K, 256) int32 of scratch (ticks, tick-down counts, decide-block flags).
+// Every word of it that a kernel reads is written earlier in the same call.
+static int rebalance_launch(int32_t* packed, int64_t ld_p, int8_t* row_exp, int8_t* col_exp,
+                            const int32_t* row_max, const int32_t* col_max, int32_t* row_hwm,
+                            int32_t* col_hwm, int32_t* seed, int64_t N, int64_t K, int32_t max_m,
+                            int32_t exp_max, int32_t exp_min, int allow_tickdown, int advance_seed,
+                            int32_t* scr, hipStream_t st) {
+  int32_t* row_t = scr;
+  int32_t* col_t = row_t + N;
+  int32_t* cnt_row = col_t + K;
+  int32_t* cnt_col = cnt_row + N;
+  int32_t* bfired = cnt_col + K;   // one flag per decide block
+  if (allow_tickdown) {
+    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)cdiv(N + K, 256)), dim3(256), 0, st, cnt_row,
+                       N + K, 0);
+    hipLaunchKernelGGL(i8_small_count_kernel, dim3((unsigned)cdiv(K, 256), (unsigned)cdiv(N, 32)),
+                       dim3(256), 0, st, packed, ld_p, N, K, cnt_row, cnt_col);
+  }
+  hipLaunchKernelGGL(rebalance_decide_kernel, dim3((unsigned)(cdiv(N, 256) + cdiv(K, 256))), dim3(256), 0, st,
+                     row_exp, col_exp, row_max, col_max, row_hwm, col_hwm, cnt_row, cnt_col, seed, N, K,
+                     max_m, exp_max, exp_min, allow_tickdown, advance_seed, row_t, col_t, bfired);
+  hipLaunchKernelGGL(rebalance_shift_kernel, dim3((unsigned)cdiv(K, 256), (unsigned)cdiv(N, 32)),
+                     dim3(256), 0, st, packed, ld_p, N, K, row_t, col_t, bfired, seed);
+  return launch_status("rebalance");
+}
+
+// Scratch of concord_rebalance_noalloc: a file-scope device array, one copy
+// per device, held until the process ends.  Host code uses the device
+// address hipGetSymbolAddress returns for it (per device), never the array's
+// name, which on the host is only a stand-in.
+constexpr int64_t kNoAllocMaxDim = 131072;   // rows and columns, each
+constexpr int64_t kNoAllocScratchWords = 4 * kNoAllocMaxDim + 2 * (kNoAllocMaxDim / 256);
+static __device__ __align__(256) int32_t scratch[kNoAllocScratchWords];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static int32_t* g_scratch_ptr[kMaxDevices];
+
+// the device address of `scratch` on device `dev`, looked up once per device
+// with that device current
+static int32_t* scratch_on(int dev) {
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("concord_rebalance_noalloc: hipGetSymbolAddress of the scratch array failed on device %d: %s",
+                dev, hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = (int32_t*)p;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace concord
+
 using namespace concord;
 
 extern "C" int concord_rebalance(int32_t* packed, int64_t ld_p, int8_t* row_exp, int8_t* col_exp,
@@ -210,23 +272,32 @@ extern "C" int concord_rebalance(int32_t* packed, int64_t ld_p, int8_t* row_exp,
     set_error("concord_rebalance: workspace of %zu bytes needed", ws.total);
     return CONCORD_EWORKSPACE;
   }
-  char* base = (char*)workspace;
-  int32_t* row_t = (int32_t*)(base + ws.scratch);
-  int32_t* col_t = row_t + N;
-  int32_t* cnt_row = col_t + K;
-  int32_t* cnt_col = cnt_row + N;
-  int32_t* bfired = cnt_col + K;   // one flag per decide block
+  return rebalance_launch(packed, ld_p, row_exp, col_exp, row_max, col_max, row_hwm, col_hwm, seed, N, K, max_m,
+                          exp_max, exp_min, allow_tickdown, advance_seed,
+                          (int32_t*)((char*)workspace + ws.scratch), (hipStream_t)stream);
+}
+
+extern "C" int concord_rebalance_noalloc(int32_t* packed, int64_t ld_p, int8_t* row_exp, int8_t* col_exp,
+                                         const int32_t* row_max, const int32_t* col_max, int32_t* row_hwm,
+                                         int32_t* col_hwm, int32_t* seed, int64_t N, int64_t K, int32_t max_m,
+                                         int32_t exp_max, int32_t exp_min, int allow_tickdown, int advance_seed,
+                                         void* stream) {
+  CONCORD_CHECK(N > 0 && K > 0, "concord_rebalance_noalloc: bad size");
+  CONCORD_CHECK(N <= kNoAllocMaxDim && K <= kNoAllocMaxDim,
+                "concord_rebalance_noalloc: N=%lld K=%lld exceed the static scratch (at most %lld rows and %lld "
+                "columns); use concord_rebalance with a workspace",
+                (long long)N, (long long)K, (long long)kNoAllocMaxDim, (long long)kNoAllocMaxDim);
+  CONCORD_CHECK(packed && row_exp && col_exp && row_max && col_max && seed,
+                "concord_rebalance_noalloc: NULL argument");
+  CONCORD_CHECK(ld_p >= K, "concord_rebalance_noalloc: leading dimension < K");
   hipStream_t st = (hipStream_t)stream;
-  if (allow_tickdown) {
-    hipLaunchKernelGGL(fill_i32_kernel, dim3((unsigned)cdiv(N + K, 256)), dim3(256), 0, st, cnt_row,
-                       N + K, 0);
-    hipLaunchKernelGGL(i8_small_count_kernel, dim3((unsigned)cdiv(K, 256), (unsigned)cdiv(N, 32)),
-                       dim3(256), 0, st, packed, ld_p, N, K, cnt_row, cnt_col);
-  }
-  hipLaunchKernelGGL(rebalance_decide_kernel, dim3((unsigned)(cdiv(N, 256) + cdiv(K, 256))), dim3(256), 0, st,
-                     row_exp, col_exp, row_max, col_max, row_hwm, col_hwm, cnt_row, cnt_col, seed, N, K,
-                     max_m, exp_max, exp_min, allow_tickdown, advance_seed, row_t, col_t, bfired);
-  hipLaunchKernelGGL(rebalance_shift_kernel, dim3((unsigned)cdiv(K, 256), (unsigned)cdiv(N, 32)),
-                     dim3(256), 0, st, packed, ld_p, N, K, row_t, col_t, bfired, seed);
-  return launch_status("rebalance");
+  int cur = -1, sdev = -1;
+  CONCORD_CHECK(hipGetDevice(&cur) == hipSuccess && hipStreamGetDevice(st, &sdev) == hipSuccess,
+                "concord_rebalance_noalloc: cannot query the current device or the stream's device");
+  CONCORD_CHECK(cur == sdev && cur >= 0 && cur < kMaxDevices,
+                "concord_rebalance_noalloc: the stream belongs to device %d, the current device is %d", sdev, cur);
+  int32_t* scr = scratch_on(cur);
+  if (scr == nullptr) return CONCORD_ELAUNCH;
+  return rebalance_launch(packed, ld_p, row_exp, col_exp, row_max, col_max, row_hwm, col_hwm, seed, N, K, max_m,
+                          exp_max, exp_min, allow_tickdown, advance_seed, scr, st);
 }

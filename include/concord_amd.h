@@ -150,6 +150,22 @@ int concord_rebalance(int32_t* packed, int64_t ld_p, int8_t* row_exp, int8_t* co
                       int32_t exp_max, int32_t exp_min, int allow_tickdown, int advance_seed,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* concord_rebalance without a workspace argument.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as concord_rebalance;
+ * its scratch is a static device array of 2.1 MB per device (held until the
+ * process ends), so N and K are each at most 131072 (larger layers get
+ * CONCORD_EINVAL; use concord_rebalance).  The stream must belong to the
+ * current device.  It calls no allocator.  Every call on one device shares
+ * that scratch: calls that overlap on one GPU (concurrent streams or host
+ * threads) race; calls in stream order do not. */
+int concord_rebalance_noalloc(int32_t* packed, int64_t ld_p, int8_t* row_exp, int8_t* col_exp,
+                              const int32_t* row_max, const int32_t* col_max, int32_t* row_hwm,
+                              int32_t* col_hwm, int32_t* seed, int64_t N, int64_t K, int32_t max_m,
+                              int32_t exp_max, int32_t exp_min, int allow_tickdown, int advance_seed,
+                              void* stream);
+
 /* load_weights / load_weights_finetune (concord/packed_b.py:1570-1603,
  * 1816-1856): fp32 W[N, ld_w] -> packed state, row_exp, col_exp = 0. */
 int concord_load_weights(const float* W, int64_t ld_w, int64_t N, int64_t K, int32_t exp_min,
