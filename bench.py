@@ -287,6 +287,108 @@ def _next_rows(layer, xb, dy, gw, reps, warmup, steps, torch, ca, pb):
     return out
 
 
+# config 4: SDXL-UNet Linear and 1x1 weights ((out, in), count, tokens M), per
+# notebook/src/sdxl_fit_smoketest.py:55-69 as tabulated for this build;
+# tokens per layer at batch 4 of a 128 x 128 latent, realistic per level:
+# 1280-channel layers at 32 x 32 (M 4096), 640-channel at 64 x 64 (M 16384),
+# 320-channel at 128 x 128 (M 65536), cross-attention k/v on 77 x 4 text
+# tokens (M 308), time/label embeddings on M 4
+SDXL_LINEAR = [((10240, 1280), 60, 4096), ((1280, 1280), 381, 4096), ((1280, 5120), 60, 4096),
+               ((1280, 2048), 120, 308), ((5120, 640), 10, 16384), ((640, 640), 70, 16384),
+               ((640, 2048), 20, 308), ((640, 2560), 10, 16384), ((640, 1280), 5, 4),
+               ((1280, 2816), 1, 4), ((320, 1280), 5, 4), ((1280, 320), 1, 4)]
+SDXL_1X1 = [((1280, 2560), 2, 4096), ((1280, 1920), 1, 4096), ((640, 1920), 1, 16384),
+            ((1280, 640), 1, 4096), ((640, 1280), 1, 16384), ((640, 960), 1, 16384),
+            ((320, 640), 2, 65536), ((320, 960), 1, 65536), ((640, 320), 1, 16384)]
+
+
+def _config4_step(steps, torch, ca, pb):
+    """Config 4: one training step over all 754 SDXL Linear and 1x1 weights
+    (2.25 B parameters held packed, 9.0 GB), each layer forward + backward
+    (dgrad, wgrad, v-hat, fused update; winner flags) on its own token count,
+    then GatedRebalance with the gate on the device.  The whole step is
+    captured in one HIP graph and replayed; 6 M N K FLOP per layer."""
+    dev = torch.device("cuda:0")
+    torch.manual_seed(4)
+    layers, flop, params = [], 0.0, 0
+    for table in (SDXL_LINEAR, SDXL_1X1):
+        for (n_out, n_in), count, m in table:
+            for _ in range(count):
+                lay = ca.ConcordLinearPackedB(n_in, n_out, bias=True, device=dev, lr=5e-4)
+                lay.disable_cohpre()
+                lay.gf_consol = 50.0
+                layers.append((lay, m))
+                flop += 6.0 * m * n_out * n_in
+                params += n_out * n_in
+    xs, dys = {}, {}
+    for la, m in layers:
+        key = (m, la.in_features, la.out_features)
+        if key not in xs:
+            xs[key] = torch.randn(m, la.in_features, device=dev).to(torch.bfloat16).requires_grad_(True)
+            dys[key] = (torch.randn(m, la.out_features, device=dev) * 1e-3).to(torch.bfloat16)
+    gate = ca.GatedRebalance([la for la, _ in layers])
+
+    def step():
+        for la, m in layers:
+            key = (m, la.in_features, la.out_features)
+            x = xs[key]
+            x.grad = None
+            la.bias.grad = None
+            la(x).backward(dys[key])
+        gate()
+
+    step()   # creates the watermark buffers; the gate wires its slabs
+    step()   # the gate builds its device plan
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    step()
+    torch.cuda.synchronize()
+    eager_ms = (time.perf_counter() - t0) * 1e3
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            step()
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(2, min(steps, 5))
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    fires = gate.fires
+    # the gate alone, no fire: watermarks zeroed, the device gate (two
+    # launches of the peak, two of the group rebalance) against the host
+    # gate (the peak, one host read, no rebalance launch)
+    gate.row_all.zero_()
+    gate.col_all.zero_()
+    t_dev = _event_time_ms(gate, 20, torch)
+    hg = ca.GatedRebalance([la for la, _ in layers], device_gate=False)
+    hg.row_all, hg.col_all, hg._peak = gate.row_all, gate.col_all, gate._peak
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(20):
+        hg()
+    torch.cuda.synchronize()
+    t_host = (time.perf_counter() - t0) * 1e3 / 20
+    a = flop / (ms * 1e-3) / 1e12
+    out = {"layers": len(layers), "params": params, "packed_GB": round(4 * params / 1e9, 2),
+           "flop_per_step": flop, "ms_per_step": round(ms, 3), "tflops": round(a, 1),
+           "frac": round(a / PEAK_BF16_TFLOPS, 4), "timing": f"one HIP graph per step, {reps} replays",
+           "eager_ms_per_step": round(eager_ms, 1), "gate_fires_in_run": fires,
+           "gate_nofire_us": {"device_gate": round(t_dev * 1e3, 1), "host_gate_with_item": round(t_host * 1e3, 1)}}
+    del g, layers, xs, dys, gate, hg
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 # config 3: SDXL-UNet linear shapes (out N, in K, tokens M) at their token
 # counts -- attention q/k/v/out, GEGLU in and out, the north-star shape, the
 # 640-channel set on 4096 x 2 tokens, cross-attention k/v on 77 x 2 tokens
@@ -395,6 +497,8 @@ def main():
     ap.add_argument("--no-next-rows", action="store_true",
                     help="skip the context timings of the rows beside the step (keeps a kernel profile to the "
                          "step's own shapes)")
+    ap.add_argument("--no-config4", action="store_true",
+                    help="skip the config-4 row (the graph-captured step over all 754 SDXL weights)")
     ap.add_argument("--only", default=None,
                     choices=["fwd", "bwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
                              "copy"])
@@ -525,6 +629,7 @@ def main():
     next_rows = {} if args.no_next_rows else _next_rows(layer, xb, dy, gw, reps, args.warmup, args.steps, torch,
                                                            ca, pb)
     sdxl_shapes = {} if args.no_next_rows else _config3_steps(args.warmup, args.steps, torch, ca)
+    config4 = None if args.no_config4 else _config4_step(args.steps, torch, ca, pb)
 
     # the reference's own dataflow on the same workload, for context: the
     # update emits the bf16 weight (materialize-merge) and the next step's
@@ -620,6 +725,9 @@ def main():
                           **next_rows),
         "sdxl_shapes": dict(note="the same step on each config-3 SDXL linear shape (out N, in K, tokens M); "
                                  "context only", **sdxl_shapes),
+        "config4_step": dict(note="config 4: one training step over the 754 SDXL Linear + 1x1 weights with "
+                                  "GatedRebalance (device gate), one HIP graph; context only",
+                             **(config4 or {})),
         "weight_cache_mode": {
             "note": "the reference's dataflow (update emits the bf16 weight; forward and dgrad are bf16 "
                     "GEMMs on it), same workload; context only",

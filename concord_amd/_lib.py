@@ -26,6 +26,11 @@ SALT_PREBUMPED = 1 << 16
 
 OK, EINVAL, ELAUNCH, EWORKSPACE = 0, -1, -2, -3
 
+# record layout of concord_rebalance_group_plan's layer table (int64 fields)
+RG_FIELDS = 16
+(RG_PACKED, RG_LD, RG_ROW_EXP, RG_COL_EXP, RG_ROW_MAX, RG_COL_MAX, RG_ROW_HWM, RG_COL_HWM, RG_SEED,
+ RG_N, RG_K, RG_MAX_M, RG_EXP_MAX, RG_EXP_MIN) = range(14)
+
 
 class UpdateParams(ctypes.Structure):
     _fields_ = [(n, ctypes.c_float) for n in (
@@ -61,6 +66,8 @@ _SIGS = {
                                          ctypes.c_int, ctypes.c_int, _P, _Z, _P]),
     "concord_rebalance_noalloc": (ctypes.c_int, [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _I, _i, _i, _i,
                                                  ctypes.c_int, ctypes.c_int, _P]),
+    "concord_rebalance_group_plan": (ctypes.c_int, [_P, _i, _P, _I, _P]),
+    "concord_rebalance_group": (ctypes.c_int, [_P, _i, _P, _i, _P, _P, _Z, _I, _P]),
     "concord_load_weights": (ctypes.c_int, [_P, _I, _I, _I, _i, _i, _i, ctypes.c_int, _P, _I, _P,
                                             _P, _P]),
     "concord_gemm_workspace_bytes": (_Z, [_I, _I, _I]),

@@ -1354,19 +1354,43 @@ class GatedRebalance:
     """Fire rebalance only when some layer's mantissa crosses MAX_M
     (notebook/src/concord_winner.py:206-262).  Every layer's row / column
     watermark buffers become slices of two shared slabs; one call is one HIP
-    reduction over both slabs (concord_watermark_peak) and one host read, and
-    the per-layer rebalance launches run only when the peak exceeds MAX_M.
+    reduction over both slabs (concord_watermark_peak) followed by the
+    rebalance of every layer when the peak exceeds MAX_M.
     Drop-in for `for m in layers: m.rebalance()`: call the instance after
-    backward.  Returns True when it fired."""
+    backward.
 
-    def __init__(self, layers):
+    device_gate=True (the default): the comparison is made on the device by
+    concord_rebalance_group, two launches over a plan of every layer, so a
+    call makes no host read and a training step that includes it can be
+    captured in one HIP graph; the call returns None and `fires` reads a
+    device counter.  Layers with allow_tickdown, or a rebalance statistics
+    hook, take the host-gated path.  The plan holds the device addresses of
+    each layer's state: after moving or replacing a layer's tensors the next
+    call rebuilds it (each eager call compares the addresses).
+    device_gate=False: one host read of the peak per call, and the call
+    returns True when it fired, as in the reference."""
+
+    def __init__(self, layers, device_gate=True):
         self.layers = [m for m in (layers or []) if hasattr(m, "rebalance")]
         self.MAX_M = max((getattr(m, "MAX_M", 24000) for m in self.layers), default=24000)
+        self.device_gate = bool(device_gate)
         self.row_all = None
         self.col_all = None
         self._peak = None
-        self.fires = 0
+        self._plan = None
+        self._plan_sig = None
+        self._plan_ws = None
+        self._plan_words = 0
+        self._fires_dev = None
+        self._host_fires = 0
         self.calls = 0
+
+    @property
+    def fires(self):
+        """Number of calls that fired (reads the device counter: one host
+        synchronisation)."""
+        dev = 0 if self._fires_dev is None else int(self._fires_dev.item())
+        return self._host_fires + dev
 
     def _wire(self):
         """Repoint the per-layer watermark buffers at slices of the shared
@@ -1377,6 +1401,7 @@ class GatedRebalance:
         self.row_all = torch.zeros(sum(rs), dtype=torch.int32, device=dev)
         self.col_all = torch.zeros(sum(cs), dtype=torch.int32, device=dev)
         self._peak = torch.zeros(1, dtype=torch.int32, device=dev)
+        self._fires_dev = torch.zeros(1, dtype=torch.int32, device=dev)
         ro = co = 0
         for m, n, k in zip(self.layers, rs, cs):
             m._row_max_buf = self.row_all[ro:ro + n]
@@ -1393,6 +1418,51 @@ class GatedRebalance:
             C.ptr(self._peak), C.ptr(ws), ws.numel(), C.stream_of(self.row_all.device)), "watermark_peak")
         return self._peak
 
+    def _group_tensors(self, m):
+        return (m.packed_w, m.row_exp, m.col_exp, m._row_max_buf, m._col_max_buf, m._row_max_hwm,
+                m._col_max_hwm, m._reb_seed)
+
+    def _use_group(self):
+        return (self.device_gate and _REB_STATS is None
+                and not any(getattr(m, "allow_tickdown", False) for m in self.layers))
+
+    def _ensure_plan(self):
+        """Build (or rebuild, when a layer's tensors moved) the device plan of
+        concord_rebalance_group."""
+        sig = tuple(0 if t is None else t.data_ptr() for m in self.layers for t in self._group_tensors(m))
+        if self._plan is not None and sig == self._plan_sig:
+            return
+        n = len(self.layers)
+        rec = (ctypes.c_int64 * (n * C.RG_FIELDS))()
+        for i, m in enumerate(self.layers):
+            pw, re, ce, rm, cm, rh, chw, seed = self._group_tensors(m)
+            N, K = _check_packed(pw, re, ce)
+            r = i * C.RG_FIELDS
+            rec[r + C.RG_PACKED] = pw.data_ptr()
+            rec[r + C.RG_LD] = pw.stride(0)
+            rec[r + C.RG_ROW_EXP] = re.data_ptr()
+            rec[r + C.RG_COL_EXP] = ce.data_ptr()
+            rec[r + C.RG_ROW_MAX] = rm.data_ptr()
+            rec[r + C.RG_COL_MAX] = cm.data_ptr()
+            rec[r + C.RG_ROW_HWM] = rh.data_ptr() if rh is not None else 0
+            rec[r + C.RG_COL_HWM] = chw.data_ptr() if chw is not None else 0
+            rec[r + C.RG_SEED] = seed.data_ptr()
+            rec[r + C.RG_N] = N
+            rec[r + C.RG_K] = K
+            rec[r + C.RG_MAX_M] = int(m.MAX_M)
+            rec[r + C.RG_EXP_MAX] = int(m.EXP_MAX)
+            rec[r + C.RG_EXP_MIN] = int(m.EXP_MIN)
+        plen = n * C.RG_FIELDS + 2 * (n + 1)
+        plan = (ctypes.c_int64 * plen)()
+        words = ctypes.c_int64(0)
+        C.check(C.lib().concord_rebalance_group_plan(rec, n, plan, plen, ctypes.byref(words)),
+                "rebalance_group_plan")
+        dev = self.layers[0].packed_w.device
+        self._plan = torch.tensor(list(plan), dtype=torch.int64).to(dev)
+        self._plan_words = int(words.value)
+        self._plan_ws = torch.empty(self._plan_words, dtype=torch.int32, device=dev)
+        self._plan_sig = sig
+
     def __call__(self):
         if not self.layers:
             return False
@@ -1402,10 +1472,18 @@ class GatedRebalance:
                 return False
             self._wire()
             return False
+        if self._use_group():
+            self._ensure_plan()
+            peak = self.peak()
+            C.check(C.lib().concord_rebalance_group(
+                C.ptr(self._plan), len(self.layers), C.ptr(peak), int(self.MAX_M), C.ptr(self._fires_dev),
+                C.ptr(self._plan_ws), self._plan_ws.numel() * 4, self._plan_words,
+                C.stream_of(peak.device)), "rebalance_group")
+            return None
         if int(self.peak().item()) > self.MAX_M:
             for m in self.layers:
                 m.rebalance()
-            self.fires += 1
+            self._host_fires += 1
             return True
         return False
 

@@ -166,6 +166,38 @@ int concord_rebalance_noalloc(int32_t* packed, int64_t ld_p, int8_t* row_exp, in
                               int32_t exp_max, int32_t exp_min, int allow_tickdown, int advance_seed,
                               void* stream);
 
+/* Gated rebalance of a group of layers: GatedRebalance.__call__
+ * (notebook/src/concord_winner.py:206-262), `if peak > MAX_M: for m in
+ * layers: m.rebalance()`, with the comparison made on the device.
+ *
+ * concord_rebalance_group_plan (host only, no GPU call): `layers` holds
+ * n_layers records of CONCORD_RG_FIELDS int64, indexed by CONCORD_RG_*:
+ * the device pointers and sizes of one layer's concord_rebalance call
+ * (packed, ld_p, row_exp, col_exp, row_max, col_max, row_hwm, col_hwm
+ * (either may be 0), seed, N, K, max_m, exp_max, exp_min; the last two
+ * fields are ignored).  Writes the plan (n_layers * CONCORD_RG_FIELDS +
+ * 2 (n_layers + 1) int64) and the int32 scratch words a call needs.  The
+ * plan is copied to device memory by the caller, once.
+ *
+ * concord_rebalance_group (two launches, no host read): when *peak >
+ * gate_max, every layer of the plan is rebalanced exactly as
+ * concord_rebalance(..., allow_tickdown = 0, advance_seed = 1) would do it,
+ * and fires[0] (when non-NULL) is advanced by one; otherwise nothing is
+ * written.  `plan` is the device copy of the plan; the workspace holds
+ * scratch_words int32.  The layers must not share packed words, exponents,
+ * watermark high-water marks or seeds.  Graph-capturable. */
+#define CONCORD_RG_FIELDS 16
+enum {
+  CONCORD_RG_PACKED = 0, CONCORD_RG_LD, CONCORD_RG_ROW_EXP, CONCORD_RG_COL_EXP, CONCORD_RG_ROW_MAX,
+  CONCORD_RG_COL_MAX, CONCORD_RG_ROW_HWM, CONCORD_RG_COL_HWM, CONCORD_RG_SEED, CONCORD_RG_N, CONCORD_RG_K,
+  CONCORD_RG_MAX_M, CONCORD_RG_EXP_MAX, CONCORD_RG_EXP_MIN
+};
+int concord_rebalance_group_plan(const int64_t* layers, int32_t n_layers, int64_t* plan, int64_t plan_len,
+                                 int64_t* scratch_words);
+int concord_rebalance_group(const int64_t* plan, int32_t n_layers, const int32_t* peak, int32_t gate_max,
+                            int32_t* fires, void* workspace, size_t workspace_bytes, int64_t scratch_words,
+                            void* stream);
+
 /* load_weights / load_weights_finetune (concord/packed_b.py:1570-1603,
  * 1816-1856): fp32 W[N, ld_w] -> packed state, row_exp, col_exp = 0. */
 int concord_load_weights(const float* W, int64_t ld_w, int64_t N, int64_t K, int32_t exp_min,

@@ -163,19 +163,8 @@ def test_config2_gpt_stack_trains():
     assert abs(np.mean(losses[-20:]) - math.log(V)) < 0.1, (losses[0], np.mean(losses[-20:]))
 
 
-# config 4: SDXL-UNet Linear and 1x1 weights (out x in, count), per
-# sdxl_fit_smoketest.py:55-69 as tabulated for this build; tokens per layer at
-# batch 4 of a 128 x 128 latent, realistic per level: 1280-channel layers at
-# 32 x 32 (M 4096), 640-channel at 64 x 64 (M 16384), 320-channel at 128 x 128
-# (M 65536), cross-attention k/v on 77 x 4 text tokens (M 308), time/label
-# embeddings on M 4
-SDXL_LINEAR = [((10240, 1280), 60, 4096), ((1280, 1280), 381, 4096), ((1280, 5120), 60, 4096),
-               ((1280, 2048), 120, 308), ((5120, 640), 10, 16384), ((640, 640), 70, 16384),
-               ((640, 2048), 20, 308), ((640, 2560), 10, 16384), ((640, 1280), 5, 4),
-               ((1280, 2816), 1, 4), ((320, 1280), 5, 4), ((1280, 320), 1, 4)]
-SDXL_1X1 = [((1280, 2560), 2, 4096), ((1280, 1920), 1, 4096), ((640, 1920), 1, 16384),
-            ((1280, 640), 1, 4096), ((640, 1280), 1, 16384), ((640, 960), 1, 16384),
-            ((320, 640), 2, 65536), ((320, 960), 1, 65536), ((640, 320), 1, 16384)]
+# config 4's SDXL-UNet Linear and 1x1 weights ((out, in), count, tokens M)
+from bench import SDXL_1X1, SDXL_LINEAR  # noqa: E402
 
 
 def _winner_oracle_params(O, layer):

@@ -1241,9 +1241,11 @@ def test_watermark_peak(nr, nc):
     assert int(host(out)[0]) == want
 
 
-def test_gated_rebalance_matches_host_gate():
-    """GatedRebalance (shared watermark slabs, one device reduction) takes the
-    same decisions and leaves every layer bit-identical to the same gate
+@pytest.mark.parametrize("device_gate", [True, False])
+def test_gated_rebalance_matches_host_gate(device_gate):
+    """GatedRebalance (shared watermark slabs, one device reduction, the
+    comparison with MAX_M on the device or on the host) takes the same
+    decisions and leaves every layer bit-identical to the same gate
     evaluated on the host (max of every layer's watermarks > MAX_M, then the
     per-layer rebalance loop), over several training steps."""
     import concord_amd as ca
@@ -1258,7 +1260,7 @@ def test_gated_rebalance_matches_host_gate():
         layers = [ca.ConcordLinearPackedB(k, n, bias=False, device=DEV, lr=5e-3) for k, n in shapes]
         for m, W in zip(layers, Ws):
             m.load_weights(W)
-        gate = ca.GatedRebalance(layers)
+        gate = ca.GatedRebalance(layers, device_gate=device_gate)
         fired = []
         for i, x in enumerate(xs):
             salt.fill_(70 + i)
@@ -1267,7 +1269,9 @@ def test_gated_rebalance_matches_host_gate():
                 h = m(h)
             h.square().mean().backward()
             if gated:
-                fired.append(gate())
+                before = gate.fires
+                gate()
+                fired.append(gate.fires > before)
             elif i == 0:
                 fired.append(False)   # the gate's first call only wires the slabs
             else:
@@ -1284,21 +1288,24 @@ def test_gated_rebalance_matches_host_gate():
         np.testing.assert_array_equal(a, b)
 
 
-def test_gated_rebalance_gate_logic():
+@pytest.mark.parametrize("device_gate", [True, False])
+def test_gated_rebalance_gate_logic(device_gate):
     """Below MAX_M nothing runs (no seed advance); one watermark above it
     fires the rebalance of every layer."""
     import concord_amd as ca
     layers = [ca.ConcordLinearPackedB(64, 96, bias=False, device=DEV),
               ca.ConcordLinearPackedB(96, 32, bias=False, device=DEV)]
-    gate = ca.GatedRebalance(layers)
+    gate = ca.GatedRebalance(layers, device_gate=device_gate)
     assert gate() is False and gate.row_all is not None
     seeds = [int(host(m._reb_seed)[0]) for m in layers]
     gate.row_all.fill_(gate.MAX_M)
     gate.col_all.fill_(7)
-    assert gate() is False
+    assert gate() is (None if device_gate else False)
     assert [int(host(m._reb_seed)[0]) for m in layers] == seeds
+    assert gate.fires == 0
     gate.col_all[40] = gate.MAX_M + 1
-    assert gate() is True and gate.fires == 1
+    assert gate() is (None if device_gate else True)
+    assert gate.fires == 1
     assert [int(host(m._reb_seed)[0]) for m in layers] == [v + 1 for v in seeds]
 
 

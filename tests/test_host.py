@@ -140,3 +140,79 @@ def test_default_knobs_match_reference():
                  "self._coh_pre = torch.ones_like"]:
         assert frag in src, frag
     assert pb._USE_FIXED_COH is True and pb._RATIO_COH is False
+
+
+def _rg_records(sizes):
+    import ctypes
+
+    from concord_amd import _lib as C
+    rec = (ctypes.c_int64 * (len(sizes) * C.RG_FIELDS))()
+    for i, (N, K) in enumerate(sizes):
+        r = i * C.RG_FIELDS
+        for f in (C.RG_PACKED, C.RG_ROW_EXP, C.RG_COL_EXP, C.RG_ROW_MAX, C.RG_COL_MAX, C.RG_SEED):
+            rec[r + f] = 0x10000 * (i + 1) + 16 * f
+        rec[r + C.RG_LD] = K
+        rec[r + C.RG_N] = N
+        rec[r + C.RG_K] = K
+        rec[r + C.RG_MAX_M] = 24000
+        rec[r + C.RG_EXP_MAX] = 7
+        rec[r + C.RG_EXP_MIN] = -8
+    return rec
+
+
+def test_rebalance_group_plan_layout(L):
+    """The group plan (host only): records copied, per-layer scratch offsets
+    (row ticks N + column ticks K + one flag per 256-row / 256-column decide
+    block), prefix sums of decide blocks and of 32 x 256 shift tiles."""
+    import ctypes
+
+    from concord_amd import _lib as C
+    sizes = [(300, 520), (1, 1), (1280, 5120), (257, 256)]
+    n = len(sizes)
+    rec = _rg_records(sizes)
+    plen = n * C.RG_FIELDS + 2 * (n + 1)
+    plan = (ctypes.c_int64 * plen)()
+    words = ctypes.c_int64(-1)
+    assert L.concord_rebalance_group_plan(rec, n, plan, plen, ctypes.byref(words)) == C.OK
+    cd = lambda a, b: -(-a // b)  # noqa: E731
+    scr, dp, tp = 0, [0], [0]
+    for i, (N, K) in enumerate(sizes):
+        r = i * C.RG_FIELDS
+        for f in range(14):
+            assert plan[r + f] == rec[r + f], (i, f)
+        assert plan[r + 14] == scr
+        nd = cd(N, 256) + cd(K, 256)
+        scr += N + K + nd
+        dp.append(dp[-1] + nd)
+        tp.append(tp[-1] + cd(N, 32) * cd(K, 256))
+    assert words.value == scr == 7254 + 257 + 256 + 3
+    assert list(plan[n * C.RG_FIELDS:n * C.RG_FIELDS + n + 1]) == dp == [0, 5, 7, 32, 35]
+    assert list(plan[n * C.RG_FIELDS + n + 1:]) == tp == [0, 30, 31, 831, 831 + 9]
+
+
+def test_rebalance_group_rejects_bad_plans(L):
+    import ctypes
+
+    from concord_amd import _lib as C
+    n = 2
+    plen = n * C.RG_FIELDS + 2 * (n + 1)
+    plan = (ctypes.c_int64 * plen)()
+    words = ctypes.c_int64(0)
+    rec = _rg_records([(10, 20), (0, 5)])
+    assert L.concord_rebalance_group_plan(rec, n, plan, plen, ctypes.byref(words)) == C.EINVAL
+    assert b"layer 1: bad size" in L.concord_last_error()
+    rec = _rg_records([(10, 20), (4, 5)])
+    rec[C.RG_FIELDS + C.RG_LD] = 4
+    assert L.concord_rebalance_group_plan(rec, n, plan, plen, ctypes.byref(words)) == C.EINVAL
+    assert b"leading dimension" in L.concord_last_error()
+    rec = _rg_records([(10, 20), (4, 5)])
+    rec[C.RG_SEED] = 0
+    assert L.concord_rebalance_group_plan(rec, n, plan, plen, ctypes.byref(words)) == C.EINVAL
+    assert b"layer 0: NULL" in L.concord_last_error()
+    rec = _rg_records([(10, 20), (4, 5)])
+    assert L.concord_rebalance_group_plan(rec, n, plan, plen - 1, ctypes.byref(words)) == C.EINVAL
+    assert L.concord_rebalance_group_plan(rec, 0, plan, plen, ctypes.byref(words)) == C.EINVAL
+    # the launch entry point checks its workspace before any GPU work
+    ws = ctypes.create_string_buffer(16)
+    assert L.concord_rebalance_group(plan, n, ws, 24000, None, ws, 16, 100, None) == C.EWORKSPACE
+    assert L.concord_rebalance_group(plan, n, None, 24000, None, ws, 16, 4, None) == C.EINVAL
