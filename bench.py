@@ -264,26 +264,34 @@ def _next_rows(layer, xb, dy, gw, reps, warmup, steps, torch, ca, pb):
         reps, torch)
     out["watermark_peak"] = hbm(t, 4 * CONFIG4_WATERMARKS, "peak_partials + peak_final over config 4's "
                                 f"{CONFIG4_WATERMARKS} row and column watermarks (4 B each)")
-    # one training step of an SDXL 640-channel 3 x 3 conv at 64 x 64, batch 2:
-    # M = 8192 positions, K = 640 * 9, N = 640; patches by unfold, products on
-    # the packed GEMMs
-    conv = ca.ConcordConv2dPackedB(640, 640, 3, padding=1, bias=True, device=dev, lr=5e-4)
-    xc = torch.randn(2, 640, 64, 64, device=dev).to(torch.bfloat16).requires_grad_(True)
-    dyc = (torch.randn(2, 640, 64, 64, device=dev) * 1e-3).to(torch.bfloat16)
+    # one training step of each SDXL 3 x 3 resnet conv shape at batch 2 of a
+    # 1024 px latent (implicit-GEMM path: patches gathered inside the GEMMs
+    # from channels-last activations): 6 M N K FLOP with M = B Ho Wo,
+    # N = out channels, K = 9 in channels
+    for cin, cout, hw in ((320, 320, 128), (640, 640, 64), (1280, 1280, 32)):
+        conv = ca.ConcordConv2dPackedB(cin, cout, 3, padding=1, bias=True, device=dev, lr=5e-4)
+        xc = torch.randn(2, cin, hw, hw, device=dev).to(torch.bfloat16).contiguous(
+            memory_format=torch.channels_last).requires_grad_(True)
+        dyc = (torch.randn(2, cout, hw, hw, device=dev) * 1e-3).to(torch.bfloat16).contiguous(
+            memory_format=torch.channels_last)
 
-    def cstep():
-        xc.grad = None
-        conv.bias.grad = None
-        conv(xc).backward(dyc)
-        conv.rebalance()
+        def cstep():
+            xc.grad = None
+            conv.bias.grad = None
+            conv(xc).backward(dyc)
+            conv.rebalance()
 
-    for _ in range(3):
-        cstep()
-    torch.cuda.synchronize()
-    t = _graph_ms(cstep, warmup, steps, torch)
-    out["conv2d_3x3_step"] = mfma(t, 6.0 * 8192 * 640 * 640 * 9,
-                                  "ConcordConv2dPackedB(640, 640, 3, padding 1) fwd + bwd + update + "
-                                  "rebalance on (2, 640, 64, 64); 6 M N K with M 8192, N 640, K 5760")
+        for _ in range(3):
+            cstep()
+        torch.cuda.synchronize()
+        t = _graph_ms(cstep, warmup, steps, torch)
+        m = 2 * hw * hw
+        key = "conv2d_3x3_step" if cin == 640 else f"conv2d_3x3_step_{cin}"
+        out[key] = mfma(t, 6.0 * m * cout * cin * 9,
+                        f"ConcordConv2dPackedB({cin}, {cout}, 3, padding 1) fwd + bwd + update + rebalance on "
+                        f"(2, {cin}, {hw}, {hw}) channels-last, implicit GEMM; 6 M N K with M {m}, N {cout}, "
+                        f"K {cin * 9}")
+        del conv, xc, dyc
     return out
 
 

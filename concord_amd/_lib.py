@@ -91,6 +91,13 @@ _SIGS = {
     "concord_conv_im2col": (ctypes.c_int, [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
     "concord_conv_col2im": (ctypes.c_int, [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
     "concord_conv_col2im_fits": (ctypes.c_int, [_I, _I, _I, _I]),
+    "concord_conv_implicit_ok": (ctypes.c_int, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I]),
+    "concord_conv_workspace_bytes": (_Z, [_I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I]),
+    "concord_conv_weight_taps": (ctypes.c_int, [_P, _I, _P, _P, _I, _I, _I, _i, _F, _P, _P]),
+    "concord_conv_grad_from_taps": (ctypes.c_int, [_P, _I, _I, _I, _P, _I, _P]),
+    "concord_conv_fwd": (ctypes.c_int, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
+    "concord_conv_dgrad": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
+    "concord_conv_wgrad": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "concord_sigmag_noise_workspace_bytes": (_Z, [_I, _I, _I]),
     "concord_sigmag_noise": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _Z, _P]),
     "concord_watermark_peak": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _Z, _P]),

@@ -7,7 +7,11 @@
 // flattening, so the layer's forward, dgrad and wgrad are the packed linear
 // products on cols.  im2col builds cols in one pass; col2im, its adjoint,
 // gathers dx from the patch gradient (see below).
+#include <algorithm>
+
 #include "common.h"
+#include "gemm.h"
+#include "workspace.h"
 
 namespace concord {
 
@@ -212,6 +216,140 @@ __global__ __launch_bounds__(256) void col2im_kernel(const uint16_t* __restrict_
   }
 }
 
+// col2im for windows too large for the staged tile: one lane per dx
+// element, the same fixed (i ascending, j ascending) fp32 sum, reading dcols
+// from global memory
+__global__ __launch_bounds__(256) void col2im_direct_kernel(const uint16_t* __restrict__ dcols, ConvGeom g,
+                                                            uint16_t* __restrict__ dx) {
+  const int64_t total = g.B * g.C * g.H * g.W;
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < total; e += (int64_t)gridDim.x * 256) {
+    const int64_t w = e % g.W, t1 = e / g.W;
+    const int64_t h = t1 % g.H, t2 = t1 / g.H;
+    const int64_t c = t2 % g.C, b = t2 / g.C;
+    float acc = 0.0f;
+    for (int64_t i = 0; i < g.kh; ++i) {
+      const int64_t hh = h + g.ph - i;
+      if (hh < 0 || hh % g.sh) continue;
+      const int64_t ho = hh / g.sh;
+      if (ho >= g.Ho) continue;
+      for (int64_t j = 0; j < g.kw; ++j) {
+        const int64_t ww = w + g.pw - j;
+        if (ww < 0 || ww % g.sw) continue;
+        const int64_t wo = ww / g.sw;
+        if (wo >= g.Wo) continue;
+        acc = __fadd_rn(acc, bf16_to_f32(dcols[((b * g.Ho + ho) * g.Wo + wo) * g.K + (c * g.kh + i) * g.kw + j]));
+      }
+    }
+    dx[e] = (uint16_t)(pack_bf16x2(acc, 0.0f) & 0xFFFFu);
+  }
+}
+
+// ---- implicit-GEMM convolution: weight and gradient in tap-major order -----
+// W'[n][t][c] = the forward weight of packed word (n, c * taps + t): the
+// GEMMs of the implicit convolution reduce over (tap, channel) with channels
+// contiguous.  A block takes one row n and kTapC channels: it reads their
+// kTapC * taps contiguous words (16 bytes per lane), decodes them
+// (materialize_gated's fp32 order: (128 ss + g sf) + 128 vs; with g = 1 this
+// equals the ungated decode, every term being an integer below 2^24) into an
+// LDS tile [taps][kTapC], then writes taps rows of kTapC channels (8 bytes
+// per lane).
+constexpr int kTapC = 256;
+constexpr int kTapLd = kTapC + 4;   // LDS row of weight_taps_kernel: tap rows 2 banks apart, 8-byte aligned
+
+__global__ __launch_bounds__(256) void weight_taps_kernel(const int32_t* __restrict__ packed, int64_t ld_p,
+                                                          const int8_t* row_exp, const int8_t* col_exp,
+                                                          int64_t Cin, int taps, int32_t bias, float gain,
+                                                          uint16_t* __restrict__ wt) {
+  extern __shared__ uint16_t tl[];   // [taps][kTapLd]
+  const int64_t n = blockIdx.y;
+  const int64_t c0 = (int64_t)blockIdx.x * kTapC;
+  const int nc = (int)min((int64_t)kTapC, Cin - c0);
+  const int ne = nc * taps;
+  const int32_t te_row = (int32_t)row_exp[n] - bias;
+  const int32_t* src = packed + n * ld_p + c0 * taps;
+  const int8_t* ce = col_exp + c0 * taps;
+  auto dec = [&](int32_t w, int e) -> uint16_t {
+    const Fields f = unpack(w);
+    const float m = __fadd_rn(__fadd_rn((float)(f.ss * 128), __fmul_rn(gain, (float)f.sf)), (float)(f.vs * 128));
+    const float v = __fmul_rn(m, exp2i(te_row + (int32_t)ce[e]));
+    return (uint16_t)(pack_bf16x2(v, 0.0f) & 0xFFFFu);
+  };
+  auto put = [&](int e, uint16_t v) {
+    const int cl = e / taps, t = e - cl * taps;
+    tl[t * kTapLd + cl] = v;
+  };
+  const bool vec = ((uintptr_t)src % 16) == 0;
+  if (vec) {
+    for (int e = threadIdx.x * 4; e < ne; e += 256 * 4) {
+      if (e + 4 <= ne) {
+        const int4 w4 = *reinterpret_cast<const int4*>(src + e);
+        put(e, dec(w4.x, e));
+        put(e + 1, dec(w4.y, e + 1));
+        put(e + 2, dec(w4.z, e + 2));
+        put(e + 3, dec(w4.w, e + 3));
+      } else {
+        for (int q = e; q < ne; ++q) put(q, dec(src[q], q));
+      }
+    }
+  } else {
+    for (int e = threadIdx.x; e < ne; e += 256) put(e, dec(src[e], e));
+  }
+  __syncthreads();
+  uint16_t* dst = wt + n * taps * Cin + c0;
+  const bool v8 = (nc % 4) == 0 && (Cin % 4) == 0 && ((uintptr_t)wt % 8) == 0 && (c0 % 4) == 0;
+  if (v8) {
+    const int q4 = nc / 4;
+    for (int e = threadIdx.x; e < q4 * taps; e += 256) {
+      const int t = e / q4, cl = (e - t * q4) * 4;
+      *reinterpret_cast<uint2*>(dst + (int64_t)t * Cin + cl) = *reinterpret_cast<const uint2*>(tl + t * kTapLd + cl);
+    }
+  } else {
+    for (int e = threadIdx.x; e < ne; e += 256) {
+      const int t = e / nc, cl = e - t * nc;
+      dst[(int64_t)t * Cin + cl] = tl[t * kTapLd + cl];
+    }
+  }
+}
+
+// g[n][c * taps + t] = gt[n][t][c]: a conv gradient from the tap-major order
+// of the implicit WGRAD back to the packed words' (c, tap) order.  Same
+// blocking as weight_taps_kernel, with the LDS tile [kTapC][taps].
+__global__ __launch_bounds__(256) void grad_from_taps_kernel(const uint16_t* __restrict__ gt, int64_t Cin,
+                                                             int taps, uint16_t* __restrict__ g, int64_t ld_g) {
+  extern __shared__ uint16_t tl[];   // [kTapC][taps]
+  const int64_t n = blockIdx.y;
+  const int64_t c0 = (int64_t)blockIdx.x * kTapC;
+  const int nc = (int)min((int64_t)kTapC, Cin - c0);
+  const int ne = nc * taps;
+  const uint16_t* src = gt + n * taps * Cin + c0;
+  const bool v8 = (nc % 4) == 0 && (Cin % 4) == 0 && ((uintptr_t)gt % 8) == 0 && (c0 % 4) == 0;
+  if (v8) {
+    const int q4 = nc / 4;
+    for (int e = threadIdx.x; e < q4 * taps; e += 256) {
+      const int t = e / q4, cl = (e - t * q4) * 4;
+      const uint2 v = *reinterpret_cast<const uint2*>(src + (int64_t)t * Cin + cl);
+      tl[cl * taps + t] = (uint16_t)(v.x & 0xFFFFu);
+      tl[(cl + 1) * taps + t] = (uint16_t)(v.x >> 16);
+      tl[(cl + 2) * taps + t] = (uint16_t)(v.y & 0xFFFFu);
+      tl[(cl + 3) * taps + t] = (uint16_t)(v.y >> 16);
+    }
+  } else {
+    for (int e = threadIdx.x; e < ne; e += 256) {
+      const int t = e / nc, cl = e - t * nc;
+      tl[cl * taps + t] = src[(int64_t)t * Cin + cl];
+    }
+  }
+  __syncthreads();
+  uint16_t* dst = g + n * ld_g + c0 * taps;
+  const bool w8 = (ne % 4) == 0 && ((uintptr_t)dst % 8) == 0;
+  if (w8) {
+    for (int e = threadIdx.x * 4; e < ne; e += 256 * 4)
+      *reinterpret_cast<uint2*>(dst + e) = *reinterpret_cast<const uint2*>(tl + e);
+  } else {
+    for (int e = threadIdx.x; e < ne; e += 256) dst[e] = tl[e];
+  }
+}
+
 constexpr size_t kCol2imLdsBudget = 64 * 1024;   // two blocks per CU
 
 // staged rows and columns a block needs at most, and the channels per block
@@ -280,8 +418,14 @@ extern "C" int concord_conv_col2im(const uint16_t* dcols, int64_t B, int64_t C, 
   ConvGeom g{B, C, H, W, kh, kw, sh, sw, ph, pw, (H + 2 * ph - kh) / sh + 1, (W + 2 * pw - kw) / sw + 1,
              C * kh * kw};
   const Col2imTile T = col2im_tile(g);
-  CONCORD_CHECK(T.cc > 0, "concord_conv_col2im: kernel window too large for the staged tile");
   if (B == 0) return CONCORD_OK;
+  if (T.cc == 0) {
+    // a window too large for the staged tile: the unstaged gather
+    const int64_t total = B * C * H * W;
+    hipLaunchKernelGGL(col2im_direct_kernel, dim3((unsigned)std::min<int64_t>(cdiv(total, 256), 65536)), dim3(256),
+                       0, (hipStream_t)stream, dcols, g, dx);
+    return launch_status("conv_col2im");
+  }
   const int64_t gy = B * ((H + kC2iH - 1) / kC2iH);
   CONCORD_CHECK(gy <= kMaxGridY && cdiv(C, T.cc) <= kMaxGridY && cdiv(W, kC2iW) < ((int64_t)1 << 31),
                 "concord_conv_col2im: grid too large (batch x rows / 4 must stay below 65536)");
@@ -295,4 +439,173 @@ extern "C" int concord_conv_col2im_fits(int64_t kh, int64_t kw, int64_t sh, int6
   ConvGeom g{};
   g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw;
   return kh > 0 && kw > 0 && sh > 0 && sw > 0 && col2im_tile(g).cc > 0;
+}
+
+// ---- implicit-GEMM convolution entry points -----------------------------------
+namespace concord {
+
+struct ConvShape {
+  int64_t B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw, Ho, Wo;
+};
+
+static bool conv_shape(int64_t B, int64_t Cin, int64_t H, int64_t W, int64_t Cout, int64_t kh, int64_t kw,
+                       int64_t sh, int64_t sw, int64_t ph, int64_t pw, ConvShape& s) {
+  if (!(B >= 0 && Cin > 0 && H > 0 && W > 0 && Cout > 0 && kh > 0 && kw > 0 && sh > 0 && sw > 0 && ph >= 0 &&
+        pw >= 0 && H + 2 * ph >= kh && W + 2 * pw >= kw && H < (1 << 20) && W < (1 << 20) && kh < 64 && kw < 64))
+    return false;
+  s = ConvShape{B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw, (H + 2 * ph - kh) / sh + 1, (W + 2 * pw - kw) / sw + 1};
+  return true;
+}
+
+// the implicit kernels take the shape: channels in 64-element stages, strides
+// 1 or 2, positions below 2^24 (exact magic division), operands below 2^30
+// bytes (32-bit buffer offsets)
+static bool conv_implicit_shape(const ConvShape& s) {
+  const int64_t lim = ((int64_t)1 << 24) - 64;
+  return s.Cin % 64 == 0 && s.Cout % 64 == 0 && (s.sh == 1 || s.sh == 2) && (s.sw == 1 || s.sw == 2) &&
+         s.kh * s.kw <= 64 &&
+         s.B * s.H * s.W < lim && s.B * s.Ho * s.Wo < lim && s.B * s.H * s.W * s.Cin * 2 < ((int64_t)1 << 30) &&
+         s.B * s.Ho * s.Wo * s.Cout * 2 < ((int64_t)1 << 30) &&
+         s.Cout * s.kh * s.kw * s.Cin * 2 < ((int64_t)1 << 30);
+}
+
+// ConvIdx of one product: gathered activation (C channels on Hg x Wg), GEMM
+// positions on Hr x Wr
+static ConvIdx conv_idx(const ConvShape& s, int64_t C, int64_t Hg, int64_t Wg, int64_t Hr, int64_t Wr,
+                        int64_t cb, int64_t act_bytes, int64_t w_bytes) {
+  ConvIdx c{};
+  c.C = (int32_t)C;
+  c.Hg = (int32_t)Hg;
+  c.Wg = (int32_t)Wg;
+  c.Hr = (int32_t)Hr;
+  c.Wr = (int32_t)Wr;
+  c.kw = (int32_t)s.kw;
+  c.ph = (int32_t)s.ph;
+  c.pw = (int32_t)s.pw;
+  c.slh = s.sh == 2 ? 1 : 0;
+  c.slw = s.sw == 2 ? 1 : 0;
+  c.cb = (int32_t)cb;
+  conv_magic((uint32_t)Wr, c.mw, c.shw);
+  conv_magic((uint32_t)Hr, c.mh, c.shh);
+  c.act_bytes = (uint32_t)act_bytes;
+  c.w_bytes = (uint32_t)w_bytes;
+  return c;
+}
+
+static GemmArgs conv_args(const uint16_t* a, int64_t lda, const void* b, int64_t ldb, uint16_t* c, int64_t ldc,
+                          int64_t I, int64_t J, int64_t R, const uint16_t* bias) {
+  GemmArgs g{};
+  g.a = a;
+  g.b = b;
+  g.lda = lda;
+  g.ldb = ldb;
+  g.c = c;
+  g.ldc = ldc;
+  g.I = I;
+  g.J = J;
+  g.R = R;
+  g.vbias = bias;
+  g.splits = 1;
+  return g;
+}
+
+}  // namespace concord
+
+#define CONV_GEOM_ARGS                                                                                      \
+  int64_t B, int64_t Cin, int64_t H, int64_t W, int64_t Cout, int64_t kh, int64_t kw, int64_t sh, int64_t sw, \
+      int64_t ph, int64_t pw
+
+extern "C" int concord_conv_implicit_ok(CONV_GEOM_ARGS) {
+  ConvShape s;
+  return conv_shape(B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw, s) && conv_implicit_shape(s);
+}
+
+extern "C" size_t concord_conv_workspace_bytes(CONV_GEOM_ARGS) {
+  ConvShape s;
+  if (!conv_shape(B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw, s)) return kSplitkCounterBytes;
+  const int64_t T = kh * kw, Mo = std::max<int64_t>(1, B * s.Ho * s.Wo), Mi = std::max<int64_t>(1, B * H * W);
+  const size_t a = gemm_conv_partial_bytes(MODE_FWD_BF16, Mo, Cout, T * Cin);
+  const size_t b = gemm_conv_partial_bytes(MODE_DGRAD_BF16, Mi, Cin, T * Cout);
+  const size_t c = gemm_conv_partial_bytes(MODE_WGRAD, Cout, T * Cin, Mo);
+  const size_t m = std::max(a, std::max(b, c));
+  return kSplitkCounterBytes + ((m + 255) / 256) * 256;
+}
+
+extern "C" int concord_conv_weight_taps(const int32_t* packed, int64_t ld_p, const int8_t* row_exp,
+                                        const int8_t* col_exp, int64_t Cout, int64_t Cin, int64_t taps,
+                                        int32_t mantissa_bias, float fast_gain, uint16_t* wt, void* stream) {
+  CONCORD_CHECK(Cout >= 0 && Cin > 0 && taps > 0 && taps <= 64 && Cout < (1LL << 31) && Cin * taps < (1LL << 31),
+                "concord_conv_weight_taps: bad size (at most 64 taps)");
+  if (Cout == 0) return CONCORD_OK;
+  CONCORD_CHECK(packed && row_exp && col_exp && wt, "concord_conv_weight_taps: NULL argument");
+  CONCORD_CHECK(ld_p >= Cin * taps, "concord_conv_weight_taps: leading dimension < in_channels * taps");
+  CONCORD_CHECK(Cout <= kMaxGridY, "concord_conv_weight_taps: more than %lld output channels",
+                (long long)kMaxGridY);
+  hipLaunchKernelGGL(weight_taps_kernel, dim3((unsigned)cdiv(Cin, kTapC), (unsigned)Cout), dim3(256),
+                     (size_t)taps * kTapLd * 2, (hipStream_t)stream, packed, ld_p, row_exp, col_exp, Cin, (int)taps,
+                     mantissa_bias, fast_gain, wt);
+  return launch_status("conv_weight_taps");
+}
+
+extern "C" int concord_conv_grad_from_taps(const uint16_t* gt, int64_t Cout, int64_t Cin, int64_t taps, uint16_t* g,
+                                           int64_t ld_g, void* stream) {
+  CONCORD_CHECK(Cout >= 0 && Cin > 0 && taps > 0 && taps <= 64 && Cout < (1LL << 31) && Cin * taps < (1LL << 31),
+                "concord_conv_grad_from_taps: bad size (at most 64 taps)");
+  if (Cout == 0) return CONCORD_OK;
+  CONCORD_CHECK(gt && g, "concord_conv_grad_from_taps: NULL argument");
+  CONCORD_CHECK(ld_g >= Cin * taps, "concord_conv_grad_from_taps: leading dimension < in_channels * taps");
+  CONCORD_CHECK(Cout <= kMaxGridY, "concord_conv_grad_from_taps: more than %lld output channels",
+                (long long)kMaxGridY);
+  hipLaunchKernelGGL(grad_from_taps_kernel, dim3((unsigned)cdiv(Cin, kTapC), (unsigned)Cout), dim3(256),
+                     (size_t)taps * kTapC * 2, (hipStream_t)stream, gt, Cin, (int)taps, g, ld_g);
+  return launch_status("conv_grad_from_taps");
+}
+
+extern "C" int concord_conv_fwd(const uint16_t* x, const uint16_t* wt, const uint16_t* bias, uint16_t* y,
+                                CONV_GEOM_ARGS, void* workspace, size_t workspace_bytes, void* stream) {
+  ConvShape s;
+  CONCORD_CHECK(conv_shape(B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw, s), "concord_conv_fwd: bad geometry");
+  CONCORD_CHECK(conv_implicit_shape(s), "concord_conv_fwd: shape not taken by the implicit kernels "
+                                        "(concord_conv_implicit_ok)");
+  if (B == 0) return CONCORD_OK;
+  CONCORD_CHECK(x && wt && y, "concord_conv_fwd: NULL argument");
+  const int64_t T = kh * kw;
+  GemmArgs g = conv_args(x, Cin, wt, T * Cin, y, Cout, B * s.Ho * s.Wo, Cout, T * Cin, bias);
+  g.cv = conv_idx(s, Cin, H, W, s.Ho, s.Wo, Cin, B * H * W * Cin * 2, Cout * T * Cin * 2);
+  const int rc = gemm_conv_launch(MODE_FWD_BF16, g, workspace, workspace_bytes, (hipStream_t)stream, "conv_fwd");
+  CONCORD_CHECK(rc != -1, "concord_conv_fwd: operands not aligned for the implicit kernels (16-byte x and "
+                          "weight, 8-byte y and bias)");
+  return rc;
+}
+
+extern "C" int concord_conv_dgrad(const uint16_t* dy, const uint16_t* wt, uint16_t* dx, CONV_GEOM_ARGS,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  ConvShape s;
+  CONCORD_CHECK(conv_shape(B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw, s), "concord_conv_dgrad: bad geometry");
+  CONCORD_CHECK(conv_implicit_shape(s), "concord_conv_dgrad: shape not taken by the implicit kernels "
+                                        "(concord_conv_implicit_ok)");
+  if (B == 0) return CONCORD_OK;
+  CONCORD_CHECK(dy && wt && dx, "concord_conv_dgrad: NULL argument");
+  const int64_t T = kh * kw;
+  GemmArgs g = conv_args(dy, Cout, wt, T * Cin, dx, Cin, B * H * W, Cin, T * Cout, nullptr);
+  g.cv = conv_idx(s, Cout, s.Ho, s.Wo, H, W, Cin, B * s.Ho * s.Wo * Cout * 2, Cout * T * Cin * 2);
+  const int rc = gemm_conv_launch(MODE_DGRAD_BF16, g, workspace, workspace_bytes, (hipStream_t)stream,
+                                  "conv_dgrad");
+  CONCORD_CHECK(rc != -1, "concord_conv_dgrad: operands not aligned for the implicit kernels");
+  return rc;
+}
+
+extern "C" int concord_conv_wgrad(const uint16_t* dy, const uint16_t* x, uint16_t* gt, CONV_GEOM_ARGS,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  ConvShape s;
+  CONCORD_CHECK(conv_shape(B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw, s), "concord_conv_wgrad: bad geometry");
+  CONCORD_CHECK(conv_implicit_shape(s), "concord_conv_wgrad: shape not taken by the implicit kernels "
+                                        "(concord_conv_implicit_ok)");
+  CONCORD_CHECK(dy && x && gt, "concord_conv_wgrad: NULL argument");
+  const int64_t T = kh * kw;
+  GemmArgs g = conv_args(dy, Cout, x, T * Cin, gt, T * Cin, Cout, T * Cin, B * s.Ho * s.Wo, nullptr);
+  g.cv = conv_idx(s, Cin, H, W, s.Ho, s.Wo, Cin, B * H * W * Cin * 2, 0);
+  const int rc = gemm_conv_launch(MODE_WGRAD, g, workspace, workspace_bytes, (hipStream_t)stream, "conv_wgrad");
+  CONCORD_CHECK(rc != -1, "concord_conv_wgrad: operands not aligned for the implicit kernels");
+  return rc;
 }

@@ -14,6 +14,37 @@ enum { MODE_FWD = 0, MODE_DGRAD = 1, MODE_WGRAD = 2, MODE_FWD_BF16 = 3, MODE_DGR
 constexpr int TR = 64;          // reduction depth per LDS stage
 constexpr int LDS_STRIDE = 72;  // bf16 per LDS row (64 + 8 pad)
 
+// Implicit-GEMM convolution (stride 1 or 2 per axis, zero padding): one
+// operand is an NHWC activation read as the patch matrix without forming it.
+// Patch index r = tap * C + c, tap = ky * kw + kx (C % 64 == 0, so a 64-deep
+// stage stays inside one tap).  A GEMM row (FWD, DGRAD) or reduction index
+// (WGRAD) is a position (b, y, x) of an Hr x Wr grid, split by exact
+// magic-number division (conv_magic).
+struct ConvIdx {
+  int32_t C;              // channels of the gathered activation
+  int32_t Hg, Wg;         // its spatial size
+  int32_t Hr, Wr;         // the grid of the GEMM's positions
+  int32_t kw;             // kernel width (taps per kernel row)
+  int32_t ph, pw;         // padding
+  int32_t slh, slw;       // log2 of the strides
+  int32_t cb;             // DGRAD: channels of a tap block of the weight operand (its in-channels)
+  uint32_t mw, mh;        // magic multipliers for / Wr and / Hr
+  int32_t shw, shh;       // and their shifts
+  uint32_t act_bytes;     // bytes of the gathered activation
+  uint32_t w_bytes;       // DGRAD: bytes of the weight operand
+};
+
+// (mg, sh) with floor(m mg / 2^sh) = floor(m / d) for every 0 <= m < 2^24:
+// sh = 24 + ceil(log2 d), mg = ceil(2^sh / d) < 2^25.  With e = mg d - 2^sh
+// in [0, d): m mg / 2^sh = m / d + m e / (d 2^sh), and m e < 2^24 d <= 2^sh,
+// so the excess stays below 1 / d.
+inline void conv_magic(uint32_t d, uint32_t& mg, int32_t& sh) {
+  int l = 0;
+  while ((1u << l) < d) ++l;
+  sh = 24 + l;
+  mg = (uint32_t)((((uint64_t)1 << sh) + d - 1) / d);
+}
+
 struct GemmArgs {
   const uint16_t* a;      // FWD: x[M,K]; DGRAD*, WGRAD: dy[M,N]
   const void* b;          // packed[N,K] int32 | x[M,K] bf16 (WGRAD) | W[N,K] bf16 (*_BF16)
@@ -38,6 +69,7 @@ struct GemmArgs {
   const uint16_t* ay;
   int64_t ldy;
   float as, at;
+  ConvIdx cv;             // implicit-GEMM convolution kernels only
 };
 
 // s * y + t * x as the Newton-Schulz combination steps take it (x is the
@@ -100,6 +132,14 @@ int gemm_bf16_combine(int mode, const uint16_t* a, int64_t lda, const uint16_t* 
 int gemm_bf16_run(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
                   int64_t ldc, int64_t I, int64_t J, int64_t R, void* ws, size_t ws_bytes, hipStream_t st,
                   const char* what);
+// implicit-GEMM convolution products (g.cv set): MODE_FWD_BF16 (x gathered,
+// W' [N][taps * C] rows), MODE_DGRAD_BF16 (dy gathered, W' rows (n, tap) by
+// the tap's column block) or MODE_WGRAD (x gathered as the column operand);
+// -1 when the operands do not take the kernels
+int gemm_conv_launch(int mode, const GemmArgs& g, void* workspace, size_t ws_bytes, hipStream_t st,
+                     const char* what);
+// split-K partial bytes gemm_conv_launch plans for an I x J x R product
+size_t gemm_conv_partial_bytes(int mode, int64_t I, int64_t J, int64_t R);
 // split-K workspace bytes (counters + partials) one such product may use
 size_t gemm_splitk_need(int mode, int64_t I, int64_t J, int64_t R);
 // split-K partial bytes the fast kernels plan for an I x J x R problem

@@ -850,6 +850,92 @@ struct RowsDma {
   }
 };
 
+// ---- implicit-GEMM convolution: gathered row operands ----------------------
+// exact m / d for 0 <= m < 2^24, (mg, sh) from conv_magic(d)
+CONCORD_DEV int32_t cdivm(int32_t m, uint32_t mg, int32_t sh) {
+  return (int32_t)(((uint64_t)(uint32_t)m * mg) >> sh);
+}
+
+// RowsDma's tile (ROWS rows x 64 columns per stage, same LDS layout and
+// swizzle) for a conv GEMM whose rows are positions and whose 64 stage
+// columns are channels c0 .. c0 + 63 of one tap.
+//   !DG (forward): row = output position (b, ho, wo); the row of the stage
+//       reads x[b][ho sh - ph + ky][wo sw - pw + kx][c0 ..], 0 outside.
+//   DG (dgrad): row = input position (b, h, w); it reads
+//       dy[b][(h + ph - ky) / sh][(w + pw - kx) / sw][c0 ..] where the
+//       division is exact and lands inside the output grid, 0 otherwise.
+template <int ROWS, int NW, bool DG>
+struct RowsDmaConv {
+  static constexpr int INSTR = ROWS / 8;
+  static constexpr int PER = INSTR / NW;
+  static_assert(PER * NW == INSTR, "rows must split evenly over the issuing waves");
+  uint32_t kc2[PER];          // byte offset of this lane's 8-channel chunk in the stage
+  int32_t yy[PER], xx[PER];   // !DG: y, x of tap (0, 0); DG: h + ph, w + pw
+  int32_t bb[PER];            // b * Hg; -1 for rows past the GEMM's last row
+  i32x4 rs;
+  int w;
+  int32_t C, Hg, Wg, kw, slh, slw;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t i0, int wave, int lane) {
+    const ConvIdx& c = g.cv;
+    w = wave;
+    C = c.C;
+    Hg = c.Hg;
+    Wg = c.Wg;
+    kw = c.kw;
+    slh = c.slh;
+    slw = c.slw;
+    const uint64_t base = (uint64_t)(uintptr_t)g.a;
+    rs = i32x4{(int32_t)(uint32_t)base, (int32_t)(uint32_t)((base >> 32) & 0xFFFF), (int32_t)c.act_bytes,
+               0x00020000};
+    for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(rs[e]);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int r = (w * PER + q) * 8 + lane / 8;
+      const int cc = (lane % 8) ^ ((r >> 1) & 7);
+      kc2[q] = (uint32_t)(cc * 16);
+      yy[q] = xx[q] = 0;
+      bb[q] = -1;
+      if (i0 + r < g.I) {
+        const int32_t m = (int32_t)(i0 + r);
+        const int32_t t = cdivm(m, c.mw, c.shw);
+        const int32_t xr = m - t * c.Wr;
+        const int32_t b = cdivm(t, c.mh, c.shh);
+        const int32_t yr = t - b * c.Hr;
+        yy[q] = DG ? yr + c.ph : (yr << c.slh) - c.ph;
+        xx[q] = DG ? xr + c.pw : (xr << c.slw) - c.pw;
+        bb[q] = b * c.Hg;
+      }
+    }
+  }
+  CONCORD_DEV void load(uint16_t* tile, int64_t r0, int64_t rem) const {
+    const int32_t tap = (int32_t)r0 / C;
+    const int32_t c0 = (int32_t)r0 - tap * C;
+    const int32_t ky = tap / kw, kx = tap - ky * kw;
+    const uint32_t so = uni((uint32_t)c0 * 2u);
+    const uint32_t base = lds_addr(tile);
+    const int32_t mh = (1 << slh) - 1, mw = (1 << slw) - 1;
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      int32_t y, x;
+      bool ok;
+      if (!DG) {
+        y = yy[q] + ky;
+        x = xx[q] + kx;
+        ok = (uint32_t)y < (uint32_t)Hg && (uint32_t)x < (uint32_t)Wg;
+      } else {
+        const int32_t yn = yy[q] - ky, xn = xx[q] - kx;
+        y = yn >> slh;
+        x = xn >> slw;
+        ok = yn >= 0 && xn >= 0 && (yn & mh) == 0 && (xn & mw) == 0 && y < Hg && x < Wg;
+      }
+      ok = ok && bb[q] >= 0 && (int64_t)(kc2[q] >> 1) < rem;
+      const uint32_t vo = ok ? ((uint32_t)(bb[q] + y) * (uint32_t)Wg + (uint32_t)x) * (uint32_t)(C * 2) + kc2[q]
+                            : kOOB;
+      dma16(rs, vo, so, uni(base + (uint32_t)((w * PER + q) * 1024)));
+    }
+  }
+};
+
 // MFMAs of one stage: A from a swizzled DMA tile, B from a padded tile.
 template <int NI, int NJ>
 CONCORD_DEV void stage_mfma_swz(f32x4 (&acc)[NI][NJ], const uint16_t* la, const uint16_t* lb, int ra, int rb,
@@ -906,13 +992,14 @@ template <int BJ, int NT> struct BSide<MODE_DGRAD_BF16, BJ, NT> {
 // waves 4-7 load B three stages ahead in registers, decode it and write it
 // into a double-buffered padded LDS tile.  One LDS barrier per stage; before
 // it every compute wave waits until its own DMA of the next stage has landed.
-template <int MODE, int BI, int BJ>
+// CONV: the A operand is the conv forward's gathered x (RowsDmaConv).
+template <int MODE, int BI, int BJ, bool CONV = false>
 __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
   constexpr int NP = 256;
   constexpr int WTI = BI / 2, WTJ = BJ / 2;
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
   typedef BSide<MODE, BJ, NP> BS;
-  typedef RowsDma<BI, 4> AD;
+  typedef typename std::conditional<CONV, RowsDmaConv<BI, 4, false>, RowsDma<BI, 4>>::type AD;
   constexpr int LB = decltype(BS::b)::LROWS;
   static_assert(LB >= BJ, "LDS tile rows");
   __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
@@ -967,7 +1054,8 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
     }
   } else {
     AD ad;
-    ad.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, wave, lane);
+    if constexpr (CONV) ad.init(g, i0, wave, lane);
+    else ad.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, wave, lane);
     ad.load(lds_a[0], r_begin, r_end - r_begin);
     ad.load(lds_a[1], r_begin + TR, r_end - r_begin - TR);
     // own DMA of stage 0 landed (stage 1's PER loads may still fly)
@@ -1048,6 +1136,79 @@ struct TrDma {
   }
 };
 
+// TrDma's tile (TR rows x COLS columns, same layout and swizzle) for the
+// WGRAD of a conv: rows are output positions m = (b, ho, wo) (the
+// reduction), columns r = tap * C + c of the patch matrix; the lane's 8
+// columns read x[b][ho sh - ph + ky][wo sw - pw + kx][c ..], 0 outside.
+template <int COLS, int NW>
+struct TrDmaConv {
+  static constexpr int ROWB = COLS * 2;
+  static constexpr int RPI = 1024 / ROWB;
+  static constexpr int INSTR = TR / RPI;
+  static constexpr int PER = INSTR / NW;
+  static_assert(COLS >= 128 && COLS <= 512 && PER * NW == INSTR, "TrDma tile");
+  uint32_t cin2[PER];          // byte offset of this lane's 8 channels within a position
+  int32_t oy[PER], ox[PER];    // ky - ph, kx - pw of their tap; oy huge negative past the tile's columns
+  int32_t lrow;
+  i32x4 rs;
+  int w;
+  int32_t Cb2, Hg, Wg, Hr, Wr, slh, slw, shw, shh;
+  uint32_t mw, mh;
+  CONCORD_DEV void init(const GemmArgs& g, int64_t j0, int wave, int lane) {
+    const ConvIdx& c = g.cv;
+    w = wave;
+    Cb2 = c.C * 2;
+    Hg = c.Hg;
+    Wg = c.Wg;
+    Hr = c.Hr;
+    Wr = c.Wr;
+    slh = c.slh;
+    slw = c.slw;
+    mw = c.mw;
+    mh = c.mh;
+    shw = c.shw;
+    shh = c.shh;
+    lrow = lane / (ROWB / 16);
+    const uint64_t base = (uint64_t)(uintptr_t)g.b;
+    rs = i32x4{(int32_t)(uint32_t)base, (int32_t)(uint32_t)((base >> 32) & 0xFFFF), (int32_t)c.act_bytes,
+               0x00020000};
+    for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(rs[e]);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int r = (w * PER + q) * RPI + lrow;
+      const int cc = (lane % (ROWB / 16)) ^ (trf(r) << 1);
+      cin2[q] = 0;
+      oy[q] = -(1 << 28);
+      ox[q] = 0;
+      if (cc * 8 < g.J - j0) {
+        const int32_t col = (int32_t)(j0 + cc * 8);
+        const int32_t tap = col / c.C;
+        const int32_t ky = tap / c.kw;
+        cin2[q] = (uint32_t)((col - tap * c.C) * 2);
+        oy[q] = ky - c.ph;
+        ox[q] = tap - ky * c.kw - c.pw;
+      }
+    }
+  }
+  CONCORD_DEV void load(uint32_t tile, int64_t r0, int64_t rem) const {
+    const int rem32 = (int)(rem < TR ? rem : TR);
+#pragma unroll
+    for (int q = 0; q < PER; ++q) {
+      const int rl = (w * PER + q) * RPI + lrow;
+      const int32_t m = (int32_t)r0 + rl;
+      const int32_t t = cdivm(m, mw, shw);
+      const int32_t xo = m - t * Wr;
+      const int32_t b = cdivm(t, mh, shh);
+      const int32_t yo = t - b * Hr;
+      const int32_t y = (yo << slh) + oy[q], x = (xo << slw) + ox[q];
+      const bool ok = rl < rem32 && (uint32_t)y < (uint32_t)Hg && (uint32_t)x < (uint32_t)Wg;
+      const uint32_t vo =
+          ok ? ((uint32_t)(b * Hg + y) * (uint32_t)Wg + (uint32_t)x) * (uint32_t)Cb2 + cin2[q] : kOOB;
+      dma16(rs, vo, 0u, uni(tile + (uint32_t)((w * PER + q) * 1024)));
+    }
+  }
+};
+
 typedef __attribute__((address_space(3))) char lds_char;
 
 // fragments of reduction step kk (32 r) of a stage tile for the 16-column
@@ -1104,7 +1265,8 @@ CONCORD_DEV void bias_acc(f32x4 (&b)[NI], const bf16x8 (&fa)[NI]) {
 // workgroups from tr_blocks on run the split-K reduction `rd` of the dgrad
 // kernel issued just before on the stream, on the CUs the WGRAD grid leaves
 // idle (200 tiles on 256 CUs at 1280 -> 5120).
-template <int BI, int BJ, int WI, int WJ, bool VH>
+// CONV: the B operand (x) is the conv wgrad's gathered patch matrix (TrDmaConv).
+template <int BI, int BJ, int WI, int WJ, bool VH, bool CONV = false>
 __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, GemmArgs rd, int tr_blocks) {
   constexpr int NW = WI * WJ, NT = 64 * NW, WTI = BI / WI, WTJ = BJ / WJ;
   if (VH && (int)blockIdx.x >= tr_blocks) {
@@ -1116,7 +1278,7 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
   }
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
   typedef TrDma<BI, NW> DA;
-  typedef TrDma<BJ, NW> DB;
+  typedef typename std::conditional<CONV, TrDmaConv<BJ, NW>, TrDma<BJ, NW>>::type DB;
   constexpr int ABYTES = TR * BI * 2, STAGE = ABYTES + TR * BJ * 2;
   constexpr int PERT = DA::PER + DB::PER;
   static_assert(TR == 64, "two 32-deep MFMA steps per stage");
@@ -1145,7 +1307,8 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
   DA da;
   DB db;
   da.init(g.a + i0, g.lda, g.I - i0, g.R, wave, lane);
-  db.init(reinterpret_cast<const uint16_t*>(g.b) + j0, g.ldb, g.J - j0, g.R, wave, lane);
+  if constexpr (CONV) db.init(g, j0, wave, lane);
+  else db.init(reinterpret_cast<const uint16_t*>(g.b) + j0, g.ldb, g.J - j0, g.R, wave, lane);
   const uint32_t ring_lds = lds_addr(ring);
   const lds_char* ring_p = (const lds_char*)ring;
   auto dma_stage = [&](int s) {
@@ -1226,8 +1389,12 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
 // a row-major [r][col] tile (ds_write_b64, the 32-byte windows swizzled as in
 // TrDma); the compute waves read the MFMA fragments with ds_read_b64_tr_b16.
 // Thread t: columns 4 (t % (COLS / 4)), rows 8 (t / (COLS / 4)) .. + 7.
-template <int COLS, int NT, bool PACKED>
+// CONV (bf16 only): the weight operand of a conv dgrad, W'[n][tap][c] with
+// rows r = tap * N + n of the reduction: a stage (64 rows of one tap) starts
+// at n0 = r0 % N, tap = r0 / N, i.e. at W' + n0 * ld + tap * cb.
+template <int COLS, int NT, bool PACKED, bool CONV = false>
 struct TrRowsB {
+  static_assert(!(CONV && PACKED), "the conv dgrad reads a bf16 weight");
   static constexpr int CG = COLS / 4, RG = NT / CG;
   static_assert(CG * RG == NT && 8 * RG == TR, "one 8-row group per thread covers the stage");
   static constexpr int ROWB = COLS * 2;
@@ -1237,6 +1404,7 @@ struct TrRowsB {
   uint32_t voff;   // row 8 rg, this thread's 4 columns (kOOB past the last column)
   uint32_t ldb;    // row stride in bytes
   int32_t rg, col;
+  int32_t nrows, cb2;   // CONV: rows per tap (N), bytes of a tap block (cb * 2)
   Rsrc rs, es;
   CONCORD_DEV void init(const void* band, int64_t ld, int64_t cols_left, int64_t R, const int8_t* exps, int t) {
     constexpr int ES = PACKED ? 4 : 2;
@@ -1247,8 +1415,24 @@ struct TrRowsB {
     if (PACKED) es = make_rsrc(exps, (uint32_t)R);
     voff = col < cols_left ? (uint32_t)((8 * rg * ld + col) * ES) : kOOB;
   }
+  // CONV: band = W' + first column of the tile (bf16), ld = taps * cb
+  CONCORD_DEV void init_conv(const GemmArgs& g, const uint16_t* band, int64_t j0, int t) {
+    col = 4 * (t % CG);
+    rg = t / CG;
+    ldb = (uint32_t)(g.ldb * 2);
+    nrows = g.cv.C;
+    cb2 = g.cv.cb * 2;
+    rs = make_rsrc(band, g.cv.w_bytes - (uint32_t)(j0 * 2));
+    voff = col < g.J - j0 ? (uint32_t)(8 * rg) * ldb + (uint32_t)(col * 2) : kOOB;
+  }
   CONCORD_DEV void load(Raw& r, int64_t r0, int64_t rem) const {
-    const uint32_t so = (uint32_t)(r0 * (int64_t)ldb);
+    uint32_t so;
+    if constexpr (CONV) {
+      const int32_t tap = (int32_t)r0 / nrows;
+      so = (uint32_t)((int32_t)r0 - tap * nrows) * ldb + (uint32_t)(tap * cb2);
+    } else {
+      so = (uint32_t)(r0 * (int64_t)ldb);
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const uint32_t o = 8 * rg + e < rem ? voff + e * ldb : kOOB;
@@ -1304,13 +1488,15 @@ CONCORD_DEV void stage_mfma_swz_tr(f32x4 (&acc)[NI][NJ], const uint16_t* la, con
 
 // 8 waves: waves 0-3 compute and move A (dy) by DMA, waves 4-7 load W rows
 // two stages ahead, decode them and write the row-major B tile.
-template <int MODE, int BI, int BJ>
+// CONV (MODE_DGRAD_BF16): the conv dgrad, dy gathered by RowsDmaConv and the
+// weight rows (n, tap) by TrRowsB's conv stage offsets.
+template <int MODE, int BI, int BJ, bool CONV = false>
 __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
   constexpr int NP = 256;
   constexpr int WTI = BI / 2, WTJ = BJ / 2;
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
-  typedef TrRowsB<BJ, NP, MODE == MODE_DGRAD> BL;
-  typedef RowsDma<BI, 4> AD;
+  typedef TrRowsB<BJ, NP, MODE == MODE_DGRAD, CONV> BL;
+  typedef typename std::conditional<CONV, RowsDmaConv<BI, 4, true>, RowsDma<BI, 4>>::type AD;
   __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
   __shared__ __attribute__((aligned(1024))) char lds_b[2][BL::LBYTES];
 
@@ -1339,7 +1525,8 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
     const int tp = t - NP;
     BL bl;
     const int esz = MODE == MODE_DGRAD ? 4 : 2;
-    bl.init(reinterpret_cast<const char*>(g.b) + j0 * esz, g.ldb, g.J - j0, g.R, g.row_exp, tp);
+    if constexpr (CONV) bl.init_conv(g, reinterpret_cast<const uint16_t*>(g.b) + j0, j0, tp);
+    else bl.init(reinterpret_cast<const char*>(g.b) + j0 * esz, g.ldb, g.J - j0, g.R, g.row_exp, tp);
     typename BL::Raw r0, r1;
     auto stage_r = [&](int st) { return r_begin + (int64_t)st * TR; };
     bl.load(r0, stage_r(0), r_end - stage_r(0));
@@ -1357,7 +1544,8 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
     }
   } else {
     AD ad;
-    ad.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, wave, lane);
+    if constexpr (CONV) ad.init(g, i0, wave, lane);
+    else ad.init(g.a + i0 * g.lda, g.lda, g.I - i0, g.R, wave, lane);
     ad.load(lds_a[0], r_begin, r_end - r_begin);
     ad.load(lds_a[1], r_begin + TR, r_end - r_begin - TR);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(AD::PER));
@@ -1573,6 +1761,63 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd0, void* workspace, size_t ws
   hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD, 256, 128>), dim3(pd.ti * pd.tj * pd.splits), dim3(512), 0, st,
                      gd);
   hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true>), dim3(tw + extra), dim3(512), 0, st, gw, gd, tw);
+  return launch_status(what);
+}
+
+// the conv products take the 8-wave DMA kernels only (shape 0 of each mode)
+static FastPlan plan_conv(int mode, int64_t I, int64_t J, int64_t R, size_t room) {
+  const FastShape one[1] = {mode == MODE_FWD_BF16 ? kFwdShapes[0] : mode == MODE_WGRAD ? kWgrShapes[0]
+                                                                                       : kColShapes[0]};
+  return plan(one, I, J, R, room);
+}
+
+size_t gemm_conv_partial_bytes(int mode, int64_t I, int64_t J, int64_t R) {
+  if (I <= 0 || J <= 0) return 0;
+  const FastPlan p = plan_conv(mode, I, J, R, (size_t)-1 / 2);
+  if (p.splits <= 1) return 0;
+  const int bi = mode == MODE_FWD_BF16 ? kFwdShapes[0].bi : mode == MODE_WGRAD ? kWgrShapes[0].bi : kColShapes[0].bi;
+  const int bj = mode == MODE_FWD_BF16 ? kFwdShapes[0].bj : mode == MODE_WGRAD ? kWgrShapes[0].bj : kColShapes[0].bj;
+  return (size_t)p.ti * p.tj * bi * bj * sizeof(float) * p.splits;
+}
+
+int gemm_conv_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_bytes, hipStream_t st,
+                     const char* what) {
+  // the output is written 8 bytes at a time; the non-gathered operand moves
+  // 16-byte chunks
+  if (!(g0.ldc % 4 == 0 && g0.J % 4 == 0 && al(g0.c, 8)) || (g0.vbias && !al(g0.vbias, 8))) return -1;
+  if (g0.cv.C % 64 != 0 || !al(mode == MODE_WGRAD ? g0.b : g0.a, 16)) return -1;
+  if (mode == MODE_FWD_BF16 && !(g0.ldb % 8 == 0 && al(g0.b, 16) && fits31(((g0.J - 1) * g0.ldb + g0.R) * 2)))
+    return -1;
+  if (mode == MODE_DGRAD_BF16 && !(g0.ldb % 4 == 0 && al(g0.b, 8) && g0.cv.cb % 4 == 0)) return -1;
+  if (mode == MODE_WGRAD && !(g0.lda % 8 == 0 && g0.I % 8 == 0 && al(g0.a, 16) && g0.J % 8 == 0 &&
+                              fits31(((g0.R - 1) * g0.lda + g0.I) * 2)))
+    return -1;
+  GemmArgs g = g0;
+  const size_t room = (workspace && ws_bytes > kSplitkCounterBytes) ? ws_bytes - kSplitkCounterBytes : 0;
+  const FastPlan p = plan_conv(mode, g.I, g.J, g.R, room);
+  g.splits = p.splits;
+  g.r_split = p.r_split;
+  g.tiles_i = p.ti;
+  g.tiles_j = p.tj;
+  if (p.splits > 1) g.part = (float*)((char*)workspace + kSplitkCounterBytes);
+  const int blocks = p.ti * p.tj * p.splits;
+  switch (mode) {
+    case MODE_FWD_BF16:
+      hipLaunchKernelGGL((gemm_dma_kernel<MODE_FWD_BF16, 256, 160, true>), dim3(blocks), dim3(512), 0, st, g);
+      launch_reduce<MODE_FWD_BF16, 256, 160, 2, 2>(g, st);
+      break;
+    case MODE_DGRAD_BF16:
+      hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD_BF16, 256, 128, true>), dim3(blocks), dim3(512), 0, st, g);
+      launch_reduce<MODE_DGRAD_BF16, 256, 128, 2, 2>(g, st);
+      break;
+    case MODE_WGRAD:
+      hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, false, true>), dim3(blocks), dim3(512), 0, st, g,
+                         GemmArgs{}, blocks);
+      launch_reduce<MODE_WGRAD, 256, 128, 4, 2>(g, st);
+      break;
+    default:
+      return -1;
+  }
   return launch_status(what);
 }
 

@@ -151,18 +151,20 @@ static MuonLayout muon_layout(int64_t N, int64_t K) {
   auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
   MuonLayout L;
   size_t o = 0;
+  // split-K region of the three products first: its tile counters sit at
+  // the workspace's start for every shape, so the zero state each product
+  // leaves them in holds across calls of different shapes
+  size_t g = gemm_splitk_need(MODE_FWD_BF16, m, m, n);
+  const size_t g2 = gemm_splitk_need(MODE_DGRAD_BF16, m, m, m), g3 = gemm_splitk_need(MODE_DGRAD_BF16, m, n, m);
+  if (g2 > g) g = g2;
+  if (g3 > g) g = g3;
+  L.gemm = o; o += r256(g);
   L.x = o; o += r256((size_t)m * n * 2);
   L.bx = o; o += r256((size_t)m * n * 2);
   L.a = o; o += r256((size_t)m * m * 2);
   L.aa = o; o += r256((size_t)m * m * 2);
   L.part = o; o += r256((size_t)cdiv(N * K, kFrobBlock) * 4);
   L.den = o; o += 256;
-  // split-K region of the three products (tile counters first, zeroed once)
-  size_t g = gemm_splitk_need(MODE_FWD_BF16, m, m, n);
-  const size_t g2 = gemm_splitk_need(MODE_DGRAD_BF16, m, m, m), g3 = gemm_splitk_need(MODE_DGRAD_BF16, m, n, m);
-  if (g2 > g) g = g2;
-  if (g3 > g) g = g3;
-  L.gemm = o; o += r256(g);
   L.total = o;
   return L;
 }
@@ -199,7 +201,7 @@ extern "C" int concord_muon_ns5(const uint16_t* g, int64_t ld_g, int64_t N, int6
   float* part = (float*)(base + L.part);
   float* den = (float*)(base + L.den);
   void* gws = base + L.gemm;
-  const size_t gws_bytes = L.total - L.gemm;
+  const size_t gws_bytes = L.x - L.gemm;
   hipStream_t st = (hipStream_t)stream;
   const bool tr = N > K;
   const int64_t m = tr ? K : N, n = tr ? N : K;

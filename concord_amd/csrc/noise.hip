@@ -243,6 +243,9 @@ static SigmagLayout sigmag_layout(int64_t M, int64_t N, int64_t K) {
   auto r256 = [](size_t b) { return (b + 255) / 256 * 256; };
   SigmagLayout L;
   size_t o = 0;
+  // the product's split-K region first: its tile counters sit at the
+  // workspace's start for every shape (see muon_layout)
+  L.gemm = o; o += r256(gemm_splitk_need(MODE_WGRAD, N, K, M));
   L.dyt = o; o += r256((size_t)M * N * 2);
   L.prod = o; o += r256((size_t)N * K * 2);
   L.part = o; o += r256((size_t)2 * cdiv(N * K, kNoiseBlock) * 4);
@@ -250,7 +253,6 @@ static SigmagLayout sigmag_layout(int64_t M, int64_t N, int64_t K) {
   L.ssum = o; o += 256;
   L.scale = o; o += 256;
   L.eps = o; o += r256((size_t)M * 4);
-  L.gemm = o; o += r256(gemm_splitk_need(MODE_WGRAD, N, K, M));
   L.total = o;
   return L;
 }
@@ -296,7 +298,7 @@ extern "C" int concord_sigmag_noise(uint16_t* grad_w, int64_t ld_g, const uint16
   hipLaunchKernelGGL(token_sum_final_kernel, dim3(1), dim3(64), 0, st, tpart, tb, ssum);
   // P = dyt^T x (the WGRAD product of the scaled dy), bf16
   const int rc = gemm_bf16_run(MODE_WGRAD, dyt, N, x, ld_x, prod, K, N, K, M, w + L.gemm,
-                               L.total - L.gemm, st, "sigmag_noise");
+                               L.dyt - L.gemm, st, "sigmag_noise");
   if (rc != CONCORD_OK) return rc;
   const float Mf = (float)(M > 1 ? M : 1);
   const int64_t nb = cdiv(N * K, kNoiseBlock);

@@ -591,6 +591,54 @@ def _bias_grad(dy):
     return out
 
 
+def _stash_step_args(ctx, layer, wbuf, rmbuf, cmbuf):
+    """The optimizer arguments the module passes to FusedConcordLinearPackedB
+    (ConcordLinearPackedB.forward), stored on ctx for _packed_step."""
+    ctx.packed_w, ctx.row_exp, ctx.col_exp = layer.packed_w, layer.row_exp, layer.col_exp
+    ctx.lr, ctx.alpha, ctx.beta1, ctx.mantissa_bias = layer._lr_buf, layer.alpha, layer.beta1, layer.MANTISSA_BIAS
+    ctx.optimizer_kind = layer.optimizer_kind
+    ctx.weight_decay, ctx.eps, ctx.step_cap = layer.weight_decay, layer._eps_buf, layer.step_cap
+    ctx.v_scale, ctx.precond_p, ctx.gf_consol = layer.v_scale, layer.precond_p, layer.gf_consol
+    ctx.drift_cancel_C, ctx.alpha_v_fast = layer.drift_cancel_C, layer.alpha_v_fast
+    ctx.wd_sv, ctx.wd_sf = layer.wd_sv, layer.wd_sf
+    ctx.mass_preserve, ctx.apply_chase = layer.mass_preserve_v, layer.apply_chase
+    ctx.track_rebalance = layer.track_rebalance
+    ctx.weight_buf, ctx.row_max_buf, ctx.col_max_buf = wbuf, rmbuf, cmbuf
+    ctx.v_row, ctx.v_col, ctx.sum_v_inv = layer.v_row, layer.v_col, layer._sum_v_inv
+    ctx.adafactor_beta2, ctx.track_adafactor_v = float(layer.adafactor_beta2), bool(layer.track_adafactor_v)
+    ctx.gf_trust_delta_sq, ctx.coh_pre = float(layer.gf_trust_delta_sq), layer._coh_pre
+
+
+def _packed_step(ctx, grad_W, prebumped, muon):
+    """The optimizer step of a packed layer's backward from its bf16 grad_W
+    (concord/packed_b.py:1281-1336): watermark zeroing unless the v-hat entry
+    already did it, then the adamw or sgd update of the packed words."""
+    if _DEBUG_CAPTURE is not None:
+        _DEBUG_CAPTURE.append(grad_W.clone())
+    if not prebumped and ctx.track_rebalance:
+        ctx.row_max_buf.zero_()
+        ctx.col_max_buf.zero_()
+    if ctx.optimizer_kind == 'adamw':
+        apply_packed_adamw(
+            ctx.packed_w, grad_W, ctx.weight_buf, ctx.row_exp, ctx.col_exp,
+            ctx.row_max_buf, ctx.col_max_buf, lr=ctx.lr, mantissa_bias=ctx.mantissa_bias,
+            alpha=ctx.alpha, beta1=ctx.beta1, weight_decay=ctx.weight_decay, eps=ctx.eps,
+            step_cap=ctx.step_cap, v_scale=ctx.v_scale, precond_p=ctx.precond_p,
+            gf_consol=ctx.gf_consol, drift_cancel_C=ctx.drift_cancel_C,
+            alpha_v_fast=ctx.alpha_v_fast, wd_sv=ctx.wd_sv, wd_sf=ctx.wd_sf,
+            mass_preserve=ctx.mass_preserve, apply_chase=ctx.apply_chase,
+            track_rebalance=ctx.track_rebalance, v_row=ctx.v_row, v_col=ctx.v_col,
+            sum_v_inv=ctx.sum_v_inv, gf_trust_delta_sq=ctx.gf_trust_delta_sq,
+            coh_pre=ctx.coh_pre, salt_prebumped=prebumped, drive_muon=muon)
+    else:
+        apply_packed_sgd(
+            ctx.packed_w, grad_W, ctx.weight_buf, ctx.row_exp, ctx.col_exp,
+            ctx.row_max_buf, ctx.col_max_buf, lr=ctx.lr, mantissa_bias=ctx.mantissa_bias,
+            alpha=ctx.alpha, beta1=ctx.beta1, alpha_v_fast=ctx.alpha_v_fast,
+            mass_preserve=ctx.mass_preserve, track_rebalance=ctx.track_rebalance,
+            salt_prebumped=prebumped)
+
+
 class FusedConcordLinearPackedB(torch.autograd.Function):
     """Linear forward; backward = dgrad + wgrad + v-hat EMA + packed update.
     Same 33 forward arguments as the reference (concord/packed_b.py:1201-1211).
@@ -708,30 +756,7 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
                 prebumped = True
             else:
                 grad_W = _wgrad(dy, x2)
-        if _DEBUG_CAPTURE is not None:
-            _DEBUG_CAPTURE.append(grad_W.clone())
-        if not prebumped and ctx.track_rebalance:
-            ctx.row_max_buf.zero_()
-            ctx.col_max_buf.zero_()
-        if ctx.optimizer_kind == 'adamw':
-            apply_packed_adamw(
-                ctx.packed_w, grad_W, ctx.weight_buf, ctx.row_exp, ctx.col_exp,
-                ctx.row_max_buf, ctx.col_max_buf, lr=ctx.lr, mantissa_bias=ctx.mantissa_bias,
-                alpha=ctx.alpha, beta1=ctx.beta1, weight_decay=ctx.weight_decay, eps=ctx.eps,
-                step_cap=ctx.step_cap, v_scale=ctx.v_scale, precond_p=ctx.precond_p,
-                gf_consol=ctx.gf_consol, drift_cancel_C=ctx.drift_cancel_C,
-                alpha_v_fast=ctx.alpha_v_fast, wd_sv=ctx.wd_sv, wd_sf=ctx.wd_sf,
-                mass_preserve=ctx.mass_preserve, apply_chase=ctx.apply_chase,
-                track_rebalance=ctx.track_rebalance, v_row=ctx.v_row, v_col=ctx.v_col,
-                sum_v_inv=ctx.sum_v_inv, gf_trust_delta_sq=ctx.gf_trust_delta_sq,
-                coh_pre=ctx.coh_pre, salt_prebumped=prebumped, drive_muon=muon)
-        else:
-            apply_packed_sgd(
-                ctx.packed_w, grad_W, ctx.weight_buf, ctx.row_exp, ctx.col_exp,
-                ctx.row_max_buf, ctx.col_max_buf, lr=ctx.lr, mantissa_bias=ctx.mantissa_bias,
-                alpha=ctx.alpha, beta1=ctx.beta1, alpha_v_fast=ctx.alpha_v_fast,
-                mass_preserve=ctx.mass_preserve, track_rebalance=ctx.track_rebalance,
-                salt_prebumped=prebumped)
+        _packed_step(ctx, grad_W, prebumped, muon)
         if ctx.has_bias and grad_bias is None:
             grad_bias = _bias_grad(dy)
         return (grad_x, None, None, None, grad_bias,
@@ -1192,8 +1217,7 @@ def _pair(v):
 class _Im2col(torch.autograd.Function):
     """(B, C, H, W) bf16 -> the (B * Ho * Wo, C * kh * kw) patch matrix in one
     HIP pass (concord_conv_im2col).  The adjoint gathers dx straight from the
-    patch gradient (concord_conv_col2im: fixed order, fp32 accumulation); a
-    window too large for its staged tile takes torch's fold instead."""
+    patch gradient (concord_conv_col2im: fixed order, fp32 accumulation)."""
 
     @staticmethod
     def forward(ctx, x, kh, kw, sh, sw, ph, pw):
@@ -1210,14 +1234,10 @@ class _Im2col(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dcols):
         B, Cin, H, W, kh, kw, sh, sw, ph, pw, L = ctx.geom
-        if dcols.dtype == torch.bfloat16 and C.lib().concord_conv_col2im_fits(kh, kw, sh, sw):
-            dcols = dcols.contiguous()
-            dx = torch.empty((B, Cin, H, W), dtype=torch.bfloat16, device=dcols.device)
-            C.check(C.lib().concord_conv_col2im(C.ptr(dcols), B, Cin, H, W, kh, kw, sh, sw, ph, pw, C.ptr(dx),
-                                                C.stream_of(dcols.device)), "conv_col2im")
-        else:
-            u = dcols.reshape(B, L, Cin * kh * kw).transpose(1, 2)
-            dx = F.fold(u, (H, W), (kh, kw), padding=(ph, pw), stride=(sh, sw))
+        dcols = dcols.to(torch.bfloat16).contiguous()
+        dx = torch.empty((B, Cin, H, W), dtype=torch.bfloat16, device=dcols.device)
+        C.check(C.lib().concord_conv_col2im(C.ptr(dcols), B, Cin, H, W, kh, kw, sh, sw, ph, pw, C.ptr(dx),
+                                            C.stream_of(dcols.device)), "conv_col2im")
         return dx, None, None, None, None, None, None
 
 
@@ -1246,17 +1266,127 @@ class _ToNCHW(torch.autograd.Function):
         return d2, None, None, None
 
 
+_CONV_WORKSPACES = {}
+
+
+def _conv_workspace(device, geom):
+    """Zero-initialised per-device split-K workspace of the implicit conv
+    products, grown to the largest geometry seen."""
+    key = _dev_key(device)
+    need = int(C.lib().concord_conv_workspace_bytes(*geom))
+    ws = _CONV_WORKSPACES.get(key)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(need, dtype=torch.uint8, device=key)
+        _CONV_WORKSPACES[key] = ws
+    return ws
+
+
+def _nhwc(t):
+    """(B, C, H, W) -> its channels-last storage viewed as (B, H, W, C)
+    (no copy when t already is channels-last contiguous)."""
+    if t.dtype != torch.bfloat16:
+        t = t.to(torch.bfloat16)
+    return t.contiguous(memory_format=torch.channels_last).permute(0, 2, 3, 1)
+
+
+class FusedConcordConv2dImplicit(torch.autograd.Function):
+    """Conv2d over the packed state by implicit GEMM on channels-last
+    activations (FusedConcordConv2dPackedB, concord/packed_b.py:1863-2025,
+    where the reference runs cuDNN on the cached bf16 weight).  Forward:
+    W'[n][tap][c] decoded from the packed words (concord_conv_weight_taps),
+    y = conv(x, W') + bias with the patches gathered inside the GEMM
+    (concord_conv_fwd).  Backward: dx by the transposed gather
+    (concord_conv_dgrad, on the pre-update W'), grad_W by the gathered WGRAD
+    (concord_conv_wgrad) put back in (c, tap) order, then the layer's
+    optimizer step (v-hat EMA, packed update), as the linear path takes it.
+    The output and dx are channels-last NCHW tensors."""
+
+    @staticmethod
+    def forward(ctx, x, bias, layer, geom, wbuf, rmbuf, cmbuf):
+        B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw = geom
+        Ho = (H + 2 * ph - kh) // sh + 1
+        Wo = (W + 2 * pw - kw) // sw + 1
+        T = kh * kw
+        dev = x.device
+        st = C.stream_of(dev)
+        x4 = _nhwc(x)
+        pw_ = layer.packed_w
+        wt = torch.empty((Cout, T * Cin), dtype=torch.bfloat16, device=dev)
+        C.check(C.lib().concord_conv_weight_taps(
+            C.ptr(pw_), pw_.stride(0), C.ptr(layer.row_exp), C.ptr(layer.col_exp), Cout, Cin, T,
+            layer.MANTISSA_BIAS, float(layer.fast_gain), C.ptr(wt), st), "conv_weight_taps")
+        bias_bf16 = None
+        if bias is not None:
+            bias_bf16 = (bias if bias.dtype == torch.bfloat16 else bias.to(torch.bfloat16)).contiguous()
+        y2 = torch.empty((B * Ho * Wo, Cout), dtype=torch.bfloat16, device=dev)
+        ws = _conv_workspace(dev, geom)
+        C.check(C.lib().concord_conv_fwd(C.ptr(x4), C.ptr(wt), C.ptr(bias_bf16), C.ptr(y2), *geom, C.ptr(ws),
+                                         ws.numel(), st), "conv_fwd")
+        ctx.save_for_backward(x4, wt)
+        ctx.geom, ctx.out_hw = geom, (Ho, Wo)
+        ctx.drive = layer.drive
+        ctx.has_bias = bias is not None
+        _stash_step_args(ctx, layer, wbuf, rmbuf, cmbuf)
+        return y2.view(B, Ho, Wo, Cout).permute(0, 3, 1, 2)
+
+    @staticmethod
+    def backward(ctx, grad_y):
+        x4, wt = ctx.saved_tensors
+        geom = ctx.geom
+        B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw = geom
+        Ho, Wo = ctx.out_hw
+        T = kh * kw
+        dy2 = _nhwc(grad_y).reshape(B * Ho * Wo, Cout)
+        dev = dy2.device
+        st = C.stream_of(dev)
+        ws = _conv_workspace(dev, geom)
+        grad_x = None
+        if ctx.needs_input_grad[0]:
+            dx = torch.empty((B, H, W, Cin), dtype=torch.bfloat16, device=dev)
+            C.check(C.lib().concord_conv_dgrad(C.ptr(dy2), C.ptr(wt), C.ptr(dx), *geom, C.ptr(ws), ws.numel(),
+                                               st), "conv_dgrad")
+            grad_x = dx.permute(0, 3, 1, 2)
+        gt = torch.empty((Cout, T * Cin), dtype=torch.bfloat16, device=dev)
+        C.check(C.lib().concord_conv_wgrad(C.ptr(dy2), C.ptr(x4), C.ptr(gt), *geom, C.ptr(ws), ws.numel(), st),
+                "conv_wgrad")
+        grad_W = torch.empty((Cout, Cin * T), dtype=torch.bfloat16, device=dev)
+        C.check(C.lib().concord_conv_grad_from_taps(C.ptr(gt), Cout, Cin, T, C.ptr(grad_W), grad_W.stride(0), st),
+                "conv_grad_from_taps")
+        salt = _get_step_counter(dev)
+        muon = ctx.drive == 'muon' and ctx.optimizer_kind == 'adamw'
+        vhat = ctx.track_adafactor_v and ctx.v_row is not None
+        prebumped = False
+        if muon:
+            grad_W = muon_ns5(grad_W)
+        if _SIGMAG_NOISE:
+            if not (muon or _SIGMAG_ISO):
+                raise RuntimeError("ConcordConv2dPackedB: the Sigma_g noise draw was switched on between this "
+                                   "layer's forward (implicit-GEMM path) and its backward")
+            iso_noise_(grad_W, salt_counter=salt)
+        if vhat and not muon:
+            vhat_ema(grad_W, ctx.v_row, ctx.v_col, ctx.sum_v_inv, ctx.adafactor_beta2,
+                     ctx.row_max_buf if ctx.track_rebalance else None,
+                     ctx.col_max_buf if ctx.track_rebalance else None, salt)
+            prebumped = True
+        _packed_step(ctx, grad_W, prebumped, muon)
+        grad_bias = _bias_grad(dy2) if ctx.has_bias else None
+        return grad_x, grad_bias, None, None, None, None, None
+
+
 class ConcordConv2dPackedB(ConcordLinearPackedB):
     """Conv2d variant of ConcordLinearPackedB (concord/packed_b.py:2028-2065):
     the same packed int32 state, an (out_channels, in_channels * kh * kw)
     matrix in nn.Conv2d's (c, i, j) flattening.  Where the reference runs
-    cuDNN on the cached bf16 weight, this layer runs the linear layer's own
-    kernels on the patch matrix: the (B * Ho * Wo, in_channels * kh * kw)
-    patches are gathered in one HIP pass (concord_conv_im2col; for a 1x1
-    kernel a transpose to channels-last), the adjoint gathers dx back from the
-    patch gradient in another (concord_conv_col2im), and the (positions,
-    out_channels) product is transposed to NCHW by the 1x1 col2im.  Forward, dgrad, wgrad with v-hat and bias, and the
-    packed update are the HIP entries of the linear path."""
+    cuDNN on the cached bf16 weight, this layer takes one of three HIP paths:
+      * 1 x 1, stride 1, no padding: the linear layer's fused dequant-GEMM
+        path on the channels-last positions (B * H * W, in_channels);
+      * in and out channels multiples of 64, strides 1 or 2: implicit GEMM
+        (FusedConcordConv2dImplicit) -- the patches are gathered inside the
+        GEMM kernels from channels-last activations, no patch matrix;
+      * otherwise (e.g. a 4-channel latent input): the patch matrix is
+        gathered in one HIP pass (concord_conv_im2col), the linear path runs
+        on it, and col2im gathers dx back (concord_conv_col2im).
+    The first two return channels-last NCHW tensors."""
 
     def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, bias=True,
                  device='cuda', alpha=0.1, beta1=0.0, lr=0.01, weight_cache=False, drive='vhat'):
@@ -1270,16 +1400,24 @@ class ConcordConv2dPackedB(ConcordLinearPackedB):
                          device=device, alpha=alpha, beta1=beta1, lr=lr, weight_cache=weight_cache,
                          drive=drive)
 
-    def _patches(self, x):
+    def _geom(self, x):
         B, cin, H, W = x.shape
         if cin != self.in_channels:
             raise ValueError(f"ConcordConv2dPackedB: expected {self.in_channels} input channels, "
                              f"got {cin}")
         (sh, sw), (ph, pw) = _pair(self.stride), _pair(self.padding)
-        Ho = (H + 2 * ph - self.kh) // sh + 1
-        Wo = (W + 2 * pw - self.kw) // sw + 1
-        cols = _Im2col.apply(x, self.kh, self.kw, sh, sw, ph, pw)
-        return cols, Ho, Wo
+        return (B, cin, H, W, self.out_channels, self.kh, self.kw, sh, sw, ph, pw)
+
+    def conv_path(self, x):
+        """'linear' (1 x 1), 'implicit' or 'im2col': the path forward(x) takes."""
+        B, cin, H, W, cout, kh, kw, sh, sw, ph, pw = self._geom(x)
+        if kh == kw == sh == sw == 1 and ph == pw == 0:
+            return 'linear'
+        # the Sigma_g noise draw needs the patch matrix
+        sigmag = _SIGMAG_NOISE and not _SIGMAG_ISO and self.drive != 'muon'
+        if not sigmag and C.lib().concord_conv_implicit_ok(B, cin, H, W, cout, kh, kw, sh, sw, ph, pw):
+            return 'implicit'
+        return 'im2col'
 
     def forward(self, x):
         if x.dim() != 4:
@@ -1287,8 +1425,20 @@ class ConcordConv2dPackedB(ConcordLinearPackedB):
         in_dtype = x.dtype
         if x.dtype != torch.bfloat16:
             x = x.to(torch.bfloat16)
-        cols, Ho, Wo = self._patches(x)
-        y = _ToNCHW.apply(super().forward(cols), x.shape[0], Ho, Wo)
+        geom = self._geom(x)
+        B, cin, H, W, cout, kh, kw, sh, sw, ph, pw = geom
+        path = self.conv_path(x)
+        if path == 'linear':
+            x2 = _nhwc(x).reshape(B * H * W, cin)
+            y = super().forward(x2).view(B, H, W, cout).permute(0, 3, 1, 2)
+        elif path == 'implicit':
+            wbuf, rmbuf, cmbuf = self._ensure_buffers()
+            y = FusedConcordConv2dImplicit.apply(x, self.bias, self, geom, wbuf, rmbuf, cmbuf)
+        else:
+            Ho = (H + 2 * ph - kh) // sh + 1
+            Wo = (W + 2 * pw - kw) // sw + 1
+            cols = _Im2col.apply(x, kh, kw, sh, sw, ph, pw)
+            y = _ToNCHW.apply(super().forward(cols), B, Ho, Wo)
         return y.to(in_dtype)
 
     @property

@@ -350,11 +350,59 @@ int concord_conv_im2col(const uint16_t* x, int64_t B, int64_t C, int64_t H, int6
  * the (i, j) with ho * sh = h + ph - i, wo * sw = w + pw - j, 0 <= ho < Ho,
  * 0 <= wo < Wo; fp32 accumulation.  Replaces the conv's input-gradient path
  * of the reference's conv class (cuDNN there).  concord_conv_col2im_fits
- * says whether the window fits the kernel's staged tile (non-zero) for the
- * given kernel size and stride. */
+ * says whether the window fits the kernel's staged LDS tile (non-zero) for
+ * the given kernel size and stride; a window that does not is gathered by
+ * an unstaged kernel with the same summation order. */
 int concord_conv_col2im(const uint16_t* dcols, int64_t B, int64_t C, int64_t H, int64_t W, int64_t kh, int64_t kw,
                         int64_t sh, int64_t sw, int64_t ph, int64_t pw, uint16_t* dx, void* stream);
 int concord_conv_col2im_fits(int64_t kh, int64_t kw, int64_t sh, int64_t sw);
+
+/* Implicit-GEMM convolution: FusedConcordConv2dPackedB's three products
+ * (concord/packed_b.py:1889-1941: F.conv2d, conv2d_input and conv2d_weight
+ * on the cached bf16 weight, cuDNN there) with the patches gathered inside
+ * the GEMM kernels, never written.  Geometry (B, Cin, H, W, Cout, kh, kw,
+ * sh, sw, ph, pw) as nn.Conv2d's: Ho = (H + 2 ph - kh) / sh + 1, Wo
+ * likewise.  Activations are channels-last (NHWC) bf16: x[B][H][W][Cin],
+ * y and dy [B][Ho][Wo][Cout], dx [B][H][W][Cin].  The weight is tap-major,
+ * wt[Cout][kh * kw][Cin] (concord_conv_weight_taps); the WGRAD writes its
+ * gradient gt in that order and concord_conv_grad_from_taps puts it back in
+ * the packed words' (Cin, kh, kw) order.  The products accumulate in fp32
+ * and round once to bf16 (split-K partials summed in a fixed order).
+ * concord_conv_implicit_ok: non-zero when the kernels take the geometry
+ * (Cin and Cout multiples of 64, strides 1 or 2, fewer than 2^24 positions
+ * and operands below 2^30 bytes); the three products return CONCORD_EINVAL
+ * otherwise.  The workspace (concord_conv_workspace_bytes, zero-initialised
+ * once, kept between calls) holds split-K counters and partials. */
+int concord_conv_implicit_ok(int64_t B, int64_t Cin, int64_t H, int64_t W, int64_t Cout, int64_t kh, int64_t kw,
+                             int64_t sh, int64_t sw, int64_t ph, int64_t pw);
+size_t concord_conv_workspace_bytes(int64_t B, int64_t Cin, int64_t H, int64_t W, int64_t Cout, int64_t kh,
+                                    int64_t kw, int64_t sh, int64_t sw, int64_t ph, int64_t pw);
+/* wt[n][t][c] = the forward weight of packed word (n, c * taps + t):
+ * bf16(((128 ss + g sf) + 128 vs) 2^(row_exp + col_exp - bias)) in fp32
+ * (concord/packed_b.py:1763-1772; g = fast_gain, 1 for the plain decode of
+ * 120-170).  taps <= 64. */
+int concord_conv_weight_taps(const int32_t* packed, int64_t ld_p, const int8_t* row_exp, const int8_t* col_exp,
+                             int64_t Cout, int64_t Cin, int64_t taps, int32_t mantissa_bias, float fast_gain,
+                             uint16_t* wt, void* stream);
+/* g[n][c * taps + t] = gt[n][t][c] (ld_g >= Cin * taps); taps <= 64. */
+int concord_conv_grad_from_taps(const uint16_t* gt, int64_t Cout, int64_t Cin, int64_t taps, uint16_t* g,
+                                int64_t ld_g, void* stream);
+/* y = conv(x, wt) + bias (bias may be NULL), y[b][ho][wo][n]. */
+int concord_conv_fwd(const uint16_t* x, const uint16_t* wt, const uint16_t* bias, uint16_t* y, int64_t B,
+                     int64_t Cin, int64_t H, int64_t W, int64_t Cout, int64_t kh, int64_t kw, int64_t sh,
+                     int64_t sw, int64_t ph, int64_t pw, void* workspace, size_t workspace_bytes, void* stream);
+/* dx = conv2d_input(dy, wt): dx[b][h][w][c] = sum over (ky, kx, n) with
+ * ho sh = h + ph - ky, wo sw = w + pw - kx inside the output grid of
+ * dy[b][ho][wo][n] wt[n][ky kw + kx][c]. */
+int concord_conv_dgrad(const uint16_t* dy, const uint16_t* wt, uint16_t* dx, int64_t B, int64_t Cin, int64_t H,
+                       int64_t W, int64_t Cout, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
+                       int64_t pw, void* workspace, size_t workspace_bytes, void* stream);
+/* gt = conv2d_weight(x, dy) in tap-major order: gt[n][ky kw + kx][c] =
+ * sum over positions (b, ho, wo) of dy[b][ho][wo][n] x[b][ho sh - ph + ky]
+ * [wo sw - pw + kx][c] (0 outside the image). */
+int concord_conv_wgrad(const uint16_t* dy, const uint16_t* x, uint16_t* gt, int64_t B, int64_t Cin, int64_t H,
+                       int64_t W, int64_t Cout, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
+                       int64_t pw, void* workspace, size_t workspace_bytes, void* stream);
 
 /* The Sigma_g-shaped draw, the reference's default when its noise is on
  * (notebook/src/prototype_packed_b.py:1489-1500): in place on the bf16

@@ -171,3 +171,255 @@ def test_col2im_matches_fp32_fold(oracle, geom):
     g = oracle.bf16_bits_to_f32(host(got)).astype(np.float64)
     tol = 2.0 ** -8 * np.abs(exact) + 2.0 ** -20 * mag
     assert np.all(np.abs(g - exact) <= tol), np.max(np.abs(g - exact) - tol)
+
+
+# ---------------------------------------------------------------- implicit GEMM
+# (cin, cout, k, stride, pad, B, H, W); channels multiples of 64, so these
+# take the implicit-GEMM path: ragged spatial sizes (positions not a multiple
+# of the 256-row tile), stride 2, mixed strides / paddings, a 5 x 5 kernel,
+# an image row wider than a 64-position stage
+IMPLICIT = [
+    (64, 64, 3, 1, 1, 2, 20, 24),
+    (128, 64, 3, 2, 1, 2, 17, 15),
+    (64, 128, 3, 1, 1, 1, 9, 70),
+    (64, 64, (3, 1), (2, 1), (1, 0), 3, 11, 13),
+    (64, 192, 5, 1, 2, 1, 12, 10),
+    (192, 64, 3, 2, 0, 2, 16, 16),
+]
+
+
+def _geom(case):
+    from torch.nn.modules.utils import _pair
+    cin, cout, k, stride, pad, B, H, W = case
+    (kh, kw), (sh, sw), (ph, pw) = _pair(k), _pair(stride), _pair(pad)
+    return (B, cin, H, W, cout, kh, kw, sh, sw, ph, pw)
+
+
+def test_conv_paths():
+    """SDXL's convs take the expected path: the 4-channel latent input and
+    output through the patch matrix, every resnet / downsample conv by
+    implicit GEMM, 1 x 1 projections through the linear path."""
+    import concord_amd as ca
+    cases = [((4, 320, 3, 1, 1), (2, 4, 128, 128), 'im2col'),
+             ((320, 320, 3, 1, 1), (2, 320, 128, 128), 'implicit'),
+             ((320, 320, 3, 2, 1), (2, 320, 128, 128), 'implicit'),
+             ((640, 1280, 3, 1, 1), (2, 640, 32, 32), 'implicit'),
+             ((960, 640, 1, 1, 0), (2, 960, 64, 64), 'linear'),
+             ((320, 4, 3, 1, 1), (2, 320, 128, 128), 'im2col')]
+    for (cin, cout, k, s, p), shape, want in cases:
+        conv = ca.ConcordConv2dPackedB(cin, cout, k, stride=s, padding=p, device=DEV)
+        x = torch.empty(shape, device=DEV, dtype=torch.bfloat16)
+        assert conv.conv_path(x) == want, ((cin, cout, k, s, p), shape)
+
+
+@pytest.mark.parametrize("case", IMPLICIT)
+def test_implicit_products_match_fp32(case):
+    """y, dx, the weight gradient the update consumes and the bias gradient
+    of the implicit-GEMM path against fp32 torch convolutions of the decoded
+    weight (rel-L2 <= 1e-2)."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    cin, cout, k, stride, pad, B, H, W = case
+    torch.manual_seed(7)
+    conv = ca.ConcordConv2dPackedB(cin, cout, k, stride=stride, padding=pad, bias=True, device=DEV, lr=1e-3)
+    with torch.no_grad():
+        conv.bias.copy_((torch.randn(cout) * 0.1).to(torch.bfloat16))
+    Wd = conv.weight.detach().float().clone()
+    bd = conv.bias.detach().float().clone()
+    x = torch.randn(B, cin, H, W, device=DEV).to(torch.bfloat16)
+    assert conv.conv_path(x) == 'implicit'
+    xc = x.clone().requires_grad_(True)
+    cap = []
+    pb._DEBUG_CAPTURE = cap
+    try:
+        y = conv(xc)
+        gy = (torch.randn_like(y.float()) * 1e-2).to(torch.bfloat16)
+        y.backward(gy)
+    finally:
+        pb._DEBUG_CAPTURE = None
+    sync()
+    torch.backends.cudnn.allow_tf32 = False
+    xf = x.float().requires_grad_(True)
+    yf = F.conv2d(xf, Wd, bd, stride=stride, padding=pad)
+    yf.backward(gy.float())
+    gw = torch.nn.grad.conv2d_weight(x.float(), Wd.shape, gy.float(), stride=stride, padding=pad)
+    assert y.shape == yf.shape and xc.grad.shape == x.shape
+    assert rel_l2(host(y.float()), host(yf)) < 1e-2
+    assert rel_l2(host(xc.grad.float()), host(xf.grad)) < 1e-2
+    assert rel_l2(host(cap[0].float()), host(gw.reshape(cout, -1))) < 1e-2
+    assert rel_l2(host(conv.bias.grad.float()), host(gy.float().sum(dim=(0, 2, 3)))) < 1e-2
+
+
+@pytest.mark.parametrize("case", IMPLICIT[:3])
+def test_implicit_abi_products_float64(oracle, case):
+    """The three C-ABI products on random bf16 operands against float64
+    references: each output is one fp32 sum rounded once to bf16, so
+    |got - exact| <= 2^-8 |exact| + 2^-17 sum |terms| elementwise."""
+    from concord_amd import _lib as C
+    from concord_amd import packed_b as pb
+    geom = _geom(case)
+    B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw = geom
+    T = kh * kw
+    Ho, Wo = (H + 2 * ph - kh) // sh + 1, (W + 2 * pw - kw) // sw + 1
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(B, H, W, Cin, generator=g).to(torch.bfloat16)
+    dy = torch.randn(B, Ho, Wo, Cout, generator=g).to(torch.bfloat16)
+    wt = (torch.randn(Cout, T, Cin, generator=g) * 0.1).to(torch.bfloat16)
+    bias = (torch.randn(Cout, generator=g) * 0.1).to(torch.bfloat16)
+    xd, dyd, wtd, bd = x.to(DEV), dy.to(DEV), wt.to(DEV), bias.to(DEV)
+    ws = pb._conv_workspace(torch.device(DEV), geom)
+    st = C.stream_of(torch.device(DEV))
+    y = torch.empty(B, Ho, Wo, Cout, dtype=torch.bfloat16, device=DEV)
+    dx = torch.empty(B, H, W, Cin, dtype=torch.bfloat16, device=DEV)
+    gt = torch.empty(Cout, T, Cin, dtype=torch.bfloat16, device=DEV)
+    C.check(C.lib().concord_conv_fwd(C.ptr(xd), C.ptr(wtd), C.ptr(bd), C.ptr(y), *geom, C.ptr(ws), ws.numel(), st),
+            "conv_fwd")
+    C.check(C.lib().concord_conv_dgrad(C.ptr(dyd), C.ptr(wtd), C.ptr(dx), *geom, C.ptr(ws), ws.numel(), st),
+            "conv_dgrad")
+    C.check(C.lib().concord_conv_wgrad(C.ptr(dyd), C.ptr(xd), C.ptr(gt), *geom, C.ptr(ws), ws.numel(), st),
+            "conv_wgrad")
+    sync()
+    x64 = x.double().permute(0, 3, 1, 2)
+    W64 = wt.double().view(Cout, kh, kw, Cin).permute(0, 3, 1, 2)
+    dy64 = dy.double().permute(0, 3, 1, 2)
+    checks = [
+        (y, F.conv2d(x64, W64, bias.double(), stride=(sh, sw), padding=(ph, pw)).permute(0, 2, 3, 1),
+         F.conv2d(x64.abs(), W64.abs(), bias.double().abs(), stride=(sh, sw), padding=(ph, pw)).permute(0, 2, 3, 1)),
+        (dx, torch.nn.grad.conv2d_input(x64.shape, W64, dy64, stride=(sh, sw), padding=(ph, pw)).permute(0, 2, 3, 1),
+         torch.nn.grad.conv2d_input(x64.shape, W64.abs(), dy64.abs(), stride=(sh, sw),
+                                    padding=(ph, pw)).permute(0, 2, 3, 1)),
+        (gt, torch.nn.grad.conv2d_weight(x64, W64.shape, dy64, stride=(sh, sw), padding=(ph, pw))
+         .permute(0, 2, 3, 1).reshape(Cout, T, Cin),
+         torch.nn.grad.conv2d_weight(x64.abs(), W64.shape, dy64.abs(), stride=(sh, sw), padding=(ph, pw))
+         .permute(0, 2, 3, 1).reshape(Cout, T, Cin)),
+    ]
+    for got, exact, mag in checks:
+        gv = oracle.bf16_bits_to_f32(host(got)).astype(np.float64)
+        ex, mg = exact.numpy(), mag.numpy()
+        tol = 2.0 ** -8 * np.abs(ex) + 2.0 ** -17 * mg
+        assert np.all(np.abs(gv - ex) <= tol), float(np.max(np.abs(gv - ex) - tol))
+
+
+@pytest.mark.parametrize("gain", [1.0, 0.37])
+def test_weight_taps_bit_exact(oracle, gain):
+    """W'[n][t][c] is the oracle's (gated) decode of word (n, c * taps + t)."""
+    from concord_amd import _lib as C
+    from gpu_util import dev, rand_state
+    rng = np.random.default_rng(5)
+    for Cout, Cin, T in [(64, 64, 9), (37, 130, 9), (5, 7, 25), (3, 64, 1)]:
+        packed, re, ce = rand_state(rng, Cout, Cin * T, sf=(-32768, 32768), exp=(-8, 7), col=(-8, 7))
+        wt = torch.empty(Cout, T, Cin, dtype=torch.bfloat16, device=DEV)
+        # the device copies stay referenced until the kernel has run
+        pd, red, ced = dev(packed), dev(re), dev(ce)
+        C.check(C.lib().concord_conv_weight_taps(C.ptr(pd), Cin * T, C.ptr(red), C.ptr(ced), Cout, Cin, T, 15, gain,
+                                                 C.ptr(wt), C.stream_of(torch.device(DEV))), "conv_weight_taps")
+        sync()
+        want = (oracle.materialize(packed, re, ce) if gain == 1.0 else
+                oracle.materialize_gated(packed, re, ce, gain))
+        np.testing.assert_array_equal(host(wt), want.reshape(Cout, Cin, T).transpose(0, 2, 1))
+
+
+def test_grad_from_taps_is_the_permutation():
+    from concord_amd import _lib as C
+    for Cout, Cin, T in [(64, 64, 9), (37, 130, 9), (5, 7, 25), (3, 64, 1)]:
+        gt = torch.randint(-2 ** 15, 2 ** 15, (Cout, T, Cin), dtype=torch.int16, device=DEV).view(torch.bfloat16)
+        g = torch.full((Cout, Cin * T + 3), 7, dtype=torch.int16, device=DEV).view(torch.bfloat16)
+        C.check(C.lib().concord_conv_grad_from_taps(C.ptr(gt), Cout, Cin, T, C.ptr(g), g.stride(0),
+                                                    C.stream_of(torch.device(DEV))), "conv_grad_from_taps")
+        sync()
+        want = host(gt).transpose(0, 2, 1).reshape(Cout, Cin * T)
+        np.testing.assert_array_equal(host(g)[:, :Cin * T], want)
+        assert (host(g)[:, Cin * T:] == 7).all()
+
+
+@pytest.mark.parametrize("case", [IMPLICIT[0], IMPLICIT[1]])
+def test_implicit_layer_state_vs_oracle(oracle, case):
+    """Three training steps of an implicit-GEMM conv layer (default flags,
+    coh_pre on): the v-hat, packed words, exponents after rebalance and the
+    bf16 forward weight, bit-exact against the oracle fed each step's
+    captured bf16 gradient (in the packed (c, tap) order)."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    O = oracle
+    cin, cout, k, stride, pad, B, H, W = case
+    torch.manual_seed(21)
+    conv = ca.ConcordConv2dPackedB(cin, cout, k, stride=stride, padding=pad, bias=True, device=DEV, lr=2e-3)
+    W0 = torch.randn(cout, cin * k * k) * 0.05
+    conv.load_weights(W0)
+    p0, r0, c0 = O.load_weights(W0.numpy())
+    np.testing.assert_array_equal(host(conv.packed_w), p0)
+    K = cin * k * k
+    st = [p0.copy(), r0.copy(), c0.copy(), np.zeros(cout, np.float32), np.zeros(K, np.float32)]
+    coh = np.ones((cout, K), np.float32)
+    flags = O.MASS_PRESERVE | O.APPLY_CHASE | O.TRACK_REBALANCE | O.GF_TRUST_REGION | O.FIXED_COH | O.COHPRE
+    P = O.UpdateParams(alpha=0.1, beta1=0.0, weight_decay=0.0, step_cap=10.0, v_scale=0.0, precond_p=0.5,
+                       gf_consol=0.0, drift_cancel_C=conv.drift_cancel_C, alpha_v_fast=0.001, wd_sv=0.0,
+                       wd_sf=0.0, gf_trust_delta_sq=1.0, gate_gain=1.0, mantissa_bias=15)
+    for step in range(3):
+        salt_next = int(host(pb._get_step_counter(DEV))[0]) + 1
+        x = torch.randn(B, cin, H, W, device=DEV).to(torch.bfloat16).requires_grad_(True)
+        cap = []
+        pb._DEBUG_CAPTURE = cap
+        try:
+            y = conv(x)
+            y.backward((torch.randn_like(y.float()) * 3e-2).to(torch.bfloat16))
+        finally:
+            pb._DEBUG_CAPTURE = None
+        conv.rebalance()
+        sync()
+        g = host(cap[0])
+        svi = O.vhat_ema(g, st[3], st[4], 0.999)
+        rm = np.zeros(cout, np.int32)
+        cm = np.zeros(K, np.int32)
+        S = O.UpdateScalars(lr=2e-3, eps=1e-10, chase_floor=0.9, leak_floor=0.999, v_bc=1.0, salt=salt_next,
+                            consolidate=1)
+        O.apply_adamw(st[0], g, None, st[1], st[2], rm, cm, st[3], st[4], svi, coh, P, S, flags)
+        O.rebalance(st[0], st[1], st[2], rm, cm, seed=step + 1)
+        np.testing.assert_array_equal(host(conv.v_row), st[3])
+        np.testing.assert_array_equal(host(conv.v_col), st[4])
+        np.testing.assert_array_equal(host(conv.packed_w), st[0])
+        np.testing.assert_array_equal(host(conv.row_exp), st[1])
+        np.testing.assert_array_equal(host(conv.col_exp), st[2])
+    np.testing.assert_array_equal(host(conv.get_weight()), O.materialize(st[0], st[1], st[2]))
+
+
+# SDXL-UNet conv shapes at batch 2 of a 1024 px latent: the 3 x 3 resnet
+# convs per level (320 ch at 128^2, 640 at 64^2, 1280 at 32^2), a stride-2
+# downsample, and the level-crossing 640 -> 1280 conv
+SDXL_CONV = [(320, 320, 3, 1, 1, 2, 128, 128), (640, 640, 3, 1, 1, 2, 64, 64), (1280, 1280, 3, 1, 1, 2, 32, 32),
+             (640, 640, 3, 2, 1, 2, 64, 64), (640, 1280, 3, 1, 1, 2, 32, 32)]
+
+
+@pytest.mark.parametrize("case", SDXL_CONV)
+def test_sdxl_conv_shapes(case):
+    """One training step of each SDXL conv shape on the implicit path: y, dx
+    and the captured weight gradient against fp32 torch convolutions of the
+    decoded weight (rel-L2 <= 1e-2), finite packed state after the update."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    cin, cout, k, stride, pad, B, H, W = case
+    torch.manual_seed(3)
+    conv = ca.ConcordConv2dPackedB(cin, cout, k, stride=stride, padding=pad, bias=True, device=DEV, lr=5e-4)
+    Wd = conv.weight.detach().float().clone()
+    x = torch.randn(B, cin, H, W, device=DEV).to(torch.bfloat16)
+    assert conv.conv_path(x) == 'implicit'
+    xc = x.clone().requires_grad_(True)
+    cap = []
+    pb._DEBUG_CAPTURE = cap
+    try:
+        y = conv(xc)
+        gy = (torch.randn_like(y.float()) * 1e-3).to(torch.bfloat16)
+        y.backward(gy)
+    finally:
+        pb._DEBUG_CAPTURE = None
+    conv.rebalance()
+    sync()
+    torch.backends.cudnn.allow_tf32 = False
+    xf = x.float().requires_grad_(True)
+    yf = F.conv2d(xf, Wd, conv.bias.detach().float(), stride=stride, padding=pad)
+    yf.backward(gy.float())
+    gw = torch.nn.grad.conv2d_weight(x.float(), Wd.shape, gy.float(), stride=stride, padding=pad)
+    assert rel_l2(host(y.float()), host(yf)) < 1e-2
+    assert rel_l2(host(xc.grad.float()), host(xf.grad)) < 1e-2
+    assert rel_l2(host(cap[0].float()), host(gw.reshape(cout, -1))) < 1e-2
+    assert torch.isfinite(conv.get_weight().float()).all().item()

@@ -873,17 +873,17 @@ def test_muon_ns5_fused_combines_match_two_step(oracle, N, K):
 def test_muon_frobenius_denominator_bit_exact(oracle, N, K):
     """The NS5 input scale max(||g||, 1e-12) * fl(1 + 1e-7) (block partials,
     then one wave chaining them in ascending order) equals the oracle's bit
-    for bit; read back from the workspace (layout: X, BX, A, AA, partials,
-    then the denominator)."""
+    for bit; read back from the workspace (layout: the split-K region, X, BX,
+    A, AA, partials, then the denominator in the last 256-byte slot)."""
+    from concord_amd import _lib as C
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(N + K)
     g = oracle.f32_to_bf16_bits_array((rng.standard_normal((N, K)) * 1e-3).astype(np.float32))
-    pb.muon_ns5(dev(g))
+    gd = dev(g)
+    pb.muon_ns5(gd)
     sync()
     ws = pb._MUON_WORKSPACES[pb._dev_key(torch.device(DEV))]
-    m, n = min(N, K), max(N, K)
-    r256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
-    off = 2 * r256(m * n * 2) + 2 * r256(m * m * 2) + r256(-(-N * K // 8192) * 4)
+    off = int(C.lib().concord_muon_workspace_bytes(N, K)) - 256
     den = host(ws[off:off + 4].view(torch.float32))[0]
     s = oracle.frob_sumsq(g)
     want = np.float32(max(np.float32(np.sqrt(np.float32(s))), np.float32(1e-12)) * np.float32(1.0 + 1e-7))
@@ -1318,8 +1318,10 @@ def test_materialize_gated_bit_exact(oracle, gain):
     re = rng.integers(-8, 8, N).astype(np.int8)
     ce = rng.integers(-8, 8, K).astype(np.int8)
     out = torch.empty((N, K), dtype=torch.bfloat16, device=DEV)
-    assert C.lib().concord_materialize_gated(C.ptr(dev(packed)), K, C.ptr(dev(re)), C.ptr(dev(ce)), N, K, 15,
-                                             gain, C.ptr(out), K, C.stream_of(torch.device(DEV))) == 0
+    # the device copies stay referenced until the kernel has run
+    pd, red, ced = dev(packed), dev(re), dev(ce)
+    assert C.lib().concord_materialize_gated(C.ptr(pd), K, C.ptr(red), C.ptr(ced), N, K, 15, gain, C.ptr(out), K,
+                                             C.stream_of(torch.device(DEV))) == 0
     sync()
     np.testing.assert_array_equal(host(out).view(np.uint16), oracle.materialize_gated(packed, re, ce, gain))
 
@@ -1481,9 +1483,15 @@ def test_sigmag_noise_parts(oracle, M, N, K):
     sync()
     ws = pb._SIGMAG_WORKSPACES[pb._dev_key(torch.device(DEV))]
     r256 = lambda b: (b + 255) // 256 * 256  # noqa: E731
-    o_prod = r256(M * N * 2)
+    # layout: split-K region, scaled dy, product, partials, token partials,
+    # sum, scale, draws (the split-K region's size is what the rest leaves)
+    from concord_amd import _lib as C
+    rest = (r256(M * N * 2) + r256(N * K * 2) + r256(2 * -(-N * K // 8192) * 4) + r256(-(-M // 8192) * 4)
+            + 256 + 256 + r256(M * 4))
+    o_dyt = int(C.lib().concord_sigmag_noise_workspace_bytes(M, N, K)) - rest
+    o_prod = o_dyt + r256(M * N * 2)
     o_ssum = o_prod + r256(N * K * 2) + r256(2 * -(-N * K // 8192) * 4) + r256(-(-M // 8192) * 4)
-    dyt = host(ws[:M * N * 2].view(torch.bfloat16)).view(np.uint16).reshape(M, N)
+    dyt = host(ws[o_dyt:o_dyt + M * N * 2].view(torch.bfloat16)).view(np.uint16).reshape(M, N)
     P = host(ws[o_prod:o_prod + N * K * 2].view(torch.bfloat16)).view(np.uint16).reshape(N, K)
     S = host(ws[o_ssum:o_ssum + 4].view(torch.float32))[0]
     eps = oracle.token_draws(313, M)
