@@ -1503,6 +1503,17 @@ def test_sigmag_noise_parts(oracle, M, N, K):
     want = oracle.sigmag_combine(host(g0).view(np.uint16), P, S, M, 0.3)
     np.testing.assert_array_equal(host(g).view(np.uint16), want)
     assert int(host(salt)[0]) == 313
+    # the reference forms the draw in fp32 ((eps * gy)^T x, prototype_packed_b.py:1492-1494);
+    # this build rounds eps*dy and the product to bf16.  The added noise against
+    # that expression in float64 (same eps, same gradient):
+    g0f = oracle.bf16_bits_to_f32(host(g0).view(np.uint16)).astype(np.float64)
+    n64 = (eps[:, None].astype(np.float64) * dyf.astype(np.float64)).T @ host(x.float()).astype(np.float64) \
+        - float(np.float64(eps.astype(np.float64).sum())) * g0f / M
+    add64 = n64 * (0.3 * np.linalg.norm(g0f) / max(np.linalg.norm(n64), 1e-12))
+    added = oracle.bf16_bits_to_f32(host(g).view(np.uint16)).astype(np.float64) - g0f
+    err = rel_l2(added, add64)
+    print(f"Sigma_g draw against the fp32-form reference in float64: rel-L2 {err:.2e}")
+    assert err < 2e-2
 
 
 def test_layer_sigmag_noise_step():
