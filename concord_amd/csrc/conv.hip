@@ -253,14 +253,18 @@ __global__ __launch_bounds__(256) void col2im_direct_kernel(const uint16_t* __re
 // equals the ungated decode, every term being an integer below 2^24) into an
 // LDS tile [taps][kTapC], then writes taps rows of kTapC channels (8 bytes
 // per lane).
+// TAPS: the tap count when known at compile time (9 for 3 x 3), so that the
+// index splits are multiplies; 0 = the runtime `taps_rt`.
 constexpr int kTapC = 256;
 constexpr int kTapLd = kTapC + 4;   // LDS row of weight_taps_kernel: tap rows 2 banks apart, 8-byte aligned
 
+template <int TAPS>
 __global__ __launch_bounds__(256) void weight_taps_kernel(const int32_t* __restrict__ packed, int64_t ld_p,
                                                           const int8_t* row_exp, const int8_t* col_exp,
-                                                          int64_t Cin, int taps, int32_t bias, float gain,
+                                                          int64_t Cin, int taps_rt, int32_t bias, float gain,
                                                           uint16_t* __restrict__ wt) {
   extern __shared__ uint16_t tl[];   // [taps][kTapLd]
+  const int taps = TAPS ? TAPS : taps_rt;
   const int64_t n = blockIdx.y;
   const int64_t c0 = (int64_t)blockIdx.x * kTapC;
   const int nc = (int)min((int64_t)kTapC, Cin - c0);
@@ -299,8 +303,9 @@ __global__ __launch_bounds__(256) void weight_taps_kernel(const int32_t* __restr
   const bool v8 = (nc % 4) == 0 && (Cin % 4) == 0 && ((uintptr_t)wt % 8) == 0 && (c0 % 4) == 0;
   if (v8) {
     const int q4 = nc / 4;
+    const bool full = nc == kTapC;   // q4 = 64: the split is a shift
     for (int e = threadIdx.x; e < q4 * taps; e += 256) {
-      const int t = e / q4, cl = (e - t * q4) * 4;
+      const int t = full ? e >> 6 : e / q4, cl = (e - t * q4) * 4;
       *reinterpret_cast<uint2*>(dst + (int64_t)t * Cin + cl) = *reinterpret_cast<const uint2*>(tl + t * kTapLd + cl);
     }
   } else {
@@ -314,9 +319,11 @@ __global__ __launch_bounds__(256) void weight_taps_kernel(const int32_t* __restr
 // g[n][c * taps + t] = gt[n][t][c]: a conv gradient from the tap-major order
 // of the implicit WGRAD back to the packed words' (c, tap) order.  Same
 // blocking as weight_taps_kernel, with the LDS tile [kTapC][taps].
+template <int TAPS>
 __global__ __launch_bounds__(256) void grad_from_taps_kernel(const uint16_t* __restrict__ gt, int64_t Cin,
-                                                             int taps, uint16_t* __restrict__ g, int64_t ld_g) {
+                                                             int taps_rt, uint16_t* __restrict__ g, int64_t ld_g) {
   extern __shared__ uint16_t tl[];   // [kTapC][taps]
+  const int taps = TAPS ? TAPS : taps_rt;
   const int64_t n = blockIdx.y;
   const int64_t c0 = (int64_t)blockIdx.x * kTapC;
   const int nc = (int)min((int64_t)kTapC, Cin - c0);
@@ -325,8 +332,9 @@ __global__ __launch_bounds__(256) void grad_from_taps_kernel(const uint16_t* __r
   const bool v8 = (nc % 4) == 0 && (Cin % 4) == 0 && ((uintptr_t)gt % 8) == 0 && (c0 % 4) == 0;
   if (v8) {
     const int q4 = nc / 4;
+    const bool full = nc == kTapC;
     for (int e = threadIdx.x; e < q4 * taps; e += 256) {
-      const int t = e / q4, cl = (e - t * q4) * 4;
+      const int t = full ? e >> 6 : e / q4, cl = (e - t * q4) * 4;
       const uint2 v = *reinterpret_cast<const uint2*>(src + (int64_t)t * Cin + cl);
       tl[cl * taps + t] = (uint16_t)(v.x & 0xFFFFu);
       tl[(cl + 1) * taps + t] = (uint16_t)(v.x >> 16);
@@ -541,9 +549,14 @@ extern "C" int concord_conv_weight_taps(const int32_t* packed, int64_t ld_p, con
   CONCORD_CHECK(ld_p >= Cin * taps, "concord_conv_weight_taps: leading dimension < in_channels * taps");
   CONCORD_CHECK(Cout <= kMaxGridY, "concord_conv_weight_taps: more than %lld output channels",
                 (long long)kMaxGridY);
-  hipLaunchKernelGGL(weight_taps_kernel, dim3((unsigned)cdiv(Cin, kTapC), (unsigned)Cout), dim3(256),
-                     (size_t)taps * kTapLd * 2, (hipStream_t)stream, packed, ld_p, row_exp, col_exp, Cin, (int)taps,
-                     mantissa_bias, fast_gain, wt);
+  const dim3 grid((unsigned)cdiv(Cin, kTapC), (unsigned)Cout);
+  const size_t lds = (size_t)taps * kTapLd * 2;
+  if (taps == 9)
+    hipLaunchKernelGGL(weight_taps_kernel<9>, grid, dim3(256), lds, (hipStream_t)stream, packed, ld_p, row_exp,
+                       col_exp, Cin, (int)taps, mantissa_bias, fast_gain, wt);
+  else
+    hipLaunchKernelGGL(weight_taps_kernel<0>, grid, dim3(256), lds, (hipStream_t)stream, packed, ld_p, row_exp,
+                       col_exp, Cin, (int)taps, mantissa_bias, fast_gain, wt);
   return launch_status("conv_weight_taps");
 }
 
@@ -556,8 +569,14 @@ extern "C" int concord_conv_grad_from_taps(const uint16_t* gt, int64_t Cout, int
   CONCORD_CHECK(ld_g >= Cin * taps, "concord_conv_grad_from_taps: leading dimension < in_channels * taps");
   CONCORD_CHECK(Cout <= kMaxGridY, "concord_conv_grad_from_taps: more than %lld output channels",
                 (long long)kMaxGridY);
-  hipLaunchKernelGGL(grad_from_taps_kernel, dim3((unsigned)cdiv(Cin, kTapC), (unsigned)Cout), dim3(256),
-                     (size_t)taps * kTapC * 2, (hipStream_t)stream, gt, Cin, (int)taps, g, ld_g);
+  const dim3 grid((unsigned)cdiv(Cin, kTapC), (unsigned)Cout);
+  const size_t lds = (size_t)taps * kTapC * 2;
+  if (taps == 9)
+    hipLaunchKernelGGL(grad_from_taps_kernel<9>, grid, dim3(256), lds, (hipStream_t)stream, gt, Cin, (int)taps, g,
+                       ld_g);
+  else
+    hipLaunchKernelGGL(grad_from_taps_kernel<0>, grid, dim3(256), lds, (hipStream_t)stream, gt, Cin, (int)taps, g,
+                       ld_g);
   return launch_status("conv_grad_from_taps");
 }
 

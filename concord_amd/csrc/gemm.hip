@@ -608,7 +608,8 @@ static int wgrad_vhat_impl(const GemmArgs* gd, const uint16_t* dy, int64_t ld_dy
     }
   }
   if (rc == -1) rc = gemm_wgrad_vhat_launch(g, gemm_workspace ? gemm_workspace_bytes : 0, st, what, &tiles_j);
-  if (rc == -1) {   // split or unaligned WGRAD: the plain product, then the partials kernels
+  if (rc == -1) rc = gemm_wgrad_vhat_split_launch(g, gemm_workspace, gemm_workspace_bytes, st, what, &tiles_j);
+  if (rc == -1) {   // unaligned WGRAD: the plain product, then the partials kernels
     g.bpart = nullptr;
     rc = launch_gemm<MODE_WGRAD>(g, gemm_workspace, gemm_workspace_bytes, st, what);
     if (rc != CONCORD_OK) return rc;

@@ -39,7 +39,7 @@ typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
 
 // a voffset at or past every buffer's num_records (which stay below 2^31)
 constexpr uint32_t kOOB = 0x80000000u;
-constexpr int kMaxSplits = 4;
+constexpr int kMaxSplits = kGemmMaxSplits;
 
 CONCORD_DEV Rsrc make_rsrc(const void* p, uint32_t bytes) {
   // dword 3 = 0x00020000: 32-bit data format, raw (stride 0) addressing
@@ -554,6 +554,54 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (idx >= splitk_reduce_items<MODE, NI, NJ, BI, BJ, WI, WJ>(g)) return;
   splitk_reduce_item<MODE, NI, NJ, BI, BJ, WI, WJ>(g, idx);
+}
+
+// Split-K reduction of a WGRAD launch, with the v-hat partials: one wave per
+// 64 x 64 accumulator wave tile sums the splits' partials in split order (the
+// additions of splitk_reduce_item), stores the bf16 tile and forms the v-hat
+// partials of the stored values in vhat_tile_partials' order, as the VH
+// epilogue does for an unsplit launch.
+template <int BI, int BJ, int WI, int WJ>
+__global__ __launch_bounds__(64) void splitk_reduce_vh_kernel(GemmArgs g) {
+  constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ, NI = WTI / 16, NJ = WTJ / 16;
+  static_assert(NI == 4 && NJ == 4, "v-hat partials take 64 x 64 wave tiles");
+  const int lane = threadIdx.x;
+  const int tiles = g.tiles_i * g.tiles_j;
+  const int tile = (int)(blockIdx.x / NAW), aw = (int)(blockIdx.x % NAW);   // one wave per accumulator wave tile
+  int bi, bj;
+  tile_of(tile, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  const int64_t row0 = (int64_t)bi * BI + (aw / WJ) * WTI, col0 = (int64_t)bj * BJ + (aw % WJ) * WTJ;
+  const int64_t PT = (int64_t)NAW * NI * NJ * 256;
+  const float* base = g.part + (int64_t)tile * g.splits * PT + (int64_t)aw * NI * NJ * 256 + lane * 4;
+  float g2[4][4][4];
+#pragma unroll
+  for (int x = 0; x < NI; ++x) {
+    // the row of 4 blocks, every split's partial loaded before any is summed
+    f32x4 part[NJ][kGemmMaxSplits];
+#pragma unroll
+    for (int y = 0; y < NJ; ++y)
+#pragma unroll
+      for (int s2 = 0; s2 < kGemmMaxSplits; ++s2)
+        part[y][s2] = s2 < g.splits ? *reinterpret_cast<const f32x4*>(base + (x * NJ + y) * 256 + s2 * PT)
+                                    : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int y = 0; y < NJ; ++y) {
+      f32x4 sum = part[y][0];
+#pragma unroll
+      for (int s2 = 1; s2 < kGemmMaxSplits; ++s2)
+        if (s2 < g.splits)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) sum[e] = __fadd_rn(sum[e], part[y][s2][e]);
+      const uint32_t lo = pack_bf16x2(sum[0], sum[1]), hi = pack_bf16x2(sum[2], sum[3]);
+      const float v[4] = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xFFFF0000u),
+                          __uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) g2[x][y][e] = __fmul_rn(v[e], v[e]);
+      const int64_t i = row0 + x * 16 + (lane & 15), j = col0 + y * 16 + 4 * (lane >> 4);
+      if (i < g.I && j < g.J) *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = make_uint2(lo, hi);
+    }
+  }
+  vhat_tile_partials(g2, lane, row0, col0, g.I, g.J, g.vh_pr, g.vh_pc);
 }
 
 // MFMAs of one TR-deep stage for a wave tile of NI x NJ 16x16 blocks whose
@@ -1252,11 +1300,12 @@ CONCORD_DEV void bias_acc(f32x4 (&b)[NI], const bf16x8 (&fa)[NI]) {
 }
 
 // VH: also write the v-hat partials of the bf16-rounded output (64 x 64 wave
-// tiles, vhat_tile.h order); only without split-K.  With g.bpart set, the
-// waves wj = 0 of block (bi, bj) also sum the A operand over the stages
+// tiles, vhat_tile.h order); only without split-K (a split launch forms them
+// in splitk_reduce_vh_kernel).  With g.bpart set, the waves wj = 0 of block
+// (bi, bj) of split sp also sum the A operand over the split's stages
 // s = bj, bj + tiles_j, ... (an MFMA against ones per fragment, fp32
-// accumulation), giving bpart[bj][i]; the bias gradient is the sum of the
-// partials over bj ascending (vhat_finalize).
+// accumulation), giving bpart[sp * tiles_j + bj][i]; the bias gradient is the
+// sum of the partials over that row index ascending (vhat_finalize).
 // The split-K reduction shape of the dgrad kernel (gemm_dgt_kernel<DGRAD, 256,
 // 128>, 2 x 2 accumulator waves of 128 x 64), which a VH launch can carry.
 #define CONCORD_DGRAD_REDUCE MODE_DGRAD, 8, 4, 256, 128, 2, 2
@@ -1329,7 +1378,7 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * PERT));   // own stage-0 DMA landed
   lds_barrier();
   bf16x8 fa0[NI], fb0[NJ], fa1[NI], fb1[NJ];
-  const bool bg = VH && g.bpart != nullptr && wj == 0;   // uniform per wave
+  const bool bg = g.bpart != nullptr && wj == 0;   // uniform per wave
   f32x4 bsum[NI];
 #pragma unroll
   for (int x = 0; x < NI; ++x) bsum[x] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -1356,7 +1405,7 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
 #pragma unroll
     for (int x = 0; x < NI; ++x) {
       const int64_t i = i0 + wi * WTI + 16 * x + (lane & 15);
-      if (lane < 16 && i < g.I) g.bpart[(int64_t)bj * g.I + i] = bsum[x][0];
+      if (lane < 16 && i < g.I) g.bpart[((int64_t)split * g.tiles_j + bj) * g.I + i] = bsum[x][0];
     }
   }
   // no DMA may still be writing LDS when the ring is reused for the output
@@ -1731,6 +1780,26 @@ int gemm_wgrad_vhat_launch(const GemmArgs& g0, size_t split_room, hipStream_t st
   g.tiles_j = p.tj;
   hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true>), dim3(p.ti * p.tj), dim3(512), 0, st, g,
                      GemmArgs{}, p.ti * p.tj);
+  return launch_status(what);
+}
+
+int gemm_wgrad_vhat_split_launch(const GemmArgs& g0, void* workspace, size_t ws_bytes, hipStream_t st,
+                                 const char* what, int* bias_rows) {
+  if (!eligible(MODE_WGRAD, g0) || !tr_eligible(g0) || !workspace) return -1;
+  const size_t room = ws_bytes > kSplitkCounterBytes ? ws_bytes - kSplitkCounterBytes : 0;
+  const FastPlan p = plan_mode(MODE_WGRAD, g0.I, g0.J, g0.R, room);
+  if (p.shape != 0 || p.splits < 2) return -1;
+  GemmArgs g = g0;
+  g.splits = p.splits;
+  g.r_split = p.r_split;
+  g.tiles_i = p.ti;
+  g.tiles_j = p.tj;
+  g.part = (float*)((char*)workspace + kSplitkCounterBytes);
+  const int tiles = p.ti * p.tj;
+  *bias_rows = p.splits * p.tj;
+  hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, false>), dim3(tiles * p.splits), dim3(512), 0, st, g,
+                     GemmArgs{}, tiles * p.splits);
+  hipLaunchKernelGGL((splitk_reduce_vh_kernel<256, 128, 4, 2>), dim3((unsigned)(tiles * 8)), dim3(64), 0, st, g);
   return launch_status(what);
 }
 

@@ -12,6 +12,9 @@
 
 namespace concord {
 
+// the most ways a GEMM splits its reduction
+constexpr int kGemmMaxSplits = 4;
+
 struct Workspace {
   size_t vhat_ticket, scratch, total;
 };
@@ -38,10 +41,10 @@ inline Workspace workspace_layout(int64_t N, int64_t K, int64_t M) {
   const size_t reb = (size_t)(2 * (N + K) + cd(N, 256) + cd(K, 256)) * sizeof(int32_t);
   // bias gradient partials (concord_wgrad_vhat places them after the v-hat
   // partials, which are still live when they are written)
-  // (slab partials of the bias-gradient kernels, or [cdiv(K, 128)][N] partials
-  // of the wgrad epilogue)
+  // (slab partials of the bias-gradient kernels, or [splits * cdiv(K, 128)][N]
+  // partials of the wgrad kernel)
   size_t bias = (size_t)(cd(M, 64) * (N > K ? N : K)) * sizeof(float);
-  const size_t bias_w = M > 0 ? (size_t)(cd(K, 128) * N) * sizeof(float) : 0;
+  const size_t bias_w = M > 0 ? (size_t)(kGemmMaxSplits * cd(K, 128) * N) * sizeof(float) : 0;
   if (bias_w > bias) bias = bias_w;
   size_t s = vhat + bias;
   if (reb > s) s = reb;
