@@ -114,9 +114,9 @@ int gemm_wgrad_vhat_launch(const GemmArgs& g, size_t split_room, hipStream_t st,
                            int* tiles_j);
 // a split WGRAD with the same results as gemm_wgrad_vhat_launch: the split
 // product (bias partials per split and j-tile when g.bpart is set), then one
-// reduction that also writes the v-hat partials; *bias_rows = the bias
-// partial rows written (splits * tiles_j).  -1 when the plan does not split
-// or the operands do not take the transpose-read kernel.
+// reduction that also writes the v-hat partials and folds the bias rows over
+// the splits; *bias_rows = the bias partial rows left (tiles_j).  -1 when the
+// plan does not split or the operands do not take the transpose-read kernel.
 int gemm_wgrad_vhat_split_launch(const GemmArgs& g, void* workspace, size_t ws_bytes, hipStream_t st,
                                  const char* what, int* bias_rows);
 // dgrad (split, its reduction deferred) then the VH WGRAD whose spare

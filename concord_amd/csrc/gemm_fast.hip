@@ -560,7 +560,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
 // 64 x 64 accumulator wave tile sums the splits' partials in split order (the
 // additions of splitk_reduce_item), stores the bf16 tile and forms the v-hat
 // partials of the stored values in vhat_tile_partials' order, as the VH
-// epilogue does for an unsplit launch.
+// epilogue does for an unsplit launch.  With bias partials (g.bpart), the
+// waves of column 0 of each tile also sum its j-tile's bias partial rows
+// over the splits, in split order, into the split-0 row, so the finalize
+// reads tiles_j rows as for an unsplit launch.
 template <int BI, int BJ, int WI, int WJ>
 __global__ __launch_bounds__(64) void splitk_reduce_vh_kernel(GemmArgs g) {
   constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ, NI = WTI / 16, NJ = WTJ / 16;
@@ -602,6 +605,16 @@ __global__ __launch_bounds__(64) void splitk_reduce_vh_kernel(GemmArgs g) {
     }
   }
   vhat_tile_partials(g2, lane, row0, col0, g.I, g.J, g.vh_pr, g.vh_pc);
+  if (g.bpart && aw % WJ == 0) {
+    const int64_t i = row0 + lane;
+    if (i < g.I) {
+      float* b = g.bpart + (int64_t)bj * g.I + i;
+      const int64_t rs = (int64_t)g.tiles_j * g.I;   // one split's rows
+      float sb = b[0];
+      for (int s2 = 1; s2 < g.splits; ++s2) sb = __fadd_rn(sb, b[s2 * rs]);
+      b[0] = sb;
+    }
+  }
 }
 
 // MFMAs of one TR-deep stage for a wave tile of NI x NJ 16x16 blocks whose
@@ -1796,7 +1809,7 @@ int gemm_wgrad_vhat_split_launch(const GemmArgs& g0, void* workspace, size_t ws_
   g.tiles_j = p.tj;
   g.part = (float*)((char*)workspace + kSplitkCounterBytes);
   const int tiles = p.ti * p.tj;
-  *bias_rows = p.splits * p.tj;
+  *bias_rows = p.tj;   // the reduction folds the splits' bias rows
   hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, false>), dim3(tiles * p.splits), dim3(512), 0, st, g,
                      GemmArgs{}, tiles * p.splits);
   hipLaunchKernelGGL((splitk_reduce_vh_kernel<256, 128, 4, 2>), dim3((unsigned)(tiles * 8)), dim3(64), 0, st, g);
