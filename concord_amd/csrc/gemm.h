@@ -83,15 +83,9 @@ CONCORD_DEV uint32_t combine_bf16x2(uint32_t yw, uint32_t xw, float s, float t) 
                      combine1(s, __uint_as_float(yw & 0xFFFF0000u), t, __uint_as_float(xw & 0xFFFF0000u)));
 }
 
-// XCD-aware tile order: workgroup w runs on XCD w % 8.  XCD x owns tile
-// indices [x*T/8, (x+1)*T/8) of a grouped row-major order (groups of GI
-// i-tiles), so the CUs of one XCD share i- and j-tiles in their L2.
-CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
-  // XCD x owns q + (x < rem) consecutive indices starting at x*q + min(x, rem):
-  // a bijection of [0, total) for any total
-  const int xcd = w % 8, slot = w / 8;
-  const int q = total / 8, rem = total % 8;
-  const int lin = xcd * q + min(xcd, rem) + slot;
+// grouped row-major tile order: groups of GI i-tiles, j-tiles ascending
+// within a group, i-tiles fastest
+CONCORD_DEV void grouped_tile(int lin, int ti, int tj, int& bi, int& bj) {
   const int GI = 8;
   const int group = lin / (GI * tj);
   const int first_i = group * GI;
@@ -99,6 +93,34 @@ CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
   const int in = lin % (GI * tj);
   bi = first_i + in % gsize;
   bj = in / gsize;
+}
+
+// XCD x (workgroups w = x mod 8) owns q + (x < rem) consecutive indices
+// starting at x*q + min(x, rem), q = total / 8, rem = total % 8: a bijection
+// of [0, total) for any total
+CONCORD_DEV int xcd_linear(int w, int total) {
+  const int xcd = w % 8, slot = w / 8;
+  const int q = total / 8, rem = total % 8;
+  return xcd * q + min(xcd, rem) + slot;
+}
+
+// XCD-aware tile order: workgroup w runs on XCD w % 8.  XCD x owns tile
+// indices [x*T/8, (x+1)*T/8) of the grouped order, so the CUs of one XCD
+// share i- and j-tiles in their L2.
+CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
+  grouped_tile(xcd_linear(w, total), ti, tj, bi, bj);
+}
+
+// Split-K launches (splits x tiles workgroups): XCD x owns a contiguous range
+// of the split-major order (split, then the grouped tiles), so its CUs share
+// one split's slices of both operands in L2, rather than every XCD reading
+// the whole reduction range of its tiles.  The split-K partial slots are
+// keyed by the row-major tile index bi * tiles_j + bj.
+CONCORD_DEV void split_tile_of(int w, int ti, int tj, int splits, int& split, int& bi, int& bj) {
+  const int tiles = ti * tj;
+  const int lin = xcd_linear(w, tiles * splits);
+  split = lin / tiles;
+  grouped_tile(lin % tiles, ti, tj, bi, bj);
 }
 
 // launch a fast-path kernel when the operands satisfy its alignment rules;

@@ -504,15 +504,13 @@ CONCORD_DEV int64_t splitk_reduce_items(const GemmArgs& g) {
 template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
 CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
   constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ;
-  const int tiles = g.tiles_i * g.tiles_j;
   const int lane = (int)(idx % 64);
   int64_t r = idx / 64;
   const int y = (int)(r % NJ); r /= NJ;
   const int x = (int)(r % NI); r /= NI;
   const int aw = (int)(r % NAW);
-  const int tile = (int)(r / NAW);
-  int bi, bj;
-  tile_of(tile, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  const int tile = (int)(r / NAW);   // row-major tile index
+  const int bi = tile / g.tiles_j, bj = tile % g.tiles_j;
   const int64_t i = (int64_t)bi * BI + (aw / WJ) * WTI + x * 16 + (lane & 15);
   const int64_t j = (int64_t)bj * BJ + (aw % WJ) * WTJ + y * 16 + 4 * (lane >> 4);
   if (i >= g.I || j >= g.J) return;
@@ -569,10 +567,9 @@ __global__ __launch_bounds__(64) void splitk_reduce_vh_kernel(GemmArgs g) {
   constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ, NI = WTI / 16, NJ = WTJ / 16;
   static_assert(NI == 4 && NJ == 4, "v-hat partials take 64 x 64 wave tiles");
   const int lane = threadIdx.x;
-  const int tiles = g.tiles_i * g.tiles_j;
-  const int tile = (int)(blockIdx.x / NAW), aw = (int)(blockIdx.x % NAW);   // one wave per accumulator wave tile
-  int bi, bj;
-  tile_of(tile, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  // one wave per accumulator wave tile; row-major tile index
+  const int tile = (int)(blockIdx.x / NAW), aw = (int)(blockIdx.x % NAW);
+  const int bi = tile / g.tiles_j, bj = tile % g.tiles_j;
   const int64_t row0 = (int64_t)bi * BI + (aw / WJ) * WTI, col0 = (int64_t)bj * BJ + (aw % WJ) * WTJ;
   const int64_t PT = (int64_t)NAW * NI * NJ * 256;
   const float* base = g.part + (int64_t)tile * g.splits * PT + (int64_t)aw * NI * NJ * 256 + lane * 4;
@@ -661,11 +658,9 @@ __global__ __launch_bounds__(64 * WI * WJ, MINB) void gemm_fast_kernel(GemmArgs 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const int wi = wave / WJ, wj = wave % WJ;
-  const int tiles = g.tiles_i * g.tiles_j;
   const int wg = blockIdx.x;
-  const int split = wg / tiles;
-  int bi, bj;
-  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  int split, bi, bj;
+  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -764,7 +759,7 @@ __global__ __launch_bounds__(64 * WI * WJ, MINB) void gemm_fast_kernel(GemmArgs 
   }
 
   static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
-  epilogue<MODE, NI, NJ, BI, BJ, WI * WJ>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, wave, t, NT,
+  epilogue<MODE, NI, NJ, BI, BJ, WI * WJ>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, wave, t, NT,
                                            &lds_a[0][0]);
 }
 
@@ -789,11 +784,9 @@ __global__ __launch_bounds__(512, 1) void gemm_ws_kernel(GemmArgs g) {
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const bool producer = wave >= 4;
-  const int tiles = g.tiles_i * g.tiles_j;
   const int wg = blockIdx.x;
-  const int split = wg / tiles;
-  int bi, bj;
-  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  int split, bi, bj;
+  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -848,7 +841,7 @@ __global__ __launch_bounds__(512, 1) void gemm_ws_kernel(GemmArgs g) {
   }
 
   static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
-  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, producer ? -1 : wave,
+  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, producer ? -1 : wave,
                                      t, 512, &lds_a[0][0]);
 }
 
@@ -1069,11 +1062,9 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const bool producer = wave >= 4;
-  const int tiles = g.tiles_i * g.tiles_j;
   const int wg = blockIdx.x;
-  const int split = wg / tiles;
-  int bi, bj;
-  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  int split, bi, bj;
+  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -1134,7 +1125,7 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
   }
 
   static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
-  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, producer ? -1 : wave,
+  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, producer ? -1 : wave,
                                      t, 512, &lds_a[0][0]);
 }
 
@@ -1349,11 +1340,9 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int tiles = g.tiles_i * g.tiles_j;
   const int wg = blockIdx.x;
-  const int split = wg / tiles;
-  int bi, bj;
-  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  int split, bi, bj;
+  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -1440,7 +1429,7 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
       }
     vhat_tile_partials(g2, lane, i0 + wi * WTI, j0 + wj * WTJ, g.I, g.J, g.vh_pr, g.vh_pc);
   }
-  epilogue<MODE_WGRAD, NI, NJ, BI, BJ, NW>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, wave, t, NT,
+  epilogue<MODE_WGRAD, NI, NJ, BI, BJ, NW>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, wave, t, NT,
                                            ring);
 }
 
@@ -1565,11 +1554,9 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const bool producer = wave >= 4;
-  const int tiles = g.tiles_i * g.tiles_j;
   const int wg = blockIdx.x;
-  const int split = wg / tiles;
-  int bi, bj;
-  tile_of(wg % tiles, g.tiles_i, g.tiles_j, tiles, bi, bj);
+  int split, bi, bj;
+  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -1625,7 +1612,7 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
   }
 
   static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
-  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, wg % tiles, producer ? -1 : wave,
+  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, producer ? -1 : wave,
                                      t, 512, &lds_a[0][0]);
 }
 
