@@ -76,57 +76,96 @@ CONCORD_DEV float ordered_sum(const float* __restrict__ v, int64_t stride, int64
   return s;
 }
 
-// two ordered sums (as ordered_sum) whose loads are issued together, 32 + 32
-// in flight: *s1 over v1[0 .. c1), *s2 over v2[0 .. c2)
-CONCORD_DEV void ordered_sum2(const float* __restrict__ v1, int64_t st1, int64_t c1, float* s1,
-                              const float* __restrict__ v2, int64_t st2, int64_t c2, float* s2) {
-  float x1 = 0.0f, x2 = 0.0f;
-  for (int64_t b = 0; b < c1 || b < c2; b += 32) {
-    float a[32], d[32];
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      a[e] = b + e < c1 ? v1[(b + e) * st1] : 0.0f;
-      d[e] = b + e < c2 ? v2[(b + e) * st2] : 0.0f;
-    }
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      if (b + e < c1) x1 = __fadd_rn(x1, a[e]);
-      if (b + e < c2) x2 = __fadd_rn(x2, d[e]);
-    }
-  }
-  *s1 = x1;
-  *s2 = x2;
-}
-
 constexpr int VH_COLS = 64;        // columns per column block of the finalize
 constexpr int VH_CHUNK = 128;      // row tiles of column partials staged at a time
+constexpr int VH_RSTAGE = 64;      // partial rows staged at a time by a row block
 
 // Row/column EMA and watermark zeroing.  Blocks [0, cdiv(N, 256)) take rows
-// and leave the halving-tree total of their 256 new v_row values in bsum;
-// the remaining blocks take VH_COLS columns each: the four waves load the
-// column partials of interleaved row tiles into LDS, one thread per column
-// then sums them in row-tile order.  The last row block to finish (a
-// device-scope ticket) chains the totals in ascending order into
-// 1 / max(sum v_row, 1e-30) and advances the salt.  The totals and the
-// ticket are device-scope atomics (cache-coherent across the XCDs), each
-// total stored and complete before its block takes a ticket, so the last
-// block reads every total without a device-wide cache write-back.
+// and leave the halving-tree total of their 256 new v_row values in bsum.
+// A row's g^2 sum adds its column-tile partials in tile order (then the bias
+// partial rows, likewise): the block stages VH_RSTAGE partial rows of its
+// 256 rows at a time in LDS, each wave moving whole partial rows with 16-byte
+// loads, and every thread then chains its own row's values.  The remaining
+// blocks take VH_COLS columns each: the four waves load the column partials
+// of interleaved row tiles into LDS, one thread per column then sums them in
+// row-tile order.  The last row block to finish (a device-scope ticket)
+// chains the totals in ascending order into 1 / max(sum v_row, 1e-30) and
+// advances the salt.  The totals and the ticket are device-scope atomics
+// (cache-coherent across the XCDs), each total stored and complete before its
+// block takes a ticket, so the last block reads every total without a
+// device-wide cache write-back.
 __global__ __launch_bounds__(256) void vhat_finalize_kernel(
     const float* __restrict__ pr, const float* __restrict__ pc, int64_t N, int64_t K, float b2,
     float omb2, float* v_row, float* v_col, int32_t* row_max, int32_t* col_max, float* bsum,
     const float* __restrict__ bpart, int64_t nbp, uint16_t* grad_bias, uint32_t* ticket,
     float* sum_v_inv, int32_t* salt) {
   __shared__ float s_part[256];
-  __shared__ float s_cols[VH_CHUNK * VH_COLS];
+  __shared__ union {
+    float rows[VH_RSTAGE * 256];      // row blocks: staged partial rows
+    float cols[VH_CHUNK * VH_COLS];   // column blocks
+  } S;
+  float* const s_cols = S.cols;
   __shared__ uint32_t s_ticket;
   const int64_t rb = cdiv(N, 256);
   const int64_t nc = cdiv(K, 64), nr = cdiv(N, 64);
   if ((int64_t)blockIdx.x < rb) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int64_t i0 = (int64_t)blockIdx.x * 256, i = i0 + t;
+    const int nrow = (int)min((int64_t)256, N - i0);
+    const int64_t nb = grad_bias ? nbp : 0;
+    const int64_t terms = nc + nb;   // the g^2 partials, then the bias partials
+    // 16-byte loads of whole 256-row blocks (uniform over the block)
+    const bool full = nrow == 256 && (N % 4) == 0 && ((uintptr_t)pr % 16) == 0 &&
+                      (nb == 0 || ((uintptr_t)bpart % 16) == 0);
+    // Stage loads are unconditional (the partial row and the row within the
+    // block clamped to the last valid ones; such copies land where no chain
+    // reads them, or are not stored), so no wait separates them.  The next
+    // stage's loads are in flight while the current stage is summed.
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    f32x4v v[VH_RSTAGE / 4];
+    const int r = 4 * lane;   // lane: rows 4 lane .. + 3 of staged partial row q
+    auto load_stage = [&](int64_t j0) {
+      const int cnt = (int)min((int64_t)VH_RSTAGE, terms - j0);
+      auto row_src = [&](int e) {
+        const int64_t j = j0 + min(wave + 4 * e, cnt - 1);
+        return (j < nc ? pr + j * N : bpart + (j - nc) * N) + i0;
+      };
+      if (full) {
+        // 16-byte streaming loads: each partial is read once (a plain load
+        // here is folded into the scalar path below by the compiler)
+#pragma unroll
+        for (int e = 0; e < VH_RSTAGE / 4; ++e)
+          v[e] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(row_src(e) + r));
+      } else {
+        const int last = nrow - 1;
+#pragma unroll
+        for (int e = 0; e < VH_RSTAGE / 4; ++e) {
+          const float* src = row_src(e);
+          v[e] = f32x4v{src[min(r, last)], src[min(r + 1, last)], src[min(r + 2, last)], src[min(r + 3, last)]};
+        }
+      }
+    };
+    float s = 0.0f, sb = 0.0f;
+    if (terms > 0) load_stage(0);
+    for (int64_t j0 = 0; j0 < terms; j0 += VH_RSTAGE) {
+      const int cnt = (int)min((int64_t)VH_RSTAGE, terms - j0);
+      __syncthreads();   // the previous stage is consumed
+#pragma unroll
+      for (int e = 0; e < VH_RSTAGE / 4; ++e)
+        if (wave + 4 * e < cnt) *reinterpret_cast<f32x4v*>(S.rows + (wave + 4 * e) * 256 + r) = v[e];
+      __syncthreads();
+      if (j0 + VH_RSTAGE < terms) load_stage(j0 + VH_RSTAGE);
+      if (t < nrow) {
+        // two plain chains (no per-term branch), so the LDS reads run ahead
+        const int c1 = (int)max((int64_t)0, min((int64_t)cnt, nc - j0));
+#pragma unroll 16
+        for (int q = 0; q < c1; ++q) s = __fadd_rn(s, S.rows[q * 256 + t]);
+#pragma unroll 16
+        for (int q = c1; q < cnt; ++q) sb = __fadd_rn(sb, S.rows[q * 256 + t]);
+      }
+    }
     float vn = 0.0f;
     if (i < N) {
-      float s, sb;
-      ordered_sum2(pr + i, N, nc, &s, bpart + i, N, grad_bias ? nbp : 0, &sb);
       vn = __fadd_rn(__fmul_rn(v_row[i], b2), __fmul_rn(omb2, s));
       v_row[i] = vn;
       if (row_max) row_max[i] = 0;
@@ -146,16 +185,15 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
     __syncthreads();
     if (s_ticket != (uint32_t)(rb - 1) || threadIdx.x >= 64) return;
     // last row block, one wave: totals 64 at a time, chained in order
-    const int lane = threadIdx.x;
-    float s = 0.0f;
+    float tot = 0.0f;
     for (int64_t c0 = 0; c0 < rb; c0 += 64) {
       const float v = c0 + lane < rb ? __hip_atomic_load(bsum + c0 + lane, __ATOMIC_RELAXED,
                                                         __HIP_MEMORY_SCOPE_AGENT) : 0.0f;
       const int cnt = (int)min((int64_t)64, rb - c0);
-      for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, lane_value(v, j));
+      for (int j = 0; j < cnt; ++j) tot = __fadd_rn(tot, lane_value(v, j));
     }
     if (lane == 0) {
-      *sum_v_inv = __fdiv_rn(1.0f, fmaxf(s, 1e-30f));
+      *sum_v_inv = __fdiv_rn(1.0f, fmaxf(tot, 1e-30f));
       if (salt) salt[0] = wadd(salt[0], 1);
       __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);   // re-armed
     }
