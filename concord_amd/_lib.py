@@ -98,6 +98,8 @@ _SIGS = {
     "concord_conv_fwd": (ctypes.c_int, [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "concord_conv_dgrad": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
     "concord_conv_wgrad": (ctypes.c_int, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P]),
+    "concord_conv_wgrad_vhat": (ctypes.c_int, [_P, _P, _P, _P, _I] + [_I] * 11 +
+                                [_D, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _P, _Z, _P]),
     "concord_sigmag_noise_workspace_bytes": (_Z, [_I, _I, _I]),
     "concord_sigmag_noise": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _P, _P, _Z, _P]),
     "concord_watermark_peak": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _Z, _P]),

@@ -11,6 +11,8 @@
 
 #include "common.h"
 #include "gemm.h"
+#include "vhat.h"
+#include "vhat_tile.h"
 #include "workspace.h"
 
 namespace concord {
@@ -358,6 +360,73 @@ __global__ __launch_bounds__(256) void grad_from_taps_kernel(const uint16_t* __r
   }
 }
 
+// grad_from_taps_kernel and vhat_partials_kernel in one pass, for 3 x 3
+// kernels (9 taps): a block takes 64 output channels n0 .. n0 + 63 and 64
+// input channels c0 .. c0 + 63, i.e. the 64 x 576 block of the packed
+// gradient g[n][c * 9 + t] whose columns start at 9 c0 (c0 and the channel
+// counts are multiples of 64, so there are no edges).  It reads gt[n][t][c0 ..]
+// (128-byte runs, 16 bytes per lane) and writes the values into LDS in the
+// packed order, rows kTvLd apart; then it writes the packed rows with 16-byte
+// stores and forms the v-hat partials of its nine 64 x 64 tiles of g exactly
+// as vhat_partials_kernel does (vhat_tile.h order, the same bf16 values).
+constexpr int kTvTaps = 9;
+constexpr int kTvCols = 64 * kTvTaps;   // packed columns of a block
+constexpr int kTvLd = kTvCols + 8;      // LDS row (halves): 16-byte rows, v-hat reads spread over the banks
+
+__global__ __launch_bounds__(256) void taps_vhat_kernel(const uint16_t* __restrict__ gt, int64_t Cin,
+                                                        uint16_t* __restrict__ g, int64_t ld_g, int64_t N,
+                                                        float* __restrict__ pr, float* __restrict__ pc) {
+  __shared__ __attribute__((aligned(16))) uint16_t tl[64 * kTvLd];   // [row][c * 9 + t]
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * 64, n0 = (int64_t)blockIdx.y * 64;
+  const int64_t K = Cin * kTvTaps;
+  constexpr int RUNS = 8 * kTvTaps;     // 16-byte chunks per row: (t, 8-channel group)
+  constexpr int PER = 64 * RUNS / 256;  // chunks per thread
+  {
+    uint4 v[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int u = t + 256 * e;
+      const int row = u / RUNS, rem = u - row * RUNS, tp = rem >> 3, ch = rem & 7;
+      v[e] = *reinterpret_cast<const uint4*>(gt + (n0 + row) * K + tp * Cin + c0 + ch * 8);
+    }
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+      const int u = t + 256 * e;
+      const int row = u / RUNS, rem = u - row * RUNS, tp = rem >> 3, ch = rem & 7;
+      uint16_t* d = tl + row * kTvLd + (ch * 8) * kTvTaps + tp;
+      const uint32_t w[4] = {v[e].x, v[e].y, v[e].z, v[e].w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) d[k * kTvTaps] = (uint16_t)(w[k >> 1] >> (16 * (k & 1)));
+    }
+  }
+  __syncthreads();
+  // packed rows, 8 columns (16 bytes) per item
+#pragma unroll
+  for (int e = 0; e < PER; ++e) {
+    const int u = t + 256 * e;
+    const int row = u / RUNS, kc = (u - row * RUNS) * 8;
+    *reinterpret_cast<uint4*>(g + (n0 + row) * ld_g + c0 * kTvTaps + kc) =
+        *reinterpret_cast<const uint4*>(tl + row * kTvLd + kc);
+  }
+  // v-hat partials: one wave per 64 x 64 tile (columns 64 jt .. of the block)
+  const int p = lane & 15, q = lane >> 4;
+  for (int jt = wave; jt < kTvTaps; jt += 4) {
+    float g2[4][4][4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        const uint2 w = *reinterpret_cast<const uint2*>(tl + (16 * x + p) * kTvLd + 64 * jt + 16 * y + 4 * q);
+        const float f[4] = {__uint_as_float(w.x << 16), __uint_as_float(w.x & 0xFFFF0000u),
+                            __uint_as_float(w.y << 16), __uint_as_float(w.y & 0xFFFF0000u)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) g2[x][y][e] = __fmul_rn(f[e], f[e]);
+      }
+    vhat_tile_partials(g2, lane, n0, c0 * kTvTaps + 64 * jt, N, K, pr, pc);
+  }
+}
+
 constexpr size_t kCol2imLdsBudget = 64 * 1024;   // two blocks per CU
 
 // staged rows and columns a block needs at most, and the channels per block
@@ -627,4 +696,53 @@ extern "C" int concord_conv_wgrad(const uint16_t* dy, const uint16_t* x, uint16_
   const int rc = gemm_conv_launch(MODE_WGRAD, g, workspace, workspace_bytes, (hipStream_t)stream, "conv_wgrad");
   CONCORD_CHECK(rc != -1, "concord_conv_wgrad: operands not aligned for the implicit kernels");
   return rc;
+}
+
+extern "C" int concord_conv_wgrad_vhat(const uint16_t* dy, const uint16_t* x, uint16_t* gt, uint16_t* grad_w,
+                                       int64_t ld_gw, CONV_GEOM_ARGS, double beta2, float* v_row, float* v_col,
+                                       float* sum_v_inv, int32_t* row_max, int32_t* col_max,
+                                       int32_t* salt_counter, uint16_t* grad_bias, void* workspace,
+                                       size_t workspace_bytes, void* gemm_workspace, size_t gemm_workspace_bytes,
+                                       void* stream) {
+  ConvShape s;
+  CONCORD_CHECK(conv_shape(B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw, s),
+                "concord_conv_wgrad_vhat: bad geometry");
+  CONCORD_CHECK(conv_implicit_shape(s), "concord_conv_wgrad_vhat: shape not taken by the implicit kernels "
+                                        "(concord_conv_implicit_ok)");
+  CONCORD_CHECK(dy && x && gt && grad_w && v_row && v_col && sum_v_inv, "concord_conv_wgrad_vhat: NULL argument");
+  const int64_t T = kh * kw, N = Cout, K = T * Cin, M = B * s.Ho * s.Wo;
+  CONCORD_CHECK(ld_gw >= K, "concord_conv_wgrad_vhat: leading dimension < in_channels * taps");
+  CONCORD_CHECK(Cout <= kMaxGridY, "concord_conv_wgrad_vhat: more than %lld output channels", (long long)kMaxGridY);
+  const hipStream_t st = (hipStream_t)stream;
+  const Workspace ws = workspace_layout(N, K, grad_bias ? M : 0);
+  CONCORD_CHECK(workspace && workspace_bytes >= ws.total, "concord_conv_wgrad_vhat: workspace of %zu bytes needed",
+                ws.total);
+  const VhatScratch v = vhat_scratch(N, K);
+  float* pr = (float*)((char*)workspace + ws.scratch);
+  float* pc = pr + v.pr;
+  float* bsum = pc + v.pc;
+  float* bpart = bsum + v.bsum;
+  uint32_t* ticket = (uint32_t*)((char*)workspace + ws.vhat_ticket);
+  // the product (tap-major gt), with the bias partials of dy when asked for
+  GemmArgs g = conv_args(dy, Cout, x, K, gt, K, Cout, K, M, nullptr);
+  g.cv = conv_idx(s, Cin, H, W, s.Ho, s.Wo, Cin, B * H * W * Cin * 2, 0);
+  g.bpart = grad_bias ? bpart : nullptr;
+  int bias_rows = 0;
+  const int rc = gemm_conv_launch(MODE_WGRAD, g, gemm_workspace, gemm_workspace ? gemm_workspace_bytes : 0, st,
+                                  "conv_wgrad_vhat", &bias_rows);
+  CONCORD_CHECK(rc != -1, "concord_conv_wgrad_vhat: operands not aligned for the implicit kernels");
+  if (rc != CONCORD_OK) return rc;
+  // the packed-order gradient and its v-hat partials
+  const bool fused = T == kTvTaps && ld_gw % 8 == 0 && ((uintptr_t)grad_w % 16) == 0 && ((uintptr_t)gt % 16) == 0;
+  if (fused) {
+    hipLaunchKernelGGL(taps_vhat_kernel, dim3((unsigned)(Cin / 64), (unsigned)(Cout / 64)), dim3(256), 0, st, gt,
+                       Cin, grad_w, ld_gw, N, pr, pc);
+  } else {
+    const int rc2 = concord_conv_grad_from_taps(gt, Cout, Cin, T, grad_w, ld_gw, stream);
+    if (rc2 != CONCORD_OK) return rc2;
+    vhat_partials_launch(grad_w, ld_gw, N, K, pr, pc, st);
+  }
+  vhat_finish_launch(pr, pc, bsum, ticket, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter,
+                     st, bpart, bias_rows, grad_bias);
+  return launch_status("conv_wgrad_vhat");
 }

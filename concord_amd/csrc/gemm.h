@@ -164,9 +164,12 @@ int gemm_bf16_run(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, i
 // implicit-GEMM convolution products (g.cv set): MODE_FWD_BF16 (x gathered,
 // W' [N][taps * C] rows), MODE_DGRAD_BF16 (dy gathered, W' rows (n, tap) by
 // the tap's column block) or MODE_WGRAD (x gathered as the column operand);
-// -1 when the operands do not take the kernels
+// -1 when the operands do not take the kernels.  A MODE_WGRAD launch with
+// g.bpart set also leaves the bias partials of dy in its first *bias_rows
+// rows of I values (one per j-tile; a split launch sums its splits' rows
+// into them, in split order).
 int gemm_conv_launch(int mode, const GemmArgs& g, void* workspace, size_t ws_bytes, hipStream_t st,
-                     const char* what);
+                     const char* what, int* bias_rows = nullptr);
 // split-K partial bytes gemm_conv_launch plans for an I x J x R product
 size_t gemm_conv_partial_bytes(int mode, int64_t I, int64_t J, int64_t R);
 // split-K workspace bytes (counters + partials) one such product may use

@@ -547,11 +547,28 @@ CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
   *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = o;
 }
 
+// bias rows of a split WGRAD (g.bpart): value f = (bj, i) of the split-0 row
+// becomes the sum over the splits' rows, in split order (as
+// splitk_reduce_vh_kernel folds them)
+CONCORD_DEV void bias_fold_item(const GemmArgs& g, int64_t f) {
+  const int64_t bj = f / g.I, i = f % g.I;
+  float* b = g.bpart + bj * g.I + i;
+  float s = *b;
+  for (int sp = 1; sp < g.splits; ++sp) s = __fadd_rn(s, b[(int64_t)sp * g.tiles_j * g.I]);
+  *b = s;
+}
+
+// threads [0, items) reduce the product; for a WGRAD with bias partials the
+// next tiles_j * I fold them
 template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
   const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= splitk_reduce_items<MODE, NI, NJ, BI, BJ, WI, WJ>(g)) return;
-  splitk_reduce_item<MODE, NI, NJ, BI, BJ, WI, WJ>(g, idx);
+  const int64_t items = splitk_reduce_items<MODE, NI, NJ, BI, BJ, WI, WJ>(g);
+  if (idx < items) {
+    splitk_reduce_item<MODE, NI, NJ, BI, BJ, WI, WJ>(g, idx);
+  } else if (MODE == MODE_WGRAD && g.bpart && idx - items < (int64_t)g.tiles_j * g.I) {
+    bias_fold_item(g, idx - items);
+  }
 }
 
 // Split-K reduction of a WGRAD launch, with the v-hat partials: one wave per
@@ -1705,7 +1722,8 @@ template <int MODE, int BI, int BJ, int WI, int WJ>
 static void launch_reduce(const GemmArgs& g, hipStream_t st) {
   if (g.splits <= 1) return;
   constexpr int NI = BI / WI / 16, NJ = BJ / WJ / 16;
-  const int64_t threads = (int64_t)g.tiles_i * g.tiles_j * WI * WJ * NI * NJ * 64;
+  int64_t threads = (int64_t)g.tiles_i * g.tiles_j * WI * WJ * NI * NJ * 64;
+  if (MODE == MODE_WGRAD && g.bpart) threads += (int64_t)g.tiles_j * g.I;   // the bias fold
   hipLaunchKernelGGL((splitk_reduce_kernel<MODE, NI, NJ, BI, BJ, WI, WJ>), dim3((unsigned)cdiv(threads, 256)),
                      dim3(256), 0, st, g);
 }
@@ -1850,7 +1868,7 @@ size_t gemm_conv_partial_bytes(int mode, int64_t I, int64_t J, int64_t R) {
 }
 
 int gemm_conv_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_bytes, hipStream_t st,
-                     const char* what) {
+                     const char* what, int* bias_rows) {
   // the output is written 8 bytes at a time; the non-gathered operand moves
   // 16-byte chunks
   if (!(g0.ldc % 4 == 0 && g0.J % 4 == 0 && al(g0.c, 8)) || (g0.vbias && !al(g0.vbias, 8))) return -1;
@@ -1869,6 +1887,8 @@ int gemm_conv_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
   g.tiles_i = p.ti;
   g.tiles_j = p.tj;
   if (p.splits > 1) g.part = (float*)((char*)workspace + kSplitkCounterBytes);
+  if (mode != MODE_WGRAD) g.bpart = nullptr;
+  if (bias_rows) *bias_rows = g.bpart ? p.tj : 0;   // split launches fold their rows in the reduction
   const int blocks = p.ti * p.tj * p.splits;
   switch (mode) {
     case MODE_FWD_BF16:

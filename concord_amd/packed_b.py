@@ -1299,6 +1299,8 @@ class FusedConcordConv2dImplicit(torch.autograd.Function):
     (concord_conv_dgrad, on the pre-update W'), grad_W by the gathered WGRAD
     (concord_conv_wgrad) put back in (c, tap) order, then the layer's
     optimizer step (v-hat EMA, packed update), as the linear path takes it.
+    Without the Muon drive or a noise draw, the WGRAD, the reorder, the v-hat
+    EMA and the bias gradient are one entry (concord_conv_wgrad_vhat).
     The output and dx are channels-last NCHW tensors."""
 
     @staticmethod
@@ -1347,15 +1349,30 @@ class FusedConcordConv2dImplicit(torch.autograd.Function):
                                                st), "conv_dgrad")
             grad_x = dx.permute(0, 3, 1, 2)
         gt = torch.empty((Cout, T * Cin), dtype=torch.bfloat16, device=dev)
-        C.check(C.lib().concord_conv_wgrad(C.ptr(dy2), C.ptr(x4), C.ptr(gt), *geom, C.ptr(ws), ws.numel(), st),
-                "conv_wgrad")
         grad_W = torch.empty((Cout, Cin * T), dtype=torch.bfloat16, device=dev)
-        C.check(C.lib().concord_conv_grad_from_taps(C.ptr(gt), Cout, Cin, T, C.ptr(grad_W), grad_W.stride(0), st),
-                "conv_grad_from_taps")
         salt = _get_step_counter(dev)
         muon = ctx.drive == 'muon' and ctx.optimizer_kind == 'adamw'
         vhat = ctx.track_adafactor_v and ctx.v_row is not None
         prebumped = False
+        grad_bias = None
+        if vhat and not muon and not _SIGMAG_NOISE:
+            # product, reorder, v-hat EMA and bias gradient in one entry
+            M = B * Ho * Wo
+            gb = torch.empty(Cout, dtype=torch.bfloat16, device=dev) if ctx.has_bias else None
+            wsu = _workspace(dev, Cout, Cin * T, M if ctx.has_bias else 0)
+            rm = ctx.row_max_buf if ctx.track_rebalance else None
+            cm = ctx.col_max_buf if ctx.track_rebalance else None
+            C.check(C.lib().concord_conv_wgrad_vhat(
+                C.ptr(dy2), C.ptr(x4), C.ptr(gt), C.ptr(grad_W), grad_W.stride(0), *geom,
+                float(ctx.adafactor_beta2), C.ptr(ctx.v_row), C.ptr(ctx.v_col), C.ptr(ctx.sum_v_inv),
+                C.ptr(rm), C.ptr(cm), C.ptr(salt), C.ptr(gb), C.ptr(wsu), wsu.numel(), C.ptr(ws), ws.numel(),
+                st), "conv_wgrad_vhat")
+            _packed_step(ctx, grad_W, True, False)
+            return grad_x, gb, None, None, None, None, None
+        C.check(C.lib().concord_conv_wgrad(C.ptr(dy2), C.ptr(x4), C.ptr(gt), *geom, C.ptr(ws), ws.numel(), st),
+                "conv_wgrad")
+        C.check(C.lib().concord_conv_grad_from_taps(C.ptr(gt), Cout, Cin, T, C.ptr(grad_W), grad_W.stride(0), st),
+                "conv_grad_from_taps")
         if muon:
             grad_W = muon_ns5(grad_W)
         if _SIGMAG_NOISE:

@@ -403,6 +403,23 @@ int concord_conv_dgrad(const uint16_t* dy, const uint16_t* wt, uint16_t* dx, int
 int concord_conv_wgrad(const uint16_t* dy, const uint16_t* x, uint16_t* gt, int64_t B, int64_t Cin, int64_t H,
                        int64_t W, int64_t Cout, int64_t kh, int64_t kw, int64_t sh, int64_t sw, int64_t ph,
                        int64_t pw, void* workspace, size_t workspace_bytes, void* stream);
+/* The conv layer's weight-gradient step of the backward
+ * (FusedConcordConv2dPackedB.backward, concord/packed_b.py:1863-2021, with
+ * the v-hat EMA of 1281-1303): concord_conv_wgrad into gt, then
+ * concord_conv_grad_from_taps into grad_w[Cout][Cin * taps] (ld_gw >=
+ * Cin * taps), then concord_vhat_ema on grad_w, with bit-identical results;
+ * for 3 x 3 kernels the reorder and the v-hat partials are one pass.  With
+ * grad_bias, also the bias gradient sum over positions of dy (concord/
+ * packed_b.py:2003-2005), from the dy fragments the product already reads,
+ * summed over its partial rows in a fixed order.  workspace:
+ * concord_workspace_bytes(Cout, Cin * taps, B * Ho * Wo) bytes (as for
+ * concord_wgrad_vhat); gemm_workspace: concord_conv_workspace_bytes. */
+int concord_conv_wgrad_vhat(const uint16_t* dy, const uint16_t* x, uint16_t* gt, uint16_t* grad_w, int64_t ld_gw,
+                            int64_t B, int64_t Cin, int64_t H, int64_t W, int64_t Cout, int64_t kh, int64_t kw,
+                            int64_t sh, int64_t sw, int64_t ph, int64_t pw, double beta2, float* v_row,
+                            float* v_col, float* sum_v_inv, int32_t* row_max, int32_t* col_max,
+                            int32_t* salt_counter, uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
+                            void* gemm_workspace, size_t gemm_workspace_bytes, void* stream);
 
 /* The Sigma_g-shaped draw, the reference's default when its noise is on
  * (notebook/src/prototype_packed_b.py:1489-1500): in place on the bf16

@@ -300,6 +300,63 @@ def test_implicit_abi_products_float64(oracle, case):
         assert np.all(np.abs(gv - ex) <= tol), float(np.max(np.abs(gv - ex) - tol))
 
 
+@pytest.mark.parametrize("case", IMPLICIT)
+def test_conv_wgrad_vhat_matches_separate_calls(oracle, case):
+    """concord_conv_wgrad_vhat against concord_conv_wgrad +
+    concord_conv_grad_from_taps + concord_vhat_ema on the same operands:
+    gt, the packed-order gradient, v_row, v_col, sum_v_inv, the salt and the
+    zeroed watermarks bit-identical (3 x 3 kernels take the fused reorder,
+    the 3 x 1 and 5 x 5 cases the two-pass one); the bias gradient within fp32
+    summation error of the float64 sum of dy, rounded once to bf16."""
+    from concord_amd import _lib as C
+    from concord_amd import packed_b as pb
+    geom = _geom(case)
+    B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw = geom
+    T = kh * kw
+    Ho, Wo = (H + 2 * ph - kh) // sh + 1, (W + 2 * pw - kw) // sw + 1
+    M, K = B * Ho * Wo, Cin * T
+    g = torch.Generator().manual_seed(13)
+    x = torch.randn(B, H, W, Cin, generator=g).to(torch.bfloat16).to(DEV)
+    dy = (torch.randn(B, Ho, Wo, Cout, generator=g) * 0.1).to(torch.bfloat16).to(DEV)
+    vr0 = torch.rand(Cout, generator=g).to(DEV)
+    vc0 = torch.rand(K, generator=g).to(DEV)
+    dev = torch.device(DEV)
+    st = C.stream_of(dev)
+    gws = pb._conv_workspace(dev, geom)
+    outs = []
+    for fused in (False, True):
+        gt = torch.empty(Cout, K, dtype=torch.bfloat16, device=DEV)
+        gw = torch.empty(Cout, K, dtype=torch.bfloat16, device=DEV)
+        vr, vc = vr0.clone(), vc0.clone()
+        svi = torch.zeros(1, device=DEV)
+        rm = torch.full((Cout,), 5, dtype=torch.int32, device=DEV)
+        cm = torch.full((K,), 5, dtype=torch.int32, device=DEV)
+        salt = torch.full((1,), 40, dtype=torch.int32, device=DEV)
+        gb = torch.empty(Cout, dtype=torch.bfloat16, device=DEV)
+        if fused:
+            ws = pb._workspace(dev, Cout, K, M)
+            C.check(C.lib().concord_conv_wgrad_vhat(
+                C.ptr(dy), C.ptr(x), C.ptr(gt), C.ptr(gw), gw.stride(0), *geom, 0.999, C.ptr(vr), C.ptr(vc),
+                C.ptr(svi), C.ptr(rm), C.ptr(cm), C.ptr(salt), C.ptr(gb), C.ptr(ws), ws.numel(), C.ptr(gws),
+                gws.numel(), st), "conv_wgrad_vhat")
+        else:
+            C.check(C.lib().concord_conv_wgrad(C.ptr(dy), C.ptr(x), C.ptr(gt), *geom, C.ptr(gws), gws.numel(), st),
+                    "conv_wgrad")
+            C.check(C.lib().concord_conv_grad_from_taps(C.ptr(gt), Cout, Cin, T, C.ptr(gw), gw.stride(0), st),
+                    "conv_grad_from_taps")
+            pb.vhat_ema(gw, vr, vc, svi, 0.999, rm, cm, salt)
+        sync()
+        outs.append([host(t).copy() for t in (gt, gw, vr, vc, svi, rm, cm, salt)] + [host(gb).copy()])
+    for a, b in zip(outs[0][:8], outs[1][:8]):
+        np.testing.assert_array_equal(a, b)
+    assert int(outs[1][7][0]) == 41 and not outs[1][5].any() and not outs[1][6].any()
+    d64 = oracle.bf16_bits_to_f32(host(dy)).astype(np.float64)
+    exact = d64.reshape(M, Cout).sum(axis=0)
+    mag = np.abs(d64.reshape(M, Cout)).sum(axis=0)
+    got = oracle.bf16_bits_to_f32(outs[1][8]).astype(np.float64)
+    assert np.all(np.abs(got - exact) <= 2.0 ** -8 * np.abs(exact) + 2.0 ** -11 * mag)
+
+
 @pytest.mark.parametrize("gain", [1.0, 0.37])
 def test_weight_taps_bit_exact(oracle, gain):
     """W'[n][t][c] is the oracle's (gated) decode of word (n, c * taps + t)."""
