@@ -1669,7 +1669,10 @@ static FastPlan plan(const FastShape (&shapes)[NS], int64_t I, int64_t J, int64_
       // a resident block's MFMA rate falls when two share a CU
       const double per_block = (double)shapes[s].bi * shapes[s].bj * (double)(rs + 2 * TR) * shapes[s].minb;
       double cost = waves * per_block * shapes[s].weight;
-      if (sp > 1) cost += (double)sp * I * J * 8.0 / kCUs;   // partial write + read, spread over CUs
+      // split-K partials: each split writes I x J fp32 and the reduction reads
+      // them back, 8 B per element and split at ~5 TB/s, in the units of
+      // per_block (~0.73 ps per unit for an 8-wave tile at full occupancy)
+      if (sp > 1) cost += (double)sp * I * J * 2.2;
       if (cost < best_cost * 0.999) {
         best_cost = cost;
         best = FastPlan{s, sp, (int)ti, (int)tj, rs};
