@@ -1329,14 +1329,14 @@ CONCORD_DEV void bias_acc(f32x4 (&b)[NI], const bf16x8 (&fa)[NI]) {
 // sum of the partials over that row index ascending (vhat_finalize).
 // The split-K reduction shape of the dgrad kernel (gemm_dgt_kernel<DGRAD, 256,
 // 128>, 2 x 2 accumulator waves of 128 x 64), which a VH launch can carry.
-#define CONCORD_DGRAD_REDUCE MODE_DGRAD, 8, 4, 256, 128, 2, 2
+#define CONCORD_DGRAD_REDUCE MODE_DGRAD, RBI / 32, 4, RBI, 128, 2, 2
 
 // Workgroups [0, tr_blocks) compute WGRAD tiles.  A VH launch may carry more:
 // workgroups from tr_blocks on run the split-K reduction `rd` of the dgrad
 // kernel issued just before on the stream, on the CUs the WGRAD grid leaves
 // idle (200 tiles on 256 CUs at 1280 -> 5120).
 // CONV: the B operand (x) is the conv wgrad's gathered patch matrix (TrDmaConv).
-template <int BI, int BJ, int WI, int WJ, bool VH, bool CONV = false>
+template <int BI, int BJ, int WI, int WJ, bool VH, bool CONV = false, int RBI = 256>
 __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, GemmArgs rd, int tr_blocks) {
   constexpr int NW = WI * WJ, NT = 64 * NW, WTI = BI / WI, WTJ = BJ / WJ;
   if (VH && (int)blockIdx.x >= tr_blocks) {
@@ -1636,13 +1636,17 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
 // ---- planning -----------------------------------------------------------------
 // weight: measured time per FLOP relative to the 8-wave kernels; the 4-wave
 // 128 x 128 kernel ran at ~255 TFLOP/s against ~650 for the transpose-read
-// WGRAD on the same conv-shaped product (640 x 5760, reduction 8192)
+// WGRAD on the same conv-shaped product (640 x 5760, reduction 8192); the
+// 192-row tiles (more of them where 256-row tiles leave CUs idle) cost ~5%
+// more per FLOP than 256 rows (the 2048 x 1280 dgrad, reduction 5120: 220
+// tiles of 192 x 128 at 0.76 ps per unit against 240 of 256 x 128 at 0.72)
 struct FastShape { int bi, bj, waves, minb; double weight; };
 
 // tile shapes per mode (index into the launch switch below); 8-wave tiles run
 // two waves per SIMD, 4-wave 128 x 128 tiles two blocks per CU
-constexpr FastShape kFwdShapes[] = {{256, 160, 8, 1, 1.0}, {256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0}};
-constexpr FastShape kColShapes[] = {{256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0}};
+constexpr FastShape kFwdShapes[] = {{256, 160, 8, 1, 1.0}, {256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0},
+                                    {192, 160, 8, 1, 1.05}, {192, 128, 8, 1, 1.05}};
+constexpr FastShape kColShapes[] = {{256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0}, {192, 128, 8, 1, 1.05}};
 constexpr FastShape kWgrShapes[] = {{256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0}};
 constexpr int kCUs = 256;
 
@@ -1832,7 +1836,7 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd0, void* workspace, size_t ws
   // the WGRAD plan of gemm_wgrad_vhat_launch with the same room, so that both
   // routes take the same product (and so the same bits)
   const FastPlan pw = plan_mode(MODE_WGRAD, gw0.I, gw0.J, gw0.R, room);
-  if (pd.shape != 0 || pd.splits < 2 || pw.shape != 0 || pw.splits != 1) return -1;
+  if ((pd.shape != 0 && pd.shape != 2) || pd.splits < 2 || pw.shape != 0 || pw.splits != 1) return -1;
   const int tw = pw.ti * pw.tj;
   const int extra = kCUs - tw;
   if (extra < 16) return -1;   // the WGRAD grid leaves too few CUs to carry the reduction
@@ -1848,9 +1852,16 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd0, void* workspace, size_t ws
   gw.tiles_i = pw.ti;
   gw.tiles_j = pw.tj;
   *tiles_j = pw.tj;
-  hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD, 256, 128>), dim3(pd.ti * pd.tj * pd.splits), dim3(512), 0, st,
-                     gd);
-  hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true>), dim3(tw + extra), dim3(512), 0, st, gw, gd, tw);
+  if (pd.shape == 0) {
+    hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD, 256, 128>), dim3(pd.ti * pd.tj * pd.splits), dim3(512), 0, st,
+                       gd);
+    hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true>), dim3(tw + extra), dim3(512), 0, st, gw, gd, tw);
+  } else {
+    hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD, 192, 128>), dim3(pd.ti * pd.tj * pd.splits), dim3(512), 0, st,
+                       gd);
+    hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true, false, 192>), dim3(tw + extra), dim3(512), 0, st, gw,
+                       gd, tw);
+  }
   return launch_status(what);
 }
 
@@ -1930,19 +1941,25 @@ int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
     case MODE_FWD:
       if (p.shape == 0) launch_dma<MODE_FWD, 256, 160>(g, blocks, st);
       else if (p.shape == 1) launch_dma<MODE_FWD, 256, 128>(g, blocks, st);
+      else if (p.shape == 3) launch_dma<MODE_FWD, 192, 160>(g, blocks, st);
+      else if (p.shape == 4) launch_dma<MODE_FWD, 192, 128>(g, blocks, st);
       else launch<MODE_FWD, 128, 128, 2, 2, 2>(g, blocks, st);
       break;
     case MODE_FWD_BF16:
       if (p.shape == 0) launch_dma<MODE_FWD_BF16, 256, 160>(g, blocks, st);
       else if (p.shape == 1) launch_dma<MODE_FWD_BF16, 256, 128>(g, blocks, st);
+      else if (p.shape == 3) launch_dma<MODE_FWD_BF16, 192, 160>(g, blocks, st);
+      else if (p.shape == 4) launch_dma<MODE_FWD_BF16, 192, 128>(g, blocks, st);
       else launch<MODE_FWD_BF16, 128, 128, 2, 2, 2>(g, blocks, st);
       break;
     case MODE_DGRAD:
       if (p.shape == 0) launch_dgt<MODE_DGRAD, 256, 128>(g, blocks, st);
+      else if (p.shape == 2) launch_dgt<MODE_DGRAD, 192, 128>(g, blocks, st);
       else launch<MODE_DGRAD, 128, 128, 2, 2, 2>(g, blocks, st);
       break;
     case MODE_DGRAD_BF16:
       if (p.shape == 0) launch_dgt<MODE_DGRAD_BF16, 256, 128>(g, blocks, st);
+      else if (p.shape == 2) launch_dgt<MODE_DGRAD_BF16, 192, 128>(g, blocks, st);
       else launch<MODE_DGRAD_BF16, 128, 128, 2, 2, 2>(g, blocks, st);
       break;
     case MODE_WGRAD:
