@@ -421,7 +421,7 @@ def test_vhat_matches_oracle(oracle, N, K):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 2056, 648), (2048, 5120, 1280), (2048, 1280, 1280), (77, 130, 200),
-                                   (64, 136, 4096)])
+                                   (64, 136, 4096), (8192, 640, 640)])
 def test_wgrad_vhat_matches_separate_calls(oracle, M, N, K):
     """wgrad with the v-hat partials formed in its epilogue (fused path when
     the product runs unsplit on the transpose-read kernel, else the separate
@@ -528,9 +528,13 @@ def test_load_weights_matches_oracle(oracle):
 # (M, N, K).  Misaligned shapes run the generic kernel; shapes whose
 # contiguous dimensions are multiples of 8 run the branch-free kernels, with
 # ragged tile edges, a reduction tail, and (64, 136, 4096) a 4-way split-K.
+# (M, N, K); the planner takes 192-row tiles for (2048, 1280, 1280) (forward and
+# dgrad, 192 x 128 split two ways), (8192, 640, 640) (unsplit) and (1024, 2816,
+# 2048) (forward 192 x 160), and splits the 640 x 640 WGRAD over 8192 tokens 8 ways
 GEMM_SHAPES = [(64, 128, 64), (77, 130, 200), (256, 384, 1280), (1, 5, 3), (130, 1000, 70),
                (2048, 1280, 1280), (2048, 5120, 1280), (300, 2050, 645),
-               (77, 136, 200), (300, 2056, 648), (1, 8, 8), (129, 1000, 72), (64, 136, 4096)]
+               (77, 136, 200), (300, 2056, 648), (1, 8, 8), (129, 1000, 72), (64, 136, 4096),
+               (8192, 640, 640), (1024, 2816, 2048)]
 
 
 def _decoded(oracle, packed, re, ce):
