@@ -571,28 +571,28 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
   }
 }
 
-// Split-K reduction of a WGRAD launch, with the v-hat partials: one wave per
-// 64 x 64 accumulator wave tile sums the splits' partials in split order (the
-// additions of splitk_reduce_item), stores the bf16 tile and forms the v-hat
-// partials of the stored values in vhat_tile_partials' order, as the VH
-// epilogue does for an unsplit launch.  With bias partials (g.bpart), the
-// waves of column 0 of each tile also sum its j-tile's bias partial rows
-// over the splits, in split order, into the split-0 row, so the finalize
-// reads tiles_j rows as for an unsplit launch.
+// Split-K reduction of a WGRAD launch, with the v-hat partials: one block per
+// 64 x 64 accumulator wave tile, its four waves one 16-row block each, sums
+// the splits' partials in split order (the additions of splitk_reduce_item),
+// stores the bf16 tile and leaves the squares of the stored values in LDS;
+// wave 0 then forms the tile's v-hat partials in vhat_tile_partials' order,
+// as the VH epilogue does for an unsplit launch.  With bias partials
+// (g.bpart), blocks of column 0 of each tile also sum its j-tile's bias
+// partial rows over the splits, in split order, into the split-0 row, so the
+// finalize reads tiles_j rows as for an unsplit launch.
 template <int BI, int BJ, int WI, int WJ>
-__global__ __launch_bounds__(64) void splitk_reduce_vh_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256) void splitk_reduce_vh_kernel(GemmArgs g) {
   constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ, NI = WTI / 16, NJ = WTJ / 16;
   static_assert(NI == 4 && NJ == 4, "v-hat partials take 64 x 64 wave tiles");
-  const int lane = threadIdx.x;
-  // one wave per accumulator wave tile; row-major tile index
+  __shared__ float s_g2[NI][NJ][4][64];   // [x][y][e][lane]: the squares, for wave 0's v-hat partials
+  const int lane = threadIdx.x & 63, x = threadIdx.x >> 6;   // wave x takes row block x of the tile
+  // one block per accumulator wave tile; row-major tile index
   const int tile = (int)(blockIdx.x / NAW), aw = (int)(blockIdx.x % NAW);
   const int bi = tile / g.tiles_j, bj = tile % g.tiles_j;
   const int64_t row0 = (int64_t)bi * BI + (aw / WJ) * WTI, col0 = (int64_t)bj * BJ + (aw % WJ) * WTJ;
   const int64_t PT = (int64_t)NAW * NI * NJ * 256;
   const float* base = g.part + (int64_t)tile * g.splits * PT + (int64_t)aw * NI * NJ * 256 + lane * 4;
-  float g2[4][4][4];
-#pragma unroll
-  for (int x = 0; x < NI; ++x) {
+  {
     // the row of 4 blocks, every split's partial loaded before any is summed
     f32x4 part[NJ][kGemmMaxSplits];
 #pragma unroll
@@ -613,13 +613,12 @@ __global__ __launch_bounds__(64) void splitk_reduce_vh_kernel(GemmArgs g) {
       const float v[4] = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xFFFF0000u),
                           __uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u)};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) g2[x][y][e] = __fmul_rn(v[e], v[e]);
+      for (int e = 0; e < 4; ++e) s_g2[x][y][e][lane] = __fmul_rn(v[e], v[e]);
       const int64_t i = row0 + x * 16 + (lane & 15), j = col0 + y * 16 + 4 * (lane >> 4);
       if (i < g.I && j < g.J) *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = make_uint2(lo, hi);
     }
   }
-  vhat_tile_partials(g2, lane, row0, col0, g.I, g.J, g.vh_pr, g.vh_pc);
-  if (g.bpart && aw % WJ == 0) {
+  if (x == 1 && g.bpart && aw % WJ == 0) {
     const int64_t i = row0 + lane;
     if (i < g.I) {
       float* b = g.bpart + (int64_t)bj * g.I + i;
@@ -629,6 +628,16 @@ __global__ __launch_bounds__(64) void splitk_reduce_vh_kernel(GemmArgs g) {
       b[0] = sb;
     }
   }
+  __syncthreads();
+  if (x != 0) return;
+  float g2[4][4][4];
+#pragma unroll
+  for (int xx = 0; xx < NI; ++xx)
+#pragma unroll
+    for (int y = 0; y < NJ; ++y)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) g2[xx][y][e] = s_g2[xx][y][e][lane];
+  vhat_tile_partials(g2, lane, row0, col0, g.I, g.J, g.vh_pr, g.vh_pc);
 }
 
 // MFMAs of one TR-deep stage for a wave tile of NI x NJ 16x16 blocks whose
@@ -1824,7 +1833,7 @@ int gemm_wgrad_vhat_split_launch(const GemmArgs& g0, void* workspace, size_t ws_
   *bias_rows = p.tj;   // the reduction folds the splits' bias rows
   hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, false>), dim3(tiles * p.splits), dim3(512), 0, st, g,
                      GemmArgs{}, tiles * p.splits);
-  hipLaunchKernelGGL((splitk_reduce_vh_kernel<256, 128, 4, 2>), dim3((unsigned)(tiles * 8)), dim3(64), 0, st, g);
+  hipLaunchKernelGGL((splitk_reduce_vh_kernel<256, 128, 4, 2>), dim3((unsigned)(tiles * 8)), dim3(256), 0, st, g);
   return launch_status(what);
 }
 
