@@ -501,8 +501,8 @@ CONCORD_DEV int64_t splitk_reduce_items(const GemmArgs& g) {
   return (int64_t)g.tiles_i * g.tiles_j * WI * WJ * NI * NJ * 64;
 }
 
-template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
-CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
+template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ, int SP>
+CONCORD_DEV void splitk_reduce_item_sp(const GemmArgs& g, int64_t idx) {
   constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ;
   const int lane = (int)(idx % 64);
   int64_t r = idx / 64;
@@ -516,12 +516,15 @@ CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
   if (i >= g.I || j >= g.J) return;
   const int64_t PT = (int64_t)NAW * NI * NJ * 256;
   const float* p = g.part + (int64_t)tile * g.splits * PT + (int64_t)aw * NI * NJ * 256 + (x * NJ + y) * 256 + lane * 4;
-  f32x4 sum = *reinterpret_cast<const f32x4*>(p);
-  for (int s2 = 1; s2 < g.splits; ++s2) {
-    const f32x4 q = *reinterpret_cast<const f32x4*>(p + s2 * PT);
+  // every split's partial loaded before any is summed (one memory round trip)
+  f32x4 part[SP];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) sum[e] = __fadd_rn(sum[e], q[e]);
-  }
+  for (int s2 = 0; s2 < SP; ++s2) part[s2] = *reinterpret_cast<const f32x4*>(p + s2 * PT);
+  f32x4 sum = part[0];
+#pragma unroll
+  for (int s2 = 1; s2 < SP; ++s2)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sum[e] = __fadd_rn(sum[e], part[s2][e]);
   const int8_t* cexp = MODE == MODE_FWD ? g.row_exp : MODE == MODE_DGRAD ? g.col_exp : nullptr;
   float sc[4] = {1.f, 1.f, 1.f, 1.f}, bs[4] = {0.f, 0.f, 0.f, 0.f};
   if (cexp) {
@@ -545,6 +548,21 @@ CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
     o = make_uint2(combine_bf16x2(yv.x, o.x, g.as, g.at), combine_bf16x2(yv.y, o.y, g.as, g.at));
   }
   *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = o;
+}
+
+// splitk_reduce_item_sp for the launch's split count (uniform), 2 .. kGemmMaxSplits
+template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
+CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
+  static_assert(kGemmMaxSplits == 8, "one case per split count");
+  switch (g.splits) {
+    case 2: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 2>(g, idx); break;
+    case 3: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 3>(g, idx); break;
+    case 4: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 4>(g, idx); break;
+    case 5: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 5>(g, idx); break;
+    case 6: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 6>(g, idx); break;
+    case 7: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 7>(g, idx); break;
+    default: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 8>(g, idx); break;
+  }
 }
 
 // bias rows of a split WGRAD (g.bpart): value f = (bj, i) of the split-0 row
