@@ -493,6 +493,44 @@ def _only(which, reps, layer, xb, dy, torch, pb):
     print(json.dumps({"only": which, "reps": reps}))
 
 
+def _child_pids():
+    """Process ids whose parent is this process (from /proc)."""
+    pids = []
+    try:
+        for tid in os.listdir("/proc/self/task"):
+            with open(f"/proc/self/task/{tid}/children") as f:
+                pids += [int(p) for p in f.read().split()]
+    except OSError:
+        pass
+    return sorted(set(pids))
+
+
+def _reap_children(limit_s=5.0):
+    """Name on stderr any child process still running at the end and wait
+    up to limit_s for it, so the script does not leave one behind."""
+    pids = _child_pids()
+    for pid in pids:
+        try:
+            with open(f"/proc/{pid}/cmdline", "rb") as f:
+                cmd = f.read().replace(b"\0", b" ").decode(errors="replace").strip()
+        except OSError:
+            cmd = "?"
+        print(f"bench: child process {pid} still running at exit: {cmd}", file=sys.stderr)
+    t0 = time.monotonic()
+    while pids and time.monotonic() - t0 < limit_s:
+        left = []
+        for pid in pids:
+            try:
+                done, _ = os.waitpid(pid, os.WNOHANG)
+            except ChildProcessError:
+                continue
+            if done == 0:
+                left.append(pid)
+        pids = left
+        if pids:
+            time.sleep(0.1)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -751,7 +789,8 @@ def main():
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
-    print(json.dumps(out))
+    print(json.dumps(out), flush=True)
+    _reap_children()
 
 
 if __name__ == "__main__":
