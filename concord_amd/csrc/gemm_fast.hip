@@ -64,10 +64,21 @@ CONCORD_DEV int32_t ld32(Rsrc r, uint32_t voff, uint32_t soff) {
 // with M = bits of 1.5 * 2^(23+e), the float whose bits are M + m is
 // 1.5 * 2^(23+e) + m * 2^e for |m| < 2^22, so subtracting 1.5 * 2^(23+e)
 // leaves m * 2^e.  m_eff = sf + 128 (ss + vs) lies in [-65536, 65279].
+// Four VALU ops per word: the two integer adds take their sign-extended
+// byte and half-word operands straight from the word through SDWA operand
+// selects (the producer waves' decode shares the SIMDs with the MFMA waves,
+// and separate v_bfe / v_ashr extracts made it 6.5 ops per word).
 CONCORD_DEV uint32_t magic(int32_t e) { return ((uint32_t)(150 + e) << 23) | 0x400000u; }
 CONCORD_DEV float dec(int32_t w, uint32_t M) {
-  const int32_t t = (int32_t)(int8_t)(w >> 8) + (int32_t)(int8_t)w;   // ss + vs
-  const uint32_t b = ((uint32_t)t << 7) + M + (uint32_t)(w >> 16);    // + 128 (ss + vs) + sf
+  int32_t t;   // ss + vs
+  asm("v_add_u32_sdwa %0, sext(%1), sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:BYTE_0"
+      : "=v"(t)
+      : "v"(w));
+  const uint32_t u = ((uint32_t)t << 7) + M;   // + 128 (ss + vs)
+  uint32_t b;  // + sf
+  asm("v_add_u32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+      : "=v"(b)
+      : "v"(u), "v"(w));
   return __fsub_rn(__uint_as_float(b), __uint_as_float(M));
 }
 
