@@ -973,7 +973,18 @@ CONCORD_DEV int32_t cdivm(int32_t m, uint32_t mg, int32_t sh) {
 //   DG (dgrad): row = input position (b, h, w); it reads
 //       dy[b][(h + ph - ky) / sh][(w + pw - kx) / sw][c0 ..] where the
 //       division is exact and lands inside the output grid, 0 otherwise.
-template <int ROWS, int NW, bool DG>
+// MASK (kernels with at most kMaskTaps taps): init resolves each row's taps
+// once into a bit mask of the taps that fall outside (or, DG, between) the
+// grid's positions and the byte offset of its tap-(0, 0) position; a stage
+// then adds the tap's offset, the same for every row (for DG as well: for
+// the taps whose division is exact, (h + ph - ky) >> s = ((h + ph) >> s) -
+// (ky >> s)), and sets bit 31 for a masked tap, which puts the load past
+// the buffer (num_records < 2^30).  Four VALU ops per row and stage instead
+// of the bounds arithmetic.  The stages a block loads past its reduction
+// range (at most two, tap index below taps + 2 <= 31) read masked or
+// ignored data.
+constexpr int kMaskTaps = 29;
+template <int ROWS, int NW, bool DG, bool MASK = false>
 struct RowsDmaConv {
   static constexpr int INSTR = ROWS / 8;
   static constexpr int PER = INSTR / NW;
@@ -981,6 +992,7 @@ struct RowsDmaConv {
   uint32_t kc2[PER];          // byte offset of this lane's 8-channel chunk in the stage
   int32_t yy[PER], xx[PER];   // !DG: y, x of tap (0, 0); DG: h + ph, w + pw
   int32_t bb[PER];            // b * Hg; -1 for rows past the GEMM's last row
+  uint32_t moff[PER], inv[PER];   // MASK: tap-(0, 0) byte offset, masked taps
   i32x4 rs;
   int w;
   int32_t C, Hg, Wg, kw, slh, slw;
@@ -1014,9 +1026,44 @@ struct RowsDmaConv {
         xx[q] = DG ? xr + c.pw : (xr << c.slw) - c.pw;
         bb[q] = b * c.Hg;
       }
+      if constexpr (MASK) {
+        // taps = kh * kw <= kMaskTaps; row ky and column kx of the kernel
+        const int32_t kh = (int32_t)(g.R / C) / kw;
+        uint32_t colv = 0;   // kernel columns kx that land on a position
+        for (int32_t kx = 0; kx < kw; ++kx) {
+          const int32_t xn = DG ? xx[q] - kx : xx[q] + kx;
+          const bool ok = DG ? (xn >= 0 && (xn & ((1 << slw) - 1)) == 0 && (xn >> slw) < Wg)
+                             : (xn >= 0 && xn < Wg);
+          colv |= ok ? 1u << kx : 0u;
+        }
+        uint32_t valid = 0;
+        for (int32_t ky = 0; ky < kh; ++ky) {
+          const int32_t yn = DG ? yy[q] - ky : yy[q] + ky;
+          const bool ok = DG ? (yn >= 0 && (yn & ((1 << slh) - 1)) == 0 && (yn >> slh) < Hg)
+                             : (yn >= 0 && yn < Hg);
+          valid |= ok ? colv << (ky * kw) : 0u;
+        }
+        inv[q] = bb[q] >= 0 ? ~valid : ~0u;
+        const int32_t y0 = DG ? yy[q] >> slh : yy[q], x0 = DG ? xx[q] >> slw : xx[q];
+        moff[q] = (uint32_t)(((bb[q] + y0) * Wg + x0) * (C * 2)) + kc2[q];
+      }
     }
   }
   CONCORD_DEV void load(uint16_t* tile, int64_t r0, int64_t rem) const {
+    if constexpr (MASK) {
+      const int32_t tap = (int32_t)r0 / C;
+      const int32_t c0 = (int32_t)r0 - tap * C;
+      const int32_t ky = tap / kw, kx = tap - ky * kw;
+      const int32_t toff = DG ? -(((ky >> slh) * Wg + (kx >> slw)) * (C * 2)) : (ky * Wg + kx) * (C * 2);
+      const uint32_t so = uni((uint32_t)c0 * 2u);
+      const uint32_t base = lds_addr(tile);
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const uint32_t vo = (moff[q] + (uint32_t)toff) | (__builtin_amdgcn_ubfe(inv[q], (uint32_t)tap, 1u) << 31);
+        dma16(rs, vo, so, uni(base + (uint32_t)((w * PER + q) * 1024)));
+      }
+      return;
+    }
     const int32_t tap = (int32_t)r0 / C;
     const int32_t c0 = (int32_t)r0 - tap * C;
     const int32_t ky = tap / kw, kx = tap - ky * kw;
@@ -1102,13 +1149,13 @@ template <int BJ, int NT> struct BSide<MODE_DGRAD_BF16, BJ, NT> {
 // into a double-buffered padded LDS tile.  One LDS barrier per stage; before
 // it every compute wave waits until its own DMA of the next stage has landed.
 // CONV: the A operand is the conv forward's gathered x (RowsDmaConv).
-template <int MODE, int BI, int BJ, bool CONV = false>
+template <int MODE, int BI, int BJ, int CONV = 0>
 __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
   constexpr int NP = 256;
   constexpr int WTI = BI / 2, WTJ = BJ / 2;
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
   typedef BSide<MODE, BJ, NP> BS;
-  typedef typename std::conditional<CONV, RowsDmaConv<BI, 4, false>, RowsDma<BI, 4>>::type AD;
+  typedef typename std::conditional<CONV != 0, RowsDmaConv<BI, 4, false, CONV == 1>, RowsDma<BI, 4>>::type AD;
   constexpr int LB = decltype(BS::b)::LROWS;
   static_assert(LB >= BJ, "LDS tile rows");
   __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
@@ -1596,13 +1643,13 @@ CONCORD_DEV void stage_mfma_swz_tr(f32x4 (&acc)[NI][NJ], const uint16_t* la, con
 // two stages ahead, decode them and write the row-major B tile.
 // CONV (MODE_DGRAD_BF16): the conv dgrad, dy gathered by RowsDmaConv and the
 // weight rows (n, tap) by TrRowsB's conv stage offsets.
-template <int MODE, int BI, int BJ, bool CONV = false>
+template <int MODE, int BI, int BJ, int CONV = 0>
 __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
   constexpr int NP = 256;
   constexpr int WTI = BI / 2, WTJ = BJ / 2;
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
-  typedef TrRowsB<BJ, NP, MODE == MODE_DGRAD, CONV> BL;
-  typedef typename std::conditional<CONV, RowsDmaConv<BI, 4, true>, RowsDma<BI, 4>>::type AD;
+  typedef TrRowsB<BJ, NP, MODE == MODE_DGRAD, (CONV != 0)> BL;
+  typedef typename std::conditional<CONV != 0, RowsDmaConv<BI, 4, true, CONV == 1>, RowsDma<BI, 4>>::type AD;
   __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
   __shared__ __attribute__((aligned(1024))) char lds_b[2][BL::LBYTES];
 
@@ -1942,13 +1989,21 @@ int gemm_conv_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
   if (mode != MODE_WGRAD) g.bpart = nullptr;
   if (bias_rows) *bias_rows = g.bpart ? p.tj : 0;   // split launches fold their rows in the reduction
   const int blocks = p.ti * p.tj * p.splits;
+  // the gathered operand's taps resolved once per row (FWD, DGRAD: R = taps * C)
+  const bool masked = g.R / g.cv.C <= kMaskTaps;
   switch (mode) {
     case MODE_FWD_BF16:
-      hipLaunchKernelGGL((gemm_dma_kernel<MODE_FWD_BF16, 256, 160, true>), dim3(blocks), dim3(512), 0, st, g);
+      if (masked)
+        hipLaunchKernelGGL((gemm_dma_kernel<MODE_FWD_BF16, 256, 160, 1>), dim3(blocks), dim3(512), 0, st, g);
+      else
+        hipLaunchKernelGGL((gemm_dma_kernel<MODE_FWD_BF16, 256, 160, 2>), dim3(blocks), dim3(512), 0, st, g);
       launch_reduce<MODE_FWD_BF16, 256, 160, 2, 2>(g, st);
       break;
     case MODE_DGRAD_BF16:
-      hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD_BF16, 256, 128, true>), dim3(blocks), dim3(512), 0, st, g);
+      if (masked)
+        hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD_BF16, 256, 128, 1>), dim3(blocks), dim3(512), 0, st, g);
+      else
+        hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD_BF16, 256, 128, 2>), dim3(blocks), dim3(512), 0, st, g);
       launch_reduce<MODE_DGRAD_BF16, 256, 128, 2, 2>(g, st);
       break;
     case MODE_WGRAD:

@@ -185,6 +185,8 @@ IMPLICIT = [
     (64, 64, (3, 1), (2, 1), (1, 0), 3, 11, 13),
     (64, 192, 5, 1, 2, 1, 12, 10),
     (192, 64, 3, 2, 0, 2, 16, 16),
+    # 49 taps: more than the gather's per-row tap masks hold (the general path)
+    (64, 64, 7, 2, 3, 1, 13, 11),
 ]
 
 
@@ -250,7 +252,7 @@ def test_implicit_products_match_fp32(case):
     assert rel_l2(host(conv.bias.grad.float()), host(gy.float().sum(dim=(0, 2, 3)))) < 1e-2
 
 
-@pytest.mark.parametrize("case", IMPLICIT[:3])
+@pytest.mark.parametrize("case", IMPLICIT[:3] + IMPLICIT[4:5] + IMPLICIT[-1:])
 def test_implicit_abi_products_float64(oracle, case):
     """The three C-ABI products on random bf16 operands against float64
     references: each output is one fp32 sum rounded once to bf16, so
