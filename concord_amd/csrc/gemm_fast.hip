@@ -1733,6 +1733,10 @@ constexpr FastShape kFwdShapes[] = {{256, 160, 8, 1, 1.0}, {256, 128, 8, 1, 1.0}
                                     {192, 160, 8, 1, 1.05}, {192, 128, 8, 1, 1.05}};
 constexpr FastShape kColShapes[] = {{256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0}, {192, 128, 8, 1, 1.05}};
 constexpr FastShape kWgrShapes[] = {{256, 128, 8, 1, 1.0}, {128, 128, 4, 2, 2.0}};
+// the conv WGRAD (I = out channels, J = taps x in channels): 128-row tiles
+// leave no empty rows for 320 and 640 channels where 256-row tiles pad I by
+// 20-60% and run a second round of blocks
+constexpr FastShape kConvWgrShapes[] = {{256, 128, 8, 1, 1.0}, {128, 256, 8, 1, 1.0}};
 constexpr int kCUs = 256;
 
 struct FastPlan { int shape, splits, ti, tj; int64_t r_split; };
@@ -1952,18 +1956,20 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd0, void* workspace, size_t ws
 
 // the conv products take the 8-wave DMA kernels only (shape 0 of each mode)
 static FastPlan plan_conv(int mode, int64_t I, int64_t J, int64_t R, size_t room) {
-  const FastShape one[1] = {mode == MODE_FWD_BF16 ? kFwdShapes[0] : mode == MODE_WGRAD ? kWgrShapes[0]
-                                                                                       : kColShapes[0]};
+  if (mode == MODE_WGRAD) return plan(kConvWgrShapes, I, J, R, room);
+  const FastShape one[1] = {mode == MODE_FWD_BF16 ? kFwdShapes[0] : kColShapes[0]};
   return plan(one, I, J, R, room);
+}
+static FastShape conv_shape(int mode, int idx) {
+  return mode == MODE_WGRAD ? kConvWgrShapes[idx] : mode == MODE_FWD_BF16 ? kFwdShapes[0] : kColShapes[0];
 }
 
 size_t gemm_conv_partial_bytes(int mode, int64_t I, int64_t J, int64_t R) {
   if (I <= 0 || J <= 0) return 0;
   const FastPlan p = plan_conv(mode, I, J, R, (size_t)-1 / 2);
   if (p.splits <= 1) return 0;
-  const int bi = mode == MODE_FWD_BF16 ? kFwdShapes[0].bi : mode == MODE_WGRAD ? kWgrShapes[0].bi : kColShapes[0].bi;
-  const int bj = mode == MODE_FWD_BF16 ? kFwdShapes[0].bj : mode == MODE_WGRAD ? kWgrShapes[0].bj : kColShapes[0].bj;
-  return (size_t)p.ti * p.tj * bi * bj * sizeof(float) * p.splits;
+  const FastShape sh = conv_shape(mode, p.shape);
+  return (size_t)p.ti * p.tj * sh.bi * sh.bj * sizeof(float) * p.splits;
 }
 
 int gemm_conv_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_bytes, hipStream_t st,
@@ -2007,9 +2013,15 @@ int gemm_conv_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
       launch_reduce<MODE_DGRAD_BF16, 256, 128, 2, 2>(g, st);
       break;
     case MODE_WGRAD:
-      hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, false, true>), dim3(blocks), dim3(512), 0, st, g,
-                         GemmArgs{}, blocks);
-      launch_reduce<MODE_WGRAD, 256, 128, 4, 2>(g, st);
+      if (p.shape == 1) {
+        hipLaunchKernelGGL((gemm_tr_kernel<128, 256, 2, 4, false, true>), dim3(blocks), dim3(512), 0, st, g,
+                           GemmArgs{}, blocks);
+        launch_reduce<MODE_WGRAD, 128, 256, 2, 4>(g, st);
+      } else {
+        hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, false, true>), dim3(blocks), dim3(512), 0, st, g,
+                           GemmArgs{}, blocks);
+        launch_reduce<MODE_WGRAD, 256, 128, 4, 2>(g, st);
+      }
       break;
     default:
       return -1;

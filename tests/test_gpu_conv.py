@@ -188,6 +188,8 @@ IMPLICIT = [
     # 49 taps: more than the gather's per-row tap masks hold (the general path)
     (64, 64, 7, 2, 3, 1, 13, 11),
 ]
+# 320 channels: the WGRAD takes 128 x 256 tiles (the cases above 256 x 128)
+WGRAD_128_ROWS = (320, 320, 3, 1, 1, 2, 24, 24)
 
 
 def _geom(case):
@@ -214,7 +216,7 @@ def test_conv_paths():
         assert conv.conv_path(x) == want, ((cin, cout, k, s, p), shape)
 
 
-@pytest.mark.parametrize("case", IMPLICIT)
+@pytest.mark.parametrize("case", IMPLICIT + [WGRAD_128_ROWS])
 def test_implicit_products_match_fp32(case):
     """y, dx, the weight gradient the update consumes and the bias gradient
     of the implicit-GEMM path against fp32 torch convolutions of the decoded
@@ -252,7 +254,7 @@ def test_implicit_products_match_fp32(case):
     assert rel_l2(host(conv.bias.grad.float()), host(gy.float().sum(dim=(0, 2, 3)))) < 1e-2
 
 
-@pytest.mark.parametrize("case", IMPLICIT[:3] + IMPLICIT[4:5] + IMPLICIT[-1:])
+@pytest.mark.parametrize("case", IMPLICIT[:3] + IMPLICIT[4:5] + IMPLICIT[-1:] + [WGRAD_128_ROWS])
 def test_implicit_abi_products_float64(oracle, case):
     """The three C-ABI products on random bf16 operands against float64
     references: each output is one fp32 sum rounded once to bf16, so
