@@ -11,6 +11,7 @@
 // 512 B (bf16 grad) segment.  Row watermarks are reduced across the wave and
 // written with one atomic max per row; column watermarks are reduced across
 // the 4 waves in LDS and written with one atomic max per column.
+#include <cstdint>
 #include "common.h"
 
 namespace concord {
@@ -557,10 +558,23 @@ __global__ void salt_bump_kernel(int32_t* c) {
 // 2048 blocks.  Blocks of one row per wave spend their time in per-block
 // set-up (the scalar loads, the column exponents and v_col): the 640 x 5760
 // conv weight's update measured 35 us at 4 rows per block and 29 us at 8.
+// rows per block: the smallest count of block rounds times rows per block
+// (one wave row each per 4 rows), with every block resident at once when
+// the grid allows (5 blocks of 4 waves per CU at this kernel's register
+// count, 256 CUs); ties go to more rows per block (less per-block set-up)
 static int choose_tn(int64_t N, int64_t col_blocks) {
-  int tn = 64;
-  while (tn > 8 && col_blocks * cdiv(N, tn) < 2048) tn >>= 1;
-  return tn;
+  const int64_t slots = 256 * 5;
+  int best = 8;
+  int64_t best_cost = INT64_MAX;
+  for (int tn = 8; tn <= 64; tn += 4) {
+    const int64_t blocks = col_blocks * cdiv(N, tn);
+    const int64_t cost = cdiv(blocks, slots) * (tn + 2);
+    if (cost <= best_cost) {
+      best_cost = cost;
+      best = tn;
+    }
+  }
+  return best;
 }
 
 static bool aligned(const void* p, int a) { return ((uintptr_t)p % a) == 0; }
