@@ -434,22 +434,34 @@ def _config3_steps(warmup, steps, torch, ca):
 
 
 def _weight_cache_step_ms(layer, x, dy, warmup, steps, torch, ca, per_graph=1):
-    """The same step on a weight_cache=True copy of the layer."""
-    wl = ca.ConcordLinearPackedB(K_IN, N_OUT, bias=True, device=x.device, lr=5e-4, weight_cache=True)
-    wl.disable_cohpre()
-    wl.gf_consol = 50.0
-    with torch.no_grad():
-        wl.load_weights(layer.get_weight().float())
+    """The same step on a weight_cache=True copy of the layer, and on a fused
+    copy made the same way, each timed twice in turn (fused, cache, fused,
+    cache) so that both see the same state and clocks: (cache ms, fused ms),
+    the means of the two timings each."""
+    W = layer.get_weight().float()
 
-    def step():
-        x.grad = None
-        wl.bias.grad = None
-        wl(x).backward(dy)
-        wl.rebalance()
+    def timed(cache):
+        wl = ca.ConcordLinearPackedB(K_IN, N_OUT, bias=True, device=x.device, lr=5e-4, weight_cache=cache)
+        wl.disable_cohpre()
+        wl.gf_consol = 50.0
+        with torch.no_grad():
+            wl.load_weights(W)
 
-    for _ in range(3):
-        step()
-    return _graph_ms(step, warmup, steps, torch, per_graph)
+        def step():
+            x.grad = None
+            wl.bias.grad = None
+            wl(x).backward(dy)
+            wl.rebalance()
+
+        for _ in range(3):
+            step()
+        return _graph_ms(step, warmup, steps, torch, per_graph)
+
+    fused = [timed(False)]
+    cache = [timed(True)]
+    fused.append(timed(False))
+    cache.append(timed(True))
+    return sum(cache) / 2, sum(fused) / 2
 
 
 def _only(which, reps, layer, xb, dy, torch, pb):
@@ -683,7 +695,7 @@ def main():
     Wd0 = layer.get_weight()
     t_bf_fwd = _event_time_ms(lambda: pb._gemm_fwd(xb, None, None, None, 15, layer.bias, Wd0), reps, torch)
     t_bf_dgrad = _event_time_ms(lambda: pb._gemm_dgrad(dy, None, None, None, 15, Wd0), reps, torch)
-    wc_ms = _weight_cache_step_ms(layer, x, dy, args.warmup, args.steps, torch, ca, per_run)
+    wc_ms, wc_fused_ms = _weight_cache_step_ms(layer, x, dy, args.warmup, args.steps, torch, ca, per_run)
 
     # library reference (hipBLASLt through torch.matmul) on the same bf16 shapes,
     # for context only: W decoded once, not part of the measured path
@@ -776,9 +788,13 @@ def main():
                              **(config4 or {})),
         "weight_cache_mode": {
             "note": "the reference's dataflow (update emits the bf16 weight; forward and dgrad are bf16 "
-                    "GEMMs on it), same workload; context only",
+                    "GEMMs on it), same workload; context only. fused_ms_per_step: the fused step on a "
+                    "copy made and timed the same way, alternating with the cache copy (same state and "
+                    "clocks; the headline above is timed first, right after the layer's init)",
             "ms_per_step": round(wc_ms, 4),
             "tflops": round(flops_step / (wc_ms * 1e-3) / 1e12, 2),
+            "fused_ms_per_step": round(wc_fused_ms, 4),
+            "fused_tflops": round(flops_step / (wc_fused_ms * 1e-3) / 1e12, 2),
             "fwd_us": round(t_bf_fwd * 1e3, 2), "dgrad_us": round(t_bf_dgrad * 1e3, 2)},
         "library_bf16_gemm_tflops": {
             "note": "torch.matmul (hipBLASLt) on a pre-decoded bf16 W, same shapes; context only",
