@@ -139,7 +139,10 @@ CONCORD_DEV void shift_word(int32_t* p, int32_t net, int64_t n, int64_t k, int64
   *p = pack(clampi(sfn, -32768, 32767), clampi(ssn, -128, 127), clampi(vn, -128, 127));
 }
 
-// One tile of 32 rows x 256 columns (rows from nb, columns from kb).  The
+// rows of a shift tile
+constexpr int kShiftRows = 16;
+
+// One tile of kShiftRows rows x 256 columns (rows from nb, columns from kb).  The
 // words to shift are those in a fired column (every row) or a fired row (the
 // other columns).  The tile lists its fired columns, unfired columns and
 // fired rows in LDS and deals the words out to all 256 threads, so waves stay
@@ -148,7 +151,7 @@ CONCORD_DEV void shift_word(int32_t* p, int32_t net, int64_t n, int64_t k, int64
 // every thread of the block with the same arguments; it begins with a
 // barrier, so consecutive calls may reuse the lists.
 struct ShiftLists {
-  int32_t fc[256], uc[256], fr[32];
+  int32_t fc[256], uc[256], fr[kShiftRows];
   int32_t nfc, nuc, nfr;
 };
 
@@ -158,7 +161,7 @@ CONCORD_DEV void shift_tile(int32_t* __restrict__ packed, int64_t ld, int64_t N,
   const int t = threadIdx.x;
   const int64_t k = kb + t;
   const int32_t ct = k < K ? col_t[k] : 0;
-  const int32_t rt_probe = (t < 32 && nb + t < N) ? row_t[nb + t] : 0;
+  const int32_t rt_probe = (t < kShiftRows && nb + t < N) ? row_t[nb + t] : 0;
   if (!__syncthreads_or(ct != 0 || rt_probe != 0)) return;
   if (t == 0) {
     L.nfc = 0;
@@ -173,7 +176,7 @@ CONCORD_DEV void shift_tile(int32_t* __restrict__ packed, int64_t ld, int64_t N,
   if (rt_probe != 0) L.fr[atomicAdd(&L.nfr, 1)] = t;
   __syncthreads();
   const int nfc = L.nfc, nuc = L.nuc, nfr = L.nfr;
-  const int rows = (int)min((int64_t)32, N - nb);
+  const int rows = (int)min((int64_t)kShiftRows, N - nb);
   const int32_t nk = (int32_t)((uint32_t)N * (uint32_t)K);
   // fired columns, all rows of the tile
   for (int it = t; it < nfc * rows; it += 256) {
@@ -197,8 +200,8 @@ __global__ __launch_bounds__(256) void rebalance_shift_kernel(int32_t* __restric
                                                               const int32_t* bfired,
                                                               const int32_t* seed_p) {
   __shared__ ShiftLists L;
-  const int64_t kb = (int64_t)blockIdx.x * 256, nb = (int64_t)blockIdx.y * 32;
-  // the decide blocks covering this tile's 32 rows and 256 columns
+  const int64_t kb = (int64_t)blockIdx.x * 256, nb = (int64_t)blockIdx.y * kShiftRows;
+  // the decide blocks covering this tile's rows and 256 columns
   if (bfired[nb / 256] == 0 && bfired[cdiv(N, 256) + kb / 256] == 0) return;
   shift_tile(packed, ld, N, K, row_t, col_t, *seed_p, kb, nb, L);
 }
@@ -321,7 +324,7 @@ __global__ __launch_bounds__(256) void rebalance_group_shift_kernel(const int64_
       const int64_t y = x - tpref[l] + lane;   // this lane's tile in the layer
       const int64_t yb = y / ct;
       const bool flagged =
-          x + lane < l_end && (L.bfired[(yb * 32) / 256] != 0 || L.bfired[rb + (y - yb * ct)] != 0);
+          x + lane < l_end && (L.bfired[(yb * kShiftRows) / 256] != 0 || L.bfired[rb + (y - yb * ct)] != 0);
       const uint64_t m = __ballot(flagged);
       if (m == 0) {
         x = min(x + 64, l_end);   // the range may go on into the next layer
@@ -329,7 +332,7 @@ __global__ __launch_bounds__(256) void rebalance_group_shift_kernel(const int64_
       }
       x += __builtin_ctzll(m);
       const int64_t yt = x - tpref[l];
-      shift_tile(L.packed, L.ld, L.N, L.K, L.row_t, L.col_t, seed, (yt % ct) * 256, (yt / ct) * 32, LS);
+      shift_tile(L.packed, L.ld, L.N, L.K, L.row_t, L.col_t, seed, (yt % ct) * 256, (yt / ct) * kShiftRows, LS);
       ++x;
     }
   }
@@ -361,7 +364,7 @@ static int rebalance_launch(int32_t* packed, int64_t ld_p, int8_t* row_exp, int8
   hipLaunchKernelGGL(rebalance_decide_kernel, dim3((unsigned)(cdiv(N, 256) + cdiv(K, 256))), dim3(256), 0, st,
                      row_exp, col_exp, row_max, col_max, row_hwm, col_hwm, cnt_row, cnt_col, seed, N, K,
                      max_m, exp_max, exp_min, allow_tickdown, advance_seed, row_t, col_t, bfired);
-  hipLaunchKernelGGL(rebalance_shift_kernel, dim3((unsigned)cdiv(K, 256), (unsigned)cdiv(N, 32)),
+  hipLaunchKernelGGL(rebalance_shift_kernel, dim3((unsigned)cdiv(K, 256), (unsigned)cdiv(N, kShiftRows)),
                      dim3(256), 0, st, packed, ld_p, N, K, row_t, col_t, bfired, seed);
   return launch_status("rebalance");
 }
@@ -410,9 +413,9 @@ extern "C" int concord_rebalance(int32_t* packed, int64_t ld_p, int8_t* row_exp,
   CONCORD_CHECK(packed && row_exp && col_exp && row_max && col_max && seed,
                 "concord_rebalance: NULL argument");
   CONCORD_CHECK(ld_p >= K, "concord_rebalance: leading dimension < K");
-  CONCORD_CHECK(cdiv(N, 32) <= kMaxGridY,
+  CONCORD_CHECK(cdiv(N, kShiftRows) <= kMaxGridY,
                 "concord_rebalance: N=%lld rows exceed the shift kernel's grid (at most %lld rows)",
-                (long long)N, (long long)(kMaxGridY * 32));
+                (long long)N, (long long)(kMaxGridY * kShiftRows));
   const Workspace ws = workspace_layout(N, K, 0);
   if (!workspace || workspace_bytes < ws.total) {
     set_error("concord_rebalance: workspace of %zu bytes needed", ws.total);
@@ -481,7 +484,7 @@ extern "C" int concord_rebalance_group_plan(const int64_t* layers, int32_t n_lay
     const int64_t nd = cdiv(N, 256) + cdiv(K, 256);
     scr += N + K + nd;
     dpref[l + 1] = dpref[l] + nd;
-    tpref[l + 1] = tpref[l] + cdiv(N, 32) * cdiv(K, 256);
+    tpref[l + 1] = tpref[l] + cdiv(N, kShiftRows) * cdiv(K, 256);
   }
   *scratch_words = scr;
   return CONCORD_OK;

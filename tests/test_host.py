@@ -163,7 +163,7 @@ def _rg_records(sizes):
 def test_rebalance_group_plan_layout(L):
     """The group plan (host only): records copied, per-layer scratch offsets
     (row ticks N + column ticks K + one flag per 256-row / 256-column decide
-    block), prefix sums of decide blocks and of 32 x 256 shift tiles."""
+    block), prefix sums of decide blocks and of 16 x 256 shift tiles."""
     import ctypes
 
     from concord_amd import _lib as C
@@ -184,10 +184,10 @@ def test_rebalance_group_plan_layout(L):
         nd = cd(N, 256) + cd(K, 256)
         scr += N + K + nd
         dp.append(dp[-1] + nd)
-        tp.append(tp[-1] + cd(N, 32) * cd(K, 256))
+        tp.append(tp[-1] + cd(N, 16) * cd(K, 256))
     assert words.value == scr == 7254 + 257 + 256 + 3
     assert list(plan[n * C.RG_FIELDS:n * C.RG_FIELDS + n + 1]) == dp == [0, 5, 7, 32, 35]
-    assert list(plan[n * C.RG_FIELDS + n + 1:]) == tp == [0, 30, 31, 831, 831 + 9]
+    assert list(plan[n * C.RG_FIELDS + n + 1:]) == tp == [0, 57, 58, 1658, 1658 + 17]
 
 
 def test_rebalance_group_rejects_bad_plans(L):
