@@ -564,7 +564,7 @@ CONCORD_DEV void splitk_reduce_item_sp(const GemmArgs& g, int64_t idx) {
 // splitk_reduce_item_sp for the launch's split count (uniform), 2 .. kGemmMaxSplits
 template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
 CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
-  static_assert(kGemmMaxSplits == 8, "one case per split count");
+  static_assert(kGemmMaxSplits == 16, "one case per split count");
   switch (g.splits) {
     case 2: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 2>(g, idx); break;
     case 3: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 3>(g, idx); break;
@@ -572,7 +572,15 @@ CONCORD_DEV void splitk_reduce_item(const GemmArgs& g, int64_t idx) {
     case 5: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 5>(g, idx); break;
     case 6: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 6>(g, idx); break;
     case 7: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 7>(g, idx); break;
-    default: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 8>(g, idx); break;
+    case 8: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 8>(g, idx); break;
+    case 9: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 9>(g, idx); break;
+    case 10: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 10>(g, idx); break;
+    case 11: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 11>(g, idx); break;
+    case 12: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 12>(g, idx); break;
+    case 13: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 13>(g, idx); break;
+    case 14: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 14>(g, idx); break;
+    case 15: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 15>(g, idx); break;
+    default: splitk_reduce_item_sp<MODE, NI, NJ, BI, BJ, WI, WJ, 16>(g, idx); break;
   }
 }
 
@@ -622,22 +630,35 @@ __global__ __launch_bounds__(256) void splitk_reduce_vh_kernel(GemmArgs g) {
   const int64_t PT = (int64_t)NAW * NI * NJ * 256;
   const float* base = g.part + (int64_t)tile * g.splits * PT + (int64_t)aw * NI * NJ * 256 + lane * 4;
   {
-    // the row of 4 blocks, every split's partial loaded before any is summed
-    f32x4 part[NJ][kGemmMaxSplits];
+    // the row of 4 blocks, eight splits' partials loaded before any of them
+    // is summed (one memory round trip per eight splits), summed in order
+    constexpr int CH = 8;
+    static_assert(kGemmMaxSplits <= 2 * CH, "two chunks of splits");
+    f32x4 sums[NJ];
 #pragma unroll
-    for (int y = 0; y < NJ; ++y)
+    for (int c0 = 0; c0 < 2 * CH; c0 += CH) {
+      if (c0 >= g.splits) break;
+      f32x4 part[NJ][CH];
 #pragma unroll
-      for (int s2 = 0; s2 < kGemmMaxSplits; ++s2)
-        part[y][s2] = s2 < g.splits ? *reinterpret_cast<const f32x4*>(base + (x * NJ + y) * 256 + s2 * PT)
-                                    : f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int y = 0; y < NJ; ++y)
+#pragma unroll
+        for (int s2 = 0; s2 < CH; ++s2)
+          part[y][s2] = c0 + s2 < g.splits
+                            ? *reinterpret_cast<const f32x4*>(base + (x * NJ + y) * 256 + (c0 + s2) * PT)
+                            : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int y = 0; y < NJ; ++y) {
+        if (c0 == 0) sums[y] = part[y][0];
+#pragma unroll
+        for (int s2 = (c0 == 0 ? 1 : 0); s2 < CH; ++s2)
+          if (c0 + s2 < g.splits)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sums[y][e] = __fadd_rn(sums[y][e], part[y][s2][e]);
+      }
+    }
 #pragma unroll
     for (int y = 0; y < NJ; ++y) {
-      f32x4 sum = part[y][0];
-#pragma unroll
-      for (int s2 = 1; s2 < kGemmMaxSplits; ++s2)
-        if (s2 < g.splits)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) sum[e] = __fadd_rn(sum[e], part[y][s2][e]);
+      const f32x4 sum = sums[y];
       const uint32_t lo = pack_bf16x2(sum[0], sum[1]), hi = pack_bf16x2(sum[2], sum[3]);
       const float v[4] = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xFFFF0000u),
                           __uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u)};

@@ -13,7 +13,7 @@
 namespace concord {
 
 // the most ways a GEMM splits its reduction
-constexpr int kGemmMaxSplits = 8;
+constexpr int kGemmMaxSplits = 16;
 
 struct Workspace {
   size_t vhat_ticket, scratch, total;
