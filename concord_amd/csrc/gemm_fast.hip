@@ -1509,8 +1509,14 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
   for (int x = 0; x < NI; ++x) bsum[x] = f32x4{0.f, 0.f, 0.f, 0.f};
   tr_frags<NI, DA::ROWB>(fa0, ring_p, la, fsw, cwa, 0);
   tr_frags<NJ, DB::ROWB>(fb0, ring_p, lb, fsw, cwb, 0);
-  for (int s = 0; s < nst; ++s) {
-    const lds_char* cur = ring_p + (s % 3) * STAGE;
+  // stage s reads ring slot SL = s % 3.  The loop is unrolled by the three
+  // slots so that every slot address is the ring's base plus a constant: the
+  // transpose reads then take their row and sub-step offsets in the
+  // instruction's offset field (one address per fragment), where a run-time
+  // slot cost two VALU ops per read (76 per stage and wave, against 32 MFMAs).
+  auto stage = [&](int s, auto slot) {
+    constexpr int SL = decltype(slot)::value;
+    const lds_char* cur = ring_p + SL * STAGE;
     tr_frags<NI, DA::ROWB>(fa1, cur, la, fsw, cwa, 1);
     tr_frags<NJ, DB::ROWB>(fb1, cur, lb, fsw, cwb, 1);
     mfma_block<NI, NJ>(acc, fa0, fb0);
@@ -1518,14 +1524,28 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
     if (bgs) bias_acc<NI>(bsum, fa0);
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(PERT));     // own stage s+1 DMA landed
     lds_barrier();                                    // stage s fully read by every wave
-    dma_stage(s + 3);
+    {
+      // stage s + 3 into the slot stage s just left
+      const int64_t r0 = r_begin + (int64_t)(s + 3) * TR;
+      const uint32_t sl = ring_lds + (uint32_t)(SL * STAGE);
+      da.load(sl, r0, r_end - r0);
+      db.load(sl + ABYTES, r0, r_end - r0);
+    }
     // after the last stage this reads a ring slot no MFMA uses (in bounds)
-    const lds_char* nxt = ring_p + ((s + 1) % 3) * STAGE;
+    const lds_char* nxt = ring_p + ((SL + 1) % 3) * STAGE;
     tr_frags<NI, DA::ROWB>(fa0, nxt, la, fsw, cwa, 0);
     tr_frags<NJ, DB::ROWB>(fb0, nxt, lb, fsw, cwb, 0);
     mfma_block<NI, NJ>(acc, fa1, fb1);
     if (bgs) bias_acc<NI>(bsum, fa1);
+  };
+  int s = 0;
+  for (; s + 3 <= nst; s += 3) {
+    stage(s, std::integral_constant<int, 0>());
+    stage(s + 1, std::integral_constant<int, 1>());
+    stage(s + 2, std::integral_constant<int, 2>());
   }
+  if (s < nst) stage(s, std::integral_constant<int, 0>());
+  if (s + 1 < nst) stage(s + 1, std::integral_constant<int, 1>());
   if (bg) {
 #pragma unroll
     for (int x = 0; x < NI; ++x) {
