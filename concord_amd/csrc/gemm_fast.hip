@@ -1236,12 +1236,34 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
     // own DMA of stage 0 landed (stage 1's PER loads may still fly)
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(AD::PER));
     lds_barrier();
-    for (int s = 0; s < nst2; ++s) {
+    // stage s reads A slot s % 3 and B slot s % 2; unrolled by their period
+    // of six (constant slot addresses; the gathered conv operand's DMA then
+    // needs no per-stage LDS base arithmetic); nst2 is even, so two or four
+    // stages remain after the unrolled loop
+    auto cstage = [&](int s, auto ph) {
+      constexpr int P = decltype(ph)::value;
       const int64_t r2 = r_begin + (int64_t)(s + 2) * TR;
-      ad.load(lds_a[(s + 2) % 3], r2, r_end - r2);
-      if (s < nst) stage_mfma_swz<NI, NJ>(acc, lds_a[s % 3], lds_b[s & 1], wi * WTI, wj * WTJ, lane);
+      ad.load(lds_a[(P + 2) % 3], r2, r_end - r2);
+      if (s < nst) stage_mfma_swz<NI, NJ>(acc, lds_a[P % 3], lds_b[P & 1], wi * WTI, wj * WTJ, lane);
       __builtin_amdgcn_s_waitcnt(vmcnt_imm(AD::PER));
       lds_barrier();
+    };
+    int s = 0;
+    for (; s + 6 <= nst2; s += 6) {
+      cstage(s, std::integral_constant<int, 0>());
+      cstage(s + 1, std::integral_constant<int, 1>());
+      cstage(s + 2, std::integral_constant<int, 2>());
+      cstage(s + 3, std::integral_constant<int, 3>());
+      cstage(s + 4, std::integral_constant<int, 4>());
+      cstage(s + 5, std::integral_constant<int, 5>());
+    }
+    if (s < nst2) {
+      cstage(s, std::integral_constant<int, 0>());
+      cstage(s + 1, std::integral_constant<int, 1>());
+    }
+    if (s + 2 < nst2) {
+      cstage(s + 2, std::integral_constant<int, 2>());
+      cstage(s + 3, std::integral_constant<int, 3>());
     }
     // no DMA may still be writing LDS when the block ends
     __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
