@@ -158,6 +158,51 @@ CONCORD_DEV int32_t adamw_element(int32_t word, float g, int32_t te, float vr, f
 // The wd_sv/wd_sf terms are skipped only when both rates are zero: then both
 // SR deltas are +-0 and their ticks are exactly 0 (floor(+-0) + (u < 0) = 0).
 
+// Field operands taken straight from the packed word by SDWA operand
+// selects (sign-extended byte 0 = vs, byte 1 = ss, high half-word = sf), so
+// the fields need no extract instructions of their own.
+CONCORD_DEV int32_t w_ss_minus_vs(int32_t w) {
+  int32_t r;
+  asm("v_sub_u32_sdwa %0, sext(%1), sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:BYTE_0"
+      : "=v"(r) : "v"(w));
+  return r;
+}
+CONCORD_DEV float w_sf_float(int32_t w) {
+  float r;
+  asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:WORD_1" : "=v"(r) : "v"(w));
+  return r;
+}
+CONCORD_DEV int32_t w_plus_sf(int32_t x, int32_t w) {
+  int32_t r;
+  asm("v_add_u32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+      : "=v"(r) : "v"(x), "v"(w));
+  return r;
+}
+CONCORD_DEV int32_t w_xor_sf(int32_t x, int32_t w) {
+  int32_t r;
+  asm("v_xor_b32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:WORD_1"
+      : "=v"(r) : "v"(x), "v"(w));
+  return r;
+}
+CONCORD_DEV int32_t w_plus_ss(int32_t x, int32_t w) {
+  int32_t r;
+  asm("v_add_u32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+      : "=v"(r) : "v"(x), "v"(w));
+  return r;
+}
+CONCORD_DEV int32_t w_plus_vs(int32_t x, int32_t w) {
+  int32_t r;
+  asm("v_add_u32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+      : "=v"(r) : "v"(x), "v"(w));
+  return r;
+}
+CONCORD_DEV int32_t w_minus_vs(int32_t x, int32_t w) {
+  int32_t r;
+  asm("v_sub_u32_sdwa %0, %1, sext(%2) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+      : "=v"(r) : "v"(x), "v"(w));
+  return r;
+}
+
 // Specialised element for the two production configurations, chosen by the
 // host only when every dropped term is an exact no-op:
 //   RATIO (winner): ratio-coherence gates + gf evaporation, no coh_pre;
@@ -173,11 +218,9 @@ CONCORD_DEV int32_t adamw_element_fast(int32_t word, float g, float scale_fwd, f
                                        float vr, float vc, float* coh_pre, int32_t ps,
                                        float C, float alpha, float avf, float lr_kappa,
                                        const Uniform& U, int32_t* m_out) {
-  const Fields f = unpack(word);
-  int32_t sf = f.sf, ss = f.ss;
-  const int32_t vs = f.vs, vsf = f.vs * 128;
-  const float d_fs = (float)sf;
-  const float d_sv = (float)(ss * 128 - vsf);
+  const int32_t w = word;
+  const float d_fs = w_sf_float(w);                      // (float) sf
+  const float d_sv = (float)wshl(w_ss_minus_vs(w), 7);   // (float) (ss * 128 - vs * 128)
   const float cd = __fmul_rn(C, d_sv);
   const float nw = __fmul_rn(__fsub_rn(d_fs, cd), scale_fwd);
   const float v_hat = __fmul_rn(__fmul_rn(vr, vc), U.svi);
@@ -188,7 +231,7 @@ CONCORD_DEV int32_t adamw_element_fast(int32_t word, float g, float scale_fwd, f
   step = fminf(fmaxf(step, -10.0f), 10.0f);
   float delta_t = __fmul_rn(__fmul_rn(-U.lr, step), scale_inv);
   if (RATIO) delta_t = __fsub_rn(delta_t, __fmul_rn(__fmul_rn(lr_kappa, __fsub_rn(1.0f, coh)), d_fs));
-  sf = wadd(sf, sr_tick(delta_t, hash_uniform(sf, ps)));
+  int32_t sf = w_plus_sf(sr_tick(delta_t, hash_mix(w_xor_sf(ps, w))), w);   // sf + tick, hash of the old sf
 
   float gate;
   if (RATIO) {
@@ -200,13 +243,13 @@ CONCORD_DEV int32_t adamw_element_fast(int32_t word, float g, float scale_fwd, f
   }
   const float chase = __fmul_rn(__fmul_rn(alpha, gate), (float)sf);
   const int32_t t2 = sr_tick(__fmul_rn(chase, 0.0078125f), hash_uniform3(sf, ps, 0x5A5A5A5A));
-  ss = wadd(ss, t2);
+  int32_t ss = w_plus_ss(t2, w);                         // ss + t2
   sf = wsub(sf, wshl(t2, 7));
-  float dv8 = __fmul_rn(__fmul_rn(avf, (float)wsub(wshl(ss, 7), vsf)), 0.0078125f);
+  float dv8 = __fmul_rn(__fmul_rn(avf, (float)wshl(w_minus_vs(ss, w), 7)), 0.0078125f);
   if (RATIO) dv8 = __fmul_rn(dv8, __fadd_rn(U.leak_floor, __fmul_rn(__fsub_rn(1.0f, U.leak_floor), coh)));
   const int32_t t3 = sr_tick(dv8, hash_uniform3(sf, ps, 0x33335555));
-  const int32_t new_v = clampi(wadd(vs, t3), -128, 127);
-  ss = wsub(ss, wsub(new_v, vs));
+  const int32_t new_v = clampi(w_plus_vs(t3, w), -128, 127);   // vs + t3, clamped
+  ss = wsub(ss, w_minus_vs(new_v, w));                  // ss - (new_v - vs)
   const int32_t sfc = clampi(sf, -32768, 32767);
   const int32_t ssc = clampi(ss, -128, 127);
   *m_out = ssc * 128 + sfc + new_v * 128;
