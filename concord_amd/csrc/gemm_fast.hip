@@ -69,6 +69,27 @@ CONCORD_DEV int32_t ld32(Rsrc r, uint32_t voff, uint32_t soff) {
 // selects (the producer waves' decode shares the SIMDs with the MFMA waves,
 // and separate v_bfe / v_ashr extracts made it 6.5 ops per word).
 CONCORD_DEV uint32_t magic(int32_t e) { return ((uint32_t)(150 + e) << 23) | 0x400000u; }
+// magic() of the sign-extended byte I of a packed word of four exponents:
+// (sext(byte) << 23) by one SDWA shift, then one add, since
+// (150 + e) << 23 | 2^22 = (e << 23) + 0x4B400000 (two ops where the byte
+// extract, shift and add took three)
+template <int I> CONCORD_DEV uint32_t magic_byte(int32_t ex) {
+  static_assert(I >= 0 && I < 4, "byte of the exponent word");
+  uint32_t r;
+  if constexpr (I == 0)
+    asm("v_lshlrev_b32_sdwa %0, 23, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_0"
+        : "=v"(r) : "v"(ex));
+  else if constexpr (I == 1)
+    asm("v_lshlrev_b32_sdwa %0, 23, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_1"
+        : "=v"(r) : "v"(ex));
+  else if constexpr (I == 2)
+    asm("v_lshlrev_b32_sdwa %0, 23, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_2"
+        : "=v"(r) : "v"(ex));
+  else
+    asm("v_lshlrev_b32_sdwa %0, 23, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:DWORD src1_sel:BYTE_3"
+        : "=v"(r) : "v"(ex));
+  return r + 0x4B400000u;
+}
 CONCORD_DEV float dec(int32_t w, uint32_t M) {
   int32_t t;   // ss + vs
   asm("v_add_u32_sdwa %0, sext(%1), sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1 src1_sel:BYTE_0"
@@ -166,8 +187,8 @@ struct RowsPacked {
     pin(r.ex);
 #pragma unroll
     for (int q = 0; q < PER; ++q) pin(r.v[q]);
-    const uint32_t e0 = magic(sbyte(r.ex, 0)), e1 = magic(sbyte(r.ex, 1)), e2 = magic(sbyte(r.ex, 2)),
-                   e3 = magic(sbyte(r.ex, 3));
+    const uint32_t e0 = magic_byte<0>(r.ex), e1 = magic_byte<1>(r.ex), e2 = magic_byte<2>(r.ex),
+                   e3 = magic_byte<3>(r.ex);
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       uint2 o;
@@ -1669,7 +1690,9 @@ struct TrRowsB {
       const int row = 8 * rg + e;
       i32x2 o;
       if constexpr (PACKED) {
-        const uint32_t M = magic(sbyte(r.ex[e / 4], e % 4));
+        const int32_t exw = r.ex[e / 4];
+        const uint32_t M = (e % 4) == 0 ? magic_byte<0>(exw) : (e % 4) == 1 ? magic_byte<1>(exw)
+                         : (e % 4) == 2 ? magic_byte<2>(exw) : magic_byte<3>(exw);
         o[0] = (int32_t)pack_bf16x2(dec(r.v[e][0], M), dec(r.v[e][1], M));
         o[1] = (int32_t)pack_bf16x2(dec(r.v[e][2], M), dec(r.v[e][3], M));
       } else {
