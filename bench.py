@@ -559,7 +559,8 @@ def main():
                     help="skip the config-4 row (the graph-captured step over all 754 SDXL weights)")
     ap.add_argument("--only", default=None,
                     choices=["fwd", "bwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
-                             "copy"])
+                             "copy", "config3"],
+                    help="time one entry alone; config3 times only the step on each config-3 SDXL shape")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--graph-steps", type=int, default=5,
                     help="training steps captured per HIP graph (1 = one graph replay per step)")
@@ -596,6 +597,9 @@ def main():
         step()
     torch.cuda.synchronize()
 
+    if args.only == "config3":
+        print(json.dumps({"sdxl_shapes": _config3_steps(args.warmup, args.steps, torch, ca)}), flush=True)
+        return
     if args.only:
         _only(args.only, args.reps, layer, x.detach(), dy, torch, pb)
         return
