@@ -295,27 +295,13 @@ def _next_rows(layer, xb, dy, gw, reps, warmup, steps, torch, ca, pb):
     return out
 
 
-# config 4: SDXL-UNet Linear and 1x1 weights ((out, in), count, tokens M), per
-# notebook/src/sdxl_fit_smoketest.py:55-69 as tabulated for this build;
-# tokens per layer at batch 4 of a 128 x 128 latent, realistic per level:
-# 1280-channel layers at 32 x 32 (M 4096), 640-channel at 64 x 64 (M 16384),
-# 320-channel at 128 x 128 (M 65536), cross-attention k/v on 77 x 4 text
-# tokens (M 308), time/label embeddings on M 4
-SDXL_LINEAR = [((10240, 1280), 60, 4096), ((1280, 1280), 381, 4096), ((1280, 5120), 60, 4096),
-               ((1280, 2048), 120, 308), ((5120, 640), 10, 16384), ((640, 640), 70, 16384),
-               ((640, 2048), 20, 308), ((640, 2560), 10, 16384), ((640, 1280), 5, 4),
-               ((1280, 2816), 1, 4), ((320, 1280), 5, 4), ((1280, 320), 1, 4)]
-SDXL_1X1 = [((1280, 2560), 2, 4096), ((1280, 1920), 1, 4096), ((640, 1920), 1, 16384),
-            ((1280, 640), 1, 4096), ((640, 1280), 1, 16384), ((640, 960), 1, 16384),
-            ((320, 640), 2, 65536), ((320, 960), 1, 65536), ((640, 320), 1, 16384)]
-
-
 def _config4_step(steps, torch, ca, pb):
     """Config 4: one training step over all 754 SDXL Linear and 1x1 weights
     (2.25 B parameters held packed, 9.0 GB), each layer forward + backward
     (dgrad, wgrad, v-hat, fused update; winner flags) on its own token count,
     then GatedRebalance with the gate on the device.  The whole step is
     captured in one HIP graph and replayed; 6 M N K FLOP per layer."""
+    from concord_amd.shapes import SDXL_1X1, SDXL_LINEAR
     dev = torch.device("cuda:0")
     torch.manual_seed(4)
     layers, flop, params = [], 0.0, 0
@@ -397,16 +383,10 @@ def _config4_step(steps, torch, ca, pb):
     return out
 
 
-# config 3: SDXL-UNet linear shapes (out N, in K, tokens M) at their token
-# counts -- attention q/k/v/out, GEGLU in and out, the north-star shape, the
-# 640-channel set on 4096 x 2 tokens, cross-attention k/v on 77 x 2 tokens
-CONFIG3 = [(1280, 1280, 2048), (10240, 1280, 2048), (1280, 5120, 2048), (5120, 1280, 2048),
-           (640, 640, 8192), (5120, 640, 8192), (640, 2560, 8192), (1280, 2048, 154)]
-
-
 def _config3_steps(warmup, steps, torch, ca):
     """The same training step (fwd, dgrad, wgrad with v-hat, update with the
     winner flags, rebalance) on each config-3 shape; 6MNK FLOP per step."""
+    from concord_amd.shapes import CONFIG3
     out = {}
     dev = torch.device("cuda:0")
     for N, K, M in CONFIG3:

@@ -26,6 +26,11 @@ SALT_PREBUMPED = 1 << 16
 
 OK, EINVAL, ELAUNCH, EWORKSPACE = 0, -1, -2, -3
 
+# byte offset of the scratch region in the update-side workspace (after its
+# 256-byte counter area); concord_rebalance leaves the row ticks and then the
+# column ticks (int32) at its start
+WS_SCRATCH = 256
+
 # record layout of concord_rebalance_group_plan's layer table (int64 fields)
 RG_FIELDS = 16
 (RG_PACKED, RG_LD, RG_ROW_EXP, RG_COL_EXP, RG_ROW_MAX, RG_COL_MAX, RG_ROW_HWM, RG_COL_HWM, RG_SEED,

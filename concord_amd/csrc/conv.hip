@@ -689,8 +689,12 @@ extern "C" int concord_conv_wgrad(const uint16_t* dy, const uint16_t* x, uint16_
   CONCORD_CHECK(conv_shape(B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw, s), "concord_conv_wgrad: bad geometry");
   CONCORD_CHECK(conv_implicit_shape(s), "concord_conv_wgrad: shape not taken by the implicit kernels "
                                         "(concord_conv_implicit_ok)");
-  CONCORD_CHECK(dy && x && gt, "concord_conv_wgrad: NULL argument");
+  CONCORD_CHECK(gt && (B == 0 || (dy && x)), "concord_conv_wgrad: NULL argument");
   const int64_t T = kh * kw;
+  if (B == 0) {   // an empty batch: the sum over no positions
+    fill_zero_bf16_launch(gt, T * Cin, Cout, T * Cin, (hipStream_t)stream);
+    return launch_status("conv_wgrad");
+  }
   GemmArgs g = conv_args(dy, Cout, x, T * Cin, gt, T * Cin, Cout, T * Cin, B * s.Ho * s.Wo, nullptr);
   g.cv = conv_idx(s, Cin, H, W, s.Ho, s.Wo, Cin, B * H * W * Cin * 2, 0);
   const int rc = gemm_conv_launch(MODE_WGRAD, g, workspace, workspace_bytes, (hipStream_t)stream, "conv_wgrad");
@@ -709,7 +713,8 @@ extern "C" int concord_conv_wgrad_vhat(const uint16_t* dy, const uint16_t* x, ui
                 "concord_conv_wgrad_vhat: bad geometry");
   CONCORD_CHECK(conv_implicit_shape(s), "concord_conv_wgrad_vhat: shape not taken by the implicit kernels "
                                         "(concord_conv_implicit_ok)");
-  CONCORD_CHECK(dy && x && gt && grad_w && v_row && v_col && sum_v_inv, "concord_conv_wgrad_vhat: NULL argument");
+  CONCORD_CHECK(gt && grad_w && v_row && v_col && sum_v_inv && (B == 0 || (dy && x)),
+                "concord_conv_wgrad_vhat: NULL argument");
   const int64_t T = kh * kw, N = Cout, K = T * Cin, M = B * s.Ho * s.Wo;
   CONCORD_CHECK(ld_gw >= K, "concord_conv_wgrad_vhat: leading dimension < in_channels * taps");
   CONCORD_CHECK(Cout <= kMaxGridY, "concord_conv_wgrad_vhat: more than %lld output channels", (long long)kMaxGridY);
@@ -717,6 +722,12 @@ extern "C" int concord_conv_wgrad_vhat(const uint16_t* dy, const uint16_t* x, ui
   const Workspace ws = workspace_layout(N, K, grad_bias ? M : 0);
   CONCORD_CHECK(workspace && workspace_bytes >= ws.total, "concord_conv_wgrad_vhat: workspace of %zu bytes needed",
                 ws.total);
+  if (B == 0) {   // an empty batch: zero tap-major and packed-order gradients, then their v-hat EMA
+    fill_zero_bf16_launch(gt, K, Cout, K, st);
+    wgrad_vhat_empty_batch(grad_w, ld_gw, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter,
+                           grad_bias, workspace, st);
+    return launch_status("conv_wgrad_vhat");
+  }
   const VhatScratch v = vhat_scratch(N, K);
   float* pr = (float*)((char*)workspace + ws.scratch);
   float* pc = pr + v.pr;

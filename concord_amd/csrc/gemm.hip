@@ -566,8 +566,12 @@ extern "C" int concord_wgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* 
                              void* workspace, size_t workspace_bytes, void* stream) {
   CONCORD_CHECK(sizes_ok(M, N, K), "concord_wgrad: bad size");
   if (N == 0 || K == 0) return CONCORD_OK;
-  CONCORD_CHECK(dy && x && grad_w, "concord_wgrad: NULL argument");
+  CONCORD_CHECK(grad_w && (M == 0 || (dy && x)), "concord_wgrad: NULL argument");
   CONCORD_CHECK(ld_dy >= N && ld_x >= K && ld_gw >= K, "concord_wgrad: bad leading dimension");
+  if (M == 0) {   // an empty batch: the sum over no tokens
+    fill_zero_bf16_launch(grad_w, ld_gw, N, K, (hipStream_t)stream);
+    return launch_status("wgrad");
+  }
   GemmArgs g = make_args(dy, x, ld_dy, ld_x, nullptr, nullptr, 0, nullptr, grad_w, ld_gw, N, K, M, false);
   return launch_gemm<MODE_WGRAD>(g, workspace, workspace_bytes, (hipStream_t)stream, "wgrad");
 }
@@ -585,6 +589,11 @@ static int wgrad_vhat_impl(const GemmArgs* gd, const uint16_t* dy, int64_t ld_dy
   if (!workspace || workspace_bytes < ws.total) {
     set_error("%s: workspace of %zu bytes needed", what, ws.total);
     return CONCORD_EWORKSPACE;
+  }
+  if (M == 0) {   // an empty batch: no dgrad rows, a zero weight gradient
+    wgrad_vhat_empty_batch(grad_w, ld_gw, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max, salt_counter,
+                           grad_bias, workspace, st);
+    return launch_status(what);
   }
   const VhatScratch v = vhat_scratch(N, K);
   float* pr = (float*)((char*)workspace + ws.scratch);
@@ -633,7 +642,7 @@ extern "C" int concord_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const uint1
                                   uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
                                   void* gemm_workspace, size_t gemm_workspace_bytes, void* stream) {
   CONCORD_CHECK(sizes_ok(M, N, K) && N > 0 && K > 0, "concord_wgrad_vhat: bad size");
-  CONCORD_CHECK(dy && x && grad_w && v_row && v_col && sum_v_inv, "concord_wgrad_vhat: NULL argument");
+  CONCORD_CHECK(grad_w && v_row && v_col && sum_v_inv && (M == 0 || (dy && x)), "concord_wgrad_vhat: NULL argument");
   CONCORD_CHECK(ld_dy >= N && ld_x >= K && ld_gw >= K, "concord_wgrad_vhat: bad leading dimension");
   return wgrad_vhat_impl(nullptr, dy, ld_dy, x, ld_x, grad_w, ld_gw, M, N, K, beta2, v_row, v_col, sum_v_inv,
                          row_max, col_max, salt_counter, grad_bias, workspace, workspace_bytes, gemm_workspace,
@@ -649,7 +658,7 @@ extern "C" int concord_dgrad_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const
                                         uint16_t* grad_bias, void* workspace, size_t workspace_bytes,
                                         void* gemm_workspace, size_t gemm_workspace_bytes, void* stream) {
   CONCORD_CHECK(sizes_ok(M, N, K) && N > 0 && K > 0, "concord_dgrad_wgrad_vhat: bad size");
-  CONCORD_CHECK(dy && packed && row_exp && col_exp && dx && x && grad_w && v_row && v_col && sum_v_inv,
+  CONCORD_CHECK(packed && row_exp && col_exp && grad_w && v_row && v_col && sum_v_inv && (M == 0 || (dy && dx && x)),
                 "concord_dgrad_wgrad_vhat: NULL argument");
   CONCORD_CHECK(ld_dy >= N && ld_p >= K && ld_dx >= K && ld_x >= K && ld_gw >= K,
                 "concord_dgrad_wgrad_vhat: bad leading dimension");

@@ -41,6 +41,10 @@ typedef int32_t i32x2 __attribute__((ext_vector_type(2)));
 constexpr uint32_t kOOB = 0x80000000u;
 constexpr int kMaxSplits = kGemmMaxSplits;
 
+// num_records of an operand band: (last row's offset + its length) in bytes,
+// 0 when the band is empty (R = 0 or no rows left makes the formula negative,
+// and a wrapped 32-bit count would put kOOB inside the buffer)
+CONCORD_DEV uint32_t nrec(int64_t bytes) { return bytes > 0 ? (uint32_t)bytes : 0u; }
 CONCORD_DEV Rsrc make_rsrc(const void* p, uint32_t bytes) {
   // dword 3 = 0x00020000: 32-bit data format, raw (stride 0) addressing
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
@@ -132,7 +136,7 @@ struct RowsBf16 {
   Rsrc rs;
   CONCORD_DEV void init(const uint16_t* band, int64_t ld, int64_t rows_left, int64_t R, int t) {
     kc = (t % 8) * 8;
-    rs = make_rsrc(band, (uint32_t)(((rows_left - 1) * ld + R) * 2));
+    rs = make_rsrc(band, nrec(((rows_left - 1) * ld + R) * 2));
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int64_t row = t / 8 + (NT / 8) * q;
@@ -168,7 +172,7 @@ struct RowsPacked {
   CONCORD_DEV void init(const int32_t* band, int64_t ld, int64_t rows_left, int64_t R,
                         const int8_t* exps, int t) {
     kc = (t % 16) * 4;
-    rs = make_rsrc(band, (uint32_t)(((rows_left - 1) * ld + R) * 4));
+    rs = make_rsrc(band, nrec(((rows_left - 1) * ld + R) * 4));
     es = make_rsrc(exps, (uint32_t)R);
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
@@ -230,7 +234,7 @@ struct ColsPacked {
                         const int8_t* exps, int t) {
     rb = G::rb(t);
     ld4 = (uint32_t)(ld * 4);
-    rs = make_rsrc(band, (uint32_t)(((R - 1) * ld + cols_left) * 4));
+    rs = make_rsrc(band, nrec(((R - 1) * ld + cols_left) * 4));
     es = make_rsrc(exps, (uint32_t)R);
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
@@ -292,7 +296,7 @@ struct ColsBf16 {
   CONCORD_DEV void init(const uint16_t* band, int64_t ld, int64_t cols_left, int64_t R, int t) {
     rb = G::rb(t);
     ld2 = (uint32_t)(ld * 2);
-    rs = make_rsrc(band, (uint32_t)(((R - 1) * ld + cols_left) * 2));
+    rs = make_rsrc(band, nrec(((R - 1) * ld + cols_left) * 2));
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
       const int64_t col = G::col(t, q);
@@ -981,7 +985,7 @@ struct RowsDma {
     // raw buffer descriptor: base address, stride 0, num_records, dword 3
     const uint64_t base = (uint64_t)(uintptr_t)band;
     rs = i32x4{(int32_t)(uint32_t)base, (int32_t)(uint32_t)((base >> 32) & 0xFFFF),
-               (int32_t)(uint32_t)(((rows_left - 1) * ld + R) * 2), 0x00020000};
+               (int32_t)nrec(((rows_left - 1) * ld + R) * 2), 0x00020000};
     for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(rs[e]);
 #pragma unroll
     for (int q = 0; q < PER; ++q) {
@@ -1332,7 +1336,7 @@ struct TrDma {
     lrow = lane / (ROWB / 16);
     const uint64_t base = (uint64_t)(uintptr_t)band;
     const int64_t bytes = ((R - 1) * ld + (cols_left < COLS ? cols_left : COLS)) * 2;
-    rs = i32x4{(int32_t)(uint32_t)base, (int32_t)(uint32_t)((base >> 32) & 0xFFFF), (int32_t)(uint32_t)bytes,
+    rs = i32x4{(int32_t)(uint32_t)base, (int32_t)(uint32_t)((base >> 32) & 0xFFFF), (int32_t)nrec(bytes),
                0x00020000};
     for (int e = 0; e < 4; ++e) rs[e] = __builtin_amdgcn_readfirstlane(rs[e]);
 #pragma unroll
@@ -1648,7 +1652,7 @@ struct TrRowsB {
     col = 4 * (t % CG);
     rg = t / CG;
     ldb = (uint32_t)(ld * ES);
-    rs = make_rsrc(band, (uint32_t)(((R - 1) * ld + cols_left) * ES));
+    rs = make_rsrc(band, nrec(((R - 1) * ld + cols_left) * ES));
     if (PACKED) es = make_rsrc(exps, (uint32_t)R);
     voff = col < cols_left ? (uint32_t)((8 * rg * ld + col) * ES) : kOOB;
   }

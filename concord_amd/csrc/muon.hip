@@ -80,7 +80,15 @@ __global__ __launch_bounds__(64) void frob_den_kernel(const float* __restrict__ 
       }
     }
   }
-  if (lane == 0) *den = __fmul_rn(fmaxf(sqrt_rn(s), 1e-12f), 1.00000011920928955078125f);
+  // the drive's g / max(||g||, 1e-12), then ns5's / (||that|| + 1e-7), as
+  // one denominator n (||g|| / n + 1e-7): for ||g|| >= 1e-12 the quotient is
+  // exactly 1 and the sum fl(1 + 1e-7); below, ||g|| / n < 1 and the input
+  // is brought back to unit norm as the reference's second division does
+  if (lane == 0) {
+    const float norm = sqrt_rn(s);
+    const float n = fmaxf(norm, 1e-12f);
+    *den = __fmul_rn(n, __fadd_rn(__fdiv_rn(norm, n), 1e-7f));
+  }
 }
 
 // dst[r][c] = bf16(op(src)) over a 64 x 64 tile, where the destination is

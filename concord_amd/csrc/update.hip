@@ -597,14 +597,12 @@ __global__ void salt_bump_kernel(int32_t* c) {
   if (threadIdx.x == 0 && blockIdx.x == 0) c[0] = wadd(c[0], 1);
 }
 
-// Rows per block: the most rows (at least 8, two per wave) that still give
-// 2048 blocks.  Blocks of one row per wave spend their time in per-block
-// set-up (the scalar loads, the column exponents and v_col): the 640 x 5760
-// conv weight's update measured 35 us at 4 rows per block and 29 us at 8.
-// rows per block: the smallest count of block rounds times rows per block
-// (one wave row each per 4 rows), with every block resident at once when
-// the grid allows (5 blocks of 4 waves per CU at this kernel's register
-// count, 256 CUs); ties go to more rows per block (less per-block set-up)
+// rows per block: the smallest count of block rounds times (rows per block
+// + 2), a round being the blocks resident at once (5 blocks of 4 waves per
+// CU at this kernel's register count, 256 CUs); the +2 prices the per-block
+// set-up (the scalar loads, the column exponents and v_col), which dominated
+// at one row per wave (the 640 x 5760 conv weight: 35 us at 4 rows per
+// block, 29 us at 8); ties go to more rows per block
 static int choose_tn(int64_t N, int64_t col_blocks) {
   const int64_t slots = 256 * 5;
   int best = 8;

@@ -23,4 +23,15 @@ void vhat_finish_launch(const float* pr, const float* pc, float* bsum, uint32_t*
 void bias_grad_launch(const uint16_t* dy, int64_t ld, int64_t M, int64_t N, uint16_t* grad_bias, float* part,
                       hipStream_t st);
 
+// p[r][c] = 0 for r < rows, c < cols (row stride ld elements); a kernel, not
+// hipMemsetAsync, so that a captured graph replays it correctly
+void fill_zero_bf16_launch(uint16_t* p, int64_t ld, int64_t rows, int64_t cols, hipStream_t st);
+
+// the weight gradient of an empty batch (M = 0): grad_w = 0, then the v-hat
+// EMA of that zero gradient (the v_row / v_col decay, watermark zeroing, salt
+// advance) and a zero bias gradient, as the product path would give them
+void wgrad_vhat_empty_batch(uint16_t* grad_w, int64_t ld_gw, int64_t N, int64_t K, double beta2, float* v_row,
+                            float* v_col, float* sum_v_inv, int32_t* row_max, int32_t* col_max,
+                            int32_t* salt_counter, uint16_t* grad_bias, void* workspace, hipStream_t st);
+
 }  // namespace concord

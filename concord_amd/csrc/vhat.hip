@@ -314,6 +314,33 @@ void bias_grad_launch(const uint16_t* dy, int64_t ld, int64_t M, int64_t N, uint
                      grad_bias);
 }
 
+__global__ __launch_bounds__(256) void fill_zero_bf16_kernel(uint16_t* p, int64_t ld, int64_t rows, int64_t cols) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) p[r * ld + c] = 0;
+}
+
+void fill_zero_bf16_launch(uint16_t* p, int64_t ld, int64_t rows, int64_t cols, hipStream_t st) {
+  if (rows <= 0 || cols <= 0) return;
+  hipLaunchKernelGGL(fill_zero_bf16_kernel, dim3((unsigned)cdiv(cols, 256), grid_y(rows)), dim3(256), 0, st, p,
+                     ld, rows, cols);
+}
+
+void wgrad_vhat_empty_batch(uint16_t* grad_w, int64_t ld_gw, int64_t N, int64_t K, double beta2, float* v_row,
+                            float* v_col, float* sum_v_inv, int32_t* row_max, int32_t* col_max,
+                            int32_t* salt_counter, uint16_t* grad_bias, void* workspace, hipStream_t st) {
+  const Workspace ws = workspace_layout(N, K, 0);
+  const VhatScratch v = vhat_scratch(N, K);
+  float* pr = (float*)((char*)workspace + ws.scratch);
+  float* pc = pr + v.pr;
+  float* bsum = pc + v.pc;
+  fill_zero_bf16_launch(grad_w, ld_gw, N, K, st);
+  vhat_partials_launch(grad_w, ld_gw, N, K, pr, pc, st);
+  // no bias partial rows: the finalize writes grad_bias = bf16(0)
+  vhat_finish_launch(pr, pc, bsum, (uint32_t*)((char*)workspace + ws.vhat_ticket), N, K, beta2, v_row, v_col,
+                     sum_v_inv, row_max, col_max, salt_counter, st, nullptr, 0, grad_bias);
+}
+
 }  // namespace concord
 
 using namespace concord;

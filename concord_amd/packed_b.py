@@ -23,7 +23,6 @@ import math
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import _lib as C
 
@@ -397,30 +396,23 @@ def vhat_ema(grad_W, v_row, v_col, sum_v_inv, beta2=0.999, row_max=None, col_max
         ws.numel(), C.stream_of(grad_W.device)), "vhat_ema")
 
 
-def _reb_stats_update(packed_w, row_exp, col_exp, row_max, col_max, MAX_M, EXP_MAX, EXP_MIN,
-                      allow_tickdown):
-    # diagnostic (concord/packed_b.py:1161-1179): host syncs, off by default
-    N, K = packed_w.shape
-    ss = (packed_w << 16) >> 24
-    vs = (packed_w << 24) >> 24
-    i8mag = torch.maximum(ss.abs(), vs.abs())
-    rmed = i8mag.median(dim=1).values.to(torch.int32)
-    cmed = i8mag.median(dim=0).values.to(torch.int32)
-    re, ce = row_exp.to(torch.int32), col_exp.to(torch.int32)
-    ru = (row_max > MAX_M) & (re < EXP_MAX)
-    cu = (col_max > MAX_M) & (ce < EXP_MAX)
-    if allow_tickdown:
-        rd = (row_max <= MAX_M) & (rmed <= 31) & (re > EXP_MIN)
-        cd = (col_max <= MAX_M) & (cmed <= 31) & (ce > EXP_MIN)
-    else:
-        rd, cd = torch.zeros_like(ru), torch.zeros_like(cu)
-    rt = ru.to(torch.int32) - rd.to(torch.int32)
-    ct = cu.to(torch.int32) - cd.to(torch.int32)
-    lsh = (-(rt[:, None] + ct[None, :])).clamp(min=0).to(torch.float32)
-    clip = ((i8mag.to(torch.float32) * torch.exp2(lsh)) > 127).sum().item()
+def _reb_stats_update(ws, N, K, mag):
+    """Rebalance diagnostics (the counters of concord/packed_b.py:1161-1179)
+    from this call's decisions: the decide kernel leaves its int32 ticks
+    (+1 up, -1 down, 0) for the N rows and then the K columns at the start of
+    the workspace scratch.  A word whose row and column ticks sum to -s
+    (tick-down) has its int8 fields shifted left by s; it clips when its
+    larger int8 magnitude before the call, `mag` (None without tick-down),
+    exceeds 127 after the shift.  Host syncs; off by default."""
+    t = ws[C.WS_SCRATCH:C.WS_SCRATCH + 4 * (N + K)].view(torch.int32)
+    rt, ct = t[:N], t[N:]
+    clip = 0
+    if mag is not None:
+        lsh = (-(rt[:, None] + ct[None, :])).clamp(min=0)
+        clip = int(((mag << lsh) > 127).sum())
     _REB_STATS['calls'] += 1
-    _REB_STATS['tickup_dim'] += int(ru.sum() + cu.sum())
-    _REB_STATS['tickdown_dim'] += int(rd.sum() + cd.sum())
+    _REB_STATS['tickup_dim'] += int((rt > 0).sum() + (ct > 0).sum())
+    _REB_STATS['tickdown_dim'] += int((rt < 0).sum() + (ct < 0).sum())
     _REB_STATS['dim_total'] += N + K
     _REB_STATS['clip_elems'] += clip
     _REB_STATS['elem_total'] += N * K
@@ -436,15 +428,18 @@ def rebalance_packed(packed_w, row_exp, col_exp, row_max, col_max, MAX_M=24000, 
     N, K = _check_packed(packed_w, row_exp, col_exp)
     if seed_buf is None:
         seed_buf = _ensure_reb_seed_tensor(packed_w.device)
-    if _REB_STATS is not None:
-        _reb_stats_update(packed_w, row_exp, col_exp, row_max, col_max, MAX_M, EXP_MAX, EXP_MIN,
-                          allow_tickdown)
+    mag = None
+    if _REB_STATS is not None and allow_tickdown:
+        # the larger int8 field magnitude of each word before the shift
+        mag = torch.maximum(((packed_w << 16) >> 24).abs(), ((packed_w << 24) >> 24).abs())
     ws = _workspace(packed_w.device, N, K)
     C.check(C.lib().concord_rebalance(
         C.ptr(packed_w), packed_w.stride(0), C.ptr(row_exp), C.ptr(col_exp), C.ptr(row_max),
         C.ptr(col_max), C.ptr(row_hwm), C.ptr(col_hwm), C.ptr(seed_buf), N, K, int(MAX_M),
         int(EXP_MAX), int(EXP_MIN), int(bool(allow_tickdown)), int(bool(advance_seed)),
         C.ptr(ws), ws.numel(), C.stream_of(packed_w.device)), "rebalance_packed")
+    if _REB_STATS is not None:
+        _reb_stats_update(ws, N, K, mag)
 
 
 def load_packed(W, packed_w, row_exp, col_exp, exp_min=-8, exp_max=7, mantissa_bias=15,
@@ -1072,11 +1067,17 @@ class ConcordLinearPackedB(nn.Module):
         return wbuf, rmbuf, cmbuf
 
     def forward(self, x):
+        return self._forward_rows(x, self.fast_gain)
+
+    def _forward_rows(self, x, fast_gain):
+        """forward() on rows of features; fast_gain < 1 gates s_fast out of the
+        forward weight (the linear layer's forward; the conv layer passes 1.0,
+        since the reference's conv forward never gates, 2046-2065)."""
         in_dtype = x.dtype
         if x.dtype != torch.bfloat16:
             x = x.to(torch.bfloat16)
         wbuf, rmbuf, cmbuf = self._ensure_buffers()
-        if self.fast_gain < 1.0:
+        if fast_gain < 1.0:
             # gate s_fast out of the forward weight (1762-1772); the GEMMs then read
             # the gated bf16 copy, the packed state keeps the full s_fast
             pw = self.packed_w
@@ -1084,7 +1085,7 @@ class ConcordLinearPackedB(nn.Module):
                 wbuf = torch.empty(pw.shape, dtype=torch.bfloat16, device=pw.device)
             C.check(C.lib().concord_materialize_gated(
                 C.ptr(pw), pw.stride(0), C.ptr(self.row_exp), C.ptr(self.col_exp), pw.shape[0],
-                pw.shape[1], self.MANTISSA_BIAS, float(self.fast_gain), C.ptr(wbuf), wbuf.stride(0),
+                pw.shape[1], self.MANTISSA_BIAS, float(fast_gain), C.ptr(wbuf), wbuf.stride(0),
                 C.stream_of(pw.device)), "materialize_gated")
         y = FusedConcordLinearPackedB.apply(
             x, self.packed_w, self.row_exp, self.col_exp, self.bias,
@@ -1316,7 +1317,7 @@ class FusedConcordConv2dImplicit(torch.autograd.Function):
         wt = torch.empty((Cout, T * Cin), dtype=torch.bfloat16, device=dev)
         C.check(C.lib().concord_conv_weight_taps(
             C.ptr(pw_), pw_.stride(0), C.ptr(layer.row_exp), C.ptr(layer.col_exp), Cout, Cin, T,
-            layer.MANTISSA_BIAS, float(layer.fast_gain), C.ptr(wt), st), "conv_weight_taps")
+            layer.MANTISSA_BIAS, 1.0, C.ptr(wt), st), "conv_weight_taps")
         bias_bf16 = None
         if bias is not None:
             bias_bf16 = (bias if bias.dtype == torch.bfloat16 else bias.to(torch.bfloat16)).contiguous()
@@ -1445,9 +1446,11 @@ class ConcordConv2dPackedB(ConcordLinearPackedB):
         geom = self._geom(x)
         B, cin, H, W, cout, kh, kw, sh, sw, ph, pw = geom
         path = self.conv_path(x)
+        # the reference's conv forward (concord/packed_b.py:2046-2065) runs on
+        # the ungated weight: fast_gain does not apply to convolutions
         if path == 'linear':
             x2 = _nhwc(x).reshape(B * H * W, cin)
-            y = super().forward(x2).view(B, H, W, cout).permute(0, 3, 1, 2)
+            y = self._forward_rows(x2, 1.0).view(B, H, W, cout).permute(0, 3, 1, 2)
         elif path == 'implicit':
             wbuf, rmbuf, cmbuf = self._ensure_buffers()
             y = FusedConcordConv2dImplicit.apply(x, self.bias, self, geom, wbuf, rmbuf, cmbuf)
@@ -1455,7 +1458,7 @@ class ConcordConv2dPackedB(ConcordLinearPackedB):
             Ho = (H + 2 * ph - kh) // sh + 1
             Wo = (W + 2 * pw - kw) // sw + 1
             cols = _Im2col.apply(x, kh, kw, sh, sw, ph, pw)
-            y = _ToNCHW.apply(super().forward(cols), B, Ho, Wo)
+            y = _ToNCHW.apply(self._forward_rows(cols, 1.0), B, Ho, Wo)
         return y.to(in_dtype)
 
     @property

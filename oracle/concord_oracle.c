@@ -658,7 +658,7 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
  *     in a block, lane t (0..255) sums elements t, t+256, ... (32 of them)
  *     ascending from 0.0f, then the halving tree over the 256 lane sums;
  *     block totals ascending from 0.0f.  norm = sqrtf(sum).
- *   X0 = bf16(g / (max(norm, 1e-12) * fl(1 + 1e-7))), transposed when N > K so
+ *   X0 = bf16(g / (n * (norm / n + 1e-7))), n = max(norm, 1e-12), transposed when N > K so
  *   X is m x n, m <= n.
  *   per iteration (a, b, c = 3.4445, -4.7750, 2.0315):
  *     A = bf16(X X^T), AA = bf16(A A), B = bf16(b A + c AA), BX = bf16(B X),
@@ -889,9 +889,11 @@ void oracle_muon_ns5(const uint16_t* g, int64_t N, int64_t K, float gamma, uint1
     const int tr = N > K;
     const int64_t m = tr ? K : N, n = tr ? N : K;
     const float norm = sqrtf(oracle_frob_sumsq(g, N, K));
-    /* g / max(||g||, 1e-12), then / (||unit|| + 1e-7) with ||unit|| = 1:
-     * exp9_muon.py:75, 82 (drive) and 47 (ns5), one fp32 product */
-    const float den = fmaxf(norm, 1e-12f) * 1.00000011920928955078125f;
+    /* g / n with n = max(||g||, 1e-12), then / (||g / n|| + 1e-7):
+     * exp9_muon.py:75, 82 (drive) and 47 (ns5), as one denominator
+     * n * (||g|| / n + 1e-7); ||g|| / n is exactly 1 for ||g|| >= 1e-12 */
+    const float nn = fmaxf(norm, 1e-12f);
+    const float den = nn * (norm / nn + 1e-7f);
     float* X = (float*)malloc((size_t)(m * n) * sizeof(float));
     float* BX = (float*)malloc((size_t)(m * n) * sizeof(float));
     float* A = (float*)malloc((size_t)(m * m) * sizeof(float));

@@ -34,8 +34,7 @@ def _winner(layer, pb):
 # (out N, in K, tokens M): attention q/k/v/out, GEGLU in / out and the
 # north-star shape on 1024 tokens x batch 2; the 640-channel set on 4096 x 2;
 # cross-attention k/v on 77 x 2 tokens
-CONFIG3 = [(1280, 1280, 2048), (10240, 1280, 2048), (1280, 5120, 2048), (5120, 1280, 2048),
-           (640, 640, 8192), (5120, 640, 8192), (640, 2560, 8192), (1280, 2048, 154)]
+from concord_amd.shapes import CONFIG3  # noqa: E402
 
 
 @pytest.mark.parametrize("N,K,M", CONFIG3)
@@ -164,7 +163,7 @@ def test_config2_gpt_stack_trains():
 
 
 # config 4's SDXL-UNet Linear and 1x1 weights ((out, in), count, tokens M)
-from bench import SDXL_1X1, SDXL_LINEAR  # noqa: E402
+from concord_amd.shapes import SDXL_1X1, SDXL_LINEAR  # noqa: E402
 
 
 def _winner_oracle_params(O, layer):

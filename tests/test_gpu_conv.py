@@ -173,6 +173,54 @@ def test_col2im_matches_fp32_fold(oracle, geom):
     assert np.all(np.abs(g - exact) <= tol), np.max(np.abs(g - exact) - tol)
 
 
+@pytest.mark.parametrize("geom", [  # (B, C, H, W, kh, kw, sh, sw, ph, pw)
+    (1, 3, 20, 18, 15, 15, 1, 1, 7, 7),
+    (2, 2, 13, 16, 14, 14, 2, 2, 6, 6),
+])
+def test_col2im_direct_matches_fp32_fold(oracle, geom):
+    """Windows too large for the staged col2im tile (more than 192 taps)
+    take the unstaged gather (col2im_direct_kernel): the same fixed-order
+    fp32 sum, so the same bound against float64 fold as above."""
+    from concord_amd import _lib as C
+    B, Cin, H, W, kh, kw, sh, sw, ph, pw = geom
+    assert C.lib().concord_conv_col2im_fits(kh, kw, sh, sw) == 0
+    Ho, Wo = (H + 2 * ph - kh) // sh + 1, (W + 2 * pw - kw) // sw + 1
+    dcols = torch.randn(B * Ho * Wo, Cin * kh * kw, device=DEV).to(torch.bfloat16)
+    got = torch.empty((B, Cin, H, W), dtype=torch.bfloat16, device=DEV)
+    C.check(C.lib().concord_conv_col2im(C.ptr(dcols), B, Cin, H, W, kh, kw, sh, sw, ph, pw, C.ptr(got),
+                                        C.stream_of(got.device)), "conv_col2im")
+    sync()
+    u = dcols.double().cpu().reshape(B, Ho * Wo, -1).transpose(1, 2)
+    exact = F.fold(u, (H, W), (kh, kw), padding=(ph, pw), stride=(sh, sw)).numpy()
+    mag = F.fold(u.abs(), (H, W), (kh, kw), padding=(ph, pw), stride=(sh, sw)).numpy()
+    g = oracle.bf16_bits_to_f32(host(got)).astype(np.float64)
+    tol = 2.0 ** -8 * np.abs(exact) + 2.0 ** -20 * mag
+    assert np.all(np.abs(g - exact) <= tol), np.max(np.abs(g - exact) - tol)
+
+
+@pytest.mark.parametrize("case", [(64, 64, 3, 1, 1, 2, 12, 10), (96, 64, 1, 1, 0, 2, 8, 8),
+                                  (8, 16, 3, 1, 1, 1, 9, 7)])
+def test_conv_forward_ignores_fast_gain(case):
+    """The reference's conv forward (concord/packed_b.py:2046-2065) runs on
+    the ungated weight: fast_gain < 1 gates only the linear layer's forward
+    (1762-1772).  On each conv path (implicit, 1 x 1 linear, im2col) a layer
+    with fast_gain 0.25 gives the same output bits as one with 1.0."""
+    import concord_amd as ca
+    cin, cout, k, stride, pad, B, H, W = case
+    torch.manual_seed(sum(case) + 3)
+    W0 = torch.randn(cout, cin, k, k) * 0.05
+    x = torch.randn(B, cin, H, W, device=DEV).to(torch.bfloat16)
+    outs = []
+    for fg in (1.0, 0.25):
+        conv = ca.ConcordConv2dPackedB(cin, cout, k, stride=stride, padding=pad, bias=True, device=DEV)
+        conv.load_weights(W0)
+        conv.fast_gain = fg
+        with torch.no_grad():
+            outs.append(conv(x).float().cpu())
+    sync()
+    assert torch.equal(outs[0], outs[1])
+
+
 # ---------------------------------------------------------------- implicit GEMM
 # (cin, cout, k, stride, pad, B, H, W); channels multiples of 64, so these
 # take the implicit-GEMM path: ragged spatial sizes (positions not a multiple

@@ -382,6 +382,51 @@ def test_rebalance_matches_oracle(oracle, N, K, tickdown):
     assert (opk != packed).any()
 
 
+@pytest.mark.parametrize("tickdown", [False, True])
+def test_rebalance_stats_count_the_calls_ticks(oracle, tickdown):
+    """The rebalance diagnostics (get_reb_stats; the counters of
+    concord/packed_b.py:1161-1179) count the call's decisions: tick-ups and
+    tick-downs are the rows and columns whose exponent the oracle's rebalance
+    moved up or down, and a word clips when its larger int8 magnitude,
+    shifted left by its row's and column's tick-down count, exceeds 127."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(77 + tickdown)
+    N, K = 300, 500
+    sf = rng.integers(-3000, 3000, (N, K))
+    small = rng.random(N) < 0.5
+    ss = np.where(small[:, None], rng.integers(-40, 40, (N, K)), rng.integers(-100, 100, (N, K)))
+    vs = np.where(small[:, None], rng.integers(-40, 40, (N, K)), rng.integers(-100, 100, (N, K)))
+    for r in rng.choice(N, 7, replace=False):
+        c = rng.integers(0, K)
+        ss[r, c], vs[r, c] = 120, 125
+    packed = oracle.pack(sf, ss, vs)
+    re = rng.integers(-6, 8, N).astype(np.int8)
+    ce = rng.integers(-6, 8, K).astype(np.int8)
+    m = ss * 128 + sf + vs * 128
+    rmax = np.abs(m).max(1).astype(np.int32)
+    cmax = np.abs(m).max(0).astype(np.int32)
+    ca.reset_reb_stats()
+    try:
+        pb.rebalance_packed(dev(packed), dev(re), dev(ce), dev(rmax), dev(cmax),
+                            seed_buf=torch.tensor([5], dtype=torch.int32, device=DEV), allow_tickdown=tickdown)
+        sync()
+        st = dict(ca.get_reb_stats())
+    finally:
+        pb._REB_STATS = None
+    ore, oce = re.copy(), ce.copy()
+    oracle.rebalance(packed.copy(), ore, oce, rmax, cmax, seed=5, allow_tickdown=tickdown)
+    dr = ore.astype(int) - re.astype(int)
+    dc = oce.astype(int) - ce.astype(int)
+    assert st["tickup_dim"] == (dr > 0).sum() + (dc > 0).sum() > 0
+    assert st["tickdown_dim"] == (dr < 0).sum() + (dc < 0).sum()
+    assert (st["tickdown_dim"] > 0) == tickdown
+    mag = np.maximum(np.abs(ss), np.abs(vs))
+    lsh = np.maximum(0, -(dr[:, None] + dc[None, :]))
+    assert st["clip_elems"] == ((mag << lsh) > 127).sum()
+    assert (st["calls"], st["dim_total"], st["elem_total"]) == (1, N + K, N * K)
+
+
 def test_rebalance_no_fire_leaves_words(oracle):
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(3)
@@ -1376,6 +1421,87 @@ def test_dgrad_wgrad_vhat_matches_separate_calls(M, N, K):
     for a, b in zip(*outs):
         np.testing.assert_array_equal(a, b)
     assert (outs[0][6] == 0).all() and outs[0][8][0] == 6
+
+
+@pytest.mark.parametrize("N,K", [(320, 192), (5120, 1280)])
+def test_empty_batch_wgrad_entries(oracle, N, K):
+    """M = 0 tokens: the weight gradient is the sum over no tokens, so the
+    wgrad entries write zeros and the v-hat entries run the EMA of that zero
+    gradient (v decays, watermarks zeroed, salt advanced, bias gradient 0).
+    The empty activations may have NULL data pointers.  (At 5120 x 1280 the
+    WGRAD tile rows exceed the operand, the case whose buffer size used to
+    go negative.)"""
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(N + K)
+    packed, re, ce = rand_state(rng, N, K)
+    pk, red, ced = dev(packed), dev(re), dev(ce)
+    dy = torch.empty((0, N), dtype=torch.bfloat16, device=DEV)
+    x = torch.empty((0, K), dtype=torch.bfloat16, device=DEV)
+    gw = pb._wgrad(dy, x)
+    sync()
+    assert (host(gw) == 0).all()
+    vr0 = (rng.random(N) * 1e-3 + 1e-7).astype(np.float32)
+    vc0 = (rng.random(K) * 1e-3 + 1e-7).astype(np.float32)
+    evr, evc = vr0.copy(), vc0.copy()
+    esvi = oracle.vhat_ema(np.zeros((N, K), np.uint16), evr, evc, 0.999)
+    for combined in (False, True):
+        vr, vc = dev(vr0.copy()), dev(vc0.copy())
+        svi = torch.ones(1, device=DEV)
+        rm = torch.full((N,), 77, dtype=torch.int32, device=DEV)
+        cm = torch.full((K,), 88, dtype=torch.int32, device=DEV)
+        salt = torch.full((1,), 5, dtype=torch.int32, device=DEV)
+        if combined:
+            dx, gw, gb = pb._dgrad_wgrad_vhat(dy, x, pk, red, ced, 15, vr, vc, svi, 0.999, rm, cm, salt,
+                                              with_bias=True)
+            assert tuple(dx.shape) == (0, K)
+        else:
+            gw, gb = pb._wgrad_vhat(dy, x, vr, vc, svi, 0.999, rm, cm, salt, with_bias=True)
+        sync()
+        assert (host(gw) == 0).all() and (host(gb) == 0).all()
+        np.testing.assert_array_equal(host(vr), evr)
+        np.testing.assert_array_equal(host(vc), evc)
+        assert host(svi)[0] == esvi
+        assert (host(rm) == 0).all() and (host(cm) == 0).all() and host(salt)[0] == 6
+
+
+def test_empty_batch_conv_wgrad_entries(oracle):
+    """B = 0 images through the implicit conv's weight-gradient entries: a
+    zero tap-major and packed-order gradient, and the v-hat EMA of zeros."""
+    from concord_amd import _lib as C
+    from concord_amd import packed_b as pb
+    geom = (0, 64, 16, 16, 320, 3, 3, 1, 1, 1, 1)
+    B, Cin, H, W, Cout, kh, kw, sh, sw, ph, pw = geom
+    K = Cin * kh * kw
+    st = C.stream_of(DEV)
+    gt = torch.full((Cout, K), 0x1234, dtype=torch.int16, device=DEV).view(torch.bfloat16)
+    ws = torch.zeros(int(C.lib().concord_conv_workspace_bytes(*geom)) + 4096, dtype=torch.uint8, device=DEV)
+    C.check(C.lib().concord_conv_wgrad(None, None, C.ptr(gt), *geom, C.ptr(ws), ws.numel(), st), "conv_wgrad")
+    sync()
+    assert (host(gt) == 0).all()
+    rng = np.random.default_rng(3)
+    vr0 = (rng.random(Cout) * 1e-3 + 1e-7).astype(np.float32)
+    vc0 = (rng.random(K) * 1e-3 + 1e-7).astype(np.float32)
+    evr, evc = vr0.copy(), vc0.copy()
+    esvi = oracle.vhat_ema(np.zeros((Cout, K), np.uint16), evr, evc, 0.999)
+    gt.view(torch.int16).fill_(0x1234)
+    gw = torch.full((Cout, K), 0x4321, dtype=torch.int16, device=DEV).view(torch.bfloat16)
+    gb = torch.full((Cout,), 0x1111, dtype=torch.int16, device=DEV).view(torch.bfloat16)
+    vr, vc = dev(vr0.copy()), dev(vc0.copy())
+    svi = torch.ones(1, device=DEV)
+    rm = torch.full((Cout,), 7, dtype=torch.int32, device=DEV)
+    cm = torch.full((K,), 8, dtype=torch.int32, device=DEV)
+    salt = torch.full((1,), 11, dtype=torch.int32, device=DEV)
+    wsu = pb._workspace(DEV, Cout, K, 0)
+    C.check(C.lib().concord_conv_wgrad_vhat(
+        None, None, C.ptr(gt), C.ptr(gw), gw.stride(0), *geom, 0.999, C.ptr(vr), C.ptr(vc), C.ptr(svi),
+        C.ptr(rm), C.ptr(cm), C.ptr(salt), C.ptr(gb), C.ptr(wsu), wsu.numel(), C.ptr(ws), ws.numel(), st),
+        "conv_wgrad_vhat")
+    sync()
+    assert (host(gt) == 0).all() and (host(gw) == 0).all() and (host(gb) == 0).all()
+    np.testing.assert_array_equal(host(vr), evr)
+    np.testing.assert_array_equal(host(vc), evc)
+    assert host(svi)[0] == esvi
+    assert (host(rm) == 0).all() and (host(cm) == 0).all() and host(salt)[0] == 12
 
 
 # ---------------------------------------------------------------- gradient noise

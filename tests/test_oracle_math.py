@@ -542,7 +542,8 @@ def _ns5_bf16_numpy(oracle, G, gamma):
         return oracle.bf16_bits_to_f32(oracle.f32_to_bf16_bits_array(np.asarray(x, np.float32))).astype(np.float64)
     a, b, c = np.float32(3.4445), np.float32(-4.7750), np.float32(2.0315)
     norm = np.float32(np.sqrt(np.float32((G * G).sum())))
-    den = np.float32(max(norm, np.float32(1e-12)) * np.float32(1.0 + 1e-7))
+    n = max(norm, np.float32(1e-12))
+    den = np.float32(n * np.float32(np.float32(norm / n) + np.float32(1e-7)))
     X = rb(G.astype(np.float32) / den)
     tr = X.shape[0] > X.shape[1]
     if tr:
@@ -593,6 +594,31 @@ def test_ns5_small_norm_input_is_normalised(oracle):
     ref = gamma * _ns5_float64(gd)
     assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 4e-2
     # and it is the same drive as for the same direction at unit scale
+    g1 = oracle.f32_to_bf16_bits_array((gd / np.linalg.norm(gd)).astype(np.float32))
+    one = oracle.bf16_bits_to_f32(oracle.muon_ns5(g1, gamma)).astype(np.float64)
+    assert np.linalg.norm(got - one) / np.linalg.norm(one) < 2e-2
+
+
+def test_ns5_norm_below_clamp_is_renormalised(oracle):
+    """Below the drive's clamp (||g|| < 1e-12) g / 1e-12 has norm < 1, and
+    ns5's own division by (that norm + 1e-7) brings it back to unit norm
+    (exp9_muon.py:75, 47).  A single denominator max(||g||, 1e-12) * (1 +
+    1e-7) would feed NS5 a matrix of norm ~0.01 here, whose five iterations
+    stay far from the quintic's band; the float64 two-step reference and the
+    unit-scale drive of the same direction both catch that."""
+    rng = np.random.default_rng(37)
+    N, K = 64, 192
+    g = rng.standard_normal((N, K))
+    g *= 1e-14 / np.linalg.norm(g)
+    gb = oracle.f32_to_bf16_bits_array(g.astype(np.float32))
+    gd = oracle.bf16_bits_to_f32(gb).astype(np.float64)
+    assert 0.9e-14 < np.linalg.norm(gd) < 1.1e-14
+    gamma = np.float32(np.sqrt(np.float32(K)))
+    got = oracle.bf16_bits_to_f32(oracle.muon_ns5(gb, gamma)).astype(np.float64)
+    ref = gamma * _ns5_float64(gd)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 4e-2
+    em = _ns5_bf16_numpy(oracle, gd, gamma)
+    assert np.linalg.norm(got - em) / np.linalg.norm(em) < 1.5e-2
     g1 = oracle.f32_to_bf16_bits_array((gd / np.linalg.norm(gd)).astype(np.float32))
     one = oracle.bf16_bits_to_f32(oracle.muon_ns5(g1, gamma)).astype(np.float64)
     assert np.linalg.norm(got - one) / np.linalg.norm(one) < 2e-2
