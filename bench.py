@@ -462,6 +462,10 @@ def _only(which, reps, layer, xb, dy, torch, pb):
         fn = lambda: pb._dgrad_wgrad_vhat(dy, xb, *st, 15, layer.v_row, layer.v_col,  # noqa: E731
                                           layer._sum_v_inv, 0.999, layer._row_max_buf, layer._col_max_buf,
                                           None, with_bias=True)
+    elif which == "ns5":
+        g5 = (torch.randn(N_OUT, K_IN, device=dev) * 1e-3).to(torch.bfloat16)
+        o5 = torch.empty_like(g5)
+        fn = lambda: pb.muon_ns5(g5, out=o5)  # noqa: E731
     elif which == "wgrad_vhat":
         fn = lambda: pb._wgrad_vhat(dy, xb, layer.v_row, layer.v_col, layer._sum_v_inv, 0.999,  # noqa: E731
                                     layer._row_max_buf, layer._col_max_buf, None, with_bias=True)
@@ -539,7 +543,7 @@ def main():
                     help="skip the config-4 row (the graph-captured step over all 754 SDXL weights)")
     ap.add_argument("--only", default=None,
                     choices=["fwd", "bwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
-                             "copy", "config3"],
+                             "copy", "ns5", "config3"],
                     help="time one entry alone; config3 times only the step on each config-3 SDXL shape")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--graph-steps", type=int, default=5,

@@ -70,6 +70,10 @@ struct GemmArgs {
   int64_t ldy;
   float as, at;
   ConvIdx cv;             // implicit-GEMM convolution kernels only
+  // symmetric product (FWD / DGRAD kernels, I == J): the count of tiles that
+  // meet the upper triangle j >= i, which alone are computed (sym_tile); the
+  // split-K slots are indexed in that order.  0: the full tile grid.
+  int sym;
 };
 
 // s * y + t * x as the Newton-Schulz combination steps take it (x is the
@@ -123,6 +127,50 @@ CONCORD_DEV void split_tile_of(int w, int ti, int tj, int splits, int& split, in
   grouped_tile(lin % tiles, ti, tj, bi, bj);
 }
 
+// Symmetric products: tile row bi (rows [bi BI, bi BI + BI)) meets the upper
+// triangle j >= i in the tile columns bj >= sym_lo(bi) = floor(bi BI / BJ),
+// the first whose columns reach past the row block's first row.  Every
+// element (i, j) with j >= i lies in such a tile.
+__host__ __device__ inline int sym_lo(int bi, int BI, int BJ) { return (int)(((int64_t)bi * BI) / BJ); }
+__host__ __device__ inline int sym_tile_count(int ti, int tj, int BI, int BJ) {
+  int n = 0;
+  for (int bi = 0; bi < ti; ++bi) {
+    const int lo = sym_lo(bi, BI, BJ);
+    n += lo < tj ? tj - lo : 0;
+  }
+  return n;
+}
+// the t-th tile of that set, rows ascending and columns ascending in a row
+CONCORD_DEV void sym_tile(int t, int ti, int tj, int BI, int BJ, int& bi, int& bj) {
+  bi = 0;
+  bj = 0;
+  for (int r = 0; r < ti; ++r) {
+    const int lo = min(tj, sym_lo(r, BI, BJ));
+    if (t < tj - lo) {
+      bi = r;
+      bj = lo + t;
+      return;
+    }
+    t -= tj - lo;
+  }
+}
+// tile (bi, bj), split and split-K slot of workgroup w of a FWD / DGRAD
+// launch: split_tile_of over the full grid (slot bi * tiles_j + bj), or for
+// a symmetric product the same XCD-contiguous split-major order over the
+// g.sym tiles of the upper triangle (slot = the tile's index among them)
+template <int BI, int BJ>
+CONCORD_DEV void gemm_tile_of(const GemmArgs& g, int w, int& split, int& bi, int& bj, int& slot) {
+  if (g.sym) {
+    const int lin = xcd_linear(w, g.sym * g.splits);
+    split = lin / g.sym;
+    slot = lin % g.sym;
+    sym_tile(slot, g.tiles_i, g.tiles_j, BI, BJ, bi, bj);
+  } else {
+    split_tile_of(w, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
+    slot = bi * g.tiles_j + bj;
+  }
+}
+
 // launch a fast-path kernel when the operands satisfy its alignment rules;
 // returns CONCORD_OK, an error code, or -1 when the generic kernel must run
 int gemm_fast_launch(int mode, const GemmArgs& g, void* workspace, size_t ws_bytes,
@@ -156,6 +204,18 @@ int64_t gemm_wgrad_vhat_tiles_j(int64_t J);
 int gemm_bf16_combine(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
                       int64_t ldc, int64_t I, int64_t J, int64_t R, const uint16_t* y, int64_t ldy, float s,
                       float t, void* ws, size_t ws_bytes, hipStream_t st, const char* what);
+// a symmetric bf16 product C[I][I] (MODE_FWD_BF16: a b^T with b = a; or
+// MODE_DGRAD_BF16: a b of two commuting symmetric matrices, e.g. b = a),
+// optionally combined as gemm_bf16_combine does (y symmetric too, or NULL):
+// only the tiles meeting the upper triangle are computed, and each of their
+// elements (i, j) with i <= j is stored at (i, j) and (j, i) by the epilogue
+// or the split-K reduction.  -1 when the operands do not take the fast
+// kernels.
+int gemm_bf16_sym(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
+                  int64_t ldc, int64_t I, int64_t R, const uint16_t* y, int64_t ldy, float s, float t, void* ws,
+                  size_t ws_bytes, hipStream_t st, const char* what);
+// split-K workspace bytes (counters + partials) gemm_bf16_sym may use
+size_t gemm_sym_splitk_need(int mode, int64_t I, int64_t R);
 // a plain bf16 product through the fast or generic kernels: MODE_FWD_BF16
 // (C[I][J] = sum_r a[i][r] b[j][r]) or MODE_DGRAD_BF16 (sum_r a[i][r] b[r][j])
 int gemm_bf16_run(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,

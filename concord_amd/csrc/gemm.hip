@@ -692,3 +692,27 @@ extern "C" int concord_gemm_bf16_dgrad(const uint16_t* dy, int64_t ld_dy, const 
   GemmArgs g = make_args(dy, w, ld_dy, ld_w, nullptr, nullptr, 0, nullptr, dx, ld_dx, M, K, N, false);
   return launch_gemm<MODE_DGRAD_BF16>(g, workspace, workspace_bytes, (hipStream_t)stream, "gemm_bf16_dgrad");
 }
+
+extern "C" size_t concord_gemm_sym_workspace_bytes(int64_t M, int64_t R, int b_rows) {
+  if (M < 1) M = 1;
+  if (R < 1) R = 1;
+  return gemm_sym_splitk_need(b_rows ? MODE_FWD_BF16 : MODE_DGRAD_BF16, M, R);
+}
+
+extern "C" int concord_gemm_bf16_sym(const uint16_t* a, int64_t ld_a, const uint16_t* b, int64_t ld_b, int b_rows,
+                                     uint16_t* c, int64_t ld_c, int64_t M, int64_t R, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
+  CONCORD_CHECK(sizes_ok(M, M, R), "concord_gemm_bf16_sym: bad size");
+  CONCORD_CHECK(b_rows || R == M, "concord_gemm_bf16_sym: a b of symmetric matrices needs R == M");
+  if (M == 0) return CONCORD_OK;
+  CONCORD_CHECK(a && b && c, "concord_gemm_bf16_sym: NULL argument");
+  CONCORD_CHECK(ld_a >= R && ld_b >= (b_rows ? R : M) && ld_c >= M, "concord_gemm_bf16_sym: bad leading dimension");
+  const int mode = b_rows ? MODE_FWD_BF16 : MODE_DGRAD_BF16;
+  CONCORD_CHECK(workspace_bytes >= gemm_sym_splitk_need(mode, M, R) || !workspace,
+                "concord_gemm_bf16_sym: workspace of %zu bytes needed", gemm_sym_splitk_need(mode, M, R));
+  const int rc = gemm_bf16_sym(mode, a, ld_a, b, ld_b, c, ld_c, M, R, nullptr, 0, 0.0f, 0.0f, workspace,
+                               workspace_bytes, (hipStream_t)stream, "gemm_bf16_sym");
+  CONCORD_CHECK(rc != -1, "concord_gemm_bf16_sym: operands not aligned for the fast kernels (16-byte bases, "
+                          "leading dimensions and M multiples of 8)");
+  return rc;
+}

@@ -497,7 +497,21 @@ CONCORD_DEV void epilogue(const GemmArgs& g, f32x4 (&acc)[NI][NJ], int64_t i0, i
   // row-contiguous stores: 8 bf16 (16 bytes) per thread when the output
   // allows, else 4 (J % 4 == 0, ldc % 4 == 0, 8-byte aligned base)
   const bool v16 = (g.ldc % 8 == 0) && (g.J % 8 == 0) && (((uintptr_t)g.c % 16) == 0);
-  if (v16) {
+  if (g.sym) {
+    // symmetric product: each element (i, j) with i <= j goes to (i, j) and
+    // (j, i); the tile's elements below the diagonal are left to the tile
+    // holding their mirror image (every element is written once)
+    for (int c = t; c < BI * BJ; c += nthreads) {
+      const int rl = c % BI, cl = c / BI;   // consecutive threads: consecutive i, so (j, i) stores coalesce
+      const int64_t i = i0 + rl, j = j0 + cl;
+      if (i <= j && j < g.J) {
+        uint32_t o = stage[rl * LDO + cl];
+        if (g.ay) o = combine_bf16x2(g.ay[i * g.ldy + j], o, g.as, g.at) & 0xFFFFu;
+        g.c[i * g.ldc + j] = (uint16_t)o;
+        g.c[j * g.ldc + i] = (uint16_t)o;
+      }
+    }
+  } else if (v16) {
     constexpr int CPR = BJ / 8;
     for (int c = t; c < BI * CPR; c += nthreads) {
       const int rl = c / CPR, cl = (c % CPR) * 8;
@@ -534,7 +548,8 @@ CONCORD_DEV void epilogue(const GemmArgs& g, f32x4 (&acc)[NI][NJ], int64_t i0, i
 // and bias, and stores 4 bf16.
 template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ>
 CONCORD_DEV int64_t splitk_reduce_items(const GemmArgs& g) {
-  return (int64_t)g.tiles_i * g.tiles_j * WI * WJ * NI * NJ * 64;
+  const int64_t tiles = g.sym ? g.sym : (int64_t)g.tiles_i * g.tiles_j;
+  return tiles * WI * WJ * NI * NJ * 64;
 }
 
 template <int MODE, int NI, int NJ, int BI, int BJ, int WI, int WJ, int SP>
@@ -545,8 +560,9 @@ CONCORD_DEV void splitk_reduce_item_sp(const GemmArgs& g, int64_t idx) {
   const int y = (int)(r % NJ); r /= NJ;
   const int x = (int)(r % NI); r /= NI;
   const int aw = (int)(r % NAW);
-  const int tile = (int)(r / NAW);   // row-major tile index
-  const int bi = tile / g.tiles_j, bj = tile % g.tiles_j;
+  const int tile = (int)(r / NAW);   // the split-K slot: row-major tile index, or the symmetric set's index
+  int bi = tile / g.tiles_j, bj = tile % g.tiles_j;
+  if (g.sym) sym_tile(tile, g.tiles_i, g.tiles_j, BI, BJ, bi, bj);
   const int64_t i = (int64_t)bi * BI + (aw / WJ) * WTI + x * 16 + (lane & 15);
   const int64_t j = (int64_t)bj * BJ + (aw % WJ) * WTJ + y * 16 + 4 * (lane >> 4);
   if (i >= g.I || j >= g.J) return;
@@ -582,6 +598,22 @@ CONCORD_DEV void splitk_reduce_item_sp(const GemmArgs& g, int64_t idx) {
   if (g.ay) {
     const uint2 yv = *reinterpret_cast<const uint2*>(g.ay + i * g.ldy + j);
     o = make_uint2(combine_bf16x2(yv.x, o.x, g.as, g.at), combine_bf16x2(yv.y, o.y, g.as, g.at));
+  }
+  if (g.sym) {
+    // symmetric product: (i, j + e) with i <= j + e goes to both positions
+    // (as the epilogue's sym branch); elements below the diagonal are skipped
+    if (i > j + 3) return;
+    if (i <= j) *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = o;
+    const uint16_t h[4] = {(uint16_t)(o.x & 0xFFFFu), (uint16_t)(o.x >> 16), (uint16_t)(o.y & 0xFFFFu),
+                           (uint16_t)(o.y >> 16)};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if (i <= j + e) {
+        if (i > j) g.c[i * g.ldc + j + e] = h[e];
+        g.c[(j + e) * g.ldc + i] = h[e];
+      }
+    }
+    return;
   }
   *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = o;
 }
@@ -760,8 +792,8 @@ __global__ __launch_bounds__(64 * WI * WJ, MINB) void gemm_fast_kernel(GemmArgs 
   const int lane = t & 63, wave = t >> 6;
   const int wi = wave / WJ, wj = wave % WJ;
   const int wg = blockIdx.x;
-  int split, bi, bj;
-  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
+  int split, bi, bj, slot;
+  gemm_tile_of<BI, BJ>(g, wg, split, bi, bj, slot);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -860,7 +892,7 @@ __global__ __launch_bounds__(64 * WI * WJ, MINB) void gemm_fast_kernel(GemmArgs 
   }
 
   static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
-  epilogue<MODE, NI, NJ, BI, BJ, WI * WJ>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, wave, t, NT,
+  epilogue<MODE, NI, NJ, BI, BJ, WI * WJ>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, slot, wave, t, NT,
                                            &lds_a[0][0]);
 }
 
@@ -1211,8 +1243,8 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
   const int lane = t & 63, wave = t >> 6;
   const bool producer = wave >= 4;
   const int wg = blockIdx.x;
-  int split, bi, bj;
-  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
+  int split, bi, bj, slot;
+  gemm_tile_of<BI, BJ>(g, wg, split, bi, bj, slot);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -1295,7 +1327,7 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
   }
 
   static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
-  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, producer ? -1 : wave,
+  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, slot, producer ? -1 : wave,
                                      t, 512, &lds_a[0][0]);
 }
 
@@ -1747,8 +1779,8 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
   const int lane = t & 63, wave = t >> 6;
   const bool producer = wave >= 4;
   const int wg = blockIdx.x;
-  int split, bi, bj;
-  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
+  int split, bi, bj, slot;
+  gemm_tile_of<BI, BJ>(g, wg, split, bi, bj, slot);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -1826,7 +1858,7 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
   }
 
   static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
-  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, producer ? -1 : wave,
+  epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, slot, producer ? -1 : wave,
                                      t, 512, &lds_a[0][0]);
 }
 
@@ -1855,29 +1887,34 @@ struct FastPlan { int shape, splits, ti, tj; int64_t r_split; };
 
 // room = bytes available for split-K partials (each split of each tile
 // takes a full BI x BJ fp32 slot)
+// sym: a symmetric product (I == J) computing only the tiles that meet the
+// upper triangle (sym_tile_count of them; gemm_tile_of)
 template <int NS>
-static FastPlan plan(const FastShape (&shapes)[NS], int64_t I, int64_t J, int64_t R, size_t room) {
+static FastPlan plan(const FastShape (&shapes)[NS], int64_t I, int64_t J, int64_t R, size_t room,
+                     bool sym = false) {
   FastPlan best{0, 1, 0, 0, R};
   double best_cost = 1e300;
   for (int s = 0; s < NS; ++s) {
     const int64_t ti = cdiv(I, shapes[s].bi), tj = cdiv(J, shapes[s].bj);
-    const size_t slot = (size_t)ti * tj * shapes[s].bi * shapes[s].bj * sizeof(float);
+    const int64_t tiles = sym ? sym_tile_count((int)ti, (int)tj, shapes[s].bi, shapes[s].bj) : ti * tj;
+    const size_t slot = (size_t)tiles * shapes[s].bi * shapes[s].bj * sizeof(float);
     const int max_splits = (int)std::min<size_t>(kMaxSplits, std::max<size_t>(1, room / slot));
     for (int sp = 1; sp <= max_splits; ++sp) {
       // split only a grid that leaves CUs idle (then up to kMaxSplits, the
       // cost below deciding); a grid that fills the chip stays unsplit
-      if (sp > 1 && (!gemm_splitk_fits(ti * tj) || ti * tj >= kCUs * shapes[s].minb)) break;
+      if (sp > 1 && (!gemm_splitk_fits(tiles) || tiles >= kCUs * shapes[s].minb)) break;
       const int64_t rs = cdiv(cdiv(R, sp), TR) * TR;
       if (sp > 1 && (sp - 1) * rs >= R) break;
       const double slots = (double)kCUs * shapes[s].minb;
-      const double waves = std::ceil((double)(ti * tj * sp) / slots);
+      const double waves = std::ceil((double)(tiles * sp) / slots);
       // a resident block's MFMA rate falls when two share a CU
       const double per_block = (double)shapes[s].bi * shapes[s].bj * (double)(rs + 2 * TR) * shapes[s].minb;
       double cost = waves * per_block * shapes[s].weight;
-      // split-K partials: each split writes I x J fp32 and the reduction reads
-      // them back, 8 B per element and split at ~5 TB/s, in the units of
-      // per_block (~0.73 ps per unit for an 8-wave tile at full occupancy)
-      if (sp > 1) cost += (double)sp * I * J * 2.2;
+      // split-K partials: each split writes I x J fp32 (the computed tiles'
+      // share of it when symmetric) and the reduction reads them back, 8 B
+      // per element and split at ~5 TB/s, in the units of per_block (~0.73 ps
+      // per unit for an 8-wave tile at full occupancy)
+      if (sp > 1) cost += sym ? (double)sp * tiles * shapes[s].bi * shapes[s].bj * 2.2 : (double)sp * I * J * 2.2;
       if (cost < best_cost * 0.999) {
         best_cost = cost;
         best = FastPlan{s, sp, (int)ti, (int)tj, rs};
@@ -1930,7 +1967,7 @@ template <int MODE, int BI, int BJ, int WI, int WJ>
 static void launch_reduce(const GemmArgs& g, hipStream_t st) {
   if (g.splits <= 1) return;
   constexpr int NI = BI / WI / 16, NJ = BJ / WJ / 16;
-  int64_t threads = (int64_t)g.tiles_i * g.tiles_j * WI * WJ * NI * NJ * 64;
+  int64_t threads = (g.sym ? (int64_t)g.sym : (int64_t)g.tiles_i * g.tiles_j) * WI * WJ * NI * NJ * 64;
   if (MODE == MODE_WGRAD && g.bpart) threads += (int64_t)g.tiles_j * g.I;   // the bias fold
   hipLaunchKernelGGL((splitk_reduce_kernel<MODE, NI, NJ, BI, BJ, WI, WJ>), dim3((unsigned)cdiv(threads, 256)),
                      dim3(256), 0, st, g);
@@ -1968,10 +2005,10 @@ static void launch(const GemmArgs& g, int blocks, hipStream_t st) {
   launch_reduce<MODE, BI, BJ, WI, WJ>(g, st);
 }
 
-static FastPlan plan_mode(int mode, int64_t I, int64_t J, int64_t R, size_t room) {
-  if (mode == MODE_FWD || mode == MODE_FWD_BF16) return plan(kFwdShapes, I, J, R, room);
+static FastPlan plan_mode(int mode, int64_t I, int64_t J, int64_t R, size_t room, bool sym = false) {
+  if (mode == MODE_FWD || mode == MODE_FWD_BF16) return plan(kFwdShapes, I, J, R, room, sym);
   if (mode == MODE_WGRAD) return plan(kWgrShapes, I, J, R, room);
-  return plan(kColShapes, I, J, R, room);
+  return plan(kColShapes, I, J, R, room, sym);
 }
 
 static const FastShape& shape_of(int mode, int idx) {
@@ -2141,19 +2178,23 @@ int gemm_conv_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
   return launch_status(what);
 }
 
-int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_bytes,
-                     hipStream_t st, const char* what) {
+// sym: the symmetric tile set (FWD / DGRAD modes; the epilogue or the
+// split-K reduction also stores each upper element's mirror image)
+static int fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_bytes, hipStream_t st,
+                       const char* what, bool sym) {
   if (!eligible(mode, g0)) return -1;
   GemmArgs g = g0;
   // split-K needs room for its partials behind the counters
   const size_t room = (workspace && ws_bytes > kSplitkCounterBytes) ? ws_bytes - kSplitkCounterBytes : 0;
-  const FastPlan p = plan_mode(mode, g.I, g.J, g.R, room);
+  const FastPlan p = plan_mode(mode, g.I, g.J, g.R, room, sym);
   g.splits = p.splits;
   g.r_split = p.r_split;
   g.tiles_i = p.ti;
   g.tiles_j = p.tj;
+  const FastShape& sh = shape_of(mode, p.shape);
+  g.sym = sym ? sym_tile_count(p.ti, p.tj, sh.bi, sh.bj) : 0;
   if (p.splits > 1) g.part = (float*)((char*)workspace + kSplitkCounterBytes);
-  const int blocks = p.ti * p.tj * p.splits;
+  const int blocks = (sym ? g.sym : p.ti * p.tj) * p.splits;
   switch (mode) {
     case MODE_FWD:
       if (p.shape == 0) launch_dma<MODE_FWD, 256, 160>(g, blocks, st);
@@ -2189,6 +2230,45 @@ int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
       return -1;
   }
   return launch_status(what);
+}
+
+int gemm_fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_bytes,
+                     hipStream_t st, const char* what) {
+  return fast_launch(mode, g0, workspace, ws_bytes, st, what, false);
+}
+
+
+int gemm_bf16_sym(int mode, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c,
+                  int64_t ldc, int64_t I, int64_t R, const uint16_t* y, int64_t ldy, float s, float t, void* ws,
+                  size_t ws_bytes, hipStream_t st, const char* what) {
+  if (mode != MODE_FWD_BF16 && mode != MODE_DGRAD_BF16) return -1;
+  if (I == 0) return CONCORD_OK;
+  GemmArgs g{};
+  g.a = a;
+  g.b = b;
+  g.lda = lda;
+  g.ldb = ldb;
+  g.c = c;
+  g.ldc = ldc;
+  g.I = I;
+  g.J = I;
+  g.R = R;
+  g.ay = y;
+  g.ldy = ldy;
+  g.as = s;
+  g.at = t;
+  return fast_launch(mode, g, ws, ws_bytes, st, what, true);
+}
+
+size_t gemm_sym_splitk_need(int mode, int64_t I, int64_t R) {
+  if (I <= 0) return kSplitkCounterBytes;
+  const FastPlan p = plan_mode(mode, I, I, R, (size_t)-1 / 2, true);
+  size_t part = 0;
+  if (p.splits > 1) {
+    const FastShape& sh = shape_of(mode, p.shape);
+    part = (size_t)sym_tile_count(p.ti, p.tj, sh.bi, sh.bj) * sh.bi * sh.bj * sizeof(float) * p.splits;
+  }
+  return kSplitkCounterBytes + ((part + 255) / 256) * 256;
 }
 
 }  // namespace concord

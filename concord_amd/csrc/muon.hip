@@ -8,12 +8,15 @@
 //   ||g||^2  blocks of 8192 elements of the row-major flattening; lane t of a
 //            block sums elements t, t + 256, ... ascending, then the halving
 //            tree over 256 lanes; block totals ascending.  norm = sqrt (RN).
-//   X0 = bf16(g / (max(norm, 1e-12) * fl(1 + 1e-7))), transposed when N > K
-//   (X is m x n, m <= n)
+//   X0 = bf16(g / (n (norm / n + 1e-7))), n = max(norm, 1e-12), transposed
+//   when N > K (X is m x n, m <= n)
 //   5 x:  A = bf16(X X^T); AA = bf16(A A); B = bf16(b A + c AA);
 //         BX = bf16(B X); X = bf16(a X + BX)      (products: bf16 MFMA, fp32 acc)
 //   out = bf16(gamma X), transposed back.
-// The three products run on the library's bf16 GEMM kernels.  The two
+// The three products run on the library's bf16 GEMM kernels; the symmetric
+// two (X X^T, and A A with B's combination) compute only the tiles that meet
+// the upper triangle and store each upper element at its mirror position too
+// (gemm_bf16_sym).  The two
 // combinations ride in the epilogue of the product they follow (A A -> B,
 // B X -> the new X; gemm_bf16_combine), which writes into a second buffer:
 // B goes to the AA buffer and X ping-pongs between two buffers.  Operands the
@@ -33,15 +36,32 @@ constexpr int kFrobBlock = 8192;
 __global__ __launch_bounds__(256) void frob_partials_kernel(const uint16_t* __restrict__ g, int64_t ld,
                                                             int64_t N, int64_t K, float* __restrict__ part) {
   __shared__ float s[256];
+  __shared__ __align__(16) uint16_t tile[kFrobBlock];
   const int64_t total = N * K;
   const int64_t b0 = (int64_t)blockIdx.x * kFrobBlock;
   float acc = 0.0f;
+  if (ld == K && b0 + kFrobBlock <= total && ((uintptr_t)g % 16) == 0) {
+    // a whole contiguous block: 16-byte loads into LDS, then each lane chains
+    // its elements t, t + 256, ... from there in the same order
+#pragma unroll
+    for (int q = 0; q < kFrobBlock / 2048; ++q) {
+      const int o = 2048 * q + 8 * threadIdx.x;
+      *reinterpret_cast<uint4*>(tile + o) = *reinterpret_cast<const uint4*>(g + b0 + o);
+    }
+    __syncthreads();
 #pragma unroll 8
-  for (int i = 0; i < kFrobBlock / 256; ++i) {
-    const int64_t e = b0 + threadIdx.x + 256 * i;
-    float v = 0.0f;
-    if (e < total) v = bf16_to_f32(ld == K ? g[e] : g[(e / K) * ld + e % K]);
-    acc = __fadd_rn(acc, __fmul_rn(v, v));
+    for (int i = 0; i < kFrobBlock / 256; ++i) {
+      const float v = bf16_to_f32(tile[threadIdx.x + 256 * i]);
+      acc = __fadd_rn(acc, __fmul_rn(v, v));
+    }
+  } else {
+#pragma unroll 8
+    for (int i = 0; i < kFrobBlock / 256; ++i) {
+      const int64_t e = b0 + threadIdx.x + 256 * i;
+      float v = 0.0f;
+      if (e < total) v = bf16_to_f32(ld == K ? g[e] : g[(e / K) * ld + e % K]);
+      acc = __fadd_rn(acc, __fmul_rn(v, v));
+    }
   }
   s[threadIdx.x] = acc;
   __syncthreads();
@@ -52,34 +72,14 @@ __global__ __launch_bounds__(256) void frob_partials_kernel(const uint16_t* __re
   if (threadIdx.x == 0) part[blockIdx.x] = s[0];
 }
 
-// den = max(sqrt(sum of the block partials ascending), 1e-12) * fl(1 + 1e-7):
-// the drive normalises g by max(||g||, 1e-12) and ns5 then divides the unit
-// matrix by (its norm + 1e-7) (exp9_muon.py:75, 82, 47), one fp32 product
-// here.  One wave: 16 x 64
-// partials are loaded at a time, then chained in ascending order by reading
-// one lane after another (every lane carries the same running sum).
+// den = n (||g|| / n + 1e-7), n = max(||g||, 1e-12), ||g|| = sqrt of the
+// block partials summed in ascending order: the drive normalises g by
+// max(||g||, 1e-12) and ns5 then divides by (the result's norm + 1e-7)
+// (exp9_muon.py:75, 82, 47).  One wave; wave_chain stages the partials in
+// LDS and chains them in index order.
 __global__ __launch_bounds__(64) void frob_den_kernel(const float* __restrict__ part, int64_t nb, float* den) {
-  constexpr int B = 16;
   const int lane = threadIdx.x;
-  float s = 0.0f;
-  for (int64_t c0 = 0; c0 < nb; c0 += 64 * B) {
-    float v[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const int64_t i = c0 + 64 * b + lane;
-      v[b] = i < nb ? part[i] : 0.0f;
-    }
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const int64_t cnt = min((int64_t)64, nb - (c0 + 64 * b));
-      if (cnt == 64) {
-#pragma unroll
-        for (int j = 0; j < 64; ++j) s = __fadd_rn(s, lane_value(v[b], j));
-      } else {
-        for (int j = 0; j < cnt; ++j) s = __fadd_rn(s, lane_value(v[b], j));
-      }
-    }
-  }
+  const float s = wave_chain(part, nb, 1);
   // the drive's g / max(||g||, 1e-12), then ns5's / (||that|| + 1e-7), as
   // one denominator n (||g|| / n + 1e-7): for ||g|| >= 1e-12 the quotient is
   // exactly 1 and the sum fl(1 + 1e-7); below, ||g|| / n < 1 and the input
@@ -127,6 +127,82 @@ __global__ __launch_bounds__(256) void ns5_copy_kernel(const uint16_t* __restric
   }
 }
 
+// ns5_copy_kernel with 16-byte accesses (bases 16-byte aligned, leading
+// dimensions multiples of 8): a thread moves 8 consecutive elements; chunks
+// crossing the matrix edge take 2-byte accesses.  The transpose goes through
+// a bf16 LDS tile whose 16-byte chunk q of row r sits at chunk q ^ swz(r),
+// so that both the chunk writes and the column reads spread over the banks.
+CONCORD_DEV int ns5_swz(int r) { return (r & 7) ^ ((r >> 3) & 7); }
+template <bool TRANS, bool DIV>
+__global__ __launch_bounds__(256) void ns5_copy_vec_kernel(const uint16_t* __restrict__ src, int64_t lds,
+                                                           uint16_t* __restrict__ dst, int64_t ldd, int64_t R,
+                                                           int64_t C, const float* den, float gamma) {
+  __shared__ __align__(16) uint16_t t[64 * 64];
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;   // destination tile
+  const float d = DIV ? *den : gamma;
+  const int cq = threadIdx.x & 7, rr = threadIdx.x >> 3;
+  auto op = [&](float v) { return DIV ? __fdiv_rn(v, d) : __fmul_rn(d, v); };
+  auto store8 = [&](int64_t r, int64_t c, const float (&v)[8]) {
+    if (c + 8 <= C) {
+      *reinterpret_cast<uint4*>(dst + r * ldd + c) =
+          make_uint4(pack_bf16x2(op(v[0]), op(v[1])), pack_bf16x2(op(v[2]), op(v[3])),
+                     pack_bf16x2(op(v[4]), op(v[5])), pack_bf16x2(op(v[6]), op(v[7])));
+    } else {
+      for (int e = 0; e < 8 && c + e < C; ++e) dst[r * ldd + c + e] = (uint16_t)(pack_bf16x2(op(v[e]), 0.0f) & 0xFFFFu);
+    }
+  };
+  if (!TRANS) {
+    for (int h = 0; h < 2; ++h) {
+      const int64_t r = r0 + rr + 32 * h, c = c0 + 8 * cq;
+      if (r >= R || c >= C) continue;
+      float v[8];
+      if (c + 8 <= C) {
+        const uint4 w = *reinterpret_cast<const uint4*>(src + r * lds + c);
+        const uint32_t q[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[2 * e] = __uint_as_float(q[e] << 16);
+          v[2 * e + 1] = __uint_as_float(q[e] & 0xFFFF0000u);
+        }
+      } else {
+        for (int e = 0; e < 8; ++e) v[e] = c + e < C ? bf16_to_f32(src[r * lds + c + e]) : 0.0f;
+      }
+      store8(r, c, v);
+    }
+    return;
+  }
+  // dst[r][c] = op(src[c][r]): the source tile is rows c0 .. c0 + 63 (< C)
+  // and columns r0 .. r0 + 63 (< R) of the C x R source
+  for (int h = 0; h < 2; ++h) {
+    const int sr = rr + 32 * h;
+    const int64_t gr = c0 + sr, gc = r0 + 8 * cq;
+    uint4 w = make_uint4(0u, 0u, 0u, 0u);
+    if (gr < C) {
+      if (gc + 8 <= R) {
+        w = *reinterpret_cast<const uint4*>(src + gr * lds + gc);
+      } else {
+        uint32_t q[4] = {0u, 0u, 0u, 0u};
+        for (int e = 0; e < 8 && gc + e < R; ++e) q[e >> 1] |= (uint32_t)src[gr * lds + gc + e] << (16 * (e & 1));
+        w = make_uint4(q[0], q[1], q[2], q[3]);
+      }
+    }
+    *reinterpret_cast<uint4*>(t + sr * 64 + 8 * (cq ^ ns5_swz(sr))) = w;
+  }
+  __syncthreads();
+  for (int h = 0; h < 2; ++h) {
+    const int dr = rr + 32 * h;   // destination row in the tile = source column
+    const int64_t r = r0 + dr, c = c0 + 8 * cq;
+    if (r >= R || c >= C) continue;
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int sr = 8 * cq + e;
+      v[e] = bf16_to_f32(t[sr * 64 + 8 * ((dr >> 3) ^ ns5_swz(sr)) + (dr & 7)]);
+    }
+    store8(r, c, v);
+  }
+}
+
 // y = bf16(s * y + t * x), elementwise over n values (B from A and AA with
 // s = b, t = c; the new X from X and BX with s = a, t = 1)
 __global__ __launch_bounds__(256) void ns5_axpby_kernel(uint16_t* __restrict__ y, const uint16_t* __restrict__ x,
@@ -164,8 +240,9 @@ static MuonLayout muon_layout(int64_t N, int64_t K) {
   // leaves them in holds across calls of different shapes
   size_t g = gemm_splitk_need(MODE_FWD_BF16, m, m, n);
   const size_t g2 = gemm_splitk_need(MODE_DGRAD_BF16, m, m, m), g3 = gemm_splitk_need(MODE_DGRAD_BF16, m, n, m);
-  if (g2 > g) g = g2;
-  if (g3 > g) g = g3;
+  const size_t g4 = gemm_sym_splitk_need(MODE_FWD_BF16, m, n), g5 = gemm_sym_splitk_need(MODE_DGRAD_BF16, m, m);
+  for (size_t v : {g2, g3, g4, g5})
+    if (v > g) g = v;
   L.gemm = o; o += r256(g);
   L.x = o; o += r256((size_t)m * n * 2);
   L.bx = o; o += r256((size_t)m * n * 2);
@@ -216,9 +293,16 @@ extern "C" int concord_muon_ns5(const uint16_t* g, int64_t ld_g, int64_t N, int6
   const int64_t nb = cdiv(N * K, kFrobBlock);
 
   hipLaunchKernelGGL(frob_partials_kernel, dim3((unsigned)nb), dim3(256), 0, st, g, ld_g, N, K, part);
-  hipLaunchKernelGGL(frob_den_kernel, dim3(1), dim3(64), 0, st, part, nb, den);
   const dim3 gx((unsigned)cdiv(n, 64), (unsigned)cdiv(m, 64));
-  if (tr)
+  hipLaunchKernelGGL(frob_den_kernel, dim3(1), dim3(64), 0, st, part, nb, den);
+  // 16-byte accesses where the gradient and X allow them (X's rows are n
+  // elements from a 256-byte aligned base)
+  const bool vin = ((uintptr_t)g % 16) == 0 && ld_g % 8 == 0 && n % 8 == 0;
+  if (tr && vin)
+    hipLaunchKernelGGL((ns5_copy_vec_kernel<true, true>), gx, dim3(256), 0, st, g, ld_g, X, n, m, n, den, 0.0f);
+  else if (vin)
+    hipLaunchKernelGGL((ns5_copy_vec_kernel<false, true>), gx, dim3(256), 0, st, g, ld_g, X, n, m, n, den, 0.0f);
+  else if (tr)
     hipLaunchKernelGGL((ns5_copy_kernel<true, true>), gx, dim3(256), 0, st, g, ld_g, X, n, m, n, den, 0.0f);
   else
     hipLaunchKernelGGL((ns5_copy_kernel<false, true>), gx, dim3(256), 0, st, g, ld_g, X, n, m, n, den, 0.0f);
@@ -226,11 +310,17 @@ extern "C" int concord_muon_ns5(const uint16_t* g, int64_t ld_g, int64_t N, int6
   if (rc != CONCORD_OK) return rc;
   const float a = 3.4445f, b = -4.7750f, c = 2.0315f;
   for (int it = 0; it < 5; ++it) {
-    rc = gemm_bf16_run(MODE_FWD_BF16, X, n, X, n, A, m, m, m, n, gws, gws_bytes, st, "muon_ns5 X X^T");
+    // A = X X^T and A A are symmetric: only the tiles meeting the upper
+    // triangle are computed, each upper element also stored at its mirror
+    rc = gemm_bf16_sym(MODE_FWD_BF16, X, n, X, n, A, m, m, n, nullptr, 0, 0.0f, 0.0f, gws, gws_bytes, st,
+                       "muon_ns5 X X^T");
+    if (rc == -1) rc = gemm_bf16_run(MODE_FWD_BF16, X, n, X, n, A, m, m, m, n, gws, gws_bytes, st, "muon_ns5 X X^T");
     if (rc != CONCORD_OK) return rc;
-    // AA buffer <- B = bf16(b A + c bf16(A A))
-    rc = gemm_bf16_combine(MODE_DGRAD_BF16, A, m, A, m, AA, m, m, m, m, A, m, b, c, gws, gws_bytes, st,
-                           "muon_ns5 A A");
+    // AA buffer <- B = bf16(b A + c bf16(A A)), symmetric as A is
+    rc = gemm_bf16_sym(MODE_DGRAD_BF16, A, m, A, m, AA, m, m, m, A, m, b, c, gws, gws_bytes, st, "muon_ns5 A A");
+    if (rc == -1)
+      rc = gemm_bf16_combine(MODE_DGRAD_BF16, A, m, A, m, AA, m, m, m, m, A, m, b, c, gws, gws_bytes, st,
+                             "muon_ns5 A A");
     if (rc == -1) {
       rc = gemm_bf16_run(MODE_DGRAD_BF16, A, m, A, m, AA, m, m, m, m, gws, gws_bytes, st, "muon_ns5 A A");
       if (rc != CONCORD_OK) return rc;
@@ -254,7 +344,14 @@ extern "C" int concord_muon_ns5(const uint16_t* g, int64_t ld_g, int64_t N, int6
   }
   // out[N][K] = bf16(gamma X) (X^T when transposed)
   const dim3 go((unsigned)cdiv(K, 64), (unsigned)cdiv(N, 64));
-  if (tr)
+  const bool vout = ((uintptr_t)out % 16) == 0 && ld_out % 8 == 0 && n % 8 == 0;
+  if (tr && vout)
+    hipLaunchKernelGGL((ns5_copy_vec_kernel<true, false>), go, dim3(256), 0, st, X, n, out, ld_out, N, K, den,
+                       gamma);
+  else if (vout)
+    hipLaunchKernelGGL((ns5_copy_vec_kernel<false, false>), go, dim3(256), 0, st, X, n, out, ld_out, N, K, den,
+                       gamma);
+  else if (tr)
     hipLaunchKernelGGL((ns5_copy_kernel<true, false>), go, dim3(256), 0, st, X, n, out, ld_out, N, K, den, gamma);
   else
     hipLaunchKernelGGL((ns5_copy_kernel<false, false>), go, dim3(256), 0, st, X, n, out, ld_out, N, K, den, gamma);

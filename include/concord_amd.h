@@ -290,6 +290,20 @@ int concord_gemm_bf16_dgrad(const uint16_t* dy, int64_t ld_dy, const uint16_t* w
                             uint16_t* dx, int64_t ld_dx, int64_t M, int64_t N, int64_t K,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/* A symmetric bf16 product c[M,M] with fp32 accumulation, as the Muon
+ * drive's NS5 iteration forms it (experiments/cpu_dynamics/exp9_muon.py:52-53,
+ * A = X X^T and A A): b_rows = 1: c = a b^T with b [M,R] row-major (b = a
+ * gives X X^T); b_rows = 0: c = a b with b [R,M] (R = M; a and b symmetric
+ * and commuting, e.g. b = a).  Only the tiles meeting the upper triangle are
+ * computed; each element (i, j) with i <= j is stored at (i, j) and (j, i),
+ * so c is exactly symmetric.  The same tile and split plans as concord_muon_ns5's.
+ * workspace: concord_muon_workspace_bytes of the NS5 shape, or any split-K
+ * workspace of at least concord_gemm_sym_workspace_bytes(M, R, b_rows). */
+size_t concord_gemm_sym_workspace_bytes(int64_t M, int64_t R, int b_rows);
+int concord_gemm_bf16_sym(const uint16_t* a, int64_t ld_a, const uint16_t* b, int64_t ld_b, int b_rows,
+                          uint16_t* c, int64_t ld_c, int64_t M, int64_t R, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
 /* grad_bias[N] = bf16(sum_m dy[m, n]) with fp32 accumulation.  Replaces
  * grad_y_flat.sum(0), concord/packed_b.py:1338-1340. */
 int concord_bias_grad(const uint16_t* dy, int64_t ld_dy, int64_t M, int64_t N,

@@ -869,13 +869,46 @@ def test_muon_ns5_matches_oracle(oracle, N, K):
     assert rel_l2(got, ref) < 2e-2
 
 
+@pytest.mark.parametrize("M,R,b_rows", [(1280, 5120, 1), (1280, 1280, 0), (96, 160, 1), (200, 200, 0),
+                                         (1000, 3000, 1)])
+def test_gemm_bf16_sym_matches_float64(oracle, M, R, b_rows):
+    """The symmetric product (only the tiles meeting the upper triangle, the
+    rest mirrored): exactly symmetric; elementwise within one bf16 rounding
+    plus the worst-case fp32 summation error of R terms (R 2^-24 sum |terms|)
+    of the float64 product, and within 4e-3 rel-L2 of it (one bf16 rounding
+    is ~1e-3)."""
+    from concord_amd import _lib as C
+    rng = np.random.default_rng(M + R + b_rows)
+    a = oracle.f32_to_bf16_bits_array(rng.standard_normal((M, R)).astype(np.float32))
+    af = oracle.bf16_bits_to_f32(a).astype(np.float64)
+    if b_rows:
+        b, exact, mag = a, af @ af.T, np.abs(af) @ np.abs(af).T
+    else:   # a symmetric operand times itself
+        s = (af + af.T) / 2
+        a = oracle.f32_to_bf16_bits_array(s.astype(np.float32))
+        af = oracle.bf16_bits_to_f32(a).astype(np.float64)
+        b, exact, mag = a, af @ af, np.abs(af) @ np.abs(af)
+    ad, bd = dev(a).view(torch.bfloat16), dev(b).view(torch.bfloat16)
+    c = torch.empty((M, M), dtype=torch.bfloat16, device=DEV)
+    ws = torch.zeros(int(C.lib().concord_gemm_sym_workspace_bytes(M, R, b_rows)), dtype=torch.uint8, device=DEV)
+    C.check(C.lib().concord_gemm_bf16_sym(C.ptr(ad), R, C.ptr(bd), R if b_rows else M, b_rows, C.ptr(c), M, M, R,
+                                          C.ptr(ws), ws.numel(), C.stream_of(torch.device(DEV))), "gemm_bf16_sym")
+    sync()
+    got = host(c).view(np.uint16)
+    np.testing.assert_array_equal(got, got.T)
+    g = oracle.bf16_bits_to_f32(got).astype(np.float64)
+    tol = 2.0 ** -8 * np.abs(exact) + R * 2.0 ** -24 * mag
+    assert np.all(np.abs(g - exact) <= tol), np.max(np.abs(g - exact) - tol)
+    assert rel_l2(g, exact) < 4e-3
+
+
 @pytest.mark.parametrize("N,K", [(1280, 5120), (5120, 1280)])
 def test_muon_ns5_fused_combines_match_two_step(oracle, N, K):
     """NS5's two combinations ride in the epilogue of the product before them
     (A A -> B = bf16(b A + c bf16(A A)), B X -> X = bf16(a X + bf16(B X))).
     Re-running the two-step route -- the library's own bf16 GEMM entries
-    (same tile and split plans), the combinations in float32 on the host --
-    gives the same bits."""
+    (same tile and split plans: the symmetric product for X X^T and A A),
+    the combinations in float32 on the host -- gives the same bits."""
     from concord_amd import _lib as C
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(N + 7)
@@ -884,7 +917,8 @@ def test_muon_ns5_fused_combines_match_two_step(oracle, N, K):
     o = pb.muon_ns5(dev(g), gamma=gamma)
     sync()
     f32, bf = np.float32, oracle.f32_to_bf16_bits_array
-    den = f32(np.sqrt(oracle.frob_sumsq(g))) + f32(1e-7)
+    nrm = f32(np.sqrt(oracle.frob_sumsq(g)))
+    den = f32(max(nrm, f32(1e-12)) * f32(f32(nrm / max(nrm, f32(1e-12))) + f32(1e-7)))
     gf = oracle.bf16_bits_to_f32(g)
     if N > K:
         gf = np.ascontiguousarray(gf.T)
@@ -896,14 +930,16 @@ def test_muon_ns5_fused_combines_match_two_step(oracle, N, K):
     for _ in range(5):
         Xd = dev(X).view(torch.bfloat16)
         A = torch.empty((m, m), dtype=torch.bfloat16, device=DEV)
-        C.check(C.lib().concord_gemm_bf16_fwd(C.ptr(Xd), n, C.ptr(Xd), n, None, C.ptr(A), m, m, m, n,
+        C.check(C.lib().concord_gemm_bf16_sym(C.ptr(Xd), n, C.ptr(Xd), n, 1, C.ptr(A), m, m, n,
                                               C.ptr(ws), ws.numel(), st), "X X^T")
         AA = torch.empty((m, m), dtype=torch.bfloat16, device=DEV)
-        C.check(C.lib().concord_gemm_bf16_dgrad(C.ptr(A), m, C.ptr(A), m, C.ptr(AA), m, m, m, m,
-                                                C.ptr(ws), ws.numel(), st), "A A")
+        C.check(C.lib().concord_gemm_bf16_sym(C.ptr(A), m, C.ptr(A), m, 0, C.ptr(AA), m, m, m,
+                                              C.ptr(ws), ws.numel(), st), "A A")
         sync()
         Af = oracle.bf16_bits_to_f32(host(A).view(np.uint16))
         AAf = oracle.bf16_bits_to_f32(host(AA).view(np.uint16))
+        np.testing.assert_array_equal(host(A), host(A).T)     # mirrored: exactly symmetric
+        np.testing.assert_array_equal(host(AA), host(AA).T)
         B = bf((b * Af + c * AAf).astype(np.float32))
         Bd = dev(B).view(torch.bfloat16)
         BX = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
@@ -920,7 +956,7 @@ def test_muon_ns5_fused_combines_match_two_step(oracle, N, K):
 
 @pytest.mark.parametrize("N,K", [(2048, 5120), (1280, 5120), (333, 1001)])
 def test_muon_frobenius_denominator_bit_exact(oracle, N, K):
-    """The NS5 input scale max(||g||, 1e-12) * fl(1 + 1e-7) (block partials,
+    """The NS5 input scale n (||g|| / n + 1e-7), n = max(||g||, 1e-12) (block partials,
     then one wave chaining them in ascending order) equals the oracle's bit
     for bit; read back from the workspace (layout: the split-K region, X, BX,
     A, AA, partials, then the denominator in the last 256-byte slot)."""
@@ -935,7 +971,9 @@ def test_muon_frobenius_denominator_bit_exact(oracle, N, K):
     off = int(C.lib().concord_muon_workspace_bytes(N, K)) - 256
     den = host(ws[off:off + 4].view(torch.float32))[0]
     s = oracle.frob_sumsq(g)
-    want = np.float32(max(np.float32(np.sqrt(np.float32(s))), np.float32(1e-12)) * np.float32(1.0 + 1e-7))
+    nrm = np.float32(np.sqrt(np.float32(s)))
+    n = max(nrm, np.float32(1e-12))
+    want = np.float32(n * np.float32(np.float32(nrm / n) + np.float32(1e-7)))
     assert den.view(np.uint32) == np.float32(want).view(np.uint32), (den, want)
 
 
