@@ -295,7 +295,52 @@ def _next_rows(layer, xb, dy, gw, reps, warmup, steps, torch, ca, pb):
     return out
 
 
-def _config4_step(steps, torch, ca, pb):
+def _config4_groups(layers, xs, dys, reps, torch):
+    """Per (out, in, tokens) group of config 4's layers: the layer step
+    (forward, backward with the fused update) of every layer of the group
+    captured in one HIP graph, replayed `reps` times; microseconds per layer
+    and the group's share of 6 M N K."""
+    groups = {}
+    for la, m in layers:
+        groups.setdefault((la.out_features, la.in_features, m), []).append(la)
+    out = {}
+    for (n_out, n_in, m), lays in groups.items():
+        key = (m, n_in, n_out)
+        x, dy = xs[key], dys[key]
+
+        def run():
+            for la in lays:
+                x.grad = None
+                la.bias.grad = None
+                la(x).backward(dy)
+        run()
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                run()
+        torch.cuda.current_stream().wait_stream(s)
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps / len(lays)
+        tf = 6.0 * m * n_out * n_in / (us * 1e-6) / 1e12
+        out[f"{n_in}to{n_out}_M{m}"] = {"layers": len(lays), "us_per_layer": round(us, 1),
+                                         "group_ms": round(us * len(lays) / 1e3, 3), "tflops": round(tf, 1),
+                                         "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+        del g
+    return out
+
+
+def _config4_step(steps, torch, ca, pb, per_group=False):
     """Config 4: one training step over all 754 SDXL Linear and 1x1 weights
     (2.25 B parameters held packed, 9.0 GB), each layer forward + backward
     (dgrad, wgrad, v-hat, fused update; winner flags) on its own token count,
@@ -377,6 +422,8 @@ def _config4_step(steps, torch, ca, pb):
            "frac": round(a / PEAK_BF16_TFLOPS, 4), "timing": f"one HIP graph per step, {reps} replays",
            "eager_ms_per_step": round(eager_ms, 1), "gate_fires_in_run": fires,
            "gate_nofire_us": {"device_gate": round(t_dev * 1e3, 1), "host_gate_with_item": round(t_host * 1e3, 1)}}
+    if per_group:
+        out["per_group"] = _config4_groups(layers, xs, dys, reps, torch)
     del g, layers, xs, dys, gate, hg
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -543,8 +590,9 @@ def main():
                     help="skip the config-4 row (the graph-captured step over all 754 SDXL weights)")
     ap.add_argument("--only", default=None,
                     choices=["fwd", "bwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
-                             "copy", "ns5", "config3"],
-                    help="time one entry alone; config3 times only the step on each config-3 SDXL shape")
+                             "copy", "ns5", "config3", "config4"],
+                    help="time one entry alone; config3 times only the step on each config-3 SDXL shape; "
+                         "config4 only the config-4 step, and each of its (shape, tokens) groups of layers")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--graph-steps", type=int, default=5,
                     help="training steps captured per HIP graph (1 = one graph replay per step)")
@@ -583,6 +631,11 @@ def main():
 
     if args.only == "config3":
         print(json.dumps({"sdxl_shapes": _config3_steps(args.warmup, args.steps, torch, ca)}), flush=True)
+        return
+    if args.only == "config4":
+        del layer, x, dy
+        torch.cuda.empty_cache()
+        print(json.dumps({"config4_step": _config4_step(args.steps, torch, ca, pb, per_group=True)}), flush=True)
         return
     if args.only:
         _only(args.only, args.reps, layer, x.detach(), dy, torch, pb)
