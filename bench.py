@@ -491,6 +491,44 @@ def _weight_cache_step_ms(layer, x, dy, warmup, steps, torch, ca, per_graph=1):
     return sum(cache) / 2, sum(fused) / 2
 
 
+def _dma_probe(reps, torch):
+    """The load paths of the GEMM kernels, measured alone (concord_amd_diag.h):
+    a 256 MiB copy through LDS-DMA loads (`reps` calls; its FETCH_SIZE /
+    WRITE_SIZE per byte calibrate the counters of the LDS-DMA kernels), then
+    the L2-to-CU rate: each workgroup streams its XCD's 1 MiB region 64 times
+    (after the first pass every load hits that XCD's L2), by LDS-DMA and by
+    register loads, 2 to 8 chunks of 16 KB in flight, one and two workgroups
+    per CU.  Prints one JSON line; GB/s per CU = bytes / time / 256."""
+    from concord_amd import _lib as C
+    dev = torch.device("cuda:0")
+    a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+
+    def copy():   # on the current stream (the capture stream inside _event_time_ms)
+        C.check(C.lib().concord_diag_dma_copy(C.ptr(a), C.ptr(b), a.numel(), C.stream_of(dev)), "diag_dma_copy")
+    for _ in range(reps):
+        copy()
+    torch.cuda.synchronize()
+    t_copy = _event_time_ms(copy, 5, torch)
+    region, rep = 1 << 20, 64
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    out = {"dma_copy_256MiB": {"us": round(t_copy * 1e3, 1), "GBps": round(2 * a.numel() / (t_copy * 1e-3) / 1e9, 1)},
+           "l2_stream": {}}
+    for lds_dma in (1, 0):
+        for depth in (2, 4, 8):
+            for per_cu in (1, 2):
+                blocks = 256 * per_cu
+
+                def run():
+                    C.check(C.lib().concord_diag_l2_stream(C.ptr(a), region, rep, blocks, depth, lds_dma, C.ptr(sink),
+                                                           C.stream_of(dev)), "diag_l2_stream")
+                t = _event_time_ms(run, 3, torch)
+                gbps_cu = blocks * region * rep / (t * 1e-3) / 1e9 / 256
+                out["l2_stream"][f"{'dma' if lds_dma else 'vgpr'}_depth{depth}_wg{per_cu}"] = {
+                    "us": round(t * 1e3, 1), "GBps_per_CU": round(gbps_cu, 1)}
+    print(json.dumps({"dma_probe": out}), flush=True)
+
+
 def _only(which, reps, layer, xb, dy, torch, pb):
     """Run one kernel of the step `reps` times (profiling entry)."""
     st = (layer.packed_w, layer.row_exp, layer.col_exp)
@@ -499,6 +537,9 @@ def _only(which, reps, layer, xb, dy, torch, pb):
         a = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
         b = torch.empty_like(a)
         fn = lambda: b.copy_(a)  # noqa: E731
+    elif which == "dma":
+        _dma_probe(reps, torch)
+        return
     elif which == "fwd":
         fn = lambda: pb._gemm_fwd(xb, *st, 15, layer.bias, None)  # noqa: E731
     elif which == "dgrad":
@@ -590,7 +631,7 @@ def main():
                     help="skip the config-4 row (the graph-captured step over all 754 SDXL weights)")
     ap.add_argument("--only", default=None,
                     choices=["fwd", "bwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
-                             "copy", "ns5", "config3", "config4"],
+                             "copy", "dma", "ns5", "config3", "config4"],
                     help="time one entry alone; config3 times only the step on each config-3 SDXL shape; "
                          "config4 only the config-4 step, and each of its (shape, tokens) groups of layers")
     ap.add_argument("--reps", type=int, default=20)

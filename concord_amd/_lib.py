@@ -90,6 +90,9 @@ _SIGS = {
     "concord_gemm_bf16_fwd": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _I, _I, _I, _I, _P, _Z, _P]),
     "concord_gemm_bf16_dgrad": (ctypes.c_int, [_P, _I, _P, _I, _P, _I, _I, _I, _I, _P, _Z, _P]),
     "concord_gemm_sym_workspace_bytes": (_Z, [_I, _I, ctypes.c_int]),
+    "concord_diag_dma_copy": (ctypes.c_int, [_P, _P, _Z, _P]),
+    "concord_diag_l2_stream": (ctypes.c_int, [_P, _Z, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P,
+                                              _P]),
     "concord_gemm_bf16_sym": (ctypes.c_int, [_P, _I, _P, _I, ctypes.c_int, _P, _I, _I, _I, _P, _Z, _P]),
     "concord_bias_grad": (ctypes.c_int, [_P, _I, _I, _I, _P, _P, _Z, _P]),
     "concord_stats_workspace_bytes": (_Z, [_I, _I]),

@@ -492,6 +492,57 @@ def test_implicit_layer_state_vs_oracle(oracle, case):
     np.testing.assert_array_equal(host(conv.get_weight()), O.materialize(st[0], st[1], st[2]))
 
 
+@pytest.mark.parametrize("case", [(640, 640, 3, 1, 1, 2, 64, 64), (320, 320, 3, 1, 1, 2, 128, 128)])
+def test_sdxl_conv_layer_state_vs_oracle(oracle, case):
+    """One training step of an SDXL-sized 3 x 3 conv layer (640 channels at
+    64^2 and 320 at 128^2, batch 2): the WGRAD takes the 128 x 256 tiles and
+    a split reduction with the v-hat partials (concord_conv_wgrad_vhat).
+    v-hat, packed words and exponents after the rebalance bit-exact against
+    the oracle fed the captured bf16 gradient, as the toy geometries above."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    O = oracle
+    cin, cout, k, stride, pad, B, H, W = case
+    torch.manual_seed(23)
+    conv = ca.ConcordConv2dPackedB(cin, cout, k, stride=stride, padding=pad, bias=True, device=DEV, lr=5e-4)
+    W0 = torch.randn(cout, cin * k * k) * 0.02
+    conv.load_weights(W0)
+    p0, r0, c0 = O.load_weights(W0.numpy())
+    K = cin * k * k
+    st = [p0.copy(), r0.copy(), c0.copy(), np.zeros(cout, np.float32), np.zeros(K, np.float32)]
+    coh = np.ones((cout, K), np.float32)
+    flags = O.MASS_PRESERVE | O.APPLY_CHASE | O.TRACK_REBALANCE | O.GF_TRUST_REGION | O.FIXED_COH | O.COHPRE
+    P = O.UpdateParams(alpha=0.1, beta1=0.0, weight_decay=0.0, step_cap=10.0, v_scale=0.0, precond_p=0.5,
+                       gf_consol=0.0, drift_cancel_C=conv.drift_cancel_C, alpha_v_fast=0.001, wd_sv=0.0,
+                       wd_sf=0.0, gf_trust_delta_sq=1.0, gate_gain=1.0, mantissa_bias=15)
+    salt_next = int(host(pb._get_step_counter(DEV))[0]) + 1
+    x = torch.randn(B, cin, H, W, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    assert conv.conv_path(x) == 'implicit'
+    cap = []
+    pb._DEBUG_CAPTURE = cap
+    try:
+        y = conv(x)
+        y.backward((torch.randn_like(y.float()) * 1e-3).to(torch.bfloat16))
+    finally:
+        pb._DEBUG_CAPTURE = None
+    conv.rebalance()
+    sync()
+    g = host(cap[0])
+    svi = O.vhat_ema(g, st[3], st[4], 0.999)
+    rm = np.zeros(cout, np.int32)
+    cm = np.zeros(K, np.int32)
+    S = O.UpdateScalars(lr=5e-4, eps=1e-10, chase_floor=0.9, leak_floor=0.999, v_bc=1.0, salt=salt_next,
+                        consolidate=1)
+    O.apply_adamw(st[0], g, None, st[1], st[2], rm, cm, st[3], st[4], svi, coh, P, S, flags)
+    O.rebalance(st[0], st[1], st[2], rm, cm, seed=1)
+    np.testing.assert_array_equal(host(conv.v_row), st[3])
+    np.testing.assert_array_equal(host(conv.v_col), st[4])
+    np.testing.assert_array_equal(host(conv.packed_w), st[0])
+    np.testing.assert_array_equal(host(conv.row_exp), st[1])
+    np.testing.assert_array_equal(host(conv.col_exp), st[2])
+    assert (st[0] != p0).any()
+
+
 # SDXL-UNet conv shapes at batch 2 of a 1024 px latent: the 3 x 3 resnet
 # convs per level (320 ch at 128^2, 640 at 64^2, 1280 at 32^2), a stride-2
 # downsample, and the level-crossing 640 -> 1280 conv

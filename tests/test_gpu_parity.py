@@ -579,7 +579,9 @@ def test_load_weights_matches_oracle(oracle):
 GEMM_SHAPES = [(64, 128, 64), (77, 130, 200), (256, 384, 1280), (1, 5, 3), (130, 1000, 70),
                (2048, 1280, 1280), (2048, 5120, 1280), (300, 2050, 645),
                (77, 136, 200), (300, 2056, 648), (1, 8, 8), (129, 1000, 72), (64, 136, 4096),
-               (8192, 640, 640), (1024, 2816, 2048)]
+               (8192, 640, 640), (1024, 2816, 2048),
+               # cross-attention k/v at batch 2 and 4 of 77 text tokens (M 154, 308)
+               (154, 1280, 2048), (308, 1280, 2048), (308, 640, 2048)]
 
 
 def _decoded(oracle, packed, re, ce):
