@@ -529,6 +529,66 @@ def _dma_probe(reps, torch):
     print(json.dumps({"dma_probe": out}), flush=True)
 
 
+def _layer_ctx(layer, pb):
+    """The attributes the backward's update reads from its autograd context,
+    taken from the layer (the module's forward passes the same objects)."""
+    import types
+    return types.SimpleNamespace(
+        packed_w=layer.packed_w, row_exp=layer.row_exp, col_exp=layer.col_exp, has_bias=True,
+        optimizer_kind="adamw", weight_buf=None, lr=layer._lr_buf, mantissa_bias=layer.MANTISSA_BIAS,
+        alpha=layer.alpha, beta1=layer.beta1, weight_decay=layer.weight_decay, eps=layer._eps_buf,
+        step_cap=layer.step_cap, v_scale=layer.v_scale, precond_p=layer.precond_p, gf_consol=layer.gf_consol,
+        drift_cancel_C=layer.drift_cancel_C, alpha_v_fast=layer.alpha_v_fast, wd_sv=layer.wd_sv, wd_sf=layer.wd_sf,
+        mass_preserve=layer.mass_preserve_v, apply_chase=layer.apply_chase, track_rebalance=layer.track_rebalance,
+        gf_trust_delta_sq=float(layer.gf_trust_delta_sq), coh_pre=layer._coh_pre, row_max_buf=layer._row_max_buf,
+        col_max_buf=layer._col_max_buf, adafactor_beta2=float(layer.adafactor_beta2), v_row=layer.v_row,
+        v_col=layer.v_col, sum_v_inv=layer._sum_v_inv)
+
+
+def _bwd_update_fns(layer, xb, dy, pb):
+    """The step's backward with its update, each way: (two_pass, fused).
+    two_pass = concord_dgrad_wgrad_vhat then concord_apply_adamw; fused =
+    concord_dgrad_wgrad_update (finalize and update in the WGRAD launch)."""
+    ctx = _layer_ctx(layer, pb)
+    salt = pb._get_step_counter(xb.device)
+
+    def two_pass():
+        _, gw, _ = pb._dgrad_wgrad_vhat(dy, xb, layer.packed_w, layer.row_exp, layer.col_exp, 15, layer.v_row,
+                                        layer.v_col, layer._sum_v_inv, 0.999, layer._row_max_buf,
+                                        layer._col_max_buf, salt, with_bias=True)
+        pb._packed_step(ctx, gw, True, False)
+
+    def fused():
+        pb._dgrad_wgrad_update(ctx, dy, xb)
+    return two_pass, fused
+
+
+def _fused_update_rows(layer, step, xb, dy, warmup, steps, G, reps, torch, pb):
+    """The wgrad-fused update beside the two-pass form, measured in the same
+    run on the same layer: the whole step (graph-timed as the headline, G
+    steps per graph) and the backward entry with its update (events over a
+    graph of `reps` calls), each way."""
+    two_pass, fused = _bwd_update_fns(layer, xb, dy, pb)
+    out = {}
+    prev = pb._FUSED_UPDATE
+    try:
+        for name, on in (("two_pass", False), ("fused", True)):
+            pb.set_fused_update(on)
+            out[f"step_ms_{name}"] = round(_graph_ms(step, warmup, steps, torch, per_graph=G), 4)
+        out["bwd_update_us_two_pass"] = round(_event_time_ms(two_pass, reps, torch) * 1e3, 2)
+        out["bwd_update_us_fused"] = round(_event_time_ms(fused, reps, torch) * 1e3, 2)
+        out["fused_launch_taken"] = bool(pb._LAST_FUSED[0])
+        out["fault"] = pb.wgrad_update_faults(xb.device)
+    finally:
+        pb.set_fused_update(prev)
+    out["kept"] = "fused" if prev else "two_pass"
+    out["note"] = ("two_pass: gemm_dgt_kernel + gemm_tr_kernel<VH> (carrying the dgrad reduction) + "
+                   "vhat_finalize_kernel + apply_adamw_fast_kernel; fused: gemm_dgt_kernel + wgrad_update_kernel "
+                   "(tiles, v-hat partials, grid barrier, finalize over the grid, grid barrier, update of each "
+                   "tile from its accumulators; no bf16 weight gradient)")
+    return out
+
+
 def _only(which, reps, layer, xb, dy, torch, pb):
     """Run one kernel of the step `reps` times (profiling entry)."""
     st = (layer.packed_w, layer.row_exp, layer.col_exp)
@@ -540,6 +600,9 @@ def _only(which, reps, layer, xb, dy, torch, pb):
     elif which == "dma":
         _dma_probe(reps, torch)
         return
+    elif which in ("bwd_update", "bwd_update_fused"):
+        two_pass, fused = _bwd_update_fns(layer, xb, dy, pb)
+        fn = fused if which == "bwd_update_fused" else two_pass
     elif which == "fwd":
         fn = lambda: pb._gemm_fwd(xb, *st, 15, layer.bias, None)  # noqa: E731
     elif which == "dgrad":
@@ -631,7 +694,7 @@ def main():
                     help="skip the config-4 row (the graph-captured step over all 754 SDXL weights)")
     ap.add_argument("--only", default=None,
                     choices=["fwd", "bwd", "dgrad", "wgrad", "wgrad_vhat", "vhat", "update", "materialize",
-                             "copy", "dma", "ns5", "config3", "config4"],
+                             "copy", "dma", "ns5", "config3", "config4", "bwd_update", "bwd_update_fused"],
                     help="time one entry alone; config3 times only the step on each config-3 SDXL shape; "
                          "config4 only the config-4 step, and each of its (shape, tokens) groups of layers")
     ap.add_argument("--reps", type=int, default=20)
@@ -754,6 +817,7 @@ def main():
                               sum_v_inv=layer._sum_v_inv, gf_trust_delta_sq=1.0, coh_pre=None,
                               salt_prebumped=True)
     t_upd = _event_time_ms(upd, reps, torch)
+    fused_rows = _fused_update_rows(layer, step, xb, dy, args.warmup, args.steps, per_run, reps, torch, pb)
     wbuf = torch.empty((N_OUT, K_IN), dtype=torch.bfloat16, device=dev)
     t_mat = _event_time_ms(lambda: pb.materialize_packed_bf16(layer.packed_w, layer.row_exp,
                                                               layer.col_exp, wbuf), reps, torch)
@@ -859,6 +923,7 @@ def main():
                         "wgrad_vhat": round(gemm_flop / (t_wgv * 1e-3) / 1e12, 1),
                         "wgrad_alone": round(gemm_flop / (t_wgrad * 1e-3) / 1e12, 1)},
         "materialize_GBps": round(DECODE_BYTES_PER_PARAM * params / (t_mat * 1e-3) / 1e9, 1),
+        "wgrad_fused_update": fused_rows,
         "muon_ns5": {"us": round(t_ns5 * 1e3, 1),
                      "tflops": round(ns5_flop / (t_ns5 * 1e-3) / 1e12, 1)},
         "next_rows": dict(note="the rows beside the step, timed on the same state; context only",

@@ -197,6 +197,12 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd, void* workspace, size_t ws_
                                  hipStream_t st, const char* what, int* tiles_j);
 // tiles along J of the WGRAD launch above (the bias partials' row count)
 int64_t gemm_wgrad_vhat_tiles_j(int64_t J);
+// the products of gemm_dgrad_wgrad_vhat_launch with the v-hat finalize and the
+// packed update carried by the WGRAD launch (wgrad_update.h); upd = 1 bare,
+// 2 winner (update_fast_path).  -1 when that launch does not apply.
+struct WgradUpd;
+int gemm_dgrad_wgrad_update_launch(const GemmArgs& gd, void* workspace, size_t ws_bytes, const GemmArgs& gw,
+                                   const WgradUpd& u, int upd, hipStream_t st, const char* what);
 // c = bf16(s * y + t * bf16(product)) for MODE_FWD_BF16 / MODE_DGRAD_BF16 on
 // the fast kernels (the combine applied in their epilogue or split-K
 // reduction); -1 when the operands do not take the fast kernels (the caller

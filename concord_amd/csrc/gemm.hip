@@ -22,7 +22,9 @@
 // Tiles are mapped XCD-aware: workgroup w runs on XCD w % 8, and each XCD
 // gets a compact block of the tile grid so its L2 serves shared operands.
 #include "gemm.h"
+#include "update_fast.h"
 #include "vhat.h"
+#include "wgrad_update.h"
 #include "workspace.h"
 
 namespace concord {
@@ -667,6 +669,124 @@ extern "C" int concord_dgrad_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const
   return wgrad_vhat_impl(&gd, dy, ld_dy, x, ld_x, grad_w, ld_gw, M, N, K, beta2, v_row, v_col, sum_v_inv,
                          row_max, col_max, salt_counter, grad_bias, workspace, workspace_bytes, gemm_workspace,
                          gemm_workspace_bytes, (hipStream_t)stream, "dgrad_wgrad_vhat");
+}
+
+// constant-clock ticks of the grid barrier's bound (100 ms), per device
+static int64_t grid_timeout_ticks() {
+  constexpr int kMaxDev = 64;
+  static int64_t ticks[kMaxDev];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+  if (ticks[dev] == 0) {
+    int khz = 0;
+    if (hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev) != hipSuccess || khz <= 0) return 0;
+    ticks[dev] = (int64_t)khz * 100;
+  }
+  return ticks[dev];
+}
+
+extern "C" int concord_dgrad_wgrad_update(
+    const uint16_t* dy, int64_t ld_dy, int32_t* packed, int64_t ld_p, const int8_t* row_exp, const int8_t* col_exp,
+    uint16_t* dx, int64_t ld_dx, const uint16_t* x, int64_t ld_x, uint16_t* grad_w, int64_t ld_gw, int copy_grad,
+    int64_t M, int64_t N, int64_t K, double beta2, float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max,
+    int32_t* col_max, float* coh_pre, int64_t ld_c, uint16_t* grad_bias, const concord_update_params* params,
+    const concord_device_scalars* scalars, uint32_t flags, void* workspace, size_t workspace_bytes,
+    void* gemm_workspace, size_t gemm_workspace_bytes, int* fused, void* stream) {
+  const char* what = "dgrad_wgrad_update";
+  if (fused) *fused = 0;
+  CONCORD_CHECK(sizes_ok(M, N, K) && N > 0 && K > 0, "concord_dgrad_wgrad_update: bad size");
+  CONCORD_CHECK(params && scalars && scalars->lr && scalars->eps && scalars->salt_counter,
+                "concord_dgrad_wgrad_update: params/scalars NULL");
+  CONCORD_CHECK(packed && row_exp && col_exp && grad_w && v_row && v_col && sum_v_inv && (M == 0 || (dy && dx && x)),
+                "concord_dgrad_wgrad_update: NULL argument");
+  CONCORD_CHECK(ld_dy >= N && ld_p >= K && ld_dx >= K && ld_x >= K && ld_gw >= K,
+                "concord_dgrad_wgrad_update: bad leading dimension");
+  CONCORD_CHECK(!(flags & CONCORD_EMIT_WEIGHT), "concord_dgrad_wgrad_update: EMIT_WEIGHT needs the separate update");
+  CONCORD_CHECK(!(flags & CONCORD_TRACK_REBALANCE) || (row_max && col_max),
+                "concord_dgrad_wgrad_update: TRACK_REBALANCE needs row_max/col_max");
+  CONCORD_CHECK(!(flags & CONCORD_RATIO_COH) || (scalars->chase_floor && scalars->leak_floor),
+                "concord_dgrad_wgrad_update: RATIO_COH needs chase_floor/leak_floor");
+  const int upd = update_fast_path(*params, flags);
+  const Workspace ws = workspace_layout(N, K, grad_bias ? M : 0);
+  if (!workspace || workspace_bytes < ws.total) {
+    set_error("%s: workspace of %zu bytes needed", what, ws.total);
+    return CONCORD_EWORKSPACE;
+  }
+  hipStream_t st = (hipStream_t)stream;
+  const GemmArgs gd =
+      make_args(dy, packed, ld_dy, ld_p, row_exp, col_exp, params->mantissa_bias, nullptr, dx, ld_dx, M, K, N, true);
+  const int64_t ticks = grid_timeout_ticks();
+  const bool layout_ok = ld_p % 4 == 0 && ((uintptr_t)packed % 16) == 0 && ((uintptr_t)col_exp % 4) == 0 &&
+                         (upd != 1 || (coh_pre && ld_c >= K && ld_c % 4 == 0 && ((uintptr_t)coh_pre % 16) == 0));
+  if (M > 0 && upd != 0 && layout_ok && ticks > 0) {
+    const VhatScratch v = vhat_scratch(N, K);
+    float* pr = (float*)((char*)workspace + ws.scratch);
+    float* pc = pr + v.pr;
+    float* bsum = pc + v.pc;
+    float* bpart = bsum + v.bsum;
+    GemmArgs gw = make_args(dy, x, ld_dy, ld_x, nullptr, nullptr, 0, nullptr, grad_w, ld_gw, N, K, M, false);
+    gw.vh_pr = pr;
+    gw.vh_pc = pc;
+    gw.bpart = grad_bias ? bpart : nullptr;
+    if (!copy_grad) gw.c = nullptr;
+    WgradUpd u{};
+    u.v_row = v_row;
+    u.v_col = v_col;
+    u.bsum = bsum;
+    u.sum_v_inv = sum_v_inv;
+    u.row_max = row_max;
+    u.col_max = col_max;
+    u.salt = scalars->salt_counter;
+    u.grad_bias = grad_bias;
+    u.b2 = (float)beta2;
+    u.omb2 = (float)(1.0 - beta2);
+    u.bar = (uint32_t*)((char*)workspace + kGridBarrierOffset);
+    u.exitc = (uint32_t*)((char*)workspace + kGridExitOffset);
+    u.fault = (uint32_t*)((char*)workspace + kGridFaultOffset);
+    u.timeout_ticks = ticks;
+    u.packed = packed;
+    u.ld_p = ld_p;
+    u.row_exp = row_exp;
+    u.col_exp = col_exp;
+    u.coh_pre = coh_pre;
+    u.ld_c = ld_c;
+    u.p = *params;
+    u.s = *scalars;
+    u.flags = flags | CONCORD_SALT_PREBUMPED;
+    const int rc = gemm_dgrad_wgrad_update_launch(gd, gemm_workspace, gemm_workspace ? gemm_workspace_bytes : 0, gw,
+                                                  u, upd, st, what);
+    if (rc != -1) {
+      if (rc == CONCORD_OK && fused) *fused = 1;
+      return rc;
+    }
+  }
+  // the two launches' worth: products + v-hat EMA, then the update
+  const int rc = wgrad_vhat_impl(&gd, dy, ld_dy, x, ld_x, grad_w, ld_gw, M, N, K, beta2, v_row, v_col, sum_v_inv,
+                                 row_max, col_max, scalars->salt_counter, grad_bias, workspace, workspace_bytes,
+                                 gemm_workspace, gemm_workspace_bytes, st, what);
+  if (rc != CONCORD_OK) return rc;
+  return concord_apply_adamw(packed, ld_p, grad_w, ld_gw, nullptr, K, row_exp, col_exp, row_max, col_max, v_row,
+                             v_col, sum_v_inv, coh_pre, ld_c, N, K, params, scalars, flags | CONCORD_SALT_PREBUMPED,
+                             stream);
+}
+
+extern "C" int concord_wgrad_update_fault(void* workspace, size_t workspace_bytes, int* fault, void* stream) {
+  CONCORD_CHECK(workspace && fault && workspace_bytes >= kGridFaultOffset + sizeof(uint32_t),
+                "concord_wgrad_update_fault: bad argument");
+  hipStream_t st = (hipStream_t)stream;
+  uint32_t v = 0;
+  uint32_t* flag = (uint32_t*)((char*)workspace + kGridFaultOffset);
+  if (hipMemcpyAsync(&v, flag, sizeof(v), hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess) {
+    set_error("concord_wgrad_update_fault: reading the flag failed");
+    return CONCORD_ELAUNCH;
+  }
+  *fault = (int)v;
+  if (v != 0 && (hipMemsetAsync(flag, 0, sizeof(v), st) != hipSuccess || hipStreamSynchronize(st) != hipSuccess)) {
+    set_error("concord_wgrad_update_fault: clearing the flag failed");
+    return CONCORD_ELAUNCH;
+  }
+  return CONCORD_OK;
 }
 
 extern "C" int concord_gemm_bf16_fwd(const uint16_t* x, int64_t ld_x, const uint16_t* w,

@@ -28,6 +28,7 @@
 
 #include "gemm.h"
 #include "vhat_tile.h"
+#include "wgrad_update.h"
 #include "workspace.h"
 
 namespace concord {
@@ -1521,24 +1522,36 @@ CONCORD_DEV void bias_acc(f32x4 (&b)[NI], const bf16x8 (&fa)[NI]) {
 // kernel issued just before on the stream, on the CUs the WGRAD grid leaves
 // idle (200 tiles on 256 CUs at 1280 -> 5120).
 // CONV: the B operand (x) is the conv wgrad's gathered patch matrix (TrDmaConv).
-template <int BI, int BJ, int WI, int WJ, bool VH, bool CONV = false, int RBI = 256>
-__global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, GemmArgs rd, int tr_blocks) {
+// UPD (1 bare, 2 winner; VH launches with the dgrad reduction only): the
+// launch also carries the v-hat finalize and the packed update
+// (wgrad_update.h); every workgroup meets the grid barriers, the WGRAD
+// workgroups update their tiles from the accumulators, and the bf16 weight
+// gradient is stored only when g.c is set.
+template <int BI, int BJ, int WI, int WJ, bool VH, bool CONV, int RBI, int UPD>
+CONCORD_DEV void gemm_tr_body(const GemmArgs& g, const GemmArgs& rd, int tr_blocks, const WgradUpd& u) {
   constexpr int NW = WI * WJ, NT = 64 * NW, WTI = BI / WI, WTJ = BJ / WJ;
-  if (VH && (int)blockIdx.x >= tr_blocks) {
-    const int64_t items = splitk_reduce_items<CONCORD_DGRAD_REDUCE>(rd);
-    const int64_t stride = (int64_t)(gridDim.x - tr_blocks) * NT;
-    for (int64_t idx = (int64_t)(blockIdx.x - tr_blocks) * NT + threadIdx.x; idx < items; idx += stride)
-      splitk_reduce_item<CONCORD_DGRAD_REDUCE>(rd, idx);
-    return;
-  }
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
   typedef TrDma<BI, NW> DA;
   typedef typename std::conditional<CONV, TrDmaConv<BJ, NW>, TrDma<BJ, NW>>::type DB;
   constexpr int ABYTES = TR * BI * 2, STAGE = ABYTES + TR * BJ * 2;
   constexpr int PERT = DA::PER + DB::PER;
   static_assert(TR == 64, "two 32-deep MFMA steps per stage");
+  static_assert(UPD == 0 || (VH && !CONV && NW == 8), "the update rides on the VH launch of 8 waves");
   __shared__ __attribute__((aligned(1024))) uint16_t ring[3 * STAGE / 2];
   static_assert(sizeof(ring) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the ring");
+  __shared__ int s_flag;
+  if (VH && (int)blockIdx.x >= tr_blocks) {
+    const int64_t items = splitk_reduce_items<CONCORD_DGRAD_REDUCE>(rd);
+    const int64_t stride = (int64_t)(gridDim.x - tr_blocks) * NT;
+    for (int64_t idx = (int64_t)(blockIdx.x - tr_blocks) * NT + threadIdx.x; idx < items; idx += stride)
+      splitk_reduce_item<CONCORD_DGRAD_REDUCE>(rd, idx);
+    if constexpr (UPD != 0) {
+      if (!grid_sync(u, gridDim.x, &s_flag)) upd_finalize(g, u, reinterpret_cast<float*>(ring));
+      grid_sync(u, 2 * gridDim.x, &s_flag);
+      grid_exit(u);
+    }
+    return;
+  }
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -1629,7 +1642,11 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
 #pragma unroll
     for (int x = 0; x < NI; ++x) {
       const int64_t i = i0 + wi * WTI + 16 * x + (lane & 15);
-      if (lane < 16 && i < g.I) g.bpart[((int64_t)split * g.tiles_j + bj) * g.I + i] = bsum[x][0];
+      if (lane < 16 && i < g.I) {
+        float* dst = g.bpart + ((int64_t)split * g.tiles_j + bj) * g.I + i;
+        if (UPD != 0) coh_store(dst, bsum[x][0]);
+        else *dst = bsum[x][0];
+      }
     }
   }
   // no DMA may still be writing LDS when the ring is reused for the output
@@ -1649,10 +1666,32 @@ __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, Ge
 #pragma unroll
         for (int e = 0; e < 4; ++e) g2[x][y][e] = __fmul_rn(v[e], v[e]);
       }
-    vhat_tile_partials(g2, lane, i0 + wi * WTI, j0 + wj * WTJ, g.I, g.J, g.vh_pr, g.vh_pc);
+    vhat_tile_partials<UPD != 0>(g2, lane, i0 + wi * WTI, j0 + wj * WTJ, g.I, g.J, g.vh_pr, g.vh_pc);
   }
-  epilogue<MODE_WGRAD, NI, NJ, BI, BJ, NW>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, wave, t, NT,
-                                           ring);
+  if (UPD == 0 || g.c)
+    epilogue<MODE_WGRAD, NI, NJ, BI, BJ, NW>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, wave, t,
+                                             NT, ring);
+  if constexpr (UPD != 0) {
+    const bool bad = grid_sync(u, gridDim.x, &s_flag);
+    if (!bad) upd_finalize(g, u, reinterpret_cast<float*>(ring));
+    if (!grid_sync(u, 2 * gridDim.x, &s_flag) && !bad) {
+      int32_t* lds = reinterpret_cast<int32_t*>(ring);
+      upd_apply<UPD == 2>(g, u, acc, i0, j0, wi, wj, lds, lds + 512);
+    }
+    grid_exit(u);
+  }
+}
+
+template <int BI, int BJ, int WI, int WJ, bool VH, bool CONV = false, int RBI = 256>
+__global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, GemmArgs rd, int tr_blocks) {
+  gemm_tr_body<BI, BJ, WI, WJ, VH, CONV, RBI, 0>(g, rd, tr_blocks, WgradUpd{});
+}
+
+// the WGRAD launch of the backward entry carrying the finalize and the update
+// (wgrad_update.h); RBI = the dgrad reduction's tile rows, UPD = 1 bare, 2 winner
+template <int RBI, int UPD>
+__global__ __launch_bounds__(512, 1) void wgrad_update_kernel(GemmArgs g, GemmArgs rd, int tr_blocks, WgradUpd u) {
+  gemm_tr_body<256, 128, 4, 2, true, false, RBI, UPD>(g, rd, tr_blocks, u);
 }
 
 // ---- DGRAD with a row-major weight tile and transpose reads -------------------
@@ -2099,6 +2138,71 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd0, void* workspace, size_t ws
                        gd);
     hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true, false, 192>), dim3(tw + extra), dim3(512), 0, st, gw,
                        gd, tw);
+  }
+  return launch_status(what);
+}
+
+// gemm_dgrad_wgrad_vhat_launch's products with the finalize and the update
+// carried by the WGRAD launch (wgrad_update_kernel).  -1 when the shapes do not
+// take that launch, when the grid (one workgroup per CU) would not be resident
+// at once, or when it has too few workgroups for the finalize's rows and columns.
+template <int RBI, int UPD>
+static bool wgrad_update_resident(int grid) {
+  constexpr int kMaxDev = 64;
+  static int cap[kMaxDev];   // resident workgroups per device, 0 = not yet known
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
+  if (cap[dev] == 0) {
+    int cus = 0, per = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void*)wgrad_update_kernel<RBI, UPD>, 512, 0) !=
+            hipSuccess)
+      return false;
+    cap[dev] = cus * per > 0 ? cus * per : -1;
+  }
+  return grid <= cap[dev];
+}
+
+int gemm_dgrad_wgrad_update_launch(const GemmArgs& gd0, void* workspace, size_t ws_bytes, const GemmArgs& gw0,
+                                   const WgradUpd& u0, int upd, hipStream_t st, const char* what) {
+  if (upd != 1 && upd != 2) return -1;
+  if (!eligible(MODE_DGRAD, gd0) || !eligible(MODE_WGRAD, gw0) || !tr_eligible(gw0)) return -1;
+  const size_t room = (workspace && ws_bytes > kSplitkCounterBytes) ? ws_bytes - kSplitkCounterBytes : 0;
+  const FastPlan pd = plan_mode(MODE_DGRAD, gd0.I, gd0.J, gd0.R, room);
+  const FastPlan pw = plan_mode(MODE_WGRAD, gw0.I, gw0.J, gw0.R, room);
+  if ((pd.shape != 0 && pd.shape != 2) || pd.splits < 2 || pw.shape != 0 || pw.splits != 1) return -1;
+  const int tw = pw.ti * pw.tj;
+  const int extra = kCUs - tw;
+  if (extra < 16) return -1;
+  if (cdiv(gw0.I, 256) + cdiv(gw0.J, 512) > tw + extra) return -1;
+  const bool r192 = pd.shape == 2;
+  const bool resident = r192 ? (upd == 2 ? wgrad_update_resident<192, 2>(tw + extra)
+                                         : wgrad_update_resident<192, 1>(tw + extra))
+                             : (upd == 2 ? wgrad_update_resident<256, 2>(tw + extra)
+                                         : wgrad_update_resident<256, 1>(tw + extra));
+  if (!resident) return -1;
+  GemmArgs gd = gd0;
+  gd.splits = pd.splits;
+  gd.r_split = pd.r_split;
+  gd.tiles_i = pd.ti;
+  gd.tiles_j = pd.tj;
+  gd.part = (float*)((char*)workspace + kSplitkCounterBytes);
+  GemmArgs gw = gw0;
+  gw.splits = 1;
+  gw.r_split = pw.r_split;
+  gw.tiles_i = pw.ti;
+  gw.tiles_j = pw.tj;
+  WgradUpd u = u0;
+  u.nbp = pw.tj;
+  const dim3 grid(tw + extra), block(512);
+  if (!r192) {
+    hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD, 256, 128>), dim3(pd.ti * pd.tj * pd.splits), block, 0, st, gd);
+    if (upd == 2) hipLaunchKernelGGL((wgrad_update_kernel<256, 2>), grid, block, 0, st, gw, gd, tw, u);
+    else hipLaunchKernelGGL((wgrad_update_kernel<256, 1>), grid, block, 0, st, gw, gd, tw, u);
+  } else {
+    hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD, 192, 128>), dim3(pd.ti * pd.tj * pd.splits), block, 0, st, gd);
+    if (upd == 2) hipLaunchKernelGGL((wgrad_update_kernel<192, 2>), grid, block, 0, st, gw, gd, tw, u);
+    else hipLaunchKernelGGL((wgrad_update_kernel<192, 1>), grid, block, 0, st, gw, gd, tw, u);
   }
   return launch_status(what);
 }

@@ -26,6 +26,9 @@ CONCORD_DEV float row_ror(float v) {
 // g2[x][y][v] = g^2 of this lane's values; row0 / col0 = first row / column of
 // the tile (multiples of 64).  Writes P_r[col0 / 64][row] (rows < N) and
 // P_c[row0 / 64][col] (columns < K); a tile that starts past N or K writes nothing.
+// COH: every partial is stored with a relaxed agent-scope atomic store, for a
+// reader in the same launch on another XCD.
+template <bool COH = false>
 CONCORD_DEV void vhat_tile_partials(const float (&g2)[4][4][4], int lane, int64_t row0, int64_t col0,
                                     int64_t N, int64_t K, float* __restrict__ pr,
                                     float* __restrict__ pc) {
@@ -43,7 +46,10 @@ CONCORD_DEV void vhat_tile_partials(const float (&g2)[4][4][4], int lane, int64_
     const float h = __fadd_rn(u, __shfl_xor(u, 16, 64));
     const float t = __fadd_rn(h, __shfl_xor(h, 32, 64));
     const int64_t n = row0 + 16 * x + p;
-    if (q == 0 && n < N) pr[(col0 / 64) * N + n] = t;
+    if (q == 0 && n < N) {
+      if (COH) __hip_atomic_store(pr + (col0 / 64) * N + n, t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      else pr[(col0 / 64) * N + n] = t;
+    }
   }
   // columns
   float cs[4][4];
@@ -63,7 +69,11 @@ CONCORD_DEV void vhat_tile_partials(const float (&g2)[4][4][4], int lane, int64_
 #pragma unroll
     for (int y = 0; y < 4; ++y) {
       const int64_t k = col0 + 16 * y + 4 * q;
-      if (k + 4 <= K && (K % 4) == 0) {
+      if (COH) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          if (k + v < K) __hip_atomic_store(dst + k + v, cs[y][v], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else if (k + 4 <= K && (K % 4) == 0) {
         *reinterpret_cast<float4*>(dst + k) = make_float4(cs[y][0], cs[y][1], cs[y][2], cs[y][3]);
       } else {
 #pragma unroll

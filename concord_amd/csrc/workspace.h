@@ -1,8 +1,12 @@
 // workspace.h -- layout of the caller-owned workspaces.
 //
 // Update-side workspace:
-// [0, 256)       counters: the v-hat "row blocks done" ticket; zero when the
-//                workspace is created and zero again after every call.
+// [0, 256)       counters: the v-hat "row blocks done" ticket (byte 0), the
+//                grid barrier's arrivals (byte 64) and exits (byte 128) of
+//                the WGRAD launch that carries the update; zero when the
+//                workspace is created and zero again after every call.  Its
+//                fault flag (byte 192) stays set until the host reads it
+//                (concord_wgrad_update_fault).
 // [256, total)   scratch shared by the entry points (they run in stream order):
 //                v-hat partials, rebalance decisions, bias-gradient partials.
 //                No entry point needs its contents to survive between calls.
@@ -18,6 +22,7 @@ constexpr int kGemmMaxSplits = 16;
 struct Workspace {
   size_t vhat_ticket, scratch, total;
 };
+constexpr size_t kGridBarrierOffset = 64, kGridExitOffset = 128, kGridFaultOffset = 192;
 
 // v-hat scratch (floats, each region a multiple of 64 so the next stays
 // 256-byte aligned): row partials per 64-column tile, column partials per

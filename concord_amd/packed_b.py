@@ -56,6 +56,9 @@ _USE_FIXED_COH = True
 _GATE_GAIN = 1.0
 _COH_WEIGHTED_V = False
 _RATIO_COH = False
+# the v-hat finalize and the adamw update carried by the backward's WGRAD
+# launch (concord_dgrad_wgrad_update) instead of launches of their own
+_FUSED_UPDATE = False
 _RATIO_CHASE_FLOOR = 0.9
 _RATIO_LEAK_FLOOR = 0.999
 _PROTO_SEMANTICS = False
@@ -84,6 +87,15 @@ def set_coh_weighted_v(enabled):
 def set_ratio_coh(enabled):
     global _RATIO_COH
     _RATIO_COH = bool(enabled)
+
+
+def set_fused_update(enabled):
+    """True: the fused-forward layer's backward with the v-hat drive runs the
+    v-hat finalize and the adamw update inside its WGRAD launch when the
+    update's flags allow it (concord_dgrad_wgrad_update); False: launches of
+    their own.  The results are the same either way."""
+    global _FUSED_UPDATE
+    _FUSED_UPDATE = bool(enabled)
 
 
 def set_ratio_coh_floors(chase, leak):
@@ -330,6 +342,32 @@ def _adamw_flags(mass_preserve, apply_chase, track_rebalance, gf_trust_delta_sq,
     return f
 
 
+def _adamw_setup(dev, lr, mantissa_bias, alpha, beta1, weight_decay, eps, step_cap, v_scale, precond_p,
+                 gf_consol, drift_cancel_C, alpha_v_fast, wd_sv, wd_sf, mass_preserve, apply_chase,
+                 track_rebalance, gf_trust_delta_sq, coh_pre, emit, salt_prebumped, drive_muon):
+    """(flags, UpdateParams, DeviceScalars) of the adamw update: the packed
+    update's hyperparameters (concord/packed_b.py:863-951) and the device
+    scalars it reads (lr, eps, floors, salt counter)."""
+    flags = _adamw_flags(mass_preserve, apply_chase, track_rebalance, gf_trust_delta_sq,
+                         gf_consol, coh_pre, emit)
+    if salt_prebumped:
+        flags |= C.SALT_PREBUMPED
+    if drive_muon:
+        flags |= C.MUON
+    lr_t = _ensure_lr_tensor(lr, dev)
+    eps_t = _ensure_eps_tensor(eps, dev)
+    cf, lf = _ensure_floor_tensors(dev)
+    P = C.UpdateParams(alpha=alpha, beta1=beta1, weight_decay=weight_decay, step_cap=step_cap,
+                       v_scale=v_scale, precond_p=precond_p, gf_consol=gf_consol,
+                       drift_cancel_C=drift_cancel_C, alpha_v_fast=alpha_v_fast, wd_sv=wd_sv,
+                       wd_sf=wd_sf, gf_trust_delta_sq=gf_trust_delta_sq, gate_gain=_GATE_GAIN,
+                       mantissa_bias=int(mantissa_bias))
+    S = C.DeviceScalars(lr_t.data_ptr(), eps_t.data_ptr(), cf.data_ptr(), lf.data_ptr(),
+                        _v_bc_buf(dev).data_ptr(), _get_step_counter(dev).data_ptr(),
+                        _get_consolidate_flag(dev).data_ptr())
+    return flags, P, S
+
+
 def apply_packed_adamw(packed_w, grad_W, weight_buf, row_exp, col_exp, row_max, col_max,
                        lr, mantissa_bias=15, alpha=0.1, beta1=0.0, weight_decay=0.0, eps=1.0,
                        step_cap=10.0, v_scale=1.0, precond_p=0.5, gf_consol=0.0,
@@ -352,27 +390,14 @@ def apply_packed_adamw(packed_w, grad_W, weight_buf, row_exp, col_exp, row_max, 
     if use_vhat:
         assert v_row is not None and v_col is not None and sum_v_inv is not None, \
             "gf_trust/gf_consol/coh_pre/ratio_coh require v_row, v_col, sum_v_inv"
-    flags = _adamw_flags(mass_preserve, apply_chase, track_rebalance, gf_trust_delta_sq,
-                         gf_consol, coh_pre, weight_buf is not None)
-    if salt_prebumped:
-        flags |= C.SALT_PREBUMPED
-    if drive_muon:
-        flags |= C.MUON
     if weight_buf is not None:
         assert weight_buf.dtype == torch.bfloat16 and tuple(weight_buf.shape) == (N, K)
     if coh_pre is not None:
         assert coh_pre.dtype == torch.float32 and tuple(coh_pre.shape) == (N, K)
-    lr_t = _ensure_lr_tensor(lr, dev)
-    eps_t = _ensure_eps_tensor(eps, dev)
-    cf, lf = _ensure_floor_tensors(dev)
-    P = C.UpdateParams(alpha=alpha, beta1=beta1, weight_decay=weight_decay, step_cap=step_cap,
-                       v_scale=v_scale, precond_p=precond_p, gf_consol=gf_consol,
-                       drift_cancel_C=drift_cancel_C, alpha_v_fast=alpha_v_fast, wd_sv=wd_sv,
-                       wd_sf=wd_sf, gf_trust_delta_sq=gf_trust_delta_sq, gate_gain=_GATE_GAIN,
-                       mantissa_bias=int(mantissa_bias))
-    S = C.DeviceScalars(lr_t.data_ptr(), eps_t.data_ptr(), cf.data_ptr(), lf.data_ptr(),
-                        _v_bc_buf(dev).data_ptr(), _get_step_counter(dev).data_ptr(),
-                        _get_consolidate_flag(dev).data_ptr())
+    flags, P, S = _adamw_setup(dev, lr, mantissa_bias, alpha, beta1, weight_decay, eps, step_cap, v_scale,
+                               precond_p, gf_consol, drift_cancel_C, alpha_v_fast, wd_sv, wd_sf, mass_preserve,
+                               apply_chase, track_rebalance, gf_trust_delta_sq, coh_pre,
+                               weight_buf is not None, salt_prebumped, drive_muon)
     C.check(C.lib().concord_apply_adamw(
         C.ptr(packed_w), packed_w.stride(0), C.ptr(grad_W), grad_W.stride(0),
         C.ptr(weight_buf), weight_buf.stride(0) if weight_buf is not None else K,
@@ -548,6 +573,61 @@ def _dgrad_wgrad_vhat(dy, x2, packed_w, row_exp, col_exp, mantissa_bias, v_row, 
         C.ptr(col_max), C.ptr(salt_counter), C.ptr(gb), C.ptr(ws), ws.numel(), C.ptr(gws), gws.numel(),
         C.stream_of(dy.device)), "dgrad_wgrad_vhat")
     return dx, gw, gb
+
+
+# whether the last _dgrad_wgrad_update call took the combined launch
+_LAST_FUSED = [0]
+
+
+def _dgrad_wgrad_update(ctx, dy, x2):
+    """_dgrad_wgrad_vhat followed by the adamw update of _packed_step, in one
+    entry (concord_dgrad_wgrad_update, same results): for the update's two
+    fast flag sets the v-hat finalize and the update run in the WGRAD launch,
+    from its tiles' accumulators (concord/packed_b.py:1263-1327, 1338-1340).
+    Returns (grad_x, grad_bias or None)."""
+    M, N = dy.shape
+    K = x2.shape[1]
+    dev = dy.device
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    gw = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    gb = torch.empty(N, dtype=torch.bfloat16, device=dev) if ctx.has_bias else None
+    gws = _gemm_workspace(dev, M, N, K)
+    ws = _workspace(dev, N, K, M if ctx.has_bias else 0)
+    dcc = ctx.drift_cancel_C
+    if dcc is None:
+        dcc = compute_drift_cancel_C(ctx.alpha, ctx.alpha_v_fast, mass_preserve=ctx.mass_preserve)
+    flags, P, S = _adamw_setup(dev, ctx.lr, ctx.mantissa_bias, ctx.alpha, ctx.beta1, ctx.weight_decay, ctx.eps,
+                               ctx.step_cap, ctx.v_scale, ctx.precond_p, ctx.gf_consol, dcc, ctx.alpha_v_fast,
+                               ctx.wd_sv, ctx.wd_sf, ctx.mass_preserve, ctx.apply_chase, ctx.track_rebalance,
+                               ctx.gf_trust_delta_sq, ctx.coh_pre, False, True, False)
+    rm = ctx.row_max_buf if ctx.track_rebalance else None
+    cm = ctx.col_max_buf if ctx.track_rebalance else None
+    cp = ctx.coh_pre
+    capture = _DEBUG_CAPTURE is not None
+    fused = ctypes.c_int(0)
+    C.check(C.lib().concord_dgrad_wgrad_update(
+        C.ptr(dy), dy.stride(0), C.ptr(ctx.packed_w), ctx.packed_w.stride(0), C.ptr(ctx.row_exp),
+        C.ptr(ctx.col_exp), C.ptr(dx), dx.stride(0), C.ptr(x2), x2.stride(0), C.ptr(gw), gw.stride(0),
+        int(capture), M, N, K, float(ctx.adafactor_beta2), C.ptr(ctx.v_row), C.ptr(ctx.v_col),
+        C.ptr(ctx.sum_v_inv), C.ptr(rm), C.ptr(cm), C.ptr(cp), cp.stride(0) if cp is not None else K, C.ptr(gb),
+        ctypes.byref(P), ctypes.byref(S), flags, C.ptr(ws), ws.numel(), C.ptr(gws), gws.numel(),
+        ctypes.byref(fused), C.stream_of(dev)), "dgrad_wgrad_update")
+    _LAST_FUSED[0] = fused.value
+    if capture:
+        _DEBUG_CAPTURE.append(gw.clone())
+    return dx, gb
+
+
+def wgrad_update_faults(device):
+    """Reads and clears the fault flag of the combined backward launch on this
+    device's workspace (synchronises): True when a launch since the last read
+    gave up a grid-barrier wait and skipped its writes."""
+    dev = torch.device(device)
+    ws = _workspace(dev, 1, 1, 0)
+    f = ctypes.c_int(0)
+    C.check(C.lib().concord_wgrad_update_fault(C.ptr(ws), ws.numel(), ctypes.byref(f), C.stream_of(dev)),
+            "wgrad_update_fault")
+    return f.value != 0
 
 
 _MUON_WORKSPACES = {}
@@ -726,10 +806,15 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
             # dgrad on the pre-update weight (1263), wgrad (1269-1277), watermark
             # zeroing (1281-1283), v-hat EMA (1288-1303), salt + 1 (910-911) and
             # grad_y.sum(0) (1338-1340) in one entry
-            grad_x, grad_W, grad_bias = _dgrad_wgrad_vhat(
-                dy, x2, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias, ctx.v_row, ctx.v_col,
-                ctx.sum_v_inv, ctx.adafactor_beta2, ctx.row_max_buf if ctx.track_rebalance else None,
-                ctx.col_max_buf if ctx.track_rebalance else None, salt, with_bias=ctx.has_bias)
+            if _FUSED_UPDATE and ctx.optimizer_kind == 'adamw':
+                # ... and the update (1281-1327) in the same entry
+                grad_x, grad_bias = _dgrad_wgrad_update(ctx, dy, x2)
+                grad_W = None
+            else:
+                grad_x, grad_W, grad_bias = _dgrad_wgrad_vhat(
+                    dy, x2, ctx.packed_w, ctx.row_exp, ctx.col_exp, ctx.mantissa_bias, ctx.v_row, ctx.v_col,
+                    ctx.sum_v_inv, ctx.adafactor_beta2, ctx.row_max_buf if ctx.track_rebalance else None,
+                    ctx.col_max_buf if ctx.track_rebalance else None, salt, with_bias=ctx.has_bias)
             grad_x = grad_x.reshape(*ctx.lead, K)
             prebumped = True
         else:
@@ -751,7 +836,8 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
                 prebumped = True
             else:
                 grad_W = _wgrad(dy, x2)
-        _packed_step(ctx, grad_W, prebumped, muon)
+        if grad_W is not None:
+            _packed_step(ctx, grad_W, prebumped, muon)
         if ctx.has_bias and grad_bias is None:
             grad_bias = _bias_grad(dy)
         return (grad_x, None, None, None, grad_bias,

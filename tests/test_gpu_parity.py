@@ -1463,6 +1463,126 @@ def test_dgrad_wgrad_vhat_matches_separate_calls(M, N, K):
     assert (outs[0][6] == 0).all() and outs[0][8][0] == 6
 
 
+def _update_backward(pb, combined, dy, x, st, winner, lr):
+    """One backward step of the fused-forward layer with the adamw update:
+    the combined entry (combined = True; returns whether its launch carried
+    the update) or the v-hat entry then the separate update."""
+    import ctypes
+    from concord_amd import _lib as C
+    M, N = dy.shape
+    K = x.shape[1]
+    pk, red, ced, vr, vc, svi, rm, cm, cp = st
+    dcc = pb.compute_drift_cancel_C(0.1, 0.001, mass_preserve=True)
+    gf = 50.0 if winner else 0.0
+    if not combined:
+        dx, gw, gb = pb._dgrad_wgrad_vhat(dy, x, pk, red, ced, 15, vr, vc, svi, 0.999, rm, cm,
+                                          pb._get_step_counter(DEV), with_bias=True)
+        pb.apply_packed_adamw(pk, gw, None, red, ced, rm, cm, lr=lr, eps=1e-10, v_scale=0.0, gf_consol=gf,
+                              drift_cancel_C=dcc, mass_preserve=True, v_row=vr, v_col=vc, sum_v_inv=svi,
+                              gf_trust_delta_sq=1.0, coh_pre=cp, salt_prebumped=True)
+        return dx, gw, gb, None
+    flags, P, S = pb._adamw_setup(DEV, lr, 15, 0.1, 0.0, 0.0, 1e-10, 10.0, 0.0, 0.5, gf, dcc, 0.001, 0.0, 0.0,
+                                  True, True, True, 1.0, cp, False, True, False)
+    dx = torch.empty((M, K), dtype=torch.bfloat16, device=DEV)
+    gw = torch.empty((N, K), dtype=torch.bfloat16, device=DEV)
+    gb = torch.empty(N, dtype=torch.bfloat16, device=DEV)
+    gws = pb._gemm_workspace(DEV, M, N, K)
+    ws = pb._workspace(DEV, N, K, M)
+    fused = ctypes.c_int(-1)
+    C.check(C.lib().concord_dgrad_wgrad_update(
+        C.ptr(dy), dy.stride(0), C.ptr(pk), pk.stride(0), C.ptr(red), C.ptr(ced), C.ptr(dx), dx.stride(0),
+        C.ptr(x), x.stride(0), C.ptr(gw), gw.stride(0), 1, M, N, K, 0.999, C.ptr(vr), C.ptr(vc), C.ptr(svi),
+        C.ptr(rm), C.ptr(cm), C.ptr(cp), cp.stride(0) if cp is not None else K, C.ptr(gb), ctypes.byref(P),
+        ctypes.byref(S), flags, C.ptr(ws), ws.numel(), C.ptr(gws), gws.numel(), ctypes.byref(fused),
+        C.stream_of(DEV)), "dgrad_wgrad_update")
+    return dx, gw, gb, fused.value
+
+
+@pytest.mark.parametrize("winner", [True, False])
+@pytest.mark.parametrize("M,N,K", [(2048, 5120, 1280), (2048, 1280, 1280), (4096, 1280, 1280), (1024, 2560, 640),
+                                   (300, 384, 256)])
+def test_dgrad_wgrad_update_matches_two_pass(M, N, K, winner):
+    """concord_dgrad_wgrad_update against concord_dgrad_wgrad_vhat followed by
+    concord_apply_adamw, two steps in a row from the same state: dx, the
+    grad_W copy, the bias gradient, v_row, v_col, 1 / sum v_row, the
+    watermarks, the salt, the packed words and coh_pre all bit-identical.
+    At the north-star shape the combined launch must carry the update, and
+    its grid barriers must not report a fault."""
+    from concord_amd import packed_b as pb
+    rng = np.random.default_rng(M + N + K + winner)
+    packed, re, ce = rand_state(rng, N, K, exp=(-8, 7), col=(-3, 3))
+    x = torch.randn(M, K, device=DEV).to(torch.bfloat16)
+    dys = [(torch.randn(M, N, device=DEV) * 1e-2).to(torch.bfloat16) for _ in range(2)]
+    vr0 = dev((rng.random(N) * 1e-3 + 1e-7).astype(np.float32))
+    vc0 = dev((rng.random(K) * 1e-3 + 1e-7).astype(np.float32))
+    cp0 = None if winner else dev(rng.random((N, K)).astype(np.float32))
+    pb.set_ratio_coh(winner)
+    pb.set_ratio_coh_floors(0.9, 0.999)
+    try:
+        runs = []
+        for combined in (True, False):
+            pb._get_step_counter(DEV).fill_(11)
+            st = [dev(packed.copy()), dev(re), dev(ce), vr0.clone(), vc0.clone(), torch.ones(1, device=DEV),
+                  torch.full((N,), 77, dtype=torch.int32, device=DEV),
+                  torch.full((K,), 88, dtype=torch.int32, device=DEV),
+                  None if winner else cp0.clone()]
+            out = []
+            for dy in dys:
+                dx, gw, gb, fused = _update_backward(pb, combined, dy, x, st, winner, 5e-4)
+                sync()
+                out.append(([host(t) for t in (dx, gw, gb)] + [host(t) for t in st if t is not None] +
+                            [host(pb._get_step_counter(DEV))], fused))
+            runs.append(out)
+        for (a, fused), (b, _) in zip(*runs):
+            if (M, N, K) == (2048, 5120, 1280):
+                assert fused == 1
+            for u, v in zip(a, b):
+                np.testing.assert_array_equal(u, v)
+        assert not pb.wgrad_update_faults(DEV)
+    finally:
+        pb.set_ratio_coh(False)
+
+
+def test_layer_fused_update_matches_separate():
+    """The module's backward through the combined entry (set_fused_update)
+    against the separate launches: 3 winner-flag steps of the north-star
+    layer (1280 -> 5120, 2048 tokens, bias) with rebalance, same words,
+    exponents, v-hat state, grad_x and bias gradient."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    torch.manual_seed(4)
+    W0 = torch.randn(5120, 1280) * 0.02
+    xs = [torch.randn(2048, 1280, device=DEV) for _ in range(3)]
+    gys = [torch.randn(2048, 5120, device=DEV) * 1e-2 for _ in range(3)]
+    pb.set_ratio_coh(True)
+    pb.set_ratio_coh_floors(0.9, 0.999)
+    res = []
+    try:
+        for fused in (True, False):
+            pb.set_fused_update(fused)
+            pb._get_step_counter(DEV).fill_(3)
+            layer = ca.ConcordLinearPackedB(1280, 5120, bias=True, device=DEV, lr=5e-4)
+            layer.disable_cohpre()
+            layer.gf_consol = 50.0
+            layer.load_weights(W0)
+            out = []
+            for x, gy in zip(xs, gys):
+                xd = x.clone().requires_grad_(True)
+                layer.bias.grad = None
+                layer(xd).backward(gy)
+                layer.rebalance()
+                sync()
+                out += [host(xd.grad.to(torch.bfloat16)), host(layer.bias.grad.to(torch.bfloat16))]
+            out += [host(t) for t in (layer.packed_w, layer.row_exp, layer.col_exp, layer.v_row, layer.v_col)]
+            res.append(out)
+        for a, b in zip(*res):
+            np.testing.assert_array_equal(a, b)
+        assert not pb.wgrad_update_faults(DEV)
+    finally:
+        pb.set_fused_update(False)
+        pb.set_ratio_coh(False)
+
+
 @pytest.mark.parametrize("N,K", [(320, 192), (5120, 1280)])
 def test_empty_batch_wgrad_entries(oracle, N, K):
     """M = 0 tokens: the weight gradient is the sum over no tokens, so the
