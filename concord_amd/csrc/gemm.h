@@ -197,6 +197,10 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd, void* workspace, size_t ws_
                                  hipStream_t st, const char* what, int* tiles_j);
 // tiles along J of the WGRAD launch above (the bias partials' row count)
 int64_t gemm_wgrad_vhat_tiles_j(int64_t J);
+// the other pairing: a split WGRAD with v-hat partials first, then the unsplit
+// dgrad carrying its split-K reduction; -1 when the plans are not of that form
+int gemm_wgrad_split_dgrad_launch(const GemmArgs& gd, const GemmArgs& gw, void* workspace, size_t ws_bytes,
+                                  hipStream_t st, const char* what, int* bias_rows);
 // the products of gemm_dgrad_wgrad_vhat_launch with the v-hat finalize and the
 // packed update carried by the WGRAD launch (wgrad_update.h); upd = 1 bare,
 // 2 winner (update_fast_path).  -1 when that launch does not apply.

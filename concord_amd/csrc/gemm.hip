@@ -612,6 +612,9 @@ static int wgrad_vhat_impl(const GemmArgs* gd, const uint16_t* dy, int64_t ld_dy
   if (gd && gd->I > 0 && gd->J > 0) {
     rc = gemm_dgrad_wgrad_vhat_launch(*gd, gemm_workspace, gemm_workspace ? gemm_workspace_bytes : 0, g, st,
                                       what, &tiles_j);
+    if (rc == -1)
+      rc = gemm_wgrad_split_dgrad_launch(*gd, g, gemm_workspace, gemm_workspace ? gemm_workspace_bytes : 0, st,
+                                         what, &tiles_j);
     if (rc == -1) {   // the products in turn
       rc = launch_gemm<MODE_DGRAD>(*gd, gemm_workspace, gemm_workspace_bytes, st, what);
       if (rc != CONCORD_OK) return rc;

@@ -676,76 +676,98 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs g) {
 // partial rows over the splits, in split order, into the split-0 row, so the
 // finalize reads tiles_j rows as for an unsplit launch.
 template <int BI, int BJ, int WI, int WJ>
-__global__ __launch_bounds__(256) void splitk_reduce_vh_kernel(GemmArgs g) {
-  constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ, NI = WTI / 16, NJ = WTJ / 16;
+struct ReduceVh {
+  static constexpr int NAW = WI * WJ, WTI = BI / WI, WTJ = BJ / WJ, NI = WTI / 16, NJ = WTJ / 16;
   static_assert(NI == 4 && NJ == 4, "v-hat partials take 64 x 64 wave tiles");
-  __shared__ float s_g2[NI][NJ][4][64];   // [x][y][e][lane]: the squares, for wave 0's v-hat partials
-  const int lane = threadIdx.x & 63, x = threadIdx.x >> 6;   // wave x takes row block x of the tile
-  // one block per accumulator wave tile; row-major tile index
-  const int tile = (int)(blockIdx.x / NAW), aw = (int)(blockIdx.x % NAW);
-  const int bi = tile / g.tiles_j, bj = tile % g.tiles_j;
-  const int64_t row0 = (int64_t)bi * BI + (aw / WJ) * WTI, col0 = (int64_t)bj * BJ + (aw % WJ) * WTJ;
-  const int64_t PT = (int64_t)NAW * NI * NJ * 256;
-  const float* base = g.part + (int64_t)tile * g.splits * PT + (int64_t)aw * NI * NJ * 256 + lane * 4;
-  {
-    // the row of 4 blocks, eight splits' partials loaded before any of them
-    // is summed (one memory round trip per eight splits), summed in order
-    constexpr int CH = 8;
-    static_assert(kGemmMaxSplits <= 2 * CH, "two chunks of splits");
-    f32x4 sums[NJ];
+  static constexpr int LDS_FLOATS = NI * NJ * 4 * 64;   // [x][y][e][lane]: the squares, for wave 0
+  // blocks of one launch: one per accumulator wave tile
+  static int blocks(const GemmArgs& g) { return g.tiles_i * g.tiles_j * NAW; }
+  // part 1 of block `blk` on threads tid in [0, 256): the split sums, the bf16
+  // tile, the squares into s_g2, the bias fold
+  static CONCORD_DEV void part1(const GemmArgs& g, int blk, int tid, float* s_g2) {
+    const int lane = tid & 63, x = tid >> 6;   // wave x takes row block x of the tile
+    // row-major tile index
+    const int tile = blk / NAW, aw = blk % NAW;
+    const int bi = tile / g.tiles_j, bj = tile % g.tiles_j;
+    const int64_t row0 = (int64_t)bi * BI + (aw / WJ) * WTI, col0 = (int64_t)bj * BJ + (aw % WJ) * WTJ;
+    const int64_t PT = (int64_t)NAW * NI * NJ * 256;
+    const float* base = g.part + (int64_t)tile * g.splits * PT + (int64_t)aw * NI * NJ * 256 + lane * 4;
+    {
+      // the row of 4 blocks, eight splits' partials loaded before any of them
+      // is summed (one memory round trip per eight splits), summed in order
+      constexpr int CH = 8;
+      static_assert(kGemmMaxSplits <= 2 * CH, "two chunks of splits");
+      f32x4 sums[NJ];
 #pragma unroll
-    for (int c0 = 0; c0 < 2 * CH; c0 += CH) {
-      if (c0 >= g.splits) break;
-      f32x4 part[NJ][CH];
+      for (int c0 = 0; c0 < 2 * CH; c0 += CH) {
+        if (c0 >= g.splits) break;
+        f32x4 part[NJ][CH];
+#pragma unroll
+        for (int y = 0; y < NJ; ++y)
+#pragma unroll
+          for (int s2 = 0; s2 < CH; ++s2)
+            part[y][s2] = c0 + s2 < g.splits
+                              ? *reinterpret_cast<const f32x4*>(base + (x * NJ + y) * 256 + (c0 + s2) * PT)
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int y = 0; y < NJ; ++y) {
+          if (c0 == 0) sums[y] = part[y][0];
+#pragma unroll
+          for (int s2 = (c0 == 0 ? 1 : 0); s2 < CH; ++s2)
+            if (c0 + s2 < g.splits)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) sums[y][e] = __fadd_rn(sums[y][e], part[y][s2][e]);
+        }
+      }
+#pragma unroll
+      for (int y = 0; y < NJ; ++y) {
+        const f32x4 sum = sums[y];
+        const uint32_t lo = pack_bf16x2(sum[0], sum[1]), hi = pack_bf16x2(sum[2], sum[3]);
+        const float v[4] = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xFFFF0000u),
+                            __uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s_g2[((x * NJ + y) * 4 + e) * 64 + lane] = __fmul_rn(v[e], v[e]);
+        const int64_t i = row0 + x * 16 + (lane & 15), j = col0 + y * 16 + 4 * (lane >> 4);
+        if (i < g.I && j < g.J) *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = make_uint2(lo, hi);
+      }
+    }
+    if (x == 1 && g.bpart && aw % WJ == 0) {
+      const int64_t i = row0 + lane;
+      if (i < g.I) {
+        float* b = g.bpart + (int64_t)bj * g.I + i;
+        const int64_t rs = (int64_t)g.tiles_j * g.I;   // one split's rows
+        float sb = b[0];
+        for (int s2 = 1; s2 < g.splits; ++s2) sb = __fadd_rn(sb, b[s2 * rs]);
+        b[0] = sb;
+      }
+    }
+  }
+  // part 2 (after a barrier over part 1's threads): wave 0 forms the tile's
+  // v-hat partials from s_g2
+  static CONCORD_DEV void part2(const GemmArgs& g, int blk, int tid, const float* s_g2) {
+    if (tid >= 64) return;
+    const int lane = tid;
+    const int tile = blk / NAW, aw = blk % NAW;
+    const int bi = tile / g.tiles_j, bj = tile % g.tiles_j;
+    const int64_t row0 = (int64_t)bi * BI + (aw / WJ) * WTI, col0 = (int64_t)bj * BJ + (aw % WJ) * WTJ;
+    float g2[4][4][4];
+#pragma unroll
+    for (int xx = 0; xx < NI; ++xx)
 #pragma unroll
       for (int y = 0; y < NJ; ++y)
 #pragma unroll
-        for (int s2 = 0; s2 < CH; ++s2)
-          part[y][s2] = c0 + s2 < g.splits
-                            ? *reinterpret_cast<const f32x4*>(base + (x * NJ + y) * 256 + (c0 + s2) * PT)
-                            : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int y = 0; y < NJ; ++y) {
-        if (c0 == 0) sums[y] = part[y][0];
-#pragma unroll
-        for (int s2 = (c0 == 0 ? 1 : 0); s2 < CH; ++s2)
-          if (c0 + s2 < g.splits)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) sums[y][e] = __fadd_rn(sums[y][e], part[y][s2][e]);
-      }
-    }
-#pragma unroll
-    for (int y = 0; y < NJ; ++y) {
-      const f32x4 sum = sums[y];
-      const uint32_t lo = pack_bf16x2(sum[0], sum[1]), hi = pack_bf16x2(sum[2], sum[3]);
-      const float v[4] = {__uint_as_float(lo << 16), __uint_as_float(lo & 0xFFFF0000u),
-                          __uint_as_float(hi << 16), __uint_as_float(hi & 0xFFFF0000u)};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) s_g2[x][y][e][lane] = __fmul_rn(v[e], v[e]);
-      const int64_t i = row0 + x * 16 + (lane & 15), j = col0 + y * 16 + 4 * (lane >> 4);
-      if (i < g.I && j < g.J) *reinterpret_cast<uint2*>(g.c + i * g.ldc + j) = make_uint2(lo, hi);
-    }
+        for (int e = 0; e < 4; ++e) g2[xx][y][e] = s_g2[((xx * NJ + y) * 4 + e) * 64 + lane];
+    vhat_tile_partials(g2, lane, row0, col0, g.I, g.J, g.vh_pr, g.vh_pc);
   }
-  if (x == 1 && g.bpart && aw % WJ == 0) {
-    const int64_t i = row0 + lane;
-    if (i < g.I) {
-      float* b = g.bpart + (int64_t)bj * g.I + i;
-      const int64_t rs = (int64_t)g.tiles_j * g.I;   // one split's rows
-      float sb = b[0];
-      for (int s2 = 1; s2 < g.splits; ++s2) sb = __fadd_rn(sb, b[s2 * rs]);
-      b[0] = sb;
-    }
-  }
+};
+
+template <int BI, int BJ, int WI, int WJ>
+__global__ __launch_bounds__(256) void splitk_reduce_vh_kernel(GemmArgs g) {
+  typedef ReduceVh<BI, BJ, WI, WJ> RV;
+  __shared__ float s_g2[RV::LDS_FLOATS];
+  RV::part1(g, (int)blockIdx.x, (int)threadIdx.x, s_g2);
   __syncthreads();
-  if (x != 0) return;
-  float g2[4][4][4];
-#pragma unroll
-  for (int xx = 0; xx < NI; ++xx)
-#pragma unroll
-    for (int y = 0; y < NJ; ++y)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) g2[xx][y][e] = s_g2[xx][y][e][lane];
-  vhat_tile_partials(g2, lane, row0, col0, g.I, g.J, g.vh_pr, g.vh_pc);
+  RV::part2(g, (int)blockIdx.x, (int)threadIdx.x, s_g2);
 }
 
 // MFMAs of one TR-deep stage for a wave tile of NI x NJ 16x16 blocks whose
@@ -1804,8 +1826,12 @@ CONCORD_DEV void stage_mfma_swz_tr(f32x4 (&acc)[NI][NJ], const uint16_t* la, con
 // two stages ahead, decode them and write the row-major B tile.
 // CONV (MODE_DGRAD_BF16): the conv dgrad, dy gathered by RowsDmaConv and the
 // weight rows (n, tap) by TrRowsB's conv stage offsets.
-template <int MODE, int BI, int BJ, int CONV = 0>
-__global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
+// CARRY (MODE_DGRAD only): workgroups from dg_blocks on run the split-K
+// reduction with v-hat partials (splitk_reduce_vh_kernel's blocks, two per
+// workgroup) of the WGRAD launch `rw` issued just before on the stream, on
+// the CUs the dgrad grid leaves idle.
+template <int MODE, int BI, int BJ, int CONV, bool CARRY>
+CONCORD_DEV void gemm_dgt_body(const GemmArgs& g, const GemmArgs& rw, int dg_blocks) {
   constexpr int NP = 256;
   constexpr int WTI = BI / 2, WTJ = BJ / 2;
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
@@ -1813,6 +1839,24 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
   typedef typename std::conditional<CONV != 0, RowsDmaConv<BI, 4, true, CONV == 1>, RowsDma<BI, 4>>::type AD;
   __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
   __shared__ __attribute__((aligned(1024))) char lds_b[2][BL::LBYTES];
+  if constexpr (CARRY) {
+    typedef ReduceVh<256, 128, 4, 2> RV;
+    static_assert(sizeof(lds_a) >= 2 * RV::LDS_FLOATS * sizeof(float), "two reduction blocks fit");
+    if ((int)blockIdx.x >= dg_blocks) {
+      const int nblk = rw.tiles_i * rw.tiles_j * RV::NAW;
+      const int half = threadIdx.x >> 8, tid = threadIdx.x & 255;
+      float* s_g2 = reinterpret_cast<float*>(&lds_a[0][0]) + half * RV::LDS_FLOATS;
+      const int stride = 2 * ((int)gridDim.x - dg_blocks);
+      for (int b0 = 2 * ((int)blockIdx.x - dg_blocks); b0 < nblk; b0 += stride) {
+        const int blk = b0 + half;
+        if (blk < nblk) RV::part1(rw, blk, tid, s_g2);
+        __syncthreads();
+        if (blk < nblk) RV::part2(rw, blk, tid, s_g2);
+        __syncthreads();   // s_g2 is reused by the next pair
+      }
+      return;
+    }
+  }
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -1899,6 +1943,18 @@ __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
   static_assert(sizeof(lds_a) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the A tiles");
   epilogue<MODE, NI, NJ, BI, BJ, 4>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, slot, producer ? -1 : wave,
                                      t, 512, &lds_a[0][0]);
+}
+
+template <int MODE, int BI, int BJ, int CONV = 0>
+__global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
+  gemm_dgt_body<MODE, BI, BJ, CONV, false>(g, g, 0);
+}
+
+// the dgrad launch carrying the split WGRAD's v-hat reduction (rw): workgroups
+// [0, dg_blocks) compute dgrad tiles, the rest run reduction blocks
+template <int BI, int BJ>
+__global__ __launch_bounds__(512, 1) void gemm_dgt_carry_kernel(GemmArgs g, GemmArgs rw, int dg_blocks) {
+  gemm_dgt_body<MODE_DGRAD, BI, BJ, 0, true>(g, rw, dg_blocks);
 }
 
 // ---- planning -----------------------------------------------------------------
@@ -2102,6 +2158,43 @@ int gemm_wgrad_vhat_split_launch(const GemmArgs& g0, void* workspace, size_t ws_
   hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, false>), dim3(tiles * p.splits), dim3(512), 0, st, g,
                      GemmArgs{}, tiles * p.splits);
   hipLaunchKernelGGL((splitk_reduce_vh_kernel<256, 128, 4, 2>), dim3((unsigned)(tiles * 8)), dim3(256), 0, st, g);
+  return launch_status(what);
+}
+
+// A split WGRAD with v-hat partials and an unsplit dgrad: the WGRAD product
+// first, then the dgrad launch with extra workgroups that run the WGRAD's
+// split-K v-hat reduction (gemm_dgt_carry_kernel) on the CUs its tiles leave
+// idle, in place of splitk_reduce_vh_kernel after it.  Same products, plans
+// and bits as gemm_wgrad_vhat_split_launch and the dgrad launched alone.
+int gemm_wgrad_split_dgrad_launch(const GemmArgs& gd0, const GemmArgs& gw0, void* workspace, size_t ws_bytes,
+                                  hipStream_t st, const char* what, int* bias_rows) {
+  if (!eligible(MODE_DGRAD, gd0) || !eligible(MODE_WGRAD, gw0) || !tr_eligible(gw0) || !workspace) return -1;
+  const size_t room = ws_bytes > kSplitkCounterBytes ? ws_bytes - kSplitkCounterBytes : 0;
+  const FastPlan pd = plan_mode(MODE_DGRAD, gd0.I, gd0.J, gd0.R, room);
+  const FastPlan pw = plan_mode(MODE_WGRAD, gw0.I, gw0.J, gw0.R, room);
+  if ((pd.shape != 0 && pd.shape != 2) || pd.splits != 1 || pw.shape != 0 || pw.splits < 2) return -1;
+  const int td = pd.ti * pd.tj;
+  const int extra = kCUs - td;
+  if (extra < 16) return -1;   // the dgrad grid leaves too few CUs to carry the reduction
+  GemmArgs gw = gw0;
+  gw.splits = pw.splits;
+  gw.r_split = pw.r_split;
+  gw.tiles_i = pw.ti;
+  gw.tiles_j = pw.tj;
+  gw.part = (float*)((char*)workspace + kSplitkCounterBytes);
+  GemmArgs gd = gd0;
+  gd.splits = 1;
+  gd.r_split = pd.r_split;
+  gd.tiles_i = pd.ti;
+  gd.tiles_j = pd.tj;
+  *bias_rows = pw.tj;
+  const int tiles = pw.ti * pw.tj;
+  hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, false>), dim3(tiles * pw.splits), dim3(512), 0, st, gw,
+                     GemmArgs{}, tiles * pw.splits);
+  if (pd.shape == 0)
+    hipLaunchKernelGGL((gemm_dgt_carry_kernel<256, 128>), dim3(td + extra), dim3(512), 0, st, gd, gw, td);
+  else
+    hipLaunchKernelGGL((gemm_dgt_carry_kernel<192, 128>), dim3(td + extra), dim3(512), 0, st, gd, gw, td);
   return launch_status(what);
 }
 

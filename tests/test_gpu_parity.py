@@ -1431,11 +1431,14 @@ def test_layer_fast_gain_forward(oracle):
     assert rel_l2(host(y.float()).astype(np.float64), ref) < 1e-2
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 5120, 1280), (2048, 1280, 1280), (1024, 2560, 640), (300, 384, 256)])
+@pytest.mark.parametrize("M,N,K", [(2048, 5120, 1280), (2048, 1280, 1280), (4096, 1280, 1280), (1024, 2560, 640),
+                                   (300, 384, 256)])
 def test_dgrad_wgrad_vhat_matches_separate_calls(M, N, K):
-    """The combined backward entry (the dgrad's split-K reduction carried by
-    the WGRAD launch where the shapes allow) gives the same dx, grad_W, bias
-    gradient, v-hat state, zeroed watermarks and salt as the two calls."""
+    """The combined backward entry gives the same dx, grad_W, bias gradient,
+    v-hat state, zeroed watermarks and salt as the two calls.  Where the shapes
+    allow, one launch carries the other's split-K reduction: the WGRAD launch
+    the dgrad's (2048 x 5120 x 1280), or the unsplit dgrad launch the split
+    WGRAD's v-hat reduction (4096 x 1280 x 1280, config 4's attention layers)."""
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(M + N + K)
     packed, re, ce = rand_state(rng, N, K, exp=(-8, 7), col=(-3, 3))
