@@ -43,6 +43,9 @@ sys.path.insert(0, ROOT)
 N_OUT, K_IN, M_TOK = 5120, 1280, 2048
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBPS = 8000.0
+# VALU issue peak: 1024 SIMDs x 16 lanes per cycle at the 2.4 GHz peak engine
+# clock (a wave64 VALU instruction holds a 16-lane SIMD for 4 cycles)
+PEAK_VALU_TLANE_OPS = 1024 * 16 * 2.4e9 / 1e12
 UPDATE_BYTES_PER_PARAM = 10      # int32 read + int32 write + bf16 grad read
 DECODE_BYTES_PER_PARAM = 6       # int32 read + bf16 write
 
@@ -90,6 +93,23 @@ def _read_traffic():
             except ValueError:
                 pass
     return out
+
+
+def _read_valu_per_word():
+    """VALU lane-instructions per packed word of the update kernel, from the
+    committed PMC summary's line `valu_per_word apply_adamw X` (64 x
+    SQ_INSTS_VALU / words)."""
+    path = os.path.join(ROOT, "profiles", "pmc_sdxl_1280x5120.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.split()
+        if len(f) == 3 and f[0] == "valu_per_word" and f[1] == "apply_adamw":
+            try:
+                return float(f[2])
+            except ValueError:
+                return None
+    return None
 
 
 def _cpu_model():
@@ -888,6 +908,19 @@ def main():
         "apply_adamw": hbm_roof("apply_adamw", "apply_adamw_fast_kernel<ratio> (packed update, winner flags)",
                                 t_upd, UPDATE_BYTES_PER_PARAM * params),
     }
+    # the update is bound by VALU issue, not HBM: its fraction of the VALU
+    # peak from the committed lane-instructions per word (SQ_INSTS_VALU), with
+    # the HBM figures kept beside it
+    vpw = _read_valu_per_word()
+    upd_hbm = dict(roofs["apply_adamw"])
+    if vpw:
+        a_valu = params * vpw / (t_upd * 1e-3) / 1e12
+        roofs["apply_adamw"] = {
+            "bound": "valu", "kernel": upd_hbm["kernel"], "achieved": round(a_valu, 2),
+            "peak": round(PEAK_VALU_TLANE_OPS, 2), "unit": "Tlane-op/s",
+            "frac": round(a_valu / PEAK_VALU_TLANE_OPS, 4), "valu_lane_instr_per_word": vpw,
+            "hbm_achieved_GBps": upd_hbm["achieved"], "hbm_frac": upd_hbm["frac"],
+            "traffic": upd_hbm["traffic"], "us": upd_hbm["us"]}
     # the longest entry the step calls (dgrad and wgrad_vhat alone are context:
     # the step runs them as bwd_products)
     step_entries = ("dqgemm_fwd", "bwd_products", "apply_adamw")
@@ -909,7 +942,7 @@ def main():
         "config": {"workload": "sdxl_linear_1280to5120_M2048_fwd_dgrad_wgrad_update_rebalance",
                    "N": N_OUT, "K": K_IN, "M": M_TOK, "optimizer": "winner (ratio_coh, gf_consol=50)",
                    "forward": "fused dequant-GEMM", "timing": mode},
-        "roofline": dict(roofs[dominant], step_kernel=dominant),
+        "roofline": dict(upd_hbm if dominant == "apply_adamw" else roofs[dominant], step_kernel=dominant),
         "rooflines": roofs,
         "kernel_us": {"dqgemm_fwd": round(t_fwd * 1e3, 2), "bwd_products": round(t_bwd * 1e3, 2),
                       "dqgemm_dgrad": round(t_dgrad * 1e3, 2),

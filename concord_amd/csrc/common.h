@@ -523,19 +523,24 @@ CONCORD_DEV void wave_chain2(const float* __restrict__ v, int64_t count, float* 
   *s1 = lane_value(x1, 0);
 }
 
-// max over the wave's 64 lanes, as a wave-uniform value.  DPP steps: prefix
-// maxima within each 16-lane row (row_shr 1, 2, 4, 8), then lane 15 of rows 0
-// and 2 into rows 1 and 3 (row_bcast:15) and lane 31 into rows 2 and 3
-// (row_bcast:31); lane 63 then holds the maximum.  A lane with no source
-// keeps its own value (bound_ctrl off, old = v), so any sign is fine.  A
-// shuffle butterfly would cost an LDS round trip per step.
+// max over the wave's 64 lanes of NON-NEGATIVE values, as a wave-uniform
+// value.  DPP steps: prefix maxima within each 16-lane row (row_shr 1, 2, 4,
+// 8), so lane 15 of row r holds the row's maximum M_r; then row_bcast:15
+// (lane 15 of each row into the next row: lane 63 = max(M_3, M_2), lane 31 =
+// max(M_1, M_0)) and row_bcast:31 (lane 31 into rows 2 and 3): lane 63 then
+// holds max(M_0 .. M_3).  A lane with no source reads 0 (bound_ctrl, old =
+// 0), which leaves a non-negative maximum unchanged, and every step writes
+// all rows (the other lanes' results are not used), so each step is one
+// v_max_i32 with a DPP operand; an old value of v, or partial row masks, would
+// need a copy and a separate DPP move per step.  A shuffle butterfly would
+// cost an LDS round trip per step.
 CONCORD_DEV int32_t wave_max(int32_t v) {
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x111, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x112, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x114, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x118, 0xF, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x142, 0xA, 0xF, false));
-  v = max(v, __builtin_amdgcn_update_dpp(v, v, 0x143, 0xC, 0xF, false));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x142, 0xF, 0xF, true));
+  v = max(v, __builtin_amdgcn_update_dpp(0, v, 0x143, 0xF, 0xF, true));
   return __builtin_amdgcn_readlane(v, 63);
 }
 

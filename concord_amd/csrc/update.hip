@@ -12,6 +12,7 @@
 // written with one atomic max per row; column watermarks are reduced across
 // the 4 waves in LDS and written with one atomic max per column.
 #include <cstdint>
+#include <type_traits>
 #include "common.h"
 #include "update_fast.h"
 
@@ -175,7 +176,6 @@ __global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
   const float C = a.p.drift_cancel_C, alpha = a.p.alpha, avf = a.p.alpha_v_fast;
   const float lr_kappa = __fmul_rn(U.lr, a.p.gf_consol);
 
-  const bool full = k0 + 4 <= a.K;
   int32_t ce[4], cmax[4];
   float vc[4];
 #pragma unroll
@@ -185,11 +185,12 @@ __global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
     vc[j] = ok ? a.v_col[k0 + j] : 0.0f;
     cmax[j] = 0;
   }
-  // row blocks blockIdx.y, blockIdx.y + gridDim.y, ... (grid.y <= kMaxGridY)
-  for (int64_t nb = (int64_t)blockIdx.y * a.tn; nb < a.N; nb += (int64_t)gridDim.y * a.tn)
-  for (int r = wave; r < a.tn; r += 4) {
-    const int64_t n = nb + r;
-    if (n >= a.N) break;
+  // one row of the lane's 4 columns; FULL: all 256 columns of the block lie
+  // inside the matrix (uniform over the block), so no lane masks its loads,
+  // stores or watermark terms
+  auto row = [&](int64_t n, auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    const bool full = FULL || k0 + 4 <= a.K;
     const int32_t te_row = (int32_t)a.row_exp[n] - a.p.mantissa_bias;
     const float vr = a.v_row[n];
     const int32_t psr = wshl((int32_t)n, 16) ^ U.salt;
@@ -257,6 +258,15 @@ __global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
       rmax = wave_max(rmax);
       if (lane == 0) atomicMax(a.row_max + n, rmax);
     }
+  };
+  const bool full_blk = kb + 256 <= a.K;
+  // row blocks blockIdx.y, blockIdx.y + gridDim.y, ... (grid.y <= kMaxGridY)
+  for (int64_t nb = (int64_t)blockIdx.y * a.tn; nb < a.N; nb += (int64_t)gridDim.y * a.tn)
+  for (int r = wave; r < a.tn; r += 4) {
+    const int64_t n = nb + r;
+    if (n >= a.N) break;
+    if (full_blk) row(n, std::true_type());
+    else row(n, std::false_type());
   }
   if (track) {
 #pragma unroll
