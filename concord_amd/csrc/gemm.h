@@ -74,6 +74,9 @@ struct GemmArgs {
   // meet the upper triangle j >= i, which alone are computed (sym_tile); the
   // split-K slots are indexed in that order.  0: the full tile grid.
   int sym;
+  // i-tiles per group of the grouped tile order (grouped_tile); 0: 8.  The
+  // order only decides which workgroup computes which tile, never a result.
+  int gi;
 };
 
 // s * y + t * x as the Newton-Schulz combination steps take it (x is the
@@ -88,12 +91,11 @@ CONCORD_DEV uint32_t combine_bf16x2(uint32_t yw, uint32_t xw, float s, float t) 
 }
 
 // grouped row-major tile order: groups of GI i-tiles, j-tiles ascending
-// within a group, i-tiles fastest
-CONCORD_DEV void grouped_tile(int lin, int ti, int tj, int& bi, int& bj) {
-  const int GI = 8;
+// within a group, i-tiles fastest (a bijection of [0, ti tj) for any GI >= 1)
+__host__ __device__ inline void grouped_tile(int lin, int ti, int tj, int& bi, int& bj, int GI = 8) {
   const int group = lin / (GI * tj);
   const int first_i = group * GI;
-  const int gsize = min(ti - first_i, GI);
+  const int gsize = ti - first_i < GI ? ti - first_i : GI;
   const int in = lin % (GI * tj);
   bi = first_i + in % gsize;
   bj = in / gsize;
@@ -102,17 +104,17 @@ CONCORD_DEV void grouped_tile(int lin, int ti, int tj, int& bi, int& bj) {
 // XCD x (workgroups w = x mod 8) owns q + (x < rem) consecutive indices
 // starting at x*q + min(x, rem), q = total / 8, rem = total % 8: a bijection
 // of [0, total) for any total
-CONCORD_DEV int xcd_linear(int w, int total) {
+__host__ __device__ inline int xcd_linear(int w, int total) {
   const int xcd = w % 8, slot = w / 8;
   const int q = total / 8, rem = total % 8;
-  return xcd * q + min(xcd, rem) + slot;
+  return xcd * q + (xcd < rem ? xcd : rem) + slot;
 }
 
 // XCD-aware tile order: workgroup w runs on XCD w % 8.  XCD x owns tile
 // indices [x*T/8, (x+1)*T/8) of the grouped order, so the CUs of one XCD
 // share i- and j-tiles in their L2.
-CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
-  grouped_tile(xcd_linear(w, total), ti, tj, bi, bj);
+CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj, int GI = 8) {
+  grouped_tile(xcd_linear(w, total), ti, tj, bi, bj, GI);
 }
 
 // Split-K launches (splits x tiles workgroups): XCD x owns a contiguous range
@@ -120,11 +122,12 @@ CONCORD_DEV void tile_of(int w, int ti, int tj, int total, int& bi, int& bj) {
 // one split's slices of both operands in L2, rather than every XCD reading
 // the whole reduction range of its tiles.  The split-K partial slots are
 // keyed by the row-major tile index bi * tiles_j + bj.
-CONCORD_DEV void split_tile_of(int w, int ti, int tj, int splits, int& split, int& bi, int& bj) {
+__host__ __device__ inline void split_tile_of(int w, int ti, int tj, int splits, int& split, int& bi, int& bj,
+                                              int GI = 8) {
   const int tiles = ti * tj;
   const int lin = xcd_linear(w, tiles * splits);
   split = lin / tiles;
-  grouped_tile(lin % tiles, ti, tj, bi, bj);
+  grouped_tile(lin % tiles, ti, tj, bi, bj, GI);
 }
 
 // Symmetric products: tile row bi (rows [bi BI, bi BI + BI)) meets the upper
@@ -166,7 +169,7 @@ CONCORD_DEV void gemm_tile_of(const GemmArgs& g, int w, int& split, int& bi, int
     slot = lin % g.sym;
     sym_tile(slot, g.tiles_i, g.tiles_j, BI, BJ, bi, bj);
   } else {
-    split_tile_of(w, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
+    split_tile_of(w, g.tiles_i, g.tiles_j, g.splits, split, bi, bj, g.gi > 0 ? g.gi : 8);
     slot = bi * g.tiles_j + bj;
   }
 }

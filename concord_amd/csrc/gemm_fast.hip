@@ -942,7 +942,7 @@ __global__ __launch_bounds__(512, 1) void gemm_ws_kernel(GemmArgs g) {
   const bool producer = wave >= 4;
   const int wg = blockIdx.x;
   int split, bi, bj;
-  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
+  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj, g.gi > 0 ? g.gi : 8);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -1579,7 +1579,7 @@ CONCORD_DEV void gemm_tr_body(const GemmArgs& g, const GemmArgs& rd, int tr_bloc
   const int lane = t & 63, wave = t >> 6;
   const int wg = blockIdx.x;
   int split, bi, bj;
-  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj);
+  split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj, g.gi > 0 ? g.gi : 8);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
   const int64_t r_begin = (int64_t)split * g.r_split;
   const int64_t r_end = min(g.R, r_begin + g.r_split);
@@ -2100,6 +2100,60 @@ static void launch(const GemmArgs& g, int blocks, hipStream_t st) {
   launch_reduce<MODE, BI, BJ, WI, WJ>(g, st);
 }
 
+// The grouped tile order's group size for a launch whose workgroups are all
+// resident at once (at most one per CU): XCD x runs the workgroups w = x mod 8,
+// and its L2 holds the operand bands those tiles read.  For each candidate
+// group size, count per XCD the distinct (split, i-tile) and (split, j-tile)
+// bands its share of split_tile_of's order touches, weighted by one band's
+// bytes per reduction step (wa = BI x A's element size, wb = BJ x B's), and
+// keep the least; ties keep 8.  Results are per grid, cached.
+static int choose_gi(int ti, int tj, int splits, int wa, int wb) {
+  const int tiles = ti * tj, total = tiles * splits;
+  if (total > kCUs || total < 16 || ti < 2) return 8;
+  struct Entry { uint64_t key; int gi; };
+  thread_local Entry cache[64] = {};
+  const uint64_t key = ((uint64_t)ti << 48) ^ ((uint64_t)tj << 36) ^ ((uint64_t)splits << 28) ^
+                       ((uint64_t)(uint32_t)wa << 14) ^ (uint64_t)(uint32_t)wb ^ 1ull;
+  Entry& e = cache[(key ^ (key >> 17) ^ (key >> 33)) & 63];
+  if (e.key == key) return e.gi;
+  auto cost = [&](int gi) {
+    int64_t c = 0;
+    for (int x = 0; x < 8; ++x) {
+      unsigned char seen_a[kCUs] = {}, seen_b[kCUs] = {};
+      int na = 0, nb = 0;
+      for (int w = x; w < total; w += 8) {
+        int split, bi, bj;
+        split_tile_of(w, ti, tj, splits, split, bi, bj, gi);
+        const int ia = split * ti + bi, ib = split * tj + bj;   // < total <= kCUs
+        if (!seen_a[ia]) { seen_a[ia] = 1; ++na; }
+        if (!seen_b[ib]) { seen_b[ib] = 1; ++nb; }
+      }
+      c += (int64_t)na * wa + (int64_t)nb * wb;
+    }
+    return c;
+  };
+  int best = 8;
+  int64_t best_cost = cost(8);
+  for (int gi = 1; gi <= (ti < 16 ? ti : 16); ++gi) {
+    const int64_t c = cost(gi);
+    if (c < best_cost) {
+      best_cost = c;
+      best = gi;
+    }
+  }
+  e.key = key;
+  e.gi = best;
+  return best;
+}
+
+// element bytes of the A and B operands' bands per mode (the packed weight
+// moves 4-byte words)
+static int band_bytes_a(int) { return 2; }
+static int band_bytes_b(int mode) { return (mode == MODE_FWD || mode == MODE_DGRAD) ? 4 : 2; }
+static int plan_gi(int mode, const FastPlan& p, int BI, int BJ) {
+  return choose_gi(p.ti, p.tj, p.splits, BI * band_bytes_a(mode), BJ * band_bytes_b(mode));
+}
+
 static FastPlan plan_mode(int mode, int64_t I, int64_t J, int64_t R, size_t room, bool sym = false) {
   if (mode == MODE_FWD || mode == MODE_FWD_BF16) return plan(kFwdShapes, I, J, R, room, sym);
   if (mode == MODE_WGRAD) return plan(kWgrShapes, I, J, R, room);
@@ -2136,6 +2190,7 @@ int gemm_wgrad_vhat_launch(const GemmArgs& g0, size_t split_room, hipStream_t st
   g.r_split = p.r_split;
   g.tiles_i = p.ti;
   g.tiles_j = p.tj;
+  g.gi = plan_gi(MODE_WGRAD, p, 256, 128);
   hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, true>), dim3(p.ti * p.tj), dim3(512), 0, st, g,
                      GemmArgs{}, p.ti * p.tj);
   return launch_status(what);
@@ -2152,6 +2207,7 @@ int gemm_wgrad_vhat_split_launch(const GemmArgs& g0, void* workspace, size_t ws_
   g.r_split = p.r_split;
   g.tiles_i = p.ti;
   g.tiles_j = p.tj;
+  g.gi = plan_gi(MODE_WGRAD, p, 256, 128);
   g.part = (float*)((char*)workspace + kSplitkCounterBytes);
   const int tiles = p.ti * p.tj;
   *bias_rows = p.tj;   // the reduction folds the splits' bias rows
@@ -2181,12 +2237,14 @@ int gemm_wgrad_split_dgrad_launch(const GemmArgs& gd0, const GemmArgs& gw0, void
   gw.r_split = pw.r_split;
   gw.tiles_i = pw.ti;
   gw.tiles_j = pw.tj;
+  gw.gi = plan_gi(MODE_WGRAD, pw, 256, 128);
   gw.part = (float*)((char*)workspace + kSplitkCounterBytes);
   GemmArgs gd = gd0;
   gd.splits = 1;
   gd.r_split = pd.r_split;
   gd.tiles_i = pd.ti;
   gd.tiles_j = pd.tj;
+  gd.gi = plan_gi(MODE_DGRAD, pd, pd.shape == 0 ? 256 : 192, 128);
   *bias_rows = pw.tj;
   const int tiles = pw.ti * pw.tj;
   hipLaunchKernelGGL((gemm_tr_kernel<256, 128, 4, 2, false>), dim3(tiles * pw.splits), dim3(512), 0, st, gw,
@@ -2215,12 +2273,14 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd0, void* workspace, size_t ws
   gd.r_split = pd.r_split;
   gd.tiles_i = pd.ti;
   gd.tiles_j = pd.tj;
+  gd.gi = plan_gi(MODE_DGRAD, pd, pd.shape == 0 ? 256 : 192, 128);
   gd.part = (float*)((char*)workspace + kSplitkCounterBytes);
   GemmArgs gw = gw0;
   gw.splits = 1;
   gw.r_split = pw.r_split;
   gw.tiles_i = pw.ti;
   gw.tiles_j = pw.tj;
+  gw.gi = plan_gi(MODE_WGRAD, pw, 256, 128);
   *tiles_j = pw.tj;
   if (pd.shape == 0) {
     hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD, 256, 128>), dim3(pd.ti * pd.tj * pd.splits), dim3(512), 0, st,
@@ -2279,12 +2339,14 @@ int gemm_dgrad_wgrad_update_launch(const GemmArgs& gd0, void* workspace, size_t 
   gd.r_split = pd.r_split;
   gd.tiles_i = pd.ti;
   gd.tiles_j = pd.tj;
+  gd.gi = plan_gi(MODE_DGRAD, pd, pd.shape == 0 ? 256 : 192, 128);
   gd.part = (float*)((char*)workspace + kSplitkCounterBytes);
   GemmArgs gw = gw0;
   gw.splits = 1;
   gw.r_split = pw.r_split;
   gw.tiles_i = pw.ti;
   gw.tiles_j = pw.tj;
+  gw.gi = plan_gi(MODE_WGRAD, pw, 256, 128);
   WgradUpd u = u0;
   u.nbp = pw.tj;
   const dim3 grid(tw + extra), block(512);
@@ -2337,6 +2399,10 @@ int gemm_conv_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_by
   g.r_split = p.r_split;
   g.tiles_i = p.ti;
   g.tiles_j = p.tj;
+  {
+    const FastShape sh = conv_shape(mode, p.shape);
+    g.gi = plan_gi(mode, p, sh.bi, sh.bj);
+  }
   if (p.splits > 1) g.part = (float*)((char*)workspace + kSplitkCounterBytes);
   if (mode != MODE_WGRAD) g.bpart = nullptr;
   if (bias_rows) *bias_rows = g.bpart ? p.tj : 0;   // split launches fold their rows in the reduction
@@ -2390,6 +2456,7 @@ static int fast_launch(int mode, const GemmArgs& g0, void* workspace, size_t ws_
   g.tiles_j = p.tj;
   const FastShape& sh = shape_of(mode, p.shape);
   g.sym = sym ? sym_tile_count(p.ti, p.tj, sh.bi, sh.bj) : 0;
+  if (!sym) g.gi = plan_gi(mode, p, sh.bi, sh.bj);
   if (p.splits > 1) g.part = (float*)((char*)workspace + kSplitkCounterBytes);
   const int blocks = (sym ? g.sym : p.ti * p.tj) * p.splits;
   switch (mode) {
