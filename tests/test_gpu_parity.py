@@ -1586,6 +1586,78 @@ def test_layer_fused_update_matches_separate():
         pb.set_ratio_coh(False)
 
 
+def test_fused_update_graph_replays_match_eager():
+    """The layer step through the combined backward launch (set_fused_update)
+    captured in a HIP graph and replayed three times, each replay followed by
+    an eager step of a twin layer through the separate launches from the same
+    state and salt: words, exponents, v-hat state and bias gradients identical
+    after every replay (the launch re-arms its own barrier counters; no memset
+    is recorded), and no barrier fault."""
+    import concord_amd as ca
+    from concord_amd import packed_b as pb
+    torch.manual_seed(6)
+    W0 = torch.randn(5120, 1280) * 0.02
+    x = torch.randn(2048, 1280, device=DEV)
+    gy = torch.randn(2048, 5120, device=DEV) * 1e-2
+    pb.set_ratio_coh(True)
+    pb.set_ratio_coh_floors(0.9, 0.999)
+    salt = pb._get_step_counter(DEV)
+    layers = []
+    for _ in range(2):
+        la = ca.ConcordLinearPackedB(1280, 5120, bias=True, device=DEV, lr=5e-4)
+        la.disable_cohpre()
+        la.gf_consol = 50.0
+        la.load_weights(W0)
+        layers.append(la)
+    xa = x.clone().requires_grad_(True)
+    xb = x.clone().requires_grad_(True)
+
+    def step(layer, xin):
+        xin.grad = None
+        layer.bias.grad = None
+        layer(xin).backward(gy)
+        layer.rebalance()
+
+    def state(layer, xin):
+        return [host(t) for t in (layer.packed_w, layer.row_exp, layer.col_exp, layer.v_row, layer.v_col,
+                                  layer.bias.grad.to(torch.bfloat16), xin.grad.to(torch.bfloat16))]
+
+    try:
+        for k in range(2):   # eager warm-up of both twins, same salts
+            salt.fill_(40 + k)
+            pb.set_fused_update(True)
+            step(layers[0], xa)
+            salt.fill_(40 + k)
+            pb.set_fused_update(False)
+            step(layers[1], xb)
+        sync()
+        for u, v in zip(state(layers[0], xa), state(layers[1], xb)):
+            np.testing.assert_array_equal(u, v)
+        pb.set_fused_update(True)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                step(layers[0], xa)
+        torch.cuda.current_stream().wait_stream(s)
+        pb.set_fused_update(False)
+        for k in range(3):
+            salt.fill_(50 + k)
+            g.replay()
+            sync()
+            assert int(host(salt)[0]) == 51 + k
+            salt.fill_(50 + k)
+            step(layers[1], xb)
+            sync()
+            for u, v in zip(state(layers[0], xa), state(layers[1], xb)):
+                np.testing.assert_array_equal(u, v)
+        assert not pb.wgrad_update_faults(DEV)
+    finally:
+        pb.set_fused_update(False)
+        pb.set_ratio_coh(False)
+
+
 @pytest.mark.parametrize("N,K", [(320, 192), (5120, 1280)])
 def test_empty_batch_wgrad_entries(oracle, N, K):
     """M = 0 tokens: the weight gradient is the sum over no tokens, so the
