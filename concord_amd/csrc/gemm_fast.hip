@@ -2106,15 +2106,18 @@ static void launch(const GemmArgs& g, int blocks, hipStream_t st) {
 // group size, count per XCD the distinct (split, i-tile) and (split, j-tile)
 // bands its share of split_tile_of's order touches, weighted by one band's
 // bytes per reduction step (wa = BI x A's element size, wb = BJ x B's), and
-// keep the least; ties keep 8.  Results are per grid, cached.
+// keep the least; ties keep 8.  One evaluation costs ~15 us of host time, so
+// results are cached per grid (512 entries per thread: a network's distinct
+// launch grids, config 4's ~60 among them, stay resident in eager loops).
 static int choose_gi(int ti, int tj, int splits, int wa, int wb) {
   const int tiles = ti * tj, total = tiles * splits;
   if (total > kCUs || total < 16 || ti < 2) return 8;
   struct Entry { uint64_t key; int gi; };
-  thread_local Entry cache[64] = {};
+  constexpr int kSlots = 512;
+  thread_local Entry cache[kSlots] = {};
   const uint64_t key = ((uint64_t)ti << 48) ^ ((uint64_t)tj << 36) ^ ((uint64_t)splits << 28) ^
                        ((uint64_t)(uint32_t)wa << 14) ^ (uint64_t)(uint32_t)wb ^ 1ull;
-  Entry& e = cache[(key ^ (key >> 17) ^ (key >> 33)) & 63];
+  Entry& e = cache[(key ^ (key >> 17) ^ (key >> 33) ^ (key >> 47)) & (kSlots - 1)];
   if (e.key == key) return e.gi;
   auto cost = [&](int gi) {
     int64_t c = 0;
