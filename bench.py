@@ -566,20 +566,17 @@ def _layer_ctx(layer, pb):
 
 
 def _bwd_update_fns(layer, xb, dy, pb):
-    """The step's backward with its update, each way: (two_pass, fused).
-    two_pass = concord_dgrad_wgrad_vhat then concord_apply_adamw; fused =
-    concord_dgrad_wgrad_update (finalize and update in the WGRAD launch)."""
+    """The step's backward with its update, each way, as the module calls it
+    (concord_dgrad_wgrad_update): (two_pass, fused).  two_pass = the separate
+    launches (the default); fused = the finalize and the update in the WGRAD
+    launch (set_fused_update)."""
     ctx = _layer_ctx(layer, pb)
-    salt = pb._get_step_counter(xb.device)
 
     def two_pass():
-        _, gw, _ = pb._dgrad_wgrad_vhat(dy, xb, layer.packed_w, layer.row_exp, layer.col_exp, 15, layer.v_row,
-                                        layer.v_col, layer._sum_v_inv, 0.999, layer._row_max_buf,
-                                        layer._col_max_buf, salt, with_bias=True)
-        pb._packed_step(ctx, gw, True, False)
+        pb._dgrad_wgrad_update(ctx, dy, xb, False)
 
     def fused():
-        pb._dgrad_wgrad_update(ctx, dy, xb)
+        pb._dgrad_wgrad_update(ctx, dy, xb, True)
     return two_pass, fused
 
 
@@ -603,7 +600,8 @@ def _fused_update_rows(layer, step, xb, dy, warmup, steps, G, reps, torch, pb):
         pb.set_fused_update(prev)
     out["kept"] = "fused" if prev else "two_pass"
     out["note"] = ("two_pass: gemm_dgt_kernel + gemm_tr_kernel<VH> (carrying the dgrad reduction) + "
-                   "vhat_finalize_kernel + apply_adamw_fast_kernel; fused: gemm_dgt_kernel + wgrad_update_kernel "
+                   "vhat_finalize_kernel (256-row totals) + apply_adamw_fast_kernel (1 / sum v_row from them); "
+                   "fused: gemm_dgt_kernel + wgrad_update_kernel "
                    "(tiles, v-hat partials, grid barrier, finalize over the grid, grid barrier, update of each "
                    "tile from its accumulators; no bf16 weight gradient)")
     return out

@@ -86,7 +86,7 @@ _SIGS = {
     "concord_dgrad_wgrad_vhat": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _i, _P, _I, _P, _I, _P, _I, _I, _I,
                                                  _I, _D, _P, _P, _P, _P, _P, _P, _P, _P, _Z, _P, _Z, _P]),
     "concord_dgrad_wgrad_update": (ctypes.c_int, [_P, _I, _P, _I, _P, _P, _P, _I, _P, _I, _P, _I, ctypes.c_int,
-                                                   _I, _I, _I, _D, _P, _P, _P, _P, _P, _P, _I, _P,
+                                                   ctypes.c_int, _I, _I, _I, _D, _P, _P, _P, _P, _P, _P, _I, _P,
                                                    ctypes.POINTER(UpdateParams), ctypes.POINTER(DeviceScalars),
                                                    ctypes.c_uint32, _P, _Z, _P, _Z, _P, _P]),
     "concord_wgrad_update_fault": (ctypes.c_int, [_P, _Z, _P, _P]),

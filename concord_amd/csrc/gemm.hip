@@ -691,7 +691,7 @@ static int64_t grid_timeout_ticks() {
 extern "C" int concord_dgrad_wgrad_update(
     const uint16_t* dy, int64_t ld_dy, int32_t* packed, int64_t ld_p, const int8_t* row_exp, const int8_t* col_exp,
     uint16_t* dx, int64_t ld_dx, const uint16_t* x, int64_t ld_x, uint16_t* grad_w, int64_t ld_gw, int copy_grad,
-    int64_t M, int64_t N, int64_t K, double beta2, float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max,
+    int fuse, int64_t M, int64_t N, int64_t K, double beta2, float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max,
     int32_t* col_max, float* coh_pre, int64_t ld_c, uint16_t* grad_bias, const concord_update_params* params,
     const concord_device_scalars* scalars, uint32_t flags, void* workspace, size_t workspace_bytes,
     void* gemm_workspace, size_t gemm_workspace_bytes, int* fused, void* stream) {
@@ -721,7 +721,7 @@ extern "C" int concord_dgrad_wgrad_update(
   const int64_t ticks = grid_timeout_ticks();
   const bool layout_ok = ld_p % 4 == 0 && ((uintptr_t)packed % 16) == 0 && ((uintptr_t)col_exp % 4) == 0 &&
                          (upd != 1 || (coh_pre && ld_c >= K && ld_c % 4 == 0 && ((uintptr_t)coh_pre % 16) == 0));
-  if (M > 0 && upd != 0 && layout_ok && ticks > 0) {
+  if (fuse && M > 0 && upd != 0 && layout_ok && ticks > 0) {
     const VhatScratch v = vhat_scratch(N, K);
     float* pr = (float*)((char*)workspace + ws.scratch);
     float* pc = pr + v.pr;
@@ -763,11 +763,22 @@ extern "C" int concord_dgrad_wgrad_update(
       return rc;
     }
   }
-  // the two launches' worth: products + v-hat EMA, then the update
-  const int rc = wgrad_vhat_impl(&gd, dy, ld_dy, x, ld_x, grad_w, ld_gw, M, N, K, beta2, v_row, v_col, sum_v_inv,
-                                 row_max, col_max, scalars->salt_counter, grad_bias, workspace, workspace_bytes,
-                                 gemm_workspace, gemm_workspace_bytes, st, what);
+  // the separate launches: products + v-hat EMA, then the update.  When the
+  // update runs the fast kernel, the finalize leaves its 256-row totals and
+  // the update chains them into 1 / sum v_row (the finalize's own chain, so
+  // the same bits), which saves the finalize's ticket round trips
+  const bool defer = adamw_fast_eligible(*params, flags, packed, ld_p, grad_w, ld_gw, coh_pre, ld_c);
+  const int rc = wgrad_vhat_impl(&gd, dy, ld_dy, x, ld_x, grad_w, ld_gw, M, N, K, beta2, v_row, v_col,
+                                 defer ? nullptr : sum_v_inv, row_max, col_max, scalars->salt_counter, grad_bias,
+                                 workspace, workspace_bytes, gemm_workspace, gemm_workspace_bytes, st, what);
   if (rc != CONCORD_OK) return rc;
+  if (defer) {
+    const VhatScratch v = vhat_scratch(N, K);
+    const float* bsum = (const float*)((char*)workspace + ws.scratch) + v.pr + v.pc;
+    return apply_adamw_fast_bsum(packed, ld_p, grad_w, ld_gw, row_exp, col_exp, row_max, col_max, v_row, v_col,
+                                 bsum, cdiv(N, 256), sum_v_inv, coh_pre, ld_c, N, K, params, scalars,
+                                 flags | CONCORD_SALT_PREBUMPED, st);
+  }
   return concord_apply_adamw(packed, ld_p, grad_w, ld_gw, nullptr, K, row_exp, col_exp, row_max, col_max, v_row,
                              v_col, sum_v_inv, coh_pre, ld_c, N, K, params, scalars, flags | CONCORD_SALT_PREBUMPED,
                              stream);

@@ -41,6 +41,12 @@ struct AdamwArgs {
   const float* v_col;
   const float* sum_v_inv;
   float* coh_pre;
+  // fast kernel only: when bsum is set, 1 / sum v_row is formed here from the
+  // finalize's 256-row totals (bsum[nbsum], chained in order as the finalize
+  // would) instead of read from sum_v_inv, and stored to svi_out
+  const float* bsum;
+  int64_t nbsum;
+  float* svi_out;
   int64_t ld_p, ld_g, ld_w, ld_c;
   int64_t N, K;
   concord_update_params p;
@@ -170,7 +176,18 @@ __global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
   U.cons = 1;
   U.consf = 1.0f;
   U.salt = *a.s.salt_counter;
-  U.svi = *a.sum_v_inv;
+  if (a.bsum) {
+    float tot = 0.0f;
+    for (int64_t c0 = 0; c0 < a.nbsum; c0 += 64) {
+      const float v = c0 + lane < a.nbsum ? a.bsum[c0 + lane] : 0.0f;
+      const int cnt = (int)min((int64_t)64, a.nbsum - c0);
+      for (int j = 0; j < cnt; ++j) tot = __fadd_rn(tot, lane_value(v, j));
+    }
+    U.svi = __fdiv_rn(1.0f, fmaxf(tot, 1e-30f));
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.svi_out = U.svi;
+  } else {
+    U.svi = *a.sum_v_inv;
+  }
   const bool track = a.flags & CONCORD_TRACK_REBALANCE;
   const bool emit = a.flags & CONCORD_EMIT_WEIGHT;
   const float C = a.p.drift_cancel_C, alpha = a.p.alpha, avf = a.p.alpha_v_fast;
@@ -522,14 +539,17 @@ extern "C" int concord_salt_bump(int32_t* salt_counter, void* stream) {
   return launch_status("salt_bump");
 }
 
-extern "C" int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t* grad,
-                                   int64_t ld_g, uint16_t* weight_buf, int64_t ld_w,
-                                   const int8_t* row_exp, const int8_t* col_exp, int32_t* row_max,
-                                   int32_t* col_max, const float* v_row, const float* v_col,
-                                   const float* sum_v_inv, float* coh_pre, int64_t ld_c, int64_t N,
-                                   int64_t K, const concord_update_params* params,
-                                   const concord_device_scalars* scalars, uint32_t flags,
-                                   void* stream) {
+namespace concord {
+
+// concord_apply_adamw; with bsum set, the fast kernel (which the caller has
+// checked applies: adamw_fast_eligible) forms 1 / sum v_row from the 256-row
+// totals and stores it to svi_out
+static int apply_adamw_impl(int32_t* packed, int64_t ld_p, const uint16_t* grad, int64_t ld_g,
+                            uint16_t* weight_buf, int64_t ld_w, const int8_t* row_exp, const int8_t* col_exp,
+                            int32_t* row_max, int32_t* col_max, const float* v_row, const float* v_col,
+                            const float* sum_v_inv, float* coh_pre, int64_t ld_c, int64_t N, int64_t K,
+                            const concord_update_params* params, const concord_device_scalars* scalars,
+                            uint32_t flags, void* stream, const float* bsum, int64_t nbsum, float* svi_out) {
   CONCORD_CHECK(N >= 0 && K >= 0, "concord_apply_adamw: negative size");
   CONCORD_CHECK(N < ((int64_t)1 << 31) && K < ((int64_t)1 << 31),
                 "concord_apply_adamw: N=%lld K=%lld outside the int32 index range",
@@ -541,7 +561,7 @@ extern "C" int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t
   CONCORD_CHECK(scalars->lr && scalars->eps && scalars->salt_counter,
                 "concord_apply_adamw: lr/eps/salt_counter NULL");
   const bool need_vhat = update_needs_vhat(flags);
-  CONCORD_CHECK(!need_vhat || (v_row && v_col && sum_v_inv),
+  CONCORD_CHECK(!need_vhat || (v_row && v_col && (sum_v_inv || bsum)),
                 "concord_apply_adamw: gf_trust/gf_consol/coh_pre/ratio_coh need v_row, v_col, sum_v_inv");
   CONCORD_CHECK(!(flags & CONCORD_RATIO_COH) || (scalars->chase_floor && scalars->leak_floor),
                 "concord_apply_adamw: RATIO_COH needs chase_floor/leak_floor");
@@ -560,16 +580,19 @@ extern "C" int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t
   a.packed = packed; a.grad = grad; a.wbuf = weight_buf; a.row_exp = row_exp;
   a.col_exp = col_exp; a.row_max = row_max; a.col_max = col_max; a.v_row = v_row;
   a.v_col = v_col; a.sum_v_inv = sum_v_inv; a.coh_pre = coh_pre;
+  a.bsum = bsum; a.nbsum = nbsum; a.svi_out = svi_out;
   a.ld_p = ld_p; a.ld_g = ld_g; a.ld_w = ld_w; a.ld_c = ld_c; a.N = N; a.K = K;
   a.p = *params; a.s = *scalars; a.flags = flags;
   const bool vec4 = (ld_p % 4 == 0) && (ld_g % 4 == 0) && aligned(packed, 16) &&
                     aligned(grad, 8) && (!cohpre || (ld_c % 4 == 0 && aligned(coh_pre, 16))) &&
                     (!(flags & CONCORD_EMIT_WEIGHT) || (ld_w % 4 == 0 && aligned(weight_buf, 8)));
+  const int fast = vec4 ? update_fast_path(*params, flags) : 0;
+  CONCORD_CHECK(!bsum || (fast != 0 && svi_out), "apply_adamw: the totals form needs the fast kernel");
   if (vec4) {
     const int64_t cb = cdiv(K, 256);
     a.tn = choose_tn(N, cb);
     const dim3 grid((unsigned)cb, grid_y(cdiv(N, a.tn)));
-    switch (update_fast_path(*params, flags)) {
+    switch (fast) {
       case 2: hipLaunchKernelGGL(apply_adamw_fast_kernel<true>, grid, dim3(256), 0, st, a); break;
       case 1: hipLaunchKernelGGL(apply_adamw_fast_kernel<false>, grid, dim3(256), 0, st, a); break;
       default: hipLaunchKernelGGL(apply_adamw_kernel<4>, grid, dim3(256), 0, st, a); break;
@@ -580,6 +603,41 @@ extern "C" int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t
     hipLaunchKernelGGL(apply_adamw_kernel<1>, dim3((unsigned)cb, grid_y(cdiv(N, a.tn))), dim3(256), 0, st, a);
   }
   return launch_status("apply_adamw");
+}
+
+bool adamw_fast_eligible(const concord_update_params& p, uint32_t flags, const int32_t* packed, int64_t ld_p,
+                         const uint16_t* grad, int64_t ld_g, const float* coh_pre, int64_t ld_c) {
+  const bool cohpre = (flags & CONCORD_COHPRE) && (flags & CONCORD_APPLY_CHASE) && !(flags & CONCORD_RATIO_COH);
+  const bool vec4 = (ld_p % 4 == 0) && (ld_g % 4 == 0) && aligned(packed, 16) && aligned(grad, 8) &&
+                    (!cohpre || (coh_pre && ld_c % 4 == 0 && aligned(coh_pre, 16))) &&
+                    !(flags & CONCORD_EMIT_WEIGHT);
+  return vec4 && update_fast_path(p, flags) != 0;
+}
+
+int apply_adamw_fast_bsum(int32_t* packed, int64_t ld_p, const uint16_t* grad, int64_t ld_g, const int8_t* row_exp,
+                          const int8_t* col_exp, int32_t* row_max, int32_t* col_max, const float* v_row,
+                          const float* v_col, const float* bsum, int64_t nbsum, float* sum_v_inv, float* coh_pre,
+                          int64_t ld_c, int64_t N, int64_t K, const concord_update_params* params,
+                          const concord_device_scalars* scalars, uint32_t flags, hipStream_t stream) {
+  return apply_adamw_impl(packed, ld_p, grad, ld_g, nullptr, K, row_exp, col_exp, row_max, col_max, v_row, v_col,
+                          nullptr, coh_pre, ld_c, N, K, params, scalars, flags, stream, bsum, nbsum, sum_v_inv);
+}
+
+}  // namespace concord
+
+using namespace concord;
+
+extern "C" int concord_apply_adamw(int32_t* packed, int64_t ld_p, const uint16_t* grad,
+                                   int64_t ld_g, uint16_t* weight_buf, int64_t ld_w,
+                                   const int8_t* row_exp, const int8_t* col_exp, int32_t* row_max,
+                                   int32_t* col_max, const float* v_row, const float* v_col,
+                                   const float* sum_v_inv, float* coh_pre, int64_t ld_c, int64_t N,
+                                   int64_t K, const concord_update_params* params,
+                                   const concord_device_scalars* scalars, uint32_t flags,
+                                   void* stream) {
+  return apply_adamw_impl(packed, ld_p, grad, ld_g, weight_buf, ld_w, row_exp, col_exp, row_max, col_max, v_row,
+                          v_col, sum_v_inv, coh_pre, ld_c, N, K, params, scalars, flags, stream, nullptr, 0,
+                          nullptr);
 }
 
 extern "C" int concord_apply_sgd(int32_t* packed, int64_t ld_p, const uint16_t* grad, int64_t ld_g,

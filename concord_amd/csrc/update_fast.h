@@ -111,6 +111,19 @@ CONCORD_DEV int32_t adamw_element_fast(int32_t word, float g, float scale_fwd, f
   return pack(sfc, ssc, new_v);
 }
 
+// whether concord_apply_adamw with these arguments runs the fast kernel
+// (update.hip)
+bool adamw_fast_eligible(const concord_update_params& p, uint32_t flags, const int32_t* packed, int64_t ld_p,
+                         const uint16_t* grad, int64_t ld_g, const float* coh_pre, int64_t ld_c);
+// concord_apply_adamw without weight_buf through the fast kernel, 1 / sum v_row
+// formed from the finalize's 256-row totals bsum[nbsum] (the finalize's
+// chain) and stored to sum_v_inv (update.hip); adamw_fast_eligible must hold
+int apply_adamw_fast_bsum(int32_t* packed, int64_t ld_p, const uint16_t* grad, int64_t ld_g, const int8_t* row_exp,
+                          const int8_t* col_exp, int32_t* row_max, int32_t* col_max, const float* v_row,
+                          const float* v_col, const float* bsum, int64_t nbsum, float* sum_v_inv, float* coh_pre,
+                          int64_t ld_c, int64_t N, int64_t K, const concord_update_params* params,
+                          const concord_device_scalars* scalars, uint32_t flags, hipStream_t stream);
+
 // 0 = generic kernel, 1 = bare fast path, 2 = winner fast path
 inline int update_fast_path(const concord_update_params& p, uint32_t flags) {
   const uint32_t need = CONCORD_FIXED_COH | CONCORD_GF_TRUST_REGION | CONCORD_APPLY_CHASE |

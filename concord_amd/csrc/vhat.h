@@ -9,7 +9,9 @@ namespace concord {
 void vhat_partials_launch(const uint16_t* grad, int64_t ld, int64_t N, int64_t K, float* pr, float* pc,
                           hipStream_t st);
 // EMA of v_row / v_col from the partials, watermark zeroing, 1 / sum v_row,
-// salt advance (row_max, col_max, salt may be NULL)
+// salt advance (row_max, col_max, salt may be NULL).  sum_v_inv == NULL:
+// bsum[cdiv(N, 256)] is left holding the 256-row totals of v_row, and the
+// update that follows forms 1 / sum v_row from them (apply_adamw_fast_bsum)
 // bpart / nbp / grad_bias (optional): grad_bias[n] = bf16(sum over b < nbp
 // ascending of bpart[b][n])
 // ticket: a zero-initialised counter the call leaves at zero again

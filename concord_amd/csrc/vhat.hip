@@ -140,7 +140,10 @@ CONCORD_DEV float staged_row_sum(const float* __restrict__ src, int64_t terms, i
 // columns each: the four waves load the column partials of interleaved row
 // tiles into LDS, one thread per column then sums them in row-tile order.
 // The last row block to finish (a device-scope ticket) chains the totals in
-// ascending order into 1 / max(sum v_row, 1e-30) and advances the salt.  The
+// ascending order into 1 / max(sum v_row, 1e-30) and advances the salt.
+// sum_v_inv == NULL: the chain is left to the update that follows (it reads
+// the totals in bsum); the row blocks only store their totals, and block 0
+// advances the salt (no block of this kernel reads it).  The
 // totals and the ticket are device-scope atomics (cache-coherent across the
 // XCDs), each total stored and complete before its block takes a ticket, so
 // the last block reads every total without a device-wide cache write-back.
@@ -159,6 +162,7 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
   const int64_t rb = cdiv(N, 256);
   const int64_t rbb = grad_bias ? rb : 0;   // bias blocks
   const int64_t nc = cdiv(K, 64), nr = cdiv(N, 64);
+  if (!sum_v_inv && salt && blockIdx.x == 0 && threadIdx.x == 0) salt[0] = wadd(salt[0], 1);
   if ((int64_t)blockIdx.x >= rb && (int64_t)blockIdx.x < rb + rbb) {
     const int64_t i0 = ((int64_t)blockIdx.x - rb) * 256, i = i0 + threadIdx.x;
     const float sb = staged_row_sum(bpart, nbp, N, i0, S.rows);
@@ -180,6 +184,10 @@ __global__ __launch_bounds__(256) void vhat_finalize_kernel(
     for (int h = 128; h >= 1; h >>= 1) {
       if (threadIdx.x < h) s_part[threadIdx.x] = __fadd_rn(s_part[threadIdx.x], s_part[threadIdx.x + h]);
       __syncthreads();
+    }
+    if (!sum_v_inv) {   // the update chains the totals
+      if (threadIdx.x == 0) bsum[blockIdx.x] = s_part[0];
+      return;
     }
     if (threadIdx.x == 0) {
       __hip_atomic_store(bsum + blockIdx.x, s_part[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -92,8 +92,8 @@ def set_ratio_coh(enabled):
 def set_fused_update(enabled):
     """True: the fused-forward layer's backward with the v-hat drive runs the
     v-hat finalize and the adamw update inside its WGRAD launch when the
-    update's flags allow it (concord_dgrad_wgrad_update); False: launches of
-    their own.  The results are the same either way."""
+    update's flags allow it (concord_dgrad_wgrad_update with fuse); False
+    (default): launches of their own.  The results are the same either way."""
     global _FUSED_UPDATE
     _FUSED_UPDATE = bool(enabled)
 
@@ -579,12 +579,12 @@ def _dgrad_wgrad_vhat(dy, x2, packed_w, row_exp, col_exp, mantissa_bias, v_row, 
 _LAST_FUSED = [0]
 
 
-def _dgrad_wgrad_update(ctx, dy, x2):
+def _dgrad_wgrad_update(ctx, dy, x2, fuse=False):
     """_dgrad_wgrad_vhat followed by the adamw update of _packed_step, in one
-    entry (concord_dgrad_wgrad_update, same results): for the update's two
+    entry (concord_dgrad_wgrad_update, same results)
+    (concord/packed_b.py:1263-1327, 1338-1340).  fuse: for the update's two
     fast flag sets the v-hat finalize and the update run in the WGRAD launch,
-    from its tiles' accumulators (concord/packed_b.py:1263-1327, 1338-1340).
-    Returns (grad_x, grad_bias or None)."""
+    from its tiles' accumulators.  Returns (grad_x, grad_bias or None)."""
     M, N = dy.shape
     K = x2.shape[1]
     dev = dy.device
@@ -608,7 +608,7 @@ def _dgrad_wgrad_update(ctx, dy, x2):
     C.check(C.lib().concord_dgrad_wgrad_update(
         C.ptr(dy), dy.stride(0), C.ptr(ctx.packed_w), ctx.packed_w.stride(0), C.ptr(ctx.row_exp),
         C.ptr(ctx.col_exp), C.ptr(dx), dx.stride(0), C.ptr(x2), x2.stride(0), C.ptr(gw), gw.stride(0),
-        int(capture), M, N, K, float(ctx.adafactor_beta2), C.ptr(ctx.v_row), C.ptr(ctx.v_col),
+        int(capture), int(bool(fuse)), M, N, K, float(ctx.adafactor_beta2), C.ptr(ctx.v_row), C.ptr(ctx.v_col),
         C.ptr(ctx.sum_v_inv), C.ptr(rm), C.ptr(cm), C.ptr(cp), cp.stride(0) if cp is not None else K, C.ptr(gb),
         ctypes.byref(P), ctypes.byref(S), flags, C.ptr(ws), ws.numel(), C.ptr(gws), gws.numel(),
         ctypes.byref(fused), C.stream_of(dev)), "dgrad_wgrad_update")
@@ -806,9 +806,11 @@ class FusedConcordLinearPackedB(torch.autograd.Function):
             # dgrad on the pre-update weight (1263), wgrad (1269-1277), watermark
             # zeroing (1281-1283), v-hat EMA (1288-1303), salt + 1 (910-911) and
             # grad_y.sum(0) (1338-1340) in one entry
-            if _FUSED_UPDATE and ctx.optimizer_kind == 'adamw':
-                # ... and the update (1281-1327) in the same entry
-                grad_x, grad_bias = _dgrad_wgrad_update(ctx, dy, x2)
+            if ctx.optimizer_kind == 'adamw':
+                # ... and the update (1281-1327) in the same entry: the
+                # separate launches, or with set_fused_update the finalize and
+                # update inside the WGRAD launch
+                grad_x, grad_bias = _dgrad_wgrad_update(ctx, dy, x2, _FUSED_UPDATE)
                 grad_W = None
             else:
                 grad_x, grad_W, grad_bias = _dgrad_wgrad_vhat(

@@ -272,20 +272,21 @@ int concord_dgrad_wgrad_vhat(const uint16_t* dy, int64_t ld_dy, const int32_t* p
  * concord_dgrad_wgrad_vhat (salt_counter = scalars->salt_counter) followed by
  * concord_apply_adamw(packed, ..., grad_w, ..., flags | CONCORD_SALT_PREBUMPED)
  * (FusedConcordLinearPackedB.backward, concord/packed_b.py:1263-1327,
- * 1338-1340), with the same results.  When the flags and parameters are one
- * of the update's two fast sets (winner or bare) and the shapes take the
- * combined launch, the v-hat finalize and the update run in the workgroups
- * of the WGRAD launch, from the accumulators of its tiles (*fused = 1): the
- * bf16 weight gradient is then written to grad_w only when copy_grad is
- * non-zero.  Otherwise the separate launches run and grad_w holds the
- * gradient.  That launch's grid barriers are bounded; should a wait exceed
+ * 1338-1340), with the same results.  With fuse non-zero, when the flags and
+ * parameters are one of the update's two fast sets (winner or bare) and the
+ * shapes take the combined launch, the v-hat finalize and the update run in
+ * the workgroups of the WGRAD launch, from the accumulators of its tiles
+ * (*fused = 1): the bf16 weight gradient is then written to grad_w only when
+ * copy_grad is non-zero.  Otherwise the separate launches run and grad_w
+ * holds the gradient; when the update runs its fast kernel, 1 / sum v_row is
+ * then formed in the update from the finalize's 256-row totals.  That launch's grid barriers are bounded; should a wait exceed
  * its bound (its workgroups not all resident), the launch skips its writes
  * and concord_wgrad_update_fault reports it.  CONCORD_EMIT_WEIGHT is not
  * taken.  Workspaces as for concord_dgrad_wgrad_vhat; fused may be NULL. */
 int concord_dgrad_wgrad_update(const uint16_t* dy, int64_t ld_dy, int32_t* packed, int64_t ld_p,
                                const int8_t* row_exp, const int8_t* col_exp, uint16_t* dx, int64_t ld_dx,
                                const uint16_t* x, int64_t ld_x, uint16_t* grad_w, int64_t ld_gw, int copy_grad,
-                               int64_t M, int64_t N, int64_t K, double beta2, float* v_row, float* v_col,
+                               int fuse, int64_t M, int64_t N, int64_t K, double beta2, float* v_row, float* v_col,
                                float* sum_v_inv, int32_t* row_max, int32_t* col_max, float* coh_pre,
                                int64_t ld_c, uint16_t* grad_bias, const concord_update_params* params,
                                const concord_device_scalars* scalars, uint32_t flags, void* workspace,

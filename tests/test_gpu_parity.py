@@ -1466,10 +1466,11 @@ def test_dgrad_wgrad_vhat_matches_separate_calls(M, N, K):
     assert (outs[0][6] == 0).all() and outs[0][8][0] == 6
 
 
-def _update_backward(pb, combined, dy, x, st, winner, lr):
+def _update_backward(pb, combined, dy, x, st, winner, lr, fuse=1):
     """One backward step of the fused-forward layer with the adamw update:
-    the combined entry (combined = True; returns whether its launch carried
-    the update) or the v-hat entry then the separate update."""
+    the combined entry (combined = True; fuse: whether it may carry the update
+    in the WGRAD launch; returns whether it did) or the v-hat entry then the
+    separate update."""
     import ctypes
     from concord_amd import _lib as C
     M, N = dy.shape
@@ -1494,23 +1495,26 @@ def _update_backward(pb, combined, dy, x, st, winner, lr):
     fused = ctypes.c_int(-1)
     C.check(C.lib().concord_dgrad_wgrad_update(
         C.ptr(dy), dy.stride(0), C.ptr(pk), pk.stride(0), C.ptr(red), C.ptr(ced), C.ptr(dx), dx.stride(0),
-        C.ptr(x), x.stride(0), C.ptr(gw), gw.stride(0), 1, M, N, K, 0.999, C.ptr(vr), C.ptr(vc), C.ptr(svi),
+        C.ptr(x), x.stride(0), C.ptr(gw), gw.stride(0), 1, fuse, M, N, K, 0.999, C.ptr(vr), C.ptr(vc), C.ptr(svi),
         C.ptr(rm), C.ptr(cm), C.ptr(cp), cp.stride(0) if cp is not None else K, C.ptr(gb), ctypes.byref(P),
         ctypes.byref(S), flags, C.ptr(ws), ws.numel(), C.ptr(gws), gws.numel(), ctypes.byref(fused),
         C.stream_of(DEV)), "dgrad_wgrad_update")
     return dx, gw, gb, fused.value
 
 
+@pytest.mark.parametrize("fuse", [1, 0])
 @pytest.mark.parametrize("winner", [True, False])
 @pytest.mark.parametrize("M,N,K", [(2048, 5120, 1280), (2048, 1280, 1280), (4096, 1280, 1280), (1024, 2560, 640),
                                    (300, 384, 256)])
-def test_dgrad_wgrad_update_matches_two_pass(M, N, K, winner):
+def test_dgrad_wgrad_update_matches_two_pass(M, N, K, winner, fuse):
     """concord_dgrad_wgrad_update against concord_dgrad_wgrad_vhat followed by
     concord_apply_adamw, two steps in a row from the same state: dx, the
     grad_W copy, the bias gradient, v_row, v_col, 1 / sum v_row, the
     watermarks, the salt, the packed words and coh_pre all bit-identical.
-    At the north-star shape the combined launch must carry the update, and
-    its grid barriers must not report a fault."""
+    fuse = 1: at the north-star shape the combined launch must carry the
+    update, and its grid barriers must not report a fault; fuse = 0: the
+    separate launches, 1 / sum v_row formed in the update from the
+    finalize's 256-row totals."""
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(M + N + K + winner)
     packed, re, ce = rand_state(rng, N, K, exp=(-8, 7), col=(-3, 3))
@@ -1531,14 +1535,14 @@ def test_dgrad_wgrad_update_matches_two_pass(M, N, K, winner):
                   None if winner else cp0.clone()]
             out = []
             for dy in dys:
-                dx, gw, gb, fused = _update_backward(pb, combined, dy, x, st, winner, 5e-4)
+                dx, gw, gb, fused = _update_backward(pb, combined, dy, x, st, winner, 5e-4, fuse)
                 sync()
                 out.append(([host(t) for t in (dx, gw, gb)] + [host(t) for t in st if t is not None] +
                             [host(pb._get_step_counter(DEV))], fused))
             runs.append(out)
         for (a, fused), (b, _) in zip(*runs):
-            if (M, N, K) == (2048, 5120, 1280):
-                assert fused == 1
+            if (M, N, K) == (2048, 5120, 1280) or not fuse:
+                assert fused == fuse
             for u, v in zip(a, b):
                 np.testing.assert_array_equal(u, v)
         assert not pb.wgrad_update_faults(DEV)
