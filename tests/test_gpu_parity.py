@@ -1505,7 +1505,7 @@ def _update_backward(pb, combined, dy, x, st, winner, lr, fuse=1):
 @pytest.mark.parametrize("fuse", [1, 0])
 @pytest.mark.parametrize("winner", [True, False])
 @pytest.mark.parametrize("M,N,K", [(2048, 5120, 1280), (2048, 1280, 1280), (4096, 1280, 1280), (1024, 2560, 640),
-                                   (300, 384, 256)])
+                                   (300, 384, 256), (0, 320, 192)])
 def test_dgrad_wgrad_update_matches_two_pass(M, N, K, winner, fuse):
     """concord_dgrad_wgrad_update against concord_dgrad_wgrad_vhat followed by
     concord_apply_adamw, two steps in a row from the same state: dx, the
