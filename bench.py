@@ -897,7 +897,8 @@ def main():
                                 t_fwd),
         "bwd_products": bwd_roof("bwd_products", "gemm_dgt_kernel<DGRAD, 256, 128> + gemm_tr_kernel<256, 128, "
                                  "4, 2, VH> carrying the dgrad's split-K reduction + vhat_finalize_kernel "
-                                 "(the step's backward entry: dgrad and wgrad, 4 M N K FLOP)", t_bwd),
+                                 "(concord_dgrad_wgrad_vhat, the step's two products and v-hat EMA, which the step runs through "
+                                 "concord_dgrad_wgrad_update before its update; 4 M N K FLOP)", t_bwd),
         "dqgemm_dgrad": gemm_roof("dqgemm_dgrad", "gemm_dgt_kernel<DGRAD, 256, 128> + splitk_reduce_kernel "
                                   "(fused dequant-GEMM dgrad, 3-way split reduction)", t_dgrad),
         "wgrad_vhat": gemm_roof("wgrad_vhat", "gemm_tr_kernel<256, 128, 4, 2, VH> + vhat_finalize_kernel "
