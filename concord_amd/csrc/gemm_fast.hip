@@ -1986,7 +1986,7 @@ struct FastPlan { int shape, splits, ti, tj; int64_t r_split; };
 // upper triangle (sym_tile_count of them; gemm_tile_of)
 template <int NS>
 static FastPlan plan(const FastShape (&shapes)[NS], int64_t I, int64_t J, int64_t R, size_t room,
-                     bool sym = false) {
+                     bool sym = false, double sym_part_cost = 2.2) {
   FastPlan best{0, 1, 0, 0, R};
   double best_cost = 1e300;
   for (int s = 0; s < NS; ++s) {
@@ -2009,7 +2009,8 @@ static FastPlan plan(const FastShape (&shapes)[NS], int64_t I, int64_t J, int64_
       // share of it when symmetric) and the reduction reads them back, 8 B
       // per element and split at ~5 TB/s, in the units of per_block (~0.73 ps
       // per unit for an 8-wave tile at full occupancy)
-      if (sp > 1) cost += sym ? (double)sp * tiles * shapes[s].bi * shapes[s].bj * 2.2 : (double)sp * I * J * 2.2;
+      if (sp > 1)
+        cost += sym ? (double)sp * tiles * shapes[s].bi * shapes[s].bj * sym_part_cost : (double)sp * I * J * 2.2;
       if (cost < best_cost * 0.999) {
         best_cost = cost;
         best = FastPlan{s, sp, (int)ti, (int)tj, rs};
@@ -2157,10 +2158,16 @@ static int plan_gi(int mode, const FastPlan& p, int BI, int BJ) {
   return choose_gi(p.ti, p.tj, p.splits, BI * band_bytes_a(mode), BJ * band_bytes_b(mode));
 }
 
+// sym_part_cost: the split-K partial cost of a symmetric product run by the
+// dgrad kernel, measured rather than modelled: NS5's A A (1280 x 1280 x 1280,
+// 40 upper-triangle tiles of 192 x 128) ran 382.5 us per drive with 3 splits
+// against 389.8 us with the 4 the plain coefficient picks (and 384.4 with 2);
+// the forward kernel's X X^T keeps the plain coefficient (6 splits, best of
+// 4, 5, 6 and 8 in the same sweep)
 static FastPlan plan_mode(int mode, int64_t I, int64_t J, int64_t R, size_t room, bool sym = false) {
   if (mode == MODE_FWD || mode == MODE_FWD_BF16) return plan(kFwdShapes, I, J, R, room, sym);
   if (mode == MODE_WGRAD) return plan(kWgrShapes, I, J, R, room);
-  return plan(kColShapes, I, J, R, room, sym);
+  return plan(kColShapes, I, J, R, room, sym, 4.0);
 }
 
 static const FastShape& shape_of(int mode, int idx) {

@@ -164,85 +164,116 @@ CONCORD_DEV int32_t adamw_element(int32_t word, float g, int32_t te, float vr, f
 template <bool RATIO>
 __global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
   __shared__ int32_t s_cmax[4][256];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave in a scalar register: the row walk below is scalar control flow
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t kb = (int64_t)blockIdx.x * 256;
   const int64_t k0 = kb + lane * 4;
-  Uniform U;
-  U.lr = *a.s.lr;
-  U.eps = *a.s.eps;
-  U.chase_floor = RATIO ? *a.s.chase_floor : 0.0f;
-  U.leak_floor = RATIO ? *a.s.leak_floor : 0.0f;
-  U.v_bc = 1.0f;
-  U.cons = 1;
-  U.consf = 1.0f;
-  U.salt = *a.s.salt_counter;
-  if (a.bsum) {
-    float tot = 0.0f;
-    for (int64_t c0 = 0; c0 < a.nbsum; c0 += 64) {
-      const float v = c0 + lane < a.nbsum ? a.bsum[c0 + lane] : 0.0f;
-      const int cnt = (int)min((int64_t)64, a.nbsum - c0);
-      for (int j = 0; j < cnt; ++j) tot = __fadd_rn(tot, lane_value(v, j));
-    }
-    U.svi = __fdiv_rn(1.0f, fmaxf(tot, 1e-30f));
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.svi_out = U.svi;
-  } else {
-    U.svi = *a.sum_v_inv;
-  }
   const bool track = a.flags & CONCORD_TRACK_REBALANCE;
   const bool emit = a.flags & CONCORD_EMIT_WEIGHT;
   const float C = a.p.drift_cancel_C, alpha = a.p.alpha, avf = a.p.alpha_v_fast;
-  const float lr_kappa = __fmul_rn(U.lr, a.p.gf_consol);
-
+  Uniform U;
+  float lr_kappa = 0.0f;
   int32_t ce[4], cmax[4];
   float vc[4];
+  // the per-block set-up: the scalars, 1 / sum v_row, the lane's column
+  // exponents and v_col (issued after the wave's first row loads, so that
+  // both round trips overlap)
+  auto setup = [&]() {
+    U.lr = *a.s.lr;
+    U.eps = *a.s.eps;
+    U.chase_floor = RATIO ? *a.s.chase_floor : 0.0f;
+    U.leak_floor = RATIO ? *a.s.leak_floor : 0.0f;
+    U.v_bc = 1.0f;
+    U.cons = 1;
+    U.consf = 1.0f;
+    U.salt = *a.s.salt_counter;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const bool ok = k0 + j < a.K;
-    ce[j] = ok ? (int32_t)a.col_exp[k0 + j] : 0;
-    vc[j] = ok ? a.v_col[k0 + j] : 0.0f;
-    cmax[j] = 0;
-  }
-  // one row of the lane's 4 columns; FULL: all 256 columns of the block lie
-  // inside the matrix (uniform over the block), so no lane masks its loads,
-  // stores or watermark terms
-  auto row = [&](int64_t n, auto full_c) {
-    constexpr bool FULL = decltype(full_c)::value;
-    const bool full = FULL || k0 + 4 <= a.K;
-    const int32_t te_row = (int32_t)a.row_exp[n] - a.p.mantissa_bias;
-    const float vr = a.v_row[n];
-    const int32_t psr = wshl((int32_t)n, 16) ^ U.salt;
-    int32_t w[4];
-    float g[4], cp[4];
-    int32_t* pp = a.packed + n * a.ld_p + k0;
-    const uint16_t* gp = a.grad + n * a.ld_g + k0;
-    float* cpp = RATIO ? nullptr : a.coh_pre + n * a.ld_c + k0;
-    if (full) {
-      const int4 wv = *reinterpret_cast<const int4*>(pp);
-      const uint2 gv = *reinterpret_cast<const uint2*>(gp);
-      w[0] = wv.x; w[1] = wv.y; w[2] = wv.z; w[3] = wv.w;
-      g[0] = __uint_as_float(gv.x << 16);
-      g[1] = __uint_as_float(gv.x & 0xFFFF0000u);
-      g[2] = __uint_as_float(gv.y << 16);
-      g[3] = __uint_as_float(gv.y & 0xFFFF0000u);
-      if (!RATIO) {
-        const float4 cv = *reinterpret_cast<const float4*>(cpp);
-        cp[0] = cv.x; cp[1] = cv.y; cp[2] = cv.z; cp[3] = cv.w;
+    for (int j = 0; j < 4; ++j) {
+      const bool ok = k0 + j < a.K;
+      ce[j] = ok ? (int32_t)a.col_exp[k0 + j] : 0;
+      vc[j] = ok ? a.v_col[k0 + j] : 0.0f;
+      cmax[j] = 0;
+    }
+    if (a.bsum) {
+      float tot = 0.0f;
+      for (int64_t c0 = 0; c0 < a.nbsum; c0 += 64) {
+        const float v = c0 + lane < a.nbsum ? a.bsum[c0 + lane] : 0.0f;
+        const int cnt = (int)min((int64_t)64, a.nbsum - c0);
+        for (int j = 0; j < cnt; ++j) tot = __fadd_rn(tot, lane_value(v, j));
       }
+      U.svi = __fdiv_rn(1.0f, fmaxf(tot, 1e-30f));
+      if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *a.svi_out = U.svi;
     } else {
+      U.svi = *a.sum_v_inv;
+    }
+    lr_kappa = __fmul_rn(U.lr, a.p.gf_consol);
+  };
+
+  // one row's inputs for the lane's 4 columns, as loaded
+  struct RowIn {
+    int4 w;
+    uint2 g;      // 4 bf16
+    float4 c;     // coh_pre (1.0 when unused)
+    int32_t re;   // row exponent
+    float vr;
+  };
+  // FULL: all 256 columns of the block lie inside the matrix (uniform over
+  // the block), so no lane masks its loads, stores or watermark terms.
+  // No branch around any load: a lane past column K - 1 reads column K - 1
+  // and drops the value, so the count of loads in flight is the same on
+  // every path and the wait for a row never drains the next row's loads
+  auto load_row = [&](int64_t n, RowIn& in, auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    in.re = a.row_exp[n];
+    in.vr = a.v_row[n];
+    const int32_t* pp = a.packed + n * a.ld_p;
+    const uint16_t* gp = a.grad + n * a.ld_g;
+    const float* cpp = RATIO ? nullptr : a.coh_pre + n * a.ld_c;
+    if (FULL) {
+      in.w = *reinterpret_cast<const int4*>(pp + k0);
+      in.g = *reinterpret_cast<const uint2*>(gp + k0);
+      in.c = RATIO ? make_float4(1.0f, 1.0f, 1.0f, 1.0f) : *reinterpret_cast<const float4*>(cpp + k0);
+    } else {
+      int32_t w[4];
+      uint32_t h[4];
+      float c[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const bool ok = k0 + j < a.K;
-        w[j] = ok ? pp[j] : 0;
-        g[j] = ok ? bf16_to_f32(gp[j]) : 0.0f;
-        cp[j] = (!RATIO && ok) ? cpp[j] : 1.0f;
+        const int64_t kj = ok ? k0 + j : a.K - 1;
+        const int32_t wl = pp[kj];
+        const uint32_t hl = gp[kj];
+        w[j] = ok ? wl : 0;
+        h[j] = ok ? hl : 0u;
+        if (RATIO) {
+          c[j] = 1.0f;
+        } else {
+          const float cl = cpp[kj];
+          c[j] = ok ? cl : 1.0f;
+        }
       }
+      in.w = make_int4(w[0], w[1], w[2], w[3]);
+      in.g = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+      in.c = make_float4(c[0], c[1], c[2], c[3]);
     }
+  };
+  auto compute_row = [&](int64_t n, const RowIn& in, auto full_c) {
+    constexpr bool FULL = decltype(full_c)::value;
+    const bool full = FULL || k0 + 4 <= a.K;
+    const int32_t te_row = in.re - a.p.mantissa_bias;
+    const int32_t psr = wshl((int32_t)n, 16) ^ U.salt;
+    const int32_t w[4] = {in.w.x, in.w.y, in.w.z, in.w.w};
+    const float g[4] = {__uint_as_float(in.g.x << 16), __uint_as_float(in.g.x & 0xFFFF0000u),
+                        __uint_as_float(in.g.y << 16), __uint_as_float(in.g.y & 0xFFFF0000u)};
+    float cp[4] = {in.c.x, in.c.y, in.c.z, in.c.w};
+    int32_t* pp = a.packed + n * a.ld_p + k0;
+    float* cpp = RATIO ? nullptr : a.coh_pre + n * a.ld_c + k0;
     int32_t out[4], m[4];
     int32_t rmax = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int32_t te = te_row + ce[j];
-      out[j] = adamw_element_fast<RATIO>(w[j], g[j], exp2i(te), exp2i(-te), vr, vc[j], &cp[j],
+      out[j] = adamw_element_fast<RATIO>(w[j], g[j], exp2i(te), exp2i(-te), in.vr, vc[j], &cp[j],
                                          psr ^ (int32_t)(k0 + j), C, alpha, avf, lr_kappa, U, &m[j]);
       const int32_t am = (full || k0 + j < a.K) ? abs(m[j]) : 0;
       rmax = max(rmax, am);
@@ -276,15 +307,31 @@ __global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
       if (lane == 0) atomicMax(a.row_max + n, rmax);
     }
   };
-  const bool full_blk = kb + 256 <= a.K;
-  // row blocks blockIdx.y, blockIdx.y + gridDim.y, ... (grid.y <= kMaxGridY)
-  for (int64_t nb = (int64_t)blockIdx.y * a.tn; nb < a.N; nb += (int64_t)gridDim.y * a.tn)
-  for (int r = wave; r < a.tn; r += 4) {
-    const int64_t n = nb + r;
-    if (n >= a.N) break;
-    if (full_blk) row(n, std::true_type());
-    else row(n, std::false_type());
-  }
+  // the wave's rows: row blocks blockIdx.y, blockIdx.y + gridDim.y, ...
+  // (grid.y <= kMaxGridY) of tn rows each, rows wave, wave + 4, ... of each;
+  // the next row's loads go out before the current row's arithmetic
+  // the loads of a row past the last (the walk's end) read row N - 1
+  auto run = [&](auto full_c) {
+    const int64_t step = (int64_t)gridDim.y * a.tn;
+    int64_t nb = (int64_t)blockIdx.y * a.tn;
+    int r = wave;
+    RowIn cur, nxt;
+    load_row(min(nb + r, a.N - 1), cur, full_c);
+    setup();
+    while (nb + r < a.N) {
+      const int64_t n = nb + r;
+      r += 4;
+      if (r >= a.tn || nb + r >= a.N) {
+        nb += step;
+        r = wave;
+      }
+      load_row(min(nb + r, a.N - 1), nxt, full_c);
+      compute_row(n, cur, full_c);
+      cur = nxt;
+    }
+  };
+  if (kb + 256 <= a.K) run(std::true_type());
+  else run(std::false_type());
   if (track) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) s_cmax[wave][lane * 4 + j] = cmax[j];
