@@ -155,6 +155,15 @@ struct RowsBf16 {
     for (int q = 0; q < PER; ++q)
       *reinterpret_cast<i32x4*>(lds + (t / 8 + (NT / 8) * q) * LDS_STRIDE + kc) = r.v[q];
   }
+  // into the swizzled [row][64] tile (swz_off): the thread's 16-byte chunk
+  // kc / 8 of rows t / 8 + (NT / 8) q, whose (row >> 1) & 7 is the same for
+  // every q
+  CONCORD_DEV void store_swz(Raw& r, uint16_t* lds, int t) const {
+    const int c = (((t % 8) ^ ((t / 8) >> 1)) & 7) * 8;
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+      *reinterpret_cast<i32x4*>(lds + (t / 8 + (NT / 8) * q) * 64 + c) = r.v[q];
+  }
 };
 
 // packed [rows][R] int32, r contiguous (the forward's W[n][k]); chunk = 4
@@ -188,7 +197,8 @@ struct RowsPacked {
     for (int q = 0; q < PER; ++q) r.v[q] = ld128(rs, ok ? voff[q] : kOOB, so);
     r.ex = ld32(es, ok ? (uint32_t)kc : kOOB, (uint32_t)r0);
   }
-  CONCORD_DEV void store(Raw& r, uint16_t* lds, int t) const {
+  template <bool SWZ = false>
+  CONCORD_DEV void store(Raw& r, uint16_t* lds, int t, int swz_col = 0) const {
     pin(r.ex);
 #pragma unroll
     for (int q = 0; q < PER; ++q) pin(r.v[q]);
@@ -199,8 +209,20 @@ struct RowsPacked {
       uint2 o;
       o.x = pack_bf16x2(dec(r.v[q].x, e0), dec(r.v[q].y, e1));
       o.y = pack_bf16x2(dec(r.v[q].z, e2), dec(r.v[q].w, e3));
-      *reinterpret_cast<uint2*>(lds + (t / 16 + (NT / 16) * q) * LDS_STRIDE + kc) = o;
+      if (SWZ)
+        *reinterpret_cast<uint2*>(lds + (t / 16 + (NT / 16) * q) * 64 + swz_col) = o;
+      else
+        *reinterpret_cast<uint2*>(lds + (t / 16 + (NT / 16) * q) * LDS_STRIDE + kc) = o;
     }
+  }
+  // the thread's 4 columns kc .. kc + 3 (half of 16-byte chunk kc / 8) in the
+  // swizzled [row][64] tile; (row >> 1) & 7 is the same for all its rows
+  CONCORD_DEV int swz_cols(int t) const {
+    return ((((t % 16) >> 1) ^ ((t / 16) >> 1)) & 7) * 8 + (t & 1) * 4;
+  }
+  template <bool S = true>
+  CONCORD_DEV void store_swz(Raw& r, uint16_t* lds, int t) const {
+    store<S>(r, lds, t, swz_cols(t));
   }
 };
 
@@ -1193,12 +1215,14 @@ struct RowsDmaConv {
   }
 };
 
-// MFMAs of one stage: A from a swizzled DMA tile, B from a padded tile.
+// MFMAs of one stage: A and B from [row][64] tiles whose 16-byte chunk c of
+// row r sits at chunk c ^ ((r >> 1) & 7) (the A tile written by DMA, the B
+// tile by the producer waves' store_swz); ra and rb are multiples of 16
 template <int NI, int NJ>
 CONCORD_DEV void stage_mfma_swz(f32x4 (&acc)[NI][NJ], const uint16_t* la, const uint16_t* lb, int ra, int rb,
                                 int lane) {
-  const int lrow = lane & 15, lk = (lane >> 4) * 8;
-  const int sw = (lane & 14) >> 1;   // (row >> 1) & 7 for row = ra + 16x + lrow
+  const int lrow = lane & 15;
+  const int sw = (lane & 14) >> 1;   // (row >> 1) & 7 for row = ra + 16x + lrow (or rb + 16y + lrow)
 #pragma unroll
   for (int kk = 0; kk < TR / 32; ++kk) {
     const int aoff = lrow * 64 + (((kk * 4 + (lane >> 4)) ^ sw) * 8);
@@ -1208,8 +1232,7 @@ CONCORD_DEV void stage_mfma_swz(f32x4 (&acc)[NI][NJ], const uint16_t* la, const 
       fa[x] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(la + (ra + x * 16) * 64 + aoff));
 #pragma unroll
     for (int y = 0; y < NJ; ++y)
-      fb[y] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(
-                                             lb + (rb + y * 16 + lrow) * LDS_STRIDE + kk * 32 + lk));
+      fb[y] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const i32x4*>(lb + (rb + y * 16) * 64 + aoff));
 #pragma unroll
     for (int x = 0; x < NI; ++x)
 #pragma unroll
@@ -1247,7 +1270,7 @@ template <int BJ, int NT> struct BSide<MODE_DGRAD_BF16, BJ, NT> {
 
 // 8 waves: waves 0-3 compute and move A by DMA (stage s+2 while computing s),
 // waves 4-7 load B three stages ahead in registers, decode it and write it
-// into a double-buffered padded LDS tile.  One LDS barrier per stage; before
+// into a double-buffered swizzled LDS tile (the A tile's layout).  One LDS barrier per stage; before
 // it every compute wave waits until its own DMA of the next stage has landed.
 // CONV: the A operand is the conv forward's gathered x (RowsDmaConv).
 template <int MODE, int BI, int BJ, int CONV = 0>
@@ -1260,7 +1283,7 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
   constexpr int LB = decltype(BS::b)::LROWS;
   static_assert(LB >= BJ, "LDS tile rows");
   __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
-  __shared__ __attribute__((aligned(16))) uint16_t lds_b[2][LB * LDS_STRIDE];
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_b[2][LB * 64];
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -1291,7 +1314,7 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
     auto stage_r = [&](int st) { return r_begin + (int64_t)st * TR; };
     bs.b.load(r0, stage_r(0), r_end - stage_r(0));
     bs.b.load(r1, stage_r(1), r_end - stage_r(1));
-    bs.b.store(r0, lds_b[0], tp);
+    bs.b.store_swz(r0, lds_b[0], tp);
     bs.b.load(r0, stage_r(2), r_end - stage_r(2));
     lds_barrier();
     // iteration s: stage s+1 -> LDS buffer (s+1)&1, then stage s+3 into its
@@ -1300,10 +1323,10 @@ __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
     // the compiler sees the same order of outstanding loads from the prologue
     // and from the loop.
     for (int s = 0; s < nst2; s += 2) {
-      bs.b.store(r1, lds_b[1], tp);
+      bs.b.store_swz(r1, lds_b[1], tp);
       bs.b.load(r1, stage_r(s + 3), r_end - stage_r(s + 3));
       lds_barrier();
-      bs.b.store(r0, lds_b[0], tp);
+      bs.b.store_swz(r0, lds_b[0], tp);
       bs.b.load(r0, stage_r(s + 4), r_end - stage_r(s + 4));
       lds_barrier();
     }
