@@ -193,11 +193,22 @@ int gemm_wgrad_vhat_launch(const GemmArgs& g, size_t split_room, hipStream_t st,
 int gemm_wgrad_vhat_split_launch(const GemmArgs& g, void* workspace, size_t ws_bytes, hipStream_t st,
                                  const char* what, int* bias_rows);
 // dgrad (split, its reduction deferred) then the VH WGRAD whose spare
-// workgroups run that reduction on the CUs the WGRAD tiles leave idle; -1
-// when the shapes do not take this path (the caller then issues the two
+// workgroups run that reduction on the CUs the WGRAD tiles leave idle; or,
+// when both grids fit the chip at once, both products in one launch
+// (gemm_dgt_tr_kernel) and the dgrad's reduction after it: left to the
+// caller when `pending` is given (*pending_rbi = its tile rows, 0 = none; the
+// caller passes them to vhat_finish_carry_launch), else launched here.  -1
+// when the shapes do not take these paths (the caller then issues the two
 // products separately).  The dgrad's split-K partials use `workspace`.
 int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd, void* workspace, size_t ws_bytes, const GemmArgs& gw,
-                                 hipStream_t st, const char* what, int* tiles_j);
+                                 hipStream_t st, const char* what, int* tiles_j, GemmArgs* pending = nullptr,
+                                 int* pending_rbi = nullptr);
+// vhat_finish_launch's finalize with a dgrad's split-K reduction (rd, tile rows
+// rbi, from gemm_dgrad_wgrad_vhat_launch) carried by extra blocks of the launch
+void vhat_finish_carry_launch(const float* pr, const float* pc, float* bsum, uint32_t* ticket, int64_t N, int64_t K,
+                              double beta2, float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max,
+                              int32_t* col_max, int32_t* salt, hipStream_t st, const float* bpart, int64_t nbp,
+                              uint16_t* grad_bias, const GemmArgs& rd, int rbi);
 // tiles along J of the WGRAD launch above (the bias partials' row count)
 int64_t gemm_wgrad_vhat_tiles_j(int64_t J);
 // the other pairing: a split WGRAD with v-hat partials first, then the unsplit

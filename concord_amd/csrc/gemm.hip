@@ -609,9 +609,11 @@ static int wgrad_vhat_impl(const GemmArgs* gd, const uint16_t* dy, int64_t ld_dy
   g.bpart = grad_bias ? bpart : nullptr;
   int tiles_j = 0;
   int rc = -1;
+  GemmArgs pend;        // a dgrad split-K reduction the finalize launch carries
+  int pend_rbi = 0;
   if (gd && gd->I > 0 && gd->J > 0) {
     rc = gemm_dgrad_wgrad_vhat_launch(*gd, gemm_workspace, gemm_workspace ? gemm_workspace_bytes : 0, g, st,
-                                      what, &tiles_j);
+                                      what, &tiles_j, &pend, &pend_rbi);
     if (rc == -1)
       rc = gemm_wgrad_split_dgrad_launch(*gd, g, gemm_workspace, gemm_workspace ? gemm_workspace_bytes : 0, st,
                                          what, &tiles_j);
@@ -633,6 +635,9 @@ static int wgrad_vhat_impl(const GemmArgs* gd, const uint16_t* dy, int64_t ld_dy
                        salt_counter, st);
   } else if (rc != CONCORD_OK) {
     return rc;
+  } else if (pend_rbi) {
+    vhat_finish_carry_launch(pr, pc, bsum, ticket, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max,
+                             salt_counter, st, bpart, tiles_j, grad_bias, pend, pend_rbi);
   } else {
     vhat_finish_launch(pr, pc, bsum, ticket, N, K, beta2, v_row, v_col, sum_v_inv, row_max, col_max,
                        salt_counter, st, bpart, tiles_j, grad_bias);

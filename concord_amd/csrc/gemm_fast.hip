@@ -27,6 +27,7 @@
 #include <cmath>
 
 #include "gemm.h"
+#include "vhat_finalize.h"
 #include "vhat_tile.h"
 #include "wgrad_update.h"
 #include "workspace.h"
@@ -1573,7 +1574,8 @@ CONCORD_DEV void bias_acc(f32x4 (&b)[NI], const bf16x8 (&fa)[NI]) {
 // workgroups update their tiles from the accumulators, and the bf16 weight
 // gradient is stored only when g.c is set.
 template <int BI, int BJ, int WI, int WJ, bool VH, bool CONV, int RBI, int UPD>
-CONCORD_DEV void gemm_tr_body(const GemmArgs& g, const GemmArgs& rd, int tr_blocks, const WgradUpd& u) {
+CONCORD_DEV void gemm_tr_body(const GemmArgs& g, const GemmArgs& rd, int tr_blocks, const WgradUpd& u, uint32_t wg,
+                              uint32_t ngrid, uint16_t* ring_mem, int* s_flag_mem) {
   constexpr int NW = WI * WJ, NT = 64 * NW, WTI = BI / WI, WTJ = BJ / WJ;
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
   typedef TrDma<BI, NW> DA;
@@ -1582,17 +1584,19 @@ CONCORD_DEV void gemm_tr_body(const GemmArgs& g, const GemmArgs& rd, int tr_bloc
   constexpr int PERT = DA::PER + DB::PER;
   static_assert(TR == 64, "two 32-deep MFMA steps per stage");
   static_assert(UPD == 0 || (VH && !CONV && NW == 8), "the update rides on the VH launch of 8 waves");
-  __shared__ __attribute__((aligned(1024))) uint16_t ring[3 * STAGE / 2];
+  // the LDS ring (at least TR_RING_BYTES, 1024-aligned) and the barrier flag
+  typedef uint16_t Ring[3 * STAGE / 2];
+  Ring& ring = *reinterpret_cast<Ring*>(ring_mem);
+  int& s_flag = *s_flag_mem;
   static_assert(sizeof(ring) >= (size_t)BI * (BJ + 8) * 2, "output staging fits in the ring");
-  __shared__ int s_flag;
-  if (VH && (int)blockIdx.x >= tr_blocks) {
+  if (VH && (int)wg >= tr_blocks) {
     const int64_t items = splitk_reduce_items<CONCORD_DGRAD_REDUCE>(rd);
-    const int64_t stride = (int64_t)(gridDim.x - tr_blocks) * NT;
-    for (int64_t idx = (int64_t)(blockIdx.x - tr_blocks) * NT + threadIdx.x; idx < items; idx += stride)
+    const int64_t stride = (int64_t)(ngrid - tr_blocks) * NT;
+    for (int64_t idx = (int64_t)(wg - tr_blocks) * NT + threadIdx.x; idx < items; idx += stride)
       splitk_reduce_item<CONCORD_DGRAD_REDUCE>(rd, idx);
     if constexpr (UPD != 0) {
-      if (!grid_sync(u, gridDim.x, &s_flag)) upd_finalize(g, u, reinterpret_cast<float*>(ring));
-      grid_sync(u, 2 * gridDim.x, &s_flag);
+      if (!grid_sync(u, ngrid, &s_flag)) upd_finalize(g, u, reinterpret_cast<float*>(ring));
+      grid_sync(u, 2 * ngrid, &s_flag);
       grid_exit(u);
     }
     return;
@@ -1600,7 +1604,6 @@ CONCORD_DEV void gemm_tr_body(const GemmArgs& g, const GemmArgs& rd, int tr_bloc
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int wg = blockIdx.x;
   int split, bi, bj;
   split_tile_of(wg, g.tiles_i, g.tiles_j, g.splits, split, bi, bj, g.gi > 0 ? g.gi : 8);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
@@ -1717,9 +1720,9 @@ CONCORD_DEV void gemm_tr_body(const GemmArgs& g, const GemmArgs& rd, int tr_bloc
     epilogue<MODE_WGRAD, NI, NJ, BI, BJ, NW>(g, acc, i0, j0, wi * WTI, wj * WTJ, split, bi * g.tiles_j + bj, wave, t,
                                              NT, ring);
   if constexpr (UPD != 0) {
-    const bool bad = grid_sync(u, gridDim.x, &s_flag);
+    const bool bad = grid_sync(u, ngrid, &s_flag);
     if (!bad) upd_finalize(g, u, reinterpret_cast<float*>(ring));
-    if (!grid_sync(u, 2 * gridDim.x, &s_flag) && !bad) {
+    if (!grid_sync(u, 2 * ngrid, &s_flag) && !bad) {
       int32_t* lds = reinterpret_cast<int32_t*>(ring);
       upd_apply<UPD == 2>(g, u, acc, i0, j0, wi, wj, lds, lds + 512);
     }
@@ -1727,16 +1730,28 @@ CONCORD_DEV void gemm_tr_body(const GemmArgs& g, const GemmArgs& rd, int tr_bloc
   }
 }
 
+// LDS bytes of gemm_tr_body's ring
+template <int BI, int BJ>
+constexpr int tr_ring_bytes() { return 3 * (TR * BI * 2 + TR * BJ * 2); }
+
+// one LDS array per kernel: the ring at offset 0 (its swizzled addresses fold
+// into instruction offsets), the barrier flag after it
 template <int BI, int BJ, int WI, int WJ, bool VH, bool CONV = false, int RBI = 256>
 __global__ __launch_bounds__(64 * WI * WJ, 1) void gemm_tr_kernel(GemmArgs g, GemmArgs rd, int tr_blocks) {
-  gemm_tr_body<BI, BJ, WI, WJ, VH, CONV, RBI, 0>(g, rd, tr_blocks, WgradUpd{});
+  __shared__ __attribute__((aligned(1024))) char lds[tr_ring_bytes<BI, BJ>() + 16];
+  gemm_tr_body<BI, BJ, WI, WJ, VH, CONV, RBI, 0>(g, rd, tr_blocks, WgradUpd{}, blockIdx.x, gridDim.x,
+                                                 reinterpret_cast<uint16_t*>(lds),
+                                                 reinterpret_cast<int*>(lds + tr_ring_bytes<BI, BJ>()));
 }
 
 // the WGRAD launch of the backward entry carrying the finalize and the update
 // (wgrad_update.h); RBI = the dgrad reduction's tile rows, UPD = 1 bare, 2 winner
 template <int RBI, int UPD>
 __global__ __launch_bounds__(512, 1) void wgrad_update_kernel(GemmArgs g, GemmArgs rd, int tr_blocks, WgradUpd u) {
-  gemm_tr_body<256, 128, 4, 2, true, false, RBI, UPD>(g, rd, tr_blocks, u);
+  __shared__ __attribute__((aligned(1024))) char lds[tr_ring_bytes<256, 128>() + 16];
+  gemm_tr_body<256, 128, 4, 2, true, false, RBI, UPD>(g, rd, tr_blocks, u, blockIdx.x, gridDim.x,
+                                                      reinterpret_cast<uint16_t*>(lds),
+                                                      reinterpret_cast<int*>(lds + tr_ring_bytes<256, 128>()));
 }
 
 // ---- DGRAD with a row-major weight tile and transpose reads -------------------
@@ -1853,24 +1868,35 @@ CONCORD_DEV void stage_mfma_swz_tr(f32x4 (&acc)[NI][NJ], const uint16_t* la, con
 // reduction with v-hat partials (splitk_reduce_vh_kernel's blocks, two per
 // workgroup) of the WGRAD launch `rw` issued just before on the stream, on
 // the CUs the dgrad grid leaves idle.
+// LDS of gemm_dgt_body: three A stage tiles of BI x 64 bf16 (dgt_a_bytes)
+// and two B stage tiles of the weight loader (dgt_b_bytes each), each set
+// 1024-aligned
+template <int BI>
+constexpr int dgt_a_bytes() { return 3 * BI * 64 * 2; }
+template <int MODE, int BJ, int CONV>
+constexpr int dgt_b_bytes() { return TrRowsB<BJ, 256, MODE == MODE_DGRAD, (CONV != 0)>::LBYTES; }
+
 template <int MODE, int BI, int BJ, int CONV, bool CARRY>
-CONCORD_DEV void gemm_dgt_body(const GemmArgs& g, const GemmArgs& rw, int dg_blocks) {
+CONCORD_DEV void gemm_dgt_body(const GemmArgs& g, const GemmArgs& rw, int dg_blocks, int wg, int ngrid,
+                               uint16_t* lds_a_mem, char* lds_b_mem) {
   constexpr int NP = 256;
   constexpr int WTI = BI / 2, WTJ = BJ / 2;
   constexpr int NI = WTI / 16, NJ = WTJ / 16;
   typedef TrRowsB<BJ, NP, MODE == MODE_DGRAD, (CONV != 0)> BL;
   typedef typename std::conditional<CONV != 0, RowsDmaConv<BI, 4, true, CONV == 1>, RowsDma<BI, 4>>::type AD;
-  __shared__ __attribute__((aligned(1024))) uint16_t lds_a[3][BI * 64];
-  __shared__ __attribute__((aligned(1024))) char lds_b[2][BL::LBYTES];
+  typedef uint16_t LdsA[3][BI * 64];
+  typedef char LdsB[2][BL::LBYTES];
+  LdsA& lds_a = *reinterpret_cast<LdsA*>(lds_a_mem);
+  LdsB& lds_b = *reinterpret_cast<LdsB*>(lds_b_mem);
   if constexpr (CARRY) {
     typedef ReduceVh<256, 128, 4, 2> RV;
     static_assert(sizeof(lds_a) >= 2 * RV::LDS_FLOATS * sizeof(float), "two reduction blocks fit");
-    if ((int)blockIdx.x >= dg_blocks) {
+    if (wg >= dg_blocks) {
       const int nblk = rw.tiles_i * rw.tiles_j * RV::NAW;
       const int half = threadIdx.x >> 8, tid = threadIdx.x & 255;
       float* s_g2 = reinterpret_cast<float*>(&lds_a[0][0]) + half * RV::LDS_FLOATS;
-      const int stride = 2 * ((int)gridDim.x - dg_blocks);
-      for (int b0 = 2 * ((int)blockIdx.x - dg_blocks); b0 < nblk; b0 += stride) {
+      const int stride = 2 * (ngrid - dg_blocks);
+      for (int b0 = 2 * (wg - dg_blocks); b0 < nblk; b0 += stride) {
         const int blk = b0 + half;
         if (blk < nblk) RV::part1(rw, blk, tid, s_g2);
         __syncthreads();
@@ -1884,7 +1910,6 @@ CONCORD_DEV void gemm_dgt_body(const GemmArgs& g, const GemmArgs& rw, int dg_blo
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
   const bool producer = wave >= 4;
-  const int wg = blockIdx.x;
   int split, bi, bj, slot;
   gemm_tile_of<BI, BJ>(g, wg, split, bi, bj, slot);
   const int64_t i0 = (int64_t)bi * BI, j0 = (int64_t)bj * BJ;
@@ -1970,14 +1995,62 @@ CONCORD_DEV void gemm_dgt_body(const GemmArgs& g, const GemmArgs& rw, int dg_blo
 
 template <int MODE, int BI, int BJ, int CONV = 0>
 __global__ __launch_bounds__(512, 1) void gemm_dgt_kernel(GemmArgs g) {
-  gemm_dgt_body<MODE, BI, BJ, CONV, false>(g, g, 0);
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_a[dgt_a_bytes<BI>() / 2];
+  __shared__ __attribute__((aligned(1024))) char lds_b[2 * dgt_b_bytes<MODE, BJ, CONV>()];
+  gemm_dgt_body<MODE, BI, BJ, CONV, false>(g, g, 0, blockIdx.x, gridDim.x, lds_a, lds_b);
 }
 
 // the dgrad launch carrying the split WGRAD's v-hat reduction (rw): workgroups
 // [0, dg_blocks) compute dgrad tiles, the rest run reduction blocks
 template <int BI, int BJ>
 __global__ __launch_bounds__(512, 1) void gemm_dgt_carry_kernel(GemmArgs g, GemmArgs rw, int dg_blocks) {
-  gemm_dgt_body<MODE_DGRAD, BI, BJ, 0, true>(g, rw, dg_blocks);
+  __shared__ __attribute__((aligned(1024))) uint16_t lds_a[dgt_a_bytes<BI>() / 2];
+  __shared__ __attribute__((aligned(1024))) char lds_b[2 * dgt_b_bytes<MODE_DGRAD, BJ, 0>()];
+  gemm_dgt_body<MODE_DGRAD, BI, BJ, 0, true>(g, rw, dg_blocks, blockIdx.x, gridDim.x, lds_a, lds_b);
+}
+
+// The dgrad and the WGRAD with its v-hat partials in one launch, for batches
+// whose two grids together fit the chip at once (a few hundred tokens: each
+// product alone leaves most CUs idle, and each takes about the same fixed
+// latency of prologue, a few stages and epilogue, so in one launch they
+// overlap).  Workgroups [0, dg_blocks) run dgrad tiles (split-K partials when
+// the plan splits), the rest WGRAD tiles; both bodies compute what their own
+// launches would.  One LDS array holds either body's tiles.
+template <int DBI>
+__global__ __launch_bounds__(512, 1) void gemm_dgt_tr_kernel(GemmArgs gd, GemmArgs gw, int dg_blocks) {
+  constexpr int A = dgt_a_bytes<DBI>(), B = 2 * dgt_b_bytes<MODE_DGRAD, 128, 0>();
+  constexpr int T = tr_ring_bytes<256, 128>();
+  static_assert(A % 1024 == 0, "the dgrad's B tiles stay 1024-aligned");
+  constexpr int BYTES = A + B > T + 16 ? A + B : T + 16;
+  __shared__ __attribute__((aligned(1024))) char lds[BYTES];
+  const int wg = blockIdx.x;
+  if (wg < dg_blocks) {
+    gemm_dgt_body<MODE_DGRAD, DBI, 128, 0, false>(gd, gd, 0, wg, dg_blocks, reinterpret_cast<uint16_t*>(lds),
+                                                  lds + A);
+  } else {
+    const int tw = (int)gridDim.x - dg_blocks;   // every remaining workgroup has a tile: no carried blocks
+    gemm_tr_body<256, 128, 4, 2, true, false, 256, 0>(gw, gw, tw, WgradUpd{}, (uint32_t)(wg - dg_blocks),
+                                                      (uint32_t)tw, reinterpret_cast<uint16_t*>(lds),
+                                                      reinterpret_cast<int*>(lds + T));
+  }
+}
+
+// vhat_finalize_kernel's blocks [0, fin_blocks) and, on the rest, the split-K
+// reduction of the dgrad (rd, RBI x 128 tiles) that gemm_dgt_tr_kernel left
+// (one item per thread, as splitk_reduce_kernel)
+template <int RBI>
+__global__ __launch_bounds__(256) void vhat_finalize_carry_kernel(
+    const float* __restrict__ pr, const float* __restrict__ pc, int64_t N, int64_t K, float b2, float omb2,
+    float* v_row, float* v_col, int32_t* row_max, int32_t* col_max, float* bsum, const float* __restrict__ bpart,
+    int64_t nbp, uint16_t* grad_bias, uint32_t* ticket, float* sum_v_inv, int32_t* salt, GemmArgs rd,
+    int fin_blocks) {
+  if ((int)blockIdx.x < fin_blocks) {
+    vhat_finalize_block(blockIdx.x, pr, pc, N, K, b2, omb2, v_row, v_col, row_max, col_max, bsum, bpart, nbp,
+                        grad_bias, ticket, sum_v_inv, salt);
+    return;
+  }
+  const int64_t idx = (int64_t)(blockIdx.x - fin_blocks) * 256 + threadIdx.x;
+  if (idx < splitk_reduce_items<CONCORD_DGRAD_REDUCE>(rd)) splitk_reduce_item<CONCORD_DGRAD_REDUCE>(rd, idx);
 }
 
 // ---- planning -----------------------------------------------------------------
@@ -2290,17 +2363,24 @@ int gemm_wgrad_split_dgrad_launch(const GemmArgs& gd0, const GemmArgs& gw0, void
 }
 
 int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd0, void* workspace, size_t ws_bytes, const GemmArgs& gw0,
-                                 hipStream_t st, const char* what, int* tiles_j) {
+                                 hipStream_t st, const char* what, int* tiles_j, GemmArgs* pending,
+                                 int* pending_rbi) {
+  if (pending_rbi) *pending_rbi = 0;
   if (!eligible(MODE_DGRAD, gd0) || !eligible(MODE_WGRAD, gw0) || !tr_eligible(gw0)) return -1;
   const size_t room = (workspace && ws_bytes > kSplitkCounterBytes) ? ws_bytes - kSplitkCounterBytes : 0;
   const FastPlan pd = plan_mode(MODE_DGRAD, gd0.I, gd0.J, gd0.R, room);
   // the WGRAD plan of gemm_wgrad_vhat_launch with the same room, so that both
   // routes take the same product (and so the same bits)
   const FastPlan pw = plan_mode(MODE_WGRAD, gw0.I, gw0.J, gw0.R, room);
-  if ((pd.shape != 0 && pd.shape != 2) || pd.splits < 2 || pw.shape != 0 || pw.splits != 1) return -1;
+  if ((pd.shape != 0 && pd.shape != 2) || pw.shape != 0 || pw.splits != 1) return -1;
   const int tw = pw.ti * pw.tj;
+  const int nd = pd.ti * pd.tj * pd.splits;
+  // both grids resident at once: one launch of both products, then the
+  // dgrad's split-K reduction (gemm_dgt_tr_kernel)
+  const bool together = nd + tw <= kCUs;
+  if (!together && pd.splits < 2) return -1;
   const int extra = kCUs - tw;
-  if (extra < 16) return -1;   // the WGRAD grid leaves too few CUs to carry the reduction
+  if (!together && extra < 16) return -1;   // the WGRAD grid leaves too few CUs to carry the reduction
   GemmArgs gd = gd0;
   gd.splits = pd.splits;
   gd.r_split = pd.r_split;
@@ -2315,6 +2395,22 @@ int gemm_dgrad_wgrad_vhat_launch(const GemmArgs& gd0, void* workspace, size_t ws
   gw.tiles_j = pw.tj;
   gw.gi = plan_gi(MODE_WGRAD, pw, 256, 128);
   *tiles_j = pw.tj;
+  if (together) {
+    if (pd.splits < 2) gd.part = nullptr;
+    const bool defer = pending && pending_rbi && pd.splits > 1;
+    if (pd.shape == 0) {
+      hipLaunchKernelGGL((gemm_dgt_tr_kernel<256>), dim3(nd + tw), dim3(512), 0, st, gd, gw, nd);
+      if (!defer) launch_reduce<MODE_DGRAD, 256, 128, 2, 2>(gd, st);
+    } else {
+      hipLaunchKernelGGL((gemm_dgt_tr_kernel<192>), dim3(nd + tw), dim3(512), 0, st, gd, gw, nd);
+      if (!defer) launch_reduce<MODE_DGRAD, 192, 128, 2, 2>(gd, st);
+    }
+    if (defer) {
+      *pending = gd;
+      *pending_rbi = pd.shape == 0 ? 256 : 192;
+    }
+    return launch_status(what);
+  }
   if (pd.shape == 0) {
     hipLaunchKernelGGL((gemm_dgt_kernel<MODE_DGRAD, 256, 128>), dim3(pd.ti * pd.tj * pd.splits), dim3(512), 0, st,
                        gd);
@@ -2566,6 +2662,24 @@ size_t gemm_sym_splitk_need(int mode, int64_t I, int64_t R) {
     part = (size_t)sym_tile_count(p.ti, p.tj, sh.bi, sh.bj) * sh.bi * sh.bj * sizeof(float) * p.splits;
   }
   return kSplitkCounterBytes + ((part + 255) / 256) * 256;
+}
+
+void vhat_finish_carry_launch(const float* pr, const float* pc, float* bsum, uint32_t* ticket, int64_t N, int64_t K,
+                              double beta2, float* v_row, float* v_col, float* sum_v_inv, int32_t* row_max,
+                              int32_t* col_max, int32_t* salt, hipStream_t st, const float* bpart, int64_t nbp,
+                              uint16_t* grad_bias, const GemmArgs& rd, int rbi) {
+  const float b2 = (float)beta2;
+  const float omb2 = (float)(1.0 - beta2);
+  const int fin = (int)vhat_finalize_blocks(N, K, grad_bias != nullptr);
+  // splitk_reduce_items: tiles x 4 accumulator waves x (RBI / 32) x 4 blocks x 64 lanes
+  const int64_t items = (int64_t)rd.tiles_i * rd.tiles_j * 4 * (rbi / 32) * 4 * 64;
+  const dim3 grid((unsigned)(fin + cdiv(items, 256)));
+  if (rbi == 256)
+    hipLaunchKernelGGL(vhat_finalize_carry_kernel<256>, grid, dim3(256), 0, st, pr, pc, N, K, b2, omb2, v_row, v_col,
+                       row_max, col_max, bsum, bpart, nbp, grad_bias, ticket, sum_v_inv, salt, rd, fin);
+  else
+    hipLaunchKernelGGL(vhat_finalize_carry_kernel<192>, grid, dim3(256), 0, st, pr, pc, N, K, b2, omb2, v_row, v_col,
+                       row_max, col_max, bsum, bpart, nbp, grad_bias, ticket, sum_v_inv, salt, rd, fin);
 }
 
 }  // namespace concord

@@ -1432,13 +1432,17 @@ def test_layer_fast_gain_forward(oracle):
 
 
 @pytest.mark.parametrize("M,N,K", [(2048, 5120, 1280), (2048, 1280, 1280), (4096, 1280, 1280), (1024, 2560, 640),
-                                   (300, 384, 256)])
+                                   (300, 384, 256), (154, 1280, 2048), (308, 1280, 2048), (308, 640, 2048),
+                                   (4, 1280, 2816), (77, 320, 1280)])
 def test_dgrad_wgrad_vhat_matches_separate_calls(M, N, K):
     """The combined backward entry gives the same dx, grad_W, bias gradient,
     v-hat state, zeroed watermarks and salt as the two calls.  Where the shapes
     allow, one launch carries the other's split-K reduction: the WGRAD launch
     the dgrad's (2048 x 5120 x 1280), or the unsplit dgrad launch the split
-    WGRAD's v-hat reduction (4096 x 1280 x 1280, config 4's attention layers)."""
+    WGRAD's v-hat reduction (4096 x 1280 x 1280, config 4's attention layers).
+    For a few hundred tokens (cross-attention at 154 and 308, the M = 4
+    embedding layers, a ragged 77) both products run in one launch
+    (gemm_dgt_tr_kernel), the dgrad's split-K reduction after it."""
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(M + N + K)
     packed, re, ce = rand_state(rng, N, K, exp=(-8, 7), col=(-3, 3))
@@ -1505,7 +1509,7 @@ def _update_backward(pb, combined, dy, x, st, winner, lr, fuse=1):
 @pytest.mark.parametrize("fuse", [1, 0])
 @pytest.mark.parametrize("winner", [True, False])
 @pytest.mark.parametrize("M,N,K", [(2048, 5120, 1280), (2048, 1280, 1280), (4096, 1280, 1280), (1024, 2560, 640),
-                                   (300, 384, 256), (0, 320, 192)])
+                                   (300, 384, 256), (0, 320, 192), (154, 1280, 2048), (308, 640, 2048)])
 def test_dgrad_wgrad_update_matches_two_pass(M, N, K, winner, fuse):
     """concord_dgrad_wgrad_update against concord_dgrad_wgrad_vhat followed by
     concord_apply_adamw, two steps in a row from the same state: dx, the
