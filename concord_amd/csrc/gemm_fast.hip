@@ -717,7 +717,10 @@ struct ReduceVh {
     const float* base = g.part + (int64_t)tile * g.splits * PT + (int64_t)aw * NI * NJ * 256 + lane * 4;
     {
       // the row of 4 blocks, eight splits' partials loaded before any of them
-      // is summed (one memory round trip per eight splits), summed in order
+      // is summed (one memory round trip per eight splits), summed in order.
+      // The loads have no branch around them (a split past the last reads the
+      // last again, unused): a load under a branch let the compiler copy its
+      // result at the join, which waited for it before the rest were issued
       constexpr int CH = 8;
       static_assert(kGemmMaxSplits <= 2 * CH, "two chunks of splits");
       f32x4 sums[NJ];
@@ -729,9 +732,8 @@ struct ReduceVh {
         for (int y = 0; y < NJ; ++y)
 #pragma unroll
           for (int s2 = 0; s2 < CH; ++s2)
-            part[y][s2] = c0 + s2 < g.splits
-                              ? *reinterpret_cast<const f32x4*>(base + (x * NJ + y) * 256 + (c0 + s2) * PT)
-                              : f32x4{0.f, 0.f, 0.f, 0.f};
+            part[y][s2] = *reinterpret_cast<const f32x4*>(base + (x * NJ + y) * 256 +
+                                                          (int64_t)min(c0 + s2, g.splits - 1) * PT);
 #pragma unroll
         for (int y = 0; y < NJ; ++y) {
           if (c0 == 0) sums[y] = part[y][0];
@@ -759,8 +761,15 @@ struct ReduceVh {
       if (i < g.I) {
         float* b = g.bpart + (int64_t)bj * g.I + i;
         const int64_t rs = (int64_t)g.tiles_j * g.I;   // one split's rows
-        float sb = b[0];
-        for (int s2 = 1; s2 < g.splits; ++s2) sb = __fadd_rn(sb, b[s2 * rs]);
+        // every split's value in flight at once (unconditional loads, as
+        // above), then summed in split order
+        float v[kGemmMaxSplits];
+#pragma unroll
+        for (int s2 = 0; s2 < kGemmMaxSplits; ++s2) v[s2] = b[(int64_t)min(s2, g.splits - 1) * rs];
+        float sb = v[0];
+#pragma unroll
+        for (int s2 = 1; s2 < kGemmMaxSplits; ++s2)
+          if (s2 < g.splits) sb = __fadd_rn(sb, v[s2]);
         b[0] = sb;
       }
     }
