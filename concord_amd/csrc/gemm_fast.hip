@@ -2337,13 +2337,43 @@ int gemm_wgrad_vhat_split_launch(const GemmArgs& g0, void* workspace, size_t ws_
 // split-K v-hat reduction (gemm_dgt_carry_kernel) on the CUs its tiles leave
 // idle, in place of splitk_reduce_vh_kernel after it.  Same products, plans
 // and bits as gemm_wgrad_vhat_split_launch and the dgrad launched alone.
+// The unsplit dgrad tile rows (192 or 256, both x 128) for the launch that
+// carries the split WGRAD's v-hat reduction (nblk blocks of 256 threads, two
+// per spare workgroup at a time).  The launch lasts as long as the longer of
+// the dgrad tiles and the carried rounds, so fewer, larger dgrad tiles can
+// win where they leave more CUs to the reduction: config 4's 1280 x 1280
+// layers at 4096 tokens take 160 tiles of 256 x 128 (96 spare CUs, 3 rounds)
+// instead of 220 of 192 x 128 (36 spare CUs, 6 rounds): 115.3 -> 110.0 us
+// per layer step.  A round is priced at kCarryRoundUnits in the planner's
+// units (~0.69 ps each): the 36-CU carry ran 6 rounds in ~34 us.
+constexpr double kCarryRoundUnits = 8.0e6;
+static FastPlan carry_dgrad_shape(const FastPlan& pd, int64_t I, int64_t R, int nblk) {
+  FastPlan best = pd;
+  double best_cost = 1e300;
+  for (int s : {0, 2}) {   // kColShapes: 256 x 128, 192 x 128 (8 waves, one block per CU)
+    const FastShape& sh = kColShapes[s];
+    const int ti = (int)cdiv(I, sh.bi), td = ti * pd.tj;
+    const int extra = kCUs - td;
+    if (extra < 16) continue;
+    const double dgrad = (double)sh.bi * sh.bj * (double)(R + 2 * TR) * sh.weight;
+    const double carry = std::ceil((double)nblk / (2.0 * extra)) * kCarryRoundUnits;
+    const double cost = std::max(dgrad, carry);
+    if (cost < best_cost * 0.999) {
+      best_cost = cost;
+      best = FastPlan{s, 1, ti, pd.tj, pd.r_split};
+    }
+  }
+  return best;
+}
+
 int gemm_wgrad_split_dgrad_launch(const GemmArgs& gd0, const GemmArgs& gw0, void* workspace, size_t ws_bytes,
                                   hipStream_t st, const char* what, int* bias_rows) {
   if (!eligible(MODE_DGRAD, gd0) || !eligible(MODE_WGRAD, gw0) || !tr_eligible(gw0) || !workspace) return -1;
   const size_t room = ws_bytes > kSplitkCounterBytes ? ws_bytes - kSplitkCounterBytes : 0;
-  const FastPlan pd = plan_mode(MODE_DGRAD, gd0.I, gd0.J, gd0.R, room);
+  FastPlan pd = plan_mode(MODE_DGRAD, gd0.I, gd0.J, gd0.R, room);
   const FastPlan pw = plan_mode(MODE_WGRAD, gw0.I, gw0.J, gw0.R, room);
   if ((pd.shape != 0 && pd.shape != 2) || pd.splits != 1 || pw.shape != 0 || pw.splits < 2) return -1;
+  pd = carry_dgrad_shape(pd, gd0.I, gd0.R, pw.ti * pw.tj * 8);
   const int td = pd.ti * pd.tj;
   const int extra = kCUs - td;
   if (extra < 16) return -1;   // the dgrad grid leaves too few CUs to carry the reduction
