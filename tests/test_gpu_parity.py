@@ -1433,7 +1433,7 @@ def test_layer_fast_gain_forward(oracle):
 
 @pytest.mark.parametrize("M,N,K", [(2048, 5120, 1280), (2048, 1280, 1280), (4096, 1280, 1280), (1024, 2560, 640),
                                    (300, 384, 256), (154, 1280, 2048), (308, 1280, 2048), (308, 640, 2048),
-                                   (4, 1280, 2816), (77, 320, 1280)])
+                                   (4, 1280, 2816), (77, 320, 1280), (64, 64, 256), (40, 72, 200)])
 def test_dgrad_wgrad_vhat_matches_separate_calls(M, N, K):
     """The combined backward entry gives the same dx, grad_W, bias gradient,
     v-hat state, zeroed watermarks and salt as the two calls.  Where the shapes
@@ -1442,7 +1442,9 @@ def test_dgrad_wgrad_vhat_matches_separate_calls(M, N, K):
     WGRAD's v-hat reduction (4096 x 1280 x 1280, config 4's attention layers).
     For a few hundred tokens (cross-attention at 154 and 308, the M = 4
     embedding layers, a ragged 77) both products run in one launch
-    (gemm_dgt_tr_kernel), the dgrad's split-K reduction after it."""
+    (gemm_dgt_tr_kernel), the dgrad's split-K reduction after it; at 64 x 64 x
+    256 the dgrad is unsplit in that launch, at 40 x 72 x 200 the edges are
+    partial tiles."""
     from concord_amd import packed_b as pb
     rng = np.random.default_rng(M + N + K)
     packed, re, ce = rand_state(rng, N, K, exp=(-8, 7), col=(-3, 3))
