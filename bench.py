@@ -353,9 +353,16 @@ def _config4_groups(layers, xs, dys, reps, torch):
         torch.cuda.synchronize()
         us = e0.elapsed_time(e1) * 1e3 / reps / len(lays)
         tf = 6.0 * m * n_out * n_in / (us * 1e-6) / 1e12
+        # the layer step's binding roofline (no rebalance here: GatedRebalance
+        # runs once per step): MFMA time of 6MNK or HBM time of its bytes
+        hb = _step_hbm_bytes(n_out, n_in, m)
+        t_roof = max(6.0 * m * n_out * n_in / (PEAK_BF16_TFLOPS * 1e12), hb / (PEAK_HBM_GBPS * 1e9))
         out[f"{n_in}to{n_out}_M{m}"] = {"layers": len(lays), "us_per_layer": round(us, 1),
                                          "group_ms": round(us * len(lays) / 1e3, 3), "tflops": round(tf, 1),
-                                         "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+                                         "frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                                         "bound": ("hbm" if hb / (PEAK_HBM_GBPS * 1e9) >
+                                                   6.0 * m * n_out * n_in / (PEAK_BF16_TFLOPS * 1e12) else "mfma"),
+                                         "roofline_frac": round(t_roof / (us * 1e-6), 4)}
         del g
     return out
 
@@ -450,9 +457,22 @@ def _config4_step(steps, torch, ca, pb, per_group=False):
     return out
 
 
+def _step_hbm_bytes(N, K, M):
+    """Algorithmic HBM bytes of one layer step: the packed words read by the
+    forward and the dgrad (4 B each), the bf16 weight gradient written once
+    and read by the update, the update's word read and write (10 B/param with
+    the gradient read), and the activations: x read by the forward and the
+    WGRAD, dx written; dy read by the dgrad and the WGRAD, y written."""
+    return 20.0 * N * K + 6.0 * M * (N + K)
+
+
 def _config3_steps(warmup, steps, torch, ca):
     """The same training step (fwd, dgrad, wgrad with v-hat, update with the
-    winner flags, rebalance) on each config-3 shape; 6MNK FLOP per step."""
+    winner flags, rebalance) on each config-3 shape; 6MNK FLOP per step.
+    Each shape is priced against the roofline that bounds it: the MFMA time
+    of its 6MNK FLOP or the HBM time of its algorithmic bytes
+    (_step_hbm_bytes), whichever is longer (HBM for the few-token
+    cross-attention shape)."""
     from concord_amd.shapes import CONFIG3
     out = {}
     dev = torch.device("cuda:0")
@@ -475,8 +495,14 @@ def _config3_steps(warmup, steps, torch, ca):
         torch.cuda.synchronize()
         t = _graph_ms(st, warmup, steps, torch)
         a = 6.0 * M * N * K / (t * 1e-3) / 1e12
+        hb = _step_hbm_bytes(N, K, M)
+        t_mfma = 6.0 * M * N * K / (PEAK_BF16_TFLOPS * 1e12)
+        t_hbm = hb / (PEAK_HBM_GBPS * 1e9)
         out[f"{K}to{N}_M{M}"] = {"ms_per_step": round(t, 4), "tflops": round(a, 1),
-                                 "frac": round(a / PEAK_BF16_TFLOPS, 4)}
+                                 "frac": round(a / PEAK_BF16_TFLOPS, 4),
+                                 "hbm_bytes": int(hb), "hbm_GBps": round(hb / (t * 1e-3) / 1e9, 1),
+                                 "bound": "hbm" if t_hbm > t_mfma else "mfma",
+                                 "roofline_frac": round(max(t_hbm, t_mfma) / (t * 1e-3), 4)}
     return out
 
 
