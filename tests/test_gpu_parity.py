@@ -1094,16 +1094,19 @@ def test_steps_reuse_buffers():
     assert ptrs() == first
 
 
-def test_graph_replay_matches_eager_steps():
+@pytest.mark.parametrize("M", [512, 154])
+def test_graph_replay_matches_eager_steps(M):
     """A HIP graph of one training step (forward, backward with the update,
     rebalance), replayed with eager work and host syncs between replays,
-    tracks an eager twin bit for bit on every replay."""
+    tracks an eager twin bit for bit on every replay.  At M = 154 the
+    backward's products run in one launch and the finalize's launch carries
+    the dgrad's split-K reduction (its ticket re-arms itself in the graph)."""
     import concord_amd as ca
     from concord_amd import packed_b as pb
     torch.manual_seed(12)
     W0 = torch.randn(1280, 1280) * 0.03
-    x = torch.randn(512, 1280, device=DEV).to(torch.bfloat16).requires_grad_(True)
-    dy = (torch.randn(512, 1280, device=DEV) * 1e-3).to(torch.bfloat16)
+    x = torch.randn(M, 1280, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    dy = (torch.randn(M, 1280, device=DEV) * 1e-3).to(torch.bfloat16)
     xe = x.detach().clone().requires_grad_(True)
     salt = pb._get_step_counter(DEV)
 
