@@ -156,9 +156,9 @@ struct RowsBf16 {
     for (int q = 0; q < PER; ++q)
       *reinterpret_cast<i32x4*>(lds + (t / 8 + (NT / 8) * q) * LDS_STRIDE + kc) = r.v[q];
   }
-  // into the swizzled [row][64] tile (swz_off): the thread's 16-byte chunk
-  // kc / 8 of rows t / 8 + (NT / 8) q, whose (row >> 1) & 7 is the same for
-  // every q
+  // into the swizzled [row][64] tile that stage_mfma_swz reads: the thread's
+  // 16-byte chunk kc / 8 of rows t / 8 + (NT / 8) q, whose (row >> 1) & 7 is
+  // the same for every q
   CONCORD_DEV void store_swz(Raw& r, uint16_t* lds, int t) const {
     const int c = (((t % 8) ^ ((t / 8) >> 1)) & 7) * 8;
 #pragma unroll
@@ -221,10 +221,7 @@ struct RowsPacked {
   CONCORD_DEV int swz_cols(int t) const {
     return ((((t % 16) >> 1) ^ ((t / 16) >> 1)) & 7) * 8 + (t & 1) * 4;
   }
-  template <bool S = true>
-  CONCORD_DEV void store_swz(Raw& r, uint16_t* lds, int t) const {
-    store<S>(r, lds, t, swz_cols(t));
-  }
+  CONCORD_DEV void store_swz(Raw& r, uint16_t* lds, int t) const { store<true>(r, lds, t, swz_cols(t)); }
 };
 
 // Column loaders: [R][cols] with cols contiguous, moved in blocks of RB r x 4
@@ -1280,8 +1277,9 @@ template <int BJ, int NT> struct BSide<MODE_DGRAD_BF16, BJ, NT> {
 
 // 8 waves: waves 0-3 compute and move A by DMA (stage s+2 while computing s),
 // waves 4-7 load B three stages ahead in registers, decode it and write it
-// into a double-buffered swizzled LDS tile (the A tile's layout).  One LDS barrier per stage; before
-// it every compute wave waits until its own DMA of the next stage has landed.
+// into a double-buffered swizzled LDS tile (the A tile's layout).  One LDS
+// barrier per stage; before it every compute wave waits until its own DMA of
+// the next stage has landed.
 // CONV: the A operand is the conv forward's gathered x (RowsDmaConv).
 template <int MODE, int BI, int BJ, int CONV = 0>
 __global__ __launch_bounds__(512, 1) void gemm_dma_kernel(GemmArgs g) {
@@ -1593,7 +1591,7 @@ CONCORD_DEV void gemm_tr_body(const GemmArgs& g, const GemmArgs& rd, int tr_bloc
   constexpr int PERT = DA::PER + DB::PER;
   static_assert(TR == 64, "two 32-deep MFMA steps per stage");
   static_assert(UPD == 0 || (VH && !CONV && NW == 8), "the update rides on the VH launch of 8 waves");
-  // the LDS ring (at least TR_RING_BYTES, 1024-aligned) and the barrier flag
+  // the LDS ring (tr_ring_bytes, 1024-aligned) and the barrier flag
   typedef uint16_t Ring[3 * STAGE / 2];
   Ring& ring = *reinterpret_cast<Ring*>(ring_mem);
   int& s_flag = *s_flag_mem;
