@@ -913,7 +913,7 @@ def main():
     # config 5's Muon drive on this layer's gradient (context: NS5 = 5 x
     # (2 m^2 n + 2 m^3 + 2 m^2 n) FLOP with m = 1280, n = 5120)
     ns5_out = torch.empty_like(gw)
-    t_ns5 = _event_time_ms(lambda: pb.muon_ns5(gw, out=ns5_out), 3, torch)
+    t_ns5 = _event_time_ms(lambda: pb.muon_ns5(gw, out=ns5_out), reps, torch)
     ns5_flop = 5.0 * (4.0 * K_IN * K_IN * N_OUT + 2.0 * K_IN ** 3)
     # no-fire rebalance: zeroed watermarks, so no row or column ticks
     layer._row_max_buf.zero_()
