@@ -7,7 +7,9 @@
 // Numerics (oracle_muon_ns5 restates them):
 //   ||g||^2  blocks of 8192 elements of the row-major flattening; lane t of a
 //            block sums elements t, t + 256, ... ascending, then the halving
-//            tree over 256 lanes; block totals ascending.  norm = sqrt (RN).
+//            tree over 256 lanes; block totals: lane l of 64 sums totals l,
+//            l + 64, ... ascending, then the halving tree over the 64 lanes.
+//            norm = sqrt (RN).
 //   X0 = bf16(g / (n (norm / n + 1e-7))), n = max(norm, 1e-12), transposed
 //   when N > K (X is m x n, m <= n)
 //   5 x:  A = bf16(X X^T); AA = bf16(A A); B = bf16(b A + c AA);
@@ -30,13 +32,14 @@
 
 namespace concord {
 
-constexpr int kFrobBlock = 8192;
+constexpr int kFrobBlock = 8192;   // elements per block of the ||g||^2 partials
 
 // per-block partial of sum g^2 in the order above
 __global__ __launch_bounds__(256) void frob_partials_kernel(const uint16_t* __restrict__ g, int64_t ld,
                                                             int64_t N, int64_t K, float* __restrict__ part) {
   __shared__ float s[256];
   __shared__ __align__(16) uint16_t tile[kFrobBlock];
+  const int t = threadIdx.x;
   const int64_t total = N * K;
   const int64_t b0 = (int64_t)blockIdx.x * kFrobBlock;
   float acc = 0.0f;
@@ -45,47 +48,60 @@ __global__ __launch_bounds__(256) void frob_partials_kernel(const uint16_t* __re
     // its elements t, t + 256, ... from there in the same order
 #pragma unroll
     for (int q = 0; q < kFrobBlock / 2048; ++q) {
-      const int o = 2048 * q + 8 * threadIdx.x;
+      const int o = 2048 * q + 8 * t;
       *reinterpret_cast<uint4*>(tile + o) = *reinterpret_cast<const uint4*>(g + b0 + o);
     }
     __syncthreads();
 #pragma unroll 8
     for (int i = 0; i < kFrobBlock / 256; ++i) {
-      const float v = bf16_to_f32(tile[threadIdx.x + 256 * i]);
+      const float v = bf16_to_f32(tile[t + 256 * i]);
       acc = __fadd_rn(acc, __fmul_rn(v, v));
     }
   } else {
 #pragma unroll 8
     for (int i = 0; i < kFrobBlock / 256; ++i) {
-      const int64_t e = b0 + threadIdx.x + 256 * i;
+      const int64_t e = b0 + t + 256 * i;
       float v = 0.0f;
       if (e < total) v = bf16_to_f32(ld == K ? g[e] : g[(e / K) * ld + e % K]);
       acc = __fadd_rn(acc, __fmul_rn(v, v));
     }
   }
-  s[threadIdx.x] = acc;
+  s[t] = acc;
   __syncthreads();
   for (int h = 128; h >= 1; h >>= 1) {
-    if (threadIdx.x < h) s[threadIdx.x] = __fadd_rn(s[threadIdx.x], s[threadIdx.x + h]);
+    if (t < h) s[t] = __fadd_rn(s[t], s[t + h]);
     __syncthreads();
   }
-  if (threadIdx.x == 0) part[blockIdx.x] = s[0];
+  if (t == 0) part[blockIdx.x] = s[0];
 }
 
 // den = n (||g|| / n + 1e-7), n = max(||g||, 1e-12), ||g|| = sqrt of the
-// block partials summed in ascending order: the drive normalises g by
-// max(||g||, 1e-12) and ns5 then divides by (the result's norm + 1e-7)
-// (exp9_muon.py:75, 82, 47).  One wave; wave_chain stages the partials in
-// LDS and chains them in index order.
+// block partials summed as above (lane l of one wave: partials l, l + 64,
+// ... ascending, every lane's partials in flight at once; then the halving
+// tree over the 64 lanes): the drive normalises g by max(||g||, 1e-12) and
+// ns5 then divides by (the result's norm + 1e-7) (exp9_muon.py:75, 82, 47).
+// For ||g|| >= 1e-12 the quotient is exactly 1 and the sum fl(1 + 1e-7);
+// below, ||g|| / n < 1 and the input is brought back to unit norm as the
+// reference's second division does.
 __global__ __launch_bounds__(64) void frob_den_kernel(const float* __restrict__ part, int64_t nb, float* den) {
-  const int lane = threadIdx.x;
-  const float s = wave_chain(part, nb, 1);
-  // the drive's g / max(||g||, 1e-12), then ns5's / (||that|| + 1e-7), as
-  // one denominator n (||g|| / n + 1e-7): for ||g|| >= 1e-12 the quotient is
-  // exactly 1 and the sum fl(1 + 1e-7); below, ||g|| / n < 1 and the input
-  // is brought back to unit norm as the reference's second division does
-  if (lane == 0) {
-    const float norm = sqrt_rn(s);
+  constexpr int kPer = 16;
+  const int t = threadIdx.x;
+  float tot = 0.0f;
+  for (int64_t c0 = 0; c0 < nb; c0 += 64 * kPer) {
+    float v[kPer];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e) {
+      const int64_t i = c0 + 64 * e + t;
+      v[e] = i < nb ? part[i] : 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < kPer; ++e)
+      if (c0 + 64 * e + t < nb) tot = __fadd_rn(tot, v[e]);
+  }
+#pragma unroll
+  for (int h = 32; h >= 1; h >>= 1) tot = __fadd_rn(tot, __shfl_down(tot, h, 64));
+  if (t == 0) {
+    const float norm = sqrt_rn(tot);
     const float n = fmaxf(norm, 1e-12f);
     *den = __fmul_rn(n, __fadd_rn(__fdiv_rn(norm, n), 1e-7f));
   }
@@ -293,8 +309,8 @@ extern "C" int concord_muon_ns5(const uint16_t* g, int64_t ld_g, int64_t N, int6
   const int64_t nb = cdiv(N * K, kFrobBlock);
 
   hipLaunchKernelGGL(frob_partials_kernel, dim3((unsigned)nb), dim3(256), 0, st, g, ld_g, N, K, part);
-  const dim3 gx((unsigned)cdiv(n, 64), (unsigned)cdiv(m, 64));
   hipLaunchKernelGGL(frob_den_kernel, dim3(1), dim3(64), 0, st, part, nb, den);
+  const dim3 gx((unsigned)cdiv(n, 64), (unsigned)cdiv(m, 64));
   // 16-byte accesses where the gradient and X allow them (X's rows are n
   // elements from a 256-byte aligned base)
   const bool vin = ((uintptr_t)g % 16) == 0 && ld_g % 8 == 0 && n % 8 == 0;

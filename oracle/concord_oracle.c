@@ -656,8 +656,9 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
  * This build's numerics (the GPU path follows them):
  *   ||g||^2: the row-major flattening of g cut into blocks of 8192 elements;
  *     in a block, lane t (0..255) sums elements t, t+256, ... (32 of them)
- *     ascending from 0.0f, then the halving tree over the 256 lane sums;
- *     block totals ascending from 0.0f.  norm = sqrtf(sum).
+ *     ascending from 0.0f, then the halving tree over the 256 lane sums.  The
+ *     block totals: lane l (0..63) sums totals l, l+64, ... ascending from
+ *     0.0f, then the halving tree over the 64 lane sums.  norm = sqrtf(sum).
  *   X0 = bf16(g / (n * (norm / n + 1e-7))), n = max(norm, 1e-12), transposed when N > K so
  *   X is m x n, m <= n.
  *   per iteration (a, b, c = 3.4445, -4.7750, 2.0315):
@@ -668,8 +669,9 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
  * bf16 rounding of the products, not bit for bit; the norm and X0 are exact. */
 float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K) {
     const int64_t total = N * K;
-    float acc = 0.0f;
-    for (int64_t b0 = 0; b0 < total; b0 += 8192) {
+    float lane[64] = {0.0f};
+    int64_t b = 0;
+    for (int64_t b0 = 0; b0 < total; b0 += 8192, ++b) {
         float part[256];
         for (int t = 0; t < 256; ++t) {
             float s = 0.0f;
@@ -682,15 +684,17 @@ float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K) {
         }
         for (int h = 128; h >= 1; h >>= 1)
             for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
-        acc = acc + part[0];
+        lane[b % 64] = lane[b % 64] + part[0];
     }
-    return acc;
+    for (int h = 32; h >= 1; h >>= 1)
+        for (int l = 0; l < h; ++l) lane[l] = lane[l] + lane[l + h];
+    return lane[0];
 }
 
 /* concord/packed_b.py:2081-2091: sig = C * (s_slow - v_slow) * 128, noise =
  * s_fast - sig, coh = sig^2 / (sig^2 + noise^2 + 1e-30) (left to right);
- * summed like oracle_frob_sumsq: 8192-word blocks, lane t chains words
- * b0 + t + 256 i, a halving tree over the 256 lanes, blocks ascending */
+ * summed in 8192-word blocks: lane t chains words b0 + t + 256 i, a
+ * halving tree over the 256 lanes, block totals ascending */
 float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C) {
     const int64_t total = N * K;
     float acc = 0.0f;

@@ -959,7 +959,7 @@ def test_muon_ns5_fused_combines_match_two_step(oracle, N, K):
 @pytest.mark.parametrize("N,K", [(2048, 5120), (1280, 5120), (333, 1001)])
 def test_muon_frobenius_denominator_bit_exact(oracle, N, K):
     """The NS5 input scale n (||g|| / n + 1e-7), n = max(||g||, 1e-12) (block partials,
-    then one wave chaining them in ascending order) equals the oracle's bit
+    then one wave: 64 lanes of ascending partial sums and a tree) equals the oracle's bit
     for bit; read back from the workspace (layout: the split-K region, X, BX,
     A, AA, partials, then the denominator in the last 256-byte slot)."""
     from concord_amd import _lib as C
