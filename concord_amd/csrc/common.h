@@ -283,196 +283,18 @@ CONCORD_DEV float pow_p(float x, float p) {
 
 // ---- reductions ------------------------------------------------------------------
 // lane j's value, j wave-uniform (a scalar read; a shuffle would take an LDS
-// round trip, which a serial chain pays once per term)
+// round trip)
 CONCORD_DEV float lane_value(float v, int j) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
 }
 
-// Lane 0 adds buf[0 .. cnt) to s in index order (buf 16-byte aligned).  A
-// full chunk of kFull terms (a multiple of 32) is one unrolled, software-
-// pipelined run; a shorter one runs batches of 32 whose LDS reads go out one
-// batch ahead, then the remaining terms one by one.
-template <int kFull>
-CONCORD_DEV float lds_chain(const float* buf, int cnt, float s) {
-  const float4* b4 = reinterpret_cast<const float4*>(buf);
-  if (cnt == kFull) {
-    // a full chunk, unrolled: the reads of batch g + 1 (8 x 16 bytes) go out
-    // before the 32 adds of batch g; the scheduling barriers keep them there
-    constexpr int G = 8, NG = kFull / (4 * G);
-    float4 r[2][G];
-#pragma unroll
-    for (int t = 0; t < G; ++t) r[0][t] = b4[t];
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      if (g + 1 < NG) {
-#pragma unroll
-        for (int t = 0; t < G; ++t) r[(g + 1) & 1][t] = b4[(g + 1) * G + t];
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < G; ++t) {
-        const float4 q = r[g & 1][t];
-        s = __fadd_rn(s, q.x);
-        s = __fadd_rn(s, q.y);
-        s = __fadd_rn(s, q.z);
-        s = __fadd_rn(s, q.w);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    return s;
-  }
-  // batches of 32 terms, alternating between two register sets; then the tail
-  int j = 0;
-  const int nb = cnt / 32;
-  if (nb > 0) {
-    float4 r0[8], r1[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) r0[t] = b4[t];
-    for (int g = 0;;) {
-      if (g + 1 < nb) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) r1[t] = b4[(g + 1) * 8 + t];
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        s = __fadd_rn(s, r0[t].x);
-        s = __fadd_rn(s, r0[t].y);
-        s = __fadd_rn(s, r0[t].z);
-        s = __fadd_rn(s, r0[t].w);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (++g == nb) break;
-      if (g + 1 < nb) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) r0[t] = b4[(g + 1) * 8 + t];
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        s = __fadd_rn(s, r1[t].x);
-        s = __fadd_rn(s, r1[t].y);
-        s = __fadd_rn(s, r1[t].z);
-        s = __fadd_rn(s, r1[t].w);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (++g == nb) break;
-    }
-    j = nb * 32;
-  }
-  for (; j < cnt; ++j) s = __fadd_rn(s, buf[j]);
-  return s;
-}
-
-// The same for two chains over a[] and b[], term j of both in turn.
-template <int kFull>
-CONCORD_DEV void lds_chain2(const float* a, const float* b, int cnt, float& x0, float& x1) {
-  const float4* a4 = reinterpret_cast<const float4*>(a);
-  const float4* b4 = reinterpret_cast<const float4*>(b);
-  if (cnt == kFull) {
-    constexpr int G = 8, NG = kFull / (4 * G);
-    float4 ra[2][G], rb[2][G];
-#pragma unroll
-    for (int t = 0; t < G; ++t) {
-      ra[0][t] = a4[t];
-      rb[0][t] = b4[t];
-    }
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      if (g + 1 < NG) {
-#pragma unroll
-        for (int t = 0; t < G; ++t) {
-          ra[(g + 1) & 1][t] = a4[(g + 1) * G + t];
-          rb[(g + 1) & 1][t] = b4[(g + 1) * G + t];
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < G; ++t) {
-        const float4 p = ra[g & 1][t], q = rb[g & 1][t];
-        x0 = __fadd_rn(x0, p.x);
-        x1 = __fadd_rn(x1, q.x);
-        x0 = __fadd_rn(x0, p.y);
-        x1 = __fadd_rn(x1, q.y);
-        x0 = __fadd_rn(x0, p.z);
-        x1 = __fadd_rn(x1, q.z);
-        x0 = __fadd_rn(x0, p.w);
-        x1 = __fadd_rn(x1, q.w);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    return;
-  }
-  // batches of 16 pairs, alternating between two register sets; then the tail
-  int j = 0;
-  const int nb = cnt / 16;
-  if (nb > 0) {
-    float4 a0[4], b0[4], a1[4], b1[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      a0[t] = a4[t];
-      b0[t] = b4[t];
-    }
-    for (int g = 0;;) {
-      if (g + 1 < nb) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          a1[t] = a4[(g + 1) * 4 + t];
-          b1[t] = b4[(g + 1) * 4 + t];
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        x0 = __fadd_rn(x0, a0[t].x);
-        x1 = __fadd_rn(x1, b0[t].x);
-        x0 = __fadd_rn(x0, a0[t].y);
-        x1 = __fadd_rn(x1, b0[t].y);
-        x0 = __fadd_rn(x0, a0[t].z);
-        x1 = __fadd_rn(x1, b0[t].z);
-        x0 = __fadd_rn(x0, a0[t].w);
-        x1 = __fadd_rn(x1, b0[t].w);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (++g == nb) break;
-      if (g + 1 < nb) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          a0[t] = a4[(g + 1) * 4 + t];
-          b0[t] = b4[(g + 1) * 4 + t];
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        x0 = __fadd_rn(x0, a1[t].x);
-        x1 = __fadd_rn(x1, b1[t].x);
-        x0 = __fadd_rn(x0, a1[t].y);
-        x1 = __fadd_rn(x1, b1[t].y);
-        x0 = __fadd_rn(x0, a1[t].z);
-        x1 = __fadd_rn(x1, b1[t].z);
-        x0 = __fadd_rn(x0, a1[t].w);
-        x1 = __fadd_rn(x1, b1[t].w);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (++g == nb) break;
-    }
-    j = nb * 16;
-  }
-  for (; j < cnt; ++j) {
-    x0 = __fadd_rn(x0, a[j]);
-    x1 = __fadd_rn(x1, b[j]);
-  }
-}
-
-// Serial sum ((0 + v[0]) + v[stride]) + ... over `count` terms, in index
-// order, as a wave-uniform value.  The wave loads 16 x 64 terms per memory
-// round trip and stages them in LDS; lane 0 chains them (lds_chain).  Called
-// by every lane of a block's only wave (it holds a block-private LDS buffer
-// and synchronises the block).
-CONCORD_DEV float wave_chain(const float* __restrict__ v, int64_t count, int64_t stride) {
+// Sum of the `count` terms v[i * stride] as 64 lane sums and a tree: lane l
+// adds v[l], v[l + 64], ... in index order from 0.0f (a round of 16 terms
+// per lane in flight at once), then the halving tree over the 64 lane sums
+// (for h = 32 .. 1, lane l < h adds lane l + h's sum).  The result goes to
+// every lane; called by all 64 lanes of a wave.
+CONCORD_DEV float wave_tree_sum(const float* __restrict__ v, int64_t count, int64_t stride) {
   constexpr int B = 16;
-  __shared__ __align__(16) float buf[64 * B];
   const int lane = threadIdx.x & 63;
   float s = 0.0f;
   for (int64_t c0 = 0; c0 < count; c0 += 64 * B) {
@@ -482,24 +304,19 @@ CONCORD_DEV float wave_chain(const float* __restrict__ v, int64_t count, int64_t
       const int64_t i = c0 + 64 * b + lane;
       a[b] = i < count ? v[i * stride] : 0.0f;
     }
-    __syncthreads();   // lane 0 is done with the previous round's values
 #pragma unroll
-    for (int b = 0; b < B; ++b) buf[64 * b + lane] = a[b];
-    __syncthreads();
-    if (lane == 0) s = lds_chain<64 * B>(buf, (int)min((int64_t)(64 * B), count - c0), s);
+    for (int b = 0; b < B; ++b)
+      if (c0 + 64 * b + lane < count) s = __fadd_rn(s, a[b]);
   }
+#pragma unroll
+  for (int h = 32; h >= 1; h >>= 1) s = __fadd_rn(s, __shfl_down(s, h, 64));
   return lane_value(s, 0);
 }
 
-// Two chains at once over interleaved pairs (v[2i], v[2i + 1]), i ascending:
-// *s0 = ((0 + v[0]) + v[2]) + ..., *s1 = ((0 + v[1]) + v[3]) + ...  Each
-// chain keeps its own order; running both side by side halves the
-// dependent-add latency of two chains in turn.  Same calling rule as
-// wave_chain.
-CONCORD_DEV void wave_chain2(const float* __restrict__ v, int64_t count, float* s0, float* s1) {
+// wave_tree_sum of the interleaved pairs: *s0 over v[0], v[2], ...; *s1 over
+// v[1], v[3], ... (`count` pairs), each in the same order.
+CONCORD_DEV void wave_tree_sum2(const float* __restrict__ v, int64_t count, float* s0, float* s1) {
   constexpr int B = 8;
-  __shared__ __align__(16) float bufa[64 * B];
-  __shared__ __align__(16) float bufb[64 * B];
   const int lane = threadIdx.x & 63;
   float x0 = 0.0f, x1 = 0.0f;
   for (int64_t c0 = 0; c0 < count; c0 += 64 * B) {
@@ -510,14 +327,17 @@ CONCORD_DEV void wave_chain2(const float* __restrict__ v, int64_t count, float* 
       a[q] = i < count ? v[2 * i] : 0.0f;
       b[q] = i < count ? v[2 * i + 1] : 0.0f;
     }
-    __syncthreads();
 #pragma unroll
-    for (int q = 0; q < B; ++q) {
-      bufa[64 * q + lane] = a[q];
-      bufb[64 * q + lane] = b[q];
-    }
-    __syncthreads();
-    if (lane == 0) lds_chain2<64 * B>(bufa, bufb, (int)min((int64_t)(64 * B), count - c0), x0, x1);
+    for (int q = 0; q < B; ++q)
+      if (c0 + 64 * q + lane < count) {
+        x0 = __fadd_rn(x0, a[q]);
+        x1 = __fadd_rn(x1, b[q]);
+      }
+  }
+#pragma unroll
+  for (int h = 32; h >= 1; h >>= 1) {
+    x0 = __fadd_rn(x0, __shfl_down(x0, h, 64));
+    x1 = __fadd_rn(x1, __shfl_down(x1, h, 64));
   }
   *s0 = lane_value(x0, 0);
   *s1 = lane_value(x1, 0);

@@ -79,13 +79,13 @@ __global__ __launch_bounds__(256) void noise_partials_kernel(const uint16_t* __r
   }
 }
 
-// scale = (sigma * sqrt(sum g^2)) / max(sqrt(sum xi^2), 1e-12), partials
-// chained in ascending order
+// scale = (sigma * sqrt(sum g^2)) / max(sqrt(sum xi^2), 1e-12), the block
+// partials of each sum added as 64 lane sums and a tree (wave_tree_sum2)
 __global__ __launch_bounds__(64) void noise_scale_kernel(const float* __restrict__ part, int64_t nb,
                                                          const float* sigma, float* scale) {
   const int lane = threadIdx.x;
   float sg, sx;
-  wave_chain2(part, nb, &sg, &sx);
+  wave_tree_sum2(part, nb, &sg, &sx);
   if (lane == 0) {
     const float ng = sqrt_rn(sg);
     const float nx = fmaxf(sqrt_rn(sx), 1e-12f);
@@ -154,7 +154,7 @@ __global__ __launch_bounds__(256) void token_scale_kernel(const uint16_t* __rest
 }
 
 // sum of eps_0 .. eps_{M-1} in kNoiseBlock blocks (lane chains, halving tree);
-// the block partials are chained by token_sum_final_kernel
+// token_sum_final_kernel adds the block partials (64 lane sums and a tree)
 __global__ __launch_bounds__(256) void token_sum_partials_kernel(int64_t M, const int32_t* salt,
                                                                  float* __restrict__ part,
                                                                  float* __restrict__ eps) {
@@ -181,7 +181,7 @@ __global__ __launch_bounds__(256) void token_sum_partials_kernel(int64_t M, cons
 
 __global__ __launch_bounds__(64) void token_sum_final_kernel(const float* __restrict__ part, int64_t nb,
                                                              float* out) {
-  const float s = wave_chain(part, nb, 1);
+  const float s = wave_tree_sum(part, nb, 1);
   if (threadIdx.x == 0) *out = s;
 }
 

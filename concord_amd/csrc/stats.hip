@@ -80,10 +80,10 @@ __global__ __launch_bounds__(256) void coherence_partials_kernel(const int32_t* 
   if (threadIdx.x == 0) part[blockIdx.x] = s[0];
 }
 
-// the block partials chained in ascending order (one wave, wave_chain)
+// the block partials added as 64 lane sums and a tree (one wave, wave_tree_sum)
 __global__ __launch_bounds__(64) void coherence_final_kernel(const float* __restrict__ part, int64_t nb,
                                                              float* out) {
-  const float s = wave_chain(part, nb, 1);
+  const float s = wave_tree_sum(part, nb, 1);
   if (threadIdx.x == 0) *out = s;
 }
 

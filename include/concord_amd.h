@@ -355,7 +355,8 @@ int concord_bias_grad(const uint16_t* dy, int64_t ld_dy, int64_t M, int64_t N,
  * v_slow), noise = s_fast - sig (gate_coherence_from_fields,
  * concord/packed_b.py:2081-2091); the layer mean of measure_coherence
  * (2094-2106) is out_sum / (N K).  Fixed order: 8192-word blocks, lanes
- * chaining a stride-256 set each, a halving tree, blocks ascending. */
+ * chaining a stride-256 set each, a halving tree; the block totals as 64
+ * lane sums (totals l, l + 64, ... ascending) and a halving tree. */
 size_t concord_stats_workspace_bytes(int64_t n_watermarks, int64_t n_words);
 int concord_watermark_peak(const int32_t* rows, int64_t n_rows, const int32_t* cols, int64_t n_cols,
                            int32_t* out, void* workspace, size_t workspace_bytes, void* stream);

@@ -650,6 +650,18 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
     free(pc);
 }
 
+/* The block totals of the fixed-order sums below (and of the GPU's
+ * wave_tree_sum): lane l (0..63) adds totals l, l+64, ... ascending from 0.0f,
+ * then the halving tree over the 64 lane sums. */
+static float lane_tree_sum(const float* v, int64_t n) {
+    float lane[64];
+    for (int l = 0; l < 64; ++l) lane[l] = 0.0f;
+    for (int64_t i = 0; i < n; ++i) lane[i % 64] = lane[i % 64] + v[i];
+    for (int h = 32; h >= 1; h >>= 1)
+        for (int l = 0; l < h; ++l) lane[l] = lane[l] + lane[l + h];
+    return lane[0];
+}
+
 /* ---- A13 Muon drive: experiments/cpu_dynamics/exp9_muon.py:44-55 (ns5),
  * 58-100 (MuonConcord.step: drive = sqrt(max(N,K)) * ns5(g / ||g||));
  * docs/MUON_IMPLEMENTATION.md:27-40 (bf16 NS, O fed to the apply as the step).
@@ -668,10 +680,10 @@ void oracle_vhat_ema(const uint16_t* grad_bf16, int64_t N, int64_t K,
  * The GPU's products accumulate in MFMA order, so GPU and oracle agree to the
  * bf16 rounding of the products, not bit for bit; the norm and X0 are exact. */
 float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K) {
-    const int64_t total = N * K;
-    float lane[64] = {0.0f};
-    int64_t b = 0;
-    for (int64_t b0 = 0; b0 < total; b0 += 8192, ++b) {
+    const int64_t total = N * K, nb = (total + 8191) / 8192;
+    float* bt = (float*)malloc((size_t)(nb > 0 ? nb : 1) * sizeof(float));
+    for (int64_t b = 0; b < nb; ++b) {
+        const int64_t b0 = b * 8192;
         float part[256];
         for (int t = 0; t < 256; ++t) {
             float s = 0.0f;
@@ -684,20 +696,22 @@ float oracle_frob_sumsq(const uint16_t* g, int64_t N, int64_t K) {
         }
         for (int h = 128; h >= 1; h >>= 1)
             for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
-        lane[b % 64] = lane[b % 64] + part[0];
+        bt[b] = part[0];
     }
-    for (int h = 32; h >= 1; h >>= 1)
-        for (int l = 0; l < h; ++l) lane[l] = lane[l] + lane[l + h];
-    return lane[0];
+    const float r = lane_tree_sum(bt, nb);
+    free(bt);
+    return r;
 }
 
 /* concord/packed_b.py:2081-2091: sig = C * (s_slow - v_slow) * 128, noise =
  * s_fast - sig, coh = sig^2 / (sig^2 + noise^2 + 1e-30) (left to right);
  * summed in 8192-word blocks: lane t chains words b0 + t + 256 i, a
- * halving tree over the 256 lanes, block totals ascending */
+ * halving tree over the 256 lanes; the block totals by lane_tree_sum */
 float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C) {
     const int64_t total = N * K;
-    float acc = 0.0f;
+    const int64_t nb = (total + 8191) / 8192;
+    float* bt = (float*)malloc((size_t)(nb > 0 ? nb : 1) * sizeof(float));
+    int64_t b = 0;
     for (int64_t b0 = 0; b0 < total; b0 += 8192) {
         float part[256];
         for (int t = 0; t < 256; ++t) {
@@ -716,9 +730,11 @@ float oracle_coherence_sum(const int32_t* packed, int64_t N, int64_t K, float C)
         }
         for (int h = 128; h >= 1; h >>= 1)
             for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
-        acc = acc + part[0];
+        bt[b++] = part[0];
     }
-    return acc;
+    const float r = lane_tree_sum(bt, nb);
+    free(bt);
+    return r;
 }
 
 /* cos(2 pi u) and sin(2 pi u), u in [0, 1) on a 2^-24 grid: quadrant and
@@ -786,7 +802,10 @@ float oracle_iso_draw(int32_t seed, int64_t e) {
 
 void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t salt) {
     const int64_t total = N * K;
-    float sg = 0.0f, sx = 0.0f;
+    const int64_t nb = (total + 8191) / 8192;
+    float* btg = (float*)malloc((size_t)(nb > 0 ? nb : 1) * sizeof(float));
+    float* btx = (float*)malloc((size_t)(nb > 0 ? nb : 1) * sizeof(float));
+    int64_t b = 0;
     for (int64_t b0 = 0; b0 < total; b0 += 8192) {
         float pg[256], px[256];
         for (int t = 0; t < 256; ++t) {
@@ -810,9 +829,13 @@ void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t sa
                 pg[t] = pg[t] + pg[t + h];
                 px[t] = px[t] + px[t + h];
             }
-        sg = sg + pg[0];
-        sx = sx + px[0];
+        btg[b] = pg[0];
+        btx[b] = px[0];
+        ++b;
     }
+    const float sg = lane_tree_sum(btg, nb), sx = lane_tree_sum(btx, nb);
+    free(btg);
+    free(btx);
     const float ng = sqrtf(sg);
     const float nx = fmaxf(sqrtf(sx), 1e-12f);
     const float scale = (sigma * ng) / nx;
@@ -821,7 +844,9 @@ void oracle_iso_noise(uint16_t* g, int64_t N, int64_t K, float sigma, int32_t sa
 }
 
 float oracle_token_sum(int32_t seed, int64_t M) {
-    float acc = 0.0f;
+    const int64_t nb = (M + 8191) / 8192;
+    float* bt = (float*)malloc((size_t)(nb > 0 ? nb : 1) * sizeof(float));
+    int64_t b = 0;
     for (int64_t b0 = 0; b0 < M; b0 += 8192) {
         float part[256];
         for (int t = 0; t < 256; ++t) {
@@ -834,15 +859,20 @@ float oracle_token_sum(int32_t seed, int64_t M) {
         }
         for (int h = 128; h >= 1; h >>= 1)
             for (int t = 0; t < h; ++t) part[t] = part[t] + part[t + h];
-        acc = acc + part[0];
+        bt[b++] = part[0];
     }
-    return acc;
+    const float r = lane_tree_sum(bt, nb);
+    free(bt);
+    return r;
 }
 
 void oracle_sigmag_combine(uint16_t* g, const uint16_t* P, int64_t N, int64_t K, float S, float Mf,
                            float sigma) {
     const int64_t total = N * K;
-    float sg = 0.0f, sx = 0.0f;
+    const int64_t nb = (total + 8191) / 8192;
+    float* btg = (float*)malloc((size_t)(nb > 0 ? nb : 1) * sizeof(float));
+    float* btx = (float*)malloc((size_t)(nb > 0 ? nb : 1) * sizeof(float));
+    int64_t b = 0;
     for (int64_t b0 = 0; b0 < total; b0 += 8192) {
         float pg[256], px[256];
         for (int t = 0; t < 256; ++t) {
@@ -863,9 +893,13 @@ void oracle_sigmag_combine(uint16_t* g, const uint16_t* P, int64_t N, int64_t K,
                 pg[t] = pg[t] + pg[t + h];
                 px[t] = px[t] + px[t + h];
             }
-        sg = sg + pg[0];
-        sx = sx + px[0];
+        btg[b] = pg[0];
+        btx[b] = px[0];
+        ++b;
     }
+    const float sg = lane_tree_sum(btg, nb), sx = lane_tree_sum(btx, nb);
+    free(btg);
+    free(btx);
     const float scale = (sigma * sqrtf(sg)) / fmaxf(sqrtf(sx), 1e-12f);
     for (int64_t e = 0; e < total; ++e) {
         const float v = bf16_to_f32(g[e]);
