@@ -155,6 +155,8 @@ CONCORD_DEV float exp2i(int32_t e) {
   e = min(max(e, -300), 300);
   return ldexpf(1.0f, e);
 }
+// exp2i for |e| <= 300, where its clamp does not bind
+CONCORD_DEV float exp2i_nc(int32_t e) { return ldexpf(1.0f, e); }
 
 CONCORD_DEV float det_exp2(float y) {
   if (y != y) return y;

@@ -273,7 +273,7 @@ __global__ __launch_bounds__(256) void apply_adamw_fast_kernel(AdamwArgs a) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int32_t te = te_row + ce[j];
-      out[j] = adamw_element_fast<RATIO>(w[j], g[j], exp2i(te), exp2i(-te), in.vr, vc[j], &cp[j],
+      out[j] = adamw_element_fast<RATIO>(w[j], g[j], exp2i_nc(te), exp2i_nc(-te), in.vr, vc[j], &cp[j],
                                          psr ^ (int32_t)(k0 + j), C, alpha, avf, lr_kappa, U, &m[j]);
       const int32_t am = (full || k0 + j < a.K) ? abs(m[j]) : 0;
       rmax = max(rmax, am);

@@ -134,6 +134,10 @@ inline int update_fast_path(const concord_update_params& p, uint32_t flags) {
         p.beta1 == 0.0f && p.weight_decay == 0.0f && p.wd_sv == 0.0f && p.wd_sf == 0.0f &&
         p.gate_gain == 1.0f && p.step_cap == 10.0f))
     return 0;
+  // the scale exponents +-(row_exp + col_exp - mantissa_bias) of int8
+  // exponents stay inside exp2i's clamp of +-300, so the fast kernels form
+  // the scales with exp2i_nc
+  if (p.mantissa_bias < -40 || p.mantissa_bias > 40) return 0;
   const bool ratio = flags & CONCORD_RATIO_COH, consol = flags & CONCORD_GF_CONSOLIDATION,
              cohpre = flags & CONCORD_COHPRE;
   if (ratio && consol) return 2;

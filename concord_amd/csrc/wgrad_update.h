@@ -274,7 +274,7 @@ CONCORD_DEV void upd_apply(const GemmArgs& g, const WgradUpd& u, f32x4 (&acc)[4]
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int32_t te = te_row + ce[y][e];
-        out[e] = adamw_element_fast<RATIO>(w[e], gv[e], exp2i(te), exp2i(-te), vr, vc[y][e], &cp[e],
+        out[e] = adamw_element_fast<RATIO>(w[e], gv[e], exp2i_nc(te), exp2i_nc(-te), vr, vc[y][e], &cp[e],
                                            psr ^ (int32_t)(j + e), C, alpha, avf, lr_kappa, U, &m[e]);
         const int32_t am = abs(m[e]);
         rmax = max(rmax, am);
